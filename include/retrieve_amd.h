@@ -1,0 +1,56 @@
+/* C ABI of libretrieve_amd.so: the MI355X (gfx950) scoring-and-selection hot path of
+ * torchretrieve / SilverTorch.
+ *
+ * Conventions for every entry point:
+ * - pointers are device pointers (HIP) unless stated; inputs are read-only and borrowed;
+ *   outputs are caller-allocated; scratch comes from a caller-allocated `workspace` whose
+ *   size the matching `*_workspace` function returns;
+ * - work is enqueued on `stream` (a hipStream_t); no entry point synchronizes the host;
+ * - the return value is 0 on success, else a status: 1 invalid argument (shape, size or
+ *   range), 2 unsupported type/width, 3 a HIP call failed, 4 workspace too small;
+ *   rt_last_error() then describes it;
+ * - top-k results order by (score desc, item index asc): ties go to the lower item index.
+ *   Rows with fewer than k candidates end in id -1 and the score sentinel (INT32_MIN for int32
+ *   scores, -inf for float scores).
+ */
+#ifndef RETRIEVE_AMD_H_
+#define RETRIEVE_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* rt_stream_t; /* hipStream_t */
+
+/* The message of the last failing call on this thread. */
+const char* rt_last_error(void);
+
+/* Exact int8 top-k over a full item table: int8 [B, D] queries x int8 [N, D] items, int32
+ * dot products, top-k by (score desc, index asc) -> ids int64 [B, k], scores int32 [B, k].
+ * D in {64, 128, 256, 512, 768, 1024}; 1 <= k <= 1024; N < 2**32 - 1.
+ * `mask` (nullable): [B, mask_words] uint64, item d of row b passes iff bit 63 - d % 64 of
+ * word d / 64 is set (SilverTorch's `filtering_bit_mask` order).
+ * Replaces: SilverTorch's scorer + radix select for one cluster holding every item
+ *   (silvertorch/silvertorch/ops/csrc/fork_search_cuda.cu:1256-1524, `st::search` with
+ *   n_probe = n_lists = 1 and divisor_for_int8 = -1), and the int8 re-rank of
+ *   retrieve/src/retrieve/modules/silvertorch.py:363-379 over all items. */
+size_t rt_int8_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k);
+int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t* items, int64_t N,
+                      int64_t D, int64_t k, const uint64_t* mask, int64_t mask_words,
+                      int64_t* out_ids, int32_t* out_scores, void* workspace,
+                      size_t workspace_bytes, rt_stream_t stream);
+
+/* Benchmark support (no counterpart in the reference): when enabled, every call brackets its
+ * dominant kernel (the main scan) with a HIP event pair on its stream; collect() waits for
+ * the recorded pairs, returns their summed milliseconds and count, and clears them. */
+int rt_profile_enable(int on);
+int rt_profile_collect(double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RETRIEVE_AMD_H_ */

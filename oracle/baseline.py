@@ -1,0 +1,47 @@
+"""The reference's CPU path, timed by ``bench.py`` as the CPU baseline (test infrastructure; see
+``oracle/__init__``). Restates ``evaluation/bench/oracle.py:95-158``: ``torch.mm`` over item
+chunks of 2M rows (``ITEM_CHUNK``, ``oracle.py:20-22``), ``torch.topk`` per chunk, and the
+lowest-id merge ``_merge_topk`` (``oracle.py:83-92``). int8 codes are cast to float32, which
+is exact (``|dot| <= 512 * 127**2 < 2**24``).
+"""
+
+from __future__ import annotations
+
+import time
+
+import torch
+
+ITEM_CHUNK = 2_000_000
+
+
+def _merge(best_s, best_i, s, i, k):
+    cs, ci = torch.cat([best_s, s], 1), torch.cat([best_i, i], 1)
+    by_id = ci.argsort(dim=1, stable=True)
+    cs, ci = cs.gather(1, by_id), ci.gather(1, by_id)
+    by_score = cs.argsort(dim=1, descending=True, stable=True)[:, :k]
+    return cs.gather(1, by_score), ci.gather(1, by_score)
+
+
+def int8_topk_cpu(q_codes: torch.Tensor, item_codes: torch.Tensor, k: int, chunk: int = ITEM_CHUNK):
+    """``(ids [B, k], scores float32 [B, k])`` of the int8 dot, ties to the lowest id."""
+    q = q_codes.float()
+    b = q.shape[0]
+    best_s = torch.full((b, k), float("-inf"))
+    best_i = torch.full((b, k), -1, dtype=torch.long)
+    for start in range(0, item_codes.shape[0], chunk):
+        part = item_codes[start : start + chunk].float()
+        scores = q @ part.t()
+        top = torch.topk(scores, min(k, part.shape[0]), dim=1)
+        best_s, best_i = _merge(best_s, best_i, top.values, top.indices + start, k)
+    return best_i, best_s
+
+
+def time_int8(q_codes, item_sample, k: int, reps: int = 3) -> tuple[float, int]:
+    """Median seconds of ``int8_topk_cpu`` over ``reps`` runs, and the threads used."""
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        int8_topk_cpu(q_codes, item_sample, k)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], torch.get_num_threads()

@@ -1,0 +1,225 @@
+// The exact top-k merge over the scan waves' lists, launch planning, and the library's error
+// store.
+#include <cstdarg>
+#include <cstdlib>
+
+#include "scan_common.h"
+#include "wave_lists.h"
+
+namespace rt {
+
+// ---- errors -----------------------------------------------------------------------------
+
+static thread_local char g_error[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+const char* last_error() { return g_error; }
+
+// ---- planning ---------------------------------------------------------------------------
+
+// Workgroups a pass aims for (about eight per CU of a 256-CU part).
+static constexpr int64_t kTargetWorkgroups = 2048;
+// Rows of the seed sample; the main pass then keeps about k * N / kSeedRows composites a
+// query (in expectation, for items in random order).
+static constexpr int64_t kSeedRows = 1 << 18;
+// Upper bound on the candidate lists' workspace (a pass may exceed it only at one workgroup
+// per query group).
+static constexpr int64_t kMaxListBytes = int64_t{512} << 20;
+
+static PassPlan plan_pass(int64_t n_rows, int64_t row_stride, int64_t n_qgroups, int64_t min_rows,
+                          int capw, int qpw) {
+  PassPlan p;
+  p.n_rows = n_rows;
+  p.row_stride = row_stride;
+  p.capw = capw;
+  int64_t gx = kTargetWorkgroups / (n_qgroups > 0 ? n_qgroups : 1);
+  gx = gx < 1 ? 1 : gx;
+  const int64_t by_rows = cdiv(n_rows, min_rows);
+  gx = gx < by_rows ? gx : by_rows;
+  gx = gx < kMaxMergeSlots / kScanWaves ? gx : kMaxMergeSlots / kScanWaves;
+  // keep the lists within kMaxListBytes (fewer, longer strips for large k or batch)
+  const int64_t per_wg = n_qgroups * kScanWaves * static_cast<int64_t>(qpw) * capw *
+                         static_cast<int64_t>(sizeof(uint64_t));
+  const int64_t by_bytes = kMaxListBytes / (per_wg > 0 ? per_wg : 1);
+  gx = gx < by_bytes ? gx : by_bytes;
+  gx = gx < 1 ? 1 : gx;
+  p.strip = align_up(static_cast<size_t>(cdiv(n_rows, gx)), kTile);
+  if (p.strip == 0) p.strip = kTile;
+  p.gx = cdiv(n_rows, p.strip);
+  if (p.gx < 1) p.gx = 1;
+  const int64_t slots = p.gx * n_qgroups * kScanWaves;
+  p.lists_bytes = static_cast<size_t>(slots) * qpw * capw * sizeof(uint64_t);
+  p.counts_bytes = static_cast<size_t>(slots) * qpw * sizeof(int);
+  return p;
+}
+
+ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw) {
+  ScanPlan s;
+  s.qpw = qpw;
+  s.n_qgroups = cdiv(B, qpw);
+  const int main_capw = static_cast<int>(next_pow2(k + 2 * kTile));
+  const int seed_capw = static_cast<int>(next_pow2(2 * k + 2 * kTile));
+  const int64_t seed_rows = kSeedRows > 16 * k ? kSeedRows : 16 * k;
+  s.seeded = N >= 8 * seed_rows;
+  if (s.seeded) {
+    s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, 256, seed_capw, qpw);
+  }
+  s.main = plan_pass(N, 1, s.n_qgroups, 1024, main_capw, qpw);
+  const size_t lists = s.main.lists_bytes > s.seed.lists_bytes ? s.main.lists_bytes
+                                                              : s.seed.lists_bytes;
+  const size_t counts = s.main.counts_bytes > s.seed.counts_bytes ? s.main.counts_bytes
+                                                                 : s.seed.counts_bytes;
+  s.off_lists = 0;
+  s.off_counts = align_up(lists, 256);
+  s.off_tau = s.off_counts + align_up(counts, 256);
+  s.total = s.off_tau + align_up(static_cast<size_t>(B) * sizeof(uint64_t), 256);
+  return s;
+}
+
+// ---- merge ------------------------------------------------------------------------------
+
+template <int M>
+__global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
+  __shared__ uint64_t buf[M];
+  __shared__ int pre[kMaxMergeSlots];
+  __shared__ int part[kMergeThreads];
+  const int tid = threadIdx.x;
+  const int64_t q = blockIdx.x;
+  const int64_t g = q / m.qpw;
+  const int qi = static_cast<int>(q % m.qpw);
+  const int S = static_cast<int>(m.gx * kScanWaves);
+  const int64_t slot0 = g * m.gx * kScanWaves;
+  const int k = m.k;
+
+  // counts of this query's lists → inclusive prefix sums
+  const int per = (S + kMergeThreads - 1) / kMergeThreads;
+  int run = 0;
+  for (int i = 0; i < per; ++i) {
+    const int s = tid * per + i;
+    if (s < S) {
+      int c = m.counts[(slot0 + s) * m.qpw + qi];
+      c = c < m.capw ? c : m.capw;
+      run += c;
+      pre[s] = run;
+    }
+  }
+  part[tid] = run;
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int t = 0; t < kMergeThreads; ++t) {
+      const int v = part[t];
+      part[t] = acc;
+      acc += v;
+    }
+  }
+  __syncthreads();
+  for (int i = 0; i < per; ++i) {
+    const int s = tid * per + i;
+    if (s < S) pre[s] += part[tid];
+  }
+  for (int i = tid; i < M; i += kMergeThreads) buf[i] = 0ull;
+  __syncthreads();
+  const int total = pre[S - 1];
+  const int room = M - k;
+
+  for (int e0 = 0; e0 < total; e0 += room) {
+    const int n = total - e0 < room ? total - e0 : room;
+    for (int i = tid; i < room; i += kMergeThreads) {
+      uint64_t v = 0ull;
+      if (i < n) {
+        const int e = e0 + i;
+        int lo = 0, hi = S - 1;  // first s with pre[s] > e
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (pre[mid] > e) hi = mid; else lo = mid + 1;
+        }
+        const int start = lo == 0 ? 0 : pre[lo - 1];
+        v = m.lists[((slot0 + lo) * m.qpw + qi) * static_cast<int64_t>(m.capw) + (e - start)];
+      }
+      buf[k + i] = v;
+    }
+    __syncthreads();
+    for (int size = 2; size <= M; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int t = tid; t < (M >> 1); t += kMergeThreads) {
+          const int i = 2 * t - (t & (stride - 1));
+          const int j = i + stride;
+          const bool desc = (i & size) == 0;
+          const uint64_t a = buf[i];
+          const uint64_t b = buf[j];
+          if ((a < b) == desc) {
+            buf[i] = b;
+            buf[j] = a;
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  if (m.tau_out != nullptr) {
+    if (tid == 0) m.tau_out[q] = buf[k - 1];
+    return;
+  }
+  for (int j = tid; j < k; j += kMergeThreads) {
+    const uint64_t c = buf[j];
+    const bool ok = c != 0ull;
+    m.out_ids[q * k + j] = ok ? static_cast<int64_t>(composite_item(c)) : -1;
+    const uint32_t key = composite_key(c);
+    if (m.score_kind == kScoreI32) {
+      static_cast<int32_t*>(m.out_scores)[q * k + j] = ok ? i32_of_key(key) : INT32_MIN;
+    } else if (m.score_kind == kScoreF32FromI32) {
+      static_cast<float*>(m.out_scores)[q * k + j] =
+          ok ? static_cast<float>(i32_of_key(key)) : -INFINITY;
+    } else {
+      static_cast<float*>(m.out_scores)[q * k + j] = ok ? f32_of_key(key) : -INFINITY;
+    }
+  }
+}
+
+__global__ void pad_kernel(int64_t* ids, void* scores, int64_t n, int score_kind) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  ids[i] = -1;
+  if (score_kind == kScoreI32) {
+    static_cast<int32_t*>(scores)[i] = INT32_MIN;
+  } else {
+    static_cast<float*>(scores)[i] = -INFINITY;
+  }
+}
+
+int launch_pad(int64_t* out_ids, void* out_scores, int64_t B, int64_t k, int score_kind,
+               hipStream_t stream) {
+  const int64_t n = B * k;
+  if (n == 0) return kOk;
+  pad_kernel<<<static_cast<unsigned>(cdiv(n, 256)), 256, 0, stream>>>(out_ids, out_scores, n,
+                                                                     score_kind);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+int launch_merge(const MergeArgs& m, hipStream_t stream) {
+  RT_CHECK_ARG(m.k >= 1 && m.k <= kMaxK, "k must be in [1, %lld], got %d",
+               static_cast<long long>(kMaxK), m.k);
+  RT_CHECK_ARG(m.gx * kScanWaves <= kMaxMergeSlots, "too many scan lists per query");
+  if (m.B == 0) return kOk;
+  const dim3 grid(static_cast<unsigned>(m.B));
+  if (m.k <= 512) {
+    merge_kernel<2048><<<grid, kMergeThreads, 0, stream>>>(m);
+  } else {
+    merge_kernel<4096><<<grid, kMergeThreads, 0, stream>>>(m);
+  }
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+}  // namespace rt
+
+extern "C" const char* rt_last_error(void) { return rt::last_error(); }

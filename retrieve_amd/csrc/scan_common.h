@@ -1,0 +1,91 @@
+// The scan → merge pipeline shared by the int8, bf16 and Hamming scans: launch planning,
+// workspace layout and the merge kernel's interface.
+//
+// One top-k call is up to four launches on the caller's stream, with no host sync:
+//   1. seed scan over a strided sample of the items (only when N is large),
+//   2. seed merge: the exact k-th best composite of the sample per query (a lower bound on the
+//      k-th best over all items),
+//   3. main scan over all items, appending only composites >= that bound,
+//   4. final merge: the exact top-k over the main scan's lists.
+#pragma once
+
+#include "rt_common.h"
+
+namespace rt {
+
+constexpr int kScanWaves = 4;       // waves per scan workgroup
+constexpr int kScanThreads = kScanWaves * kWave;
+constexpr int kTile = 16;           // items per MFMA tile
+constexpr int kMergeThreads = 256;
+constexpr int64_t kMaxK = 1024;
+constexpr int64_t kMaxMergeSlots = 8192;  // lists a query's merge reads (gx * waves)
+
+// The scan kernels' arguments (the element type of queries/items is the kernel's).
+struct ScanArgs {
+  const void* queries;     // [B, D]
+  int64_t B;
+  const void* items;       // [N, D] (or [N, W] words)
+  int64_t n_rows;          // rows of this pass's index space
+  int64_t row_stride;      // item index = row * row_stride (the sample pass strides)
+  int64_t strip;           // rows per workgroup, a multiple of kTile
+  int k;
+  int capw;                // list capacity (power of two, >= k + kTile)
+  const uint64_t* tau_in;  // [B] lower bounds (composites) or null
+  const uint64_t* mask;    // [B, mask_words] item bits, item d at bit 63 - d % 64, or null
+  int64_t mask_words;
+  uint64_t* lists;         // [slots, qpw, capw]
+  int* counts;             // [slots, qpw]
+};
+
+enum ScoreKind : int {
+  kScoreI32 = 0,       // the key is an int32 score; write int32
+  kScoreF32FromI32 = 1,  // the key is an int32 score; write it as float
+  kScoreF32 = 2,       // the key is a float score; write float
+};
+
+struct MergeArgs {
+  const uint64_t* lists;
+  const int* counts;
+  int capw;
+  int qpw;          // queries per scan wave
+  int64_t gx;       // scan workgroups per query group
+  int64_t B;
+  int k;
+  uint64_t* tau_out;   // threshold mode: [B]
+  int64_t* out_ids;    // final mode: [B, k]
+  void* out_scores;    // final mode: [B, k]
+  int score_kind;
+};
+
+// One pass of a scan: its grid and list geometry.
+struct PassPlan {
+  int64_t n_rows = 0;
+  int64_t row_stride = 1;
+  int64_t strip = 0;
+  int64_t gx = 0;
+  int capw = 0;
+  size_t lists_bytes = 0;
+  size_t counts_bytes = 0;
+};
+
+struct ScanPlan {
+  int qpw = 16;
+  int64_t n_qgroups = 0;
+  bool seeded = false;
+  PassPlan seed;
+  PassPlan main;
+  // workspace layout (byte offsets)
+  size_t off_lists = 0, off_counts = 0, off_tau = 0, total = 0;
+};
+
+// Sizes the passes for B queries (qpw per wave) over N rows and top-k.
+ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw);
+
+// Writes the -1 / sentinel pads of an empty result.
+int launch_pad(int64_t* out_ids, void* out_scores, int64_t B, int64_t k, int score_kind,
+               hipStream_t stream);
+
+// Launches the merge (threshold mode when tau_out != null).
+int launch_merge(const MergeArgs& m, hipStream_t stream);
+
+}  // namespace rt

@@ -1,0 +1,240 @@
+"""The CPU oracle against the reference's golden vectors, closed forms and brute force."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import filters as of
+from oracle import quantize as oq
+from oracle import scan as osc
+from oracle import select as osel
+from tests.conftest import rng
+
+
+# --- int8 ---------------------------------------------------------------------------------
+
+
+def test_int8_kat(kat):
+    a, _ = kat
+    s = osc.int8_scores(a["int8_kat_query"], a["int8_kat_items"])
+    assert s.tolist() == [a["int8_kat_scores"].tolist()]
+    ids, sc = osc.int8_topk(a["int8_kat_query"], a["int8_kat_items"], 2)
+    assert ids.tolist() == [[1, 0]] and sc.tolist() == [[39, 17]]
+
+
+def test_int8_scores_equal_python_int_dots():
+    g = rng(1)
+    q = g.integers(-128, 128, (3, 64), dtype=np.int8)
+    it = g.integers(-128, 128, (50, 64), dtype=np.int8)
+    got = osc.int8_scores(q, it)
+    for b in range(3):
+        for n in range(50):
+            want = sum(int(x) * int(y) for x, y in zip(q[b], it[n]))
+            assert got[b, n] == want
+
+
+def test_int8_scores_extreme_accumulation():
+    # the largest |dot| at D = 1024: (-128)(-128) * 1024 = 2**24, still exact
+    q = np.full((1, 1024), -128, np.int8)
+    it = np.full((2, 1024), -128, np.int8)
+    it[1] = 127
+    assert osc.int8_scores(q, it).tolist() == [[2**24, -128 * 127 * 1024]]
+
+
+# --- popcount / Hamming -------------------------------------------------------------------
+
+
+def test_popcount_kat(kat):
+    a, _ = kat
+    assert osc.popcount64(a["popcount_kat_in"]).tolist() == a["popcount_kat_out"].tolist()
+
+
+def test_popcount_random_words():
+    x = rng(2).integers(-(2**63), 2**63 - 1, 200, dtype=np.int64)
+    want = [bin(int(v) & ((1 << 64) - 1)).count("1") for v in x]
+    assert osc.popcount64(x).tolist() == want
+
+
+def test_hamming_equals_pm1_dot():
+    """``64 W - 2 * hamming`` is the dot product of the ±1 expansions of the bits."""
+    g = rng(3)
+    q = g.integers(-(2**63), 2**63 - 1, (4, 8), dtype=np.int64)
+    it = g.integers(-(2**63), 2**63 - 1, (30, 8), dtype=np.int64)
+
+    def pm1(words):
+        u = words.view(np.uint64)
+        bits = (u[..., None] >> np.arange(64, dtype=np.uint64)) & np.uint64(1)
+        return bits.reshape(words.shape[0], -1).astype(np.int64) * 2 - 1
+
+    assert np.array_equal(osc.hamming_scores(q, it), pm1(q) @ pm1(it).T)
+
+
+# --- selection ----------------------------------------------------------------------------
+
+
+def _brute_topk(scores, k, valid=None):
+    out = []
+    for r, row in enumerate(scores.tolist()):
+        cand = [(-s, i) for i, s in enumerate(row) if valid is None or valid[r][i]]
+        out.append([i for _, i in sorted(cand)[:k]])
+    return out
+
+
+@pytest.mark.parametrize("n,k", [(10, 3), (200, 50), (1000, 7), (37, 37), (5, 9)])
+def test_topk_rows_brute_force_heavy_ties(n, k):
+    g = rng(n * 31 + k)
+    s = g.integers(-3, 4, (6, n)).astype(np.int32)
+    valid = g.random((6, n)) > 0.2
+    ids, sc = osel.topk_rows(s, k, valid)
+    want = _brute_topk(s, k, valid)
+    for r in range(6):
+        m = len(want[r])
+        assert ids[r, :m].tolist() == want[r]
+        assert (ids[r, m:] == -1).all() and (sc[r, m:] == osel.INT32_MIN).all()
+        assert sc[r, :m].tolist() == [s[r, i] for i in want[r]]
+
+
+def test_merge_topk_equals_topk_of_union():
+    g = rng(4)
+    s = g.integers(0, 5, (3, 40)).astype(np.float32)
+    ids = np.tile(np.arange(40), (3, 1))
+    a_s, a_i = osel.merge_topk(s[:, :17], ids[:, :17], s[:, 17:], ids[:, 17:], 9)
+    want_i, want_s = osel.topk_rows(s, 9)
+    assert np.array_equal(a_i, want_i) and np.array_equal(a_s, want_s)
+
+
+def test_lowest_id_tie_kat(kat):
+    """The reference harness's planted tie: items 2 and 13 identical; the lower id first."""
+    a, meta = kat
+    items, queries = a["tie_items"], a["tie_queries"]
+    masks = a["tie_masks"][a["tie_qa"]]
+    scores = (queries @ items.T).astype(np.float32)
+    ids, _ = osel.topk_rows(scores, meta["tie_k"], masks)
+    assert ids[5, 4:].tolist() == meta["tie_row5_tail"]
+
+
+def test_composite_key_orders_score_desc_then_id_asc():
+    s = np.array([5, 5, -3, 7, 5], np.int32)
+    i = np.array([9, 2, 0, 100, 3])
+    c = osel.composite_key(s, i)
+    order = np.argsort(-c.astype(np.float64), kind="stable")  # exact for these magnitudes
+    order = sorted(range(5), key=lambda j: -int(c[j]))
+    assert [int(i[j]) for j in order] == [100, 2, 3, 9, 0]
+
+
+# --- quantization -------------------------------------------------------------------------
+
+
+def test_quantize_extremes(kat):
+    a, _ = kat
+    codes, scales = oq.quantize_int8(a["quant_extremes_in"])
+    assert codes[:, 0].tolist() == [127, 127] and codes[:, 1].tolist() == [-127, -127]
+    assert codes.max() <= 127 and codes.min() >= -127
+    assert np.allclose(scales, np.array([1.0, 2.0]) / 127.0, atol=1e-6)
+
+
+def test_quantize_half_to_even(kat):
+    a, _ = kat
+    codes, _ = oq.quantize_int8(a["quant_half_in"])
+    assert codes.tolist() == a["quant_half_codes"].tolist()
+
+
+def test_quantize_zero_and_tiny_rows():
+    x = np.zeros((2, 16), np.float32)
+    x[1, 3] = 1e-30
+    codes, scales = oq.quantize_int8(x)
+    assert (codes[0] == 0).all() and np.isfinite(scales).all()
+    assert scales[0] == np.float32(1e-8) * (np.float32(1) / np.float32(127))
+    assert codes[1, 3] == 0  # 1e-30 / 1e-8 * 127 rounds to 0
+
+
+def test_pack_signs_lsb_first():
+    v = np.full((1, 128), -1.0, np.float32)
+    v[0, 0] = 1.0  # word 0 bit 0
+    v[0, 127] = 1.0  # word 1 bit 63
+    w = oq.pack_signs(v).view(np.uint64)
+    assert w[0, 0] == 1 and w[0, 1] == np.uint64(1) << np.uint64(63)
+
+
+# --- filters ------------------------------------------------------------------------------
+
+
+def test_clause_match_brute_force():
+    g = rng(5)
+    attrs = g.integers(-1, 4, (60, 3, 2))
+    rev = np.array([False, True, False])
+    q = g.integers(-1, 4, (7, 3))
+    got = of.clause_match(attrs, rev, q)
+    for b in range(7):
+        for n in range(60):
+            ok = True
+            for c in range(3):
+                if q[b, c] == -1:
+                    continue
+                m = any(v == q[b, c] for v in attrs[n, c])
+                ok &= m != rev[c]
+            assert got[b, n] == ok
+
+
+def test_clause_sets_reduce_to_singletons():
+    g = rng(6)
+    attrs = g.integers(-1, 5, (80, 4, 1))
+    q = g.integers(-1, 5, (9, 4))
+    q = np.where(q == -1, -1, q)
+    got = of.clause_match_sets(attrs, q[:, :, None])
+    # an item value of -1 never matches a set, while clause_match compares -1 == -1 only
+    # for inactive clauses (skipped), so the two agree
+    assert np.array_equal(got, of.clause_match(attrs, np.zeros(4, bool), q))
+
+
+def test_murmur_smhasher_verification(kat):
+    _, meta = kat
+    assert of.smhasher_verification() == meta["murmur3_x64_128_verification"]
+
+
+def test_readme_bloom_kat(kat):
+    a, meta = kat
+    attrs = a["readme_attrs"]
+    words, offs = of.bloom_build(attrs, meta["readme_build_k"],
+                                 b_multiplier=meta["readme_b_multiplier"])
+    for text, hits in zip(meta["readme_queries"], meta["readme_hits"]):
+        m = of.bloom_expression_mask(words, offs, 4, text, meta["readme_build_k"],
+                                     meta["readme_hash_k"])
+        assert np.nonzero(m)[0].tolist() == hits
+        assert np.nonzero(of.exact_expression_mask(attrs, text))[0].tolist() == hits
+
+
+def test_expression_mapping_kat(kat):
+    a, meta = kat
+    assert of.queries_to_expressions(a["expr_kat_in"]) == meta["expr_kat_out"]
+    assert of.queries_to_expressions(a["expr_kat_in"], [False, True]) == \
+        meta["expr_kat_out_reverse"]
+
+
+def test_bloom_layout_position():
+    """Doc 70 sits in bundle 0, column 1, bit 57; doc 2050 in bundle 1, column 0, bit 61."""
+    attrs = np.full((2100, 1, 1), -1, np.int64)
+    attrs[70, 0, 0] = 5
+    attrs[2050, 0, 0] = 5
+    words, offs = of.bloom_build(attrs, 3, bits_per_doc=64)
+    assert offs.tolist() == [0, 64, 128]
+    pos = of.bit_positions(0, 5, 64, 3)
+    w = words.view(np.uint64)
+    want = {}
+    for p in pos:
+        want[p * 32 + 1] = np.uint64(1) << np.uint64(57)
+        want[(64 + p) * 32 + 0] = np.uint64(1) << np.uint64(61)
+    nz = {int(i): w[i] for i in np.nonzero(w)[0]}
+    assert nz == want
+
+
+def test_bloom_no_false_negatives():
+    g = rng(7)
+    attrs = g.integers(0, 20, (3000, 3, 1))
+    words, offs = of.bloom_build(attrs, 3, bits_per_doc=64)
+    for f in range(3):
+        for v in range(0, 20, 3):
+            m = of.term_mask(words, offs, 3000, f, v, 3, 7)
+            exact = (attrs[:, f, 0] == v)
+            assert (m | ~exact).all()  # every doc holding the token is found
