@@ -28,18 +28,21 @@ static constexpr int64_t kTargetWorkgroups = 2048;
 // Rows of the seed sample; the main pass then keeps about k * N / kSeedRows composites a
 // query (in expectation, for items in random order).
 static constexpr int64_t kSeedRows = 1 << 18;
+// Sample rows per seed workgroup (16 per wave, one tile each): many waves, so the k-th largest
+// of their maxima is close to the k-th best of the sample.
+static constexpr int64_t kSeedRowsPerWorkgroup = 64;
 // Upper bound on the candidate lists' workspace (a pass may exceed it only at one workgroup
 // per query group).
 static constexpr int64_t kMaxListBytes = int64_t{512} << 20;
 
 static PassPlan plan_pass(int64_t n_rows, int64_t row_stride, int64_t n_qgroups, int64_t min_rows,
-                          int capw, int qpw) {
+                          int capw, int qpw, int64_t min_gx = 1) {
   PassPlan p;
   p.n_rows = n_rows;
   p.row_stride = row_stride;
   p.capw = capw;
   int64_t gx = kTargetWorkgroups / (n_qgroups > 0 ? n_qgroups : 1);
-  gx = gx < 1 ? 1 : gx;
+  gx = gx < min_gx ? min_gx : gx;
   const int64_t by_rows = cdiv(n_rows, min_rows);
   gx = gx < by_rows ? gx : by_rows;
   gx = gx < kMaxMergeSlots / kScanWaves ? gx : kMaxMergeSlots / kScanWaves;
@@ -64,11 +67,11 @@ ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw) {
   s.qpw = qpw;
   s.n_qgroups = cdiv(B, qpw);
   const int main_capw = static_cast<int>(next_pow2(k + 2 * kTile));
-  const int seed_capw = static_cast<int>(next_pow2(2 * k + 2 * kTile));
   const int64_t seed_rows = kSeedRows > 16 * k ? kSeedRows : 16 * k;
   s.seeded = N >= 8 * seed_rows;
   if (s.seeded) {
-    s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, 256, seed_capw, qpw);
+    // one-entry lists (each seed wave's best); at least k waves per query group
+    s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, kSeedRowsPerWorkgroup, 1, qpw, k);
   }
   s.main = plan_pass(N, 1, s.n_qgroups, 1024, main_capw, qpw);
   const size_t lists = s.main.lists_bytes > s.seed.lists_bytes ? s.main.lists_bytes
@@ -84,11 +87,76 @@ ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw) {
 
 // ---- merge ------------------------------------------------------------------------------
 
-template <int M>
+constexpr int kMergeChunk = 4096;  // list entries gathered into LDS per round
+
+// Block-wide radix select over keys[0, n) in LDS: the kth (1-based) largest, MSB-first over
+// eight 8-bit digits. 1 <= kth <= n. Every thread of the block calls it.
+__device__ uint64_t block_select_desc(const uint64_t* keys, int n, int kth, unsigned* hist,
+                                      int* sh) {
+  const int tid = threadIdx.x;
+  uint64_t prefix = 0ull;
+  uint64_t mask = 0ull;
+  if (tid == 0) sh[1] = kth;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += blockDim.x) hist[i] = 0u;
+    __syncthreads();
+    for (int i = tid; i < n; i += blockDim.x) {
+      const uint64_t v = keys[i];
+      if ((v & mask) == prefix) atomicAdd(&hist[(v >> shift) & 255ull], 1u);
+    }
+    __syncthreads();
+    if (tid < kWave) {
+      // lane l covers digits 255 - 4l - j, j < 4 (descending digit order across the wave)
+      const int lane = tid;
+      unsigned c[4];
+      unsigned sum = 0u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = hist[255 - 4 * lane - j];
+        sum += c[j];
+      }
+      unsigned incl = sum;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const unsigned t = __shfl_up(incl, off);
+        if (lane >= off) incl += t;
+      }
+      const unsigned excl = incl - sum;
+      const unsigned want = static_cast<unsigned>(sh[1]);
+      if (excl < want && want <= incl) {
+        unsigned run = excl;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (run + c[j] >= want) {
+            sh[0] = 255 - 4 * lane - j;
+            sh[1] = static_cast<int>(want - run);
+            break;
+          }
+          run += c[j];
+        }
+      }
+    }
+    __syncthreads();
+    prefix |= static_cast<uint64_t>(sh[0]) << shift;
+    mask |= 255ull << shift;
+    __syncthreads();
+  }
+  return prefix;
+}
+
+// The exact top-k of one query over all its scan lists. Rounds of up to kMergeChunk list
+// entries are gathered behind the current best (at most k entries), the k-th largest of the
+// union is found by radix select and only the entries >= it are kept; the survivors are
+// sorted at the end. With tau_out set, only the k-th composite is written (0 when fewer than
+// k entries exist: no bound).
+template <int KP>
 __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
-  __shared__ uint64_t buf[M];
+  __shared__ uint64_t buf[KP + kMergeChunk];
+  __shared__ uint64_t tmp[KP];
   __shared__ int pre[kMaxMergeSlots];
+  __shared__ unsigned hist[256];
   __shared__ int part[kMergeThreads];
+  __shared__ int sh[3];
   const int tid = threadIdx.x;
   const int64_t q = blockIdx.x;
   const int64_t g = q / m.qpw;
@@ -97,14 +165,17 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   const int64_t slot0 = g * m.gx * kScanWaves;
   const int k = m.k;
 
-  // counts of this query's lists → inclusive prefix sums
+  // list lengths → inclusive prefix sums over this query's lists
   const int per = (S + kMergeThreads - 1) / kMergeThreads;
   int run = 0;
   for (int i = 0; i < per; ++i) {
     const int s = tid * per + i;
     if (s < S) {
-      int c = m.counts[(slot0 + s) * m.qpw + qi];
-      c = c < m.capw ? c : m.capw;
+      int c = m.capw;
+      if (m.counts != nullptr) {
+        c = m.counts[(slot0 + s) * m.qpw + qi];
+        c = c < m.capw ? c : m.capw;
+      }
       run += c;
       pre[s] = run;
     }
@@ -124,48 +195,60 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     const int s = tid * per + i;
     if (s < S) pre[s] += part[tid];
   }
-  for (int i = tid; i < M; i += kMergeThreads) buf[i] = 0ull;
   __syncthreads();
   const int total = pre[S - 1];
-  const int room = M - k;
 
-  for (int e0 = 0; e0 < total; e0 += room) {
-    const int n = total - e0 < room ? total - e0 : room;
-    for (int i = tid; i < room; i += kMergeThreads) {
-      uint64_t v = 0ull;
-      if (i < n) {
-        const int e = e0 + i;
-        int lo = 0, hi = S - 1;  // first s with pre[s] > e
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (pre[mid] > e) hi = mid; else lo = mid + 1;
-        }
-        const int start = lo == 0 ? 0 : pre[lo - 1];
-        v = m.lists[((slot0 + lo) * m.qpw + qi) * static_cast<int64_t>(m.capw) + (e - start)];
-      }
-      buf[k + i] = v;
+  int held = 0;
+  for (int e0 = 0; e0 < total; e0 += kMergeChunk) {
+    const int n = total - e0 < kMergeChunk ? total - e0 : kMergeChunk;
+    for (int s = tid; s < S; s += kMergeThreads) {
+      const int lo = s == 0 ? 0 : pre[s - 1];
+      const int hi = pre[s];
+      const int a = lo > e0 ? lo : e0;
+      const int b = hi < e0 + n ? hi : e0 + n;
+      const uint64_t* list = m.lists + ((slot0 + s) * m.qpw + qi) * static_cast<int64_t>(m.capw);
+      for (int e = a; e < b; ++e) buf[held + (e - e0)] = list[e - lo];
     }
     __syncthreads();
-    for (int size = 2; size <= M; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int t = tid; t < (M >> 1); t += kMergeThreads) {
-          const int i = 2 * t - (t & (stride - 1));
-          const int j = i + stride;
-          const bool desc = (i & size) == 0;
-          const uint64_t a = buf[i];
-          const uint64_t b = buf[j];
-          if ((a < b) == desc) {
-            buf[i] = b;
-            buf[j] = a;
-          }
-        }
-        __syncthreads();
+    const int cnt = held + n;
+    if (cnt > k) {
+      const uint64_t kth = block_select_desc(buf, cnt, k, hist, sh);
+      if (tid == 0) sh[2] = 0;
+      __syncthreads();
+      for (int i = tid; i < cnt; i += kMergeThreads) {
+        const uint64_t v = buf[i];
+        if (v >= kth) tmp[atomicAdd(&sh[2], 1)] = v;
       }
+      __syncthreads();
+      for (int i = tid; i < k; i += kMergeThreads) buf[i] = tmp[i];
+      held = k;
+    } else {
+      held = cnt;
+    }
+    __syncthreads();
+  }
+
+  for (int i = held + tid; i < KP; i += kMergeThreads) buf[i] = 0ull;
+  __syncthreads();
+  for (int size = 2; size <= KP; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = tid; t < (KP >> 1); t += kMergeThreads) {
+        const int i = 2 * t - (t & (stride - 1));
+        const int j = i + stride;
+        const bool desc = (i & size) == 0;
+        const uint64_t a = buf[i];
+        const uint64_t b = buf[j];
+        if ((a < b) == desc) {
+          buf[i] = b;
+          buf[j] = a;
+        }
+      }
+      __syncthreads();
     }
   }
 
   if (m.tau_out != nullptr) {
-    if (tid == 0) m.tau_out[q] = buf[k - 1];
+    if (tid == 0) m.tau_out[q] = held >= k ? buf[k - 1] : 0ull;
     return;
   }
   for (int j = tid; j < k; j += kMergeThreads) {
@@ -211,10 +294,14 @@ int launch_merge(const MergeArgs& m, hipStream_t stream) {
   RT_CHECK_ARG(m.gx * kScanWaves <= kMaxMergeSlots, "too many scan lists per query");
   if (m.B == 0) return kOk;
   const dim3 grid(static_cast<unsigned>(m.B));
-  if (m.k <= 512) {
-    merge_kernel<2048><<<grid, kMergeThreads, 0, stream>>>(m);
+  if (m.k <= 128) {
+    merge_kernel<128><<<grid, kMergeThreads, 0, stream>>>(m);
+  } else if (m.k <= 256) {
+    merge_kernel<256><<<grid, kMergeThreads, 0, stream>>>(m);
+  } else if (m.k <= 512) {
+    merge_kernel<512><<<grid, kMergeThreads, 0, stream>>>(m);
   } else {
-    merge_kernel<4096><<<grid, kMergeThreads, 0, stream>>>(m);
+    merge_kernel<1024><<<grid, kMergeThreads, 0, stream>>>(m);
   }
   RT_CHECK_HIP(hipGetLastError());
   return kOk;

@@ -45,7 +45,7 @@ enum ScoreKind : int {
 
 struct MergeArgs {
   const uint64_t* lists;
-  const int* counts;
+  const int* counts;   // null: every list holds capw entries
   int capw;
   int qpw;          // queries per scan wave
   int64_t gx;       // scan workgroups per query group

@@ -14,7 +14,11 @@ namespace rt {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-template <int KSTEPS>
+// SEED: the sample pass. Instead of candidate lists each wave keeps, per query, only its best
+// composite over its rows and writes it as a one-entry list (a.capw == 1); the k-th largest of
+// those maxima is a lower bound on the k-th best item (k distinct waves each hold an item at
+// least that good).
+template <int KSTEPS, bool SEED>
 __global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
   constexpr int QPW = 16;
   constexpr int64_t D = KSTEPS * 64;
@@ -53,6 +57,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
   const int64_t r1 = r0 + a.strip < a.n_rows ? r0 + a.strip : a.n_rows;
   const int64_t ntiles = r1 > r0 ? cdiv(r1 - r0, kTile) : 0;
 
+  uint64_t best = 0ull;  // SEED only
   for (int64_t t = wave; t < ntiles; t += kScanWaves) {
     const int64_t rb = r0 + t * kTile;
     int64_t lr = rb + col;
@@ -65,6 +70,18 @@ __global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], qf[s], acc, 0, 0, 0);
+    }
+    if constexpr (SEED) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = rb + 4 * grp + r;
+        const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
+        bool ok = row < r1;
+        if (ok && qmask != nullptr) ok = (qmask[item >> 6] >> (63 - (item & 63))) & 1ull;
+        const uint64_t c = composite(key_of_i32(acc[r]), item);
+        best = ok && c > best ? c : best;
+      }
+      continue;
     }
     const bool hit = acc[0] >= ts || acc[1] >= ts || acc[2] >= ts || acc[3] >= ts;
     if (!__any(hit)) continue;
@@ -99,34 +116,47 @@ __global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
       }
     }
   }
+  if constexpr (SEED) {
+    uint64_t o = __shfl_xor(best, 16);
+    best = o > best ? o : best;
+    o = __shfl_xor(best, 32);
+    best = o > best ? o : best;
+    if (lane < QPW) lists[lane] = best;
+    return;
+  }
   wave_sync_memory();
   if (lane < QPW) a.counts[slot * QPW + lane] = cnt[lane];
 }
 
 template <int KSTEPS>
-static int launch_scan_int8(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups,
+static int launch_scan_int8(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, bool seed,
                             hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.gx), static_cast<unsigned>(n_qgroups));
+  if (seed) {
+    scan_int8_kernel<KSTEPS, true><<<grid, kScanThreads, 0, stream>>>(a);
+    RT_CHECK_HIP(hipGetLastError());
+    return kOk;
+  }
   const size_t lds = kScanWaves * (p.capw * sizeof(uint64_t) + 16 * sizeof(int));
   if (lds > 65536) {
-    RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(scan_int8_kernel<KSTEPS>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     static_cast<int>(lds)));
+    RT_CHECK_HIP(hipFuncSetAttribute(
+        reinterpret_cast<const void*>(scan_int8_kernel<KSTEPS, false>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
   }
-  scan_int8_kernel<KSTEPS><<<grid, kScanThreads, lds, stream>>>(a);
+  scan_int8_kernel<KSTEPS, false><<<grid, kScanThreads, lds, stream>>>(a);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }
 
 static int dispatch_scan_int8(int64_t D, const ScanArgs& a, const PassPlan& p, int64_t nqg,
-                              hipStream_t stream) {
+                              bool seed, hipStream_t stream) {
   switch (D) {
-    case 64: return launch_scan_int8<1>(a, p, nqg, stream);
-    case 128: return launch_scan_int8<2>(a, p, nqg, stream);
-    case 256: return launch_scan_int8<4>(a, p, nqg, stream);
-    case 512: return launch_scan_int8<8>(a, p, nqg, stream);
-    case 768: return launch_scan_int8<12>(a, p, nqg, stream);
-    case 1024: return launch_scan_int8<16>(a, p, nqg, stream);
+    case 64: return launch_scan_int8<1>(a, p, nqg, seed, stream);
+    case 128: return launch_scan_int8<2>(a, p, nqg, seed, stream);
+    case 256: return launch_scan_int8<4>(a, p, nqg, seed, stream);
+    case 512: return launch_scan_int8<8>(a, p, nqg, seed, stream);
+    case 768: return launch_scan_int8<12>(a, p, nqg, seed, stream);
+    case 1024: return launch_scan_int8<16>(a, p, nqg, seed, stream);
     default:
       set_error("int8 scan supports D in {64, 128, 256, 512, 768, 1024}, got %lld",
                 static_cast<long long>(D));
@@ -194,14 +224,16 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
       a.strip = plan.seed.strip;
       a.capw = plan.seed.capw;
       a.tau_in = nullptr;
-      int st = dispatch_scan_int8(D, a, plan.seed, plan.n_qgroups, stream);
+      int st = dispatch_scan_int8(D, a, plan.seed, plan.n_qgroups, true, stream);
       if (st != kOk) return st;
-      m.capw = plan.seed.capw;
+      m.capw = 1;
+      m.counts = nullptr;  // one entry per list: each seed wave's best
       m.gx = plan.seed.gx;
       m.tau_out = tau;
       st = launch_merge(m, stream);
       if (st != kOk) return st;
       m.tau_out = nullptr;
+      m.counts = counts;
     }
     a.n_rows = plan.main.n_rows;
     a.row_stride = 1;
@@ -210,7 +242,7 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
     a.tau_in = plan.seeded ? tau : nullptr;
     hipEvent_t stop;
     profile_begin(stream, &stop);
-    int st = dispatch_scan_int8(D, a, plan.main, plan.n_qgroups, stream);
+    int st = dispatch_scan_int8(D, a, plan.main, plan.n_qgroups, false, stream);
     profile_end(stream, stop);
     if (st != kOk) return st;
     m.capw = plan.main.capw;
