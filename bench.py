@@ -58,6 +58,9 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=2_000_000,
                     help="items of the CPU baseline's bounded sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 2 GiB device copy three times (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters against a known byte count)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one GPU per box); "
@@ -73,6 +76,15 @@ def main() -> int:
     items = int8_table(n, d, 1234, dev)
     queries = int8_table(b, d, 99, dev)
     torch.cuda.synchronize()
+
+    if args.copy_probe:
+        src = torch.empty(2 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy probe: 3 x 2 GiB device copies")
+        del src, dst
 
     op = torch.ops.retrieve.int8_scan_topk
     log(f"warmup {args.warmup}")

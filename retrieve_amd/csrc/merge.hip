@@ -217,7 +217,11 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
       __syncthreads();
       for (int i = tid; i < cnt; i += kMergeThreads) {
         const uint64_t v = buf[i];
-        if (v >= kth) tmp[atomicAdd(&sh[2], 1)] = v;
+        if (v >= kth) {
+          // exactly k entries are >= kth, except for repeated empty (0) seed entries
+          const int p = atomicAdd(&sh[2], 1);
+          if (p < k) tmp[p] = v;
+        }
       }
       __syncthreads();
       for (int i = tid; i < k; i += kMergeThreads) buf[i] = tmp[i];

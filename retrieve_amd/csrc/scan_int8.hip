@@ -32,7 +32,9 @@ __global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
   const int64_t slot = (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) * kScanWaves +
                        wave;
   uint64_t* lists = a.lists + slot * QPW * a.capw;
-  if (lane < QPW) cnt[lane] = 0;
+  if constexpr (!SEED) {
+    if (lane < QPW) cnt[lane] = 0;
+  }
 
   const int8_t* Q = static_cast<const int8_t*>(a.queries);
   const int8_t* I = static_cast<const int8_t*>(a.items);
@@ -50,7 +52,8 @@ __global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
     for (int s = 0; s < KSTEPS; ++s) qf[s] = v4i{0, 0, 0, 0};
   }
   int32_t ts = i32_of_key(composite_key(tau));
-  const uint64_t* qmask = a.mask != nullptr ? a.mask + qrow * a.mask_words : nullptr;
+  const uint64_t* qmask =
+      a.mask != nullptr && qrow < a.B ? a.mask + qrow * a.mask_words : nullptr;
   wave_sync_memory();
 
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * a.strip;
