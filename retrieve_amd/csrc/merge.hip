@@ -23,7 +23,7 @@ const char* last_error() { return g_error; }
 
 // ---- planning ---------------------------------------------------------------------------
 
-// Workgroups a pass aims for (about eight per CU of a 256-CU part).
+// Workgroups a seed pass aims for, and the main pass's when the device cannot be queried.
 static constexpr int64_t kTargetWorkgroups = 2048;
 // Rows of the seed sample; the main pass then keeps about k * N / kSeedRows composites a
 // query (in expectation, for items in random order).
@@ -36,12 +36,12 @@ static constexpr int64_t kSeedRowsPerWorkgroup = 64;
 static constexpr int64_t kMaxListBytes = int64_t{512} << 20;
 
 static PassPlan plan_pass(int64_t n_rows, int64_t row_stride, int64_t n_qgroups, int64_t min_rows,
-                          int capw, int qpw, int64_t min_gx = 1) {
+                          int capw, int qpw, int64_t target_wgs, int64_t min_gx = 1) {
   PassPlan p;
   p.n_rows = n_rows;
   p.row_stride = row_stride;
   p.capw = capw;
-  int64_t gx = kTargetWorkgroups / (n_qgroups > 0 ? n_qgroups : 1);
+  int64_t gx = target_wgs / (n_qgroups > 0 ? n_qgroups : 1);
   gx = gx < min_gx ? min_gx : gx;
   const int64_t by_rows = cdiv(n_rows, min_rows);
   gx = gx < by_rows ? gx : by_rows;
@@ -62,7 +62,19 @@ static PassPlan plan_pass(int64_t n_rows, int64_t row_stride, int64_t n_qgroups,
   return p;
 }
 
-ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw) {
+int64_t main_workgroups() {
+  int dev = 0;
+  int cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0) {
+    return kTargetWorkgroups;
+  }
+  const int64_t t = static_cast<int64_t>(cus) * kMainWorkgroupsPerCU;
+  return t < kMaxResidentWorkgroups ? t : kMaxResidentWorkgroups;
+}
+
+ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw, int64_t target_wgs) {
   ScanPlan s;
   s.qpw = qpw;
   s.n_qgroups = cdiv(B, qpw);
@@ -71,9 +83,10 @@ ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw) {
   s.seeded = N >= 8 * seed_rows;
   if (s.seeded) {
     // one-entry lists (each seed wave's best); at least k waves per query group
-    s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, kSeedRowsPerWorkgroup, 1, qpw, k);
+    s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, kSeedRowsPerWorkgroup, 1, qpw,
+                       kTargetWorkgroups, k);
   }
-  s.main = plan_pass(N, 1, s.n_qgroups, 1024, main_capw, qpw);
+  s.main = plan_pass(N, 1, s.n_qgroups, 1024, main_capw, qpw, target_wgs);
   const size_t lists = s.main.lists_bytes > s.seed.lists_bytes ? s.main.lists_bytes
                                                               : s.seed.lists_bytes;
   const size_t counts = s.main.counts_bytes > s.seed.counts_bytes ? s.main.counts_bytes
@@ -89,8 +102,11 @@ ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw) {
 
 constexpr int kMergeChunk = 4096;  // list entries gathered into LDS per round
 
-// Block-wide radix select over keys[0, n) in LDS: the kth (1-based) largest, MSB-first over
-// eight 8-bit digits. 1 <= kth <= n. Every thread of the block calls it.
+// Block-wide radix select over keys[0, n) in LDS, MSB-first 8-bit digits. Returns a bound T
+// such that exactly kth keys are >= T (the keys are distinct except for repeated zeros): the
+// kth largest key, or, when a digit pass finds the kth largest key's bucket holding exactly the
+// keys still wanted, that bucket's lowest possible value (the search stops there).
+// 1 <= kth <= n. Every thread of the block calls it.
 __device__ uint64_t block_select_desc(const uint64_t* keys, int n, int kth, unsigned* hist,
                                       int* sh) {
   const int tid = threadIdx.x;
@@ -130,6 +146,7 @@ __device__ uint64_t block_select_desc(const uint64_t* keys, int n, int kth, unsi
           if (run + c[j] >= want) {
             sh[0] = 255 - 4 * lane - j;
             sh[1] = static_cast<int>(want - run);
+            sh[3] = c[j] == want - run;  // the bucket is exactly the keys still wanted
             break;
           }
           run += c[j];
@@ -139,7 +156,9 @@ __device__ uint64_t block_select_desc(const uint64_t* keys, int n, int kth, unsi
     __syncthreads();
     prefix |= static_cast<uint64_t>(sh[0]) << shift;
     mask |= 255ull << shift;
+    const bool done = sh[3] != 0;
     __syncthreads();
+    if (done) break;
   }
   return prefix;
 }
@@ -154,9 +173,10 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   __shared__ uint64_t buf[KP + kMergeChunk];
   __shared__ uint64_t tmp[KP];
   __shared__ int pre[kMaxMergeSlots];
+  __shared__ short owner[kMergeChunk];
   __shared__ unsigned hist[256];
   __shared__ int part[kMergeThreads];
-  __shared__ int sh[3];
+  __shared__ int sh[4];
   const int tid = threadIdx.x;
   const int64_t q = blockIdx.x;
   const int64_t g = q / m.qpw;
@@ -165,55 +185,74 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   const int64_t slot0 = g * m.gx * kScanWaves;
   const int k = m.k;
 
-  // list lengths → inclusive prefix sums over this query's lists
-  const int per = (S + kMergeThreads - 1) / kMergeThreads;
-  int run = 0;
-  for (int i = 0; i < per; ++i) {
-    const int s = tid * per + i;
-    if (s < S) {
-      int c = m.capw;
-      if (m.counts != nullptr) {
-        c = m.counts[(slot0 + s) * m.qpw + qi];
+  // list lengths → inclusive prefix sums over this query's lists (flat: S one-entry lists
+  // stored contiguously per query, lists + q * S)
+  int total = S;
+  if (!m.flat) {
+    const int per = (S + kMergeThreads - 1) / kMergeThreads;
+    int run = 0;
+    for (int i = 0; i < per; ++i) {
+      const int s = tid * per + i;
+      if (s < S) {
+        int c = m.counts[(slot0 + s) * m.qpw + qi];
         c = c < m.capw ? c : m.capw;
+        run += c;
+        pre[s] = run;
       }
-      run += c;
-      pre[s] = run;
     }
-  }
-  part[tid] = run;
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int t = 0; t < kMergeThreads; ++t) {
-      const int v = part[t];
-      part[t] = acc;
-      acc += v;
+    part[tid] = run;
+    __syncthreads();
+    if (tid == 0) {
+      int acc = 0;
+      for (int t = 0; t < kMergeThreads; ++t) {
+        const int v = part[t];
+        part[t] = acc;
+        acc += v;
+      }
     }
+    __syncthreads();
+    for (int i = 0; i < per; ++i) {
+      const int s = tid * per + i;
+      if (s < S) pre[s] += part[tid];
+    }
+    __syncthreads();
+    total = pre[S - 1];
   }
-  __syncthreads();
-  for (int i = 0; i < per; ++i) {
-    const int s = tid * per + i;
-    if (s < S) pre[s] += part[tid];
-  }
-  __syncthreads();
-  const int total = pre[S - 1];
+  if (tid == 0) sh[3] = 0;
 
   int held = 0;
   for (int e0 = 0; e0 < total; e0 += kMergeChunk) {
     const int n = total - e0 < kMergeChunk ? total - e0 : kMergeChunk;
-    for (int s = tid; s < S; s += kMergeThreads) {
-      const int lo = s == 0 ? 0 : pre[s - 1];
-      const int hi = pre[s];
-      const int a = lo > e0 ? lo : e0;
-      const int b = hi < e0 + n ? hi : e0 + n;
-      const uint64_t* list = m.lists + ((slot0 + s) * m.qpw + qi) * static_cast<int64_t>(m.capw);
-      for (int e = a; e < b; ++e) buf[held + (e - e0)] = list[e - lo];
+    if (m.flat) {
+      const uint64_t* row = m.lists + q * static_cast<int64_t>(S);
+      for (int i = tid; i < n; i += kMergeThreads) buf[held + i] = row[e0 + i];
+    } else {
+      // owner[] maps each entry of the window to its list (LDS only), then every thread
+      // loads independent entries
+      for (int s = tid; s < S; s += kMergeThreads) {
+        const int lo = s == 0 ? 0 : pre[s - 1];
+        const int hi = pre[s];
+        const int a = lo > e0 ? lo : e0;
+        const int b = hi < e0 + n ? hi : e0 + n;
+        for (int e = a; e < b; ++e) owner[e - e0] = static_cast<short>(s);
+      }
+      __syncthreads();
+      for (int i = tid; i < n; i += kMergeThreads) {
+        const int s = owner[i];
+        const int lo = s == 0 ? 0 : pre[s - 1];
+        const uint64_t* list =
+            m.lists + ((slot0 + s) * m.qpw + qi) * static_cast<int64_t>(m.capw);
+        buf[held + i] = list[e0 + i - lo];
+      }
     }
     __syncthreads();
     const int cnt = held + n;
     if (cnt > k) {
       const uint64_t kth = block_select_desc(buf, cnt, k, hist, sh);
-      if (tid == 0) sh[2] = 0;
+      if (tid == 0) {
+        sh[2] = 0;
+        sh[3] = 0;
+      }
       __syncthreads();
       for (int i = tid; i < cnt; i += kMergeThreads) {
         const uint64_t v = buf[i];

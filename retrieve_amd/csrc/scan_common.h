@@ -45,7 +45,8 @@ enum ScoreKind : int {
 
 struct MergeArgs {
   const uint64_t* lists;
-  const int* counts;   // null: every list holds capw entries
+  const int* counts;   // per-list lengths (unused when flat)
+  bool flat;           // lists is [B, gx * waves] one-entry lists, contiguous per query
   int capw;
   int qpw;          // queries per scan wave
   int64_t gx;       // scan workgroups per query group
@@ -78,8 +79,18 @@ struct ScanPlan {
   size_t off_lists = 0, off_counts = 0, off_tau = 0, total = 0;
 };
 
-// Sizes the passes for B queries (qpw per wave) over N rows and top-k.
-ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw);
+// Upper bound on a main pass's workgroups (the workspace functions size for it).
+constexpr int64_t kMaxResidentWorkgroups = 4096;
+// Main-pass workgroups per CU: two, each streaming its share of every window of the table
+// (measured best on MI355X; more workgroups only add candidate lists).
+constexpr int64_t kMainWorkgroupsPerCU = 2;
+
+// Main-pass workgroups for the current device: CUs x kMainWorkgroupsPerCU.
+int64_t main_workgroups();
+
+// Sizes the passes for B queries (qpw per wave) over N rows and top-k; the main pass runs
+// target_wgs workgroups across all query groups.
+ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw, int64_t target_wgs);
 
 // Writes the -1 / sentinel pads of an empty result.
 int launch_pad(int64_t* out_ids, void* out_scores, int64_t B, int64_t k, int score_kind,

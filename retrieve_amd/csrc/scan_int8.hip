@@ -6,6 +6,13 @@
 // the scores of query l % 16 for items 4 * (l / 16) + r, r < 4. The K order inside an
 // operand is free (integer sums are exact): lane l feeds bytes [64 s + 16 (l / 16), +16) of
 // its item row and of its query row at step s, the same bytes on both sides.
+//
+// Main pass: a tile (16 contiguous rows, 16 * D bytes) is read with coalesced nontemporal
+// 16-byte loads (each instruction 1 KiB contiguous), staged in the wave's LDS with rows padded
+// by 16 bytes, and read back in the MFMA layout. Tiles are dealt round-robin over all waves of
+// a query group, so the whole GPU streams one contiguous window of the table at a time.
+// Seed pass: the strided sample, read directly in the MFMA layout (rows are not contiguous).
+#include "mfma_topk.h"
 #include "profile.h"
 #include "scan_common.h"
 #include "wave_lists.h"
@@ -14,53 +21,43 @@ namespace rt {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// SEED: the sample pass. Instead of candidate lists each wave keeps, per query, only its best
-// composite over its rows and writes it as a one-entry list (a.capw == 1); the k-th largest of
-// those maxima is a lower bound on the k-th best item (k distinct waves each hold an item at
-// least that good).
-template <int KSTEPS, bool SEED>
-__global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
-  constexpr int QPW = 16;
+template <int KSTEPS>
+__device__ inline void load_query_fragments(const ScanArgs& a, int64_t qrow, int grp, v4i* qf) {
   constexpr int64_t D = KSTEPS * 64;
-  extern __shared__ uint64_t smem[];
-  const int lane = lane_id();
-  const int wave = threadIdx.x >> 6;
-  const int col = lane & 15;
-  const int grp = lane >> 4;
-  uint64_t* scratch = smem + wave * a.capw;
-  int* cnt = reinterpret_cast<int*>(smem + kScanWaves * a.capw) + wave * QPW;
-  const int64_t slot = (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) * kScanWaves +
-                       wave;
-  uint64_t* lists = a.lists + slot * QPW * a.capw;
-  if constexpr (!SEED) {
-    if (lane < QPW) cnt[lane] = 0;
-  }
-
   const int8_t* Q = static_cast<const int8_t*>(a.queries);
-  const int8_t* I = static_cast<const int8_t*>(a.items);
-  const int64_t qrow = static_cast<int64_t>(blockIdx.y) * QPW + col;
-  v4i qf[KSTEPS];
-  uint64_t tau = ~0ull;  // padding query columns never pass
   if (qrow < a.B) {
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
       qf[s] = *reinterpret_cast<const v4i*>(Q + qrow * D + s * 64 + grp * 16);
     }
-    tau = a.tau_in != nullptr ? a.tau_in[qrow] : 0ull;
   } else {
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) qf[s] = v4i{0, 0, 0, 0};
   }
-  int32_t ts = i32_of_key(composite_key(tau));
+}
+
+// Seed pass over the strided sample: each wave keeps, per query, only its best composite over
+// its rows and writes it to a.lists[qrow * S + wave index] (S = waves of the grid row); the
+// k-th largest of those maxima is a lower bound on the k-th best item (k distinct waves each
+// hold an item at least that good).
+template <int KSTEPS>
+__global__ void __launch_bounds__(kScanThreads) seed_int8_kernel(ScanArgs a) {
+  constexpr int64_t D = KSTEPS * 64;
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int8_t* I = static_cast<const int8_t*>(a.items);
+  const int64_t qrow = static_cast<int64_t>(blockIdx.y) * 16 + col;
+  v4i qf[KSTEPS];
+  load_query_fragments<KSTEPS>(a, qrow, grp, qf);
   const uint64_t* qmask =
       a.mask != nullptr && qrow < a.B ? a.mask + qrow * a.mask_words : nullptr;
-  wave_sync_memory();
 
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * a.strip;
   const int64_t r1 = r0 + a.strip < a.n_rows ? r0 + a.strip : a.n_rows;
   const int64_t ntiles = r1 > r0 ? cdiv(r1 - r0, kTile) : 0;
-
-  uint64_t best = 0ull;  // SEED only
+  uint64_t best = 0ull;
   for (int64_t t = wave; t < ntiles; t += kScanWaves) {
     const int64_t rb = r0 + t * kTile;
     int64_t lr = rb + col;
@@ -74,92 +71,150 @@ __global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
     for (int s = 0; s < KSTEPS; ++s) {
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], qf[s], acc, 0, 0, 0);
     }
-    if constexpr (SEED) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = rb + 4 * grp + r;
-        const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
-        bool ok = row < r1;
-        if (ok && qmask != nullptr) ok = (qmask[item >> 6] >> (63 - (item & 63))) & 1ull;
-        const uint64_t c = composite(key_of_i32(acc[r]), item);
-        best = ok && c > best ? c : best;
-      }
-      continue;
-    }
-    const bool hit = acc[0] >= ts || acc[1] >= ts || acc[2] >= ts || acc[3] >= ts;
-    if (!__any(hit)) continue;
-
-    // slow path: exact composite test, filter bit, append
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t row = rb + 4 * grp + r;
-      if (row < r1 && acc[r] >= ts) {
-        const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
-        const uint64_t c = composite(key_of_i32(acc[r]), item);
-        bool keep = c >= tau;
-        if (keep && qmask != nullptr) {
-          keep = (qmask[item >> 6] >> (63 - (item & 63))) & 1ull;
-        }
-        if (keep) {
-          const int pos = atomicAdd(&cnt[col], 1);
-          lists[col * a.capw + pos] = c;
-        }
-      }
-    }
-    wave_sync_memory();
-    const bool full = cnt[col] > a.capw - kTile;
-    uint64_t need = __ballot(full) & 0xffffull;
-    while (need != 0ull) {
-      const int c = __builtin_ctzll(need);
-      need &= need - 1;
-      const uint64_t nt = wave_compact(lists + c * a.capw, &cnt[c], scratch, a.capw, a.k);
-      if (col == c && nt > tau) {
-        tau = nt;
-        ts = i32_of_key(composite_key(nt));
-      }
+      const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
+      bool ok = row < r1;
+      if (ok && qmask != nullptr) ok = (qmask[item >> 6] >> (63 - (item & 63))) & 1ull;
+      const uint64_t c = composite(key_of_i32(acc[r]), item);
+      best = ok && c > best ? c : best;
     }
   }
-  if constexpr (SEED) {
-    uint64_t o = __shfl_xor(best, 16);
-    best = o > best ? o : best;
-    o = __shfl_xor(best, 32);
-    best = o > best ? o : best;
-    if (lane < QPW) lists[lane] = best;
-    return;
+  uint64_t o = __shfl_xor(best, 16);
+  best = o > best ? o : best;
+  o = __shfl_xor(best, 32);
+  best = o > best ? o : best;
+  const int64_t S = static_cast<int64_t>(gridDim.x) * kScanWaves;
+  if (lane < 16 && qrow < a.B) {
+    a.lists[qrow * S + static_cast<int64_t>(blockIdx.x) * kScanWaves + wave] = best;
   }
-  wave_sync_memory();
-  if (lane < QPW) a.counts[slot * QPW + lane] = cnt[lane];
+}
+
+// LDS row pitch of a staged tile: D + 16 bytes, so the 16 rows of an MFMA read start on
+// different banks.
+template <int KSTEPS>
+constexpr int tile_pitch() {
+  return KSTEPS * 64 + 16;
 }
 
 template <int KSTEPS>
-static int launch_scan_int8(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, bool seed,
-                            hipStream_t stream) {
+constexpr size_t main_static_lds() {
+  return static_cast<size_t>(kScanWaves) * kTile * tile_pitch<KSTEPS>();
+}
+
+// Main pass: every item (row_stride 1), candidate lists per wave.
+template <int KSTEPS>
+__global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
+  constexpr int64_t D = KSTEPS * 64;
+  constexpr int P = tile_pitch<KSTEPS>();
+  constexpr int LOADS = KSTEPS;  // 16-byte loads per lane per tile: 16 * D / 1024
+  extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  int8_t* base = reinterpret_cast<int8_t*>(smem);
+  int8_t* stage = base + wave * kTile * P;
+  uint64_t* scratch = reinterpret_cast<uint64_t*>(base + main_static_lds<KSTEPS>()) + wave * a.capw;
+  int* cnt = reinterpret_cast<int*>(base + main_static_lds<KSTEPS>() +
+                                    kScanWaves * a.capw * sizeof(uint64_t)) + wave * 16;
+  const int64_t wave_in_group = static_cast<int64_t>(blockIdx.x) * kScanWaves + wave;
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * kScanWaves;
+  const int64_t slot = static_cast<int64_t>(blockIdx.y) * waves + wave_in_group;
+  if (lane < 16) cnt[lane] = 0;
+
+  const int8_t* I = static_cast<const int8_t*>(a.items);
+  const int64_t qrow = static_cast<int64_t>(blockIdx.y) * 16 + col;
+  v4i qf[KSTEPS];
+  load_query_fragments<KSTEPS>(a, qrow, grp, qf);
+  WaveTopK16<int32_t> top;
+  top.lists = a.lists + slot * 16 * a.capw;
+  top.cnt = cnt;
+  top.scratch = scratch;
+  top.capw = a.capw;
+  top.k = a.k;
+  top.qmask = a.mask != nullptr && qrow < a.B ? a.mask + qrow * a.mask_words : nullptr;
+  top.set_tau(qrow < a.B ? (a.tau_in != nullptr ? a.tau_in[qrow] : 0ull) : ~0ull);
+  wave_sync_memory();
+
+  const int64_t n = a.n_rows;
+  const int64_t ntiles = cdiv(n, kTile);
+  // load j of a tile covers its bytes [1024 j + 16 lane, +16): row (1024 j + 16 lane) / D
+  v4i v[LOADS];
+  auto load_tile = [&](int64_t t) {
+    const int64_t base_row = t * kTile;
+    const v4i* src = reinterpret_cast<const v4i*>(I + base_row * D) + lane;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int off = 1024 * j + 16 * lane;
+      const int64_t row = base_row + off / D;
+      v[j] = row < n ? __builtin_nontemporal_load(src + 64 * j) : v4i{0, 0, 0, 0};
+    }
+  };
+
+  int64_t t = wave_in_group;
+  if (t < ntiles) load_tile(t);
+  for (; t < ntiles; t += waves) {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int off = 1024 * j + 16 * lane;
+      *reinterpret_cast<v4i*>(stage + (off / D) * P + off % D) = v[j];
+    }
+    wave_sync_memory();
+    v4i af[KSTEPS];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      af[s] = *reinterpret_cast<const v4i*>(stage + col * P + grp * 16 + s * 64);
+    }
+    if (t + waves < ntiles) load_tile(t + waves);
+    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], qf[s], acc, 0, 0, 0);
+    }
+    const int32_t sc[4] = {acc[0], acc[1], acc[2], acc[3]};
+    top.push(sc, t * kTile + 4 * grp, n, 1);
+    wave_sync_memory();
+  }
+  wave_sync_memory();
+  if (lane < 16) a.counts[slot * 16 + lane] = cnt[lane];
+}
+
+template <int KSTEPS>
+static size_t main_lds_bytes(int capw) {
+  return main_static_lds<KSTEPS>() + kScanWaves * (capw * sizeof(uint64_t) + 16 * sizeof(int));
+}
+
+template <int KSTEPS>
+static int launch_int8(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, bool seed,
+                       hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.gx), static_cast<unsigned>(n_qgroups));
   if (seed) {
-    scan_int8_kernel<KSTEPS, true><<<grid, kScanThreads, 0, stream>>>(a);
+    seed_int8_kernel<KSTEPS><<<grid, kScanThreads, 0, stream>>>(a);
     RT_CHECK_HIP(hipGetLastError());
     return kOk;
   }
-  const size_t lds = kScanWaves * (p.capw * sizeof(uint64_t) + 16 * sizeof(int));
+  const size_t lds = main_lds_bytes<KSTEPS>(p.capw);
   if (lds > 65536) {
-    RT_CHECK_HIP(hipFuncSetAttribute(
-        reinterpret_cast<const void*>(scan_int8_kernel<KSTEPS, false>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(scan_int8_kernel<KSTEPS>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds)));
   }
-  scan_int8_kernel<KSTEPS, false><<<grid, kScanThreads, lds, stream>>>(a);
+  scan_int8_kernel<KSTEPS><<<grid, kScanThreads, lds, stream>>>(a);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }
 
-static int dispatch_scan_int8(int64_t D, const ScanArgs& a, const PassPlan& p, int64_t nqg,
-                              bool seed, hipStream_t stream) {
+static int dispatch_int8(int64_t D, const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed,
+                         hipStream_t stream) {
   switch (D) {
-    case 64: return launch_scan_int8<1>(a, p, nqg, seed, stream);
-    case 128: return launch_scan_int8<2>(a, p, nqg, seed, stream);
-    case 256: return launch_scan_int8<4>(a, p, nqg, seed, stream);
-    case 512: return launch_scan_int8<8>(a, p, nqg, seed, stream);
-    case 768: return launch_scan_int8<12>(a, p, nqg, seed, stream);
-    case 1024: return launch_scan_int8<16>(a, p, nqg, seed, stream);
+    case 64: return launch_int8<1>(a, p, nqg, seed, stream);
+    case 128: return launch_int8<2>(a, p, nqg, seed, stream);
+    case 256: return launch_int8<4>(a, p, nqg, seed, stream);
+    case 512: return launch_int8<8>(a, p, nqg, seed, stream);
+    case 768: return launch_int8<12>(a, p, nqg, seed, stream);
+    case 1024: return launch_int8<16>(a, p, nqg, seed, stream);
     default:
       set_error("int8 scan supports D in {64, 128, 256, 512, 768, 1024}, got %lld",
                 static_cast<long long>(D));
@@ -173,7 +228,7 @@ using namespace rt;
 
 extern "C" size_t rt_int8_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
   (void)D;
-  return plan_scan(B, N, k, 16).total;
+  return plan_scan(B, N, k, 16, kMaxResidentWorkgroups).total;
 }
 
 extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t* items,
@@ -189,7 +244,8 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
                "queries and items must be 16-byte aligned");
   RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
   if (B == 0) return kOk;
-  const ScanPlan plan = plan_scan(B, N, k, 16);
+  if (N == 0) return launch_pad(out_ids, out_scores, B, k, kScoreI32, stream);
+  const ScanPlan plan = plan_scan(B, N, k, 16, main_workgroups());
   if (workspace_bytes < plan.total) {
     set_error("workspace too small: %zu < %zu", workspace_bytes, plan.total);
     return kWorkspaceTooSmall;
@@ -216,41 +272,35 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
   m.B = B;
   m.k = static_cast<int>(k);
 
-  if (N == 0) {
-    // nothing to score: -1 / INT32_MIN pads
-    return launch_pad(out_ids, out_scores, B, k, kScoreI32, stream);
-  }
-  {
-    if (plan.seeded) {
-      a.n_rows = plan.seed.n_rows;
-      a.row_stride = plan.seed.row_stride;
-      a.strip = plan.seed.strip;
-      a.capw = plan.seed.capw;
-      a.tau_in = nullptr;
-      int st = dispatch_scan_int8(D, a, plan.seed, plan.n_qgroups, true, stream);
-      if (st != kOk) return st;
-      m.capw = 1;
-      m.counts = nullptr;  // one entry per list: each seed wave's best
-      m.gx = plan.seed.gx;
-      m.tau_out = tau;
-      st = launch_merge(m, stream);
-      if (st != kOk) return st;
-      m.tau_out = nullptr;
-      m.counts = counts;
-    }
-    a.n_rows = plan.main.n_rows;
-    a.row_stride = 1;
-    a.strip = plan.main.strip;
-    a.capw = plan.main.capw;
-    a.tau_in = plan.seeded ? tau : nullptr;
-    hipEvent_t stop;
-    profile_begin(stream, &stop);
-    int st = dispatch_scan_int8(D, a, plan.main, plan.n_qgroups, false, stream);
-    profile_end(stream, stop);
+  if (plan.seeded) {
+    a.n_rows = plan.seed.n_rows;
+    a.row_stride = plan.seed.row_stride;
+    a.strip = plan.seed.strip;
+    a.capw = 1;
+    a.tau_in = nullptr;
+    int st = dispatch_int8(D, a, plan.seed, plan.n_qgroups, true, stream);
     if (st != kOk) return st;
-    m.capw = plan.main.capw;
-    m.gx = plan.main.gx;
+    m.capw = 1;
+    m.flat = true;  // one entry per seed wave, contiguous per query
+    m.gx = plan.seed.gx;
+    m.tau_out = tau;
+    st = launch_merge(m, stream);
+    if (st != kOk) return st;
+    m.tau_out = nullptr;
+    m.flat = false;
   }
+  a.n_rows = N;
+  a.row_stride = 1;
+  a.strip = plan.main.strip;
+  a.capw = plan.main.capw;
+  a.tau_in = plan.seeded ? tau : nullptr;
+  hipEvent_t stop;
+  profile_begin(stream, &stop);
+  int st = dispatch_int8(D, a, plan.main, plan.n_qgroups, false, stream);
+  profile_end(stream, stop);
+  if (st != kOk) return st;
+  m.capw = plan.main.capw;
+  m.gx = plan.main.gx;
   m.out_ids = out_ids;
   m.out_scores = out_scores;
   m.score_kind = kScoreI32;
