@@ -43,6 +43,32 @@ int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t* items, int
                       int64_t* out_ids, int32_t* out_scores, void* workspace,
                       size_t workspace_bytes, rt_stream_t stream);
 
+/* Dense (bf16 / fp16) full-scan top-k: queries [B, D] x items [N, D] of the same 16-bit type
+ * (dtype 0 = bf16, 1 = fp16), fp32 accumulation on the matrix cores, top-k by
+ * (score desc, index asc) -> ids int64 [B, k], scores float [B, k]. D in {32, 64, 128, 256,
+ * 384, 512}; 1 <= k <= 1024. `mask` as for rt_int8_scan_topk.
+ * Replaces: PostfilterKNN's torch.mm(q, E_t, out_dtype=fp32) + masked_topk / two_level_topk
+ *   (retrieve/src/retrieve/modules/knn.py:62-76, retrieve/src/retrieve/functional.py:30-85)
+ *   for LiNR V1's dense scores, fused so the [B, N] score matrix is never written. */
+size_t rt_dense_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k);
+int rt_dense_scan_topk(const void* queries, int64_t B, const void* items, int64_t N, int64_t D,
+                       int64_t k, int dtype, const uint64_t* mask, int64_t mask_words,
+                       int64_t* out_ids, float* out_scores, void* workspace,
+                       size_t workspace_bytes, rt_stream_t stream);
+
+/* Exact 1-bit Hamming top-k over a full code table: query_bits [B, W] x item_bits [N, W]
+ * (uint64 words, bit b of word w = dimension 64 w + b), score = 64 W - 2 popcount(q ^ item),
+ * top-k by (score desc, index asc) -> ids int64 [B, k], scores [B, k] (int32, or float when
+ * score_f32 != 0). W in {1, 2, 4, 8, 16}; 1 <= k <= 1024. `mask` as for rt_int8_scan_topk.
+ * Replaces: the Triton full-scan kernel + torch.topk of
+ *   retrieve/src/retrieve/ops/triton/oporp_1bit_match_topk.py:47-122, 217-234, 261-273
+ *   (torch.ops.retrieve.oporp_1bit_match_topk_full). */
+size_t rt_hamming_scan_topk_workspace(int64_t B, int64_t N, int64_t W, int64_t k);
+int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits,
+                         int64_t N, int64_t W, int64_t k, const uint64_t* mask,
+                         int64_t mask_words, int64_t* out_ids, void* out_scores, int score_f32,
+                         void* workspace, size_t workspace_bytes, rt_stream_t stream);
+
 /* Benchmark support (no counterpart in the reference): when enabled, every call brackets its
  * dominant kernel (the main scan) with a HIP event pair on its stream; collect() waits for
  * the recorded pairs, returns their summed milliseconds and count, and clears them. */

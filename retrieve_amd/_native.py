@@ -25,6 +25,18 @@ _c_int = ctypes.c_int
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rt_last_error": (ctypes.c_char_p, []),
     "rt_int8_scan_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "rt_hamming_scan_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "rt_hamming_scan_topk": (
+        _c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_int, _c_p,
+         _c_sz, _c_p],
+    ),
+    "rt_dense_scan_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "rt_dense_scan_topk": (
+        _c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_p, _c_p,
+         _c_sz, _c_p],
+    ),
     "rt_profile_enable": (_c_int, [_c_int]),
     "rt_profile_collect": (_c_int, [_c_p, _c_p]),
     "rt_int8_scan_topk": (

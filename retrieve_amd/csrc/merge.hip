@@ -28,12 +28,12 @@ static constexpr int64_t kTargetWorkgroups = 2048;
 // Rows of the seed sample; the main pass then keeps about k * N / kSeedRows composites a
 // query (in expectation, for items in random order).
 static constexpr int64_t kSeedRows = 1 << 18;
-// Sample rows per seed workgroup (16 per wave, one tile each): many waves, so the k-th largest
-// of their maxima is close to the k-th best of the sample.
-static constexpr int64_t kSeedRowsPerWorkgroup = 64;
+// At least this many sampled rows per wanted item (keeps the main pass's candidates near
+// k * N / seed_rows for large k).
+static constexpr int64_t kSeedRowsPerK = 1024;
 // Upper bound on the candidate lists' workspace (a pass may exceed it only at one workgroup
 // per query group).
-static constexpr int64_t kMaxListBytes = int64_t{512} << 20;
+static constexpr int64_t kMaxListBytes = int64_t{2} << 30;
 
 static PassPlan plan_pass(int64_t n_rows, int64_t row_stride, int64_t n_qgroups, int64_t min_rows,
                           int capw, int qpw, int64_t target_wgs, int64_t min_gx = 1) {
@@ -74,16 +74,16 @@ int64_t main_workgroups() {
   return t < kMaxResidentWorkgroups ? t : kMaxResidentWorkgroups;
 }
 
-ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw, int64_t target_wgs) {
+ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw, int64_t target_wgs, int main_capw,
+                   int tile_rows) {
   ScanPlan s;
   s.qpw = qpw;
   s.n_qgroups = cdiv(B, qpw);
-  const int main_capw = static_cast<int>(next_pow2(k + 2 * kTile));
-  const int64_t seed_rows = kSeedRows > 16 * k ? kSeedRows : 16 * k;
+  const int64_t seed_rows = kSeedRows > kSeedRowsPerK * k ? kSeedRows : kSeedRowsPerK * k;
   s.seeded = N >= 8 * seed_rows;
   if (s.seeded) {
-    // one-entry lists (each seed wave's best); at least k waves per query group
-    s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, kSeedRowsPerWorkgroup, 1, qpw,
+    // one-entry lists (each seed wave's best); at least k workgroups (4k waves) per group
+    s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, kScanWaves * tile_rows, 1, qpw,
                        kTargetWorkgroups, k);
   }
   s.main = plan_pass(N, 1, s.n_qgroups, 1024, main_capw, qpw, target_wgs);
@@ -100,25 +100,74 @@ ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw, int64_t target_wgs)
 
 // ---- merge ------------------------------------------------------------------------------
 
-constexpr int kMergeChunk = 4096;  // list entries gathered into LDS per round
+constexpr int kMergeChunk = 10240;  // list entries gathered into LDS per round
+constexpr int kMergeWaves = kMergeThreads / kWave;
 
-// Block-wide radix select over keys[0, n) in LDS, MSB-first 8-bit digits. Returns a bound T
-// such that exactly kth keys are >= T (the keys are distinct except for repeated zeros): the
-// kth largest key, or, when a digit pass finds the kth largest key's bucket holding exactly the
+// Block-wide min and max of keys[0, n) (LDS). Every thread calls it; all get the results.
+__device__ void block_minmax(const uint64_t* keys, int n, uint64_t* red, uint64_t* lo,
+                             uint64_t* hi) {
+  const int tid = threadIdx.x;
+  uint64_t a = ~0ull;
+  uint64_t b = 0ull;
+  for (int i = tid; i < n; i += blockDim.x) {
+    const uint64_t v = keys[i];
+    a = v < a ? v : a;
+    b = v > b ? v : b;
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const uint64_t oa = __shfl_xor(a, off);
+    const uint64_t ob = __shfl_xor(b, off);
+    a = oa < a ? oa : a;
+    b = ob > b ? ob : b;
+  }
+  if ((tid & (kWave - 1)) == 0) {
+    red[2 * (tid / kWave)] = a;
+    red[2 * (tid / kWave) + 1] = b;
+  }
+  __syncthreads();
+  a = ~0ull;
+  b = 0ull;
+  for (int w = 0; w < static_cast<int>(blockDim.x) / kWave; ++w) {
+    a = red[2 * w] < a ? red[2 * w] : a;
+    b = red[2 * w + 1] > b ? red[2 * w + 1] : b;
+  }
+  *lo = a;
+  *hi = b;
+  __syncthreads();
+}
+
+// Block-wide radix select over keys[0, n) in LDS, MSB-first digits of up to 8 bits, starting
+// below the bits every key shares (min and max agree there). Returns a bound T such that
+// exactly kth keys are >= T (the keys are distinct except for repeated zeros): the kth
+// largest key, or, when a digit pass finds the kth largest key's bucket holding exactly the
 // keys still wanted, that bucket's lowest possible value (the search stops there).
 // 1 <= kth <= n. Every thread of the block calls it.
 __device__ uint64_t block_select_desc(const uint64_t* keys, int n, int kth, unsigned* hist,
-                                      int* sh) {
+                                      int* sh, uint64_t* red) {
   const int tid = threadIdx.x;
-  uint64_t prefix = 0ull;
-  uint64_t mask = 0ull;
-  if (tid == 0) sh[1] = kth;
-  for (int shift = 56; shift >= 0; shift -= 8) {
+  uint64_t kmin;
+  uint64_t kmax;
+  block_minmax(keys, n, red, &kmin, &kmax);
+  const uint64_t diff = kmin ^ kmax;
+  if (diff == 0ull) return kmin;
+  int top = 63 - __builtin_clzll(diff);  // highest bit where keys differ
+  uint64_t mask = top == 63 ? 0ull : ~((2ull << top) - 1ull);
+  uint64_t prefix = kmin & mask;
+  if (tid == 0) {
+    sh[1] = kth;
+    sh[3] = 0;
+  }
+  __syncthreads();
+  while (true) {
+    const int low = top >= 7 ? top - 7 : 0;
+    const int width = top - low + 1;
+    const uint64_t dmask = (1ull << width) - 1ull;
     for (int i = tid; i < 256; i += blockDim.x) hist[i] = 0u;
     __syncthreads();
     for (int i = tid; i < n; i += blockDim.x) {
       const uint64_t v = keys[i];
-      if ((v & mask) == prefix) atomicAdd(&hist[(v >> shift) & 255ull], 1u);
+      if ((v & mask) == prefix) atomicAdd(&hist[(v >> low) & dmask], 1u);
     }
     __syncthreads();
     if (tid < kWave) {
@@ -154,11 +203,12 @@ __device__ uint64_t block_select_desc(const uint64_t* keys, int n, int kth, unsi
       }
     }
     __syncthreads();
-    prefix |= static_cast<uint64_t>(sh[0]) << shift;
-    mask |= 255ull << shift;
-    const bool done = sh[3] != 0;
+    prefix |= static_cast<uint64_t>(sh[0]) << low;
+    mask |= dmask << low;
+    const bool done = sh[3] != 0 || low == 0;
     __syncthreads();
     if (done) break;
+    top = low - 1;
   }
   return prefix;
 }
@@ -176,6 +226,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   __shared__ short owner[kMergeChunk];
   __shared__ unsigned hist[256];
   __shared__ int part[kMergeThreads];
+  __shared__ uint64_t red[2 * kMergeWaves];
   __shared__ int sh[4];
   const int tid = threadIdx.x;
   const int64_t q = blockIdx.x;
@@ -218,7 +269,6 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     __syncthreads();
     total = pre[S - 1];
   }
-  if (tid == 0) sh[3] = 0;
 
   int held = 0;
   for (int e0 = 0; e0 < total; e0 += kMergeChunk) {
@@ -228,7 +278,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
       for (int i = tid; i < n; i += kMergeThreads) buf[held + i] = row[e0 + i];
     } else {
       // owner[] maps each entry of the window to its list (LDS only), then every thread
-      // loads independent entries
+      // loads independent entries, four in flight
       for (int s = tid; s < S; s += kMergeThreads) {
         const int lo = s == 0 ? 0 : pre[s - 1];
         const int hi = pre[s];
@@ -237,22 +287,31 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
         for (int e = a; e < b; ++e) owner[e - e0] = static_cast<short>(s);
       }
       __syncthreads();
-      for (int i = tid; i < n; i += kMergeThreads) {
-        const int s = owner[i];
-        const int lo = s == 0 ? 0 : pre[s - 1];
-        const uint64_t* list =
-            m.lists + ((slot0 + s) * m.qpw + qi) * static_cast<int64_t>(m.capw);
-        buf[held + i] = list[e0 + i - lo];
+      for (int i0 = tid; i0 < n; i0 += 4 * kMergeThreads) {
+        uint64_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = i0 + u * kMergeThreads;
+          v[u] = 0ull;
+          if (i < n) {
+            const int s = owner[i];
+            const int lo = s == 0 ? 0 : pre[s - 1];
+            v[u] = m.lists[((slot0 + s) * m.qpw + qi) * static_cast<int64_t>(m.capw) +
+                           (e0 + i - lo)];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = i0 + u * kMergeThreads;
+          if (i < n) buf[held + i] = v[u];
+        }
       }
     }
     __syncthreads();
     const int cnt = held + n;
     if (cnt > k) {
-      const uint64_t kth = block_select_desc(buf, cnt, k, hist, sh);
-      if (tid == 0) {
-        sh[2] = 0;
-        sh[3] = 0;
-      }
+      const uint64_t kth = block_select_desc(buf, cnt, k, hist, sh, red);
+      if (tid == 0) sh[2] = 0;
       __syncthreads();
       for (int i = tid; i < cnt; i += kMergeThreads) {
         const uint64_t v = buf[i];

@@ -16,7 +16,7 @@ namespace rt {
 constexpr int kScanWaves = 4;       // waves per scan workgroup
 constexpr int kScanThreads = kScanWaves * kWave;
 constexpr int kTile = 16;           // items per MFMA tile
-constexpr int kMergeThreads = 256;
+constexpr int kMergeThreads = 512;
 constexpr int64_t kMaxK = 1024;
 constexpr int64_t kMaxMergeSlots = 8192;  // lists a query's merge reads (gx * waves)
 
@@ -29,7 +29,8 @@ struct ScanArgs {
   int64_t row_stride;      // item index = row * row_stride (the sample pass strides)
   int64_t strip;           // rows per workgroup, a multiple of kTile
   int k;
-  int capw;                // list capacity (power of two, >= k + kTile)
+  int qpw;                 // queries per wave (a query group), for scans that vary it
+  int capw;                // list capacity (>= k + the appends one tile can make)
   const uint64_t* tau_in;  // [B] lower bounds (composites) or null
   const uint64_t* mask;    // [B, mask_words] item bits, item d at bit 63 - d % 64, or null
   int64_t mask_words;
@@ -89,8 +90,10 @@ constexpr int64_t kMainWorkgroupsPerCU = 2;
 int64_t main_workgroups();
 
 // Sizes the passes for B queries (qpw per wave) over N rows and top-k; the main pass runs
-// target_wgs workgroups across all query groups.
-ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw, int64_t target_wgs);
+// target_wgs workgroups across all query groups with lists of main_capw entries; a scan wave
+// scores tiles of tile_rows rows.
+ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw, int64_t target_wgs, int main_capw,
+                   int tile_rows);
 
 // Writes the -1 / sentinel pads of an empty result.
 int launch_pad(int64_t* out_ids, void* out_scores, int64_t B, int64_t k, int score_kind,

@@ -1,11 +1,14 @@
-// int8 × int8 → int32 full scan with the exact fused top-k (SilverTorch's int8 scorer
-// semantics: int32 accumulation, ties to the lower item index).
+// Dense full scans with the exact fused top-k, on the matrix cores: int8 × int8 → int32
+// (SilverTorch's int8 scorer semantics: int32 accumulation; v_mfma_i32_16x16x64_i8) and
+// bf16 / fp16 × same → fp32 (LiNR's dense scores; v_mfma_f32_16x16x32_bf16 / _f16). Ties go to
+// the lower item index.
 //
-// Each wave multiplies 16-item tiles of the item table against its 16 queries with
-// v_mfma_i32_16x16x64_i8 (items as the A operand, queries as B), so after a tile lane l holds
-// the scores of query l % 16 for items 4 * (l / 16) + r, r < 4. The K order inside an
-// operand is free (integer sums are exact): lane l feeds bytes [64 s + 16 (l / 16), +16) of
-// its item row and of its query row at step s, the same bytes on both sides.
+// Each wave multiplies 16-item tiles of the item table against its 16 queries (items as the
+// A operand, queries as B), so after a tile lane l holds the scores of query l % 16 for items
+// 4 * (l / 16) + r, r < 4. Every MFMA consumes 64 bytes of each row: lane l feeds bytes
+// [64 s + 16 (l / 16), +16) of its item row and of its query row at step s, the same bytes on
+// both sides (the K order inside an operand is free: exact for integers, and within the fp32
+// rounding the tolerance covers for the float types).
 //
 // Main pass: a tile (16 contiguous rows, 16 * D bytes) is read with coalesced nontemporal
 // 16-byte loads (each instruction 1 KiB contiguous), staged in the wave's LDS with rows padded
@@ -20,10 +23,47 @@
 namespace rt {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
+// One MFMA step (64 bytes of K) per element type. Score is the per-item score type.
+struct I8Op {
+  using Score = int32_t;
+  using Acc = v4i;
+  static constexpr int kind = kScoreI32;
+  __device__ static Acc zero() { return Acc{0, 0, 0, 0}; }
+  __device__ static Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+};
+
+struct BF16Op {
+  using Score = float;
+  using Acc = v4f;
+  static constexpr int kind = kScoreF32;
+  __device__ static Acc zero() { return Acc{0.f, 0.f, 0.f, 0.f}; }
+  __device__ static Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a),
+                                                   __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+  }
+};
+
+struct F16Op {
+  using Score = float;
+  using Acc = v4f;
+  static constexpr int kind = kScoreF32;
+  __device__ static Acc zero() { return Acc{0.f, 0.f, 0.f, 0.f}; }
+  __device__ static Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a),
+                                                  __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+  }
+};
+
+// KSTEPS = row bytes / 64 (D * element size / 64).
 template <int KSTEPS>
 __device__ inline void load_query_fragments(const ScanArgs& a, int64_t qrow, int grp, v4i* qf) {
-  constexpr int64_t D = KSTEPS * 64;
+  constexpr int64_t D = KSTEPS * 64;  // row bytes
   const int8_t* Q = static_cast<const int8_t*>(a.queries);
   if (qrow < a.B) {
 #pragma unroll
@@ -40,9 +80,10 @@ __device__ inline void load_query_fragments(const ScanArgs& a, int64_t qrow, int
 // its rows and writes it to a.lists[qrow * S + wave index] (S = waves of the grid row); the
 // k-th largest of those maxima is a lower bound on the k-th best item (k distinct waves each
 // hold an item at least that good).
-template <int KSTEPS>
-__global__ void __launch_bounds__(kScanThreads) seed_int8_kernel(ScanArgs a) {
-  constexpr int64_t D = KSTEPS * 64;
+template <class Op, int KSTEPS>
+__global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
+  using Score = typename Op::Score;
+  constexpr int64_t D = KSTEPS * 64;  // row bytes
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
@@ -66,18 +107,16 @@ __global__ void __launch_bounds__(kScanThreads) seed_int8_kernel(ScanArgs a) {
     v4i af[KSTEPS];
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) af[s] = *reinterpret_cast<const v4i*>(ip + s * 64);
-    v4i acc = {0, 0, 0, 0};
+    typename Op::Acc acc = Op::zero();
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], qf[s], acc, 0, 0, 0);
-    }
+    for (int s = 0; s < KSTEPS; ++s) acc = Op::mma(af[s], qf[s], acc);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t row = rb + 4 * grp + r;
       const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
       bool ok = row < r1;
       if (ok && qmask != nullptr) ok = (qmask[item >> 6] >> (63 - (item & 63))) & 1ull;
-      const uint64_t c = composite(key_of_i32(acc[r]), item);
+      const uint64_t c = composite(KeyOps<Score>::key(acc[r]), item);
       best = ok && c > best ? c : best;
     }
   }
@@ -104,9 +143,10 @@ constexpr size_t main_static_lds() {
 }
 
 // Main pass: every item (row_stride 1), candidate lists per wave.
-template <int KSTEPS>
-__global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
-  constexpr int64_t D = KSTEPS * 64;
+template <class Op, int KSTEPS>
+__global__ void __launch_bounds__(kScanThreads) scan_mfma_kernel(ScanArgs a) {
+  using Score = typename Op::Score;
+  constexpr int64_t D = KSTEPS * 64;  // row bytes
   constexpr int P = tile_pitch<KSTEPS>();
   constexpr int LOADS = KSTEPS;  // 16-byte loads per lane per tile: 16 * D / 1024
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
@@ -128,7 +168,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
   const int64_t qrow = static_cast<int64_t>(blockIdx.y) * 16 + col;
   v4i qf[KSTEPS];
   load_query_fragments<KSTEPS>(a, qrow, grp, qf);
-  WaveTopK16<int32_t> top;
+  WaveTopK16<Score> top;
   top.lists = a.lists + slot * 16 * a.capw;
   top.cnt = cnt;
   top.scratch = scratch;
@@ -168,12 +208,10 @@ __global__ void __launch_bounds__(kScanThreads) scan_int8_kernel(ScanArgs a) {
       af[s] = *reinterpret_cast<const v4i*>(stage + col * P + grp * 16 + s * 64);
     }
     if (t + waves < ntiles) load_tile(t + waves);
-    v4i acc = {0, 0, 0, 0};
+    typename Op::Acc acc = Op::zero();
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], qf[s], acc, 0, 0, 0);
-    }
-    const int32_t sc[4] = {acc[0], acc[1], acc[2], acc[3]};
+    for (int s = 0; s < KSTEPS; ++s) acc = Op::mma(af[s], qf[s], acc);
+    const Score sc[4] = {acc[0], acc[1], acc[2], acc[3]};
     top.push(sc, t * kTile + 4 * grp, n, 1);
     wave_sync_memory();
   }
@@ -186,55 +224,54 @@ static size_t main_lds_bytes(int capw) {
   return main_static_lds<KSTEPS>() + kScanWaves * (capw * sizeof(uint64_t) + 16 * sizeof(int));
 }
 
-template <int KSTEPS>
-static int launch_int8(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, bool seed,
+template <class Op, int KSTEPS>
+static int launch_mfma(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, bool seed,
                        hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.gx), static_cast<unsigned>(n_qgroups));
   if (seed) {
-    seed_int8_kernel<KSTEPS><<<grid, kScanThreads, 0, stream>>>(a);
+    seed_mfma_kernel<Op, KSTEPS><<<grid, kScanThreads, 0, stream>>>(a);
     RT_CHECK_HIP(hipGetLastError());
     return kOk;
   }
   const size_t lds = main_lds_bytes<KSTEPS>(p.capw);
   if (lds > 65536) {
-    RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(scan_int8_kernel<KSTEPS>),
+    RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(scan_mfma_kernel<Op, KSTEPS>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds)));
   }
-  scan_int8_kernel<KSTEPS><<<grid, kScanThreads, lds, stream>>>(a);
+  scan_mfma_kernel<Op, KSTEPS><<<grid, kScanThreads, lds, stream>>>(a);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }
 
-static int dispatch_int8(int64_t D, const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed,
-                         hipStream_t stream) {
-  switch (D) {
-    case 64: return launch_int8<1>(a, p, nqg, seed, stream);
-    case 128: return launch_int8<2>(a, p, nqg, seed, stream);
-    case 256: return launch_int8<4>(a, p, nqg, seed, stream);
-    case 512: return launch_int8<8>(a, p, nqg, seed, stream);
-    case 768: return launch_int8<12>(a, p, nqg, seed, stream);
-    case 1024: return launch_int8<16>(a, p, nqg, seed, stream);
+// Row sizes supported: 64, 128, 256, 512, 768, 1024 bytes (int8 D; half the D for 16-bit).
+template <class Op>
+static int dispatch_mfma(int64_t row_bytes, const ScanArgs& a, const PassPlan& p, int64_t nqg,
+                         bool seed, hipStream_t stream) {
+  switch (row_bytes) {
+    case 64: return launch_mfma<Op, 1>(a, p, nqg, seed, stream);
+    case 128: return launch_mfma<Op, 2>(a, p, nqg, seed, stream);
+    case 256: return launch_mfma<Op, 4>(a, p, nqg, seed, stream);
+    case 512: return launch_mfma<Op, 8>(a, p, nqg, seed, stream);
+    case 768: return launch_mfma<Op, 12>(a, p, nqg, seed, stream);
+    case 1024: return launch_mfma<Op, 16>(a, p, nqg, seed, stream);
     default:
-      set_error("int8 scan supports D in {64, 128, 256, 512, 768, 1024}, got %lld",
-                static_cast<long long>(D));
+      set_error("dense scan supports rows of 64, 128, 256, 512, 768 or 1024 bytes, got %lld",
+                static_cast<long long>(row_bytes));
       return kInvalidArgument;
   }
 }
 
-}  // namespace rt
+// List capacity: k kept after a compaction plus room for the next tiles' appends (a tile adds
+// at most 16 per query), a power of two (the compaction sorts it whole).
+static int mfma_capw(int64_t k) { return static_cast<int>(next_pow2(k + 2 * kTile)); }
 
-using namespace rt;
-
-extern "C" size_t rt_int8_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
-  (void)D;
-  return plan_scan(B, N, k, 16, kMaxResidentWorkgroups).total;
-}
-
-extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t* items,
-                                 int64_t N, int64_t D, int64_t k, const uint64_t* mask,
-                                 int64_t mask_words, int64_t* out_ids, int32_t* out_scores,
-                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+// seed scan → seed threshold merge → main scan → final merge, on `stream`, no host sync
+template <class Op>
+static int run_mfma_scan(const void* queries, int64_t B, const void* items, int64_t N,
+                         int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
+                         int64_t* out_ids, void* out_scores, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
   RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
   RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
                static_cast<long long>(kMaxK), static_cast<long long>(k));
@@ -244,8 +281,8 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
                "queries and items must be 16-byte aligned");
   RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
   if (B == 0) return kOk;
-  if (N == 0) return launch_pad(out_ids, out_scores, B, k, kScoreI32, stream);
-  const ScanPlan plan = plan_scan(B, N, k, 16, main_workgroups());
+  if (N == 0) return launch_pad(out_ids, out_scores, B, k, Op::kind, stream);
+  const ScanPlan plan = plan_scan(B, N, k, 16, main_workgroups(), mfma_capw(k), kTile);
   if (workspace_bytes < plan.total) {
     set_error("workspace too small: %zu < %zu", workspace_bytes, plan.total);
     return kWorkspaceTooSmall;
@@ -260,6 +297,7 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
   a.B = B;
   a.items = items;
   a.k = static_cast<int>(k);
+  a.qpw = 16;
   a.mask = mask;
   a.mask_words = mask_words;
   a.lists = lists;
@@ -278,7 +316,7 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
     a.strip = plan.seed.strip;
     a.capw = 1;
     a.tau_in = nullptr;
-    int st = dispatch_int8(D, a, plan.seed, plan.n_qgroups, true, stream);
+    int st = dispatch_mfma<Op>(row_bytes, a, plan.seed, plan.n_qgroups, true, stream);
     if (st != kOk) return st;
     m.capw = 1;
     m.flat = true;  // one entry per seed wave, contiguous per query
@@ -296,13 +334,51 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
   a.tau_in = plan.seeded ? tau : nullptr;
   hipEvent_t stop;
   profile_begin(stream, &stop);
-  int st = dispatch_int8(D, a, plan.main, plan.n_qgroups, false, stream);
+  int st = dispatch_mfma<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, stream);
   profile_end(stream, stop);
   if (st != kOk) return st;
   m.capw = plan.main.capw;
   m.gx = plan.main.gx;
   m.out_ids = out_ids;
   m.out_scores = out_scores;
-  m.score_kind = kScoreI32;
+  m.score_kind = Op::kind;
   return launch_merge(m, stream);
+}
+
+}  // namespace rt
+
+using namespace rt;
+
+extern "C" size_t rt_int8_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
+  (void)D;
+  return plan_scan(B, N, k, 16, kMaxResidentWorkgroups, mfma_capw(k), kTile).total;
+}
+
+extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t* items,
+                                 int64_t N, int64_t D, int64_t k, const uint64_t* mask,
+                                 int64_t mask_words, int64_t* out_ids, int32_t* out_scores,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return run_mfma_scan<I8Op>(queries, B, items, N, D, k, mask, mask_words, out_ids, out_scores,
+                             workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t rt_dense_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
+  (void)D;
+  return plan_scan(B, N, k, 16, kMaxResidentWorkgroups, mfma_capw(k), kTile).total;
+}
+
+extern "C" int rt_dense_scan_topk(const void* queries, int64_t B, const void* items, int64_t N,
+                                  int64_t D, int64_t k, int dtype, const uint64_t* mask,
+                                  int64_t mask_words, int64_t* out_ids, float* out_scores,
+                                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (dtype == 0) {
+    return run_mfma_scan<BF16Op>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
+                                 out_scores, workspace, workspace_bytes, stream);
+  }
+  if (dtype == 1) {
+    return run_mfma_scan<F16Op>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
+                                out_scores, workspace, workspace_bytes, stream);
+  }
+  set_error("dense scan dtype must be 0 (bf16) or 1 (fp16), got %d", dtype);
+  return kInvalidType;
 }

@@ -40,19 +40,19 @@ __device__ inline void wave_sort_desc(uint64_t* s, int n) {
   }
 }
 
-// Sorts list[0, *count) (global) through `scratch` (LDS, capw entries), keeps the best
-// min(count, k), and returns the k-th composite (0 while fewer than k are held). Called by
-// the whole wave with a wave-uniform list.
-__device__ inline uint64_t wave_compact(uint64_t* list, int* count, uint64_t* scratch, int capw,
+// Sorts list[0, *count) (global) through `scratch` (LDS, sort_n entries: a power of two >=
+// *count), keeps the best min(count, k), and returns the k-th composite (0 while fewer than k
+// are held). Called by the whole wave with a wave-uniform list.
+__device__ inline uint64_t wave_compact(uint64_t* list, int* count, uint64_t* scratch, int sort_n,
                                         int k) {
   const int lane = lane_id();
   wave_sync_memory();
   const int n = *count;
-  for (int i = lane; i < capw; i += kWave) {
+  for (int i = lane; i < sort_n; i += kWave) {
     scratch[i] = i < n ? load_coherent(list + i) : 0ull;
   }
   wave_sync_memory();
-  wave_sort_desc(scratch, capw);
+  wave_sort_desc(scratch, sort_n);
   const int keep = n < k ? n : k;
   for (int i = lane; i < keep; i += kWave) {
     list[i] = scratch[i];

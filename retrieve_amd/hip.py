@@ -86,4 +86,144 @@ def _(query_codes, item_codes, k, mask=None):
     )
 
 
-__all__ = ["int8_scan_topk"]
+# --- bf16 / fp16 dense full scan + top-k -----------------------------------------------------
+
+_DENSE_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
+
+
+@torch.library.custom_op("retrieve::dense_scan_topk", mutates_args=(), device_types="cuda")
+def dense_scan_topk(
+    query: Tensor, item_embs: Tensor, k: int, mask: Tensor | None = None
+) -> tuple[Tensor, Tensor]:
+    """Dense full-scan top-k: ``query [B, D]`` against ``item_embs [N, D]`` (both bf16 or both
+    fp16), fp32 accumulation, top ``k`` by (score desc, index asc) → ``(ids int64 [B, k],
+    scores fp32 [B, k])``, ``-1`` / ``-inf`` where fewer than ``k`` items pass ``mask``. LiNR
+    V1's ``torch.mm`` + ``masked_topk`` (``modules/knn.py:62-76``) without the ``[B, N]``
+    score matrix."""
+    if query.dim() != 2 or item_embs.dim() != 2:
+        raise ValueError("query must be [B, D] and item_embs [N, D]")
+    if query.dtype not in _DENSE_DTYPES or item_embs.dtype != query.dtype:
+        raise TypeError("query and item_embs must both be bfloat16 or both float16")
+    if query.shape[1] != item_embs.shape[1]:
+        raise ValueError(f"D mismatch: query D={query.shape[1]} vs item D={item_embs.shape[1]}")
+    if not 1 <= k <= 1024:
+        raise ValueError(f"k must be in [1, 1024], got {k}")
+    _check_items(item_embs=item_embs)
+    b, d = query.shape
+    n = item_embs.shape[0]
+    if mask is not None:
+        if mask.dtype != torch.int64:
+            raise TypeError("mask must be int64 words")
+        if mask.dim() != 2 or mask.shape[0] != b or mask.shape[1] < (n + 63) // 64:
+            raise ValueError(f"mask must be [B, ceil(N/64)] = [{b}, {(n + 63) // 64}]")
+        mask = mask.contiguous()
+    q = query.contiguous()
+    dev = nat.require_device(q, item_embs)
+    ids = torch.empty((b, k), dtype=torch.int64, device=dev)
+    scores = torch.empty((b, k), dtype=torch.float32, device=dev)
+    lib = nat.lib()
+    ws = nat.workspace(lib.rt_dense_scan_topk_workspace(b, n, d, k), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_dense_scan_topk(
+            nat.ptr(q), b, nat.ptr(item_embs), n, d, k, _DENSE_DTYPES[q.dtype], nat.ptr(mask),
+            0 if mask is None else mask.shape[1], nat.ptr(ids), nat.ptr(scores), nat.ptr(ws),
+            ws.numel(), nat.stream(dev),
+        )
+    nat.check(st)
+    return ids, scores
+
+
+@dense_scan_topk.register_fake
+def _(query, item_embs, k, mask=None):
+    b = query.shape[0]
+    return (query.new_empty((b, k), dtype=torch.int64),
+            query.new_empty((b, k), dtype=torch.float32))
+
+
+# --- 1-bit Hamming full scan + top-k --------------------------------------------------------
+
+
+def _hamming_prep(query_bits: Tensor, item_bits: Tensor, k: int, mask: Tensor | None):
+    """``_oporp_prep``'s checks (``ops/triton/oporp_1bit_match_topk.py:148-165``)."""
+    if query_bits.dim() != 2 or item_bits.dim() != 2:
+        raise ValueError("query_bits must be [B, W] and item_bits [N, W]")
+    if query_bits.dtype != torch.int64 or item_bits.dtype != torch.int64:
+        raise TypeError("query_bits and item_bits must be int64")
+    if query_bits.shape[1] != item_bits.shape[1]:
+        raise ValueError(
+            f"W mismatch: query_bits W={query_bits.shape[1]} vs item_bits W={item_bits.shape[1]}"
+        )
+    if not 1 <= k <= 1024:
+        raise ValueError(f"k must be in [1, 1024], got {k}")
+    _check_items(item_bits=item_bits)
+    b, n = query_bits.shape[0], item_bits.shape[0]
+    if mask is not None:
+        if mask.dtype != torch.int64:
+            raise TypeError("mask must be int64 words")
+        if mask.dim() != 2 or mask.shape[0] != b or mask.shape[1] < (n + 63) // 64:
+            raise ValueError(f"mask must be [B, ceil(N/64)] = [{b}, {(n + 63) // 64}]")
+        mask = mask.contiguous()
+    return query_bits.contiguous(), mask
+
+
+def _hamming_call(query_bits, item_bits, k, mask, score_dtype):
+    q, mask = _hamming_prep(query_bits, item_bits, k, mask)
+    dev = nat.require_device(q, item_bits)
+    b, w = q.shape
+    n = item_bits.shape[0]
+    ids = torch.empty((b, k), dtype=torch.int64, device=dev)
+    scores = torch.empty((b, k), dtype=score_dtype, device=dev)
+    lib = nat.lib()
+    ws = nat.workspace(lib.rt_hamming_scan_topk_workspace(b, n, w, k), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_hamming_scan_topk(
+            nat.ptr(q), b, nat.ptr(item_bits), n, w, k, nat.ptr(mask),
+            0 if mask is None else mask.shape[1], nat.ptr(ids), nat.ptr(scores),
+            int(score_dtype == torch.float32), nat.ptr(ws), ws.numel(), nat.stream(dev),
+        )
+    nat.check(st)
+    return ids, scores
+
+
+@torch.library.custom_op("retrieve::hamming_scan_topk", mutates_args=(), device_types="cuda")
+def hamming_scan_topk(
+    query_bits: Tensor, item_bits: Tensor, k: int, mask: Tensor | None = None
+) -> tuple[Tensor, Tensor]:
+    """Exact 1-bit Hamming full-scan top-k on the integer score ``64 W - 2 popcount(q ^ item)``:
+    ``(ids int64 [B, k], scores int32 [B, k])``, ties to the lower index, ``-1`` /
+    ``INT32_MIN`` where fewer than ``k`` items pass ``mask``."""
+    return _hamming_call(query_bits, item_bits, k, mask, torch.int32)
+
+
+@hamming_scan_topk.register_fake
+def _(query_bits, item_bits, k, mask=None):
+    b = query_bits.shape[0]
+    return (query_bits.new_empty((b, k)), query_bits.new_empty((b, k), dtype=torch.int32))
+
+
+@torch.library.custom_op(
+    "retrieve::oporp_1bit_match_topk_full", mutates_args=(), device_types="cuda"
+)
+def oporp_1bit_match_topk_full(
+    query_bits: Tensor, item_bits: Tensor, k: int
+) -> tuple[Tensor, Tensor]:
+    """Full-scan Sign-OPORP 1-bit Hamming top-K (``ops/triton/oporp_1bit_match_topk.py:261-273``):
+    ``64·W − 2·popcount(q ^ item)`` over every row of ``item_bits`` → ``(ids [B, k] int64,
+    scores [B, k] fp32)``; ties go to the lower index (the reference's ``torch.topk`` leaves
+    them unspecified). ``k > N`` pads ``-1`` / ``-inf`` (the reference's layer asserts
+    ``k <= N``)."""
+    return _hamming_call(query_bits, item_bits, k, None, torch.float32)
+
+
+@oporp_1bit_match_topk_full.register_fake
+def _(query_bits, item_bits, k):
+    b = query_bits.shape[0]
+    return (query_bits.new_empty((b, k)), query_bits.new_empty((b, k), dtype=torch.float32))
+
+
+__all__ = [
+    "dense_scan_topk",
+    "hamming_scan_topk",
+    "int8_scan_topk",
+    "oporp_1bit_match_topk_full",
+]

@@ -1,0 +1,107 @@
+"""1-bit Hamming full scan + exact top-k on the GPU against the oracle (bit-exact integer
+scores and ids, ties to the lower index): ``torch.ops.retrieve.hamming_scan_topk`` and the
+reference-schema ``torch.ops.retrieve.oporp_1bit_match_topk_full``."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import scan as osc
+from tests.conftest import rng
+from tests.test_int8_scan import _pack
+
+pytestmark = pytest.mark.gpu
+
+
+def _codes(g, n, w):
+    return g.integers(-(2**63), 2**63 - 1, (n, w), dtype=np.int64)
+
+
+def _check(dev, q, items, k, mask=None):
+    print(f"hamming scan B={q.shape[0]} N={items.shape[0]} W={q.shape[1]} k={k} "
+          f"mask={mask is not None}", flush=True)
+    qt = torch.from_numpy(q).to(dev)
+    it = torch.from_numpy(items).to(dev)
+    mt = None if mask is None else torch.from_numpy(_pack(mask)).to(dev)
+    ids, sc = torch.ops.retrieve.hamming_scan_topk(qt, it, k, mt)
+    torch.cuda.synchronize()
+    want_ids, want_sc = osc.hamming_topk(q, items, k, mask)
+    assert np.array_equal(sc.cpu().numpy(), want_sc)
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+
+
+def test_popcount_kat(dev, kat):
+    """The reference's popcount words as one-word codes against a zero query: scores are
+    64 - 2 * popcount."""
+    a, _ = kat
+    items = a["popcount_kat_in"].reshape(-1, 1)
+    q = np.zeros((1, 1), np.int64)
+    ids, sc = torch.ops.retrieve.hamming_scan_topk(
+        torch.from_numpy(q).to(dev), torch.from_numpy(items).to(dev), items.shape[0]
+    )
+    got = dict(zip(ids[0].tolist(), sc[0].tolist()))
+    assert [got[i] for i in range(items.shape[0])] == \
+        [64 - 2 * int(p) for p in a["popcount_kat_out"]]
+
+
+@pytest.mark.parametrize(
+    "b,n,w,k",
+    [(1, 1, 8, 1), (1, 100, 1, 10), (5, 3000, 2, 50), (16, 20000, 8, 100),
+     (65, 10000, 4, 100), (3, 50000, 16, 1000), (70, 4099, 8, 7)],
+)
+def test_random_parity(dev, b, n, w, k):
+    g = rng(b * 7 + n + w * 13 + k)
+    _check(dev, _codes(g, b, w), _codes(g, n, w), k)
+
+
+def test_heavy_ties_few_bits(dev):
+    """W = 1 codes with only 8 distinct rows: huge tie groups at every boundary."""
+    g = rng(31)
+    base = _codes(g, 8, 1)
+    items = base[g.integers(0, 8, 40000)]
+    q = _codes(g, 9, 1)
+    _check(dev, q, items, 100)
+    _check(dev, q, items, 1000)
+
+
+def test_masked(dev):
+    g = rng(32)
+    q = _codes(g, 6, 8)
+    items = _codes(g, 30000, 8)
+    mask = g.random((6, 30000)) < 0.1
+    mask[1] = g.random(30000) < 0.001
+    mask[3] = False
+    _check(dev, q, items, 100, mask)
+
+
+def test_seeded_path_k1000(dev):
+    """N above the k = 1000 seed threshold (8 x 1024 x k rows): config 5's top-1000 over
+    512-bit codes."""
+    g = rng(33)
+    q = _codes(g, 8, 8)
+    items = _codes(g, 8_400_000, 8)
+    _check(dev, q, items, 1000)
+
+
+def test_unseeded_large_k(dev):
+    """k = 1000 below the seed threshold: every wave's lists fill and compact from scratch."""
+    g = rng(35)
+    q = _codes(g, 20, 8)
+    items = _codes(g, 2_200_000, 8)
+    _check(dev, q, items, 1000)
+
+
+def test_oporp_full_schema(dev):
+    g = rng(34)
+    q = torch.from_numpy(_codes(g, 4, 8)).to(dev)
+    it = torch.from_numpy(_codes(g, 5000, 8)).to(dev)
+    ids, sc = torch.ops.retrieve.oporp_1bit_match_topk_full(q, it, 64)
+    assert ids.dtype == torch.int64 and sc.dtype == torch.float32 and sc.shape == (4, 64)
+    ids2, sc2 = torch.ops.retrieve.hamming_scan_topk(q, it, 64)
+    assert torch.equal(ids, ids2) and torch.equal(sc, sc2.float())
+    with pytest.raises(TypeError):
+        torch.ops.retrieve.oporp_1bit_match_topk_full(q.int(), it, 3)
+    with pytest.raises(ValueError):
+        torch.ops.retrieve.oporp_1bit_match_topk_full(q[:, :4], it, 3)
