@@ -56,6 +56,19 @@ int rt_dense_scan_topk(const void* queries, int64_t B, const void* items, int64_
                        int64_t* out_ids, float* out_scores, void* workspace,
                        size_t workspace_bytes, rt_stream_t stream);
 
+/* Large-batch form of rt_int8_scan_topk / rt_dense_scan_topk (same results): register-blocked
+ * 32x32 MFMA tiles, 256 queries per workgroup held in registers, item tiles shared through
+ * LDS. dtype 0 = int8 (int32 scores), 1 = bf16, 2 = fp16 (float scores). Rows of 128, 256 or
+ * 512 bytes (int8 D in {128, 256, 512}; 16-bit D in {64, 128, 256}). `row_bytes` of the
+ * workspace function is D times the element size.
+ * Replaces: the same reference paths as rt_int8_scan_topk / rt_dense_scan_topk at batches
+ *   where they become a GEMM (B >= 128). */
+size_t rt_blocked_scan_topk_workspace(int64_t B, int64_t N, int64_t row_bytes, int64_t k);
+int rt_blocked_scan_topk(const void* queries, int64_t B, const void* items, int64_t N, int64_t D,
+                         int64_t k, int dtype, const uint64_t* mask, int64_t mask_words,
+                         int64_t* out_ids, void* out_scores, void* workspace,
+                         size_t workspace_bytes, rt_stream_t stream);
+
 /* Exact 1-bit Hamming top-k over a full code table: query_bits [B, W] x item_bits [N, W]
  * (uint64 words, bit b of word w = dimension 64 w + b), score = 64 W - 2 popcount(q ^ item),
  * top-k by (score desc, index asc) -> ids int64 [B, k], scores [B, k] (int32, or float when

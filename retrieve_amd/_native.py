@@ -37,6 +37,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_p, _c_p,
          _c_sz, _c_p],
     ),
+    "rt_blocked_scan_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "rt_blocked_scan_topk": (
+        _c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_p, _c_p,
+         _c_sz, _c_p],
+    ),
     "rt_profile_enable": (_c_int, [_c_int]),
     "rt_profile_collect": (_c_int, [_c_p, _c_p]),
     "rt_int8_scan_topk": (

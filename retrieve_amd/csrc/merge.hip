@@ -36,7 +36,8 @@ static constexpr int64_t kSeedRowsPerK = 1024;
 static constexpr int64_t kMaxListBytes = int64_t{2} << 30;
 
 static PassPlan plan_pass(int64_t n_rows, int64_t row_stride, int64_t n_qgroups, int64_t min_rows,
-                          int capw, int qpw, int64_t target_wgs, int64_t min_gx = 1) {
+                          int capw, int64_t lists_per_wg, int64_t lists_per_query_per_wg,
+                          int64_t target_wgs, int64_t min_gx = 1) {
   PassPlan p;
   p.n_rows = n_rows;
   p.row_stride = row_stride;
@@ -45,9 +46,10 @@ static PassPlan plan_pass(int64_t n_rows, int64_t row_stride, int64_t n_qgroups,
   gx = gx < min_gx ? min_gx : gx;
   const int64_t by_rows = cdiv(n_rows, min_rows);
   gx = gx < by_rows ? gx : by_rows;
-  gx = gx < kMaxMergeSlots / kScanWaves ? gx : kMaxMergeSlots / kScanWaves;
-  // keep the lists within kMaxListBytes (fewer, longer strips for large k or batch)
-  const int64_t per_wg = n_qgroups * kScanWaves * static_cast<int64_t>(qpw) * capw *
+  const int64_t by_slots = kMaxMergeSlots / lists_per_query_per_wg;
+  gx = gx < by_slots ? gx : by_slots;
+  // keep the lists within kMaxListBytes (fewer workgroups for large k or batch)
+  const int64_t per_wg = n_qgroups * lists_per_wg * static_cast<int64_t>(capw) *
                          static_cast<int64_t>(sizeof(uint64_t));
   const int64_t by_bytes = kMaxListBytes / (per_wg > 0 ? per_wg : 1);
   gx = gx < by_bytes ? gx : by_bytes;
@@ -56,9 +58,10 @@ static PassPlan plan_pass(int64_t n_rows, int64_t row_stride, int64_t n_qgroups,
   if (p.strip == 0) p.strip = kTile;
   p.gx = cdiv(n_rows, p.strip);
   if (p.gx < 1) p.gx = 1;
-  const int64_t slots = p.gx * n_qgroups * kScanWaves;
-  p.lists_bytes = static_cast<size_t>(slots) * qpw * capw * sizeof(uint64_t);
-  p.counts_bytes = static_cast<size_t>(slots) * qpw * sizeof(int);
+  p.S = p.gx * lists_per_query_per_wg;
+  p.lists_bytes = static_cast<size_t>(p.gx) * n_qgroups * lists_per_wg * capw * sizeof(uint64_t);
+  p.counts_bytes = static_cast<size_t>(p.gx) * n_qgroups * lists_per_wg * sizeof(int);
+  // the seed's flat one-entry lists: [B rounded up to groups][S]
   return p;
 }
 
@@ -74,19 +77,22 @@ int64_t main_workgroups() {
   return t < kMaxResidentWorkgroups ? t : kMaxResidentWorkgroups;
 }
 
-ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw, int64_t target_wgs, int main_capw,
-                   int tile_rows) {
+ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int64_t qpg, int64_t lists_per_wg,
+                   int64_t target_wgs, int main_capw, int64_t seed_rows_per_wg) {
   ScanPlan s;
-  s.qpw = qpw;
-  s.n_qgroups = cdiv(B, qpw);
+  s.qpg = qpg;
+  s.n_qgroups = cdiv(B, qpg);
+  // a query's lists per workgroup: every wave scores all of the row's queries (lists_per_wg ==
+  // waves * qpg), or one wave owns each query (lists_per_wg == qpg)
+  const int64_t lpq = lists_per_wg / qpg;
   const int64_t seed_rows = kSeedRows > kSeedRowsPerK * k ? kSeedRows : kSeedRowsPerK * k;
   s.seeded = N >= 8 * seed_rows;
   if (s.seeded) {
-    // one-entry lists (each seed wave's best); at least k workgroups (4k waves) per group
-    s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, kScanWaves * tile_rows, 1, qpw,
-                       kTargetWorkgroups, k);
+    // one-entry lists (each seed wave's best); at least 4k of them per query
+    s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, seed_rows_per_wg, 1, lists_per_wg,
+                       lpq, kTargetWorkgroups, cdiv(4 * k, lpq));
   }
-  s.main = plan_pass(N, 1, s.n_qgroups, 1024, main_capw, qpw, target_wgs);
+  s.main = plan_pass(N, 1, s.n_qgroups, 1024, main_capw, lists_per_wg, lpq, target_wgs);
   const size_t lists = s.main.lists_bytes > s.seed.lists_bytes ? s.main.lists_bytes
                                                               : s.seed.lists_bytes;
   const size_t counts = s.main.counts_bytes > s.seed.counts_bytes ? s.main.counts_bytes
@@ -232,8 +238,8 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   const int64_t q = blockIdx.x;
   const int64_t g = q / m.qpw;
   const int qi = static_cast<int>(q % m.qpw);
-  const int S = static_cast<int>(m.gx * kScanWaves);
-  const int64_t slot0 = g * m.gx * kScanWaves;
+  const int S = static_cast<int>(m.S);
+  const int64_t slot0 = g * m.S;
   const int k = m.k;
 
   // list lengths → inclusive prefix sums over this query's lists (flat: S one-entry lists
@@ -393,7 +399,7 @@ int launch_pad(int64_t* out_ids, void* out_scores, int64_t B, int64_t k, int sco
 int launch_merge(const MergeArgs& m, hipStream_t stream) {
   RT_CHECK_ARG(m.k >= 1 && m.k <= kMaxK, "k must be in [1, %lld], got %d",
                static_cast<long long>(kMaxK), m.k);
-  RT_CHECK_ARG(m.gx * kScanWaves <= kMaxMergeSlots, "too many scan lists per query");
+  RT_CHECK_ARG(m.S >= 1 && m.S <= kMaxMergeSlots, "too many scan lists per query");
   if (m.B == 0) return kOk;
   const dim3 grid(static_cast<unsigned>(m.B));
   if (m.k <= 128) {

@@ -1,0 +1,446 @@
+// Large-batch dense scans with the exact fused top-k: register-blocked 32x32 MFMA tiles.
+//
+// A workgroup (4 waves) owns 256 queries: each wave keeps the B-operand fragments of its 64
+// queries in registers for the whole kernel. Item tiles of 64 rows are dealt round-robin to
+// the workgroups of a query group; a tile is read once from HBM with coalesced nontemporal
+// loads, staged (double-buffered) in LDS, and every wave multiplies it against its 64 queries
+// as 2 x 2 tiles of 32x32 outputs (v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_{bf16,f16}:
+// each instruction consumes 32 bytes of K per row). Lane l of an output tile holds query
+// (col tile * 32 + l % 32) and, in register i, item (row tile * 32 + (i/4)*8 + (l/32)*4 + i%4).
+// Per MFMA, lane l feeds bytes [32 s + 16 (l / 32), +16) of its row on both sides.
+//
+// Operand reuse: each staged item byte feeds 64 queries per wave and each register-held query
+// byte feeds every item of the grid row, so the matrix cores, not LDS or HBM, bound the
+// kernel at large batches.
+#include "profile.h"
+#include "scan_common.h"
+#include "wave_lists.h"
+
+namespace rt {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+constexpr int kBlkRows = 64;      // items per staged tile
+constexpr int kBlkQpw = 64;       // queries per wave
+constexpr int kBlkQpg = kScanWaves * kBlkQpw;  // queries per workgroup (query group)
+
+struct I8x32 {
+  using Score = int32_t;
+  using Acc = v16i;
+  static constexpr int kind = kScoreI32;
+  __device__ static Acc zero() { return Acc{}; }
+  __device__ static Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+  __device__ static uint32_t key(Score s) { return key_of_i32(s); }
+  __device__ static Score thresh(uint64_t tau) { return i32_of_key(composite_key(tau)); }
+};
+
+struct BF16x32 {
+  using Score = float;
+  using Acc = v16f;
+  static constexpr int kind = kScoreF32;
+  __device__ static Acc zero() { return Acc{}; }
+  __device__ static Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a),
+                                                   __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+  }
+  __device__ static uint32_t key(Score s) { return key_of_f32(s); }
+  __device__ static Score thresh(uint64_t tau) {
+    const uint32_t k = composite_key(tau);
+    return k <= key_of_f32(-INFINITY) ? -INFINITY : f32_of_key(k);
+  }
+};
+
+struct F16x32 : BF16x32 {
+  __device__ static Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a),
+                                                  __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+  }
+};
+
+template <int RB>  // row bytes
+constexpr int blk_pitch() {
+  return RB + 16;
+}
+
+template <int RB>
+constexpr size_t blk_stage_bytes() {
+  return static_cast<size_t>(2) * kBlkRows * blk_pitch<RB>();  // double buffer
+}
+
+// SEED: per query, each wave's best composite over the strided sample, written to
+// lists[q * S + wave index] (one-entry lists); else candidate lists per (wave, query).
+template <class Op, int RB, bool SEED>
+__global__ void __launch_bounds__(kScanThreads) scan_blocked_kernel(ScanArgs a) {
+  using Score = typename Op::Score;
+  constexpr int KS = RB / 32;  // MFMA steps per row
+  constexpr int P = blk_pitch<RB>();
+  constexpr int TILE_BYTES = kBlkRows * RB;
+  constexpr int LOADS = TILE_BYTES / (kScanThreads * 16);  // 16-byte loads per thread
+  static_assert(TILE_BYTES % (kScanThreads * 16) == 0, "tile must split into 16-byte loads");
+  extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
+  int8_t* stage = reinterpret_cast<int8_t*>(smem);
+  uint64_t* scratch = reinterpret_cast<uint64_t*>(stage + blk_stage_bytes<RB>());
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid >> 6;
+  const int c32 = lane & 31;
+  const int half = lane >> 5;
+  int* cnt = reinterpret_cast<int*>(scratch + kScanWaves * a.capw) + wave * kBlkQpw;
+
+  const int64_t wg = blockIdx.x;
+  const int64_t nwg = gridDim.x;
+  const int64_t q0 = static_cast<int64_t>(blockIdx.y) * kBlkQpg + wave * kBlkQpw;
+  const int8_t* Q = static_cast<const int8_t*>(a.queries);
+  const int8_t* I = static_cast<const int8_t*>(a.items);
+
+  // this lane's queries: q0 + c32 (col tile 0) and q0 + 32 + c32 (col tile 1)
+  v4i qf[2][KS];
+  uint64_t tau[2];
+  Score ts[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t q = q0 + 32 * j + c32;
+    if (q < a.B) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        qf[j][s] = *reinterpret_cast<const v4i*>(Q + q * RB + 32 * s + 16 * half);
+      }
+      tau[j] = a.tau_in != nullptr ? a.tau_in[q] : 0ull;
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qf[j][s] = v4i{0, 0, 0, 0};
+      tau[j] = ~0ull;
+    }
+    ts[j] = Op::thresh(tau[j]);
+  }
+  const uint64_t* qmask[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t q = q0 + 32 * j + c32;
+    qmask[j] = a.mask != nullptr && q < a.B ? a.mask + q * a.mask_words : nullptr;
+  }
+  uint64_t best[2] = {0ull, 0ull};  // SEED
+  // list slot of this wave: query group (64 queries) g = blockIdx.y * 4 + wave, slot g * nwg + wg
+  const int64_t slot = (static_cast<int64_t>(blockIdx.y) * kScanWaves + wave) * nwg + wg;
+  uint64_t* lists = a.lists + slot * kBlkQpw * static_cast<int64_t>(a.capw);
+  if constexpr (!SEED) {
+    for (int i = lane; i < kBlkQpw; i += kWave) cnt[i] = 0;
+  }
+
+  const int64_t n = a.n_rows;
+  const int64_t ntiles = cdiv(n, kBlkRows);
+  v4i v[LOADS];
+  // load l of a tile covers its bytes [(l * 256 + tid) * 16, +16); row = that / RB
+  auto load_tile = [&](int64_t t) {
+    const int64_t r0 = t * kBlkRows;
+#pragma unroll
+    for (int l = 0; l < LOADS; ++l) {
+      const int off = (l * kScanThreads + tid) * 16;
+      const int64_t row = r0 + off / RB;
+      if (row < n) {
+        const v4i* src = reinterpret_cast<const v4i*>(I + row * a.row_stride * RB + off % RB);
+        v[l] = SEED ? *src : __builtin_nontemporal_load(src);
+      } else {
+        v[l] = v4i{0, 0, 0, 0};
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+    int8_t* dst = stage + buf * kBlkRows * P;
+#pragma unroll
+    for (int l = 0; l < LOADS; ++l) {
+      const int off = (l * kScanThreads + tid) * 16;
+      *reinterpret_cast<v4i*>(dst + (off / RB) * P + off % RB) = v[l];
+    }
+  };
+
+  int64_t t = wg;
+  int buf = 0;
+  if (t < ntiles) {
+    load_tile(t);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (; t < ntiles; t += nwg) {
+    const bool more = t + nwg < ntiles;
+    if (more) load_tile(t + nwg);
+    const int8_t* src = stage + buf * kBlkRows * P;
+    typename Op::Acc acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = Op::zero();
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      v4i af[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        af[i] = *reinterpret_cast<const v4i*>(src + (32 * i + c32) * P + 32 * s + 16 * half);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma(af[i], qf[j][s], acc[i][j]);
+    }
+    if (more) store_tile(buf ^ 1);
+
+    const int64_t rb = t * kBlkRows;
+    if constexpr (SEED) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = rb + 32 * i + (r / 4) * 8 + half * 4 + (r % 4);
+          const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            bool ok = row < n;
+            if (ok && qmask[j] != nullptr) {
+              ok = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
+            }
+            const uint64_t c = composite(Op::key(acc[i][j][r]), item);
+            best[j] = ok && c > best[j] ? c : best[j];
+          }
+        }
+    } else {
+      bool hit = false;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) hit |= acc[i][j][r] >= ts[j];
+      if (__any(hit)) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const Score sc = acc[i][j][r];
+              const int64_t row = rb + 32 * i + (r / 4) * 8 + half * 4 + (r % 4);
+              if (row < n && sc >= ts[j]) {
+                const uint32_t item = static_cast<uint32_t>(row);
+                const uint64_t c = composite(Op::key(sc), item);
+                bool keep = c >= tau[j];
+                if (keep && qmask[j] != nullptr) {
+                  keep = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
+                }
+                if (keep) {
+                  const int q = 32 * j + c32;
+                  const int pos = atomicAdd(&cnt[q], 1);
+                  lists[q * static_cast<int64_t>(a.capw) + pos] = c;
+                }
+              }
+            }
+        wave_sync_memory();
+        // a query gains at most 64 entries per tile
+        for (int jq = 0; jq < 2; ++jq) {
+          const bool full = cnt[32 * jq + c32] > a.capw - kBlkRows;
+          uint64_t need = __ballot(full) & 0xffffffffull;
+          while (need != 0ull) {
+            const int c = __builtin_ctzll(need);
+            need &= need - 1;
+            const int q = 32 * jq + c;
+            const uint64_t nt = wave_compact(lists + q * static_cast<int64_t>(a.capw), &cnt[q],
+                                             scratch + wave * a.capw, a.capw, a.k);
+            if (c32 == c && nt > tau[jq]) {
+              tau[jq] = nt;
+              ts[jq] = Op::thresh(nt);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  if constexpr (SEED) {
+    // flat one-entry lists: a query's maxima, one per workgroup, at lists[q * nwg + wg]
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint64_t o = __shfl_xor(best[j], 32);
+      const uint64_t b = o > best[j] ? o : best[j];
+      const int64_t q = q0 + 32 * j + c32;
+      if (half == 0 && q < a.B) a.lists[q * nwg + wg] = b;
+    }
+  } else {
+    wave_sync_memory();
+    for (int i = lane; i < kBlkQpw; i += kWave) a.counts[slot * kBlkQpw + i] = cnt[i];
+  }
+}
+
+template <int RB>
+static size_t blk_lds(int capw) {
+  return blk_stage_bytes<RB>() + kScanWaves * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
+}
+
+template <class Op, int RB>
+static int launch_blk(const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed,
+                      hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.gx), static_cast<unsigned>(nqg));
+  const size_t lds = blk_lds<RB>(seed ? 0 : p.capw);
+  const void* fn = seed ? reinterpret_cast<const void*>(scan_blocked_kernel<Op, RB, true>)
+                        : reinterpret_cast<const void*>(scan_blocked_kernel<Op, RB, false>);
+  if (lds > 65536) {
+    RT_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds)));
+  }
+  if (seed) {
+    scan_blocked_kernel<Op, RB, true><<<grid, kScanThreads, lds, stream>>>(a);
+  } else {
+    scan_blocked_kernel<Op, RB, false><<<grid, kScanThreads, lds, stream>>>(a);
+  }
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+template <class Op>
+static int dispatch_blk(int64_t row_bytes, const ScanArgs& a, const PassPlan& p, int64_t nqg,
+                        bool seed, hipStream_t stream) {
+  switch (row_bytes) {
+    case 128: return launch_blk<Op, 128>(a, p, nqg, seed, stream);
+    case 256: return launch_blk<Op, 256>(a, p, nqg, seed, stream);
+    case 512: return launch_blk<Op, 512>(a, p, nqg, seed, stream);
+    default:
+      set_error("blocked scan supports rows of 128, 256 or 512 bytes, got %lld",
+                static_cast<long long>(row_bytes));
+      return kInvalidArgument;
+  }
+}
+
+static size_t blk_lds_for(int64_t row_bytes, int capw) {
+  return static_cast<size_t>(2) * kBlkRows * (row_bytes + 16) +
+         kScanWaves * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
+}
+
+constexpr size_t kMaxLds = 160 * 1024;
+
+// List capacity: k plus a tile's appends (64 per query), a power of two (sorted whole).
+static int blk_capw(int64_t k) { return static_cast<int>(next_pow2(k + kBlkRows)); }
+
+// Workgroups of the blocked main pass per CU (LDS-bound: the double-buffered stage).
+constexpr int64_t kBlkWorkgroupsPerCU = 1;
+
+template <class Op>
+static int run_blocked(const void* queries, int64_t B, const void* items, int64_t N,
+                       int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
+                       int64_t* out_ids, void* out_scores, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+  RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
+  RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
+               static_cast<long long>(kMaxK), static_cast<long long>(k));
+  RT_CHECK_ARG(N < 0xffffffffll, "N must be < 2**32 - 1");
+  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(queries) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(items) % 16 == 0,
+               "queries and items must be 16-byte aligned");
+  RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
+  if (B == 0) return kOk;
+  if (N == 0) return launch_pad(out_ids, out_scores, B, k, Op::kind, stream);
+  int dev = 0;
+  int cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  }
+  const ScanPlan plan = plan_scan(B, N, k, kBlkQpg, kBlkQpg, cus * kBlkWorkgroupsPerCU,
+                                  blk_capw(k), kBlkRows);
+  RT_CHECK_ARG(blk_lds_for(row_bytes, plan.main.capw) <= kMaxLds,
+               "k = %lld is too large for the blocked scan at %lld-byte rows",
+               static_cast<long long>(k), static_cast<long long>(row_bytes));
+  if (workspace_bytes < plan.total) {
+    set_error("workspace too small: %zu < %zu", workspace_bytes, plan.total);
+    return kWorkspaceTooSmall;
+  }
+  char* ws = static_cast<char*>(workspace);
+  uint64_t* lists = reinterpret_cast<uint64_t*>(ws + plan.off_lists);
+  int* counts = reinterpret_cast<int*>(ws + plan.off_counts);
+  uint64_t* tau = reinterpret_cast<uint64_t*>(ws + plan.off_tau);
+
+  ScanArgs a{};
+  a.queries = queries;
+  a.B = B;
+  a.items = items;
+  a.k = static_cast<int>(k);
+  a.qpw = kBlkQpw;
+  a.mask = mask;
+  a.mask_words = mask_words;
+  a.lists = lists;
+  a.counts = counts;
+
+  MergeArgs m{};
+  m.lists = lists;
+  m.counts = counts;
+  m.qpw = kBlkQpw;  // one list per query per slot; a slot is (64-query group, workgroup)
+  m.B = B;
+  m.k = static_cast<int>(k);
+
+  if (plan.seeded) {
+    a.n_rows = plan.seed.n_rows;
+    a.row_stride = plan.seed.row_stride;
+    a.capw = 1;
+    a.tau_in = nullptr;
+    int st = dispatch_blk<Op>(row_bytes, a, plan.seed, plan.n_qgroups, true, stream);
+    if (st != kOk) return st;
+    m.capw = 1;
+    m.flat = true;
+    m.S = plan.seed.S;
+    m.tau_out = tau;
+    st = launch_merge(m, stream);
+    if (st != kOk) return st;
+    m.tau_out = nullptr;
+    m.flat = false;
+  }
+  a.n_rows = N;
+  a.row_stride = 1;
+  a.capw = plan.main.capw;
+  a.tau_in = plan.seeded ? tau : nullptr;
+  hipEvent_t stop;
+  profile_begin(stream, &stop);
+  int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, stream);
+  profile_end(stream, stop);
+  if (st != kOk) return st;
+  m.capw = plan.main.capw;
+  m.S = plan.main.S;
+  m.out_ids = out_ids;
+  m.out_scores = out_scores;
+  m.score_kind = Op::kind;
+  return launch_merge(m, stream);
+}
+
+}  // namespace rt
+
+using namespace rt;
+
+extern "C" size_t rt_blocked_scan_topk_workspace(int64_t B, int64_t N, int64_t row_bytes,
+                                                 int64_t k) {
+  (void)row_bytes;
+  return plan_scan(B, N, k, kBlkQpg, kBlkQpg, kMaxResidentWorkgroups, blk_capw(k), kBlkRows).total;
+}
+
+// dtype: 0 int8 (int32 scores), 1 bf16, 2 fp16 (float scores); D elements per row.
+extern "C" int rt_blocked_scan_topk(const void* queries, int64_t B, const void* items, int64_t N,
+                                    int64_t D, int64_t k, int dtype, const uint64_t* mask,
+                                    int64_t mask_words, int64_t* out_ids, void* out_scores,
+                                    void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  switch (dtype) {
+    case 0:
+      return run_blocked<I8x32>(queries, B, items, N, D, k, mask, mask_words, out_ids,
+                                out_scores, workspace, workspace_bytes, stream);
+    case 1:
+      return run_blocked<BF16x32>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
+                                  out_scores, workspace, workspace_bytes, stream);
+    case 2:
+      return run_blocked<F16x32>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
+                                 out_scores, workspace, workspace_bytes, stream);
+    default:
+      set_error("blocked scan dtype must be 0 (int8), 1 (bf16) or 2 (fp16), got %d", dtype);
+      return kInvalidType;
+  }
+}

@@ -18,7 +18,7 @@ constexpr int kScanThreads = kScanWaves * kWave;
 constexpr int kTile = 16;           // items per MFMA tile
 constexpr int kMergeThreads = 512;
 constexpr int64_t kMaxK = 1024;
-constexpr int64_t kMaxMergeSlots = 8192;  // lists a query's merge reads (gx * waves)
+constexpr int64_t kMaxMergeSlots = 8192;  // lists a query's merge reads
 
 // The scan kernels' arguments (the element type of queries/items is the kernel's).
 struct ScanArgs {
@@ -49,8 +49,8 @@ struct MergeArgs {
   const int* counts;   // per-list lengths (unused when flat)
   bool flat;           // lists is [B, gx * waves] one-entry lists, contiguous per query
   int capw;
-  int qpw;          // queries per scan wave
-  int64_t gx;       // scan workgroups per query group
+  int qpw;          // queries per list slot (a slot holds one list per such query)
+  int64_t S;        // list slots per query: query q's lists are slots [q/qpw * S, +S)
   int64_t B;
   int k;
   uint64_t* tau_out;   // threshold mode: [B]
@@ -65,13 +65,14 @@ struct PassPlan {
   int64_t row_stride = 1;
   int64_t strip = 0;
   int64_t gx = 0;
+  int64_t S = 0;           // lists per query
   int capw = 0;
   size_t lists_bytes = 0;
   size_t counts_bytes = 0;
 };
 
 struct ScanPlan {
-  int qpw = 16;
+  int64_t qpg = 16;        // queries per workgroup row (grid.y groups)
   int64_t n_qgroups = 0;
   bool seeded = false;
   PassPlan seed;
@@ -89,11 +90,12 @@ constexpr int64_t kMainWorkgroupsPerCU = 2;
 // Main-pass workgroups for the current device: CUs x kMainWorkgroupsPerCU.
 int64_t main_workgroups();
 
-// Sizes the passes for B queries (qpw per wave) over N rows and top-k; the main pass runs
-// target_wgs workgroups across all query groups with lists of main_capw entries; a scan wave
-// scores tiles of tile_rows rows.
-ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int qpw, int64_t target_wgs, int main_capw,
-                   int tile_rows);
+// Sizes the passes for B queries over N rows and top-k. A workgroup row (grid.y) covers qpg
+// queries and each workgroup keeps lists_per_wg candidate lists (of main_capw entries in the
+// main pass); the main pass runs target_wgs workgroups in all; a seed workgroup scores at
+// least seed_rows_per_wg sampled rows.
+ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int64_t qpg, int64_t lists_per_wg,
+                   int64_t target_wgs, int main_capw, int64_t seed_rows_per_wg);
 
 // Writes the -1 / sentinel pads of an empty result.
 int launch_pad(int64_t* out_ids, void* out_scores, int64_t B, int64_t k, int score_kind,

@@ -229,7 +229,9 @@ using namespace rt;
 extern "C" size_t rt_hamming_scan_topk_workspace(int64_t B, int64_t N, int64_t W, int64_t k) {
   (void)W;
   const int qpw = ham_qpw(B > 0 ? B : 1);
-  return plan_scan(B, N, k, qpw, kMaxResidentWorkgroups, ham_capw(k), kHamTile).total;
+  return plan_scan(B, N, k, qpw, kScanWaves * qpw, kMaxResidentWorkgroups, ham_capw(k),
+                   kScanWaves * kHamTile)
+      .total;
 }
 
 extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits,
@@ -250,7 +252,8 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const
   const int kind = score_f32 ? kScoreF32FromI32 : kScoreI32;
   if (N == 0) return launch_pad(out_ids, out_scores, B, k, kind, stream);
   const int qpw = ham_qpw(B);
-  const ScanPlan plan = plan_scan(B, N, k, qpw, main_workgroups(), ham_capw(k), kHamTile);
+  const ScanPlan plan = plan_scan(B, N, k, qpw, kScanWaves * qpw, main_workgroups(), ham_capw(k),
+                                  kScanWaves * kHamTile);
   if (workspace_bytes < plan.total) {
     set_error("workspace too small: %zu < %zu", workspace_bytes, plan.total);
     return kWorkspaceTooSmall;
@@ -287,7 +290,7 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const
     if (st != kOk) return st;
     m.capw = 1;
     m.flat = true;
-    m.gx = plan.seed.gx;
+    m.S = plan.seed.S;
     m.tau_out = tau;
     st = launch_merge(m, stream);
     if (st != kOk) return st;
@@ -304,7 +307,7 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const
   profile_end(stream, stop);
   if (st != kOk) return st;
   m.capw = plan.main.capw;
-  m.gx = plan.main.gx;
+  m.S = plan.main.S;
   m.out_ids = out_ids;
   m.out_scores = out_scores;
   m.score_kind = kind;

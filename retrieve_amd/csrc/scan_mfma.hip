@@ -282,7 +282,8 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
   if (B == 0) return kOk;
   if (N == 0) return launch_pad(out_ids, out_scores, B, k, Op::kind, stream);
-  const ScanPlan plan = plan_scan(B, N, k, 16, main_workgroups(), mfma_capw(k), kTile);
+  const ScanPlan plan = plan_scan(B, N, k, 16, kScanWaves * 16, main_workgroups(), mfma_capw(k),
+                                  kScanWaves * kTile);
   if (workspace_bytes < plan.total) {
     set_error("workspace too small: %zu < %zu", workspace_bytes, plan.total);
     return kWorkspaceTooSmall;
@@ -320,7 +321,7 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
     if (st != kOk) return st;
     m.capw = 1;
     m.flat = true;  // one entry per seed wave, contiguous per query
-    m.gx = plan.seed.gx;
+    m.S = plan.seed.S;
     m.tau_out = tau;
     st = launch_merge(m, stream);
     if (st != kOk) return st;
@@ -338,7 +339,7 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   profile_end(stream, stop);
   if (st != kOk) return st;
   m.capw = plan.main.capw;
-  m.gx = plan.main.gx;
+  m.S = plan.main.S;
   m.out_ids = out_ids;
   m.out_scores = out_scores;
   m.score_kind = Op::kind;
@@ -351,7 +352,7 @@ using namespace rt;
 
 extern "C" size_t rt_int8_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
   (void)D;
-  return plan_scan(B, N, k, 16, kMaxResidentWorkgroups, mfma_capw(k), kTile).total;
+  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k), kScanWaves * kTile).total;
 }
 
 extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t* items,
@@ -364,7 +365,7 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
 
 extern "C" size_t rt_dense_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
   (void)D;
-  return plan_scan(B, N, k, 16, kMaxResidentWorkgroups, mfma_capw(k), kTile).total;
+  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k), kScanWaves * kTile).total;
 }
 
 extern "C" int rt_dense_scan_topk(const void* queries, int64_t B, const void* items, int64_t N,

@@ -23,6 +23,36 @@ def _check_items(**tables: Tensor) -> None:
             raise ValueError(f"{name} must be contiguous (copy it once at index build)")
 
 
+# --- large-batch dispatch ---------------------------------------------------------------------
+
+# From this batch on the dense scans run the register-blocked kernel (256 queries per
+# workgroup, item tiles read once per 256 queries) instead of 16 queries per wave.
+BLOCKED_MIN_BATCH = 128
+_BLOCKED_ROW_BYTES = (128, 256, 512)
+
+
+def _use_blocked(b: int, row_bytes: int, k: int) -> bool:
+    capw = 1 << (k + 64 - 1).bit_length()
+    lds = 2 * 64 * (row_bytes + 16) + 4 * (capw * 8 + 64 * 4)
+    return b >= BLOCKED_MIN_BATCH and row_bytes in _BLOCKED_ROW_BYTES and lds <= 160 * 1024
+
+
+def _blocked(q: Tensor, items: Tensor, k: int, dtype: int, mask: Tensor | None,
+             ids: Tensor, scores: Tensor) -> None:
+    b, d = q.shape
+    n = items.shape[0]
+    lib = nat.lib()
+    dev = q.device
+    ws = nat.workspace(lib.rt_blocked_scan_topk_workspace(b, n, d * q.element_size(), k), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_blocked_scan_topk(
+            nat.ptr(q), b, nat.ptr(items), n, d, k, dtype, nat.ptr(mask),
+            0 if mask is None else mask.shape[1], nat.ptr(ids), nat.ptr(scores), nat.ptr(ws),
+            ws.numel(), nat.stream(dev),
+        )
+    nat.check(st)
+
+
 # --- int8 full scan + top-k ---------------------------------------------------------------
 
 
@@ -64,6 +94,9 @@ def int8_scan_topk(
     n = item_codes.shape[0]
     ids = torch.empty((b, k), dtype=torch.int64, device=dev)
     scores = torch.empty((b, k), dtype=torch.int32, device=dev)
+    if _use_blocked(b, d, k):
+        _blocked(q, item_codes, k, 0, mask, ids, scores)
+        return ids, scores
     lib = nat.lib()
     ws_bytes = lib.rt_int8_scan_topk_workspace(b, n, d, k)
     ws = nat.workspace(ws_bytes, dev)
@@ -121,6 +154,9 @@ def dense_scan_topk(
     dev = nat.require_device(q, item_embs)
     ids = torch.empty((b, k), dtype=torch.int64, device=dev)
     scores = torch.empty((b, k), dtype=torch.float32, device=dev)
+    if _use_blocked(b, 2 * d, k):
+        _blocked(q, item_embs, k, 1 + _DENSE_DTYPES[q.dtype], mask, ids, scores)
+        return ids, scores
     lib = nat.lib()
     ws = nat.workspace(lib.rt_dense_scan_topk_workspace(b, n, d, k), dev)
     with torch.cuda.device(dev):

@@ -70,6 +70,17 @@ def test_random_parity(dev, b, n, d, k):
     _check(dev, q, it, k)
 
 
+@pytest.mark.parametrize("b,n,d,k", [(128, 20000, 128, 100), (1024, 5000, 64, 10),
+                                     (300, 3000, 256, 1000)])
+def test_large_batch_parity(dev, b, n, d, k):
+    """B >= 128 runs the register-blocked kernel."""
+    g = rng(b + n + d + k + 5)
+    q = g.standard_normal((b, d)).astype(np.float32)
+    it = g.standard_normal((n, d)).astype(np.float32)
+    _check(dev, q, it, k)
+    _check(dev, q, it, k, torch.float16)
+
+
 def test_fp16(dev):
     g = rng(41)
     q = g.standard_normal((9, 128)).astype(np.float32)

@@ -175,3 +175,26 @@ def test_full_size_properties(dev):
         assert not (beats[r] & ~member).any()
     del items
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize(
+    "b,n,d,k", [(128, 5000, 512, 100), (300, 20000, 128, 10), (257, 30000, 256, 1000),
+                (1024, 3000, 512, 7)],
+)
+def test_large_batch_parity(dev, b, n, d, k):
+    """B >= 128 runs the register-blocked kernel (256 queries per workgroup)."""
+    g = rng(b * 3 + n + d + k)
+    q = g.integers(-128, 128, (b, d), dtype=np.int8)
+    items = g.integers(-128, 128, (n, d), dtype=np.int8)
+    _check(dev, q, items, k)
+
+
+def test_large_batch_seeded_ties_masked(dev):
+    g = rng(16)
+    base = g.integers(-127, 128, (64, 128), dtype=np.int8)
+    items = base[g.integers(0, 64, 2_200_000)]
+    q = g.integers(-128, 128, (200, 128), dtype=np.int8)
+    _check(dev, q, items, 100)
+    mask = g.random((130, 50000)) < 0.05
+    mask[7] = False
+    _check(dev, q[:130], items[:50000], 100, mask)
