@@ -48,7 +48,9 @@ struct WaveTopK16 {
   // pass. item = row * row_stride. Appends composites >= tau that pass the filter; compacts
   // lists that could overflow on the next tile.
   __device__ void push(const Score acc[4], int64_t row0, int64_t r1, int64_t row_stride) {
-    const bool hit = acc[0] >= ts || acc[1] >= ts || acc[2] >= ts || acc[3] >= ts;
+    const Score m01 = acc[0] > acc[1] ? acc[0] : acc[1];
+    const Score m23 = acc[2] > acc[3] ? acc[2] : acc[3];
+    const bool hit = (m01 > m23 ? m01 : m23) >= ts;
     if (!__any(hit)) return;
     const int col = lane_id() & 15;
 #pragma unroll

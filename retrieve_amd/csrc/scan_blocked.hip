@@ -27,6 +27,8 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 constexpr int kBlkRows = 64;      // items per staged tile
 constexpr int kBlkQpw = 64;       // queries per wave
 constexpr int kBlkQpg = kScanWaves * kBlkQpw;  // queries per workgroup (query group)
+// Cache-policy bits of the main pass's direct-to-LDS loads (streamed once: nontemporal).
+constexpr int kNontemporal = 2;
 
 struct I8x32 {
   using Score = int32_t;
@@ -63,26 +65,62 @@ struct F16x32 : BF16x32 {
   }
 };
 
-template <int RB>  // row bytes
-constexpr int blk_pitch() {
-  return RB + 16;
+// Tiles in flight: 3 at 512-byte rows (32 KiB each), 4 below.
+template <int RB>
+constexpr int blk_stages() {
+  return RB >= 512 ? 3 : 4;
 }
 
 template <int RB>
 constexpr size_t blk_stage_bytes() {
-  return static_cast<size_t>(2) * kBlkRows * blk_pitch<RB>();  // double buffer
+  return static_cast<size_t>(blk_stages<RB>()) * kBlkRows * RB;
 }
 
-// SEED: per query, each wave's best composite over the strided sample, written to
-// lists[q * S + wave index] (one-entry lists); else candidate lists per (wave, query).
+// Waves per SIMD: two for rows up to 256 bytes (each one's MFMAs cover the other's waits);
+// one at 512-byte rows, where 64 queries' fragments take 128 registers.
+template <int RB>
+constexpr int blk_waves_per_simd() {
+  return RB >= 512 ? 1 : 2;
+}
+
+// The max of an accumulator tile's 16 values, as a tree of v_max / v_max3 (not a serial
+// compare chain). NaN scores drop out of the float max, as they never pass a threshold.
+__device__ inline int32_t vmax(int32_t a, int32_t b) { return a > b ? a : b; }
+__device__ inline float vmax(float a, float b) { return __builtin_fmaxf(a, b); }
+
+template <class Score, class Acc>
+__device__ inline Score max16(const Acc& v) {
+  Score m[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m[i] = vmax(static_cast<Score>(v[2 * i]), static_cast<Score>(v[2 * i + 1]));
+#pragma unroll
+  for (int w = 4; w > 0; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; ++i) m[i] = vmax(m[i], m[i + w]);
+  return m[0];
+}
+
+// s_waitcnt immediate: vmcnt <= N (N < 64), expcnt and lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// SEED: per query, each workgroup's best composite over the strided sample, written to
+// lists[q * gridDim.x + workgroup] (one-entry lists); else candidate lists per (wave, query).
 template <class Op, int RB, bool SEED>
-__global__ void __launch_bounds__(kScanThreads) scan_blocked_kernel(ScanArgs a) {
+__global__ void __launch_bounds__(kScanThreads)
+    __attribute__((amdgpu_waves_per_eu(blk_waves_per_simd<RB>(), blk_waves_per_simd<RB>())))
+    scan_blocked_kernel(ScanArgs a) {
   using Score = typename Op::Score;
   constexpr int KS = RB / 32;  // MFMA steps per row
-  constexpr int P = blk_pitch<RB>();
   constexpr int TILE_BYTES = kBlkRows * RB;
-  constexpr int LOADS = TILE_BYTES / (kScanThreads * 16);  // 16-byte loads per thread
+  constexpr int LOADS = TILE_BYTES / (kScanThreads * 16);  // 16-byte loads per thread per tile
+  constexpr int CH = RB / 16;                              // 16-byte chunks per row
+  constexpr int STAGES = blk_stages<RB>();
   static_assert(TILE_BYTES % (kScanThreads * 16) == 0, "tile must split into 16-byte loads");
+  static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   int8_t* stage = reinterpret_cast<int8_t*>(smem);
   uint64_t* scratch = reinterpret_cast<uint64_t*>(stage + blk_stage_bytes<RB>());
@@ -103,6 +141,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_blocked_kernel(ScanArgs a) 
   v4i qf[2][KS];
   uint64_t tau[2];
   Score ts[2];
+  const uint64_t* qmask[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int64_t q = q0 + 32 * j + c32;
@@ -118,11 +157,6 @@ __global__ void __launch_bounds__(kScanThreads) scan_blocked_kernel(ScanArgs a) 
       tau[j] = ~0ull;
     }
     ts[j] = Op::thresh(tau[j]);
-  }
-  const uint64_t* qmask[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t q = q0 + 32 * j + c32;
     qmask[j] = a.mask != nullptr && q < a.B ? a.mask + q * a.mask_words : nullptr;
   }
   uint64_t best[2] = {0ull, 0ull};  // SEED
@@ -135,68 +169,74 @@ __global__ void __launch_bounds__(kScanThreads) scan_blocked_kernel(ScanArgs a) 
 
   const int64_t n = a.n_rows;
   const int64_t ntiles = cdiv(n, kBlkRows);
-  v4i v[LOADS];
-  // load l of a tile covers its bytes [(l * 256 + tid) * 16, +16); row = that / RB
-  auto load_tile = [&](int64_t t) {
-    const int64_t r0 = t * kBlkRows;
+  // Staged tile layout (no padding): row r's 16-byte chunk c sits at r * RB + (c ^ (r % CH)) * 16,
+  // so the 32 rows of an MFMA read start on different banks. A wave's direct-to-LDS load writes
+  // 1 KiB contiguously in lane order, so the swizzle goes into the global address each lane
+  // fetches (a permutation within the row: still one contiguous 1 KiB span per instruction).
+  auto issue = [&](int64_t tt, int st) {
+    int8_t* base = stage + st * TILE_BYTES;
 #pragma unroll
     for (int l = 0; l < LOADS; ++l) {
-      const int off = (l * kScanThreads + tid) * 16;
-      const int64_t row = r0 + off / RB;
-      if (row < n) {
-        const v4i* src = reinterpret_cast<const v4i*>(I + row * a.row_stride * RB + off % RB);
-        v[l] = SEED ? *src : __builtin_nontemporal_load(src);
-      } else {
-        v[l] = v4i{0, 0, 0, 0};
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-    int8_t* dst = stage + buf * kBlkRows * P;
-#pragma unroll
-    for (int l = 0; l < LOADS; ++l) {
-      const int off = (l * kScanThreads + tid) * 16;
-      *reinterpret_cast<v4i*>(dst + (off / RB) * P + off % RB) = v[l];
+      const int sidx = l * kScanThreads + wave * kWave + lane;  // 16-byte slot of the tile
+      const int r = sidx / CH;
+      const int c = (sidx % CH) ^ (r % CH);
+      int64_t row = tt * kBlkRows + r;
+      row = row < n ? row : n - 1;  // rows past the end load a valid row and are never scored
+      const int8_t* g = I + row * a.row_stride * RB + c * 16;
+      __builtin_amdgcn_global_load_lds(
+          g,
+          (__attribute__((address_space(3))) void*)(base + (l * kScanThreads + wave * kWave) * 16),
+          16, 0, SEED ? 0 : kNontemporal);
     }
   };
 
   int64_t t = wg;
-  int buf = 0;
-  if (t < ntiles) {
-    load_tile(t);
-    store_tile(0);
+#pragma unroll
+  for (int st = 0; st < STAGES - 1; ++st) {
+    if (t + st * nwg < ntiles) issue(t + st * nwg, st);
   }
-  __syncthreads();
-  for (; t < ntiles; t += nwg) {
-    const bool more = t + nwg < ntiles;
-    if (more) load_tile(t + nwg);
-    const int8_t* src = stage + buf * kBlkRows * P;
-    typename Op::Acc acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = Op::zero();
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      v4i af[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        af[i] = *reinterpret_cast<const v4i*>(src + (32 * i + c32) * P + 32 * s + 16 * half);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma(af[i], qf[j][s], acc[i][j]);
+  // vmcnt retires in issue order on this architecture (one counter for loads and stores), so
+  // waiting until at most the later tiles' loads are outstanding also covers any list store
+  // issued in between.
+  for (int it = 0; t < ntiles; ++it, t += nwg) {
+    const int64_t tn = t + (STAGES - 1) * nwg;
+    if (tn < ntiles) issue(tn, (it + STAGES - 1) % STAGES);
+    // this tile's loads are done once at most the later tiles' loads are outstanding
+    const int64_t after = (ntiles - 1 - t) / nwg;  // this workgroup's tiles after t
+    const int later = static_cast<int>(after < STAGES - 1 ? after : STAGES - 1);
+    if (later >= 3) {
+      wait_vmcnt<3 * LOADS < 64 ? 3 * LOADS : 0>();
+    } else if (later == 2) {
+      wait_vmcnt<2 * LOADS>();
+    } else if (later == 1) {
+      wait_vmcnt<LOADS>();
+    } else {
+      wait_vmcnt<0>();
     }
-    if (more) store_tile(buf ^ 1);
+    __syncthreads();
 
-    const int64_t rb = t * kBlkRows;
-    if constexpr (SEED) {
+    const int8_t* src = stage + (it % STAGES) * TILE_BYTES;
+    // two passes of 32 rows: 2 accumulator tiles (this wave's 64 queries) per pass
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i) {
+      // all of the pass's A fragments first, so the LDS reads overlap the MFMA stream
+      v4i af[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int r = 32 * i + c32;
+        af[s] = *reinterpret_cast<const v4i*>(src + r * RB + (((2 * s + half) ^ (r % CH)) * 16));
+      }
+      typename Op::Acc acc[2] = {Op::zero(), Op::zero()};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[j] = Op::mma(af[s], qf[j][s], acc[j]);
+      }
+      const int64_t rb = t * kBlkRows + 32 * i;
+      if constexpr (SEED) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t row = rb + 32 * i + (r / 4) * 8 + half * 4 + (r % 4);
+          const int64_t row = rb + (r / 4) * 8 + half * 4 + (r % 4);
           const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
@@ -204,27 +244,22 @@ __global__ void __launch_bounds__(kScanThreads) scan_blocked_kernel(ScanArgs a) 
             if (ok && qmask[j] != nullptr) {
               ok = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
             }
-            const uint64_t c = composite(Op::key(acc[i][j][r]), item);
+            const uint64_t c = composite(Op::key(acc[j][r]), item);
             best[j] = ok && c > best[j] ? c : best[j];
           }
         }
-    } else {
-      bool hit = false;
+      } else {
+        // fast path: one compare per query column against the max of its 16 scores
+        bool hit = false;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) hit |= acc[i][j][r] >= ts[j];
-      if (__any(hit)) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 2; ++j) hit |= max16<Score>(acc[j]) >= ts[j];
+        if (__any(hit)) {
 #pragma unroll
           for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const Score sc = acc[i][j][r];
-              const int64_t row = rb + 32 * i + (r / 4) * 8 + half * 4 + (r % 4);
+              const Score sc = acc[j][r];
+              const int64_t row = rb + (r / 4) * 8 + half * 4 + (r % 4);
               if (row < n && sc >= ts[j]) {
                 const uint32_t item = static_cast<uint32_t>(row);
                 const uint64_t c = composite(Op::key(sc), item);
@@ -239,27 +274,27 @@ __global__ void __launch_bounds__(kScanThreads) scan_blocked_kernel(ScanArgs a) 
                 }
               }
             }
-        wave_sync_memory();
-        // a query gains at most 64 entries per tile
-        for (int jq = 0; jq < 2; ++jq) {
-          const bool full = cnt[32 * jq + c32] > a.capw - kBlkRows;
-          uint64_t need = __ballot(full) & 0xffffffffull;
-          while (need != 0ull) {
-            const int c = __builtin_ctzll(need);
-            need &= need - 1;
-            const int q = 32 * jq + c;
-            const uint64_t nt = wave_compact(lists + q * static_cast<int64_t>(a.capw), &cnt[q],
-                                             scratch + wave * a.capw, a.capw, a.k);
-            if (c32 == c && nt > tau[jq]) {
-              tau[jq] = nt;
-              ts[jq] = Op::thresh(nt);
+          wave_sync_memory();
+          // a query gains at most 32 entries per pass
+          for (int jq = 0; jq < 2; ++jq) {
+            const bool full = cnt[32 * jq + c32] > a.capw - kBlkRows;
+            uint64_t need = __ballot(full) & 0xffffffffull;
+            while (need != 0ull) {
+              const int c = __builtin_ctzll(need);
+              need &= need - 1;
+              const int q = 32 * jq + c;
+              const uint64_t nt = wave_compact(lists + q * static_cast<int64_t>(a.capw),
+                                               &cnt[q], scratch + wave * a.capw, a.capw, a.k);
+              if (c32 == c && nt > tau[jq]) {
+                tau[jq] = nt;
+                ts[jq] = Op::thresh(nt);
+              }
             }
           }
         }
       }
     }
     __syncthreads();
-    buf ^= 1;
   }
 
   if constexpr (SEED) {
@@ -317,7 +352,7 @@ static int dispatch_blk(int64_t row_bytes, const ScanArgs& a, const PassPlan& p,
 }
 
 static size_t blk_lds_for(int64_t row_bytes, int capw) {
-  return static_cast<size_t>(2) * kBlkRows * (row_bytes + 16) +
+  return static_cast<size_t>(row_bytes >= 512 ? 3 : 4) * kBlkRows * row_bytes +
          kScanWaves * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
 }
 
@@ -326,8 +361,6 @@ constexpr size_t kMaxLds = 160 * 1024;
 // List capacity: k plus a tile's appends (64 per query), a power of two (sorted whole).
 static int blk_capw(int64_t k) { return static_cast<int>(next_pow2(k + kBlkRows)); }
 
-// Workgroups of the blocked main pass per CU (LDS-bound: the double-buffered stage).
-constexpr int64_t kBlkWorkgroupsPerCU = 1;
 
 template <class Op>
 static int run_blocked(const void* queries, int64_t B, const void* items, int64_t N,
@@ -349,7 +382,8 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   if (hipGetDevice(&dev) == hipSuccess) {
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   }
-  const ScanPlan plan = plan_scan(B, N, k, kBlkQpg, kBlkQpg, cus * kBlkWorkgroupsPerCU,
+  const int64_t per_cu = row_bytes >= 512 ? 1 : 2;  // blk_waves_per_simd
+  const ScanPlan plan = plan_scan(B, N, k, kBlkQpg, kBlkQpg, cus * per_cu,
                                   blk_capw(k), kBlkRows);
   RT_CHECK_ARG(blk_lds_for(row_bytes, plan.main.capw) <= kMaxLds,
                "k = %lld is too large for the blocked scan at %lld-byte rows",
