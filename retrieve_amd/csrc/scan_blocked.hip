@@ -40,6 +40,9 @@ struct I8x32 {
   }
   __device__ static uint32_t key(Score s) { return key_of_i32(s); }
   __device__ static Score thresh(uint64_t tau) { return i32_of_key(composite_key(tau)); }
+  // scores are already ordered ints: the hit test takes maxima of the raw values
+  static constexpr bool kIntScores = true;
+  __device__ static int32_t skey(Score s) { return s; }
 };
 
 struct BF16x32 {
@@ -55,6 +58,13 @@ struct BF16x32 {
   __device__ static Score thresh(uint64_t tau) {
     const uint32_t k = composite_key(tau);
     return k <= key_of_f32(-INFINITY) ? -INFINITY : f32_of_key(k);
+  }
+  static constexpr bool kIntScores = false;
+  // Order-preserving map of a float to int32 (signed compare): the bits of a non-negative
+  // float, the magnitude bits flipped for a negative one (-0.0 maps below +0.0, as in key order).
+  __device__ static int32_t skey(Score s) {
+    const int32_t b = __builtin_bit_cast(int32_t, s);
+    return b >= 0 ? b : b ^ 0x7fffffff;
   }
 };
 
@@ -83,21 +93,30 @@ constexpr int blk_waves_per_simd() {
   return RB >= 512 ? 1 : 2;
 }
 
-// The max of an accumulator tile's 16 values, as a tree of v_max / v_max3 (not a serial
-// compare chain). NaN scores drop out of the float max, as they never pass a threshold.
-__device__ inline int32_t vmax(int32_t a, int32_t b) { return a > b ? a : b; }
-__device__ inline float vmax(float a, float b) { return __builtin_fmaxf(a, b); }
+__device__ inline int32_t imax(int32_t a, int32_t b) { return a > b ? a : b; }
 
-template <class Score, class Acc>
-__device__ inline Score max16(const Acc& v) {
-  Score m[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) m[i] = vmax(static_cast<Score>(v[2 * i]), static_cast<Score>(v[2 * i + 1]));
-#pragma unroll
-  for (int w = 4; w > 0; w >>= 1)
-#pragma unroll
-    for (int i = 0; i < w; ++i) m[i] = vmax(m[i], m[i + w]);
-  return m[0];
+// Max of 4 accumulator values in the signed-int key domain of Op::skey. RAW: take maxima of the
+// raw bits as ints (v_max3_i32, no NaN canonicalisation) -- exact for every value with the sign
+// bit clear and below every such value otherwise, so it decides "max >= threshold" whenever the
+// threshold's key is >= 0. Else the float max (NaN drops out) mapped through skey.
+// (by value: __builtin_bit_cast applied directly to a vector element v[i] reads element 0)
+template <class S>
+__device__ inline int32_t raw_bits(S s) {
+  return __builtin_bit_cast(int32_t, s);
+}
+
+template <class Op, bool RAW, class Acc>
+__device__ inline int32_t group_max(const Acc& v, int g) {
+  if constexpr (RAW) {
+    return imax(imax(imax(raw_bits(v[4 * g]), raw_bits(v[4 * g + 1])), raw_bits(v[4 * g + 2])),
+                raw_bits(v[4 * g + 3]));
+  } else {
+    const float m = __builtin_fmaxf(__builtin_fmaxf(static_cast<float>(v[4 * g]),
+                                                    static_cast<float>(v[4 * g + 1])),
+                                    __builtin_fmaxf(static_cast<float>(v[4 * g + 2]),
+                                                    static_cast<float>(v[4 * g + 3])));
+    return Op::skey(static_cast<typename Op::Score>(m));
+  }
 }
 
 // s_waitcnt immediate: vmcnt <= N (N < 64), expcnt and lgkmcnt unconstrained (gfx9 encoding).
@@ -105,6 +124,18 @@ template <int N>
 __device__ inline void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Workgroup barrier over the staged tiles: waits for this wave's LDS accesses (lgkmcnt(0)),
+// then s_barrier. __syncthreads() would also wait for every outstanding global load (its
+// workgroup release fence), draining the tiles still in flight; the direct-to-LDS loads of the
+// tile about to be read are covered by the wait_vmcnt before this. The empty asm statements
+// keep the compiler from moving memory accesses across the barrier.
+__device__ inline void tile_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt and expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // SEED: per query, each workgroup's best composite over the strided sample, written to
@@ -159,13 +190,16 @@ __global__ void __launch_bounds__(kScanThreads)
     ts[j] = Op::thresh(tau[j]);
     qmask[j] = a.mask != nullptr && q < a.B ? a.mask + q * a.mask_words : nullptr;
   }
+  // thresholds in the skey domain, and whether the raw-bits group maxima decide the hit test
+  int32_t th[2] = {Op::skey(ts[0]), Op::skey(ts[1])};
+  bool raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
   uint64_t best[2] = {0ull, 0ull};  // SEED
   // list slot of this wave: query group (64 queries) g = blockIdx.y * 4 + wave, slot g * nwg + wg
   const int64_t slot = (static_cast<int64_t>(blockIdx.y) * kScanWaves + wave) * nwg + wg;
   uint64_t* lists = a.lists + slot * kBlkQpw * static_cast<int64_t>(a.capw);
-  if constexpr (!SEED) {
-    for (int i = lane; i < kBlkQpw; i += kWave) cnt[i] = 0;
-  }
+  // list lengths of this lane's two queries (the same in both halves of the wave): each list
+  // belongs to this wave alone, so appends take positions from ballots, not atomics
+  int nq[2] = {0, 0};
 
   const int64_t n = a.n_rows;
   const int64_t ntiles = cdiv(n, kBlkRows);
@@ -173,20 +207,47 @@ __global__ void __launch_bounds__(kScanThreads)
   // so the 32 rows of an MFMA read start on different banks. A wave's direct-to-LDS load writes
   // 1 KiB contiguously in lane order, so the swizzle goes into the global address each lane
   // fetches (a permutation within the row: still one contiguous 1 KiB span per instruction).
+  int toff[LOADS];  // this lane's byte offset in a full tile (row r, swizzled chunk c)
+#pragma unroll
+  for (int l = 0; l < LOADS; ++l) {
+    const int sidx = l * kScanThreads + wave * kWave + lane;  // 16-byte slot of the tile
+    const int r = sidx / CH;
+    toff[l] = r * RB + ((sidx % CH) ^ (r % CH)) * 16;
+  }
+  // Several query groups (gridDim.y > 1) read the same tiles from this XCD's L2: keep the lines
+  // (temporal loads); with one group each tile is read once and streams past (nontemporal).
+  const bool shared_tiles = gridDim.y > 1;
   auto issue = [&](int64_t tt, int st) {
     int8_t* base = stage + st * TILE_BYTES;
+    if (!SEED && (tt + 1) * kBlkRows <= n) {
+      // a full tile of consecutive rows: a uniform tile address plus 32-bit lane offsets
+      const int8_t* tile = I + tt * static_cast<int64_t>(TILE_BYTES);
+#pragma unroll
+      for (int l = 0; l < LOADS; ++l) {
+        // (the global address goes through a named pointer: passing the sum straight to the
+        // builtin drops the kernel from the host-side compile)
+        const int8_t* g = tile + toff[l];
+        int8_t* dst = base + (l * kScanThreads + wave * kWave) * 16;
+        if (shared_tiles) {
+          __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(dst), 16,
+                                           0, 0);
+        } else {
+          __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(dst), 16,
+                                           0, kNontemporal);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int l = 0; l < LOADS; ++l) {
-      const int sidx = l * kScanThreads + wave * kWave + lane;  // 16-byte slot of the tile
-      const int r = sidx / CH;
-      const int c = (sidx % CH) ^ (r % CH);
+      const int r = toff[l] / RB;
       int64_t row = tt * kBlkRows + r;
       row = row < n ? row : n - 1;  // rows past the end load a valid row and are never scored
-      const int8_t* g = I + row * a.row_stride * RB + c * 16;
+      const int8_t* g = I + row * a.row_stride * RB + toff[l] % RB;
       __builtin_amdgcn_global_load_lds(
           g,
           (__attribute__((address_space(3))) void*)(base + (l * kScanThreads + wave * kWave) * 16),
-          16, 0, SEED ? 0 : kNontemporal);
+          16, 0, 0);
     }
   };
 
@@ -195,48 +256,52 @@ __global__ void __launch_bounds__(kScanThreads)
   for (int st = 0; st < STAGES - 1; ++st) {
     if (t + st * nwg < ntiles) issue(t + st * nwg, st);
   }
-  // vmcnt retires in issue order on this architecture (one counter for loads and stores), so
-  // waiting until at most the later tiles' loads are outstanding also covers any list store
-  // issued in between.
+  static_assert(STAGES >= 3 && STAGES <= 4, "wait ladder covers 1-2 later tiles");
   for (int it = 0; t < ntiles; ++it, t += nwg) {
-    const int64_t tn = t + (STAGES - 1) * nwg;
-    if (tn < ntiles) issue(tn, (it + STAGES - 1) % STAGES);
-    // this tile's loads are done once at most the later tiles' loads are outstanding
+    // Tile t has landed once at most the loads of this workgroup's later tiles issued so far
+    // (up to STAGES - 2 of them) are outstanding: vmcnt retires in issue order on this
+    // architecture, one counter for loads and stores, so list stores issued in between only
+    // make the wait stricter.
     const int64_t after = (ntiles - 1 - t) / nwg;  // this workgroup's tiles after t
-    const int later = static_cast<int>(after < STAGES - 1 ? after : STAGES - 1);
-    if (later >= 3) {
-      wait_vmcnt<3 * LOADS < 64 ? 3 * LOADS : 0>();
-    } else if (later == 2) {
-      wait_vmcnt<2 * LOADS>();
+    const int later = static_cast<int>(after < STAGES - 2 ? after : STAGES - 2);
+    if (later >= 2) {
+      wait_vmcnt<STAGES >= 4 ? 2 * LOADS : 0>();
     } else if (later == 1) {
       wait_vmcnt<LOADS>();
     } else {
       wait_vmcnt<0>();
     }
-    __syncthreads();
+    // every wave's share of tile t is in LDS, and every wave is done reading tile t - nwg, whose
+    // stage the next load goes into
+    tile_barrier();
+    const int64_t tn = t + (STAGES - 1) * nwg;
+    if (tn < ntiles) issue(tn, (it + STAGES - 1) % STAGES);
 
     const int8_t* src = stage + (it % STAGES) * TILE_BYTES;
-    // two passes of 32 rows: 2 accumulator tiles (this wave's 64 queries) per pass
+    // 2 x 2 output tiles (rows 32 i + ..., this wave's query columns 32 j + ...): four
+    // independent accumulator chains keep the matrix pipeline full
+    typename Op::Acc acc[2][2] = {{Op::zero(), Op::zero()}, {Op::zero(), Op::zero()}};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      // all of the pass's A fragments first, so the LDS reads overlap the MFMA stream
-      v4i af[KS];
+    for (int s = 0; s < KS; ++s) {
+      v4i af[2];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
+      for (int i = 0; i < 2; ++i) {
         const int r = 32 * i + c32;
-        af[s] = *reinterpret_cast<const v4i*>(src + r * RB + (((2 * s + half) ^ (r % CH)) * 16));
+        af[i] = *reinterpret_cast<const v4i*>(src + r * RB + (((2 * s + half) ^ (r % CH)) * 16));
       }
-      typename Op::Acc acc[2] = {Op::zero(), Op::zero()};
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[j] = Op::mma(af[s], qf[j][s], acc[j]);
-      }
-      const int64_t rb = t * kBlkRows + 32 * i;
-      if constexpr (SEED) {
+        for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma(af[i], qf[j][s], acc[i][j]);
+    }
+    // register r of tile (i, j) holds row t * 64 + 32 i + (r / 4) * 8 + 4 half + r % 4
+    const int64_t rt = t * kBlkRows + 4 * half;
+    if constexpr (SEED) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t row = rb + (r / 4) * 8 + half * 4 + (r % 4);
+          const int64_t row = rt + 32 * i + (r / 4) * 8 + (r % 4);
           const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
@@ -244,57 +309,90 @@ __global__ void __launch_bounds__(kScanThreads)
             if (ok && qmask[j] != nullptr) {
               ok = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
             }
-            const uint64_t c = composite(Op::key(acc[j][r]), item);
+            const uint64_t c = composite(Op::key(acc[i][j][r]), item);
             best[j] = ok && c > best[j] ? c : best[j];
           }
         }
-      } else {
-        // fast path: one compare per query column against the max of its 16 scores
-        bool hit = false;
+    } else {
+      // fast path: the max of each group of 4 registers (rows 8 g + 4 half + 0..3), and one
+      // compare per tile column against the max of its 4 group maxima
+      int32_t gm[2][2][4];
+      bool hit = false;
+      if (raw) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) hit |= max16<Score>(acc[j]) >= ts[j];
-        if (__any(hit)) {
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, true>(acc[i][j], g);
+            hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= th[j];
+          }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, false>(acc[i][j], g);
+            hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= th[j];
+          }
+      }
+      if (__any(hit)) {
+        // slow path, narrowed by wave-uniform ballots: groups with a hit, then their registers
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const Score sc = acc[j][r];
-              const int64_t row = rb + (r / 4) * 8 + half * 4 + (r % 4);
-              if (row < n && sc >= ts[j]) {
+            for (int g = 0; g < 4; ++g) {
+              if (__ballot(gm[i][j][g] >= th[j]) == 0ull) continue;
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                const Score sc = acc[i][j][4 * g + u];
+                if (__ballot(sc >= ts[j]) == 0ull) continue;
+                const int64_t row = rt + 32 * i + 8 * g + u;
                 const uint32_t item = static_cast<uint32_t>(row);
                 const uint64_t c = composite(Op::key(sc), item);
-                bool keep = c >= tau[j];
+                bool keep = row < n && sc >= ts[j] && c >= tau[j];
                 if (keep && qmask[j] != nullptr) {
                   keep = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
                 }
+                // lanes l and l ^ 32 score the same query: the upper half's entry goes second
+                const uint64_t kb = __ballot(keep);
+                const int lo = static_cast<int>(static_cast<uint32_t>(kb) >> c32 & 1u);
+                const int hi = static_cast<int>(static_cast<uint32_t>(kb >> 32) >> c32 & 1u);
                 if (keep) {
-                  const int q = 32 * j + c32;
-                  const int pos = atomicAdd(&cnt[q], 1);
-                  lists[q * static_cast<int64_t>(a.capw) + pos] = c;
+                  lists[(32 * j + c32) * static_cast<int64_t>(a.capw) + nq[j] + (half ? lo : 0)] =
+                      c;
                 }
+                nq[j] += lo + hi;
               }
             }
-          wave_sync_memory();
-          // a query gains at most 32 entries per pass
-          for (int jq = 0; jq < 2; ++jq) {
-            const bool full = cnt[32 * jq + c32] > a.capw - kBlkRows;
-            uint64_t need = __ballot(full) & 0xffffffffull;
-            while (need != 0ull) {
-              const int c = __builtin_ctzll(need);
-              need &= need - 1;
-              const int q = 32 * jq + c;
-              const uint64_t nt = wave_compact(lists + q * static_cast<int64_t>(a.capw),
-                                               &cnt[q], scratch + wave * a.capw, a.capw, a.k);
-              if (c32 == c && nt > tau[jq]) {
+        // a query gains at most 64 entries per tile: compact the lists that could overflow on
+        // the next one (wave_compact waits for the stores above before reading them back)
+#pragma unroll
+        for (int jq = 0; jq < 2; ++jq) {
+          uint64_t need = __ballot(nq[jq] > a.capw - kBlkRows) & 0xffffffffull;
+          while (need != 0ull) {
+            const int c = __builtin_ctzll(need);
+            need &= need - 1;
+            const int q = 32 * jq + c;
+            if (lane == c) cnt[q] = nq[jq];
+            const uint64_t nt = wave_compact(lists + q * static_cast<int64_t>(a.capw), &cnt[q],
+                                             scratch + wave * a.capw, a.capw, a.k);
+            if (c32 == c) {
+              nq[jq] = cnt[q];
+              if (nt > tau[jq]) {
                 tau[jq] = nt;
                 ts[jq] = Op::thresh(nt);
+                th[jq] = Op::skey(ts[jq]);
               }
             }
           }
         }
+        raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
       }
     }
-    __syncthreads();
   }
 
   if constexpr (SEED) {
@@ -306,9 +404,9 @@ __global__ void __launch_bounds__(kScanThreads)
       const int64_t q = q0 + 32 * j + c32;
       if (half == 0 && q < a.B) a.lists[q * nwg + wg] = b;
     }
-  } else {
-    wave_sync_memory();
-    for (int i = lane; i < kBlkQpw; i += kWave) a.counts[slot * kBlkQpw + i] = cnt[i];
+  } else if (half == 0) {
+    a.counts[slot * kBlkQpw + c32] = nq[0];
+    a.counts[slot * kBlkQpw + 32 + c32] = nq[1];
   }
 }
 
