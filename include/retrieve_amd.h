@@ -88,6 +88,32 @@ int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const uint64_t* 
 int rt_profile_enable(int on);
 int rt_profile_collect(double* total_ms, int64_t* launches);
 
+/* ---- exact clause filter --------------------------------------------------------------
+ *
+ * Replaces the clause kernels behind torch.ops.retrieve.clause_mask / clause_mask_scores
+ * (retrieve/src/retrieve/ops/triton/clause_mask.py:270-303; predicate functional.py:173-185)
+ * and the exact payload filter of st::search (silvertorch/.../fork_filters.cuh:15-56).
+ * item_attrs [N, C, A] int64 (-1 pads); clause_is_reverse [C] 0/1; query_values [B, C, V]
+ * int64, -1 pads (V == 1: the reference's [B, C], -1 = inactive clause). Clause c is active
+ * for row b iff one of its V values is not -1; it matches iff an item value equals one of
+ * them, XOR reverse[c]; an item passes iff every active clause matches. C <= 32.
+ * mode 0: out = packed bits [B, ceil(N/64)] uint64, item d at bit 63 - d % 64 (the scans'
+ *         mask layout), AND-ed with and_mask (same layout) when it is not null;
+ * mode 1: out = [B, N] uint8 0/1;
+ * mode 2: out = [B, N] float: scores[b, d] (contiguous [B, N]) where row b passes, -inf else. */
+int rt_clause_filter(const int64_t* item_attrs, int64_t N, int64_t C, int64_t A,
+                     const int8_t* clause_is_reverse, const int64_t* query_values, int64_t B,
+                     int64_t V, int mode, const float* scores, const uint64_t* and_mask,
+                     void* out, hipStream_t stream);
+
+/* Packed mask [B, ceil(N/64)] (layout above) -> each row's set items in ascending order:
+ * out_indices[b, 0:counts[b]] (int64, [B, N] buffer; the tail is not written), counts [B].
+ * The compaction of torch.ops.retrieve.clause_compact
+ * (retrieve/src/retrieve/ops/triton/clause_compact.py:174-187, _host.py:50-79). */
+size_t rt_mask_compact_workspace(int64_t B, int64_t N);
+int rt_mask_compact(const uint64_t* mask, int64_t B, int64_t N, int64_t* out_indices,
+                    int64_t* counts, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

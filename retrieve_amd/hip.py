@@ -263,3 +263,176 @@ __all__ = [
     "int8_scan_topk",
     "oporp_1bit_match_topk_full",
 ]
+
+
+# --- exact clause filter (functional.py:173-185) --------------------------------------------
+
+_CLAUSE_BITS, _CLAUSE_BOOL, _CLAUSE_SCORES = 0, 1, 2
+
+
+def _clause_prep(item_clause_attrs: Tensor, clause_is_reverse: Tensor, query_values: Tensor,
+                 *, sets: bool = False):
+    """The checks of ``ops/triton/clause_mask.py:158-181``: ``[N, C, A_max]`` items (contiguous),
+    ``[B, C]`` query values (``[B, C, V]`` value sets where ``sets``), ``[C]`` reverse flags."""
+    if item_clause_attrs.dim() != 3:
+        raise ValueError("item_clause_attrs must be [N, C, A_max]")
+    if query_values.dim() != 2 and not (sets and query_values.dim() == 3):
+        raise ValueError("query_clause_attrs must be [B, C]" + (" or [B, C, V]" if sets else ""))
+    n, c, _ = item_clause_attrs.shape
+    if query_values.shape[1] != c:
+        raise ValueError(f"clause-count mismatch: items C={c}, query C={query_values.shape[1]}")
+    if item_clause_attrs.dtype != torch.int64 or query_values.dtype != torch.int64:
+        raise TypeError("item_clause_attrs and query_clause_attrs must be int64")
+    if clause_is_reverse.shape != (c,):
+        raise ValueError(f"clause_is_reverse must be [C] = [{c}]")
+    if c > 32:
+        raise ValueError(f"at most 32 clauses, got C={c}")
+    _check_items(item_clause_attrs=item_clause_attrs)
+    rev = clause_is_reverse.to(torch.int8).contiguous()
+    q = query_values.contiguous()
+    if q.dim() == 2:
+        q = q.unsqueeze(2)
+    return rev, q
+
+
+def _clause_filter(item_clause_attrs: Tensor, rev: Tensor, q: Tensor, mode: int, out: Tensor,
+                   scores: Tensor | None = None, and_mask: Tensor | None = None) -> None:
+    n, c, a = item_clause_attrs.shape
+    b, _, v = q.shape
+    if b == 0 or n == 0:
+        return
+    dev = nat.require_device(item_clause_attrs, q, rev, out)
+    with torch.cuda.device(dev):
+        st = nat.lib().rt_clause_filter(
+            nat.ptr(item_clause_attrs), n, c, a, nat.ptr(rev), nat.ptr(q), b, v, mode,
+            nat.ptr(scores), nat.ptr(and_mask), nat.ptr(out), nat.stream(dev),
+        )
+    nat.check(st)
+
+
+@torch.library.custom_op("retrieve::clause_mask", mutates_args=(), device_types="cuda")
+def clause_mask(
+    item_clause_attrs: Tensor, clause_is_reverse: Tensor, query_clause_attrs: Tensor
+) -> Tensor:
+    """Exact clause evaluation → ``[B, N]`` bool (``ops/triton/clause_mask.py:270-281``): clause
+    ``c`` matches iff some item value equals the query value, XOR ``clause_is_reverse[c]``; a
+    query value ``-1`` is an inactive clause; AND over clauses."""
+    rev, q = _clause_prep(item_clause_attrs, clause_is_reverse, query_clause_attrs)
+    out = torch.empty((q.shape[0], item_clause_attrs.shape[0]), dtype=torch.bool,
+                      device=query_clause_attrs.device)
+    _clause_filter(item_clause_attrs, rev, q, _CLAUSE_BOOL, out)
+    return out
+
+
+@clause_mask.register_fake
+def _(item_clause_attrs, clause_is_reverse, query_clause_attrs):
+    return query_clause_attrs.new_empty(
+        (query_clause_attrs.shape[0], item_clause_attrs.shape[0]), dtype=torch.bool
+    )
+
+
+@torch.library.custom_op("retrieve::clause_mask_scores", mutates_args=(), device_types="cuda")
+def clause_mask_scores(
+    scores: Tensor, item_clause_attrs: Tensor, clause_is_reverse: Tensor,
+    query_clause_attrs: Tensor,
+) -> Tensor:
+    """``where(clause_mask(...), scores, -inf)`` in one pass (``ops/triton/clause_mask.py:284-303``);
+    ``scores`` must be ``[B, N]`` float32."""
+    rev, q = _clause_prep(item_clause_attrs, clause_is_reverse, query_clause_attrs)
+    b, n = q.shape[0], item_clause_attrs.shape[0]
+    if scores.shape != (b, n) or scores.dtype != torch.float32:
+        raise ValueError(
+            f"scores must be [B, N] = {[b, n]} float32, got {list(scores.shape)} {scores.dtype}"
+        )
+    s = scores.contiguous()
+    out = torch.empty((b, n), dtype=torch.float32, device=scores.device)
+    _clause_filter(item_clause_attrs, rev, q, _CLAUSE_SCORES, out, scores=s)
+    return out
+
+
+@clause_mask_scores.register_fake
+def _(scores, item_clause_attrs, clause_is_reverse, query_clause_attrs):
+    return torch.empty_like(scores)
+
+
+@torch.library.custom_op("retrieve::clause_bits", mutates_args=(), device_types="cuda")
+def clause_bits(
+    item_clause_attrs: Tensor, clause_is_reverse: Tensor, query_values: Tensor,
+    and_mask: Tensor | None = None,
+) -> Tensor:
+    """The clause filter as the scans' packed mask: ``[B, ceil(N/64)]`` int64 words, item ``d``
+    at bit ``63 - d % 64`` (the order of ``silvertorch/.../ops/official/__init__.py:33-35``).
+    ``query_values`` is ``[B, C]`` (the reference predicate) or ``[B, C, V]`` value sets, ``-1``
+    pads: clause ``c`` is active iff a value is not ``-1`` and matches iff an item value is in
+    the set. ``and_mask`` (same layout) is AND-ed in, e.g. a Bloom pre-filter."""
+    rev, q = _clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
+    b, n = q.shape[0], item_clause_attrs.shape[0]
+    w = (n + 63) // 64
+    if and_mask is not None:
+        if and_mask.dtype != torch.int64 or and_mask.shape != (b, w):
+            raise ValueError(f"and_mask must be [B, ceil(N/64)] = [{b}, {w}] int64")
+        and_mask = and_mask.contiguous()
+    out = torch.empty((b, w), dtype=torch.int64, device=query_values.device)
+    _clause_filter(item_clause_attrs, rev, q, _CLAUSE_BITS, out, and_mask=and_mask)
+    return out
+
+
+@clause_bits.register_fake
+def _(item_clause_attrs, clause_is_reverse, query_values, and_mask=None):
+    n = item_clause_attrs.shape[0]
+    return query_values.new_empty((query_values.shape[0], (n + 63) // 64), dtype=torch.int64)
+
+
+def _mask_compact(mask: Tensor, n: int) -> tuple[Tensor, Tensor]:
+    b = mask.shape[0]
+    dev = mask.device
+    ids = torch.empty((b, n), dtype=torch.int64, device=dev)
+    counts = torch.empty((b,), dtype=torch.int64, device=dev)
+    if b == 0:
+        return ids, counts
+    nat.require_device(mask)
+    lib = nat.lib()
+    ws = nat.workspace(lib.rt_mask_compact_workspace(b, n), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_mask_compact(nat.ptr(mask), b, n, nat.ptr(ids), nat.ptr(counts),
+                                 nat.ptr(ws), ws.numel(), nat.stream(dev))
+    nat.check(st)
+    return ids, counts
+
+
+@torch.library.custom_op("retrieve::mask_compact", mutates_args=(), device_types="cuda")
+def mask_compact(mask: Tensor, n: int) -> tuple[Tensor, Tensor]:
+    """Packed mask ``[B, ceil(n/64)]`` int64 → ``(ids [B, n] int64, counts [B] int64)``: row
+    ``b``'s set items in ascending order on ``[0, counts[b])``; the tail is not written."""
+    if mask.dtype != torch.int64 or mask.dim() != 2 or mask.shape[1] != (n + 63) // 64:
+        raise ValueError(f"mask must be [B, ceil(n/64)] int64 for n={n}")
+    return _mask_compact(mask.contiguous(), n)
+
+
+@mask_compact.register_fake
+def _(mask, n):
+    b = mask.shape[0]
+    return mask.new_empty((b, n), dtype=torch.int64), mask.new_empty((b,), dtype=torch.int64)
+
+
+@torch.library.custom_op("retrieve::clause_compact", mutates_args=(), device_types="cuda")
+def clause_compact(
+    item_clause_attrs: Tensor, clause_is_reverse: Tensor, query_clause_attrs: Tensor
+) -> tuple[Tensor, Tensor]:
+    """Clause evaluation + compaction → ``(positive_indices [B, N] int64, counts [B] int64)``
+    (``ops/triton/clause_compact.py:174-187``): row ``b``'s passing items in ascending order on
+    ``[0, counts[b])``; the tail is not written."""
+    rev, q = _clause_prep(item_clause_attrs, clause_is_reverse, query_clause_attrs)
+    b, n = q.shape[0], item_clause_attrs.shape[0]
+    bits = torch.empty((b, (n + 63) // 64), dtype=torch.int64, device=query_clause_attrs.device)
+    _clause_filter(item_clause_attrs, rev, q, _CLAUSE_BITS, bits)
+    return _mask_compact(bits, n)
+
+
+@clause_compact.register_fake
+def _(item_clause_attrs, clause_is_reverse, query_clause_attrs):
+    b, n = query_clause_attrs.shape[0], item_clause_attrs.shape[0]
+    return (
+        query_clause_attrs.new_empty((b, n), dtype=torch.int64),
+        query_clause_attrs.new_empty((b,), dtype=torch.int64),
+    )
