@@ -98,13 +98,14 @@ int rt_profile_collect(double* total_ms, int64_t* launches);
  * for row b iff one of its V values is not -1; it matches iff an item value equals one of
  * them, XOR reverse[c]; an item passes iff every active clause matches. C <= 32.
  * mode 0: out = packed bits [B, ceil(N/64)] uint64, item d at bit 63 - d % 64 (the scans'
- *         mask layout), AND-ed with and_mask (same layout) when it is not null;
+ *         mask layout), AND-ed with and_mask ([B, and_mask_words] words, same bit layout, e.g.
+ *         a Bloom search's [B, n_bundles * 32]) when it is not null;
  * mode 1: out = [B, N] uint8 0/1;
  * mode 2: out = [B, N] float: scores[b, d] (contiguous [B, N]) where row b passes, -inf else. */
 int rt_clause_filter(const int64_t* item_attrs, int64_t N, int64_t C, int64_t A,
                      const int8_t* clause_is_reverse, const int64_t* query_values, int64_t B,
                      int64_t V, int mode, const float* scores, const uint64_t* and_mask,
-                     void* out, hipStream_t stream);
+                     int64_t and_mask_words, void* out, rt_stream_t stream);
 
 /* Packed mask [B, ceil(N/64)] (layout above) -> each row's set items in ascending order:
  * out_indices[b, 0:counts[b]] (int64, [B, N] buffer; the tail is not written), counts [B].
@@ -112,7 +113,49 @@ int rt_clause_filter(const int64_t* item_attrs, int64_t N, int64_t C, int64_t A,
  * (retrieve/src/retrieve/ops/triton/clause_compact.py:174-187, _host.py:50-79). */
 size_t rt_mask_compact_workspace(int64_t B, int64_t N);
 int rt_mask_compact(const uint64_t* mask, int64_t B, int64_t N, int64_t* out_indices,
-                    int64_t* counts, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                    int64_t* counts, void* workspace, size_t workspace_bytes,
+                    rt_stream_t stream);
+
+/* ---- Bloom index (bit-sliced 2048-doc bundles) -----------------------------------------
+ *
+ * Layout (silvertorch/.../bloom_indexer.cpp:79-110): bundle beta (docs 2048 beta ..) is
+ * w_beta = bundle_b_offsets[beta+1] - bundle_b_offsets[beta] bits per doc; position p of doc d
+ * is bit 63 - d % 64 of word (bundle_b_offsets[beta] + p) * 32 + (d % 2048) / 64. A token
+ * (feature id, value) sets the first k distinct murmur(id, value, seed) % w_beta over seeds
+ * 0, 1, ... (MurmurHash3_x64_128 of the 16-byte key id || value, h1 ^ h2;
+ * silvertorch/.../bloom_index_util.cuh:60-107, 185-208).
+ * Features (the st:: build ops' jagged layout, retrieve/src/retrieve/ops/official/adapter.py:
+ * 45-62): feature_ids int32 [C]; feature_offsets int64 [N * C + 1], the values of doc d,
+ * feature c at feature_values[feature_offsets[d*C + c] .. feature_offsets[d*C + c + 1]). */
+
+/* max_terms[beta] = max over the bundle's docs of the doc's value count (the upstream width is
+ * (int64)((double)(max_terms * k) * b_multiplier), bloom_indexer.cpp:52-70). nb = ceil(N/2048). */
+int rt_bloom_bundle_terms(const int64_t* feature_offsets, int64_t N, int64_t C, int64_t* max_terms,
+                          rt_stream_t stream);
+
+/* Writes every word of the index (words: bundle_b_offsets[nb] * 32 uint64). max_width = the
+ * largest w_beta (<= 256); 1 <= k <= 10, k <= every nonzero w_beta.
+ * Replaces: st::bloom_index_build / st::bloom_index_build_fixed
+ *   (silvertorch/.../bloom_indexer.cpp:117-136, bloom_indexer_cuda.cu:291-344, 942-961). */
+int rt_bloom_build(const int32_t* feature_ids, int64_t C, const int64_t* feature_offsets,
+                   const int64_t* feature_values, int64_t N, const int64_t* bundle_b_offsets,
+                   int64_t max_width, int64_t k, uint64_t* words, rt_stream_t stream);
+
+/* Evaluates plan_count encoded plans (retrieve_amd/bloom.py: per plan 8 byte offsets
+ * [ops, offsets, parameters, hashes] x [begin, end) into plan_data, data_bytes long) over
+ * every column: a term holds for a doc iff the first k distinct (hash % w_beta) of its hash_k
+ * stored hashes are all set (silvertorch/.../bloom_index_search_cuda.cu:305-349); AND / OR /
+ * NOT / EMPTY as in :471-534. Outputs (either may be null): out_mask [plan_count, nb * 32]
+ * words in the mask layout above, out_bool [plan_count, nb * 2048] 0/1 bytes. A malformed
+ * plan yields no match. 1 <= k <= 10, 1 <= max_stack <= 64.
+ * Replaces: st::bloom_index_search_batch(_prepared)
+ *   (silvertorch/.../bloom_index_search.cpp:551-590, bloom_index_search_cuda.cu:1829-1856). */
+size_t rt_bloom_search_workspace(int64_t data_bytes);
+int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, int64_t n_bundles,
+                    const int64_t* plan_offsets, const int8_t* plan_data, int64_t data_bytes,
+                    int64_t plan_count, int64_t max_stack, int64_t k, int64_t hash_k,
+                    int64_t* out_mask, uint8_t* out_bool, void* workspace, size_t workspace_bytes,
+                    rt_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -47,7 +47,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rt_profile_collect": (_c_int, [_c_p, _c_p]),
     "rt_clause_filter": (
         _c_int,
-        [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_p],
+        [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_i64,
+         _c_p, _c_p],
+    ),
+    "rt_bloom_bundle_terms": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "rt_bloom_build": (
+        _c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p],
+    ),
+    "rt_bloom_search_workspace": (_c_sz, [_c_i64]),
+    "rt_bloom_search": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
+         _c_sz, _c_p],
     ),
     "rt_mask_compact_workspace": (_c_sz, [_c_i64, _c_i64]),
     "rt_mask_compact": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p]),

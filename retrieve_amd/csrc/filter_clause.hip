@@ -36,7 +36,8 @@ struct ClauseArgs {
   int64_t B;
   int V;
   int64_t rows_per_wg;     // query rows each workgroup loops over
-  const uint64_t* and_mask;  // [B, W] or null (bits mode)
+  const uint64_t* and_mask;  // [B, and_words] or null (bits mode)
+  int64_t and_words;
   const float* scores;       // [B, N] (scores mode)
   void* out;
   int64_t W;
@@ -115,7 +116,7 @@ __global__ void __launch_bounds__(kClauseThreads) clause_kernel(ClauseArgs a) {
       uint64_t word = __builtin_bitreverse64(__ballot(pass));
       const int64_t w = (d - lane) >> 6;
       if (lane == 0 && w < a.W) {
-        if (a.and_mask != nullptr) word &= a.and_mask[b * a.W + w];
+        if (a.and_mask != nullptr) word &= a.and_mask[b * a.and_words + w];
         static_cast<uint64_t*>(a.out)[b * a.W + w] = word;
       }
     } else if constexpr (MODE == kClauseBool) {
@@ -237,13 +238,16 @@ using namespace rt;
 extern "C" int rt_clause_filter(const int64_t* item_attrs, int64_t N, int64_t C, int64_t A,
                                 const int8_t* clause_is_reverse, const int64_t* query_values,
                                 int64_t B, int64_t V, int mode, const float* scores,
-                                const uint64_t* and_mask, void* out, hipStream_t stream) {
+                                const uint64_t* and_mask, int64_t and_mask_words, void* out,
+                                hipStream_t stream) {
   RT_CHECK_ARG(N >= 0 && B >= 0, "N and B must be >= 0");
   RT_CHECK_ARG(C >= 0 && C <= kMaxClauses, "C must be in [0, %d], got %lld", kMaxClauses,
                static_cast<long long>(C));
   RT_CHECK_ARG(A >= 0 && A <= 4096 && V >= 1 && V <= 4096, "A must be >= 0 and V >= 1");
   RT_CHECK_ARG(mode >= kClauseBits && mode <= kClauseScores, "mode must be 0, 1 or 2");
   RT_CHECK_ARG(mode != kClauseScores || scores != nullptr, "scores mode needs scores");
+  RT_CHECK_ARG(and_mask == nullptr || and_mask_words >= cdiv(N, 64),
+               "and_mask rows must have >= ceil(N/64) words");
   RT_CHECK_ARG(N < (int64_t{1} << 40), "N too large");
   if (B == 0 || N == 0) return kOk;
   RT_CHECK_ARG(C == 0 || clause_is_reverse != nullptr, "clause_is_reverse is null");
@@ -259,6 +263,7 @@ extern "C" int rt_clause_filter(const int64_t* item_attrs, int64_t N, int64_t C,
   a.B = B;
   a.V = static_cast<int>(V);
   a.and_mask = and_mask;
+  a.and_words = and_mask_words;
   a.scores = scores;
   a.out = out;
   a.W = cdiv(N, 64);

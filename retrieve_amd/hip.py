@@ -305,7 +305,8 @@ def _clause_filter(item_clause_attrs: Tensor, rev: Tensor, q: Tensor, mode: int,
     with torch.cuda.device(dev):
         st = nat.lib().rt_clause_filter(
             nat.ptr(item_clause_attrs), n, c, a, nat.ptr(rev), nat.ptr(q), b, v, mode,
-            nat.ptr(scores), nat.ptr(and_mask), nat.ptr(out), nat.stream(dev),
+            nat.ptr(scores), nat.ptr(and_mask), 0 if and_mask is None else and_mask.shape[1],
+            nat.ptr(out), nat.stream(dev),
         )
     nat.check(st)
 
@@ -364,13 +365,15 @@ def clause_bits(
     at bit ``63 - d % 64`` (the order of ``silvertorch/.../ops/official/__init__.py:33-35``).
     ``query_values`` is ``[B, C]`` (the reference predicate) or ``[B, C, V]`` value sets, ``-1``
     pads: clause ``c`` is active iff a value is not ``-1`` and matches iff an item value is in
-    the set. ``and_mask`` (same layout) is AND-ed in, e.g. a Bloom pre-filter."""
+    the set. ``and_mask`` (``[B, >= ceil(N/64)]`` words, same bit layout) is AND-ed in, e.g. a
+    Bloom search's ``[B, n_bundles * 32]`` pre-filter."""
     rev, q = _clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
     b, n = q.shape[0], item_clause_attrs.shape[0]
     w = (n + 63) // 64
     if and_mask is not None:
-        if and_mask.dtype != torch.int64 or and_mask.shape != (b, w):
-            raise ValueError(f"and_mask must be [B, ceil(N/64)] = [{b}, {w}] int64")
+        if and_mask.dtype != torch.int64 or and_mask.dim() != 2 or and_mask.shape[0] != b \
+                or and_mask.shape[1] < w:
+            raise ValueError(f"and_mask must be [B, >= ceil(N/64)] = [{b}, >= {w}] int64")
         and_mask = and_mask.contiguous()
     out = torch.empty((b, w), dtype=torch.int64, device=query_values.device)
     _clause_filter(item_clause_attrs, rev, q, _CLAUSE_BITS, out, and_mask=and_mask)

@@ -1,0 +1,277 @@
+"""The ``torch.ops.st.*`` surface (SilverTorch's op namespace) on the HIP library: the Bloom
+index build, the expression parser and the Bloom plan search, with the reference's schemas
+(``silvertorch/.../ops/csrc/bloom_indexer.cpp:117-136``, ``expression_query_parser.cpp:457-465``,
+``bloom_index_search.cpp:551-590``). Importing this module registers them (as loading the
+reference's extension does); ``import retrieve_amd`` registers nothing.
+
+The parser's plan bytes are this library's own encoding (``retrieve_amd.bloom``), read only by
+the searches here; the index words follow the reference's bundle layout bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from retrieve_amd import _native as nat
+from retrieve_amd import bloom as bl
+
+DOCS_PER_BUNDLE = 2048
+WORDS_PER_BUNDLE = 32
+MAX_K = 10  # MAX_K_V2: positions per term
+MAX_BUILD_WIDTH = 256  # bits per doc the HIP build supports
+MAX_STACK = 64
+
+_LIB = torch.library.Library("st", "FRAGMENT")
+_LIB.define(
+    "parse_expression_query_batch(str[] expressions, Tensor silvertorch_ks, int bloom_hash_k, "
+    "bool return_query_plan=True, int max_sub_queries=5) -> (int, Tensor[])"
+)
+_LIB.define(
+    "bloom_index_build(Tensor feature_ids, Tensor feature_offsets, Tensor feature_values, "
+    "float b_multiplier, int k, bool fast_build=False) -> (Tensor, Tensor)"
+)
+_LIB.define(
+    "bloom_index_build_fixed(Tensor feature_ids, Tensor feature_offsets, Tensor feature_values, "
+    "int bits_per_doc, int k, bool fast_build=False) -> (Tensor, Tensor)"
+)
+_LIB.define(
+    "bloom_index_search_batch(Tensor bloom_index, Tensor bloom_bundle_b_offsets, "
+    "Tensor bloom_query_plans_data, Tensor bloom_query_plans_offsets, int k, int hash_k, "
+    "bool return_bool_mask=True) -> Tensor"
+)
+_LIB.define(
+    "bloom_index_search_batch_prepared(Tensor bloom_index, Tensor bloom_bundle_b_offsets, "
+    "Tensor plans, int plan_count, int max_stack_size, int k, int hash_k, "
+    "bool return_bool_mask=False) -> Tensor"
+)
+
+
+# --- parser ---------------------------------------------------------------------------------
+
+
+def _parse(expressions, silvertorch_ks, bloom_hash_k, return_query_plan=True, max_sub_queries=5):
+    """``(max_stack_size, [plans_data int8, plans_offsets int64 [8 * B]])`` on the CPU;
+    ``silvertorch_ks`` is accepted and unused, as upstream (``expression_query_parser.cpp:395``)."""
+    max_stack, data, offsets = bl.parse_batch(list(expressions), int(bloom_hash_k),
+                                              int(max_sub_queries))
+    if not return_query_plan:
+        return max_stack, []
+    return max_stack, [torch.from_numpy(data.view(np.int8)), torch.from_numpy(offsets)]
+
+
+_LIB.impl("parse_expression_query_batch", _parse, "CompositeExplicitAutograd")
+
+
+# --- build ----------------------------------------------------------------------------------
+
+
+def _features(feature_ids: Tensor, feature_offsets: Tensor, feature_values: Tensor):
+    if feature_ids.dim() != 1 or feature_offsets.dim() != 1 or feature_values.dim() != 1:
+        raise ValueError("feature_ids, feature_offsets and feature_values must be 1-D")
+    c = feature_ids.numel()
+    if c == 0 or (feature_offsets.numel() - 1) % c != 0:
+        raise ValueError("feature_offsets must hold N * C + 1 entries")
+    dev = nat.require_device(feature_ids, feature_offsets, feature_values)
+    fid = feature_ids.to(torch.int32).contiguous()
+    fo = feature_offsets.to(torch.int64).contiguous()
+    fv = feature_values.to(torch.int64).contiguous()
+    # the kernels read feature_values[fo[i] : fo[i + 1]]: the ranges must stay inside it
+    if int(fo[0].item()) != 0 or int(fo[-1].item()) != fv.numel() or \
+            bool((fo[1:] < fo[:-1]).any().item()):
+        raise ValueError("feature_offsets must rise from 0 to len(feature_values)")
+    return dev, fid, fo, fv, c, (feature_offsets.numel() - 1) // c
+
+
+def _build(dev, fid, fo, fv, c, n, offsets: Tensor, max_width: int, k: int) -> Tensor:
+    total = int(offsets[-1].item()) if offsets.numel() > 1 else 0
+    words = torch.empty(total * WORDS_PER_BUNDLE, dtype=torch.int64, device=dev)
+    if total == 0:
+        return words
+    with torch.cuda.device(dev):
+        st = nat.lib().rt_bloom_build(
+            nat.ptr(fid), c, nat.ptr(fo), nat.ptr(fv), n, nat.ptr(offsets), max_width, k,
+            nat.ptr(words), nat.stream(dev),
+        )
+    nat.check(st)
+    return words
+
+
+def _build_fixed(feature_ids, feature_offsets, feature_values, bits_per_doc, k, fast_build=False):
+    """Every bundle ``bits_per_doc`` bits per doc (``bloom_indexer_cuda.cu:942-961``)."""
+    dev, fid, fo, fv, c, n = _features(feature_ids, feature_offsets, feature_values)
+    if not 1 <= k <= MAX_K:
+        raise ValueError(f"k must be in [1, {MAX_K}], got {k}")
+    if not k <= bits_per_doc <= MAX_BUILD_WIDTH:
+        raise ValueError(f"bits_per_doc must be in [k, {MAX_BUILD_WIDTH}], got {bits_per_doc}")
+    nb = -(-n // DOCS_PER_BUNDLE)
+    offsets = torch.arange(nb + 1, dtype=torch.int64, device=dev) * int(bits_per_doc)
+    return _build(dev, fid, fo, fv, c, n, offsets, int(bits_per_doc), int(k)), offsets
+
+
+def _build_upstream(feature_ids, feature_offsets, feature_values, b_multiplier, k,
+                    fast_build=False):
+    """Bundle width ``(int64)((double)(max_terms * k) * b_multiplier)``
+    (``bloom_indexer.cpp:52-70``)."""
+    if not b_multiplier > 1.0:
+        raise RuntimeError("b_multiplier must be greater than 1.0")
+    dev, fid, fo, fv, c, n = _features(feature_ids, feature_offsets, feature_values)
+    if not 1 <= k <= MAX_K:
+        raise ValueError(f"k must be in [1, {MAX_K}], got {k}")
+    nb = -(-n // DOCS_PER_BUNDLE)
+    max_terms = torch.empty(nb, dtype=torch.int64, device=dev)
+    if nb:
+        with torch.cuda.device(dev):
+            st = nat.lib().rt_bloom_bundle_terms(nat.ptr(fo), n, c, nat.ptr(max_terms),
+                                                 nat.stream(dev))
+        nat.check(st)
+    widths = ((max_terms * int(k)).double() * float(b_multiplier)).to(torch.int64)
+    offsets = torch.zeros(nb + 1, dtype=torch.int64, device=dev)
+    offsets[1:] = widths.cumsum(0)
+    max_width = int(widths.max().item()) if nb else 0
+    if max_width > MAX_BUILD_WIDTH:
+        raise ValueError(f"a bundle needs {max_width} bits per doc; the build supports "
+                         f"{MAX_BUILD_WIDTH}")
+    return _build(dev, fid, fo, fv, c, n, offsets, max_width, int(k)), offsets
+
+
+_LIB.impl("bloom_index_build_fixed", _build_fixed, "CUDA")
+_LIB.impl("bloom_index_build", _build_upstream, "CUDA")
+
+
+@torch.library.register_fake("st::bloom_index_build_fixed")
+def _(feature_ids, feature_offsets, feature_values, bits_per_doc, k, fast_build=False):
+    n = (feature_offsets.shape[0] - 1) // feature_ids.shape[0]
+    nb = -(-n // DOCS_PER_BUNDLE)
+    return (feature_values.new_empty((nb * bits_per_doc * WORDS_PER_BUNDLE,)),
+            feature_values.new_empty((nb + 1,)))
+
+
+# --- search ---------------------------------------------------------------------------------
+
+
+def _max_stack(data: np.ndarray, offsets: np.ndarray) -> int:
+    """The evaluation stack depth of host-side encoded plans (ops segment walk)."""
+    deepest = 1
+    for i in range(offsets.size // 8):
+        o = offsets[8 * i : 8 * i + 8]
+        ops = data[o[0] : o[1]].view(np.uint8)
+        ends = data[o[2] : o[3]].view(np.int32)
+        depth = 0
+        for j, op in enumerate(ops.tolist()):
+            if op in (bl.AND, bl.OR):
+                depth -= int(ends[j + 1] - ends[j]) - 1
+            elif op in (bl.TERM, bl.EMPTY):
+                depth += 1
+            deepest = max(deepest, depth)
+    return deepest
+
+
+def _search(bloom_index: Tensor, offsets: Tensor, plan_offsets: Tensor, data: Tensor,
+            data_bytes: int, plan_count: int, max_stack: int, k: int, hash_k: int,
+            return_bool: bool) -> Tensor:
+    dev = nat.require_device(bloom_index, offsets, plan_offsets, data)
+    if bloom_index.dtype != torch.int64 or offsets.dtype != torch.int64:
+        raise TypeError("bloom_index and bloom_bundle_b_offsets must be int64")
+    nb = offsets.numel() - 1
+    cols = nb * WORDS_PER_BUNDLE
+    if return_bool:
+        out = torch.empty((plan_count, cols * 64), dtype=torch.bool, device=dev)
+    else:
+        out = torch.empty((plan_count, cols), dtype=torch.int64, device=dev)
+    if plan_count == 0 or nb <= 0:
+        return out
+    lib = nat.lib()
+    ws = nat.workspace(lib.rt_bloom_search_workspace(data_bytes), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_bloom_search(
+            nat.ptr(bloom_index), nat.ptr(offsets), nb, nat.ptr(plan_offsets), nat.ptr(data),
+            data_bytes, plan_count, max(1, min(int(max_stack), MAX_STACK)), k, hash_k,
+            None if return_bool else nat.ptr(out), nat.ptr(out) if return_bool else None,
+            nat.ptr(ws), ws.numel(), nat.stream(dev),
+        )
+    nat.check(st)
+    return out
+
+
+def _search_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max_stack_size, k,
+                     hash_k, return_bool_mask=False):
+    """Plans prepared once on the device: ``plans`` int64 ``[8 * plan_count + data words]``,
+    the offsets then the parser's data (``bloom_index_search_cuda.cu:103-137``)."""
+    if plans.dtype != torch.int64 or plans.dim() != 1 or plans.numel() < 8 * plan_count:
+        raise ValueError("plans must be int64 [8 * plan_count + data words]")
+    if max_stack_size > MAX_STACK:
+        raise ValueError(f"max_stack_size must be <= {MAX_STACK}")
+    plans = plans.contiguous()
+    data = plans[8 * plan_count :]
+    return _search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), plans, data,
+                   data.numel() * 8, int(plan_count), int(max_stack_size), int(k), int(hash_k),
+                   bool(return_bool_mask))
+
+
+def _search_batch(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data,
+                  bloom_query_plans_offsets, k, hash_k, return_bool_mask=True):
+    """Plans as the parser returns them (host tensors are copied to the index's device)."""
+    dev = bloom_index.device
+    data = bloom_query_plans_data.contiguous()
+    offs = bloom_query_plans_offsets.to(torch.int64).contiguous()
+    if offs.numel() % 8:
+        raise ValueError("bloom_query_plans_offsets must hold 8 offsets per plan")
+    max_stack = MAX_STACK
+    if data.device.type == "cpu" and offs.device.type == "cpu":
+        max_stack = _max_stack(data.numpy().view(np.uint8), offs.numpy())
+        if max_stack > MAX_STACK:
+            raise ValueError(f"plans need a stack of {max_stack} (> {MAX_STACK})")
+    nbytes = data.numel()
+    # 8-aligned device copy of the data
+    dev_data = torch.zeros((nbytes + 7) // 8, dtype=torch.int64, device=dev)
+    if nbytes:
+        dev_data.view(torch.uint8)[:nbytes].copy_(data.view(torch.uint8).to(dev))
+    return _search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), offs.to(dev),
+                   dev_data, nbytes, offs.numel() // 8, max_stack, int(k), int(hash_k),
+                   bool(return_bool_mask))
+
+
+_LIB.impl("bloom_index_search_batch_prepared", _search_prepared, "CUDA")
+_LIB.impl("bloom_index_search_batch", _search_batch, "CUDA")
+
+
+@torch.library.register_fake("st::bloom_index_search_batch_prepared")
+def _(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max_stack_size, k, hash_k,
+      return_bool_mask=False):
+    cols = (bloom_bundle_b_offsets.shape[0] - 1) * WORDS_PER_BUNDLE
+    if return_bool_mask:
+        return bloom_index.new_empty((plan_count, cols * 64), dtype=torch.bool)
+    return bloom_index.new_empty((plan_count, cols), dtype=torch.int64)
+
+
+# --- helpers for the filtered scans -----------------------------------------------------------
+
+
+def attrs_to_features(attrs: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """``[N, C, A]`` int64 attrs (``-1`` pads) → ``(feature_ids int32 [C], feature_offsets int64
+    [N * C + 1], feature_values int64)``: the clause index is the feature id
+    (``ops/official/adapter.py:45-62``)."""
+    if attrs.dim() != 3:
+        raise ValueError(f"attrs must be [N, C, A_max], got shape {tuple(attrs.shape)}")
+    n, c, _ = attrs.shape
+    attrs = attrs.long()
+    valid = attrs != -1
+    offsets = torch.zeros(n * c + 1, dtype=torch.int64, device=attrs.device)
+    offsets[1:] = valid.sum(-1).reshape(-1).cumsum(0)
+    values = attrs.reshape(-1)[valid.reshape(-1)]
+    return (torch.arange(c, dtype=torch.int32, device=attrs.device), offsets.contiguous(),
+            values.contiguous())
+
+
+def prepare_plans(expressions: list[str], hash_k: int, device: torch.device,
+                  max_sub_queries: int = 5) -> tuple[Tensor, int, int]:
+    """Parse once and upload: ``(blob int64 [8 * B + data words], plan_count, max_stack)``, the
+    layout ``bloom_index_search_batch_prepared`` reads (as ``adapter.prepare_plans``)."""
+    max_stack, data, offsets = bl.parse_batch(list(expressions), int(hash_k), max_sub_queries)
+    b = len(expressions)
+    blob = np.zeros(8 * b + (data.size + 7) // 8, np.int64)
+    blob[: 8 * b] = offsets
+    blob[8 * b :].view(np.uint8)[: data.size] = data
+    return torch.from_numpy(blob).to(device), b, max_stack
