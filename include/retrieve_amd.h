@@ -157,6 +157,29 @@ int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, int6
                     int64_t* out_mask, uint8_t* out_bool, void* workspace, size_t workspace_bytes,
                     rt_stream_t stream);
 
+/* ---- candidate lists ----------------------------------------------------------------
+ *
+ * Exact top-k over each query's own candidates: query row b against items
+ * positive_indices[b, 0 : min(counts[b], P)] (int64 ids into the [N, D] table; ids outside
+ * [0, N) are skipped), top-k by (score desc, item id asc) -> out_ids int64 [B, k] (-1 past the
+ * row's candidates and, for float scores, where the score is not finite), out_scores [B, k].
+ * kind 0 / 1 / 2: fp16 / bf16 / fp32 items [N, D] with float32 queries [B, D], fp32 dot,
+ *   float scores;
+ * kind 3: int8 items and queries [., D], int32 scores;
+ * kind 4: bit codes of D uint64 words, score 64 D - 2 popcount(q ^ item), float scores.
+ * Row bytes D * element size: a multiple of 16, at most 8192. 1 <= k <= 1024.
+ * Replaces: torch.ops.retrieve.fused_masked_knn_topk
+ *   (retrieve/src/retrieve/ops/triton/fused_masked_knn_topk.py:289-310; twin
+ *   ops/reference/fused_masked_knn_topk.py:9-29), oporp_1bit_match_topk_indirect
+ *   (ops/triton/oporp_1bit_match_topk.py:274-292; twin ops/reference/
+ *   oporp_1bit_match_topk.py:29-41), and SilverTorch's int8 re-rank of given ids
+ *   (retrieve/src/retrieve/modules/silvertorch.py:363-379). */
+size_t rt_cand_topk_workspace(int64_t B, int64_t P, int64_t k);
+int rt_cand_topk(const void* queries, int64_t B, const void* items, int64_t N, int64_t D, int kind,
+                 const int64_t* positive_indices, int64_t P, const int64_t* counts, int64_t k,
+                 int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
+                 rt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -103,3 +103,28 @@ def candidate_int8_topk(
         ids[r, : order.size] = c[order]
         sc[r, : order.size] = s[order]
     return ids, sc
+
+
+def candidate_topk(
+    scores_fn, candidate_ids: np.ndarray, counts: np.ndarray, k: int, *, pad_to_k: bool,
+    empty_score,
+) -> tuple[np.ndarray, np.ndarray]:
+    """Top-k over ``candidate_ids[b, :counts[b]]`` by (score desc, item id asc); ``scores_fn(b,
+    ids)`` scores one row's candidates. ``min(k, P)`` columns unless ``pad_to_k``; slots past a
+    row's candidates hold ``-1`` / ``empty_score``. The selection of ``masked_topk`` with
+    ``valid = counts_to_valid(counts, P)`` (``functional.py:52-85``;
+    ``ops/reference/fused_masked_knn_topk.py:9-29``, ``oporp_1bit_match_topk.py:29-41``), ties
+    by the lowest-id rule."""
+    b, p = candidate_ids.shape
+    kk = k if pad_to_k else min(k, p)
+    ids = np.full((b, kk), -1, np.int64)
+    sc = np.full((b, kk), empty_score)
+    for r in range(b):
+        c = candidate_ids[r, : max(0, min(int(counts[r]), p))]
+        if c.size == 0:
+            continue
+        s = np.asarray(scores_fn(r, c))
+        order = np.lexsort((c, -s))[: min(kk, c.size)]
+        ids[r, : order.size] = c[order]
+        sc[r, : order.size] = s[order]
+    return ids, sc

@@ -62,6 +62,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "rt_mask_compact_workspace": (_c_sz, [_c_i64, _c_i64]),
     "rt_mask_compact": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p]),
+    "rt_cand_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),
+    "rt_cand_topk": (
+        _c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p,
+         _c_sz, _c_p],
+    ),
     "rt_int8_scan_topk": (
         _c_int,
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],

@@ -439,3 +439,145 @@ def _(item_clause_attrs, clause_is_reverse, query_clause_attrs):
         query_clause_attrs.new_empty((b, n), dtype=torch.int64),
         query_clause_attrs.new_empty((b,), dtype=torch.int64),
     )
+
+
+# --- candidate lists: gather + score + top-k ----------------------------------------------------
+
+_CAND_KIND = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def _cand_check(positive_indices: Tensor, counts: Tensor, b: int) -> Tensor:
+    if positive_indices.dim() != 2 or positive_indices.shape[0] != b:
+        raise ValueError(f"positive_indices must be [B, P] with B={b}")
+    if counts.dim() != 1 or counts.shape[0] != b:
+        raise ValueError(f"counts must be [B] with B={b}")
+    if positive_indices.dtype != torch.int64:
+        raise TypeError("positive_indices must be int64")
+    _check_items(positive_indices=positive_indices)
+    return counts.to(torch.int64).contiguous()
+
+
+def _cand_topk(q: Tensor, items: Tensor, d: int, kind: int, positive_indices: Tensor,
+               counts: Tensor, k: int, score_dtype: torch.dtype) -> tuple[Tensor, Tensor]:
+    b, p = positive_indices.shape
+    dev = nat.require_device(q, items, positive_indices, counts)
+    ids = torch.empty((b, k), dtype=torch.int64, device=dev)
+    scores = torch.empty((b, k), dtype=score_dtype, device=dev)
+    if b == 0:
+        return ids, scores
+    lib = nat.lib()
+    ws = nat.workspace(lib.rt_cand_topk_workspace(b, p, k), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_cand_topk(
+            nat.ptr(q), b, nat.ptr(items), items.shape[0], d, kind, nat.ptr(positive_indices), p,
+            nat.ptr(counts), k, nat.ptr(ids), nat.ptr(scores), nat.ptr(ws), ws.numel(),
+            nat.stream(dev),
+        )
+    nat.check(st)
+    return ids, scores
+
+
+@torch.library.custom_op("retrieve::fused_masked_knn_topk", mutates_args=(), device_types="cuda")
+def fused_masked_knn_topk(
+    query: Tensor, item_embs: Tensor, positive_indices: Tensor, counts: Tensor, k: int
+) -> tuple[Tensor, Tensor]:
+    """Top-``k`` of the fp32 dot of ``query [B, D]`` with ``item_embs[positive_indices[b,
+    :counts[b]]]`` → ``(ids int64 [B, k], scores fp32 [B, k])``, ties to the lower item id, ``-1``
+    where no candidate is left or the score is not finite
+    (``ops/triton/fused_masked_knn_topk.py:289-310``). ``P < k`` raises ``ValueError``."""
+    if query.dim() != 2 or item_embs.dim() != 2:
+        raise ValueError("query must be [B, D] and item_embs [N, D]")
+    if query.dtype not in _CAND_KIND or item_embs.dtype not in _CAND_KIND:
+        raise TypeError("query and item_embs must be float16, bfloat16 or float32, "
+                        f"got {query.dtype} and {item_embs.dtype}")
+    if query.shape[1] != item_embs.shape[1]:
+        raise ValueError(f"D mismatch: query D={query.shape[1]} vs item D={item_embs.shape[1]}")
+    if positive_indices.dim() == 2 and positive_indices.shape[1] < k:
+        raise ValueError(
+            f"positive_indices has {positive_indices.shape[1]} columns, fewer than k={k}")
+    if not 1 <= k <= 1024:
+        raise ValueError(f"k must be in [1, 1024], got {k}")
+    _check_items(item_embs=item_embs)
+    counts = _cand_check(positive_indices, counts, query.shape[0])
+    q = query.to(torch.float32).contiguous()
+    return _cand_topk(q, item_embs, query.shape[1], _CAND_KIND[item_embs.dtype],
+                      positive_indices, counts, k, torch.float32)
+
+
+@fused_masked_knn_topk.register_fake
+def _(query, item_embs, positive_indices, counts, k):
+    b = query.shape[0]
+    return (query.new_empty((b, k), dtype=torch.int64),
+            query.new_empty((b, k), dtype=torch.float32))
+
+
+@torch.library.custom_op(
+    "retrieve::oporp_1bit_match_topk_indirect", mutates_args=(), device_types="cuda"
+)
+def oporp_1bit_match_topk_indirect(
+    query_bits: Tensor, item_bits: Tensor, k: int, positive_indices: Tensor, counts: Tensor
+) -> tuple[Tensor, Tensor]:
+    """Hamming top-``k`` over ``positive_indices[b, :counts[b]]`` only
+    (``ops/triton/oporp_1bit_match_topk.py:274-292``): score ``64 W - 2 popcount`` as fp32,
+    ``min(k, P)`` columns (no pad tail), ties to the lower item id."""
+    if query_bits.dim() != 2 or item_bits.dim() != 2:
+        raise ValueError("query_bits must be [B, W] and item_bits [N, W]")
+    if query_bits.dtype != torch.int64 or item_bits.dtype != torch.int64:
+        raise TypeError("query_bits and item_bits must be int64")
+    if query_bits.shape[1] != item_bits.shape[1]:
+        raise ValueError(f"W mismatch: query_bits W={query_bits.shape[1]} vs item_bits "
+                         f"W={item_bits.shape[1]}")
+    _check_items(item_bits=item_bits)
+    counts = _cand_check(positive_indices, counts, query_bits.shape[0])
+    kk = min(k, positive_indices.shape[1])
+    if k < 1 or kk > 1024:
+        raise ValueError(f"k must be >= 1 and min(k, P) <= 1024, got k={k}")
+    b = query_bits.shape[0]
+    if kk == 0:
+        return (query_bits.new_empty((b, 0), dtype=torch.int64),
+                query_bits.new_empty((b, 0), dtype=torch.float32))
+    return _cand_topk(query_bits.contiguous(), item_bits, query_bits.shape[1], 4,
+                      positive_indices, counts, kk, torch.float32)
+
+
+@oporp_1bit_match_topk_indirect.register_fake
+def _(query_bits, item_bits, k, positive_indices, counts):
+    kk = min(k, positive_indices.shape[1])
+    b = query_bits.shape[0]
+    return (query_bits.new_empty((b, kk), dtype=torch.int64),
+            query_bits.new_empty((b, kk), dtype=torch.float32))
+
+
+@torch.library.custom_op("retrieve::int8_candidates_topk", mutates_args=(), device_types="cuda")
+def int8_candidates_topk(
+    query_codes: Tensor, item_codes: Tensor, positive_indices: Tensor, counts: Tensor, k: int
+) -> tuple[Tensor, Tensor]:
+    """Exact int8 re-rank of given ids: int32 dots of ``query_codes [B, D]`` with
+    ``item_codes[positive_indices[b, :counts[b]]]``, top ``min(k, P)`` by (score desc, item id
+    asc) → ``(ids int64, scores int32)``, ``-1`` / ``INT32_MIN`` past a row's candidates (the
+    selection of ``modules/silvertorch.py:363-379``, before its fp32 scaling)."""
+    if query_codes.dim() != 2 or item_codes.dim() != 2:
+        raise ValueError("query_codes must be [B, D] and item_codes [N, D]")
+    if query_codes.dtype != torch.int8 or item_codes.dtype != torch.int8:
+        raise TypeError("query_codes and item_codes must be int8")
+    if query_codes.shape[1] != item_codes.shape[1]:
+        raise ValueError("D mismatch between query_codes and item_codes")
+    _check_items(item_codes=item_codes)
+    counts = _cand_check(positive_indices, counts, query_codes.shape[0])
+    kk = min(k, positive_indices.shape[1])
+    if k < 1 or kk > 1024:
+        raise ValueError(f"k must be >= 1 and min(k, P) <= 1024, got k={k}")
+    b = query_codes.shape[0]
+    if kk == 0:
+        return (query_codes.new_empty((b, 0), dtype=torch.int64),
+                query_codes.new_empty((b, 0), dtype=torch.int32))
+    return _cand_topk(query_codes.contiguous(), item_codes, query_codes.shape[1], 3,
+                      positive_indices, counts, kk, torch.int32)
+
+
+@int8_candidates_topk.register_fake
+def _(query_codes, item_codes, positive_indices, counts, k):
+    kk = min(k, positive_indices.shape[1])
+    b = query_codes.shape[0]
+    return (query_codes.new_empty((b, kk), dtype=torch.int64),
+            query_codes.new_empty((b, kk), dtype=torch.int32))

@@ -238,3 +238,27 @@ def test_bloom_no_false_negatives():
             m = of.term_mask(words, offs, 3000, f, v, 3, 7)
             exact = (attrs[:, f, 0] == v)
             assert (m | ~exact).all()  # every doc holding the token is found
+
+
+def test_candidate_topk_brute_force():
+    """``candidate_topk`` against a brute-force full sort over each row's first ``counts[b]``
+    candidates (tie-heavy scores, duplicates, short rows) and against ``candidate_int8_topk``."""
+    g = rng(91)
+    b, p, k = 6, 40, 7
+    cand = g.integers(0, 25, (b, p))
+    counts = np.array([40, 3, 0, 39, 7, 12])
+    table = g.integers(-2, 3, 25)  # few distinct scores: ties everywhere
+    ids, sc = osc.candidate_topk(lambda r, c: table[c], cand, counts, k, pad_to_k=True,
+                                 empty_score=np.iinfo(np.int64).min)
+    for r in range(b):
+        c = cand[r, : counts[r]]
+        pairs = sorted(((-int(table[i]), int(i)) for i in c))[:k]
+        want = [i for _, i in pairs] + [-1] * (k - len(pairs))
+        assert ids[r].tolist() == want
+    codes = g.integers(-128, 128, (25, 64), dtype=np.int8)
+    q = g.integers(-128, 128, (b, 64), dtype=np.int8)
+    full = np.full(b, p)
+    ids2, sc2 = osc.candidate_topk(lambda r, c: osc.int8_scores(q[r:r + 1], codes[c])[0], cand,
+                                   full, 9, pad_to_k=False, empty_score=np.iinfo(np.int32).min)
+    want_ids, want_sc = osc.candidate_int8_topk(q, codes, cand, 9)
+    assert np.array_equal(ids2, want_ids) and np.array_equal(sc2.astype(np.int32), want_sc)
