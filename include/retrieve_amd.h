@@ -180,6 +180,57 @@ int rt_cand_topk(const void* queries, int64_t B, const void* items, int64_t N, i
                  int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
                  rt_stream_t stream);
 
+/* [1, N] float scores of one fp16 query [D] against the fp16 [D, N] item table (row k of the
+ * table is dimension k of every item), accumulated as acc = fma(q[k], e[k, n], acc) for
+ * k = 0 .. D-1 in fp32.
+ * Replaces: torch.ops.retrieve.gemv_scores (retrieve/src/retrieve/ops/triton/gemv_scores.py:
+ *   19-43), the B = 1 scorer of PostfilterKNN (retrieve/src/retrieve/modules/knn.py:62-66). */
+int rt_gemv_scores(const uint16_t* query, const uint16_t* item_embs_t, int64_t D, int64_t N,
+                   float* out, rt_stream_t stream);
+
+/* ---- SilverTorch search ------------------------------------------------------------------- */
+
+/* Per-row int8 quantization: abs_max = max(max |x|, 1e-8), scales[r] = abs_max * fp32(1/127),
+ * codes = clamp(rint(fp32(fp64(x) / fp64(abs_max)) * 127), -128, 127) (x float32 [rows, dim]).
+ * Replaces: probe_prep's quantization (silvertorch/.../fork_search_cuda.cu:653-700; the
+ *   GPU form of retrieve/src/retrieve/indexing/quantize.py:9-18). */
+int rt_quantize_int8_rows(const float* x, int64_t rows, int64_t dim, int8_t* codes, float* scales,
+                          rt_stream_t stream);
+
+/* The exact clause filter over st::search's clause-major int32 slot layout (slots [R, N]; clause
+ * c in rows clause_slots[c] .. clause_slots[c+1], -1 pads; query_values [B, C] int32, -1 =
+ * inactive) -> packed bits [B, ceil(N/64)] as rt_clause_filter's mode 0, AND-ed with and_mask.
+ * Replaces: the exact payload filter of st::search (silvertorch/.../fork_filters.cuh:15-56,
+ *   fork_search_cuda.cu:957-1179). */
+int rt_clause_slots_filter(const int32_t* slots, int64_t R, int64_t N, const int64_t* clause_slots,
+                           int64_t C, const int8_t* clause_is_reverse, const int32_t* query_values,
+                           int64_t B, const uint64_t* and_mask, int64_t and_mask_words,
+                           uint64_t* out, rt_stream_t stream);
+
+/* Top-k of SilverTorch's search over each row's probed clusters: row b's slots are the items of
+ * clusters probe_ids[b, 0..n_probe) (sorted positions cluster_offsets[c] .. + cluster_sizes[c])
+ * end to end, at most `width` of them; keys are the int32 dot of the int8 codes (divisor -1) or
+ * fp16(float(dot) / divisor); top-k by (key desc, slot asc); items whose position's mask bit is
+ * clear are skipped. Epilogue: out_ids = sort_perm[position], out_scores = (fp32(dot) * q_scale)
+ * * global_scale[0] (fp16 path: score16 * ((q_scale * divisor) * global_scale[0])), -1 / -inf
+ * pads. D (code bytes) a multiple of 16; n_probe <= 1024; 1 <= k <= 1024.
+ * Replaces: st::search (silvertorch/.../fork_search_cuda.cu:1256-1524; schema
+ *   fork_search.cpp:13-39) after its filter stage. */
+size_t rt_ivf_search_workspace(int64_t B, int64_t width, int64_t k);
+int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64_t B, const int8_t* item_codes,
+                  int64_t N, int64_t D, const int64_t* probe_ids, int64_t n_probe,
+                  const int64_t* cluster_offsets, const int64_t* cluster_sizes, int64_t n_lists,
+                  int64_t width, const uint64_t* mask, int64_t mask_words, int64_t divisor,
+                  const int64_t* sort_perm, int64_t n_perm, const float* global_scale, int64_t k,
+                  int64_t* out_ids, float* out_scores, void* workspace, size_t workspace_bytes,
+                  rt_stream_t stream);
+
+/* The search epilogue alone, for a one-list search run as a full scan: ids [B, k] hold item
+ * positions (-1 empty) and become sort_perm[position]; raw_dots [B, k] int32 -> out_scores. */
+int rt_search_epilogue(int64_t* ids, const int32_t* raw_dots, float* out_scores, int64_t B,
+                       int64_t k, const int64_t* sort_perm, int64_t n_perm, const float* q_scales,
+                       const float* global_scale, rt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

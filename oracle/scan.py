@@ -128,3 +128,15 @@ def candidate_topk(
         ids[r, : order.size] = c[order]
         sc[r, : order.size] = s[order]
     return ids, sc
+
+
+def gemv_scores(q16: np.ndarray, e_t16: np.ndarray) -> np.ndarray:
+    """``[D]`` fp16 query against the ``[D, N]`` fp16 table → ``[N]`` float32, acc =
+    fma(q[k], e[k, :], acc) for k = 0 .. D-1 (``ops/triton/gemv_scores.py:19-28``). The product of
+    two fp16 values is exact in float32, so each fma is one float32 add of the exact product."""
+    q = np.asarray(q16, np.float16).astype(np.float32)
+    e = np.asarray(e_t16, np.float16)
+    acc = np.zeros(e.shape[1], np.float32)
+    for k in range(e.shape[0]):
+        acc = acc + q[k] * e[k].astype(np.float32)
+    return acc

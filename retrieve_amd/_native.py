@@ -68,6 +68,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p,
          _c_sz, _c_p],
     ),
+    "rt_gemv_scores": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "rt_quantize_int8_rows": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "rt_clause_slots_filter": (
+        _c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
+    ),
+    "rt_ivf_search_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),
+    "rt_ivf_search": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_p,
+         _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],
+    ),
+    "rt_search_epilogue": (
+        _c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p],
+    ),
     "rt_int8_scan_topk": (
         _c_int,
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],

@@ -138,6 +138,74 @@ static void launch_clause(const ClauseArgs& a, dim3 grid, hipStream_t stream) {
   }
 }
 
+// ---- the clause-major int32 slot layout of st::search -------------------------------------
+//
+// fork_clause_attrs (retrieve/src/retrieve/ops/official/adapter.py:68-89): slots [R, N] int32,
+// clause c in rows clause_slots[c] .. clause_slots[c+1], each doc's values sorted descending
+// with -1 pads last; queries [B, C] int32, -1 = inactive clause (INT32_MIN, for values no doc can
+// hold, matches nothing). The exact_pass of fork_filters.cuh:15-41. Lane <-> doc: the doc's R
+// values are read coalesced (row r of the table) into registers once.
+constexpr int kRegSlots = 16;
+
+struct SlotClauseArgs {
+  const int32_t* slots;  // [R, N]
+  int64_t N;
+  int R;
+  const int64_t* clause_slots;  // [C + 1]
+  int C;
+  const int8_t* reverse;  // [C]
+  const int32_t* q;       // [B, C]
+  int64_t B;
+  int64_t rows_per_wg;
+  const uint64_t* and_mask;
+  int64_t and_words;
+  uint64_t* out;  // [B, W]
+  int64_t W;
+};
+
+template <bool REG>
+__global__ void __launch_bounds__(kClauseThreads) slot_clause_kernel(SlotClauseArgs a) {
+  const int64_t d = static_cast<int64_t>(blockIdx.x) * kClauseThreads + threadIdx.x;
+  const bool valid = d < a.N;
+  const int lane = lane_id();
+  int32_t v[kRegSlots];
+  if constexpr (REG) {
+#pragma unroll
+    for (int r = 0; r < kRegSlots; ++r) v[r] = (r < a.R && valid) ? a.slots[r * a.N + d] : -1;
+  }
+  uint32_t rev_mask = 0;
+  for (int c = 0; c < a.C; ++c) rev_mask |= a.reverse[c] != 0 ? 1u << c : 0u;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * a.rows_per_wg;
+  const int64_t b1 = b0 + a.rows_per_wg < a.B ? b0 + a.rows_per_wg : a.B;
+  for (int64_t b = b0; b < b1; ++b) {
+    const int32_t* qb = a.q + b * a.C;
+    uint32_t active = 0;
+    uint32_t match = 0;
+    for (int c = 0; c < a.C; ++c) {
+      const int32_t val = qb[c];
+      if (val == -1) continue;
+      active |= 1u << c;
+      const int r0 = static_cast<int>(a.clause_slots[c]);
+      const int r1 = static_cast<int>(a.clause_slots[c + 1]);
+      bool eq = false;
+      if constexpr (REG) {
+#pragma unroll
+        for (int r = 0; r < kRegSlots; ++r) eq |= r >= r0 && r < r1 && v[r] == val;
+      } else {
+        for (int r = r0; r < r1 && valid; ++r) eq |= a.slots[r * a.N + d] == val;
+      }
+      match |= eq ? 1u << c : 0u;
+    }
+    const bool pass = valid && ((match ^ rev_mask) & active) == active;
+    uint64_t word = __builtin_bitreverse64(__ballot(pass));
+    const int64_t w = (d - lane) >> 6;
+    if (lane == 0 && w < a.W) {
+      if (a.and_mask != nullptr) word &= a.and_mask[b * a.and_words + w];
+      a.out[b * a.W + w] = word;
+    }
+  }
+}
+
 // ---- packed mask -> ascending ids ------------------------------------------------------
 
 // Word w of a row with the bits of items >= N cleared (a caller's mask may set them).
@@ -323,6 +391,47 @@ extern "C" int rt_mask_compact(const uint64_t* mask, int64_t B, int64_t N, int64
                                                                   counts);
   RT_CHECK_HIP(hipGetLastError());
   mask_scatter_kernel<<<grid, 256, 0, stream>>>(mask, W, T, N, chunk_offsets, out_indices);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+extern "C" int rt_clause_slots_filter(const int32_t* slots, int64_t R, int64_t N,
+                                      const int64_t* clause_slots, int64_t C,
+                                      const int8_t* clause_is_reverse, const int32_t* query_values,
+                                      int64_t B, const uint64_t* and_mask, int64_t and_mask_words,
+                                      uint64_t* out, hipStream_t stream) {
+  RT_CHECK_ARG(N >= 0 && B >= 0 && R >= 0, "N, B and R must be >= 0");
+  RT_CHECK_ARG(C >= 0 && C <= kMaxClauses, "C must be in [0, %d]", kMaxClauses);
+  RT_CHECK_ARG(R <= (int64_t{1} << 20), "too many slot rows");
+  RT_CHECK_ARG(and_mask == nullptr || and_mask_words >= cdiv(N, 64),
+               "and_mask rows must have >= ceil(N/64) words");
+  if (B == 0 || N == 0) return kOk;
+  SlotClauseArgs a{};
+  a.slots = slots;
+  a.N = N;
+  a.R = static_cast<int>(R);
+  a.clause_slots = clause_slots;
+  a.C = static_cast<int>(C);
+  a.reverse = clause_is_reverse;
+  a.q = query_values;
+  a.B = B;
+  a.and_mask = and_mask;
+  a.and_words = and_mask_words;
+  a.out = out;
+  a.W = cdiv(N, 64);
+  const int64_t gx = cdiv(N, kClauseThreads);
+  RT_CHECK_ARG(gx < (int64_t{1} << 31), "N too large");
+  int64_t gy = cdiv(4096, gx);
+  gy = gy < 1 ? 1 : (gy > B ? B : gy);
+  gy = gy > 65535 ? 65535 : gy;
+  a.rows_per_wg = cdiv(B, gy);
+  gy = cdiv(B, a.rows_per_wg);
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  if (R <= kRegSlots) {
+    slot_clause_kernel<true><<<grid, kClauseThreads, 0, stream>>>(a);
+  } else {
+    slot_clause_kernel<false><<<grid, kClauseThreads, 0, stream>>>(a);
+  }
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }

@@ -1,0 +1,443 @@
+// SilverTorch's search after phase 1 (silvertorch/.../ops/csrc/fork_search_cuda.cu:1256-1524):
+// query quantization, the int8 scorer over each query's probed clusters, the selection by
+// (key desc, slot asc) and the epilogue id = sort_perm[position], score = dequantized dot.
+//
+// Slots: query row b's probed clusters c_j = probe_ids[b, j] (items at sorted positions
+// cluster_offsets[c_j] .. + cluster_sizes[c_j]) laid end to end in probe order; slot s of the
+// row is the s-th of those items, and ties go to the lower slot. The row holds at most `width`
+// slots (max_tensor_size_per_row rounded up to 32, as the reference's score buffer).
+//
+// Keys: the int32 dot (divisor -1), or the fp16 score fp16(float(dot) / divisor) of the serving
+// path (index_mm_helpers.cuh:48-65), ordered as fp16 values (ties merge distinct dots).
+//
+// The range scan is the candidate kernel's layout: a group of L lanes loads one item row with
+// 16-byte loads and reduces its v_dot4 partial sums by xor-shuffles; every wave keeps a
+// candidate list under a rising threshold; the shared merge picks the k best composites.
+#include "scan_common.h"
+#include "wave_lists.h"
+
+namespace rt {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kQuantThreads = 256;
+constexpr int kIvfThreads = 256;
+constexpr int kIvfWaves = kIvfThreads / kWave;
+constexpr int kIvfMaxProbe = 1024;
+constexpr int kIvfMaxWgsPerRow = 64;
+
+// ---- query quantization (A1 / A2) ------------------------------------------------------------
+
+// Per row: abs_max = max(max |x|, 1e-8); scale = abs_max * fp32(1/127); code =
+// clamp(rint(fp32(fp64(x) / fp64(abs_max)) * 127), -128, 127) (fork_search_cuda.cu:680-699;
+// retrieve/src/retrieve/indexing/quantize.py:9-18). One workgroup per row.
+__global__ void __launch_bounds__(kQuantThreads) quantize_rows_kernel(const float* x,
+                                                                      int64_t dim, int8_t* codes,
+                                                                      float* scales) {
+  __shared__ float red[kQuantThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * dim;
+  float m = 0.f;
+  for (int64_t d = threadIdx.x; d < dim; d += kQuantThreads) m = fmaxf(m, fabsf(xr[d]));
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (lane_id() == 0) red[threadIdx.x / kWave] = m;
+  __syncthreads();
+  m = red[0];
+  for (int w = 1; w < kQuantThreads / kWave; ++w) m = fmaxf(m, red[w]);
+  m = fmaxf(m, 1e-8f);
+  if (threadIdx.x == 0) scales[row] = m * (1.0f / 127.0f);
+  const double a = static_cast<double>(m);
+  int8_t* out = codes + row * dim;
+  for (int64_t d = threadIdx.x; d < dim; d += kQuantThreads) {
+    float v = static_cast<float>(static_cast<double>(xr[d]) / a) * 127.0f;
+    v = fminf(fmaxf(rintf(v), -128.0f), 127.0f);
+    out[d] = static_cast<int8_t>(v);
+  }
+}
+
+// ---- range scan ------------------------------------------------------------------------------
+
+struct IvfArgs {
+  const int8_t* q;  // [B, RB] codes
+  int64_t B;
+  const int8_t* items;  // [N, RB]
+  int64_t N;
+  int RB;
+  const int64_t* probe_ids;  // [B, n_probe]
+  int64_t n_probe;
+  const int64_t* cluster_offsets;  // [n_lists]
+  const int64_t* cluster_sizes;    // [n_lists]
+  int64_t n_lists;
+  int64_t width;
+  const uint64_t* mask;  // [B, mask_words], item position d at bit 63 - d % 64, or null
+  int64_t mask_words;
+  int divisor;  // -1: int32 keys
+  int k;
+  int capw;
+  uint64_t* lists;
+  int* list_counts;
+};
+
+// The row's probed ranges: start[j], and prefix[j] = slots before range j (prefix[n] = total,
+// clamped at width). Ranges of invalid clusters, or reaching outside the table, are empty.
+__device__ inline int64_t load_ranges(const IvfArgs& a, int64_t b, int64_t* start,
+                                      int64_t* prefix) {
+  const int tid = threadIdx.x;
+  for (int64_t j = tid; j < a.n_probe; j += blockDim.x) {
+    const int64_t c = a.probe_ids[b * a.n_probe + j];
+    int64_t s = 0;
+    int64_t len = 0;
+    if (c >= 0 && c < a.n_lists) {
+      s = a.cluster_offsets[c];
+      len = a.cluster_sizes[c];
+      if (s < 0 || len < 0 || s > a.N || len > a.N - s) len = 0;
+    }
+    start[j] = s;
+    prefix[j + 1] = len;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    prefix[0] = 0;
+    for (int64_t j = 0; j < a.n_probe; ++j) {
+      const int64_t t = prefix[j] + prefix[j + 1];
+      prefix[j + 1] = t < a.width ? t : a.width;
+    }
+  }
+  __syncthreads();
+  return prefix[a.n_probe];
+}
+
+// the range holding slot s: the last j with prefix[j] <= s
+__device__ inline int64_t range_of(const int64_t* prefix, int64_t n, int64_t s) {
+  int64_t lo = 0;
+  int64_t hi = n - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (prefix[mid] <= s) {
+      lo = mid;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  return lo;
+}
+
+__device__ inline uint32_t search_key(int32_t dot, int divisor) {
+  if (divisor == -1) return key_of_i32(dot);
+  const _Float16 h = static_cast<_Float16>(static_cast<float>(dot) / static_cast<float>(divisor));
+  return key_of_f32(static_cast<float>(h));
+}
+
+template <int L, int NC>
+__global__ void __launch_bounds__(kIvfThreads) ivf_scan_kernel(IvfArgs a) {
+  constexpr int R = kWave / L;
+  extern __shared__ uint64_t smem[];
+  int64_t* start = reinterpret_cast<int64_t*>(smem);
+  int64_t* prefix = start + a.n_probe;
+  uint64_t* scratch = reinterpret_cast<uint64_t*>(prefix + a.n_probe + 1);
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid >> 6;
+  const int grp = lane / L;
+  const int gl = lane % L;
+  int* cnt_lds = reinterpret_cast<int*>(scratch + kIvfWaves * a.capw);
+  const int64_t b = blockIdx.y;
+  const int64_t gx = gridDim.x;
+  const int64_t S = gx * kIvfWaves;
+  const int64_t slot_list = static_cast<int64_t>(blockIdx.x) * kIvfWaves + wave;
+  uint64_t* list = a.lists + (b * S + slot_list) * a.capw;
+  scratch += wave * a.capw;
+
+  const int64_t total = load_ranges(a, b, start, prefix);
+  const int nchunks = a.RB / 16;
+  v4i qv[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = gl + j * L;
+    qv[j] = c < nchunks ? *reinterpret_cast<const v4i*>(a.q + b * a.RB + c * 16)
+                        : v4i{0, 0, 0, 0};
+  }
+  const uint64_t* mrow = a.mask != nullptr ? a.mask + b * a.mask_words : nullptr;
+
+  uint64_t tau = 0;
+  int cnt = 0;
+  const int64_t step = gx * kIvfWaves * R;
+  for (int64_t base = slot_list * R; base < total; base += step) {
+    const int64_t s = base + grp;
+    bool ok = s < total;
+    int64_t pos = 0;
+    if (ok) {
+      const int64_t j = range_of(prefix, a.n_probe, s);
+      pos = start[j] + (s - prefix[j]);
+      if (mrow != nullptr) ok = (mrow[pos >> 6] >> (63 - (pos & 63))) & 1ull;
+    }
+    int32_t dot = 0;
+    if (ok) {
+      const int8_t* row = a.items + pos * a.RB;
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int c = gl + j * L;
+        if (c < nchunks) {
+          const v4i x = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(row + c * 16));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dot = __builtin_amdgcn_sdot4(x[e], qv[j][e], dot, false);
+        }
+      }
+    }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off);
+    const uint64_t c = composite(search_key(dot, a.divisor), static_cast<uint32_t>(s));
+    const bool keep = ok && gl == 0 && c >= tau;
+    const uint64_t bal = __ballot(keep);
+    if (bal != 0ull) {
+      const int before = __popcll(bal & ((1ull << lane) - 1ull));
+      if (keep) list[cnt + before] = c;
+      cnt += __popcll(bal);
+      if (cnt > a.capw - R) {
+        if (lane == 0) cnt_lds[wave] = cnt;
+        const uint64_t nt = wave_compact(list, &cnt_lds[wave], scratch, a.capw, a.k);
+        cnt = cnt_lds[wave];
+        tau = nt > tau ? nt : tau;
+      }
+    }
+  }
+  if (lane == 0) a.list_counts[b * S + slot_list] = cnt;
+}
+
+// ---- epilogue -------------------------------------------------------------------------------
+
+struct EpiArgs {
+  int64_t* ids;     // in: slots (ranges) or positions, -1 empty; out: sort_perm ids
+  const void* raw;  // [B, k] int32 dots, or float fp16 scores
+  float* scores;    // out [B, k]
+  int64_t B;
+  int64_t k;
+  bool ranges;  // ids are slots of the probed ranges (else item positions)
+  IvfArgs a;    // the ranges (when `ranges`)
+  const int64_t* sort_perm;
+  int64_t n_perm;
+  const float* q_scales;
+  const float* global_scale;
+  int divisor;
+};
+
+// One workgroup per row. Scores (fork_search_cuda.cu:585-591): int32 path
+// (fp32(dot) * q_scale) * global_scale; fp16 path score16 * ((q_scale * divisor) *
+// global_scale), each product rounded to nearest.
+__global__ void __launch_bounds__(kIvfThreads) search_epilogue_kernel(EpiArgs e) {
+  extern __shared__ uint64_t smem[];
+  const int64_t b = blockIdx.x;
+  int64_t* start = reinterpret_cast<int64_t*>(smem);
+  int64_t* prefix = start + (e.ranges ? e.a.n_probe : 0);
+  if (e.ranges) load_ranges(e.a, b, start, prefix);
+  const float qs = e.q_scales[b];
+  const float gs = e.global_scale[0];
+  for (int64_t i = threadIdx.x; i < e.k; i += blockDim.x) {
+    const int64_t x = e.ids[b * e.k + i];
+    int64_t id = -1;
+    float score = -INFINITY;
+    if (x >= 0) {
+      int64_t pos = x;
+      if (e.ranges) {
+        const int64_t j = range_of(prefix, e.a.n_probe, x);
+        pos = start[j] + (x - prefix[j]);
+      }
+      if (pos >= 0 && pos < e.n_perm) {
+        id = e.sort_perm[pos];
+        if (e.divisor == -1) {
+          const float dot = static_cast<float>(static_cast<const int32_t*>(e.raw)[b * e.k + i]);
+          score = __fmul_rn(__fmul_rn(dot, qs), gs);
+        } else {
+          const float s16 = static_cast<const float*>(e.raw)[b * e.k + i];
+          score = __fmul_rn(s16, __fmul_rn(__fmul_rn(qs, static_cast<float>(e.divisor)), gs));
+        }
+      }
+    }
+    e.ids[b * e.k + i] = id;
+    e.scores[b * e.k + i] = score;
+  }
+}
+
+template <int L, int NC>
+static void launch_ivf(const IvfArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
+  if (lds > 64 * 1024) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&ivf_scan_kernel<L, NC>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  }
+  ivf_scan_kernel<L, NC><<<grid, kIvfThreads, lds, stream>>>(a);
+}
+
+static int ivf_capw(int64_t k) { return static_cast<int>(next_pow2(k + kWave)); }
+
+static int64_t ivf_gx(int64_t B, int64_t width) {
+  int64_t gx = cdiv(2048, B > 0 ? B : 1);
+  const int64_t by_rows = cdiv(width, 1024);
+  gx = gx < by_rows ? gx : by_rows;
+  gx = gx < 1 ? 1 : gx;
+  return gx < kIvfMaxWgsPerRow ? gx : kIvfMaxWgsPerRow;
+}
+
+}  // namespace rt
+
+using namespace rt;
+
+extern "C" int rt_quantize_int8_rows(const float* x, int64_t rows, int64_t dim, int8_t* codes,
+                                     float* scales, hipStream_t stream) {
+  RT_CHECK_ARG(rows >= 0 && dim >= 1, "rows must be >= 0 and dim >= 1");
+  RT_CHECK_ARG(rows <= (int64_t{1} << 31) - 1, "too many rows");
+  if (rows == 0) return kOk;
+  quantize_rows_kernel<<<static_cast<unsigned>(rows), kQuantThreads, 0, stream>>>(x, dim, codes,
+                                                                                 scales);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+extern "C" size_t rt_ivf_search_workspace(int64_t B, int64_t width, int64_t k) {
+  if (B <= 0 || k <= 0) return 256;
+  const int64_t S = ivf_gx(B, width) * kIvfWaves;
+  return align_up(static_cast<size_t>(B * S) * ivf_capw(k) * sizeof(uint64_t), 256) +
+         align_up(static_cast<size_t>(B * S) * sizeof(int), 256) +
+         align_up(static_cast<size_t>(B * k) * sizeof(float), 256);
+}
+
+// Top-k over each row's probed ranges of int8 codes (slots, ties to the lower slot), then the
+// epilogue: out_ids = sort_perm[position] (-1 pads), out_scores dequantized (-inf pads).
+extern "C" int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64_t B,
+                             const int8_t* item_codes, int64_t N, int64_t D,
+                             const int64_t* probe_ids, int64_t n_probe,
+                             const int64_t* cluster_offsets, const int64_t* cluster_sizes,
+                             int64_t n_lists, int64_t width, const uint64_t* mask,
+                             int64_t mask_words, int64_t divisor, const int64_t* sort_perm,
+                             int64_t n_perm, const float* global_scale, int64_t k,
+                             int64_t* out_ids, float* out_scores, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream) {
+  RT_CHECK_ARG(B >= 0 && N >= 0 && n_probe >= 0 && n_lists >= 0 && width >= 0,
+               "sizes must be >= 0");
+  RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
+               static_cast<long long>(kMaxK), static_cast<long long>(k));
+  RT_CHECK_ARG(D % 16 == 0 && D >= 16 && D <= 8192, "D must be a multiple of 16 in [16, 8192]");
+  RT_CHECK_ARG(n_probe <= kIvfMaxProbe, "n_probe must be <= %d", kIvfMaxProbe);
+  RT_CHECK_ARG(divisor == -1 || divisor >= 1, "divisor_for_int8 must be -1 or >= 1");
+  RT_CHECK_ARG(width < 0xffffffffll, "width must be < 2**32 - 1");
+  RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must cover every item");
+  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(item_codes) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(q_codes) % 16 == 0,
+               "codes must be 16-byte aligned");
+  RT_CHECK_ARG(B <= 65535, "B must be <= 65535");
+  if (B == 0) return kOk;
+  const size_t need = rt_ivf_search_workspace(B, width, k);
+  if (workspace_bytes < need) {
+    set_error("workspace too small: %zu < %zu", workspace_bytes, need);
+    return kWorkspaceTooSmall;
+  }
+  const int64_t gx = ivf_gx(B, width);
+  const int64_t S = gx * kIvfWaves;
+  const int capw = ivf_capw(k);
+  IvfArgs a{};
+  a.q = q_codes;
+  a.B = B;
+  a.items = item_codes;
+  a.N = N;
+  a.RB = static_cast<int>(D);
+  a.probe_ids = probe_ids;
+  a.n_probe = n_probe;
+  a.cluster_offsets = cluster_offsets;
+  a.cluster_sizes = cluster_sizes;
+  a.n_lists = n_lists;
+  a.width = width;
+  a.mask = mask;
+  a.mask_words = mask_words;
+  a.divisor = static_cast<int>(divisor);
+  a.k = static_cast<int>(k);
+  a.capw = capw;
+  char* ws = static_cast<char*>(workspace);
+  a.lists = reinterpret_cast<uint64_t*>(ws);
+  ws += align_up(static_cast<size_t>(B * S) * capw * sizeof(uint64_t), 256);
+  a.list_counts = reinterpret_cast<int*>(ws);
+  ws += align_up(static_cast<size_t>(B * S) * sizeof(int), 256);
+  void* raw = ws;
+  const int score_kind = divisor == -1 ? kScoreI32 : kScoreF32;
+  if (n_probe > 0) {
+    const size_t lds = static_cast<size_t>(2 * n_probe + 1) * sizeof(int64_t) +
+                       static_cast<size_t>(kIvfWaves) * capw * sizeof(uint64_t) +
+                       kIvfWaves * sizeof(int);
+    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(B));
+    if (D <= 1024) {
+      switch (D) {
+        case 16: launch_ivf<1, 1>(a, grid, lds, stream); break;
+        case 32: launch_ivf<2, 1>(a, grid, lds, stream); break;
+        case 64: launch_ivf<4, 1>(a, grid, lds, stream); break;
+        case 128: launch_ivf<8, 1>(a, grid, lds, stream); break;
+        case 256: launch_ivf<16, 1>(a, grid, lds, stream); break;
+        case 512: launch_ivf<32, 1>(a, grid, lds, stream); break;
+        default: launch_ivf<64, 1>(a, grid, lds, stream); break;
+      }
+    } else if (D <= 2048) {
+      launch_ivf<64, 2>(a, grid, lds, stream);
+    } else if (D <= 4096) {
+      launch_ivf<64, 4>(a, grid, lds, stream);
+    } else {
+      launch_ivf<64, 8>(a, grid, lds, stream);
+    }
+    RT_CHECK_HIP(hipGetLastError());
+    MergeArgs m{};
+    m.lists = a.lists;
+    m.counts = a.list_counts;
+    m.capw = capw;
+    m.qpw = 1;
+    m.S = S;
+    m.B = B;
+    m.k = static_cast<int>(k);
+    m.out_ids = out_ids;
+    m.out_scores = raw;
+    m.score_kind = score_kind;
+    const int st = launch_merge(m, stream);
+    if (st != kOk) return st;
+  } else {
+    const int st = launch_pad(out_ids, raw, B, k, score_kind, stream);
+    if (st != kOk) return st;
+  }
+  EpiArgs e{};
+  e.ids = out_ids;
+  e.raw = raw;
+  e.scores = out_scores;
+  e.B = B;
+  e.k = k;
+  e.ranges = true;
+  e.a = a;
+  e.sort_perm = sort_perm;
+  e.n_perm = n_perm;
+  e.q_scales = q_scales;
+  e.global_scale = global_scale;
+  e.divisor = static_cast<int>(divisor);
+  const size_t lds = static_cast<size_t>(2 * n_probe + 1) * sizeof(int64_t);
+  search_epilogue_kernel<<<static_cast<unsigned>(B), kIvfThreads, lds, stream>>>(e);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+// The epilogue alone, for a full scan's results: in_ids are item positions (-1 empty), raw the
+// int32 dots [B, k].
+extern "C" int rt_search_epilogue(int64_t* ids, const int32_t* raw_dots, float* out_scores,
+                                  int64_t B, int64_t k, const int64_t* sort_perm, int64_t n_perm,
+                                  const float* q_scales, const float* global_scale,
+                                  hipStream_t stream) {
+  RT_CHECK_ARG(B >= 0 && k >= 1, "B must be >= 0 and k >= 1");
+  if (B == 0) return kOk;
+  EpiArgs e{};
+  e.ids = ids;
+  e.raw = raw_dots;
+  e.scores = out_scores;
+  e.B = B;
+  e.k = k;
+  e.ranges = false;
+  e.sort_perm = sort_perm;
+  e.n_perm = n_perm;
+  e.q_scales = q_scales;
+  e.global_scale = global_scale;
+  e.divisor = -1;
+  search_epilogue_kernel<<<static_cast<unsigned>(B), kIvfThreads, 0, stream>>>(e);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}

@@ -581,3 +581,31 @@ def _(query_codes, item_codes, positive_indices, counts, k):
     b = query_codes.shape[0]
     return (query_codes.new_empty((b, kk), dtype=torch.int64),
             query_codes.new_empty((b, kk), dtype=torch.int32))
+
+
+# --- B = 1 dense scores in cuBLAS gemv2N order ---------------------------------------------------
+
+
+@torch.library.custom_op("retrieve::gemv_scores", mutates_args=(), device_types="cuda")
+def gemv_scores(query: Tensor, item_embs_t: Tensor) -> Tensor:
+    """``query [1, D]`` fp16 against ``item_embs_t [D, N]`` fp16 (contiguous) → ``[1, N]`` fp32,
+    one fp32 FMA per k in order (``ops/triton/gemv_scores.py:31-43``)."""
+    if query.dim() != 2 or query.shape[0] != 1 or query.dtype != torch.float16 or \
+            item_embs_t.dtype != torch.float16 or item_embs_t.dim() != 2 or \
+            item_embs_t.shape[0] != query.shape[1]:
+        raise ValueError("gemv_scores takes one fp16 query row and an fp16 [D, N] table")
+    _check_items(item_embs_t=item_embs_t)
+    d, n = item_embs_t.shape
+    q = query.contiguous()
+    dev = nat.require_device(q, item_embs_t)
+    out = torch.empty((1, n), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        st = nat.lib().rt_gemv_scores(nat.ptr(q), nat.ptr(item_embs_t), d, n, nat.ptr(out),
+                                      nat.stream(dev))
+    nat.check(st)
+    return out
+
+
+@gemv_scores.register_fake
+def _(query, item_embs_t):
+    return query.new_empty((1, item_embs_t.shape[1]), dtype=torch.float32)

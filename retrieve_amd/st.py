@@ -168,7 +168,7 @@ def _max_stack(data: np.ndarray, offsets: np.ndarray) -> int:
     return deepest
 
 
-def _search(bloom_index: Tensor, offsets: Tensor, plan_offsets: Tensor, data: Tensor,
+def _bloom_search(bloom_index: Tensor, offsets: Tensor, plan_offsets: Tensor, data: Tensor,
             data_bytes: int, plan_count: int, max_stack: int, k: int, hash_k: int,
             return_bool: bool) -> Tensor:
     dev = nat.require_device(bloom_index, offsets, plan_offsets, data)
@@ -205,7 +205,7 @@ def _search_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max
         raise ValueError(f"max_stack_size must be <= {MAX_STACK}")
     plans = plans.contiguous()
     data = plans[8 * plan_count :]
-    return _search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), plans, data,
+    return _bloom_search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), plans, data,
                    data.numel() * 8, int(plan_count), int(max_stack_size), int(k), int(hash_k),
                    bool(return_bool_mask))
 
@@ -228,7 +228,7 @@ def _search_batch(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data,
     dev_data = torch.zeros((nbytes + 7) // 8, dtype=torch.int64, device=dev)
     if nbytes:
         dev_data.view(torch.uint8)[:nbytes].copy_(data.view(torch.uint8).to(dev))
-    return _search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), offs.to(dev),
+    return _bloom_search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), offs.to(dev),
                    dev_data, nbytes, offs.numel() // 8, max_stack, int(k), int(hash_k),
                    bool(return_bool_mask))
 
@@ -275,3 +275,177 @@ def prepare_plans(expressions: list[str], hash_k: int, device: torch.device,
     blob[: 8 * b] = offsets
     blob[8 * b :].view(np.uint8)[: data.size] = data
     return torch.from_numpy(blob).to(device), b, max_stack
+
+
+# --- SilverTorch search (fork_search.cpp:13-49) -------------------------------------------------
+
+_LIB.define(
+    "search(Tensor query, Tensor probe_ids, Tensor cluster_offsets, Tensor cluster_sizes, "
+    "Tensor item_codes, Tensor sort_perm, Tensor global_scale, int k, "
+    "int max_tensor_size_per_row, int divisor_for_int8=-1, Tensor? filtering_bit_mask=None, "
+    "Tensor? bloom_index=None, Tensor? bloom_bundle_b_offsets=None, Tensor? plans=None, "
+    "int plan_count=0, int max_stack_size=0, Tensor? query_plan_index=None, int bloom_k=0, "
+    "int hash_k=0, Tensor? item_clause_attrs=None, Tensor? clause_slots=None, "
+    "Tensor? clause_is_reverse=None, Tensor? query_clause_attrs=None) -> (Tensor, Tensor)"
+)
+_LIB.define(
+    "probe_prep(Tensor query, Tensor probe_ids, Tensor cluster_offsets, Tensor cluster_sizes) "
+    "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)"
+)
+
+MAX_SEARCH_K = 1024  # kSelectMaxK
+MAX_PROBE = 1024
+
+
+def quantize_rows(query: Tensor) -> tuple[Tensor, Tensor]:
+    """float32 ``[B, D]`` → ``(codes int8 [B, D], scales float32 [B])`` on the GPU (the
+    quantization of ``fork_search_cuda.cu:680-699``)."""
+    q = query.to(torch.float32).contiguous()
+    dev = nat.require_device(q)
+    b, d = q.shape
+    codes = torch.empty((b, d), dtype=torch.int8, device=dev)
+    scales = torch.empty((b,), dtype=torch.float32, device=dev)
+    if b and d:
+        with torch.cuda.device(dev):
+            st = nat.lib().rt_quantize_int8_rows(nat.ptr(q), b, d, nat.ptr(codes),
+                                                 nat.ptr(scales), nat.stream(dev))
+        nat.check(st)
+    return codes, scales
+
+
+def _probe_prep(query, probe_ids, cluster_offsets, cluster_sizes):
+    """``(codes, scales, cluster_ids, cluster_length, selected_offsets, warp_size,
+    warp_rounded_length_cumsum, remaining_length_cumsum, warp_size_cumsum)``
+    (``fork_search_cuda.cu:653-768, 1200-1254``): the quantized rows, the probed clusters'
+    ids / lengths / offsets, and the 32-doc warp bookkeeping of the reference's scorer
+    (per-row cumulative warp-rounded lengths; cumulative remainders and warp counts over all
+    rows)."""
+    if query.dim() != 2 or query.dtype != torch.float32:
+        raise RuntimeError("query must be float32 [B, D]")
+    if probe_ids.dim() != 2 or probe_ids.shape[0] != query.shape[0]:
+        raise RuntimeError("probe_ids must be [B, n_probe]")
+    if cluster_offsets.dtype != torch.int64 or cluster_sizes.dtype != torch.int64:
+        raise RuntimeError("cluster_offsets and cluster_sizes must be int64")
+    codes, scales = quantize_rows(query)
+    probes = probe_ids.to(torch.int64).contiguous()
+    lens = cluster_sizes[probes]
+    offs = cluster_offsets[probes]
+    warps = lens // 32
+    rem = lens % 32
+    return (codes, scales, probes.clone(), lens, offs, warps.to(torch.int32).reshape(-1),
+            (warps * 32).cumsum(1).to(torch.int32), rem.reshape(-1).cumsum(0).to(torch.int32),
+            warps.reshape(-1).cumsum(0).to(torch.int32))
+
+
+_LIB.impl("probe_prep", _probe_prep, "CUDA")
+
+
+def _capturing() -> bool:
+    return torch.cuda.is_current_stream_capturing()
+
+
+def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sort_perm,
+            global_scale, k, max_tensor_size_per_row, divisor_for_int8=-1,
+            filtering_bit_mask=None, bloom_index=None, bloom_bundle_b_offsets=None, plans=None,
+            plan_count=0, max_stack_size=0, query_plan_index=None, bloom_k=0, hash_k=0,
+            item_clause_attrs=None, clause_slots=None, clause_is_reverse=None,
+            query_clause_attrs=None):
+    """SilverTorch's forward after phase 1 on the HIP kernels: quantize the rows, filter (at most
+    one of a full-N mask, Bloom plans -- with the exact recheck when ``query_clause_attrs`` is
+    given -- or the exact clauses), score the probed clusters' int8 codes and keep the top ``k``
+    by (key desc, slot asc), then ``id = sort_perm[position]`` and the dequantized score
+    (``fork_search_cuda.cu:1256-1524``). A one-list int32 search runs as the full scan."""
+    if item_codes.dtype != torch.int8 or item_codes.dim() != 2 or \
+            item_codes.shape[1] != query.shape[1]:
+        raise RuntimeError("item_codes must be int8 [N, D] with the query's D")
+    exact = query_clause_attrs is not None
+    if filtering_bit_mask is not None and (plans is not None or exact):
+        raise RuntimeError("search takes one filter: plans (+ query_clause_attrs to recheck), "
+                           "query_clause_attrs or filtering_bit_mask")
+    if exact and (item_clause_attrs is None or clause_slots is None or clause_is_reverse is None):
+        raise RuntimeError("the exact filter needs item_clause_attrs, clause_slots and "
+                           "clause_is_reverse")
+    if not 1 <= k <= MAX_SEARCH_K:
+        raise RuntimeError(f"k must be in [1, {MAX_SEARCH_K}], got {k}")
+    if probe_ids.dim() != 2 or probe_ids.shape[0] != query.shape[0] or \
+            probe_ids.shape[1] > MAX_PROBE:
+        raise RuntimeError(f"probe_ids must be [B, n_probe <= {MAX_PROBE}]")
+    if not item_codes.is_contiguous():
+        raise ValueError("item_codes must be contiguous (copy it once at index build)")
+    dev = nat.require_device(query, item_codes, sort_perm, cluster_offsets, cluster_sizes)
+    b, d = query.shape
+    n = item_codes.shape[0]
+    codes, scales = quantize_rows(query)
+    mask = None
+    if filtering_bit_mask is not None:
+        mask = filtering_bit_mask.to(torch.int64).contiguous()
+    if plans is not None:
+        if bloom_index is None or bloom_bundle_b_offsets is None:
+            raise RuntimeError("plans need bloom_index and bloom_bundle_b_offsets")
+        bm = _search_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count,
+                              max_stack_size, bloom_k, hash_k, False)
+        mask = bm[query_plan_index.to(torch.int64)] if query_plan_index is not None else bm[:b]
+        mask = mask.contiguous()
+    if exact:
+        out = torch.empty((b, (n + 63) // 64), dtype=torch.int64, device=dev)
+        slots = item_clause_attrs.to(torch.int32).contiguous()
+        cs = clause_slots.to(torch.int64).contiguous()
+        rev = clause_is_reverse.to(torch.int8).contiguous()
+        qv = query_clause_attrs.to(torch.int64)
+        qv = torch.where((qv >= -1) & (qv <= 2**31 - 1), qv, -(2**31)).to(torch.int32)
+        with torch.cuda.device(dev):
+            st = nat.lib().rt_clause_slots_filter(
+                nat.ptr(slots), slots.shape[0] if slots.dim() == 2 else 0, n, nat.ptr(cs),
+                cs.numel() - 1, nat.ptr(rev), nat.ptr(qv.contiguous()), b, nat.ptr(mask),
+                0 if mask is None else mask.shape[1], nat.ptr(out), nat.stream(dev))
+        nat.check(st)
+        mask = out
+    width = (int(max_tensor_size_per_row) + 31) // 32 * 32
+    ids = torch.empty((b, k), dtype=torch.int64, device=dev)
+    scores = torch.empty((b, k), dtype=torch.float32, device=dev)
+    if b == 0:
+        return ids, scores
+    perm = sort_perm.to(torch.int64).contiguous()
+    gs = global_scale.to(torch.float32).reshape(-1).contiguous()
+    offs = cluster_offsets.to(torch.int64).contiguous()
+    sizes = cluster_sizes.to(torch.int64).contiguous()
+    probes = probe_ids.to(torch.int64).contiguous()
+    lib = nat.lib()
+    full = (divisor_for_int8 == -1 and offs.numel() == 1 and probes.shape[1] == 1
+            and width >= n and not _capturing()
+            and int(offs[0].item()) == 0 and int(sizes[0].item()) == n)
+    if full:
+        # one list holding every item in order: slot = position, the full-scan kernels
+        from retrieve_amd import hip  # noqa: F401  (registers torch.ops.retrieve.*)
+        pos, dots = torch.ops.retrieve.int8_scan_topk(codes, item_codes, k, mask)
+        ids.copy_(pos)
+        with torch.cuda.device(dev):
+            st = lib.rt_search_epilogue(nat.ptr(ids), nat.ptr(dots), nat.ptr(scores), b, k,
+                                        nat.ptr(perm), perm.numel(), nat.ptr(scales), nat.ptr(gs),
+                                        nat.stream(dev))
+        nat.check(st)
+        return ids, scores
+    ws = nat.workspace(lib.rt_ivf_search_workspace(b, width, k), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_ivf_search(
+            nat.ptr(codes), nat.ptr(scales), b, nat.ptr(item_codes), n, d, nat.ptr(probes),
+            probes.shape[1], nat.ptr(offs), nat.ptr(sizes), offs.numel(), width, nat.ptr(mask),
+            0 if mask is None else mask.shape[1], int(divisor_for_int8), nat.ptr(perm),
+            perm.numel(), nat.ptr(gs), k, nat.ptr(ids), nat.ptr(scores), nat.ptr(ws), ws.numel(),
+            nat.stream(dev))
+    nat.check(st)
+    return ids, scores
+
+
+_LIB.impl("search", _st_search, "CUDA")
+
+
+@torch.library.register_fake("st::search")
+def _(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sort_perm, global_scale, k,
+      max_tensor_size_per_row, divisor_for_int8=-1, filtering_bit_mask=None, bloom_index=None,
+      bloom_bundle_b_offsets=None, plans=None, plan_count=0, max_stack_size=0,
+      query_plan_index=None, bloom_k=0, hash_k=0, item_clause_attrs=None, clause_slots=None,
+      clause_is_reverse=None, query_clause_attrs=None):
+    rows = query.shape[0]
+    return (query.new_empty((rows, k), dtype=torch.int64),
+            query.new_empty((rows, k), dtype=torch.float32))

@@ -262,3 +262,53 @@ def test_candidate_topk_brute_force():
                                    full, 9, pad_to_k=False, empty_score=np.iinfo(np.int32).min)
     want_ids, want_sc = osc.candidate_int8_topk(q, codes, cand, 9)
     assert np.array_equal(ids2, want_ids) and np.array_equal(sc2.astype(np.int32), want_sc)
+
+
+def test_gemv_oracle_equals_fma_order():
+    """The float32 oracle of the in-order fp16 GEMV against exact rational arithmetic per step:
+    every step is round-to-nearest of (acc + q_k * e_k) with the product exact."""
+    from fractions import Fraction
+
+    g = rng(95)
+    q = g.standard_normal(40).astype(np.float16)
+    e = g.standard_normal((40, 5)).astype(np.float16)
+    got = osc.gemv_scores(q, e)
+    for n in range(5):
+        acc = np.float32(0)
+        for k in range(40):
+            exact = Fraction(float(acc)) + Fraction(float(q[k])) * Fraction(float(e[k, n]))
+            acc = np.float32(float(exact))  # one rounding (float(exact) is exact-enough here)
+        assert got[n] == acc
+
+
+def test_search_oracle_one_list_is_the_full_scan():
+    """One list of every item, identity permutation: the search oracle is the int8 full-scan
+    top-k of the quantized rows (pinned by the int8 KAT), scored (dot * scale) * global_scale."""
+    from oracle import quantize as oq
+    from oracle import silvertorch as ost
+
+    g = rng(96)
+    n, d, b, k = 3000, 64, 5, 20
+    items = g.integers(-128, 128, (n, d), dtype=np.int8)
+    q = g.standard_normal((b, d)).astype(np.float32)
+    ids, sc = ost.search(q, np.zeros((b, 1), np.int64), [0], [n], items, np.arange(n), [0.5], k,
+                         n)
+    codes, scales = oq.quantize_int8(q)
+    want_ids, want_dots = osc.int8_topk(codes, items, k)
+    assert np.array_equal(ids, want_ids)
+    assert np.array_equal(sc, (want_dots.astype(np.float32) * scales[:, None]) * np.float32(0.5))
+
+
+def test_search_oracle_slot_order_by_hand():
+    """Two clusters probed in the order [1, 0]: slots are cluster 1's items, then cluster 0's;
+    equal rows tie, so the lowest slots win; ``width`` truncates; ``sort_perm`` maps ids."""
+    from oracle import silvertorch as ost
+
+    items = np.ones((6, 16), np.int8)  # every dot equal
+    perm = np.array([10, 11, 12, 13, 14, 15])
+    q = np.ones((1, 16), np.float32)
+    ids, _ = ost.search(q, np.array([[1, 0]]), [0, 4], [4, 2], items, perm, [1.0], 3, 64)
+    assert ids.tolist() == [[14, 15, 10]]
+    ids, _ = ost.search(q, np.array([[1, 0]]), [0, 4], [4, 2], items, perm, [1.0], 8, 5)
+    # width 5 -> 32 slots after rounding: all 6 items, then -1 pads
+    assert ids.tolist() == [[14, 15, 10, 11, 12, 13, -1, -1]]

@@ -1,0 +1,162 @@
+"""``torch.ops.st.search`` / ``st.probe_prep`` on the GPU against the CPU restatement
+(``oracle.silvertorch``): quantization bit for bit, one-list full scans and IVF probes (int32
+and fp16 key paths), ties to the lower slot, ``sort_perm`` ids and dequantized scores, and the
+filters (full-N mask, Bloom plans with the exact recheck, exact clauses in the slot layout)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import retrieve_amd.st as st
+from oracle import filters as of
+from oracle import quantize as oq
+from oracle import silvertorch as ost
+from retrieve_amd import bloom as bl
+from tests.conftest import rng
+from tests.test_int8_scan import _pack
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(dev, x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def _ivf(g, n, d, n_lists):
+    """Items sorted by cluster: offsets / sizes of n_lists contiguous clusters, a random
+    sort_perm (sorted position -> original id)."""
+    cuts = np.sort(g.choice(np.arange(1, n), n_lists - 1, replace=False))
+    offsets = np.concatenate([[0], cuts]).astype(np.int64)
+    sizes = np.diff(np.concatenate([offsets, [n]])).astype(np.int64)
+    items = g.integers(-128, 128, (n, d), dtype=np.int8)
+    perm = g.permutation(n).astype(np.int64)
+    return items, offsets, sizes, perm
+
+
+def _run(dev, q, probes, offsets, sizes, items, perm, gs, k, width, divisor=-1, **kw):
+    print(f"search B={q.shape[0]} N={items.shape[0]} D={q.shape[1]} n_lists={len(offsets)} "
+          f"n_probe={probes.shape[1]} k={k} width={width} divisor={divisor} "
+          f"filters={sorted(kw)}", flush=True)
+    ids, sc = torch.ops.st.search(
+        _t(dev, q), _t(dev, probes), _t(dev, offsets), _t(dev, sizes), _t(dev, items),
+        _t(dev, perm), _t(dev, np.array([gs], np.float32)), k, width, divisor, **kw)
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), sc.cpu().numpy()
+
+
+def test_probe_prep(dev):
+    g = rng(101)
+    q = (g.standard_normal((9, 200)) * np.exp(g.standard_normal((9, 1)))).astype(np.float32)
+    q[3] = 0.0  # abs_max clamps to 1e-8
+    q[4, :7] = [127 * 0.01 / 2.54, -2.54, 0.5, 1.5, -0.5, 2.5, 0.0]  # exact .5 quotients
+    sizes = g.integers(0, 100, 12).astype(np.int64)
+    offsets = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    probes = g.integers(0, 12, (9, 5)).astype(np.int64)
+    out = torch.ops.st.probe_prep(_t(dev, q), _t(dev, probes), _t(dev, offsets), _t(dev, sizes))
+    codes, scales = oq.quantize_int8(q)
+    assert np.array_equal(out[0].cpu().numpy(), codes)
+    assert np.array_equal(out[1].cpu().numpy(), scales)
+    lens = sizes[probes]
+    assert np.array_equal(out[3].cpu().numpy(), lens)
+    assert np.array_equal(out[4].cpu().numpy(), offsets[probes])
+    assert np.array_equal(out[6].cpu().numpy(), np.cumsum((lens // 32) * 32, axis=1))
+    assert np.array_equal(out[7].cpu().numpy(), np.cumsum((lens % 32).reshape(-1)))
+    assert np.array_equal(out[8].cpu().numpy(), np.cumsum((lens // 32).reshape(-1)))
+
+
+@pytest.mark.parametrize("divisor", [-1, 64])
+def test_one_list_full_scan(dev, divisor):
+    g = rng(102)
+    n, d, b, k = 60_000, 128, 6, 100
+    items, _, _, perm = _ivf(g, n, d, 2)
+    q = g.standard_normal((b, d)).astype(np.float32)
+    probes = np.zeros((b, 1), np.int64)
+    ids, sc = _run(dev, q, probes, [0], [n], items, perm, 0.25, k, n, divisor)
+    want_ids, want_sc = ost.search(q, probes, [0], [n], items, perm, [0.25], k, n, divisor)
+    assert np.array_equal(ids, want_ids)
+    assert np.array_equal(sc, want_sc)
+
+
+@pytest.mark.parametrize("divisor", [-1, 128])
+@pytest.mark.parametrize("n_lists,n_probe,width_frac", [(50, 8, 1.0), (7, 7, 0.5), (300, 40, 1.0)])
+def test_ivf_probes(dev, divisor, n_lists, n_probe, width_frac):
+    g = rng(103 + n_lists + n_probe)
+    n, d, b, k = 40_000, 256, 5, 100
+    items, offsets, sizes, perm = _ivf(g, n, d, n_lists)
+    q = g.standard_normal((b, d)).astype(np.float32)
+    probes = np.stack([g.permutation(n_lists)[:n_probe] for _ in range(b)]).astype(np.int64)
+    probes[0, 1] = 10**6  # an invalid cluster id probes nothing
+    width = int(max(sizes[probes[r][probes[r] < n_lists]].sum() for r in range(b)) * width_frac)
+    ids, sc = _run(dev, q, probes, offsets, sizes, items, perm, 1.5, k, width, divisor)
+    want_ids, want_sc = ost.search(q, probes, offsets, sizes, items, perm, [1.5], k, width,
+                                   divisor)
+    assert np.array_equal(ids, want_ids)
+    assert np.array_equal(sc, want_sc)
+
+
+def test_ties_go_to_the_lower_slot(dev):
+    g = rng(104)
+    n, d = 5000, 64
+    items, offsets, sizes, perm = _ivf(g, n, d, 10)
+    items[:] = items[0]  # every dot equal
+    q = g.standard_normal((3, d)).astype(np.float32)
+    probes = np.array([[9, 2, 5], [0, 1, 2], [4, 4, 3]], np.int64)  # a repeated probe too
+    ids, _ = _run(dev, q, probes, offsets, sizes, items, perm, 1.0, 50, n)
+    want_ids, _ = ost.search(q, probes, offsets, sizes, items, perm, [1.0], 50, n)
+    assert np.array_equal(ids, want_ids)
+
+
+def test_filters(dev):
+    g = rng(105)
+    n, d, b, k, c = 30_000, 64, 6, 50, 3
+    items, offsets, sizes, perm = _ivf(g, n, d, 20)
+    q = g.standard_normal((b, d)).astype(np.float32)
+    probes = np.stack([g.permutation(20)[:6] for _ in range(b)]).astype(np.int64)
+    width = n
+    # full-N mask
+    valid = g.random((b, n)) < 0.3
+    ids, sc = _run(dev, q, probes, offsets, sizes, items, perm, 1.0, k, width,
+                   filtering_bit_mask=_t(dev, _pack(valid)))
+    want = ost.search(q, probes, offsets, sizes, items, perm, [1.0], k, width, valid=valid)
+    assert np.array_equal(ids, want[0]) and np.array_equal(sc, want[1])
+    # exact clauses in the slot layout (one value per doc and clause, -1 for none)
+    attrs = g.integers(0, 8, (n, c, 1)).astype(np.int64)
+    attrs[g.random((n, c, 1)) < 0.2] = -1
+    qa = g.integers(0, 8, (b, c)).astype(np.int64)
+    qa[g.random((b, c)) < 0.3] = -1
+    rev = np.array([0, 1, 0], bool)
+    exact = of.clause_match(attrs, rev, qa)
+    slots = attrs[:, :, 0].T.astype(np.int32)  # [R = C, N]: one slot row per clause
+    cs = np.arange(c + 1, dtype=np.int64)
+    kw = dict(item_clause_attrs=_t(dev, slots), clause_slots=_t(dev, cs),
+              clause_is_reverse=_t(dev, rev), query_clause_attrs=_t(dev, qa))
+    ids, sc = _run(dev, q, probes, offsets, sizes, items, perm, 1.0, k, width, **kw)
+    want = ost.search(q, probes, offsets, sizes, items, perm, [1.0], k, width, valid=exact)
+    assert np.array_equal(ids, want[0]) and np.array_equal(sc, want[1])
+    # Bloom plans + the exact recheck: bloom AND exact == exact
+    fid, fo, fv = st.attrs_to_features(_t(dev, attrs))
+    words, boffs = torch.ops.st.bloom_index_build_fixed(fid, fo, fv, 64, 3)
+    exprs = bl.queries_to_expressions(qa, rev)
+    blob, count, max_stack = st.prepare_plans(exprs, 7, dev)
+    ids, sc = _run(dev, q, probes, offsets, sizes, items, perm, 1.0, k, width,
+                   bloom_index=words, bloom_bundle_b_offsets=boffs, plans=blob,
+                   plan_count=count, max_stack_size=max_stack, bloom_k=3, hash_k=7, **kw)
+    assert np.array_equal(ids, want[0]) and np.array_equal(sc, want[1])
+
+
+def test_errors(dev):
+    q = torch.zeros((2, 64), device=dev)
+    items = torch.zeros((10, 64), dtype=torch.int8, device=dev)
+    probes = torch.zeros((2, 1), dtype=torch.int64, device=dev)
+    o = torch.zeros(1, dtype=torch.int64, device=dev)
+    s = torch.full((1,), 10, dtype=torch.int64, device=dev)
+    perm = torch.arange(10, device=dev)
+    gs = torch.ones(1, device=dev)
+    with pytest.raises(RuntimeError):
+        torch.ops.st.search(q, probes, o, s, items.float(), perm, gs, 5, 10)
+    with pytest.raises(RuntimeError):
+        torch.ops.st.search(q, probes, o, s, items, perm, gs, 5, 10,
+                            filtering_bit_mask=torch.zeros((2, 1), dtype=torch.int64, device=dev),
+                            query_clause_attrs=torch.zeros((2, 1), dtype=torch.int64, device=dev))
