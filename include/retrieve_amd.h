@@ -93,7 +93,8 @@ int rt_profile_collect(double* total_ms, int64_t* launches);
  * Replaces the clause kernels behind torch.ops.retrieve.clause_mask / clause_mask_scores
  * (retrieve/src/retrieve/ops/triton/clause_mask.py:270-303; predicate functional.py:173-185)
  * and the exact payload filter of st::search (silvertorch/.../fork_filters.cuh:15-56).
- * item_attrs [N, C, A] int64 (-1 pads); clause_is_reverse [C] 0/1; query_values [B, C, V]
+ * item_attrs [N, C, A] of int16 / int32 / int64 (attr_bytes 2 / 4 / 8; -1 pads; the reference's
+ * tables are int64); clause_is_reverse [C] 0/1; query_values [B, C, V]
  * int64, -1 pads (V == 1: the reference's [B, C], -1 = inactive clause). Clause c is active
  * for row b iff one of its V values is not -1; it matches iff an item value equals one of
  * them, XOR reverse[c]; an item passes iff every active clause matches. C <= 32.
@@ -102,10 +103,12 @@ int rt_profile_collect(double* total_ms, int64_t* launches);
  *         a Bloom search's [B, n_bundles * 32]) when it is not null;
  * mode 1: out = [B, N] uint8 0/1;
  * mode 2: out = [B, N] float: scores[b, d] (contiguous [B, N]) where row b passes, -inf else. */
-int rt_clause_filter(const int64_t* item_attrs, int64_t N, int64_t C, int64_t A,
+size_t rt_clause_filter_workspace(int64_t B, int64_t C, int64_t V);
+int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t N, int64_t C, int64_t A,
                      const int8_t* clause_is_reverse, const int64_t* query_values, int64_t B,
                      int64_t V, int mode, const float* scores, const uint64_t* and_mask,
-                     int64_t and_mask_words, void* out, rt_stream_t stream);
+                     int64_t and_mask_words, void* out, void* workspace, size_t workspace_bytes,
+                     rt_stream_t stream);
 
 /* Packed mask [B, ceil(N/64)] (layout above) -> each row's set items in ascending order:
  * out_indices[b, 0:counts[b]] (int64, [B, N] buffer; the tail is not written), counts [B].

@@ -22,8 +22,12 @@ def _merge(best_s, best_i, s, i, k):
     return cs.gather(1, by_score), ci.gather(1, by_score)
 
 
-def int8_topk_cpu(q_codes: torch.Tensor, item_codes: torch.Tensor, k: int, chunk: int = ITEM_CHUNK):
-    """``(ids [B, k], scores float32 [B, k])`` of the int8 dot, ties to the lowest id."""
+def int8_topk_cpu(q_codes: torch.Tensor, item_codes: torch.Tensor, k: int, chunk: int = ITEM_CHUNK,
+                  valid_fn=None):
+    """``(ids [B, k], scores float32 [B, k])`` of the int8 dot, ties to the lowest id.
+    ``valid_fn(start, stop)`` (optional) gives the ``[B, stop - start]`` bool filter of a chunk:
+    failing items score ``-inf`` before the chunk's ``topk`` (the postfilter gate of
+    ``evaluation/bench/postfilter.py:41-59``)."""
     q = q_codes.float()
     b = q.shape[0]
     best_s = torch.full((b, k), float("-inf"))
@@ -31,17 +35,36 @@ def int8_topk_cpu(q_codes: torch.Tensor, item_codes: torch.Tensor, k: int, chunk
     for start in range(0, item_codes.shape[0], chunk):
         part = item_codes[start : start + chunk].float()
         scores = q @ part.t()
+        if valid_fn is not None:
+            scores = scores.masked_fill(~valid_fn(start, start + part.shape[0]), float("-inf"))
         top = torch.topk(scores, min(k, part.shape[0]), dim=1)
         best_s, best_i = _merge(best_s, best_i, top.values, top.indices + start, k)
     return best_i, best_s
 
 
-def time_int8(q_codes, item_sample, k: int, reps: int = 3) -> tuple[float, int]:
+def clause_sets_valid(item_attrs: torch.Tensor, query_sets: torch.Tensor):
+    """``valid_fn`` of value-set clauses: ``[N, C, A]`` attrs, ``[B, C, V]`` sets (``-1``
+    pads, an all ``-1`` clause inactive); clause ``c`` passes iff an item value is in the set."""
+
+    def fn(start, stop):
+        part = item_attrs[start:stop]
+        out = torch.ones((query_sets.shape[0], part.shape[0]), dtype=torch.bool)
+        for r in range(query_sets.shape[0]):
+            for c in range(query_sets.shape[1]):
+                vals = query_sets[r, c][query_sets[r, c] != -1]
+                if vals.numel():
+                    out[r] &= torch.isin(part[:, c, :], vals).any(1)
+        return out
+
+    return fn
+
+
+def time_int8(q_codes, item_sample, k: int, reps: int = 3, valid_fn=None) -> tuple[float, int]:
     """Median seconds of ``int8_topk_cpu`` over ``reps`` runs, and the threads used."""
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        int8_topk_cpu(q_codes, item_sample, k)
+        int8_topk_cpu(q_codes, item_sample, k, valid_fn=valid_fn)
         times.append(time.perf_counter() - t0)
     times.sort()
     return times[len(times) // 2], torch.get_num_threads()

@@ -45,21 +45,22 @@ def clause_match(item_attrs: np.ndarray, reverse: np.ndarray, query: np.ndarray)
     return (m | inactive).all(axis=-1)
 
 
-def clause_match_sets(item_attrs: np.ndarray, query_sets: np.ndarray) -> np.ndarray:
-    """Value-set clauses: ``query_sets [B, C, V]`` (``-1`` pads). Clause ``c`` passes iff some
-    item value is in the row's set; a clause whose set is all ``-1`` is inactive. With ``V ==
-    1`` this is ``clause_match`` with no reverse clause."""
+def clause_match_sets(item_attrs: np.ndarray, query_sets: np.ndarray, reverse=None) -> np.ndarray:
+    """Value-set clauses: ``query_sets [B, C, V]`` (``-1`` pads). Clause ``c`` matches iff some
+    item value is in the row's set, XOR ``reverse[c]``; a clause whose set is all ``-1`` is
+    inactive. With ``V == 1`` this is ``clause_match``."""
     qs = np.asarray(query_sets)
     items = np.asarray(item_attrs)
     b, c, _ = qs.shape
+    rev = np.zeros(c, bool) if reverse is None else np.asarray(reverse, bool)
     out = np.ones((b, items.shape[0]), dtype=bool)
     for r in range(b):
         for ci in range(c):
             vals = qs[r, ci][qs[r, ci] != -1]
             if vals.size == 0:
                 continue
-            hit = np.isin(items[:, ci, :], vals) & (items[:, ci, :] != -1)
-            out[r] &= hit.any(axis=1)
+            hit = (np.isin(items[:, ci, :], vals) & (items[:, ci, :] != -1)).any(axis=1)
+            out[r] &= hit ^ rev[ci]
     return out
 
 

@@ -20,14 +20,19 @@
 namespace rt {
 
 constexpr int kClauseThreads = 256;
-constexpr int kRegAttrs = 16;  // C * A up to this is held in registers
+constexpr int kRegAttrs = 16;  // one value per clause (A == 1), C up to this: held in registers
 constexpr int kMaxClauses = 32;
 constexpr int kCompactWords = 128;  // 64-bit mask words per compaction chunk (one wave)
+// Rows whose values all lie in [0, kSetDomain) test membership in a per-clause bitmap (staged
+// in LDS) instead of walking the value list.
+constexpr int kSetDomain = 1024;
+constexpr int kSetWords = kSetDomain / 64;
+constexpr int kMaxBitmapLds = 64 * 1024;
 
 enum ClauseMode : int { kClauseBits = 0, kClauseBool = 1, kClauseScores = 2 };
 
 struct ClauseArgs {
-  const int64_t* attrs;  // [N, C, A]
+  const void* attrs;  // [N, C, A] of int16, int32 or int64 (the kernel's T)
   int64_t N;
   int C;
   int A;
@@ -35,6 +40,13 @@ struct ClauseArgs {
   const int64_t* qvals;   // [B, C, V], -1 pads
   int64_t B;
   int V;
+  // per row, from the prep pass: the active clauses, and each clause's values without pads
+  const uint32_t* active;  // [B]
+  const int32_t* nv;       // [B, C]
+  const int64_t* qc;       // [B, C, V], clause c's first nv[b, c] entries
+  const uint32_t* small;   // [B]: every value of the row in [0, kSetDomain)
+  const uint32_t* rev_mask;  // [1]: bit c = clause_is_reverse[c]
+  const uint64_t* bitmaps;  // [B, C, kSetWords]: the row's value set of clause c (small rows)
   int64_t rows_per_wg;     // query rows each workgroup loops over
   const uint64_t* and_mask;  // [B, and_words] or null (bits mode)
   int64_t and_words;
@@ -43,48 +55,104 @@ struct ClauseArgs {
   int64_t W;
 };
 
-template <bool REG>
-__device__ inline int64_t item_attr(const int64_t (&at)[kRegAttrs], const int64_t* row, int i) {
+template <bool REG, class T>
+__device__ inline int64_t item_attr(const int64_t (&at)[kRegAttrs], const T* row, int i) {
   if constexpr (REG) {
     return at[i];
   } else {
-    return row[i];
+    return static_cast<int64_t>(row[i]);
   }
 }
 
+// Per query row (one thread each): the active clause mask, and each clause's values with the
+// -1 pads removed, so the item pass visits only real values.
+__global__ void clause_prep_kernel(const int64_t* qvals, int64_t B, int C, int V,
+                                   const int8_t* reverse, uint32_t* active, int32_t* nv,
+                                   int64_t* qc, uint32_t* small, uint64_t* bitmaps,
+                                   uint32_t* rev_mask) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b == 0) {
+    uint32_t r = 0;
+    for (int c = 0; c < C; ++c) r |= reverse[c] != 0 ? 1u << c : 0u;
+    rev_mask[0] = r;
+  }
+  if (b >= B) return;
+  uint32_t act = 0;
+  bool fits = true;
+  for (int c = 0; c < C; ++c) {
+    const int64_t* src = qvals + (b * C + c) * V;
+    int64_t* dst = qc + (b * C + c) * V;
+    uint64_t* bm = bitmaps + (b * C + c) * kSetWords;
+    for (int w = 0; w < kSetWords; ++w) bm[w] = 0ull;
+    int n = 0;
+    for (int v = 0; v < V; ++v) {
+      const int64_t x = src[v];
+      if (x == -1) continue;
+      dst[n++] = x;
+      if (x >= 0 && x < kSetDomain) {
+        bm[x >> 6] |= 1ull << (x & 63);
+      } else {
+        fits = false;
+      }
+    }
+    nv[b * C + c] = n;
+    act |= n > 0 ? 1u << c : 0u;
+  }
+  active[b] = act;
+  small[b] = fits ? 1u : 0u;
+}
+
 // One query row against this lane's item: 1 iff every active clause matches.
-template <bool REG>
+template <bool REG, class T>
 __device__ inline bool clause_pass(const ClauseArgs& a, const int64_t (&at)[kRegAttrs],
-                                   const int64_t* row, int64_t b, uint32_t rev_mask) {
-  const int64_t* q = a.qvals + b * a.C * a.V;
-  uint32_t active = 0;
+                                   const T* row, int64_t b, uint32_t rev_mask,
+                                   const uint64_t* bm, uint32_t active) {
+  // (active == 0: no clause, every item passes)
+  const int32_t* nvb = a.nv + b * a.C;
+  const int64_t* qcb = a.qc + b * a.C * a.V;
   uint32_t match = 0;
-  if constexpr (REG) {
-    // attribute slot i belongs to clause i / A: unrolled so the registers are indexed statically
+  if (bm != nullptr) {
+    // the row's sets as bitmaps (LDS): one lookup per attribute value
+    if constexpr (REG) {  // A == 1: register i holds clause i's value
+#pragma unroll
+      for (int i = 0; i < kRegAttrs; ++i) {
+        const int64_t x = at[i];
+        if (((active >> i) & 1u) && x >= 0 && x < kSetDomain) {
+          match |= ((bm[i * kSetWords + (x >> 6)] >> (x & 63)) & 1ull) ? 1u << i : 0u;
+        }
+      }
+    } else {
+      for (int c = 0; c < a.C; ++c) {
+        if (((active >> c) & 1u) == 0u) continue;
+        for (int x = 0; x < a.A; ++x) {
+          const int64_t v = item_attr<REG, T>(at, row, c * a.A + x);
+          if (v >= 0 && v < kSetDomain && ((bm[c * kSetWords + (v >> 6)] >> (v & 63)) & 1ull)) {
+            match |= 1u << c;
+          }
+        }
+      }
+    }
+    return ((match ^ rev_mask) & active) == active;
+  }
+  if constexpr (REG) {  // A == 1: unrolled so the registers are indexed statically
 #pragma unroll
     for (int i = 0; i < kRegAttrs; ++i) {
-      if (i < a.C * a.A) {
-        const int c = i / a.A;
-        const int64_t* qc = q + c * a.V;
+      if ((active >> i) & 1u) {
+        const int64_t* vals = qcb + i * a.V;
+        const int n = nvb[i];
         bool eq = false;
-        for (int v = 0; v < a.V; ++v) {
-          const int64_t val = qc[v];
-          if (val == -1) continue;
-          active |= 1u << c;
-          eq |= at[i] == val;
-        }
-        match |= eq ? 1u << c : 0u;
+        for (int v = 0; v < n; ++v) eq |= at[i] == vals[v];
+        match |= eq ? 1u << i : 0u;
       }
     }
   } else {
     for (int c = 0; c < a.C; ++c) {
-      const int64_t* qc = q + c * a.V;
+      if (((active >> c) & 1u) == 0u) continue;
+      const int64_t* vals = qcb + c * a.V;
+      const int n = nvb[c];
       bool eq = false;
-      for (int v = 0; v < a.V; ++v) {
-        const int64_t val = qc[v];
-        if (val == -1) continue;
-        active |= 1u << c;
-        for (int x = 0; x < a.A; ++x) eq |= item_attr<REG>(at, row, c * a.A + x) == val;
+      for (int v = 0; v < n; ++v) {
+        for (int x = 0; x < a.A; ++x) eq |= item_attr<REG, T>(at, row, c * a.A + x) == vals[v];
       }
       match |= eq ? 1u << c : 0u;
     }
@@ -92,49 +160,234 @@ __device__ inline bool clause_pass(const ClauseArgs& a, const int64_t (&at)[kReg
   return ((match ^ rev_mask) & active) == active;
 }
 
-template <int MODE, bool REG>
+// Each workgroup stages its query rows' set bitmaps in LDS once, then walks 256-item chunks
+// round-robin with the other workgroups of its row range.
+template <int MODE, bool REG, class T>
 __global__ void __launch_bounds__(kClauseThreads) clause_kernel(ClauseArgs a) {
-  const int64_t d = static_cast<int64_t>(blockIdx.x) * kClauseThreads + threadIdx.x;
-  const bool valid = d < a.N;
+  const int lane = lane_id();
   const int ca = a.C * a.A;
-  const int64_t* row = a.attrs + (valid ? d : 0) * ca;
-  int64_t at[kRegAttrs];
-  if constexpr (REG) {
-#pragma unroll
-    for (int i = 0; i < kRegAttrs; ++i) at[i] = (i < ca && valid) ? row[i] : -1;
-  }
-  uint32_t rev_mask = 0;
-  for (int c = 0; c < a.C; ++c) rev_mask |= a.reverse[c] != 0 ? 1u << c : 0u;
-
+  const uint32_t rev_mask = a.C > 0 ? a.rev_mask[0] : 0u;
   const int64_t b0 = static_cast<int64_t>(blockIdx.y) * a.rows_per_wg;
   const int64_t b1 = b0 + a.rows_per_wg < a.B ? b0 + a.rows_per_wg : a.B;
-  const int lane = lane_id();
-  for (int64_t b = b0; b < b1; ++b) {
-    const bool pass = valid && clause_pass<REG>(a, at, row, b, rev_mask);
+  extern __shared__ uint64_t bm_lds[];
+  __shared__ uint32_t row_active[kWave];
+  __shared__ uint32_t row_small[kWave];
+  const int64_t row_words = static_cast<int64_t>(a.C) * kSetWords;
+  if (a.C > 0) {
+    for (int64_t i = threadIdx.x; i < (b1 - b0) * row_words; i += kClauseThreads) {
+      bm_lds[i] = a.bitmaps[b0 * row_words + i];
+    }
+    for (int64_t i = threadIdx.x; i < b1 - b0; i += kClauseThreads) {
+      row_active[i] = a.active[b0 + i];
+      row_small[i] = a.small[b0 + i];
+    }
+  }
+  __syncthreads();
+
+  const int nrows = static_cast<int>(b1 - b0);  // <= kWave (rows_per_wg is capped)
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kClauseThreads; base < a.N;
+       base += static_cast<int64_t>(gridDim.x) * kClauseThreads) {
+    const int64_t d = base + threadIdx.x;
+    const bool valid = d < a.N;
+    // bits mode: lane j handles row b0 + j's word of this wave's 64 items -- its AND-mask word
+    // is loaded here for all rows at once, and the row words are stored together after the loop
+    const int64_t wword = (d - lane) >> 6;
+    uint64_t am = ~0ull;
+    uint64_t mine = 0ull;
     if constexpr (MODE == kClauseBits) {
-      // item (wave base + l) at bit 63 - l of its word
-      uint64_t word = __builtin_bitreverse64(__ballot(pass));
-      const int64_t w = (d - lane) >> 6;
-      if (lane == 0 && w < a.W) {
-        if (a.and_mask != nullptr) word &= a.and_mask[b * a.and_words + w];
-        static_cast<uint64_t*>(a.out)[b * a.W + w] = word;
+      if (a.and_mask != nullptr && lane < nrows && wword < a.W) {
+        am = a.and_mask[(b0 + lane) * a.and_words + wword];
       }
-    } else if constexpr (MODE == kClauseBool) {
-      if (valid) static_cast<uint8_t*>(a.out)[b * a.N + d] = pass ? 1 : 0;
-    } else {
-      if (valid) {
-        static_cast<float*>(a.out)[b * a.N + d] = pass ? a.scores[b * a.N + d] : -INFINITY;
+    }
+    // lanes past the end read item 0 (no divergent loads) and are masked out
+    const T* row = static_cast<const T*>(a.attrs) + (valid ? d : 0) * ca;
+    int64_t at[kRegAttrs];
+    if constexpr (REG) {
+      // unconditional in-row loads (slot min(i, C - 1)) and a branch-free select, so the
+      // loads issue back to back
+#pragma unroll
+      for (int i = 0; i < kRegAttrs; ++i) {
+        const int64_t x = static_cast<int64_t>(row[i < ca ? i : ca - 1]);
+        const int64_t keep = -static_cast<int64_t>(i < ca);  // all ones or zero
+        at[i] = (x & keep) | ~keep;                           // x, or -1 past the row
+      }
+    }
+    for (int64_t b = b0; b < b1; ++b) {
+      const bool small = a.C > 0 && row_small[b - b0] != 0u;
+      const uint32_t active = a.C > 0 ? row_active[b - b0] : 0u;
+      const uint64_t* bm = small ? bm_lds + (b - b0) * row_words : nullptr;
+      const bool pass = valid && clause_pass<REG, T>(a, at, row, b, rev_mask, bm, active);
+      if constexpr (MODE == kClauseBits) {
+        // item (wave base + l) at bit 63 - l of its word, kept by lane b - b0
+        const uint64_t word = __builtin_bitreverse64(__ballot(pass));
+        mine = lane == static_cast<int>(b - b0) ? word : mine;
+      } else if constexpr (MODE == kClauseBool) {
+        if (valid) static_cast<uint8_t*>(a.out)[b * a.N + d] = pass ? 1 : 0;
+      } else {
+        if (valid) {
+          static_cast<float*>(a.out)[b * a.N + d] = pass ? a.scores[b * a.N + d] : -INFINITY;
+        }
+      }
+    }
+    if constexpr (MODE == kClauseBits) {
+      if (lane < nrows && wword < a.W) {
+        static_cast<uint64_t*>(a.out)[(b0 + lane) * a.W + wword] = mine & am;
       }
     }
   }
 }
 
-template <int MODE>
+// Query-mask form (C <= kQmaskClauses): a workgroup takes up to 32 query rows and builds in LDS
+// qm[c][x] = the rows whose clause-c set holds x, for x in [0, kSetDomain). An item then costs
+// one LDS lookup per attribute value for all its rows at once:
+//   pass_c = (OR over its values x of qm[c][x]) XOR (rev[c] ? ~0 : 0), OR the rows where c is
+//   inactive; the item's row mask is the AND over c.
+// Rows with a value outside [0, kSetDomain) take the value-list path row by row.
+constexpr int kQmaskRows = 32;
+constexpr int kQmaskClauses = 16;
+
+template <int MODE, bool REG, class T>
+__global__ void __launch_bounds__(kClauseThreads) clause_qmask_kernel(ClauseArgs a) {
+  const int lane = lane_id();
+  const int ca = a.C * a.A;
+  const uint32_t rev_mask = a.C > 0 ? a.rev_mask[0] : 0u;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * kQmaskRows;
+  const int nrows = static_cast<int>(b0 + kQmaskRows < a.B ? kQmaskRows : a.B - b0);
+  extern __shared__ uint32_t qm[];  // [C][kSetDomain]
+  __shared__ uint32_t clause_xor[kQmaskClauses];
+  __shared__ uint32_t clause_or[kQmaskClauses];
+  __shared__ uint32_t row_active[kQmaskRows];
+  __shared__ uint32_t slow_rows;
+  for (int i = threadIdx.x; i < a.C * kSetDomain; i += kClauseThreads) qm[i] = 0u;
+  if (threadIdx.x < kQmaskRows) {
+    const int r = threadIdx.x;
+    row_active[r] = r < nrows ? a.active[b0 + r] : 0u;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t slow = 0u;
+    for (int r = 0; r < nrows; ++r) slow |= a.small[b0 + r] != 0u ? 0u : 1u << r;
+    slow_rows = slow;
+    for (int c = 0; c < a.C; ++c) {
+      uint32_t inactive = slow;  // slow rows: any value here, replaced below
+      for (int r = 0; r < nrows; ++r) inactive |= (row_active[r] >> c) & 1u ? 0u : 1u << r;
+      clause_xor[c] = (rev_mask >> c) & 1u ? ~0u : 0u;
+      clause_or[c] = inactive;
+    }
+  }
+  // every (row, clause) value of the fast rows sets its row's bit
+  for (int rc = threadIdx.x; rc < nrows * a.C; rc += kClauseThreads) {
+    const int r = rc / a.C;
+    const int c = rc - r * a.C;
+    const int64_t b = b0 + r;
+    if (a.small[b] == 0u) continue;
+    const int64_t* vals = a.qc + (b * a.C + c) * a.V;
+    const int n = a.nv[b * a.C + c];
+    for (int v = 0; v < n; ++v) atomicOr(&qm[c * kSetDomain + vals[v]], 1u << r);
+  }
+  __syncthreads();
+  const uint32_t slow = slow_rows;
+  const uint32_t fast = ~slow;
+
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kClauseThreads; base < a.N;
+       base += static_cast<int64_t>(gridDim.x) * kClauseThreads) {
+    const int64_t d = base + threadIdx.x;
+    const bool valid = d < a.N;
+    const int64_t wword = (d - lane) >> 6;
+    uint64_t am = ~0ull;
+    if constexpr (MODE == kClauseBits) {
+      if (a.and_mask != nullptr && lane < nrows && wword < a.W) {
+        am = a.and_mask[(b0 + lane) * a.and_words + wword];
+      }
+    }
+    const T* row = static_cast<const T*>(a.attrs) + (valid ? d : 0) * ca;
+    int64_t at[kRegAttrs];
+    uint32_t m = ~0u;
+    if constexpr (REG) {
+#pragma unroll
+      for (int i = 0; i < kRegAttrs; ++i) {
+        const int64_t x = static_cast<int64_t>(row[i < ca ? i : ca - 1]);
+        const int64_t keep = -static_cast<int64_t>(i < ca);
+        at[i] = (x & keep) | ~keep;
+      }
+#pragma unroll
+      for (int c = 0; c < kRegAttrs; ++c) {
+        if (c < a.C) {
+          const uint64_t x = static_cast<uint64_t>(at[c]);
+          const uint32_t h = x < static_cast<uint64_t>(kSetDomain) ? qm[c * kSetDomain + x] : 0u;
+          m &= (h ^ clause_xor[c]) | clause_or[c];
+        }
+      }
+    } else {
+      for (int c = 0; c < a.C; ++c) {
+        uint32_t h = 0u;
+        for (int j = 0; j < a.A; ++j) {
+          const uint64_t x = static_cast<uint64_t>(static_cast<int64_t>(row[c * a.A + j]));
+          h |= x < static_cast<uint64_t>(kSetDomain) ? qm[c * kSetDomain + x] : 0u;
+        }
+        m &= (h ^ clause_xor[c]) | clause_or[c];
+      }
+    }
+    m &= fast;
+    for (uint32_t rest = slow; rest != 0u; rest &= rest - 1u) {
+      const int r = __builtin_ctz(rest);
+      const bool pass = clause_pass<REG, T>(a, at, row, b0 + r, rev_mask, nullptr, row_active[r]);
+      m |= pass ? 1u << r : 0u;
+    }
+    if (!valid) m = 0u;
+
+    if constexpr (MODE == kClauseBits) {
+      // row r's word of this wave's 64 items, kept by lane r and stored by all rows at once
+      uint64_t mine = 0ull;
+      for (int r = 0; r < nrows; ++r) {
+        const uint64_t word = __builtin_bitreverse64(__ballot((m >> r) & 1u));
+        mine = lane == r ? word : mine;
+      }
+      if (lane < nrows && wword < a.W) {
+        static_cast<uint64_t*>(a.out)[(b0 + lane) * a.W + wword] = mine & am;
+      }
+    } else if (valid) {
+      for (int r = 0; r < nrows; ++r) {
+        const int64_t b = b0 + r;
+        const bool pass = (m >> r) & 1u;
+        if constexpr (MODE == kClauseBool) {
+          static_cast<uint8_t*>(a.out)[b * a.N + d] = pass ? 1 : 0;
+        } else {
+          static_cast<float*>(a.out)[b * a.N + d] = pass ? a.scores[b * a.N + d] : -INFINITY;
+        }
+      }
+    }
+  }
+}
+
+template <int MODE, class T>
 static void launch_clause(const ClauseArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.C * a.A <= kRegAttrs) {
-    clause_kernel<MODE, true><<<grid, kClauseThreads, 0, stream>>>(a);
+  if (a.C >= 1 && a.C <= kQmaskClauses) {
+    const size_t qlds = static_cast<size_t>(a.C) * kSetDomain * sizeof(uint32_t);
+    if (a.A == 1) {
+      clause_qmask_kernel<MODE, true, T><<<grid, kClauseThreads, qlds, stream>>>(a);
+    } else {
+      clause_qmask_kernel<MODE, false, T><<<grid, kClauseThreads, qlds, stream>>>(a);
+    }
+    return;
+  }
+  const size_t lds = static_cast<size_t>(a.rows_per_wg) * a.C * kSetWords * sizeof(uint64_t);
+  if (a.A == 1 && a.C <= kRegAttrs) {
+    clause_kernel<MODE, true, T><<<grid, kClauseThreads, lds, stream>>>(a);
   } else {
-    clause_kernel<MODE, false><<<grid, kClauseThreads, 0, stream>>>(a);
+    clause_kernel<MODE, false, T><<<grid, kClauseThreads, lds, stream>>>(a);
+  }
+}
+
+template <int MODE>
+static void launch_clause_typed(const ClauseArgs& a, int attr_bytes, dim3 grid,
+                                hipStream_t stream) {
+  if (attr_bytes == 2) {
+    launch_clause<MODE, int16_t>(a, grid, stream);
+  } else if (attr_bytes == 4) {
+    launch_clause<MODE, int32_t>(a, grid, stream);
+  } else {
+    launch_clause<MODE, int64_t>(a, grid, stream);
   }
 }
 
@@ -303,16 +556,39 @@ __global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
 
 using namespace rt;
 
-extern "C" int rt_clause_filter(const int64_t* item_attrs, int64_t N, int64_t C, int64_t A,
+struct ClauseWs {
+  size_t nv, qc, small, bitmaps, rev, total;
+};
+
+static ClauseWs clause_ws_parts(int64_t B, int64_t C, int64_t V) {
+  ClauseWs w;
+  w.nv = align_up(static_cast<size_t>(B) * sizeof(uint32_t), 256);
+  w.qc = w.nv + align_up(static_cast<size_t>(B * C) * sizeof(int32_t), 256);
+  w.small = w.qc + align_up(static_cast<size_t>(B * C * V) * sizeof(int64_t), 256);
+  w.bitmaps = w.small + align_up(static_cast<size_t>(B) * sizeof(uint32_t), 256);
+  w.rev = w.bitmaps + align_up(static_cast<size_t>(B * C) * kSetWords * sizeof(uint64_t), 256);
+  w.total = w.rev + 256;
+  return w;
+}
+
+extern "C" size_t rt_clause_filter_workspace(int64_t B, int64_t C, int64_t V) {
+  if (B <= 0 || C <= 0 || V <= 0) return 256;
+  return clause_ws_parts(B, C, V).total;
+}
+
+extern "C" int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t N, int64_t C,
+                                int64_t A,
                                 const int8_t* clause_is_reverse, const int64_t* query_values,
                                 int64_t B, int64_t V, int mode, const float* scores,
                                 const uint64_t* and_mask, int64_t and_mask_words, void* out,
-                                hipStream_t stream) {
+                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
   RT_CHECK_ARG(N >= 0 && B >= 0, "N and B must be >= 0");
   RT_CHECK_ARG(C >= 0 && C <= kMaxClauses, "C must be in [0, %d], got %lld", kMaxClauses,
                static_cast<long long>(C));
   RT_CHECK_ARG(A >= 0 && A <= 4096 && V >= 1 && V <= 4096, "A must be >= 0 and V >= 1");
   RT_CHECK_ARG(mode >= kClauseBits && mode <= kClauseScores, "mode must be 0, 1 or 2");
+  RT_CHECK_ARG(attr_bytes == 2 || attr_bytes == 4 || attr_bytes == 8,
+               "attr_bytes must be 2, 4 or 8 (int16, int32, int64 attributes)");
   RT_CHECK_ARG(mode != kClauseScores || scores != nullptr, "scores mode needs scores");
   RT_CHECK_ARG(and_mask == nullptr || and_mask_words >= cdiv(N, 64),
                "and_mask rows must have >= ceil(N/64) words");
@@ -335,22 +611,57 @@ extern "C" int rt_clause_filter(const int64_t* item_attrs, int64_t N, int64_t C,
   a.scores = scores;
   a.out = out;
   a.W = cdiv(N, 64);
-  const int64_t gx = cdiv(N, kClauseThreads);
-  RT_CHECK_ARG(gx < (int64_t{1} << 31), "N too large");
-  // enough workgroups to fill the device: split the rows when the items alone are too few
+  if (C > 0) {
+    const ClauseWs p = clause_ws_parts(B, C, V);
+    if (workspace_bytes < p.total) {
+      set_error("workspace too small: %zu < %zu", workspace_bytes, p.total);
+      return kWorkspaceTooSmall;
+    }
+    char* ws = static_cast<char*>(workspace);
+    a.active = reinterpret_cast<uint32_t*>(ws);
+    a.nv = reinterpret_cast<int32_t*>(ws + p.nv);
+    a.qc = reinterpret_cast<int64_t*>(ws + p.qc);
+    a.small = reinterpret_cast<uint32_t*>(ws + p.small);
+    a.bitmaps = reinterpret_cast<uint64_t*>(ws + p.bitmaps);
+    a.rev_mask = reinterpret_cast<uint32_t*>(ws + p.rev);
+    clause_prep_kernel<<<static_cast<unsigned>(cdiv(B, 64)), 64, 0, stream>>>(
+        query_values, B, static_cast<int>(C), static_cast<int>(V), clause_is_reverse,
+        const_cast<uint32_t*>(a.active), const_cast<int32_t*>(a.nv), const_cast<int64_t*>(a.qc),
+        const_cast<uint32_t*>(a.small), const_cast<uint64_t*>(a.bitmaps),
+        const_cast<uint32_t*>(a.rev_mask));
+    RT_CHECK_HIP(hipGetLastError());
+  }
+  // about 4096 workgroups in all, each looping over item chunks (the staging is amortized)
+  int64_t gx = cdiv(N, kClauseThreads);
+  gx = gx < 4096 ? gx : 4096;
+  // split the rows when the items alone give too few workgroups
   int64_t gy = cdiv(4096, gx);
   gy = gy < 1 ? 1 : gy;
   gy = gy > B ? B : gy;
   gy = gy > 65535 ? 65535 : gy;
   a.rows_per_wg = cdiv(B, gy);
+  // the rows' bitmaps staged per workgroup stay within kMaxBitmapLds
+  if (C > 0) {
+    const int64_t max_rows = kMaxBitmapLds / (C * kSetWords * static_cast<int64_t>(sizeof(uint64_t)));
+    a.rows_per_wg = a.rows_per_wg < max_rows ? a.rows_per_wg : max_rows;
+  }
+  // a wave's lanes carry the rows' words (bits mode) and the staged row flags
+  a.rows_per_wg = a.rows_per_wg < kWave ? a.rows_per_wg : kWave;
+  if (C >= 1 && C <= kQmaskClauses) {
+    // the query-mask form: 32 rows per workgroup, the table built once per workgroup
+    a.rows_per_wg = kQmaskRows;
+    gx = cdiv(N, kClauseThreads);
+    gx = gx < 2048 ? gx : 2048;
+  }
   gy = cdiv(B, a.rows_per_wg);
+  RT_CHECK_ARG(gy <= 65535, "too many query rows");
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
   if (mode == kClauseBits) {
-    launch_clause<kClauseBits>(a, grid, stream);
+    launch_clause_typed<kClauseBits>(a, attr_bytes, grid, stream);
   } else if (mode == kClauseBool) {
-    launch_clause<kClauseBool>(a, grid, stream);
+    launch_clause_typed<kClauseBool>(a, attr_bytes, grid, stream);
   } else {
-    launch_clause<kClauseScores>(a, grid, stream);
+    launch_clause_typed<kClauseScores>(a, attr_bytes, grid, stream);
   }
   RT_CHECK_HIP(hipGetLastError());
   return kOk;

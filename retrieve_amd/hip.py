@@ -270,6 +270,9 @@ __all__ = [
 _CLAUSE_BITS, _CLAUSE_BOOL, _CLAUSE_SCORES = 0, 1, 2
 
 
+_ATTR_DTYPES = (torch.int16, torch.int32, torch.int64)
+
+
 def _clause_prep(item_clause_attrs: Tensor, clause_is_reverse: Tensor, query_values: Tensor,
                  *, sets: bool = False):
     """The checks of ``ops/triton/clause_mask.py:158-181``: ``[N, C, A_max]`` items (contiguous),
@@ -281,8 +284,12 @@ def _clause_prep(item_clause_attrs: Tensor, clause_is_reverse: Tensor, query_val
     n, c, _ = item_clause_attrs.shape
     if query_values.shape[1] != c:
         raise ValueError(f"clause-count mismatch: items C={c}, query C={query_values.shape[1]}")
-    if item_clause_attrs.dtype != torch.int64 or query_values.dtype != torch.int64:
-        raise TypeError("item_clause_attrs and query_clause_attrs must be int64")
+    # the reference ops take int64 tables; the packed-bits form also takes int16 / int32 ones
+    attr_ok = item_clause_attrs.dtype in _ATTR_DTYPES if sets else \
+        item_clause_attrs.dtype == torch.int64
+    if not attr_ok or query_values.dtype != torch.int64:
+        raise TypeError("item_clause_attrs must be int64 (int16 / int32 also for clause_bits) "
+                        "and query values int64")
     if clause_is_reverse.shape != (c,):
         raise ValueError(f"clause_is_reverse must be [C] = [{c}]")
     if c > 32:
@@ -302,11 +309,14 @@ def _clause_filter(item_clause_attrs: Tensor, rev: Tensor, q: Tensor, mode: int,
     if b == 0 or n == 0:
         return
     dev = nat.require_device(item_clause_attrs, q, rev, out)
+    lib = nat.lib()
+    ws = nat.workspace(lib.rt_clause_filter_workspace(b, c, v), dev)
     with torch.cuda.device(dev):
-        st = nat.lib().rt_clause_filter(
-            nat.ptr(item_clause_attrs), n, c, a, nat.ptr(rev), nat.ptr(q), b, v, mode,
+        st = lib.rt_clause_filter(
+            nat.ptr(item_clause_attrs), item_clause_attrs.element_size(), n, c, a, nat.ptr(rev),
+            nat.ptr(q), b, v, mode,
             nat.ptr(scores), nat.ptr(and_mask), 0 if and_mask is None else and_mask.shape[1],
-            nat.ptr(out), nat.stream(dev),
+            nat.ptr(out), nat.ptr(ws), ws.numel(), nat.stream(dev),
         )
     nat.check(st)
 
@@ -365,7 +375,7 @@ def clause_bits(
     at bit ``63 - d % 64`` (the order of ``silvertorch/.../ops/official/__init__.py:33-35``).
     ``query_values`` is ``[B, C]`` (the reference predicate) or ``[B, C, V]`` value sets, ``-1``
     pads: clause ``c`` is active iff a value is not ``-1`` and matches iff an item value is in
-    the set. ``and_mask`` (``[B, >= ceil(N/64)]`` words, same bit layout) is AND-ed in, e.g. a
+    the set. ``item_clause_attrs`` may be int16 / int32 (a compact copy of the table). ``and_mask`` (``[B, >= ceil(N/64)]`` words, same bit layout) is AND-ed in, e.g. a
     Bloom search's ``[B, n_bundles * 32]`` pre-filter."""
     rev, q = _clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
     b, n = q.shape[0], item_clause_attrs.shape[0]

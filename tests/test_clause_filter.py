@@ -192,3 +192,56 @@ def test_errors(dev):
         torch.ops.retrieve.clause_mask(attrs.int(), rev, q)
     with pytest.raises(ValueError):
         torch.ops.retrieve.clause_mask_scores(torch.zeros(3, 9, device=dev), attrs, rev, q)
+
+
+@pytest.mark.parametrize("dtype", [np.int16, np.int32])
+def test_compact_attr_tables(dev, dtype):
+    """``clause_bits`` over an int16 / int32 copy of the table equals the int64 oracle."""
+    g = rng(58)
+    n, c = 70_000, 8
+    attrs = _attrs(g, n, c, 1, 1000, 0.1)
+    sets = g.integers(0, 1000, (5, c, 3), dtype=np.int64)
+    sets[g.random(sets.shape) < 0.6] = -1
+    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs.astype(dtype)),
+                                          _t(dev, np.zeros(c, bool)), _t(dev, sets))
+    assert np.array_equal(bits.cpu().numpy(), _pack(of.clause_match_sets(attrs, sets)))
+    with pytest.raises(TypeError):
+        torch.ops.retrieve.clause_mask(_t(dev, attrs.astype(dtype)), _t(dev, np.zeros(c, bool)),
+                                       _t(dev, sets[:, :, 0]))
+
+
+def test_large_and_negative_values(dev):
+    """Rows whose values fall outside [0, 1024) walk their value lists; the others test bitmaps;
+    item values outside the bitmap domain never match a bitmap row."""
+    g = rng(59)
+    n, c = 40_000, 4
+    attrs = g.integers(-5, 3000, (n, c, 2), dtype=np.int64)
+    attrs[:, :, 1] = g.integers(0, 40, (n, c))  # small values too
+    sets = g.integers(0, 40, (8, c, 3), dtype=np.int64)
+    sets[g.random(sets.shape) < 0.5] = -1
+    sets[1, 0, 0] = 2500  # list rows
+    sets[5, 2, 1] = -4
+    rev = np.array([0, 1, 0, 0], bool)
+    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, sets))
+    assert np.array_equal(bits.cpu().numpy(), _pack(of.clause_match_sets(attrs, sets, rev)))
+
+
+@pytest.mark.parametrize("c,a", [(8, 1), (3, 3), (18, 1)])
+def test_row_groups_mixed_rows(dev, c, a):
+    """More than 32 query rows (several row groups, the last partial), list rows among the
+    bitmap rows, reverse clauses and an AND mask; C above 16 takes the per-row bitmap form."""
+    g = rng(60 + c + a)
+    n, b = 30_001, 45
+    attrs = g.integers(-3, 60, (n, c, a), dtype=np.int64)
+    sets = g.integers(0, 60, (b, c, 2), dtype=np.int64)
+    sets[g.random(sets.shape) < 0.5] = -1
+    sets[[2, 33, 40], 0, 0] = [5000, -7, 1024]  # list rows in two groups
+    sets[10] = -1  # every clause inactive
+    rev = (np.arange(c) % 3 == 1)
+    want = of.clause_match_sets(attrs, sets, rev)
+    pre = g.random((b, n)) < 0.7
+    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, sets),
+                                          _t(dev, _pack(pre)))
+    assert np.array_equal(bits.cpu().numpy(), _pack(want & pre))
+    m = torch.ops.retrieve.clause_mask(_t(dev, attrs), _t(dev, rev), _t(dev, sets[:, :, 0]))
+    assert np.array_equal(m.cpu().numpy(), of.clause_match(attrs, rev, sets[:, :, 0]))

@@ -186,6 +186,14 @@ def test_clause_sets_reduce_to_singletons():
     # an item value of -1 never matches a set, while clause_match compares -1 == -1 only
     # for inactive clauses (skipped), so the two agree
     assert np.array_equal(got, of.clause_match(attrs, np.zeros(4, bool), q))
+    rev = np.array([True, False, True, False])
+    assert np.array_equal(of.clause_match_sets(attrs, q[:, :, None], rev),
+                          of.clause_match(attrs, rev, q))
+    # a set is the OR of its singletons: two-value sets against a by-hand union
+    two = g.integers(0, 5, (9, 4, 2))
+    two[:, 1:, :] = -1  # only clause 0 active
+    union = of.clause_match_sets(attrs, two[:, :, :1]) | of.clause_match_sets(attrs, two[:, :, 1:])
+    assert np.array_equal(of.clause_match_sets(attrs, two), union)
 
 
 def test_murmur_smhasher_verification(kat):
