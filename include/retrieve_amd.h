@@ -153,7 +153,7 @@ int rt_bloom_build(const int32_t* feature_ids, int64_t C, const int64_t* feature
  * plan yields no match. 1 <= k <= 10, 1 <= max_stack <= 64.
  * Replaces: st::bloom_index_search_batch(_prepared)
  *   (silvertorch/.../bloom_index_search.cpp:551-590, bloom_index_search_cuda.cu:1829-1856). */
-size_t rt_bloom_search_workspace(int64_t data_bytes);
+size_t rt_bloom_search_workspace(int64_t data_bytes, int64_t plan_count);
 int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, int64_t n_bundles,
                     const int64_t* plan_offsets, const int8_t* plan_data, int64_t data_bytes,
                     int64_t plan_count, int64_t max_stack, int64_t k, int64_t hash_k,

@@ -55,7 +55,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rt_bloom_build": (
         _c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p],
     ),
-    "rt_bloom_search_workspace": (_c_sz, [_c_i64]),
+    "rt_bloom_search_workspace": (_c_sz, [_c_i64, _c_i64]),
     "rt_bloom_search": (
         _c_int,
         [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,

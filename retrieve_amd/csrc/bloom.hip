@@ -177,10 +177,11 @@ struct BloomSearchArgs {
   int max_stack;
   int k;
   int hash_k;
-  const int32_t* resolved;  // [data_bytes / 8] positions parallel to the hash words, or null
-  const int32_t* uniform;   // [1]: 1 iff every bundle has the same width (resolve pass)
-  int64_t* out_mask;        // [plan_count, nb * 32] or null
-  uint8_t* out_bool;        // [plan_count, nb * 32 * 64] or null
+  bool words_aligned16;
+  const int32_t* hdr;    // [plan_count, 4] from the prep pass: PlanStatus, ops, hash word 0
+  const uint32_t* prog;   // [plan_count, kProgMaxOps, 2] program words
+  int64_t* out_mask;      // [plan_count, nb * 32] or null
+  uint8_t* out_bool;      // [plan_count, nb * 32 * 64] or null
 };
 
 // The first k distinct hash % w among a term's stored hashes (fewer if they do not hold k).
@@ -206,42 +207,521 @@ __device__ inline bool plan_ok(const int64_t* o, int64_t data_bytes) {
   return ok && (o[2] % 4) == 0 && (o[4] % 4) == 0 && (o[6] % 8) == 0;
 }
 
-// One workgroup: whether all bundles share a width, and if so every term's positions for it
-// (resolved[hash word index of the term's first hash + i], -1 past the distinct ones).
-__global__ void __launch_bounds__(kBloomThreads) bloom_resolve_kernel(BloomSearchArgs a,
-                                                                      int32_t* resolved,
-                                                                      int32_t* uniform) {
-  __shared__ int all_same;
-  if (threadIdx.x == 0) all_same = 1;
-  __syncthreads();
-  const int64_t w0 = a.bundle_off[1] - a.bundle_off[0];
-  for (int64_t beta = threadIdx.x; beta < a.nb; beta += kBloomThreads) {
-    if (a.bundle_off[beta + 1] - a.bundle_off[beta] != w0) all_same = 0;
+// One plan's result word for this lane's column, in the mask layout and/or as 64 bytes.
+__device__ inline void write_column(const BloomSearchArgs& a, int64_t b, int64_t ncol,
+                                    int64_t col, uint64_t res) {
+  // through global-address-space views: counted in vmcnt only (flat stores also hold lgkmcnt,
+  // which the evaluation's LDS waits would then wait on)
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(1))) int64_t gi64;
+  typedef __attribute__((address_space(1))) u32x4 gu4;
+  if (a.out_mask != nullptr) {
+    gi64* om = (gi64*)(a.out_mask);
+    om[b * ncol + col] = static_cast<int64_t>(res);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) uniform[0] = all_same;
-  if (!all_same || w0 <= 0) return;
-  const int kk = a.k < a.hash_k ? a.k : a.hash_k;  // positions a term can resolve
-  for (int64_t b = threadIdx.x; b < a.plan_count; b += kBloomThreads) {
-    const int64_t* o = a.plan_offsets + 8 * b;
-    if (!plan_ok(o, a.data_bytes)) continue;
-    const int64_t h0 = o[6] / 8;
-    const int64_t nh = (o[7] - o[6]) / 8;
-    const uint64_t* hashes = reinterpret_cast<const uint64_t*>(a.data) + h0;
-    for (int64_t t = 0; (t + 1) * a.hash_k <= nh; ++t) {
-      uint32_t pos[kBloomMaxK];
-      const int got = resolve_positions(hashes + t * a.hash_k, a.hash_k, a.k,
-                                        static_cast<uint64_t>(w0), pos);
-      for (int i = 0; i < kk; ++i) {
-        resolved[h0 + t * a.hash_k + i] = i < got ? static_cast<int32_t>(pos[i]) : -1;
+  if (a.out_bool != nullptr) {
+    // 64 bytes per column, doc 64 col + q at byte q (bit 63 - q of the word)
+    gu4* ob = (gu4*)(a.out_bool + (b * ncol + col) * 64);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      u32x4 x;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        uint32_t y = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int q = 16 * v + 4 * u + t;
+          y |= static_cast<uint32_t>((res >> (63 - q)) & 1ull) << (8 * t);
+        }
+        x[u] = y;
       }
+      ob[v] = x;
     }
   }
 }
 
+// ---- plan prep: a program for the column kernel ----------------------------------------
+//
+// Post-order evaluation pushes every child of an n-ary AND / OR before the operator pops them,
+// so an OR of 30 terms needs 30 stack slots. Folding a node's value into its previous sibling
+// as soon as it is complete (AND / OR are associative and commutative) gives the same result
+// with at most one slot per tree level. The prep pass checks each plan exactly as the stack
+// evaluation does (a malformed plan matches nothing), marks every node "push" (a first child,
+// or the root) or "fold into the top with the parent's operator", and writes two program words
+// per op. A TERM's positions p (for the width of bundle 0) are stored as the byte offsets
+// p * 256 of their words in a staged bundle column, 14 bits each, the first repeated past the
+// term's distinct positions (AND is idempotent):
+//   word 0: bits 0-1 kind: TERM, EMPTY, PASS (an AND / OR whose children are folded into the
+//           top: pop it), NOT (pop, invert); bits 2-3 place: push, AND into the top, OR into
+//           the top; bits 4-17 offset 0; bits 18-31 offset 1
+//   word 1: bits 0-13 offset 2; bits 16-29 offset 3
+// Plans the program cannot hold (more than kFoldDepth levels, more than 4 positions a term,
+// bundle 0 wider than 64 bits, more than kProgMaxOps ops) are left to the stack evaluation.
+constexpr int kFoldDepth = 4;
+constexpr int kProgMaxPos = 4;
+constexpr int kColMaxWidth = 64;
+constexpr int kProgMaxOps = 512;
+constexpr int kPrepThreads = 256;
+constexpr uint32_t kColPosBytes = kBloomWordsPerBundle * sizeof(uint64_t);  // 256
+
+enum PlanStatus : int32_t { kPlanProgram = 0, kPlanNone = 1, kPlanStack = 2 };
+
+// A plan's header: its status, op count and first hash word, one 16-byte load for the column
+// kernel (whose program slot sits at a fixed place, so nothing waits on the plan's offsets).
+__device__ inline void write_header(int32_t* hdr, int64_t b, int32_t status, int32_t n_ops,
+                                    int64_t h0) {
+  int32_t* h = hdr + 4 * b;
+  h[0] = status;
+  h[1] = n_ops;
+  h[2] = static_cast<int32_t>(h0);
+  h[3] = static_cast<int32_t>(h0 >> 32);
+}
+enum ProgKind : uint32_t { kKindTerm = 0, kKindEmpty = 1, kKindPass = 2, kKindNot = 3 };
+enum ProgPlace : uint32_t { kPlacePush = 0, kPlaceAnd = 1, kPlaceOr = 2 };
+
+__global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArgs a,
+                                                                  int32_t* hdr,
+                                                                  uint32_t* prog) {
+  __shared__ uint8_t ops[kProgMaxOps];
+  __shared__ uint8_t place[kProgMaxOps];
+  __shared__ uint32_t term_pos[kProgMaxOps][2];  // the positions part of each term's words
+  __shared__ int32_t stk[kBloomMaxStack];
+  const int64_t b = blockIdx.x;
+  const int64_t* o = a.plan_offsets + 8 * b;
+  const int tid = threadIdx.x;
+  if (!plan_ok(o, a.data_bytes)) {
+    if (tid == 0) write_header(hdr, b, kPlanNone, 0, 0);
+    return;
+  }
+  const int64_t n_ops = o[1] - o[0];
+  const int64_t nh = (o[7] - o[6]) / 8;
+  const int64_t n_terms = nh / a.hash_k;
+  const int64_t w0 = a.bundle_off[1] - a.bundle_off[0];
+  const int kk = a.k < a.hash_k ? a.k : a.hash_k;
+  if (n_ops > kProgMaxOps || w0 < 1 || w0 > kColMaxWidth || kk > kProgMaxPos) {
+    if (tid == 0) write_header(hdr, b, kPlanStack, 0, 0);
+    return;
+  }
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(a.data + o[0]);
+  for (int64_t i = tid; i < n_ops; i += kPrepThreads) {
+    ops[i] = src[i];
+    place[i] = kPlacePush;
+  }
+  const uint64_t* hashes = reinterpret_cast<const uint64_t*>(a.data) + o[6] / 8;
+  // a valid plan uses at most n_ops terms (each is an op)
+  const int64_t used_terms = n_terms < n_ops ? n_terms : n_ops;
+  for (int64_t t = tid; t < used_terms; t += kPrepThreads) {
+    uint32_t pos[kBloomMaxK];
+    const int got = resolve_positions(hashes + t * a.hash_k, a.hash_k, a.k,
+                                      static_cast<uint64_t>(w0), pos);
+    uint32_t off[kProgMaxPos];
+    for (int q = 0; q < kProgMaxPos; ++q) off[q] = pos[q < got ? q : 0] * kColPosBytes;
+    term_pos[t][0] = (off[0] << 4) | (off[1] << 18);
+    term_pos[t][1] = off[2] | (off[3] << 16);
+  }
+  __syncthreads();
+  if (tid != 0) return;
+
+  // the stack evaluation's checks, recording each node's place
+  const int32_t* offs = reinterpret_cast<const int32_t*>(a.data + o[2]);
+  const int64_t n_offs = (o[3] - o[2]) / 4;
+  bool bad = false;
+  int sp = 0;
+  int64_t term = 0;
+  for (int64_t i = 0; i < n_ops && !bad; ++i) {
+    const uint8_t op = ops[i];
+    if (op == kOpTerm) {
+      if ((term + 1) * a.hash_k > nh) {
+        bad = true;
+        break;
+      }
+      ++term;
+    } else if (op == kOpAnd || op == kOpOr) {
+      if (i + 1 >= n_offs) {
+        bad = true;
+        break;
+      }
+      const int n = offs[i + 1] - offs[i];
+      if (n < 1 || n > sp) {
+        bad = true;
+        break;
+      }
+      for (int q = sp - n + 1; q < sp; ++q) place[stk[q]] = op == kOpAnd ? kPlaceAnd : kPlaceOr;
+      sp -= n;
+    } else if (op == kOpNot) {
+      if (sp < 1) {
+        bad = true;
+        break;
+      }
+      sp -= 1;
+    } else if (op != kOpEmpty) {
+      bad = true;
+      break;
+    }
+    if (sp >= a.max_stack) {
+      bad = true;
+      break;
+    }
+    stk[sp++] = static_cast<int32_t>(i);
+  }
+  if (bad || sp != 1) {
+    write_header(hdr, b, kPlanNone, 0, 0);
+    return;
+  }
+  // the folded evaluation's depth, and the program
+  int depth = 0;
+  int deepest = 0;
+  term = 0;
+  uint32_t* out = prog + b * kProgMaxOps * 2;
+  for (int64_t i = 0; i < n_ops; ++i) {
+    const uint8_t op = ops[i];
+    uint32_t w0 = 0u;
+    uint32_t w1 = 0u;
+    if (op == kOpTerm) {
+      w0 = kKindTerm | term_pos[term][0];
+      w1 = term_pos[term][1];
+      ++term;
+    } else if (op == kOpEmpty) {
+      w0 = kKindEmpty;
+    } else {
+      w0 = op == kOpNot ? kKindNot : kKindPass;
+      --depth;
+    }
+    if (place[i] == kPlacePush) {
+      ++depth;
+      deepest = depth > deepest ? depth : deepest;
+    }
+    out[2 * i] = w0 | (static_cast<uint32_t>(place[i]) << 2);
+    out[2 * i + 1] = w1;
+  }
+  write_header(hdr, b, deepest <= kFoldDepth ? kPlanProgram : kPlanStack,
+               static_cast<int32_t>(n_ops), o[6] / 8);
+}
+
+// ---- column kernel: programs over LDS-staged bundles -------------------------------------
+//
+// A workgroup stages two bundles (64 columns, 2 * 64 * 32 words = 32 KiB at 64 bits per doc)
+// in LDS once; its four waves then run the programs of its plans (wave w: plans w, w + 4, ...),
+// lane <-> column, the top of the folded stack in a register and the levels below it in LDS.
+// Every index word leaves HBM once per workgroup. Lanes of a bundle whose width differs from
+// bundle 0's resolve their positions from the stored hashes and read HBM.
+constexpr int kColThreads = 256;
+constexpr int kColWaves = kColThreads / kWave;
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// A term from its stored hashes for a bundle of width w (any width the build allows): the AND of
+// the words at the first k distinct hash % w. Duplicates are found in a bitmask of the positions
+// taken, so nothing here needs an indexed array (or a private stack).
+__device__ inline uint64_t term_from_hashes(const BloomSearchArgs& a, int64_t h0, int64_t term,
+                                            const uint64_t* wcol, int64_t w) {
+  if (w <= 0) return 0ull;  // a bundle with no bits holds no term
+  const uint64_t* h = reinterpret_cast<const uint64_t*>(a.data) + h0 + term * a.hash_k;
+  uint64_t seen[kBloomMaxBuildWidth / 64] = {0ull, 0ull, 0ull, 0ull};
+  uint64_t r = ~0ull;
+  int got = 0;
+  for (int s = 0; s < a.hash_k && got < a.k; ++s) {
+    const uint32_t p = static_cast<uint32_t>(h[s] % static_cast<uint64_t>(w));
+    const uint64_t bit = 1ull << (p & 63u);
+    uint64_t taken = 0ull;
+#pragma unroll
+    for (int q = 0; q < kBloomMaxBuildWidth / 64; ++q) taken |= (p >> 6) == q ? seen[q] & bit : 0;
+    if (taken == 0ull) {
+#pragma unroll
+      for (int q = 0; q < kBloomMaxBuildWidth / 64; ++q) seen[q] |= (p >> 6) == q ? bit : 0ull;
+      r &= wcol[static_cast<int64_t>(p) * kBloomWordsPerBundle];
+      ++got;
+    }
+  }
+  return r;
+}
+
+// A value every lane holds alike, moved to scalar registers.
+__device__ inline int64_t uniform64(int64_t x) {
+  const uint64_t u = static_cast<uint64_t>(x);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Global-memory views (address space 1, reached by C-style casts): loads and stores through them
+// count in vmcnt only, not also in lgkmcnt as flat accesses do, so LDS waits do not wait for
+// them.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const uint32_t gu32;
+typedef __attribute__((address_space(1))) const i32x4 gi32x4;
+
+// The staged column word at byte offset q (a position's p * 256).
+__device__ inline uint64_t column_word(const char* lcol, uint32_t q) {
+  return *reinterpret_cast<const uint64_t*>(lcol + q);
+}
+
+// AND of a term's KK position words from the staged column (the loads issue back to back).
+template <int KK>
+__device__ inline uint64_t staged_term(const char* lcol, uint32_t w0, uint32_t w1) {
+  uint64_t v = column_word(lcol, (w0 >> 4) & 0x3fffu);
+  if constexpr (KK > 1) v &= column_word(lcol, w0 >> 18);
+  if constexpr (KK > 2) v &= column_word(lcol, w1 & 0x3fffu);
+  if constexpr (KK > 3) v &= column_word(lcol, w1 >> 16);
+  return v;
+}
+
+// The folded stack machine's state over one plan.
+struct FoldState {
+  uint64_t top;
+  int sp;
+  int64_t term;
+};
+
+// Ops li = 0 .. cnt-1 of a chunk whose words lane li holds (lo, hi): no memory access but LDS.
+// STAGED: every lane's bundle is in LDS (the wave takes no per-lane branch); otherwise lanes
+// whose bundle is not staged resolve positions from the stored hashes.
+//
+// Runs: a TERM followed by TERMs that fold into the top with one operator P (OR or AND) are
+// siblings under a P node (a folding TERM's previous sibling is the op just before it), so the
+// first one's place is push or P. The run is evaluated as v = T0 P T1 P ... and placed once,
+// in a loop with no per-op dispatch; its length comes from a ballot over the chunk's words.
+template <int KK, bool STAGED>
+__device__ inline void run_ops(FoldState& f, uint32_t lo, uint32_t hi, int cnt,
+                               const BloomSearchArgs& a, int64_t h0, const char* lcol,
+                               bool mine_staged, const uint64_t* wcol, int64_t my_w,
+                               uint64_t (&stk)[kFoldDepth - 1][kWave], int lane) {
+  auto term_at = [&](int li) -> uint64_t {
+    const uint32_t w0 = __builtin_amdgcn_readlane(lo, li);
+    const uint32_t w1 = __builtin_amdgcn_readlane(hi, li);
+    uint64_t v;
+    if (STAGED || mine_staged) {
+      v = staged_term<KK>(lcol, w0, w1);
+    } else {
+      v = term_from_hashes(a, h0, f.term, wcol, my_w);
+    }
+    ++f.term;
+    return v;
+  };
+  const bool in_chunk = lane < cnt;
+  const bool is_term = (lo & 3u) == kKindTerm;
+  const uint64_t or_run = __ballot(in_chunk && is_term && ((lo >> 2) & 3u) == kPlaceOr);
+  const uint64_t and_run = __ballot(in_chunk && is_term && ((lo >> 2) & 3u) == kPlaceAnd);
+  for (int li = 0; li < cnt;) {
+    const uint32_t w0 = __builtin_amdgcn_readlane(lo, li);
+    const uint32_t kind = w0 & 3u;
+    uint64_t v;
+    if (kind == kKindTerm) {
+      v = term_at(li);
+      // the run's continuation: ops li + 1, li + 2, ... that fold with one operator
+      const uint64_t ors = li + 1 < kWave ? or_run >> (li + 1) : 0ull;
+      const uint64_t ands = li + 1 < kWave ? and_run >> (li + 1) : 0ull;
+      const int n_or = static_cast<int>(__builtin_ctzll(~ors));
+      const int n_and = static_cast<int>(__builtin_ctzll(~ands));
+      int j = li + 1;
+      if (n_or > 0) {
+        const int end = j + n_or;
+        for (; j + 1 < end; j += 2) {
+          const uint64_t x = term_at(j);
+          const uint64_t y = term_at(j + 1);
+          v |= x | y;
+        }
+        if (j < end) v |= term_at(j++);
+      } else if (n_and > 0) {
+        const int end = j + n_and;
+        for (; j + 1 < end; j += 2) {
+          const uint64_t x = term_at(j);
+          const uint64_t y = term_at(j + 1);
+          v &= x & y;
+        }
+        if (j < end) v &= term_at(j++);
+      }
+      li = j;
+    } else {
+      if (kind == kKindEmpty) {
+        v = ~0ull;
+      } else {
+        v = kind == kKindNot ? ~f.top : f.top;
+        --f.sp;
+        if (f.sp >= 1) f.top = stk[f.sp - 1][lane];
+      }
+      ++li;
+    }
+    const uint32_t where = (w0 >> 2) & 3u;
+    if (where == kPlaceOr) {
+      f.top |= v;
+    } else if (where == kPlaceAnd) {
+      f.top &= v;
+    } else {
+      if (f.sp >= 1) stk[f.sp - 1][lane] = f.top;
+      f.top = v;
+      ++f.sp;
+    }
+  }
+}
+
+// One plan: its first 64 ops from the prefetched words (lo0, hi0), any further ones loaded here.
+template <int KK, bool STAGED>
+__device__ inline uint64_t run_program(const BloomSearchArgs& a, gu32* prog, uint32_t lo0,
+                                       uint32_t hi0, int n_ops, int64_t h0, const char* lcol,
+                                       bool mine_staged, const uint64_t* wcol, int64_t my_w,
+                                       uint64_t (&stk)[kFoldDepth - 1][kWave], int lane) {
+  FoldState f{0ull, 0, 0};
+  run_ops<KK, STAGED>(f, lo0, hi0, n_ops < kWave ? n_ops : kWave, a, h0, lcol, mine_staged,
+                      wcol, my_w, stk, lane);
+  for (int c0 = kWave; c0 < n_ops; c0 += kWave) {
+    const int cnt = n_ops - c0 < kWave ? n_ops - c0 : kWave;
+    const uint32_t lo = prog[2 * (c0 + lane)];
+    const uint32_t hi = prog[2 * (c0 + lane) + 1];
+    run_ops<KK, STAGED>(f, lo, hi, cnt, a, h0, lcol, mine_staged, wcol, my_w, stk, lane);
+  }
+  return f.top;
+}
+
+// KK = min(k, hash_k): the positions every term's program words carry.
+template <int KK>
+__global__ void __launch_bounds__(kColThreads) bloom_column_kernel(BloomSearchArgs a) {
+  __shared__ uint64_t idx[2 * kColMaxWidth * kBloomWordsPerBundle];
+  __shared__ uint64_t fold[kColWaves][kFoldDepth - 1][kWave];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int64_t beta0 = static_cast<int64_t>(blockIdx.x) * 2;
+  const int64_t w0 = uniform64(a.bundle_off[1] - a.bundle_off[0]);
+  // the two bundles: staged when their width is bundle 0's (the programs' positions)
+  int64_t off[3];
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+    off[h] = beta0 + h <= a.nb ? uniform64(a.bundle_off[beta0 + h]) : 0;
+  }
+  bool staged[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    staged[h] = beta0 + h < a.nb && off[h + 1] - off[h] == w0 && w0 >= 1 && w0 <= kColMaxWidth;
+  }
+  {
+    // every load of both bundles in flight before the first LDS store: 16 bytes a load when
+    // the index is 16-byte aligned (a bundle starts at a multiple of 256 bytes from it)
+    const int n = static_cast<int>(w0) * kBloomWordsPerBundle;  // words per bundle
+    if (a.words_aligned16) {
+      constexpr int kIt = kColMaxWidth * kBloomWordsPerBundle / 2 / kColThreads;
+      v4u r[2][kIt];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const v4u* g = reinterpret_cast<const v4u*>(a.words + off[h] * kBloomWordsPerBundle);
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+          const int i = tid + it * kColThreads;
+          r[h][it] = staged[h] && 2 * i < n ? __builtin_nontemporal_load(g + i) : v4u{0, 0, 0, 0};
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        v4u* l = reinterpret_cast<v4u*>(idx + h * kColMaxWidth * kBloomWordsPerBundle);
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+          const int i = tid + it * kColThreads;
+          if (staged[h] && 2 * i < n) l[i] = r[h][it];
+        }
+      }
+    } else {
+      constexpr int kIt = kColMaxWidth * kBloomWordsPerBundle / kColThreads;
+      uint64_t r[2][kIt];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint64_t* g = a.words + off[h] * kBloomWordsPerBundle;
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+          const int i = tid + it * kColThreads;
+          r[h][it] = staged[h] && i < n ? __builtin_nontemporal_load(g + i) : 0ull;
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint64_t* l = idx + h * kColMaxWidth * kBloomWordsPerBundle;
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+          const int i = tid + it * kColThreads;
+          if (staged[h] && i < n) l[i] = r[h][it];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const int half = lane >> 5;
+  const int j = lane & 31;
+  const int64_t col = beta0 * kBloomWordsPerBundle + lane;
+  const int64_t ncol = a.nb * kBloomWordsPerBundle;
+  const bool valid = beta0 + half < a.nb;
+  const bool mine_staged = half == 0 ? staged[0] : staged[1];
+  // wave-uniform: both bundles staged (or the second absent)
+  const bool all_staged =
+      __builtin_amdgcn_readfirstlane(staged[0] && (staged[1] || beta0 + 1 >= a.nb)) != 0;
+  const char* lcol =
+      reinterpret_cast<const char*>(idx + half * kColMaxWidth * kBloomWordsPerBundle + j);
+  const int64_t my_off = half == 0 ? off[0] : off[1];
+  const int64_t my_w = valid ? (half == 0 ? off[1] - off[0] : off[2] - off[1]) : 0;
+  const uint64_t* wcol = a.words + my_off * kBloomWordsPerBundle + j;
+  uint64_t(&stk)[kFoldDepth - 1][kWave] = fold[wave];
+
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * a.plans_per_wg;
+  const int64_t b1 = b0 + a.plans_per_wg < a.plan_count ? b0 + a.plans_per_wg : a.plan_count;
+  // each plan's header and first 64 program ops are loaded while the plan before it runs (a
+  // plan's slot holds kProgMaxOps >= 64 ops, so the loads stay inside it)
+  gu32* progs = (gu32*)(a.prog);
+  gi32x4* hdrs = (gi32x4*)(a.hdr);
+  int64_t b = b0 + wave;
+  i32x4 h_next = {0, 0, 0, 0};
+  uint32_t lo_next = 0u;
+  uint32_t hi_next = 0u;
+  if (b < b1) {
+    h_next = hdrs[b];
+    lo_next = progs[b * kProgMaxOps * 2 + 2 * lane];
+    hi_next = progs[b * kProgMaxOps * 2 + 2 * lane + 1];
+  }
+  for (; b < b1; b += kColWaves) {
+    const i32x4 h = h_next;
+    const uint32_t lo = lo_next;
+    const uint32_t hi = hi_next;
+    // wait for this plan's words here, before the next plan's loads are issued: the waits the
+    // compiler would place inside the op loop also cover those newer loads
+    asm volatile("" ::"v"(h), "v"(lo), "v"(hi));
+    if (b + kColWaves < b1) {
+      const int64_t nb = b + kColWaves;
+      h_next = hdrs[nb];
+      lo_next = progs[nb * kProgMaxOps * 2 + 2 * lane];
+      hi_next = progs[nb * kProgMaxOps * 2 + 2 * lane + 1];
+    }
+    const int32_t st = __builtin_amdgcn_readfirstlane(h[0]);
+    if (st == kPlanStack) continue;  // the stack evaluation writes it
+    uint64_t top = 0ull;
+    if (st == kPlanProgram) {
+      gu32* prog = progs + b * kProgMaxOps * 2;
+      const int n_ops = __builtin_amdgcn_readfirstlane(h[1]);  // <= kProgMaxOps
+      const int64_t h0 = static_cast<int64_t>(
+          (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(h[3])))
+           << 32) |
+          static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(h[2])));
+      if (all_staged) {
+        top = run_program<KK, true>(a, prog, lo, hi, n_ops, h0, lcol, true, wcol, my_w, stk,
+                                    lane);
+      } else {
+        top = run_program<KK, false>(a, prog, lo, hi, n_ops, h0, lcol, mine_staged, wcol, my_w,
+                                     stk, lane);
+      }
+    }
+    if (valid) write_column(a, b, ncol, col, top);
+  }
+}
+
+// ---- stack evaluation: the plans the program cannot hold --------------------------------
+//
+// Lane <-> column, the evaluation stack in LDS ([max_stack][256] words), positions resolved
+// from the stored hashes per column.
 __global__ void __launch_bounds__(kBloomThreads) bloom_search_kernel(BloomSearchArgs a) {
   extern __shared__ uint64_t stk[];  // [max_stack][kBloomThreads]
   const int tid = threadIdx.x;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * a.plans_per_wg;
+  const int64_t b1 = b0 + a.plans_per_wg < a.plan_count ? b0 + a.plans_per_wg : a.plan_count;
+  // most launches have no plan for this kernel: leave before touching anything else
+  bool mine = false;
+  for (int64_t b = b0 + tid; b < b1; b += kBloomThreads) mine |= a.hdr[4 * b] == kPlanStack;
+  if (!__syncthreads_or(mine)) return;
   const int64_t ncol = a.nb * kBloomWordsPerBundle;
   const int64_t col = static_cast<int64_t>(blockIdx.x) * kBloomThreads + tid;
   const bool valid = col < ncol;
@@ -249,12 +729,10 @@ __global__ void __launch_bounds__(kBloomThreads) bloom_search_kernel(BloomSearch
   const int j = static_cast<int>(col % kBloomWordsPerBundle);
   const int64_t off = a.bundle_off[beta];
   const int64_t w = a.bundle_off[beta + 1] - off;
-  const bool uniform = a.uniform[0] != 0;
   const uint64_t* wcol = a.words + off * kBloomWordsPerBundle + j;  // position p at wcol[32 p]
 
-  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * a.plans_per_wg;
-  const int64_t b1 = b0 + a.plans_per_wg < a.plan_count ? b0 + a.plans_per_wg : a.plan_count;
   for (int64_t b = b0; b < b1; ++b) {
+    if (a.hdr[4 * b] != kPlanStack) continue;  // the column kernel writes it
     const int64_t* o = a.plan_offsets + 8 * b;
     // a malformed plan evaluates to no match instead of reading out of bounds
     bool bad = !plan_ok(o, a.data_bytes);
@@ -274,26 +752,7 @@ __global__ void __launch_bounds__(kBloomThreads) bloom_search_kernel(BloomSearch
           bad = true;
           break;
         }
-        if (w <= 0) {
-          r = 0ull;  // a bundle with no bits holds no term
-        } else if (uniform) {
-          r = ~0ull;
-          const int32_t* rp = a.resolved + h0 + term * a.hash_k;
-          const int kk = a.k < a.hash_k ? a.k : a.hash_k;
-          for (int q = 0; q < kk; ++q) {
-            const int32_t p = rp[q];
-            if (p < 0) break;
-            r &= wcol[static_cast<int64_t>(p) * kBloomWordsPerBundle];
-          }
-        } else {
-          r = ~0ull;
-          uint32_t pos[kBloomMaxK];
-          const uint64_t* h = reinterpret_cast<const uint64_t*>(a.data) + h0 + term * a.hash_k;
-          const int got = resolve_positions(h, a.hash_k, a.k, static_cast<uint64_t>(w), pos);
-          for (int q = 0; q < got; ++q) {
-            r &= wcol[static_cast<int64_t>(pos[q]) * kBloomWordsPerBundle];
-          }
-        }
+        r = term_from_hashes(a, h0, term, wcol, w);
         ++term;
       } else if (op == kOpAnd || op == kOpOr) {
         if (i + 1 >= n_offs) {
@@ -329,28 +788,7 @@ __global__ void __launch_bounds__(kBloomThreads) bloom_search_kernel(BloomSearch
       stk[(sp++) * kBloomThreads + tid] = r;
     }
     const uint64_t res = (!bad && sp == 1) ? stk[tid] : 0ull;
-    if (valid) {
-      if (a.out_mask != nullptr) a.out_mask[b * ncol + col] = static_cast<int64_t>(res);
-      if (a.out_bool != nullptr) {
-        // 64 bytes per column, doc 64 col + q at byte q (bit 63 - q of the word)
-        uint4* ob = reinterpret_cast<uint4*>(a.out_bool + (b * ncol + col) * 64);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          uint32_t x[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            uint32_t y = 0;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const int q = 16 * v + 4 * u + t;
-              y |= static_cast<uint32_t>((res >> (63 - q)) & 1ull) << (8 * t);
-            }
-            x[u] = y;
-          }
-          ob[v] = make_uint4(x[0], x[1], x[2], x[3]);
-        }
-      }
-    }
+    if (valid) write_column(a, b, ncol, col, res);
   }
 }
 
@@ -397,9 +835,11 @@ extern "C" int rt_bloom_build(const int32_t* feature_ids, int64_t C,
   return kOk;
 }
 
-extern "C" size_t rt_bloom_search_workspace(int64_t data_bytes) {
-  const int64_t words = data_bytes > 0 ? data_bytes / 8 : 0;
-  return 256 + align_up(static_cast<size_t>(words) * sizeof(int32_t), 256);
+extern "C" size_t rt_bloom_search_workspace(int64_t data_bytes, int64_t plan_count) {
+  (void)data_bytes;  // the programs are per plan
+  const int64_t plans = plan_count > 0 ? plan_count : 0;
+  return align_up(static_cast<size_t>(plans) * 16, 256) +
+         align_up(static_cast<size_t>(plans) * kProgMaxOps * 2 * sizeof(uint32_t), 256);
 }
 
 extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets,
@@ -418,12 +858,16 @@ extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_of
                static_cast<long long>(max_stack));
   RT_CHECK_ARG(out_mask != nullptr || out_bool != nullptr, "no output");
   RT_CHECK_ARG(reinterpret_cast<uintptr_t>(plan_data) % 8 == 0, "plan data must be 8-aligned");
+  RT_CHECK_ARG(plan_count <= (int64_t{1} << 31) - 1, "too many plans");
   if (n_bundles == 0 || plan_count == 0) return kOk;
-  const size_t need = rt_bloom_search_workspace(data_bytes);
+  const size_t need = rt_bloom_search_workspace(data_bytes, plan_count);
   if (workspace_bytes < need) {
     set_error("workspace too small: %zu < %zu", workspace_bytes, need);
     return kWorkspaceTooSmall;
   }
+  int32_t* hdr = static_cast<int32_t*>(workspace);
+  uint32_t* prog = reinterpret_cast<uint32_t*>(
+      static_cast<char*>(workspace) + align_up(static_cast<size_t>(plan_count) * 16, 256));
   BloomSearchArgs a{};
   a.words = words;
   a.bundle_off = bundle_b_offsets;
@@ -435,13 +879,39 @@ extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_of
   a.max_stack = static_cast<int>(max_stack);
   a.k = static_cast<int>(k);
   a.hash_k = static_cast<int>(hash_k);
-  a.uniform = static_cast<int32_t*>(workspace);
-  a.resolved = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + 256);
+  a.words_aligned16 = reinterpret_cast<uintptr_t>(words) % 16 == 0;
+  a.hdr = hdr;
+  a.prog = prog;
   a.out_mask = out_mask;
   a.out_bool = out_bool;
-  bloom_resolve_kernel<<<1, kBloomThreads, 0, stream>>>(
-      a, const_cast<int32_t*>(a.resolved), const_cast<int32_t*>(a.uniform));
+  bloom_prep_kernel<<<static_cast<unsigned>(plan_count), kPrepThreads, 0, stream>>>(a, hdr,
+                                                                                     prog);
   RT_CHECK_HIP(hipGetLastError());
+
+  // column kernel: two bundles per workgroup, plans split over y when that gives too few
+  const int64_t cx = cdiv(n_bundles, 2);
+  RT_CHECK_ARG(cx < (int64_t{1} << 31), "too many bundles");
+  int64_t cy = cdiv(2048, cx);
+  const int64_t max_cy = cdiv(plan_count, kColWaves);
+  cy = cy > max_cy ? max_cy : cy;
+  cy = cy < 1 ? 1 : cy;
+  cy = cy > 65535 ? 65535 : cy;
+  a.plans_per_wg = cdiv(plan_count, cy);
+  cy = cdiv(plan_count, a.plans_per_wg);
+  const dim3 cgrid(static_cast<unsigned>(cx), static_cast<unsigned>(cy));
+  const int64_t kk = k < hash_k ? k : hash_k;  // > kProgMaxPos: every plan takes the stack path
+  if (kk == 1) {
+    bloom_column_kernel<1><<<cgrid, kColThreads, 0, stream>>>(a);
+  } else if (kk == 2) {
+    bloom_column_kernel<2><<<cgrid, kColThreads, 0, stream>>>(a);
+  } else if (kk == 3) {
+    bloom_column_kernel<3><<<cgrid, kColThreads, 0, stream>>>(a);
+  } else if (kk == 4) {
+    bloom_column_kernel<4><<<cgrid, kColThreads, 0, stream>>>(a);
+  }
+  RT_CHECK_HIP(hipGetLastError());
+
+  // stack evaluation of the rest (its workgroups skip the plans the column kernel wrote)
   const int64_t gx = cdiv(n_bundles * kBloomWordsPerBundle, kBloomThreads);
   RT_CHECK_ARG(gx < (int64_t{1} << 31), "too many bundles");
   int64_t gy = cdiv(2048, gx);

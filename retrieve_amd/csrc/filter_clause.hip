@@ -53,6 +53,7 @@ struct ClauseArgs {
   const float* scores;       // [B, N] (scores mode)
   void* out;
   int64_t W;
+  int mode;  // ClauseMode (the row kernel branches on it; the others take it as a template)
 };
 
 template <bool REG, class T>
@@ -64,42 +65,65 @@ __device__ inline int64_t item_attr(const int64_t (&at)[kRegAttrs], const T* row
   }
 }
 
-// Per query row (one thread each): the active clause mask, and each clause's values with the
-// -1 pads removed, so the item pass visits only real values.
-__global__ void clause_prep_kernel(const int64_t* qvals, int64_t B, int C, int V,
-                                   const int8_t* reverse, uint32_t* active, int32_t* nv,
-                                   int64_t* qc, uint32_t* small, uint64_t* bitmaps,
-                                   uint32_t* rev_mask) {
-  const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (b == 0) {
+// Per query row (one workgroup each, one wave per clause): each clause's values with the -1
+// pads removed (ballot compaction, in order), its 1024-bit set bitmap (LDS atomics), and the
+// row's active clause mask and whether every value lies in [0, kSetDomain).
+constexpr int kPrepThreads = 256;
+
+__global__ void __launch_bounds__(kPrepThreads) clause_prep_kernel(
+    const int64_t* qvals, int64_t B, int C, int V, const int8_t* reverse, uint32_t* active,
+    int32_t* nv, int64_t* qc, uint32_t* small, uint64_t* bitmaps, uint32_t* rev_mask) {
+  __shared__ uint64_t bm[kPrepThreads / kWave][kSetWords];
+  __shared__ uint32_t clause_act[kMaxClauses];
+  __shared__ uint32_t clause_fits[kMaxClauses];
+  const int64_t b = blockIdx.x;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  if (b == 0 && threadIdx.x == 0) {
     uint32_t r = 0;
     for (int c = 0; c < C; ++c) r |= reverse[c] != 0 ? 1u << c : 0u;
     rev_mask[0] = r;
   }
-  if (b >= B) return;
-  uint32_t act = 0;
-  bool fits = true;
-  for (int c = 0; c < C; ++c) {
+  for (int c = wave; c < C; c += kPrepThreads / kWave) {
+    if (lane < kSetWords) bm[wave][lane] = 0ull;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
     const int64_t* src = qvals + (b * C + c) * V;
     int64_t* dst = qc + (b * C + c) * V;
-    uint64_t* bm = bitmaps + (b * C + c) * kSetWords;
-    for (int w = 0; w < kSetWords; ++w) bm[w] = 0ull;
     int n = 0;
-    for (int v = 0; v < V; ++v) {
-      const int64_t x = src[v];
-      if (x == -1) continue;
-      dst[n++] = x;
-      if (x >= 0 && x < kSetDomain) {
-        bm[x >> 6] |= 1ull << (x & 63);
-      } else {
-        fits = false;
-      }
+    bool fits = true;
+    for (int v0 = 0; v0 < V; v0 += kWave) {
+      const int64_t x = v0 + lane < V ? src[v0 + lane] : -1;
+      const bool keep = x != -1;
+      const uint64_t mask = __ballot(keep);
+      const int pos = n + static_cast<int>(__popcll(mask & ((1ull << lane) - 1ull)));
+      if (keep) dst[pos] = x;
+      n += static_cast<int>(__popcll(mask));
+      const bool in_set = keep && x >= 0 && x < kSetDomain;
+      fits &= __ballot(keep && !in_set) == 0ull;
+      if (in_set) atomicOr(&bm[wave][x >> 6], 1ull << (x & 63));
     }
-    nv[b * C + c] = n;
-    act |= n > 0 ? 1u << c : 0u;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (lane < kSetWords) bitmaps[(b * C + c) * kSetWords + lane] = bm[wave][lane];
+    if (lane == 0) {
+      nv[b * C + c] = n;
+      clause_act[c] = n > 0 ? 1u : 0u;
+      clause_fits[c] = fits ? 1u : 0u;
+    }
+    __builtin_amdgcn_wave_barrier();
   }
-  active[b] = act;
-  small[b] = fits ? 1u : 0u;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t act = 0u;
+    bool fits = true;
+    for (int c = 0; c < C; ++c) {
+      act |= clause_act[c] << c;
+      fits &= clause_fits[c] != 0u;
+    }
+    active[b] = act;
+    small[b] = fits ? 1u : 0u;
+  }
 }
 
 // One query row against this lane's item: 1 iff every active clause matches.
@@ -360,8 +384,216 @@ __global__ void __launch_bounds__(kClauseThreads) clause_qmask_kernel(ClauseArgs
   }
 }
 
+// ---- one value per clause (A == 1), C <= 16: the row kernel --------------------------
+//
+// The query-mask form with C and T known at compile time. An item's C values arrive with the
+// widest loads its row size allows; the table holds, per clause, kSetDomain + 1 row masks with
+// the clause's reverse flag and its unconstrained rows (inactive clause, list rows) folded in:
+//   tab[c][x] = (qm[c][x] XOR rev[c]) OR unconstrained[c],  tab[c][kSetDomain]: values outside
+// [0, kSetDomain), which no bitmap row holds. An item's row mask is the AND of C lookups.
+// Lane l of a wave takes item (wave base + 63 - l), so a ballot is a mask word as it is stored
+// (item d at bit 63 - d % 64); lane r keeps row r's word and the rows store together.
+constexpr int kTabStride = kSetDomain + 1;
+
+template <class T, int C>
+struct RowShape {
+  static constexpr int kBytes = C * static_cast<int>(sizeof(T));
+  static constexpr int kLoad = kBytes % 16 == 0 ? 16 : kBytes % 8 == 0 ? 8 : kBytes % 4 == 0 ? 4 : 2;
+  static constexpr int kWords = (kBytes + 3) / 4;
+};
+
+typedef uint32_t v4w __attribute__((ext_vector_type(4)));
+
+typedef uint32_t v2w __attribute__((ext_vector_type(2)));
+
+template <class T, int C>
+__device__ inline void load_row(const char* p, uint32_t (&w)[RowShape<T, C>::kWords]) {
+  using S = RowShape<T, C>;
+  if constexpr (S::kLoad == 16) {
+#pragma unroll
+    for (int j = 0; j < S::kBytes / 16; ++j) {
+      const v4w x = *reinterpret_cast<const v4w*>(p + 16 * j);
+      w[4 * j] = x[0];
+      w[4 * j + 1] = x[1];
+      w[4 * j + 2] = x[2];
+      w[4 * j + 3] = x[3];
+    }
+  } else if constexpr (S::kLoad == 8) {
+#pragma unroll
+    for (int j = 0; j < S::kBytes / 8; ++j) {
+      const v2w x = *reinterpret_cast<const v2w*>(p + 8 * j);
+      w[2 * j] = x[0];
+      w[2 * j + 1] = x[1];
+    }
+  } else if constexpr (S::kLoad == 4) {
+#pragma unroll
+    for (int j = 0; j < S::kBytes / 4; ++j) w[j] = reinterpret_cast<const uint32_t*>(p)[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < S::kWords; ++j) w[j] = 0u;
+#pragma unroll
+    for (int j = 0; j < S::kBytes / 2; ++j) {
+      w[j / 2] |= static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(p)[j]) << (16 * (j % 2));
+    }
+  }
+}
+
+// Clause c's value: its table slot, and the value itself (for the list rows).
+template <class T, int C>
+__device__ inline uint32_t row_slot(const uint32_t (&w)[RowShape<T, C>::kWords], int c,
+                                    int64_t& value) {
+  if constexpr (sizeof(T) == 2) {
+    const int32_t x = static_cast<int16_t>(w[c / 2] >> (16 * (c % 2)));
+    value = x;
+    return static_cast<uint32_t>(x) < static_cast<uint32_t>(kSetDomain) ? static_cast<uint32_t>(x)
+                                                                          : kSetDomain;
+  } else if constexpr (sizeof(T) == 4) {
+    const int32_t x = static_cast<int32_t>(w[c]);
+    value = x;
+    return static_cast<uint32_t>(x) < static_cast<uint32_t>(kSetDomain) ? static_cast<uint32_t>(x)
+                                                                          : kSetDomain;
+  } else {
+    const uint32_t lo = w[2 * c];
+    const uint32_t hi = w[2 * c + 1];
+    value = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+    return hi == 0u && lo < static_cast<uint32_t>(kSetDomain) ? lo : kSetDomain;
+  }
+}
+
+template <class T, int C>
+__global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a) {
+  using S = RowShape<T, C>;
+  extern __shared__ uint32_t tab[];  // [C][kTabStride]
+  __shared__ uint32_t row_active[kQmaskRows];
+  __shared__ uint32_t clause_fold[2][C];  // XOR, then OR, per clause
+  __shared__ uint32_t slow_rows;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const uint32_t rev_mask = a.rev_mask[0];
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * kQmaskRows;
+  const int nrows = static_cast<int>(b0 + kQmaskRows < a.B ? kQmaskRows : a.B - b0);
+
+  for (int i = tid; i < C * kTabStride; i += kClauseThreads) tab[i] = 0u;
+  if (tid == 0) slow_rows = 0u;
+  if (tid < kQmaskRows) row_active[tid] = tid < nrows ? a.active[b0 + tid] : 0u;
+  __syncthreads();
+  if (tid < nrows && a.small[b0 + tid] == 0u) atomicOr(&slow_rows, 1u << tid);
+  // every (row, clause) value of the bitmap rows sets its row's bit
+  for (int rc = tid; rc < nrows * C; rc += kClauseThreads) {
+    const int r = rc / C;
+    const int c = rc - r * C;
+    const int64_t b = b0 + r;
+    if (a.small[b] == 0u) continue;
+    const int64_t* vals = a.qc + (b * C + c) * a.V;
+    const int n = a.nv[b * C + c];
+    for (int v = 0; v < n; ++v) atomicOr(&tab[c * kTabStride + vals[v]], 1u << r);
+  }
+  __syncthreads();
+  const uint32_t slow = slow_rows;
+  if (tid < C) {
+    uint32_t unconstrained = slow;
+    for (int r = 0; r < nrows; ++r) unconstrained |= (row_active[r] >> tid) & 1u ? 0u : 1u << r;
+    clause_fold[0][tid] = (rev_mask >> tid) & 1u ? ~0u : 0u;
+    clause_fold[1][tid] = unconstrained;
+  }
+  __syncthreads();
+  for (int i = tid; i < C * kTabStride; i += kClauseThreads) {
+    const int c = i / kTabStride;
+    tab[i] = (tab[i] ^ clause_fold[0][c]) | clause_fold[1][c];
+  }
+  __syncthreads();
+  const uint32_t fast = ~slow;
+
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kClauseThreads; base < a.N;
+       base += static_cast<int64_t>(gridDim.x) * kClauseThreads) {
+    const int64_t wbase = base + wave * kWave;
+    const int64_t d = wbase + (kWave - 1 - lane);
+    const bool valid = d < a.N;
+    const int64_t wword = wbase >> 6;
+    uint64_t am = ~0ull;
+    if (a.mode == kClauseBits && a.and_mask != nullptr && lane < nrows && wword < a.W) {
+      am = a.and_mask[(b0 + lane) * a.and_words + wword];
+    }
+    uint32_t w[S::kWords];
+    load_row<T, C>(static_cast<const char*>(a.attrs) + (valid ? d : 0) * S::kBytes, w);
+    uint32_t slot[C];
+    int64_t at[kRegAttrs];
+#pragma unroll
+    for (int c = 0; c < kRegAttrs; ++c) at[c] = -1;
+#pragma unroll
+    for (int c = 0; c < C; ++c) slot[c] = row_slot<T, C>(w, c, at[c]);
+    uint32_t m = fast;
+#pragma unroll
+    for (int c = 0; c < C; ++c) m &= tab[c * kTabStride + slot[c]];
+    for (uint32_t rest = slow; rest != 0u; rest &= rest - 1u) {
+      const int r = __builtin_ctz(rest);
+      const bool pass = clause_pass<true, T>(a, at, nullptr, b0 + r, rev_mask, nullptr,
+                                             row_active[r]);
+      m |= pass ? 1u << r : 0u;
+    }
+    if (!valid) m = 0u;
+
+    if (a.mode == kClauseBits) {
+      uint64_t mine = 0ull;
+      for (int r = 0; r < nrows; ++r) {
+        const uint64_t word = __ballot((m >> r) & 1u);
+        mine = lane == r ? word : mine;
+      }
+      if (lane < nrows && wword < a.W) {
+        static_cast<uint64_t*>(a.out)[(b0 + lane) * a.W + wword] = mine & am;
+      }
+    } else if (valid) {
+      for (int r = 0; r < nrows; ++r) {
+        const int64_t b = b0 + r;
+        const bool pass = (m >> r) & 1u;
+        if (a.mode == kClauseBool) {
+          static_cast<uint8_t*>(a.out)[b * a.N + d] = pass ? 1 : 0;
+        } else {
+          static_cast<float*>(a.out)[b * a.N + d] = pass ? a.scores[b * a.N + d] : -INFINITY;
+        }
+      }
+    }
+  }
+}
+
+template <class T, int C>
+static bool launch_row_kernel(const ClauseArgs& a, dim3 grid, hipStream_t stream) {
+  if (reinterpret_cast<uintptr_t>(a.attrs) % RowShape<T, C>::kLoad != 0) return false;
+  const size_t lds = static_cast<size_t>(C) * kTabStride * sizeof(uint32_t);
+  clause_row_kernel<T, C><<<grid, kClauseThreads, lds, stream>>>(a);
+  return true;
+}
+
+// The row kernel for A == 1 and 1 <= C <= 16 (false: the attribute table is not aligned for its
+// loads, or the shape is not one it takes).
+template <class T>
+static bool launch_row_typed(const ClauseArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.A != 1) return false;
+  switch (a.C) {
+    case 1: return launch_row_kernel<T, 1>(a, grid, stream);
+    case 2: return launch_row_kernel<T, 2>(a, grid, stream);
+    case 3: return launch_row_kernel<T, 3>(a, grid, stream);
+    case 4: return launch_row_kernel<T, 4>(a, grid, stream);
+    case 5: return launch_row_kernel<T, 5>(a, grid, stream);
+    case 6: return launch_row_kernel<T, 6>(a, grid, stream);
+    case 7: return launch_row_kernel<T, 7>(a, grid, stream);
+    case 8: return launch_row_kernel<T, 8>(a, grid, stream);
+    case 9: return launch_row_kernel<T, 9>(a, grid, stream);
+    case 10: return launch_row_kernel<T, 10>(a, grid, stream);
+    case 11: return launch_row_kernel<T, 11>(a, grid, stream);
+    case 12: return launch_row_kernel<T, 12>(a, grid, stream);
+    case 13: return launch_row_kernel<T, 13>(a, grid, stream);
+    case 14: return launch_row_kernel<T, 14>(a, grid, stream);
+    case 15: return launch_row_kernel<T, 15>(a, grid, stream);
+    case 16: return launch_row_kernel<T, 16>(a, grid, stream);
+    default: return false;
+  }
+}
+
 template <int MODE, class T>
 static void launch_clause(const ClauseArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.C >= 1 && a.C <= kQmaskClauses && launch_row_typed<T>(a, grid, stream)) return;
   if (a.C >= 1 && a.C <= kQmaskClauses) {
     const size_t qlds = static_cast<size_t>(a.C) * kSetDomain * sizeof(uint32_t);
     if (a.A == 1) {
@@ -583,6 +815,7 @@ extern "C" int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t 
                                 const uint64_t* and_mask, int64_t and_mask_words, void* out,
                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
   RT_CHECK_ARG(N >= 0 && B >= 0, "N and B must be >= 0");
+  RT_CHECK_ARG(B <= (int64_t{1} << 21), "B must be <= 2^21 query rows");
   RT_CHECK_ARG(C >= 0 && C <= kMaxClauses, "C must be in [0, %d], got %lld", kMaxClauses,
                static_cast<long long>(C));
   RT_CHECK_ARG(A >= 0 && A <= 4096 && V >= 1 && V <= 4096, "A must be >= 0 and V >= 1");
@@ -611,6 +844,7 @@ extern "C" int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t 
   a.scores = scores;
   a.out = out;
   a.W = cdiv(N, 64);
+  a.mode = mode;
   if (C > 0) {
     const ClauseWs p = clause_ws_parts(B, C, V);
     if (workspace_bytes < p.total) {
@@ -624,7 +858,7 @@ extern "C" int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t 
     a.small = reinterpret_cast<uint32_t*>(ws + p.small);
     a.bitmaps = reinterpret_cast<uint64_t*>(ws + p.bitmaps);
     a.rev_mask = reinterpret_cast<uint32_t*>(ws + p.rev);
-    clause_prep_kernel<<<static_cast<unsigned>(cdiv(B, 64)), 64, 0, stream>>>(
+    clause_prep_kernel<<<static_cast<unsigned>(B), kPrepThreads, 0, stream>>>(
         query_values, B, static_cast<int>(C), static_cast<int>(V), clause_is_reverse,
         const_cast<uint32_t*>(a.active), const_cast<int32_t*>(a.nv), const_cast<int64_t*>(a.qc),
         const_cast<uint32_t*>(a.small), const_cast<uint64_t*>(a.bitmaps),

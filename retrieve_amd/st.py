@@ -183,7 +183,7 @@ def _bloom_search(bloom_index: Tensor, offsets: Tensor, plan_offsets: Tensor, da
     if plan_count == 0 or nb <= 0:
         return out
     lib = nat.lib()
-    ws = nat.workspace(lib.rt_bloom_search_workspace(data_bytes), dev)
+    ws = nat.workspace(lib.rt_bloom_search_workspace(data_bytes, plan_count), dev)
     with torch.cuda.device(dev):
         st = lib.rt_bloom_search(
             nat.ptr(bloom_index), nat.ptr(offsets), nb, nat.ptr(plan_offsets), nat.ptr(data),

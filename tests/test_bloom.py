@@ -165,3 +165,42 @@ def test_errors(dev):
         torch.ops.st.bloom_index_build(fid, fo, fv, 1.0, 3)
     with pytest.raises(ValueError):
         torch.ops.st.bloom_index_build_fixed(fid, fo, fv, 64, 11)
+
+
+def _nested(depth: int) -> str:
+    """AND / OR alternating ``depth`` levels deep, each level with a term beside the subtree."""
+    e = "0:1"
+    for d in range(depth):
+        e = f"({e} {'AND' if d % 2 else 'OR'} {d % 4}:{d % 5})"
+    return e
+
+
+@pytest.mark.parametrize("bits,k,hash_k,n", [(64, 3, 7, 4500), (64, 5, 7, 1000),
+                                             (128, 3, 7, 1000), (64, 2, 2, 70)])
+def test_search_paths(dev, bits, k, hash_k, n):
+    """Programs over LDS-staged bundles (64 bits, k <= 4) and the stack evaluation (deep plans,
+    k > 4, wider bundles) in one batch; many plans over few bundles split across workgroups."""
+    g = rng(86 + bits + k + n)
+    attrs = _attrs(g, n, 4, 1, 6, 0.2)
+    words, offs = _build(dev, attrs, k, bits=bits)
+    ow, oo = of.bloom_build(attrs, k, bits_per_doc=bits)
+    exprs = [_random_expr(g) for _ in range(16)]
+    exprs += [_nested(d) for d in (3, 4, 5, 6, 9)]
+    exprs += ["NOT (NOT (NOT (NOT (NOT (0:1 OR 1:1)))))", "0:0 OR 0:1 OR 0:2 OR 0:3 OR 0:4"]
+    got = _unpack(_search(dev, words, offs, exprs, k, hash_k), n)
+    for e, row in zip(exprs, got):
+        want = of.bloom_expression_mask(ow, oo, n, e, k, hash_k)
+        assert np.array_equal(row, want), e
+
+
+def test_stack_limit_matches_nothing(dev):
+    """A plan that needs more stack than max_stack_size matches nothing; the others evaluate."""
+    g = rng(90)
+    attrs = _attrs(g, 3000, 2, 1, 5, 0.0)
+    words, offs = _build(dev, attrs, 3, bits=64)
+    blob, count, _ = st.prepare_plans(["0:1 OR 1:2 OR 0:3", "0:1", "NOT 1:2"], 7, dev)
+    m = torch.ops.st.bloom_index_search_batch_prepared(words, offs, blob, count, 2, 3, 7)
+    assert (m[0] == 0).all()
+    full = torch.ops.st.bloom_index_search_batch_prepared(words, offs, blob, count, 3, 3, 7)
+    assert (full[0] != 0).any()
+    assert torch.equal(m[1:], full[1:])
