@@ -1,19 +1,26 @@
 """Benchmark of the scoring-and-selection hot path on one MI355X.
 
-Default workload: the metric's filtered top-100 over the 30M x 512 int8 table. Items are
-per-row int8 quantizations of N(0,1) float32 rows (scale = max|x| / 127), queries likewise
-(B = 16); every item carries the 8 categorical attributes of the filtered-kNN configuration
-(cardinalities 16 .. 1000, Zipf(1.1) values) and a 64-bit, 3-hash Bloom signature over its
-(attribute, value) tokens; each query is an AND over 1-3 attributes of OR over value sets, tuned
-to 10 % selectivity. A step is the filtered forward over one query batch, inputs resident in
-HBM: the Bloom pre-filter (plans prepared once, outside the timed region, as the reference's
-prepare_queries), the exact clause post-check on the Bloom survivors, and the int8 scan with the
-fused exact top-100 (ties to the lower index). ``--filter none`` times the plain scan.
+Default workload (``--workload filtered``): the metric's filtered top-100 over the 30M x 512
+int8 table. Items are per-row int8 quantizations of N(0,1) float32 rows (scale = max|x| / 127),
+queries likewise (B = 16); every item carries the 8 categorical attributes of the filtered-kNN
+configuration (cardinalities 16 .. 1000, Zipf(1.1) values) and a 64-bit, 3-hash Bloom signature
+over its (attribute, value) tokens; each query is an AND over 1-3 attributes of OR over value
+sets, tuned to 10 % selectivity. A step is the filtered forward over one query batch, inputs
+resident in HBM: the Bloom pre-filter (plans prepared once, outside the timed region, as the
+reference's prepare_queries), the exact clause post-check on the Bloom survivors, and the int8
+scan with the fused exact top-100 (ties to the lower index).
 
-Prints one JSON line with the whole-job throughput (queries/s), the dominant kernel's (the int8
-scan's) roofline fraction measured live with HIP events on its launch stream, and the
-reference's CPU path (torch.mm over item chunks + the filter + top-k) timed on a bounded sample
-on this host.
+Other workloads (the remaining configurations, same JSON line):
+  int8     the plain int8 scan top-k (configuration 4; ``--batch`` 1 / 16 / 256 / 1024)
+  dense    bf16 top-100 over 10M x 128 clustered, L2-normalised items (configuration 2), with
+           recall@100 against exact float32 scoring of the unrounded items
+  binary   1-bit retrieval: SimHash codes (sign of a Gaussian projection, 512 bits) scanned by
+           Hamming score for the top-1000 under the Bloom + exact filter at 10 %, re-ranked by
+           the int8 codes of the same vectors to the top-100 (configuration 5, B = 256)
+
+Prints one JSON line with the whole-job throughput (queries/s), the dominant kernel's roofline
+fraction measured live with HIP events on its launch stream, and the reference's CPU path timed
+on a bounded sample on this host.
 """
 
 from __future__ import annotations
@@ -32,6 +39,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+VALU_PEAK = 256 * 64 * 2.4e9  # 32-bit lane-ops/s: 256 CUs x 64 lanes x 2.4 GHz
+# HBM bytes per launch of the main scan (FETCH_SIZE + WRITE_SIZE, copy-calibrated), measured with
+# rocprofv3 --pmc for these exact workloads; keyed by (workload, N, D, B, k). See profiles/.
+MEASURED_TRAFFIC: dict = {}
 CARDINALITIES = (16, 32, 64, 128, 256, 512, 1000, 1000)
 BLOOM_BITS, BLOOM_K, HASH_K = 64, 3, 7
 
@@ -106,20 +117,94 @@ def query_sets(attrs: torch.Tensor, b: int, selectivity: float, seed: int) -> np
     return out
 
 
+def dense_table(n: int, d: int, centres: torch.Tensor, seed: int, dev: torch.device,
+                chunk: int = 1 << 20) -> torch.Tensor:
+    """[N, D] float32 rows centre[u] + 0.3 N(0,1), u uniform over the centres, L2-normalised."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    out = torch.empty((n, d), dtype=torch.float32, device=dev)
+    for s in range(0, n, chunk):
+        m = min(chunk, n - s)
+        u = torch.randint(0, centres.shape[0], (m,), generator=gen, device=dev)
+        x = centres[u] + 0.3 * torch.randn((m, d), generator=gen, device=dev)
+        out[s : s + m] = torch.nn.functional.normalize(x, dim=1)
+    return out
+
+
+def simhash_tables(n: int, d: int, proj: torch.Tensor, seed: int, dev: torch.device,
+                   chunk: int = 1 << 20) -> tuple[torch.Tensor, torch.Tensor]:
+    """N(0,1) rows x: their SimHash codes (bit b of word w = (x @ proj.T)[64 w + b] > 0, the
+    reference's LSB-first packing) and their per-row int8 codes."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    bits_out = torch.empty((n, proj.shape[0] // 64), dtype=torch.int64, device=dev)
+    codes = torch.empty((n, d), dtype=torch.int8, device=dev)
+    shifts = torch.arange(64, device=dev, dtype=torch.int64)
+    for s in range(0, n, chunk):
+        m = min(chunk, n - s)
+        x = torch.randn((m, d), generator=gen, device=dev)
+        signs = (x @ proj.t() > 0).view(m, -1, 64).long()
+        bits_out[s : s + m] = (signs << shifts).sum(-1)
+        codes[s : s + m] = quantize_rows(x)
+    return bits_out, codes
+
+
+class Filter:
+    """The filtered-kNN configuration's attributes, Bloom index and query plans for B rows."""
+
+    def __init__(self, n: int, b: int, selectivity: float, dev: torch.device):
+        import retrieve_amd.st as st
+        from retrieve_amd import bloom as bl
+
+        log("generating attributes, Bloom index and query plans")
+        self.attrs = attr_table(n, 4321, dev)
+        sets = query_sets(self.attrs, b, selectivity, 77)
+        fid, fo, fv = st.attrs_to_features(self.attrs.long())
+        self.words, self.offs = torch.ops.st.bloom_index_build_fixed(fid, fo, fv, BLOOM_BITS,
+                                                                     BLOOM_K)
+        del fid, fo, fv
+        self.blob, self.plan_count, self.max_stack = st.prepare_plans(
+            bl.sets_to_expressions(sets), HASH_K, dev)
+        self.rev = torch.zeros(len(CARDINALITIES), dtype=torch.bool, device=dev)
+        self.sets = torch.from_numpy(sets).to(dev)
+        exact = torch.ops.retrieve.clause_bits(self.attrs, self.rev, self.sets)
+        counts = torch.ops.retrieve.mask_compact(exact, n)[1]
+        self.selectivity = (counts.double() / n).cpu().numpy()
+        torch.cuda.synchronize()
+        log(f"selectivity per row: mean {self.selectivity.mean():.4f}, "
+            f"min {self.selectivity.min():.4f}, max {self.selectivity.max():.4f}")
+
+    def mask(self) -> torch.Tensor:
+        """One batch's filter: Bloom pre-filter, then the exact post-check of its survivors."""
+        pre = torch.ops.st.bloom_index_search_batch_prepared(
+            self.words, self.offs, self.blob, self.plan_count, self.max_stack, BLOOM_K, HASH_K)
+        return torch.ops.retrieve.clause_bits(self.attrs, self.rev, self.sets, pre)
+
+    def bytes(self, n: int, b: int) -> int:
+        """Algorithmic bytes of one batch's filter: Bloom words, int16 attributes, the masks."""
+        return n * BLOOM_BITS // 8 + n * len(CARDINALITIES) * 2 + 3 * b * n // 8
+
+    def valid_fn(self, ns: int):
+        from oracle import baseline
+
+        return baseline.clause_sets_valid(self.attrs[:ns].cpu().long(), self.sets.cpu())
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--batch", type=int, default=16)
-    ap.add_argument("--n", type=int, default=30_000_000)
-    ap.add_argument("--d", type=int, default=512)
+    ap.add_argument("--workload", choices=("filtered", "int8", "dense", "binary"),
+                    default="filtered")
+    ap.add_argument("--batch", type=int, default=None,
+                    help="query batch (default: 16 filtered / int8, 64 dense, 256 binary)")
+    ap.add_argument("--n", type=int, default=None,
+                    help="items (default: 30M, dense 10M)")
+    ap.add_argument("--d", type=int, default=None, help="dimensions (default 512, dense 128)")
     ap.add_argument("--k", type=int, default=100)
-    ap.add_argument("--filter", choices=("bloom", "none"), default="bloom",
-                    help="bloom: Bloom pre-filter + exact clause post-check (the metric's "
-                         "filtered top-100); none: the plain scan")
+    ap.add_argument("--filter", choices=("bloom", "none"), default=None,
+                    help="kept for older command lines: none = --workload int8")
     ap.add_argument("--selectivity", type=float, default=0.1)
-    ap.add_argument("--cpu-sample", type=int, default=2_000_000,
+    ap.add_argument("--cpu-sample", type=int, default=None,
                     help="items of the CPU baseline's bounded sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -130,49 +215,153 @@ def main() -> int:
         print("bench.py measures one GPU: this build has no multi-GPU path (one GPU per box); "
               "run with --gpus 1", file=sys.stderr)
         return 2
+    if args.filter == "none":
+        args.workload = "int8"
 
     import retrieve_amd.hip  # noqa: F401  (registers torch.ops.retrieve.*)
-    import retrieve_amd.st as st
+    import retrieve_amd.st  # noqa: F401  (registers torch.ops.st.*)
     from retrieve_amd import _native
-    from retrieve_amd import bloom as bl
 
     dev = torch.device("cuda:0")
-    b, n, d, k = args.batch, args.n, args.d, args.k
-    filtered = args.filter == "bloom"
-    log(f"generating items {n}x{d} int8 and queries {b}x{d}")
-    items = int8_table(n, d, 1234, dev)
-    queries = int8_table(b, d, 99, dev)
+    wl = args.workload
+    b = args.batch or {"filtered": 16, "int8": 16, "dense": 64, "binary": 256}[wl]
+    n = args.n or (10_000_000 if wl == "dense" else 30_000_000)
+    d = args.d or (128 if wl == "dense" else 512)
+    k = args.k
+    extra: dict = {}
+    cpu_fn = None
+
+    if wl in ("filtered", "int8"):
+        log(f"generating items {n}x{d} int8 and queries {b}x{d}")
+        items = int8_table(n, d, 1234, dev)
+        queries = int8_table(b, d, 99, dev)
+        flt = Filter(n, b, args.selectivity, dev) if wl == "filtered" else None
+
+        def step():
+            return torch.ops.retrieve.int8_scan_topk(queries, items, k,
+                                                    flt.mask() if flt else None)
+
+        scan_bytes = n * d + b * d  # the item table once + the query block
+        scan_ops = 2 * b * n * d
+        step_bytes = scan_bytes + (flt.bytes(n, b) if flt else 0)
+        bound = "hbm" if 2 * b < 625 else "mfma"  # int8 ridge: 625 OP/B
+        dtype = "int8"
+        data = ("synthetic: per-row int8 of N(0,1) float32 rows (torch generator seeds 1234 / "
+                "99)" + ("; attributes Zipf(1.1) (seed 4321), query sets numpy seed 77"
+                         if flt else ""))
+        workload = f"int8 scan top-{k}: N={n} D={d} B={b}"
+        if flt:
+            workload = (f"filtered int8 top-{k}: N={n} D={d} B={b}; Bloom {BLOOM_BITS} bits/item, "
+                        f"{BLOOM_K} hashes pre-filter + exact AND-of-OR clause post-check over 8 "
+                        f"attributes at {args.selectivity:.0%} target selectivity")
+            extra["measured_selectivity"] = float(flt.selectivity.mean())
+        metric = ("queries/sec + achieved HBM GB/s, filtered top-100 over 30Mx512 int8 items"
+                  if flt else "queries/sec + achieved HBM GB/s, int8 top-100 over 30Mx512 items")
+
+        def cpu_fn():
+            from oracle import baseline
+
+            ns = min(args.cpu_sample or 2_000_000, n)
+            valid_fn = flt.valid_fn(ns) if flt else None
+            t_s, threads = baseline.time_int8(queries.cpu(), items[:ns].cpu(), k,
+                                              valid_fn=valid_fn)
+            what = "torch.mm over 2M-row chunks + topk + lowest-id merge"
+            if flt:
+                what = "the exact value-set filter (torch.isin) gating " + what
+            return t_s * (n / ns), threads, f"B={b} queries x first {ns} of {n} items ({what})"
+
+    elif wl == "dense":
+        log(f"generating {n}x{d} clustered items (1024 centres) and {b} queries")
+        gen = torch.Generator(device=dev).manual_seed(2024)
+        centres = torch.randn((1024, d), generator=gen, device=dev)
+        items32 = dense_table(n, d, centres, 2025, dev)
+        q32 = dense_table(b, d, centres, 2026, dev)
+        items = items32.bfloat16()
+        queries = q32.bfloat16()
+
+        def step():
+            return torch.ops.retrieve.dense_scan_topk(queries, items, k)
+
+        # recall@k against exact float32 scoring of the unrounded rows (chunked torch.mm)
+        torch.backends.cuda.matmul.allow_tf32 = False
+        best_s = torch.full((b, k), float("-inf"), device=dev)
+        best_i = torch.full((b, k), -1, dtype=torch.int64, device=dev)
+        for s0 in range(0, n, 1 << 21):
+            sc = q32 @ items32[s0 : s0 + (1 << 21)].t()
+            top = torch.topk(sc, min(k, sc.shape[1]), dim=1)
+            cs = torch.cat([best_s, top.values], 1)
+            ci = torch.cat([best_i, top.indices + s0], 1)
+            t2 = torch.topk(cs, k, dim=1)
+            best_s, best_i = t2.values, ci.gather(1, t2.indices)
+        got = step()[0]
+        hits = (got.unsqueeze(2) == best_i.unsqueeze(1)).any(2).sum().item()
+        extra["recall_at_k_vs_fp32"] = hits / (b * k)
+        log(f"recall@{k} vs exact fp32: {extra['recall_at_k_vs_fp32']:.4f}")
+        del items32
+
+        scan_bytes = n * d * 2 + b * d * 2
+        scan_ops = 2 * b * n * d
+        step_bytes = scan_bytes
+        bound = "hbm" if b < 312 else "mfma"  # bf16 ridge: 312.5 FLOP/B
+        dtype = "bf16"
+        data = ("synthetic: 1024 N(0,1) centres (seed 2024), items centre + 0.3 N(0,1) "
+                "L2-normalised (seed 2025), queries likewise (seed 2026), stored bf16")
+        workload = f"dense bf16 top-{k}: N={n} D={d} B={b} (clustered, L2-normalised)"
+        metric = "queries/sec + achieved HBM GB/s, bf16 top-100 over 10Mx128 items"
+
+        def cpu_fn():
+            from oracle import baseline
+
+            ns = min(args.cpu_sample or 1_000_000, n)
+            t_s, threads = baseline.time_topk(queries.cpu().float(), items[:ns].cpu().float(), k)
+            return (t_s * (n / ns), threads,
+                    f"B={b} queries x first {ns} of {n} items (float32 torch.mm over 2M-row "
+                    "chunks + topk + lowest-id merge)")
+
+    else:  # binary
+        k1 = 1000
+        log(f"generating {n} SimHash codes ({d} bits) + int8 rerank codes, {b} queries")
+        gen = torch.Generator(device=dev).manual_seed(555)
+        proj = torch.randn((d, d), generator=gen, device=dev)
+        item_bits, item_codes = simhash_tables(n, d, proj, 556, dev)
+        q_bits, q_codes = simhash_tables(b, d, proj, 557, dev)
+        flt = Filter(n, b, args.selectivity, dev)
+
+        def step():
+            ids1, _ = torch.ops.retrieve.hamming_scan_topk(q_bits, item_bits, k1, flt.mask())
+            counts = (ids1 >= 0).sum(1)
+            return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
+
+        scan_bytes = n * d // 8 + b * d // 8
+        scan_ops = 2 * b * n * (d // 32)  # XOR + popcount per 32-bit word pair
+        step_bytes = scan_bytes + flt.bytes(n, b) + b * k1 * d
+        bound = "hbm"
+        dtype = "u64 (1-bit codes) / int8 rerank"
+        data = ("synthetic: N(0,1) rows (seed 556) and queries (seed 557), SimHash over a "
+                "N(0,1) 512x512 projection (seed 555), int8 codes of the same rows; attributes "
+                "Zipf(1.1) (seed 4321), query sets numpy seed 77")
+        workload = (f"binary top-{k1} + int8 rerank top-{k}: N={n} bits={d} B={b}; Bloom + exact "
+                    f"filter at {args.selectivity:.0%} target selectivity")
+        extra["measured_selectivity"] = float(flt.selectivity.mean())
+        metric = ("queries/sec + achieved HBM GB/s, filtered 1-bit top-1000 + int8 rerank "
+                  "top-100 over 30M items")
+
+        def cpu_fn():
+            from oracle import baseline
+
+            ns = min(args.cpu_sample or 200_000, n)
+            valid = flt.valid_fn(ns)(0, ns).numpy()
+            t0 = time.perf_counter()
+            baseline.hamming_rerank_cpu(q_bits.cpu().numpy(), q_codes.cpu().numpy(),
+                                        item_bits[:ns].cpu().numpy(),
+                                        item_codes[:ns].cpu().numpy(), k1, k, valid)
+            t_s = time.perf_counter() - t0
+            return (t_s * (n / ns), 1,
+                    f"B={b} queries x first {ns} of {n} items (numpy XOR + bitwise_count in "
+                    "32K-item chunks, exact filter, top-1000 by (score, id), int8 re-rank of "
+                    "the candidates), one run, scaled")
+
     torch.cuda.synchronize()
-
-    rev = words = offs = blob = sets_t = attrs = None
-    plan_count = max_stack = 0
-    measured_sel = None
-    if filtered:
-        log("generating attributes, Bloom index and query plans")
-        attrs = attr_table(n, 4321, dev)
-        sets = query_sets(attrs, b, args.selectivity, 77)
-        fid, fo, fv = st.attrs_to_features(attrs.long())
-        words, offs = torch.ops.st.bloom_index_build_fixed(fid, fo, fv, BLOOM_BITS, BLOOM_K)
-        del fid, fo, fv
-        blob, plan_count, max_stack = st.prepare_plans(bl.sets_to_expressions(sets), HASH_K, dev)
-        rev = torch.zeros(len(CARDINALITIES), dtype=torch.bool, device=dev)
-        sets_t = torch.from_numpy(sets).to(dev)
-        exact = torch.ops.retrieve.clause_bits(attrs, rev, sets_t)
-        counts = torch.ops.retrieve.mask_compact(exact, n)[1]
-        measured_sel = (counts.double() / n).cpu().numpy()
-        del exact
-        torch.cuda.synchronize()
-        log(f"selectivity per row: mean {measured_sel.mean():.4f}, "
-            f"min {measured_sel.min():.4f}, max {measured_sel.max():.4f}")
-
-    def step():
-        mask = None
-        if filtered:
-            pre = torch.ops.st.bloom_index_search_batch_prepared(
-                words, offs, blob, plan_count, max_stack, BLOOM_K, HASH_K)
-            mask = torch.ops.retrieve.clause_bits(attrs, rev, sets_t, pre)
-        return torch.ops.retrieve.int8_scan_topk(queries, items, k, mask)
-
     if args.copy_probe:
         src = torch.empty(2 << 30, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -202,46 +391,34 @@ def main() -> int:
     _native.check(lib.rt_profile_enable(0))
     ms_step = wall * 1e3 / args.steps
     kernel_ms = total_ms.value / max(1, launches.value)
-    scan_bytes = n * d + b * d  # the item table once + the query block
-    achieved = scan_bytes / (kernel_ms * 1e-3) / 1e9
-    # the whole step's algorithmic bytes: + Bloom words, the int16 attributes, the masks
-    step_bytes = scan_bytes
-    if filtered:
-        step_bytes += n * BLOOM_BITS // 8 + n * len(CARDINALITIES) * 2 + 3 * b * n // 8
-    log(f"ms/step {ms_step:.3f}; main scan {kernel_ms:.3f} ms ({achieved:.0f} GB/s)")
+    if bound == "hbm":
+        achieved = scan_bytes / (kernel_ms * 1e-3) / 1e9
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved = scan_ops / (kernel_ms * 1e-3) / 1e12
+        peak = {"int8": 5000.0, "bf16": 2500.0}[dtype]
+        unit = "TFLOP/s"
+    log(f"ms/step {ms_step:.3f}; main scan {kernel_ms:.3f} ms ({achieved:.0f} {unit})")
+    if wl == "binary":
+        # the Hamming scan's VALU use: 2 ops (XOR, popcount) per 32-bit word pair and query
+        extra["hamming_valu_lane_ops_per_s"] = scan_ops / (kernel_ms * 1e-3)
+        extra["hamming_valu_frac"] = extra["hamming_valu_lane_ops_per_s"] / VALU_PEAK
 
     cpu = None
     if not args.no_cpu:
-        from oracle import baseline
-
-        ns = min(args.cpu_sample, n)
-        log(f"cpu baseline on {ns} items")
-        q_cpu = queries.cpu()
-        it_cpu = items[:ns].cpu()
-        valid_fn = None
-        if filtered:
-            valid_fn = baseline.clause_sets_valid(attrs[:ns].cpu().long(), sets_t.cpu())
-        t_s, threads = baseline.time_int8(q_cpu, it_cpu, k, valid_fn=valid_fn)
-        t_full = t_s * (n / ns)
-        what = "torch.mm over 2M-row chunks + topk + lowest-id merge"
-        if filtered:
-            what = "the exact value-set filter (torch.isin) gating " + what
+        log("cpu baseline")
+        t_full, threads, sample = cpu_fn()
         cpu = {
             "value": b / t_full,
             "unit": "queries/s",
             "cores": threads,
             "kind": "port",
-            "sample": f"B={b} queries x first {ns} of {n} items ({what}), median of 3, scaled "
-                      f"x{n / ns:.1f} to the full table; host has {os.cpu_count()} logical CPUs",
+            "sample": sample + f"; host has {os.cpu_count()} logical CPUs",
         }
 
-    workload = f"int8 scan top-{k}: N={n} D={d} B={b}"
-    if filtered:
-        workload = (f"filtered int8 top-{k}: N={n} D={d} B={b}; Bloom {BLOOM_BITS} bits/item, "
-                    f"{BLOOM_K} hashes pre-filter + exact AND-of-OR clause post-check over 8 "
-                    f"attributes at {args.selectivity:.0%} target selectivity")
+    traffic = MEASURED_TRAFFIC.get((wl, n, d, b, k))
     line = {
-        "metric": "queries/sec + achieved HBM GB/s, filtered top-100 over 30Mx512 int8 items",
+        "metric": metric,
         "value": b * args.steps / wall,
         "unit": "queries/s",
         "n_gpus": 1,
@@ -251,22 +428,22 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic: per-row int8 of N(0,1) float32 rows (torch generator seeds 1234 / "
-                "99); attributes Zipf(1.1) (seed 4321), query sets numpy seed 77",
+        "dtype": dtype,
+        "data": data,
         "config": {
             "workload": workload,
             "global_batch": b,
+            "main_kernel_ms": kernel_ms,
             "achieved_hbm_gbs_whole_step": step_bytes / (ms_step * 1e-3) / 1e9,
-            "measured_selectivity": None if measured_sel is None else float(measured_sel.mean()),
+            **extra,
         },
         "roofline": {
-            "bound": "hbm",
+            "bound": bound,
             "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "peak": peak,
+            "unit": unit,
+            "frac": achieved / peak,
+            "traffic": traffic,
         },
         "cpu_baseline": cpu,
     }

@@ -143,7 +143,8 @@ __global__ void __launch_bounds__(kCandThreads) cand_scan_kernel(CandArgs a) {
   for (int j = 0; j < NC; ++j) {
     const int c = gl + j * L;
     if constexpr (kFloat) {
-      const float* q = static_cast<const float*>(a.queries) + b * (a.RB / (KIND == kCandF32 ? 4 : 2));
+      const float* q =
+          static_cast<const float*>(a.queries) + b * (a.RB / (KIND == kCandF32 ? 4 : 2));
 #pragma unroll
       for (int e = 0; e < QF; ++e) qf[j][e] = c < nchunks ? q[c * QF + e] : 0.f;
     } else {

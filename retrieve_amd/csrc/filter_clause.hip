@@ -398,7 +398,8 @@ constexpr int kTabStride = kSetDomain + 1;
 template <class T, int C>
 struct RowShape {
   static constexpr int kBytes = C * static_cast<int>(sizeof(T));
-  static constexpr int kLoad = kBytes % 16 == 0 ? 16 : kBytes % 8 == 0 ? 8 : kBytes % 4 == 0 ? 4 : 2;
+  static constexpr int kLoad =
+      kBytes % 16 == 0 ? 16 : kBytes % 8 == 0 ? 8 : kBytes % 4 == 0 ? 4 : 2;
   static constexpr int kWords = (kBytes + 3) / 4;
 };
 
@@ -876,7 +877,8 @@ extern "C" int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t 
   a.rows_per_wg = cdiv(B, gy);
   // the rows' bitmaps staged per workgroup stay within kMaxBitmapLds
   if (C > 0) {
-    const int64_t max_rows = kMaxBitmapLds / (C * kSetWords * static_cast<int64_t>(sizeof(uint64_t)));
+    const int64_t max_rows =
+        kMaxBitmapLds / (C * kSetWords * static_cast<int64_t>(sizeof(uint64_t)));
     a.rows_per_wg = a.rows_per_wg < max_rows ? a.rows_per_wg : max_rows;
   }
   // a wave's lanes carry the rows' words (bits mode) and the staged row flags

@@ -56,7 +56,9 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint16_t* __re
       if (k < D) {
         const float qk = half_to_float(q[k]);
 #pragma unroll
-        for (int i = 0; i < kGemvItems; ++i) acc[i] = __builtin_fmaf(qk, half_to_float(x[u][i]), acc[i]);
+        for (int i = 0; i < kGemvItems; ++i) {
+          acc[i] = __builtin_fmaf(qk, half_to_float(x[u][i]), acc[i]);
+        }
       }
     }
   }

@@ -12,6 +12,8 @@
 // Operand reuse: each staged item byte feeds 64 queries per wave and each register-held query
 // byte feeds every item of the grid row, so the matrix cores, not LDS or HBM, bound the
 // kernel at large batches.
+#include <type_traits>
+
 #include "profile.h"
 #include "scan_common.h"
 #include "wave_lists.h"
@@ -76,14 +78,14 @@ struct F16x32 : BF16x32 {
 };
 
 // Tiles in flight: 3 at 512-byte rows (32 KiB each), 4 below.
-template <int RB>
-constexpr int blk_stages() {
-  return RB >= 512 ? 3 : 4;
-}
+// Staged tiles: 4 when they fit in LDS beside the lists (more bytes in flight per CU), else 3
+// (512-byte rows with large k).
+constexpr int blk_min_stages(int64_t rb) { return rb >= 512 ? 3 : 4; }
+constexpr int kBlkMaxStages = 4;
 
-template <int RB>
+template <int RB, int STAGES>
 constexpr size_t blk_stage_bytes() {
-  return static_cast<size_t>(blk_stages<RB>()) * kBlkRows * RB;
+  return static_cast<size_t>(STAGES) * kBlkRows * RB;
 }
 
 // Waves per SIMD: two for rows up to 256 bytes (each one's MFMAs cover the other's waits);
@@ -140,7 +142,7 @@ __device__ inline void tile_barrier() {
 
 // SEED: per query, each workgroup's best composite over the strided sample, written to
 // lists[q * gridDim.x + workgroup] (one-entry lists); else candidate lists per (wave, query).
-template <class Op, int RB, bool SEED>
+template <class Op, int RB, bool SEED, int STAGES>
 __global__ void __launch_bounds__(kScanThreads)
     __attribute__((amdgpu_waves_per_eu(blk_waves_per_simd<RB>(), blk_waves_per_simd<RB>())))
     scan_blocked_kernel(ScanArgs a) {
@@ -149,12 +151,11 @@ __global__ void __launch_bounds__(kScanThreads)
   constexpr int TILE_BYTES = kBlkRows * RB;
   constexpr int LOADS = TILE_BYTES / (kScanThreads * 16);  // 16-byte loads per thread per tile
   constexpr int CH = RB / 16;                              // 16-byte chunks per row
-  constexpr int STAGES = blk_stages<RB>();
   static_assert(TILE_BYTES % (kScanThreads * 16) == 0, "tile must split into 16-byte loads");
   static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   int8_t* stage = reinterpret_cast<int8_t*>(smem);
-  uint64_t* scratch = reinterpret_cast<uint64_t*>(stage + blk_stage_bytes<RB>());
+  uint64_t* scratch = reinterpret_cast<uint64_t*>(stage + blk_stage_bytes<RB, STAGES>());
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid >> 6;
@@ -165,6 +166,8 @@ __global__ void __launch_bounds__(kScanThreads)
   const int64_t wg = blockIdx.x;
   const int64_t nwg = gridDim.x;
   const int64_t q0 = static_cast<int64_t>(blockIdx.y) * kBlkQpg + wave * kBlkQpw;
+  // this wave's 32-query column tiles that hold real queries (wave-uniform)
+  const int cols = q0 >= a.B ? 0 : (q0 + 32 >= a.B ? 1 : 2);
   const int8_t* Q = static_cast<const int8_t*>(a.queries);
   const int8_t* I = static_cast<const int8_t*>(a.items);
 
@@ -277,121 +280,135 @@ __global__ void __launch_bounds__(kScanThreads)
     const int64_t tn = t + (STAGES - 1) * nwg;
     if (tn < ntiles) issue(tn, (it + STAGES - 1) % STAGES);
 
-    const int8_t* src = stage + (it % STAGES) * TILE_BYTES;
-    // 2 x 2 output tiles (rows 32 i + ..., this wave's query columns 32 j + ...): four
-    // independent accumulator chains keep the matrix pipeline full
-    typename Op::Acc acc[2][2] = {{Op::zero(), Op::zero()}, {Op::zero(), Op::zero()}};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      v4i af[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int r = 32 * i + c32;
-        af[i] = *reinterpret_cast<const v4i*>(src + r * RB + (((2 * s + half) ^ (r % CH)) * 16));
-      }
+    // only the 32-query column tiles that hold real queries are multiplied (NC of them; a
+    // wave of padding only helps with the loads)
+    auto tile_body = [&](auto nc) {
+      constexpr int NC = decltype(nc)::value;
+      const int8_t* src = stage + (it % STAGES) * TILE_BYTES;
+      // 2 x 2 output tiles (rows 32 i + ..., this wave's query columns 32 j + ...): four
+      // independent accumulator chains keep the matrix pipeline full
+      typename Op::Acc acc[2][NC];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma(af[i], qf[j][s], acc[i][j]);
-    }
-    // register r of tile (i, j) holds row t * 64 + 32 i + (r / 4) * 8 + 4 half + r % 4
-    const int64_t rt = t * kBlkRows + 4 * half;
-    if constexpr (SEED) {
+        for (int j = 0; j < NC; ++j) acc[i][j] = Op::zero();
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int s = 0; s < KS; ++s) {
+        v4i af[2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = rt + 32 * i + (r / 4) * 8 + (r % 4);
-          const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            bool ok = row < n;
-            if (ok && qmask[j] != nullptr) {
-              ok = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
-            }
-            const uint64_t c = composite(Op::key(acc[i][j][r]), item);
-            best[j] = ok && c > best[j] ? c : best[j];
-          }
+        for (int i = 0; i < 2; ++i) {
+          const int r = 32 * i + c32;
+          af[i] = *reinterpret_cast<const v4i*>(src + r * RB + (((2 * s + half) ^ (r % CH)) * 16));
         }
-    } else {
-      // fast path: the max of each group of 4 registers (rows 8 g + 4 half + 0..3), and one
-      // compare per tile column against the max of its 4 group maxima
-      int32_t gm[2][2][4];
-      bool hit = false;
-      if (raw) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
+          for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(af[i], qf[j][s], acc[i][j]);
+      }
+      // register r of tile (i, j) holds row t * 64 + 32 i + (r / 4) * 8 + 4 half + r % 4
+      const int64_t rt = t * kBlkRows + 4 * half;
+      if constexpr (SEED) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, true>(acc[i][j], g);
-            hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= th[j];
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t row = rt + 32 * i + (r / 4) * 8 + (r % 4);
+            const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+              bool ok = row < n;
+              if (ok && qmask[j] != nullptr) {
+                ok = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
+              }
+              const uint64_t c = composite(Op::key(acc[i][j][r]), item);
+              best[j] = ok && c > best[j] ? c : best[j];
+            }
           }
       } else {
+        // fast path: the max of each group of 4 registers (rows 8 g + 4 half + 0..3), and one
+        // compare per tile column against the max of its 4 group maxima
+        int32_t gm[2][NC][4];
+        bool hit = false;
+        if (raw) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < NC; ++j) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, false>(acc[i][j], g);
-            hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= th[j];
-          }
-      }
-      if (__any(hit)) {
-        // slow path, narrowed by wave-uniform ballots: groups with a hit, then their registers
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              if (__ballot(gm[i][j][g] >= th[j]) == 0ull) continue;
-#pragma unroll
-              for (int u = 0; u < 4; ++u) {
-                const Score sc = acc[i][j][4 * g + u];
-                if (__ballot(sc >= ts[j]) == 0ull) continue;
-                const int64_t row = rt + 32 * i + 8 * g + u;
-                const uint32_t item = static_cast<uint32_t>(row);
-                const uint64_t c = composite(Op::key(sc), item);
-                bool keep = row < n && sc >= ts[j] && c >= tau[j];
-                if (keep && qmask[j] != nullptr) {
-                  keep = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
-                }
-                // lanes l and l ^ 32 score the same query: the upper half's entry goes second
-                const uint64_t kb = __ballot(keep);
-                const int lo = static_cast<int>(static_cast<uint32_t>(kb) >> c32 & 1u);
-                const int hi = static_cast<int>(static_cast<uint32_t>(kb >> 32) >> c32 & 1u);
-                if (keep) {
-                  lists[(32 * j + c32) * static_cast<int64_t>(a.capw) + nq[j] + (half ? lo : 0)] =
-                      c;
-                }
-                nq[j] += lo + hi;
-              }
+              for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, true>(acc[i][j], g);
+              hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= th[j];
             }
-        // a query gains at most 64 entries per tile: compact the lists that could overflow on
-        // the next one (wave_compact waits for the stores above before reading them back)
+        } else {
 #pragma unroll
-        for (int jq = 0; jq < 2; ++jq) {
-          uint64_t need = __ballot(nq[jq] > a.capw - kBlkRows) & 0xffffffffull;
-          while (need != 0ull) {
-            const int c = __builtin_ctzll(need);
-            need &= need - 1;
-            const int q = 32 * jq + c;
-            if (lane == c) cnt[q] = nq[jq];
-            const uint64_t nt = wave_compact(lists + q * static_cast<int64_t>(a.capw), &cnt[q],
-                                             scratch + wave * a.capw, a.capw, a.k);
-            if (c32 == c) {
-              nq[jq] = cnt[q];
-              if (nt > tau[jq]) {
-                tau[jq] = nt;
-                ts[jq] = Op::thresh(nt);
-                th[jq] = Op::skey(ts[jq]);
-              }
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+#pragma unroll
+              for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, false>(acc[i][j], g);
+              hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= th[j];
             }
-          }
         }
-        raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
+        if (__any(hit)) {
+          // slow path, narrowed by wave-uniform ballots: groups with a hit, then their registers
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < NC; ++j)
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                if (__ballot(gm[i][j][g] >= th[j]) == 0ull) continue;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  const Score sc = acc[i][j][4 * g + u];
+                  if (__ballot(sc >= ts[j]) == 0ull) continue;
+                  const int64_t row = rt + 32 * i + 8 * g + u;
+                  const uint32_t item = static_cast<uint32_t>(row);
+                  const uint64_t c = composite(Op::key(sc), item);
+                  bool keep = row < n && sc >= ts[j] && c >= tau[j];
+                  if (keep && qmask[j] != nullptr) {
+                    keep = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
+                  }
+                  // lanes l and l ^ 32 score the same query: the upper half's entry goes second
+                  const uint64_t kb = __ballot(keep);
+                  const int lo = static_cast<int>(static_cast<uint32_t>(kb) >> c32 & 1u);
+                  const int hi = static_cast<int>(static_cast<uint32_t>(kb >> 32) >> c32 & 1u);
+                  if (keep) {
+                    lists[(32 * j + c32) * static_cast<int64_t>(a.capw) + nq[j] + (half ? lo : 0)] =
+                        c;
+                  }
+                  nq[j] += lo + hi;
+                }
+              }
+          // a query gains at most 64 entries per tile: compact the lists that could overflow on
+          // the next one (wave_compact waits for the stores above before reading them back)
+#pragma unroll
+          for (int jq = 0; jq < NC; ++jq) {
+            uint64_t need = __ballot(nq[jq] > a.capw - kBlkRows) & 0xffffffffull;
+            while (need != 0ull) {
+              const int c = __builtin_ctzll(need);
+              need &= need - 1;
+              const int q = 32 * jq + c;
+              if (lane == c) cnt[q] = nq[jq];
+              const uint64_t nt = wave_compact(lists + q * static_cast<int64_t>(a.capw), &cnt[q],
+                                               scratch + wave * a.capw, a.capw, a.k);
+              if (c32 == c) {
+                nq[jq] = cnt[q];
+                if (nt > tau[jq]) {
+                  tau[jq] = nt;
+                  ts[jq] = Op::thresh(nt);
+                  th[jq] = Op::skey(ts[jq]);
+                }
+              }
+            }
+          }
+          raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
+        }
       }
+    };
+    if (cols == 2) {
+      tile_body(std::integral_constant<int, 2>{});
+    } else if (cols == 1) {
+      tile_body(std::integral_constant<int, 1>{});
     }
   }
 
@@ -410,29 +427,38 @@ __global__ void __launch_bounds__(kScanThreads)
   }
 }
 
-template <int RB>
-static size_t blk_lds(int capw) {
-  return blk_stage_bytes<RB>() + kScanWaves * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
+constexpr size_t kMaxLds = 160 * 1024;
+
+static size_t blk_lds(int64_t row_bytes, int stages, int capw) {
+  return static_cast<size_t>(stages) * kBlkRows * row_bytes +
+         kScanWaves * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
+}
+
+template <class Op, int RB, bool SEED, int STAGES>
+static int launch_blk_staged(const ScanArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
+  const void* fn = reinterpret_cast<const void*>(scan_blocked_kernel<Op, RB, SEED, STAGES>);
+  if (lds > 65536) {
+    RT_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds)));
+  }
+  scan_blocked_kernel<Op, RB, SEED, STAGES><<<grid, kScanThreads, lds, stream>>>(a);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
 }
 
 template <class Op, int RB>
 static int launch_blk(const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed,
                       hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.gx), static_cast<unsigned>(nqg));
-  const size_t lds = blk_lds<RB>(seed ? 0 : p.capw);
-  const void* fn = seed ? reinterpret_cast<const void*>(scan_blocked_kernel<Op, RB, true>)
-                        : reinterpret_cast<const void*>(scan_blocked_kernel<Op, RB, false>);
-  if (lds > 65536) {
-    RT_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     static_cast<int>(lds)));
-  }
+  const int capw = seed ? 0 : p.capw;
+  const bool deep = blk_lds(RB, kBlkMaxStages, capw) <= kMaxLds;
+  const size_t lds = blk_lds(RB, deep ? kBlkMaxStages : 3, capw);
   if (seed) {
-    scan_blocked_kernel<Op, RB, true><<<grid, kScanThreads, lds, stream>>>(a);
-  } else {
-    scan_blocked_kernel<Op, RB, false><<<grid, kScanThreads, lds, stream>>>(a);
+    return deep ? launch_blk_staged<Op, RB, true, kBlkMaxStages>(a, grid, lds, stream)
+                : launch_blk_staged<Op, RB, true, 3>(a, grid, lds, stream);
   }
-  RT_CHECK_HIP(hipGetLastError());
-  return kOk;
+  return deep ? launch_blk_staged<Op, RB, false, kBlkMaxStages>(a, grid, lds, stream)
+              : launch_blk_staged<Op, RB, false, 3>(a, grid, lds, stream);
 }
 
 template <class Op>
@@ -450,11 +476,8 @@ static int dispatch_blk(int64_t row_bytes, const ScanArgs& a, const PassPlan& p,
 }
 
 static size_t blk_lds_for(int64_t row_bytes, int capw) {
-  return static_cast<size_t>(row_bytes >= 512 ? 3 : 4) * kBlkRows * row_bytes +
-         kScanWaves * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
+  return blk_lds(row_bytes, blk_min_stages(row_bytes), capw);
 }
-
-constexpr size_t kMaxLds = 160 * 1024;
 
 // List capacity: k plus a tile's appends (64 per query), a power of two (sorted whole).
 static int blk_capw(int64_t k) { return static_cast<int>(next_pow2(k + kBlkRows)); }

@@ -177,7 +177,9 @@ __global__ void __launch_bounds__(kScanThreads) scan_hamming_kernel(ScanArgs a, 
   for (int i = lane; i < qpw; i += kWave) a.counts[slot * qpw + i] = cnt[i];
 }
 
-static int ham_capw(int64_t k) { return static_cast<int>(align_up(static_cast<size_t>(k) + kWave, 64)); }
+static int ham_capw(int64_t k) {
+  return static_cast<int>(align_up(static_cast<size_t>(k) + kWave, 64));
+}
 
 static size_t ham_lds(int qpw, int scratch_n, int64_t W) {
   return static_cast<size_t>(qpw) * W * sizeof(uint64_t) +
@@ -234,8 +236,9 @@ extern "C" size_t rt_hamming_scan_topk_workspace(int64_t B, int64_t N, int64_t W
       .total;
 }
 
-extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits,
-                                    int64_t N, int64_t W, int64_t k, const uint64_t* mask,
+extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B,
+                                    const uint64_t* item_bits, int64_t N, int64_t W, int64_t k,
+                                    const uint64_t* mask,
                                     int64_t mask_words, int64_t* out_ids, void* out_scores,
                                     int score_f32, void* workspace, size_t workspace_bytes,
                                     hipStream_t stream) {
@@ -246,7 +249,8 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const
   RT_CHECK_ARG(W == 1 || W == 2 || W == 4 || W == 8 || W == 16,
                "W (64-bit words per code) must be in {1, 2, 4, 8, 16}, got %lld",
                static_cast<long long>(W));
-  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(item_bits) % 16 == 0, "item_bits must be 16-byte aligned");
+  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(item_bits) % 16 == 0,
+               "item_bits must be 16-byte aligned");
   RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
   if (B == 0) return kOk;
   const int kind = score_f32 ? kScoreF32FromI32 : kScoreI32;

@@ -352,7 +352,9 @@ using namespace rt;
 
 extern "C" size_t rt_int8_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
   (void)D;
-  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k), kScanWaves * kTile).total;
+  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k),
+                   kScanWaves * kTile)
+      .total;
 }
 
 extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t* items,
@@ -365,7 +367,9 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
 
 extern "C" size_t rt_dense_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
   (void)D;
-  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k), kScanWaves * kTile).total;
+  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k),
+                   kScanWaves * kTile)
+      .total;
 }
 
 extern "C" int rt_dense_scan_topk(const void* queries, int64_t B, const void* items, int64_t N,

@@ -27,7 +27,7 @@ def _check_items(**tables: Tensor) -> None:
 
 # From this batch on the dense scans run the register-blocked kernel (256 queries per
 # workgroup, item tiles read once per 256 queries) instead of 16 queries per wave.
-BLOCKED_MIN_BATCH = 128
+BLOCKED_MIN_BATCH = 32
 _BLOCKED_ROW_BYTES = (128, 256, 512)
 
 
@@ -347,7 +347,8 @@ def clause_mask_scores(
     scores: Tensor, item_clause_attrs: Tensor, clause_is_reverse: Tensor,
     query_clause_attrs: Tensor,
 ) -> Tensor:
-    """``where(clause_mask(...), scores, -inf)`` in one pass (``ops/triton/clause_mask.py:284-303``);
+    """``where(clause_mask(...), scores, -inf)`` in one pass
+    (``ops/triton/clause_mask.py:284-303``);
     ``scores`` must be ``[B, N]`` float32."""
     rev, q = _clause_prep(item_clause_attrs, clause_is_reverse, query_clause_attrs)
     b, n = q.shape[0], item_clause_attrs.shape[0]
@@ -375,8 +376,9 @@ def clause_bits(
     at bit ``63 - d % 64`` (the order of ``silvertorch/.../ops/official/__init__.py:33-35``).
     ``query_values`` is ``[B, C]`` (the reference predicate) or ``[B, C, V]`` value sets, ``-1``
     pads: clause ``c`` is active iff a value is not ``-1`` and matches iff an item value is in
-    the set. ``item_clause_attrs`` may be int16 / int32 (a compact copy of the table). ``and_mask`` (``[B, >= ceil(N/64)]`` words, same bit layout) is AND-ed in, e.g. a
-    Bloom search's ``[B, n_bundles * 32]`` pre-filter."""
+    the set. ``item_clause_attrs`` may be int16 / int32 (a compact copy of the table).
+    ``and_mask`` (``[B, >= ceil(N/64)]`` words, same bit layout) is AND-ed in, e.g. a Bloom
+    search's ``[B, n_bundles * 32]`` pre-filter."""
     rev, q = _clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
     b, n = q.shape[0], item_clause_attrs.shape[0]
     w = (n + 63) // 64

@@ -205,9 +205,9 @@ def _search_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max
         raise ValueError(f"max_stack_size must be <= {MAX_STACK}")
     plans = plans.contiguous()
     data = plans[8 * plan_count :]
-    return _bloom_search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), plans, data,
-                   data.numel() * 8, int(plan_count), int(max_stack_size), int(k), int(hash_k),
-                   bool(return_bool_mask))
+    return _bloom_search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), plans,
+                         data, data.numel() * 8, int(plan_count), int(max_stack_size), int(k),
+                         int(hash_k), bool(return_bool_mask))
 
 
 def _search_batch(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data,
@@ -228,9 +228,9 @@ def _search_batch(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data,
     dev_data = torch.zeros((nbytes + 7) // 8, dtype=torch.int64, device=dev)
     if nbytes:
         dev_data.view(torch.uint8)[:nbytes].copy_(data.view(torch.uint8).to(dev))
-    return _bloom_search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), offs.to(dev),
-                   dev_data, nbytes, offs.numel() // 8, max_stack, int(k), int(hash_k),
-                   bool(return_bool_mask))
+    return _bloom_search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(),
+                         offs.to(dev), dev_data, nbytes, offs.numel() // 8, max_stack, int(k),
+                         int(hash_k), bool(return_bool_mask))
 
 
 _LIB.impl("bloom_index_search_batch_prepared", _search_prepared, "CUDA")
