@@ -42,7 +42,10 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
 VALU_PEAK = 256 * 64 * 2.4e9  # 32-bit lane-ops/s: 256 CUs x 64 lanes x 2.4 GHz
 # HBM bytes per launch of the main scan (FETCH_SIZE + WRITE_SIZE, copy-calibrated), measured with
 # rocprofv3 --pmc for these exact workloads; keyed by (workload, N, D, B, k). See profiles/.
-MEASURED_TRAFFIC: dict = {}
+MEASURED_TRAFFIC: dict = {
+    # profiles/filtered_int8_30Mx512_b16.md: FETCH_SIZE 7,580,854 KiB x 2 + WRITE_SIZE 5,786 KiB
+    ("filtered", 30_000_000, 512, 16, 100): 15_531_514_360,
+}
 CARDINALITIES = (16, 32, 64, 128, 256, 512, 1000, 1000)
 BLOOM_BITS, BLOOM_K, HASH_K = 64, 3, 7
 
