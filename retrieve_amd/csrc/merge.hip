@@ -223,7 +223,7 @@ __device__ uint64_t block_select_desc(const uint64_t* keys, int n, int kth, unsi
 // entries are gathered behind the current best (at most k entries), the k-th largest of the
 // union is found by radix select and only the entries >= it are kept; the survivors are
 // sorted at the end. With tau_out set, only the k-th composite is written (0 when fewer than
-// k entries exist: no bound).
+// k entries exist: no bound; with tau_keep, the larger of it and the bound already there).
 template <int KP>
 __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   __shared__ uint64_t buf[KP + kMergeChunk];
@@ -356,7 +356,11 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   }
 
   if (m.tau_out != nullptr) {
-    if (tid == 0) m.tau_out[q] = held >= k ? buf[k - 1] : 0ull;
+    if (tid == 0) {
+      const uint64_t t = held >= k ? buf[k - 1] : 0ull;
+      const uint64_t old = m.tau_keep ? m.tau_out[q] : 0ull;
+      m.tau_out[q] = t > old ? t : old;
+    }
     return;
   }
   for (int j = tid; j < k; j += kMergeThreads) {

@@ -1,11 +1,13 @@
 // Large-batch dense scans with the exact fused top-k: register-blocked 32x32 MFMA tiles.
 //
-// A workgroup (4 waves) owns 256 queries: each wave keeps the B-operand fragments of its 64
-// queries in registers for the whole kernel. Item tiles of 64 rows are dealt round-robin to
-// the workgroups of a query group; a tile is read once from HBM with coalesced nontemporal
-// loads, staged (double-buffered) in LDS, and every wave multiplies it against its 64 queries
-// as 2 x 2 tiles of 32x32 outputs (v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_{bf16,f16}:
-// each instruction consumes 32 bytes of K per row). Lane l of an output tile holds query
+// A workgroup owns 256 queries: each 64-query group's B-operand fragments stay in the registers
+// of its wave(s) for the whole kernel. Item tiles of 64 rows are dealt round-robin to the
+// workgroups of a query group; a tile is read once from HBM with coalesced loads straight into
+// LDS (3-4 stages in flight), and each wave multiplies its rows against its 64 queries in 32x32
+// output tiles (v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_{bf16,f16}: each instruction
+// consumes 32 bytes of K per row). At 512-byte rows two waves share a query group, 32 rows each
+// (8 waves, two per SIMD: one's MFMAs run while the other reads LDS or tests its scores); below,
+// one wave takes all 64 rows (4 waves, two workgroups per CU). Lane l of an output tile holds query
 // (col tile * 32 + l % 32) and, in register i, item (row tile * 32 + (i/4)*8 + (l/32)*4 + i%4).
 // Per MFMA, lane l feeds bytes [32 s + 16 (l / 32), +16) of its row on both sides.
 //
@@ -28,7 +30,15 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 constexpr int kBlkRows = 64;      // items per staged tile
 constexpr int kBlkQpw = 64;       // queries per wave
-constexpr int kBlkQpg = kScanWaves * kBlkQpw;  // queries per workgroup (query group)
+constexpr int kBlkQgWaves = 4;    // 64-query groups per workgroup
+constexpr int kBlkQpg = kBlkQgWaves * kBlkQpw;  // queries per workgroup (query group)
+
+// Waves per query group: at 512-byte rows two (each takes 32 rows of a tile: 8 waves, two per
+// SIMD, fit the registers of 64 queries' fragments); below, one wave takes all 64 rows and two
+// 4-wave workgroups share a CU.
+constexpr int blk_row_halves(int64_t rb) { return rb >= 512 ? 2 : 1; }
+constexpr int blk_waves(int64_t rb) { return kBlkQgWaves * blk_row_halves(rb); }
+constexpr int blk_threads(int64_t rb) { return blk_waves(rb) * kWave; }
 // Cache-policy bits of the main pass's direct-to-LDS loads (streamed once: nontemporal).
 constexpr int kNontemporal = 2;
 
@@ -77,7 +87,6 @@ struct F16x32 : BF16x32 {
   }
 };
 
-// Tiles in flight: 3 at 512-byte rows (32 KiB each), 4 below.
 // Staged tiles: 4 when they fit in LDS beside the lists (more bytes in flight per CU), else 3
 // (512-byte rows with large k).
 constexpr int blk_min_stages(int64_t rb) { return rb >= 512 ? 3 : 4; }
@@ -88,11 +97,10 @@ constexpr size_t blk_stage_bytes() {
   return static_cast<size_t>(STAGES) * kBlkRows * RB;
 }
 
-// Waves per SIMD: two for rows up to 256 bytes (each one's MFMAs cover the other's waits);
-// one at 512-byte rows, where 64 queries' fragments take 128 registers.
+// Waves per SIMD: two (one 8-wave workgroup per CU at 512-byte rows, two 4-wave ones below).
 template <int RB>
 constexpr int blk_waves_per_simd() {
-  return RB >= 512 ? 1 : 2;
+  return 2;
 }
 
 __device__ inline int32_t imax(int32_t a, int32_t b) { return a > b ? a : b; }
@@ -143,15 +151,19 @@ __device__ inline void tile_barrier() {
 // SEED: per query, each workgroup's best composite over the strided sample, written to
 // lists[q * gridDim.x + workgroup] (one-entry lists); else candidate lists per (wave, query).
 template <class Op, int RB, bool SEED, int STAGES>
-__global__ void __launch_bounds__(kScanThreads)
+__global__ void __launch_bounds__(blk_threads(RB))
     __attribute__((amdgpu_waves_per_eu(blk_waves_per_simd<RB>(), blk_waves_per_simd<RB>())))
     scan_blocked_kernel(ScanArgs a) {
   using Score = typename Op::Score;
   constexpr int KS = RB / 32;  // MFMA steps per row
+  constexpr int kBlkRowHalves = blk_row_halves(RB);
+  constexpr int kBlkWaves = blk_waves(RB);
+  constexpr int kBlkThreads = blk_threads(RB);
+  constexpr int RTW = 2 / kBlkRowHalves;  // 32-row tiles per wave
   constexpr int TILE_BYTES = kBlkRows * RB;
-  constexpr int LOADS = TILE_BYTES / (kScanThreads * 16);  // 16-byte loads per thread per tile
+  constexpr int LOADS = TILE_BYTES / (kBlkThreads * 16);  // 16-byte loads per thread per tile
   constexpr int CH = RB / 16;                              // 16-byte chunks per row
-  static_assert(TILE_BYTES % (kScanThreads * 16) == 0, "tile must split into 16-byte loads");
+  static_assert(TILE_BYTES % (kBlkThreads * 16) == 0, "tile must split into 16-byte loads");
   static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   int8_t* stage = reinterpret_cast<int8_t*>(smem);
@@ -161,11 +173,13 @@ __global__ void __launch_bounds__(kScanThreads)
   const int wave = tid >> 6;
   const int c32 = lane & 31;
   const int half = lane >> 5;
-  int* cnt = reinterpret_cast<int*>(scratch + kScanWaves * a.capw) + wave * kBlkQpw;
+  int* cnt = reinterpret_cast<int*>(scratch + kBlkWaves * a.capw) + wave * kBlkQpw;
+  const int wq = wave % kBlkQgWaves;  // this wave's 64-query group in the workgroup
+  const int wr = wave / kBlkQgWaves;  // and its 32 rows of each tile
 
   const int64_t wg = blockIdx.x;
   const int64_t nwg = gridDim.x;
-  const int64_t q0 = static_cast<int64_t>(blockIdx.y) * kBlkQpg + wave * kBlkQpw;
+  const int64_t q0 = static_cast<int64_t>(blockIdx.y) * kBlkQpg + wq * kBlkQpw;
   // this wave's 32-query column tiles that hold real queries (wave-uniform)
   const int cols = q0 >= a.B ? 0 : (q0 + 32 >= a.B ? 1 : 2);
   const int8_t* Q = static_cast<const int8_t*>(a.queries);
@@ -197,15 +211,19 @@ __global__ void __launch_bounds__(kScanThreads)
   int32_t th[2] = {Op::skey(ts[0]), Op::skey(ts[1])};
   bool raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
   uint64_t best[2] = {0ull, 0ull};  // SEED
-  // list slot of this wave: query group (64 queries) g = blockIdx.y * 4 + wave, slot g * nwg + wg
-  const int64_t slot = (static_cast<int64_t>(blockIdx.y) * kScanWaves + wave) * nwg + wg;
+  // list slot of this wave: query group (64 queries) g = blockIdx.y * 4 + wq; a query's lists
+  // are slots g * S + s, s = wg * 2 + wr (S = 2 nwg per query)
+  const int64_t slot =
+      ((static_cast<int64_t>(blockIdx.y) * kBlkQgWaves + wq) * nwg + wg) * kBlkRowHalves + wr;
   uint64_t* lists = a.lists + slot * kBlkQpw * static_cast<int64_t>(a.capw);
   // list lengths of this lane's two queries (the same in both halves of the wave): each list
   // belongs to this wave alone, so appends take positions from ballots, not atomics
   int nq[2] = {0, 0};
 
   const int64_t n = a.n_rows;
-  const int64_t ntiles = cdiv(n, kBlkRows);
+  // the main pass may scan every tstride-th tile only (the threshold sample pass)
+  const int64_t tstride = !SEED && a.tile_stride > 1 ? a.tile_stride : 1;
+  const int64_t ntiles = cdiv(cdiv(n, kBlkRows), tstride);
   // Staged tile layout (no padding): row r's 16-byte chunk c sits at r * RB + (c ^ (r % CH)) * 16,
   // so the 32 rows of an MFMA read start on different banks. A wave's direct-to-LDS load writes
   // 1 KiB contiguously in lane order, so the swizzle goes into the global address each lane
@@ -213,14 +231,15 @@ __global__ void __launch_bounds__(kScanThreads)
   int toff[LOADS];  // this lane's byte offset in a full tile (row r, swizzled chunk c)
 #pragma unroll
   for (int l = 0; l < LOADS; ++l) {
-    const int sidx = l * kScanThreads + wave * kWave + lane;  // 16-byte slot of the tile
+    const int sidx = l * kBlkThreads + wave * kWave + lane;  // 16-byte slot of the tile
     const int r = sidx / CH;
     toff[l] = r * RB + ((sidx % CH) ^ (r % CH)) * 16;
   }
   // Several query groups (gridDim.y > 1) read the same tiles from this XCD's L2: keep the lines
   // (temporal loads); with one group each tile is read once and streams past (nontemporal).
   const bool shared_tiles = gridDim.y > 1;
-  auto issue = [&](int64_t tt, int st) {
+  auto issue = [&](int64_t lt, int st) {
+    const int64_t tt = lt * tstride;  // the tile in the item table
     int8_t* base = stage + st * TILE_BYTES;
     if (!SEED && (tt + 1) * kBlkRows <= n) {
       // a full tile of consecutive rows: a uniform tile address plus 32-bit lane offsets
@@ -230,7 +249,7 @@ __global__ void __launch_bounds__(kScanThreads)
         // (the global address goes through a named pointer: passing the sum straight to the
         // builtin drops the kernel from the host-side compile)
         const int8_t* g = tile + toff[l];
-        int8_t* dst = base + (l * kScanThreads + wave * kWave) * 16;
+        int8_t* dst = base + (l * kBlkThreads + wave * kWave) * 16;
         if (shared_tiles) {
           __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(dst), 16,
                                            0, 0);
@@ -249,7 +268,7 @@ __global__ void __launch_bounds__(kScanThreads)
       const int8_t* g = I + row * a.row_stride * RB + toff[l] % RB;
       __builtin_amdgcn_global_load_lds(
           g,
-          (__attribute__((address_space(3))) void*)(base + (l * kScanThreads + wave * kWave) * 16),
+          (__attribute__((address_space(3))) void*)(base + (l * kBlkThreads + wave * kWave) * 16),
           16, 0, 0);
     }
   };
@@ -287,32 +306,32 @@ __global__ void __launch_bounds__(kScanThreads)
       const int8_t* src = stage + (it % STAGES) * TILE_BYTES;
       // 2 x 2 output tiles (rows 32 i + ..., this wave's query columns 32 j + ...): four
       // independent accumulator chains keep the matrix pipeline full
-      typename Op::Acc acc[2][NC];
+      typename Op::Acc acc[RTW][NC];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RTW; ++i)
 #pragma unroll
         for (int j = 0; j < NC; ++j) acc[i][j] = Op::zero();
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        v4i af[2];
+        v4i af[RTW];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int r = 32 * i + c32;
+        for (int i = 0; i < RTW; ++i) {
+          const int r = 32 * (wr + i) + c32;
           af[i] = *reinterpret_cast<const v4i*>(src + r * RB + (((2 * s + half) ^ (r % CH)) * 16));
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < RTW; ++i)
 #pragma unroll
           for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(af[i], qf[j][s], acc[i][j]);
       }
       // register r of tile (i, j) holds row t * 64 + 32 i + (r / 4) * 8 + 4 half + r % 4
-      const int64_t rt = t * kBlkRows + 4 * half;
+      const int64_t rt = t * tstride * kBlkRows + 4 * half;
       if constexpr (SEED) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < RTW; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int64_t row = rt + 32 * i + (r / 4) * 8 + (r % 4);
+            const int64_t row = rt + 32 * (wr + i) + (r / 4) * 8 + (r % 4);
             const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
@@ -327,11 +346,11 @@ __global__ void __launch_bounds__(kScanThreads)
       } else {
         // fast path: the max of each group of 4 registers (rows 8 g + 4 half + 0..3), and one
         // compare per tile column against the max of its 4 group maxima
-        int32_t gm[2][NC][4];
+        int32_t gm[RTW][NC][4];
         bool hit = false;
         if (raw) {
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < RTW; ++i)
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
 #pragma unroll
@@ -340,7 +359,7 @@ __global__ void __launch_bounds__(kScanThreads)
             }
         } else {
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < RTW; ++i)
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
 #pragma unroll
@@ -351,7 +370,7 @@ __global__ void __launch_bounds__(kScanThreads)
         if (__any(hit)) {
           // slow path, narrowed by wave-uniform ballots: groups with a hit, then their registers
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < RTW; ++i)
 #pragma unroll
             for (int j = 0; j < NC; ++j)
 #pragma unroll
@@ -361,7 +380,7 @@ __global__ void __launch_bounds__(kScanThreads)
                 for (int u = 0; u < 4; ++u) {
                   const Score sc = acc[i][j][4 * g + u];
                   if (__ballot(sc >= ts[j]) == 0ull) continue;
-                  const int64_t row = rt + 32 * i + 8 * g + u;
+                  const int64_t row = rt + 32 * (wr + i) + 8 * g + u;
                   const uint32_t item = static_cast<uint32_t>(row);
                   const uint64_t c = composite(Op::key(sc), item);
                   bool keep = row < n && sc >= ts[j] && c >= tau[j];
@@ -379,7 +398,7 @@ __global__ void __launch_bounds__(kScanThreads)
                   nq[j] += lo + hi;
                 }
               }
-          // a query gains at most 64 entries per tile: compact the lists that could overflow on
+          // a query gains at most 32 entries per tile: compact the lists that could overflow on
           // the next one (wave_compact waits for the stores above before reading them back)
 #pragma unroll
           for (int jq = 0; jq < NC; ++jq) {
@@ -419,7 +438,7 @@ __global__ void __launch_bounds__(kScanThreads)
       const uint64_t o = __shfl_xor(best[j], 32);
       const uint64_t b = o > best[j] ? o : best[j];
       const int64_t q = q0 + 32 * j + c32;
-      if (half == 0 && q < a.B) a.lists[q * nwg + wg] = b;
+      if (half == 0 && q < a.B) a.lists[(q * nwg + wg) * kBlkRowHalves + wr] = b;
     }
   } else if (half == 0) {
     a.counts[slot * kBlkQpw + c32] = nq[0];
@@ -431,7 +450,7 @@ constexpr size_t kMaxLds = 160 * 1024;
 
 static size_t blk_lds(int64_t row_bytes, int stages, int capw) {
   return static_cast<size_t>(stages) * kBlkRows * row_bytes +
-         kScanWaves * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
+         blk_waves(row_bytes) * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
 }
 
 template <class Op, int RB, bool SEED, int STAGES>
@@ -441,7 +460,7 @@ static int launch_blk_staged(const ScanArgs& a, dim3 grid, size_t lds, hipStream
     RT_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds)));
   }
-  scan_blocked_kernel<Op, RB, SEED, STAGES><<<grid, kScanThreads, lds, stream>>>(a);
+  scan_blocked_kernel<Op, RB, SEED, STAGES><<<grid, blk_threads(RB), lds, stream>>>(a);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }
@@ -479,6 +498,13 @@ static size_t blk_lds_for(int64_t row_bytes, int capw) {
   return blk_lds(row_bytes, blk_min_stages(row_bytes), capw);
 }
 
+// The threshold sample pass (512-byte rows, batches of at least kSampleMinBatch queries: where
+// the list appends behind the seed's bound cost more than the pass): every kSampleTileStride-th
+// tile, when that gives kSampleMinTiles tiles or more.
+constexpr int64_t kSampleMinBatch = 512;
+constexpr int64_t kSampleTileStride = 8;
+constexpr int64_t kSampleMinTiles = 4096;
+
 // List capacity: k plus a tile's appends (64 per query), a power of two (sorted whole).
 static int blk_capw(int64_t k) { return static_cast<int>(next_pow2(k + kBlkRows)); }
 
@@ -503,9 +529,10 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   if (hipGetDevice(&dev) == hipSuccess) {
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   }
-  const int64_t per_cu = row_bytes >= 512 ? 1 : 2;  // blk_waves_per_simd
-  const ScanPlan plan = plan_scan(B, N, k, kBlkQpg, kBlkQpg, cus * per_cu,
-                                  blk_capw(k), kBlkRows);
+  // workgroups resident per CU: one 8-wave workgroup at 512-byte rows, two 4-wave ones below
+  const int64_t per_cu = row_bytes >= 512 ? 1 : 2;
+  const ScanPlan plan = plan_scan(B, N, k, kBlkQpg, blk_waves(row_bytes) * kBlkQpw,
+                                  cus * per_cu, blk_capw(k), kBlkRows);
   RT_CHECK_ARG(blk_lds_for(row_bytes, plan.main.capw) <= kMaxLds,
                "k = %lld is too large for the blocked scan at %lld-byte rows",
                static_cast<long long>(k), static_cast<long long>(row_bytes));
@@ -556,6 +583,24 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   a.row_stride = 1;
   a.capw = plan.main.capw;
   a.tau_in = plan.seeded ? tau : nullptr;
+  if (plan.seeded && row_bytes >= 512 && B >= kSampleMinBatch &&
+      N >= kSampleMinTiles * kSampleTileStride * kBlkRows) {
+    // at large batches the list appends behind a loose bound cost more than the matrix work:
+    // the exact k-th over every kSampleTileStride-th tile (the main kernel on those tiles, then
+    // a threshold merge) tightens the bound about N / (sample rows) fold for the main pass
+    a.tile_stride = kSampleTileStride;
+    int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, stream);
+    if (st != kOk) return st;
+    m.capw = plan.main.capw;
+    m.S = plan.main.S;
+    m.tau_out = tau;
+    m.tau_keep = true;
+    st = launch_merge(m, stream);
+    if (st != kOk) return st;
+    m.tau_out = nullptr;
+    m.tau_keep = false;
+    a.tile_stride = 1;
+  }
   hipEvent_t stop;
   profile_begin(stream, &stop);
   int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, stream);
@@ -575,8 +620,9 @@ using namespace rt;
 
 extern "C" size_t rt_blocked_scan_topk_workspace(int64_t B, int64_t N, int64_t row_bytes,
                                                  int64_t k) {
-  (void)row_bytes;
-  return plan_scan(B, N, k, kBlkQpg, kBlkQpg, kMaxResidentWorkgroups, blk_capw(k), kBlkRows).total;
+  return plan_scan(B, N, k, kBlkQpg, blk_waves(row_bytes) * kBlkQpw, kMaxResidentWorkgroups,
+                   blk_capw(k), kBlkRows)
+      .total;
 }
 
 // dtype: 0 int8 (int32 scores), 1 bf16, 2 fp16 (float scores); D elements per row.

@@ -27,6 +27,8 @@ struct ScanArgs {
   const void* items;       // [N, D] (or [N, W] words)
   int64_t n_rows;          // rows of this pass's index space
   int64_t row_stride;      // item index = row * row_stride (the sample pass strides)
+  int64_t tile_stride;     // blocked main kernel: pass tile t reads tile t * tile_stride (0, 1:
+                           // every tile)
   int64_t strip;           // rows per workgroup, a multiple of kTile
   int k;
   int qpw;                 // queries per wave (a query group), for scans that vary it
@@ -54,6 +56,7 @@ struct MergeArgs {
   int64_t B;
   int k;
   uint64_t* tau_out;   // threshold mode: [B]
+  bool tau_keep;       // threshold mode: write max(tau_out[q], the new bound)
   int64_t* out_ids;    // final mode: [B, k]
   void* out_scores;    // final mode: [B, k]
   int score_kind;

@@ -122,3 +122,12 @@ def test_errors(dev):
         torch.ops.retrieve.dense_scan_topk(q, it.half(), 3)
     with pytest.raises(ValueError):
         torch.ops.retrieve.dense_scan_topk(q[:, :32], it, 3)
+
+
+def test_large_batch_sample_pass(dev):
+    """bf16 at B = 256 over 2.2M clustered rows: the blocked kernel's seeded path."""
+    g = rng(18)
+    centres = g.standard_normal((64, 128))
+    it = _clustered(g, 2_200_000, 128, centres)
+    q = _clustered(g, 256, 128, centres)
+    _check(dev, q, it, 100)

@@ -199,3 +199,20 @@ def test_large_batch_seeded_ties_masked(dev):
     mask = g.random((130, 50000)) < 0.05
     mask[7] = False
     _check(dev, q[:130], items[:50000], 100, mask)
+
+
+def test_large_batch_sample_pass(dev):
+    """512-byte rows, B >= 512 over N >= 2.1M rows run the threshold sample pass (every 8th
+    tile) before the main pass: heavy ties across the sampled and unsampled tiles, and a mask
+    with an empty row and a row whose few passing items miss the sample."""
+    g = rng(17)
+    base = g.integers(-127, 128, (256, 512), dtype=np.int8)
+    n = 2_100_000
+    items = base[g.integers(0, 256, n)]
+    q = g.integers(-128, 128, (512, 512), dtype=np.int8)
+    _check(dev, q, items, 100)
+    mask = g.random((512, n)) < 0.02
+    mask[3] = False
+    mask[5] = False
+    mask[5, 64 * 9 : 64 * 9 + 40] = True  # only in an unsampled tile
+    _check(dev, q, items, 100, mask)
