@@ -72,7 +72,7 @@ int rt_blocked_scan_topk(const void* queries, int64_t B, const void* items, int6
 /* Exact 1-bit Hamming top-k over a full code table: query_bits [B, W] x item_bits [N, W]
  * (uint64 words, bit b of word w = dimension 64 w + b), score = 64 W - 2 popcount(q ^ item),
  * top-k by (score desc, index asc) -> ids int64 [B, k], scores [B, k] (int32, or float when
- * score_f32 != 0). W in {1, 2, 4, 8, 16}; 1 <= k <= 1024. `mask` as for rt_int8_scan_topk.
+ * score_f32 != 0). 1 <= W <= 16; 1 <= k <= 1024. `mask` as for rt_int8_scan_topk.
  * Replaces: the Triton full-scan kernel + torch.topk of
  *   retrieve/src/retrieve/ops/triton/oporp_1bit_match_topk.py:47-122, 217-234, 261-273
  *   (torch.ops.retrieve.oporp_1bit_match_topk_full). */
@@ -118,6 +118,12 @@ size_t rt_mask_compact_workspace(int64_t B, int64_t N);
 int rt_mask_compact(const uint64_t* mask, int64_t B, int64_t N, int64_t* out_indices,
                     int64_t* counts, void* workspace, size_t workspace_bytes,
                     rt_stream_t stream);
+
+/* [B, N] 0/1 bytes (a bool mask) -> packed words [B, ceil(N/64)] (layout above), the form the
+ * scans take. Replaces: the boolean `mask` argument of PostfilterKNN.forward / masked_topk
+ *   (retrieve/src/retrieve/modules/knn.py:68-76, functional.py:57-85) handed to a fused scan. */
+int rt_pack_mask(const uint8_t* valid, int64_t B, int64_t N, uint64_t* words,
+                 rt_stream_t stream);
 
 /* ---- Bloom index (bit-sliced 2048-doc bundles) -----------------------------------------
  *
@@ -183,6 +189,19 @@ int rt_cand_topk(const void* queries, int64_t B, const void* items, int64_t N, i
                  int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
                  rt_stream_t stream);
 
+/* Int8 re-rank of original ids: candidate c of row b (c < 0 or c >= N = padding, skipped) is
+ * item_codes row item_rows[c] (a permutation, e.g. SilverTorch's inv_perm), scored as the float
+ * (float(dot) * q_scales[b]) * global_scale[0]; the top min(k, P) by (score desc, id asc) ->
+ * out_ids int64 / out_scores float32 [B, k], -1 / -inf past a row's candidates. Workspace as
+ * rt_cand_topk_workspace(B, P, k).
+ * Replaces: SilverTorch._forward_candidates (retrieve/src/retrieve/modules/silvertorch.py:
+ *   363-379): the gather through inv_perm, the fp32 bmm of codes, the scaling and masked_topk. */
+int rt_int8_rerank_topk(const int8_t* q_codes, const float* q_scales, int64_t B,
+                        const int8_t* item_codes, int64_t N, int64_t D, const int64_t* item_rows,
+                        const float* global_scale, const int64_t* candidate_ids, int64_t P,
+                        const int64_t* counts, int64_t k, int64_t* out_ids, float* out_scores,
+                        void* workspace, size_t workspace_bytes, rt_stream_t stream);
+
 /* [1, N] float scores of one fp16 query [D] against the fp16 [D, N] item table (row k of the
  * table is dimension k of every item), accumulated as acc = fma(q[k], e[k, n], acc) for
  * k = 0 .. D-1 in fp32.
@@ -193,12 +212,22 @@ int rt_gemv_scores(const uint16_t* query, const uint16_t* item_embs_t, int64_t D
 
 /* ---- SilverTorch search ------------------------------------------------------------------- */
 
-/* Per-row int8 quantization: abs_max = max(max |x|, 1e-8), scales[r] = abs_max * fp32(1/127),
- * codes = clamp(rint(fp32(fp64(x) / fp64(abs_max)) * 127), -128, 127) (x float32 [rows, dim]).
- * Replaces: probe_prep's quantization (silvertorch/.../fork_search_cuda.cu:653-700; the
- *   GPU form of retrieve/src/retrieve/indexing/quantize.py:9-18). */
-int rt_quantize_int8_rows(const float* x, int64_t rows, int64_t dim, int8_t* codes, float* scales,
-                          rt_stream_t stream);
+/* Per-row int8 quantization: abs_max = max(max |x|, 1e-8),
+ * codes = clamp(rint(fp32(fp64(x) / fp64(abs_max)) * 127), -128, 127) (x float32 [rows, dim]);
+ * scales[r] = abs_max / 127 when scale_div (quantize_int8), else abs_max * fp32(1/127)
+ * (probe_prep).
+ * Replaces: probe_prep's quantization (silvertorch/.../fork_search_cuda.cu:653-700) and
+ *   retrieve/src/retrieve/indexing/quantize.py:9-18 (quantize_int8). */
+int rt_quantize_int8_rows(const float* x, int64_t rows, int64_t dim, int8_t* codes,
+                          float* scales, int scale_div, rt_stream_t stream);
+
+/* Sign bits of float32 rows [rows, dim] (dim a multiple of 64) -> [rows, dim / 64] words, LSB
+ * first: bit b of word w is x[r, 64 w + b] > 0 (NaN and -0 give 0).
+ * Replaces: _pack_signs_to_int64 (retrieve/src/retrieve/indexing/quantize.py:63-72), the packing
+ *   step of quantize_simhash_1bit / project_simhash_1bit_query and the Sign-OPORP projections
+ *   (:99-173). */
+int rt_pack_signs(const float* x, int64_t rows, int64_t dim, uint64_t* words,
+                  rt_stream_t stream);
 
 /* The exact clause filter over st::search's clause-major int32 slot layout (slots [R, N]; clause
  * c in rows clause_slots[c] .. clause_slots[c+1], -1 pads; query_values [B, C] int32, -1 =

@@ -13,16 +13,20 @@ INV127 = np.float32(1.0) / np.float32(127.0)
 ABS_MAX_FLOOR = np.float32(1e-8)
 
 
-def quantize_int8(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+def quantize_int8(x: np.ndarray, divide: bool = False) -> tuple[np.ndarray, np.ndarray]:
     """Per-row symmetric int8: ``retrieve/src/retrieve/indexing/quantize.py:9-18`` as the GPU
     computes it (``silvertorch/.../fork_search_cuda.cu:680-699``): ``abs_max = max(max|x|,
-    fp32(1e-8))``; ``scale = abs_max * fp32(1/127)``; ``code = clamp(rint(fp32(fp64(x) /
+    fp32(1e-8))``; ``scale = abs_max * fp32(1/127)`` (``divide``: ``fp32(abs_max / 127)``, the
+    Python function's ``abs_max / 127.0``); ``code = clamp(rint(fp32(fp64(x) /
     fp64(abs_max)) * 127), -128, 127)`` with round-half-to-even.
 
     ``x`` is ``[R, D]`` float32. Returns ``(codes int8 [R, D], scales float32 [R])``."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     abs_max = np.maximum(np.abs(x).max(axis=1), ABS_MAX_FLOOR).astype(np.float32)
-    scales = (abs_max * INV127).astype(np.float32)
+    if divide:
+        scales = (abs_max / np.float32(127.0)).astype(np.float32)
+    else:
+        scales = (abs_max * INV127).astype(np.float32)
     q = (x.astype(np.float64) / abs_max.astype(np.float64)[:, None]).astype(np.float32)
     v = np.rint(q * np.float32(127.0))
     codes = np.clip(v, -128, 127).astype(np.int8)

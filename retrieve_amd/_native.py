@@ -70,7 +70,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_sz, _c_p],
     ),
     "rt_gemv_scores": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
-    "rt_quantize_int8_rows": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "rt_quantize_int8_rows": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_int, _c_p]),
+    "rt_pack_mask": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "rt_pack_signs": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "rt_int8_rerank_topk": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p,
+         _c_p, _c_p, _c_sz, _c_p],
+    ),
     "rt_clause_slots_filter": (
         _c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
     ),

@@ -25,7 +25,14 @@ constexpr int kCandWaves = kCandThreads / kWave;
 constexpr int kCandMaxWgsPerQuery = 64;
 constexpr int kCandMaxChunks = 8;  // 16-byte chunks per lane: rows up to 64 * 16 * 8 bytes
 
-enum CandKind : int { kCandF16 = 0, kCandBF16 = 1, kCandF32 = 2, kCandI8 = 3, kCandBits = 4 };
+enum CandKind : int {
+  kCandF16 = 0,
+  kCandBF16 = 1,
+  kCandF32 = 2,
+  kCandI8 = 3,
+  kCandBits = 4,
+  kCandI8Scaled = 5,  // int8 dots keyed on the float score (dot * query scale) * global scale
+};
 
 // (by value: __builtin_bit_cast applied directly to a vector element x[i] reads element 0)
 __device__ inline float as_float(int32_t v) { return __builtin_bit_cast(float, v); }
@@ -85,16 +92,35 @@ struct CandOp<kCandI8> {
 };
 
 template <>
+struct CandOp<kCandI8Scaled> : CandOp<kCandI8> {};
+
+template <>
 struct CandOp<kCandBits> {
   using Acc = int32_t;
-  // matching bits minus differing bits of the chunk's 128: 128 - 2 popcount(q ^ x)
+  // -2 popcount(q ^ x) of the chunk; the row's 8 * RB bits are added once after the reduction,
+  // so a half chunk (zeros in both halves) counts only its own 64 bits
   __device__ static int32_t chunk(v4i x, v4i q) {
     int32_t d = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) d += __builtin_popcount(static_cast<uint32_t>(x[i] ^ q[i]));
-    return 128 - 2 * d;
+    return -2 * d;
   }
 };
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+// 16-byte chunk c of a row of rb bytes; the last chunk of a row of 8 (mod 16) bytes is loaded as
+// 8 bytes and zero-extended.
+template <bool NT>
+__device__ inline v4i load_chunk(const int8_t* row, int c, int rb) {
+  if (16 * c + 8 == rb) {
+    const v2i h = NT ? __builtin_nontemporal_load(reinterpret_cast<const v2i*>(row + 16 * c))
+                     : *reinterpret_cast<const v2i*>(row + 16 * c);
+    return v4i{h[0], h[1], 0, 0};
+  }
+  return NT ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(row + 16 * c))
+            : *reinterpret_cast<const v4i*>(row + 16 * c);
+}
 
 struct CandArgs {
   const void* queries;  // [B, RB] bytes (float32 rows for the floating kinds)
@@ -105,6 +131,9 @@ struct CandArgs {
   const int64_t* ids;  // [B, P] candidate item ids
   int64_t P;
   const int64_t* counts;  // [B]
+  const int64_t* rows;    // [N] item id -> row of items, or null (row = id)
+  const float* qscale;    // [B], kCandI8Scaled only
+  const float* gscale;    // [1], kCandI8Scaled only
   int k;
   int capw;
   uint64_t* lists;  // [B, S, capw]
@@ -136,7 +165,7 @@ __global__ void __launch_bounds__(kCandThreads) cand_scan_kernel(CandArgs a) {
   count = count < 0 ? 0 : (count > a.P ? a.P : count);
 
   // this lane's query chunks: c = gl + j * L
-  const int nchunks = a.RB / 16;
+  const int nchunks = (a.RB + 15) / 16;
   v4i qb[NC];
   float qf[NC][QF];
 #pragma unroll
@@ -149,10 +178,15 @@ __global__ void __launch_bounds__(kCandThreads) cand_scan_kernel(CandArgs a) {
       for (int e = 0; e < QF; ++e) qf[j][e] = c < nchunks ? q[c * QF + e] : 0.f;
     } else {
       const int8_t* q = static_cast<const int8_t*>(a.queries) + b * a.RB;
-      qb[j] = c < nchunks ? *reinterpret_cast<const v4i*>(q + c * 16) : v4i{0, 0, 0, 0};
+      qb[j] = c < nchunks ? load_chunk<false>(q, c, a.RB) : v4i{0, 0, 0, 0};
     }
   }
 
+  float qs = 0.f, gs = 0.f;
+  if constexpr (KIND == kCandI8Scaled) {
+    qs = a.qscale[b];
+    gs = a.gscale[0];
+  }
   uint64_t tau = 0;  // composites below it cannot reach this wave's best k
   int cnt = 0;
   const int64_t step = gx * kCandWaves * R;
@@ -163,14 +197,19 @@ __global__ void __launch_bounds__(kCandThreads) cand_scan_kernel(CandArgs a) {
     bool ok = p < count;
     int64_t item = ok ? a.ids[b * a.P + p] : 0;
     ok = ok && item >= 0 && item < a.N;  // ids outside the table are skipped, not read
+    int64_t r = item;
+    if (a.rows != nullptr && ok) {
+      r = a.rows[item];
+      ok = r >= 0 && r < a.N;
+    }
     typename Op::Acc s = 0;
     if (ok) {
-      const int8_t* row = I + item * a.RB;
+      const int8_t* row = I + r * a.RB;
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
         const int c = gl + j * L;
         if (c < nchunks) {
-          const v4i x = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(row + c * 16));
+          const v4i x = load_chunk<true>(row, c, a.RB);
           if constexpr (kFloat) {
             s += Op::chunk(x, qf[j]);
           } else {
@@ -181,9 +220,14 @@ __global__ void __launch_bounds__(kCandThreads) cand_scan_kernel(CandArgs a) {
     }
 #pragma unroll
     for (int off = L / 2; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if constexpr (KIND == kCandBits) s += 8 * a.RB;
     uint64_t c = 0;
     if constexpr (kFloat) {
       c = composite(key_of_f32(static_cast<float>(s)), static_cast<uint32_t>(item));
+    } else if constexpr (KIND == kCandI8Scaled) {
+      // two roundings in this order, as (dots * q_scales) * global_scale in fp32
+      const float v = (static_cast<float>(s) * qs) * gs;
+      c = composite(key_of_f32(v), static_cast<uint32_t>(item));
     } else {  // int8 dots and bit-code scores are exact int32
       c = composite(key_of_i32(static_cast<int32_t>(s)), static_cast<uint32_t>(item));
     }
@@ -222,7 +266,7 @@ static void launch_cand(const CandArgs& a, dim3 grid, size_t lds, hipStream_t st
 template <int KIND>
 static int dispatch_cand(const CandArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
   // L lanes per row (16 bytes each, up to 64), NC 16-byte chunks per lane
-  switch (a.RB) {
+  switch ((a.RB + 15) / 16 * 16) {
     case 16: launch_cand<KIND, 1, 1>(a, grid, lds, stream); break;
     case 32: launch_cand<KIND, 2, 1>(a, grid, lds, stream); break;
     case 64: launch_cand<KIND, 4, 1>(a, grid, lds, stream); break;
@@ -264,28 +308,34 @@ extern "C" size_t rt_cand_topk_workspace(int64_t B, int64_t P, int64_t k) {
          align_up(static_cast<size_t>(B * S) * sizeof(int), 256);
 }
 
-// kind: 0 fp16, 1 bf16, 2 fp32 items with float32 queries [B, D] (float scores); 3 int8
-// (int32 scores); 4 bit codes of D 64-bit words (score 64 D - 2 popcount, float scores).
-extern "C" int rt_cand_topk(const void* queries, int64_t B, const void* items, int64_t N,
-                            int64_t D, int kind, const int64_t* positive_indices, int64_t P,
-                            const int64_t* counts, int64_t k, int64_t* out_ids, void* out_scores,
-                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
+namespace rt {
+
+static int cand_topk(const void* queries, int64_t B, const void* items, int64_t N, int64_t D,
+                     int kind, const int64_t* positive_indices, int64_t P, const int64_t* counts,
+                     const int64_t* rows, const float* qscale, const float* gscale, int64_t k,
+                     int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
   RT_CHECK_ARG(B >= 0 && N >= 0 && P >= 0 && D >= 1, "B, N, P must be >= 0 and D >= 1");
   RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
                static_cast<long long>(kMaxK), static_cast<long long>(k));
-  RT_CHECK_ARG(kind >= kCandF16 && kind <= kCandBits, "kind must be in [0, 4]");
-  static const int elem[] = {2, 2, 4, 1, 8};
+  RT_CHECK_ARG(kind >= kCandF16 && kind <= kCandI8Scaled, "kind must be in [0, 5]");
+  static const int elem[] = {2, 2, 4, 1, 8, 1};
   const int64_t rb = D * elem[kind];
-  RT_CHECK_ARG(rb % 16 == 0 && rb <= 64 * 16 * kCandMaxChunks,
-               "row bytes (D * element size = %lld) must be a multiple of 16 and <= %d",
-               static_cast<long long>(rb), 64 * 16 * kCandMaxChunks);
-  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(items) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(queries) % 16 == 0,
-               "queries and items must be 16-byte aligned");
+  // bit codes: any number of 64-bit words; the other kinds whole 16-byte chunks
+  const int64_t unit = kind == kCandBits ? 8 : 16;
+  RT_CHECK_ARG(rb % unit == 0 && rb <= 64 * 16 * kCandMaxChunks,
+               "row bytes (D * element size = %lld) must be a multiple of %lld and <= %d",
+               static_cast<long long>(rb), static_cast<long long>(unit),
+               64 * 16 * kCandMaxChunks);
+  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(items) % unit == 0 &&
+                   reinterpret_cast<uintptr_t>(queries) % unit == 0,
+               "queries and items must be %lld-byte aligned", static_cast<long long>(unit));
   RT_CHECK_ARG(N < 0xffffffffll, "N must be < 2**32 - 1");
   // bit codes score as exact int32 keys, written as float
   const int score_kind =
       kind == kCandI8 ? kScoreI32 : (kind == kCandBits ? kScoreF32FromI32 : kScoreF32);
+  RT_CHECK_ARG(kind != kCandI8Scaled || (qscale != nullptr && gscale != nullptr),
+               "the scaled int8 kind needs query and global scales");
   if (B == 0) return kOk;
   if (P == 0 || N == 0) return launch_pad(out_ids, out_scores, B, k, score_kind, stream);
   const size_t need = rt_cand_topk_workspace(B, P, k);
@@ -306,6 +356,9 @@ extern "C" int rt_cand_topk(const void* queries, int64_t B, const void* items, i
   a.ids = positive_indices;
   a.P = P;
   a.counts = counts;
+  a.rows = rows;
+  a.qscale = qscale;
+  a.gscale = gscale;
   a.k = static_cast<int>(k);
   a.capw = capw;
   a.lists = static_cast<uint64_t*>(workspace);
@@ -320,6 +373,7 @@ extern "C" int rt_cand_topk(const void* queries, int64_t B, const void* items, i
     case kCandBF16: dispatch_cand<kCandBF16>(a, grid, lds, stream); break;
     case kCandF32: dispatch_cand<kCandF32>(a, grid, lds, stream); break;
     case kCandI8: dispatch_cand<kCandI8>(a, grid, lds, stream); break;
+    case kCandI8Scaled: dispatch_cand<kCandI8Scaled>(a, grid, lds, stream); break;
     default: dispatch_cand<kCandBits>(a, grid, lds, stream); break;
   }
   RT_CHECK_HIP(hipGetLastError());
@@ -343,4 +397,31 @@ extern "C" int rt_cand_topk(const void* queries, int64_t B, const void* items, i
     RT_CHECK_HIP(hipGetLastError());
   }
   return kOk;
+}
+
+}  // namespace rt
+
+// kind: 0 fp16, 1 bf16, 2 fp32 items with float32 queries [B, D] (float scores); 3 int8
+// (int32 scores); 4 bit codes of D 64-bit words (score 64 D - 2 popcount, float scores).
+extern "C" int rt_cand_topk(const void* queries, int64_t B, const void* items, int64_t N,
+                            int64_t D, int kind, const int64_t* positive_indices, int64_t P,
+                            const int64_t* counts, int64_t k, int64_t* out_ids, void* out_scores,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  RT_CHECK_ARG(kind >= kCandF16 && kind <= kCandBits, "kind must be in [0, 4]");
+  return cand_topk(queries, B, items, N, D, kind, positive_indices, P, counts, nullptr, nullptr,
+                   nullptr, k, out_ids, out_scores, workspace, workspace_bytes, stream);
+}
+
+// SilverTorch's re-rank of given ids: candidate id c (-1 = padding) is scored from row
+// item_rows[c] of item_codes (the cluster-sorted table), key (float(dot) * q_scales[b]) *
+// global_scale[0], ties to the lower id.
+extern "C" int rt_int8_rerank_topk(const int8_t* q_codes, const float* q_scales, int64_t B,
+                                   const int8_t* item_codes, int64_t N, int64_t D,
+                                   const int64_t* item_rows, const float* global_scale,
+                                   const int64_t* candidate_ids, int64_t P, const int64_t* counts,
+                                   int64_t k, int64_t* out_ids, float* out_scores,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return cand_topk(q_codes, B, item_codes, N, D, kCandI8Scaled, candidate_ids, P, counts,
+                   item_rows, q_scales, global_scale, k, out_ids, out_scores, workspace,
+                   workspace_bytes, stream);
 }

@@ -903,6 +903,35 @@ extern "C" int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t 
   return kOk;
 }
 
+// [B, N] 0/1 bytes -> [B, ceil(N/64)] mask words, item d at bit 63 - d % 64: lane l of a wave
+// takes item (wave base + 63 - l), so its ballot is the word as stored.
+__global__ void __launch_bounds__(kClauseThreads) pack_mask_kernel(const uint8_t* valid,
+                                                                   int64_t N, int64_t W,
+                                                                   uint64_t* words) {
+  const int lane = lane_id();
+  const int64_t b = blockIdx.y;
+  const int64_t w = (static_cast<int64_t>(blockIdx.x) * kClauseThreads + threadIdx.x) / kWave;
+  if (w >= W) return;  // whole waves
+  const int64_t d = w * kWave + (kWave - 1 - lane);
+  const bool v = d < N && valid[b * N + d] != 0;
+  const uint64_t word = __ballot(v);
+  if (lane == 0) words[b * W + w] = word;
+}
+
+extern "C" int rt_pack_mask(const uint8_t* valid, int64_t B, int64_t N, uint64_t* words,
+                            hipStream_t stream) {
+  RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
+  RT_CHECK_ARG(B <= 65535, "B must be <= 65535");
+  const int64_t W = cdiv(N, 64);
+  if (B == 0 || W == 0) return kOk;
+  const int64_t gx = cdiv(W * kWave, kClauseThreads);
+  RT_CHECK_ARG(gx < (int64_t{1} << 31), "N too large");
+  pack_mask_kernel<<<dim3(static_cast<unsigned>(gx), static_cast<unsigned>(B)), kClauseThreads, 0,
+                     stream>>>(valid, N, W, words);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
 extern "C" size_t rt_mask_compact_workspace(int64_t B, int64_t N) {
   if (B <= 0 || N <= 0) return 256;
   const int64_t T = compact_chunks(N);

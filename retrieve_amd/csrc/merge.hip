@@ -144,10 +144,11 @@ __device__ void block_minmax(const uint64_t* keys, int n, uint64_t* red, uint64_
 }
 
 // Block-wide radix select over keys[0, n) in LDS, MSB-first digits of up to 8 bits, starting
-// below the bits every key shares (min and max agree there). Returns a bound T such that
-// exactly kth keys are >= T (the keys are distinct except for repeated zeros): the kth
-// largest key, or, when a digit pass finds the kth largest key's bucket holding exactly the
-// keys still wanted, that bucket's lowest possible value (the search stops there).
+// below the bits every key shares (min and max agree there). Returns a bound T with at
+// most kth keys > T and at least kth keys >= T (exactly kth for distinct keys): the kth
+// largest key counted with repeats, or, when a digit pass finds the kth largest key's bucket
+// holding exactly the keys still wanted, that bucket's lowest possible value (the search
+// stops there).
 // 1 <= kth <= n. Every thread of the block calls it.
 __device__ uint64_t block_select_desc(const uint64_t* keys, int n, int kth, unsigned* hist,
                                       int* sh, uint64_t* red) {
@@ -319,10 +320,16 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
       const uint64_t kth = block_select_desc(buf, cnt, k, hist, sh, red);
       if (tid == 0) sh[2] = 0;
       __syncthreads();
+      // at most k entries are above kth; equal entries (repeated empty seed entries, or a
+      // candidate listed twice) fill the remaining places, any copy being as good as another
       for (int i = tid; i < cnt; i += kMergeThreads) {
         const uint64_t v = buf[i];
-        if (v >= kth) {
-          // exactly k entries are >= kth, except for repeated empty (0) seed entries
+        if (v > kth) tmp[atomicAdd(&sh[2], 1)] = v;
+      }
+      __syncthreads();
+      for (int i = tid; i < cnt; i += kMergeThreads) {
+        const uint64_t v = buf[i];
+        if (v == kth) {
           const int p = atomicAdd(&sh[2], 1);
           if (p < k) tmp[p] = v;
         }

@@ -16,13 +16,18 @@ namespace rt {
 constexpr int kHamTile = kWave;  // items per tile: one per lane
 constexpr int kHamMaxQpw = 64;   // queries a wave scores (a query group)
 
+// A row of W words: 16-byte loads when W is even (rows 16-byte aligned), 8-byte loads when odd.
 template <int W>
 __device__ inline void load_codes(const uint32_t* __restrict__ I, int64_t item, uint32_t* iw) {
   const uint4* p = reinterpret_cast<const uint4*>(I + item * (2 * W));
-  if constexpr (W == 1) {
-    const uint2 v = *reinterpret_cast<const uint2*>(I + item * 2);
-    iw[0] = v.x;
-    iw[1] = v.y;
+  if constexpr (W % 2 == 1) {
+    const uint2* p2 = reinterpret_cast<const uint2*>(I + item * (2 * W));
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      const uint2 v = p2[j];
+      iw[2 * j] = v.x;
+      iw[2 * j + 1] = v.y;
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < W / 2; ++j) {
@@ -207,19 +212,24 @@ static int launch_ham(const ScanArgs& a, const PassPlan& p, int64_t nqg, bool se
   return kOk;
 }
 
+constexpr int kHamMaxWords = 16;
+
+template <int W>
+static int dispatch_ham_from(int64_t w, const ScanArgs& a, const PassPlan& p, int64_t nqg,
+                             bool seed, hipStream_t stream) {
+  if (w == W) return launch_ham<W>(a, p, nqg, seed, stream);
+  if constexpr (W < kHamMaxWords) {
+    return dispatch_ham_from<W + 1>(w, a, p, nqg, seed, stream);
+  } else {
+    set_error("Hamming scan supports W (64-bit words per code) in [1, %d], got %lld",
+              kHamMaxWords, static_cast<long long>(w));
+    return kInvalidArgument;
+  }
+}
+
 static int dispatch_ham(int64_t W, const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed,
                         hipStream_t stream) {
-  switch (W) {
-    case 1: return launch_ham<1>(a, p, nqg, seed, stream);
-    case 2: return launch_ham<2>(a, p, nqg, seed, stream);
-    case 4: return launch_ham<4>(a, p, nqg, seed, stream);
-    case 8: return launch_ham<8>(a, p, nqg, seed, stream);
-    case 16: return launch_ham<16>(a, p, nqg, seed, stream);
-    default:
-      set_error("Hamming scan supports W (64-bit words per code) in {1, 2, 4, 8, 16}, got %lld",
-                static_cast<long long>(W));
-      return kInvalidArgument;
-  }
+  return dispatch_ham_from<1>(W, a, p, nqg, seed, stream);
 }
 
 static int ham_qpw(int64_t B) { return static_cast<int>(B < kHamMaxQpw ? B : kHamMaxQpw); }
@@ -246,11 +256,11 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B,
   RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
                static_cast<long long>(kMaxK), static_cast<long long>(k));
   RT_CHECK_ARG(N < 0xffffffffll, "N must be < 2**32 - 1");
-  RT_CHECK_ARG(W == 1 || W == 2 || W == 4 || W == 8 || W == 16,
-               "W (64-bit words per code) must be in {1, 2, 4, 8, 16}, got %lld",
+  RT_CHECK_ARG(W >= 1 && W <= kHamMaxWords,
+               "W (64-bit words per code) must be in [1, %d], got %lld", kHamMaxWords,
                static_cast<long long>(W));
-  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(item_bits) % 16 == 0,
-               "item_bits must be 16-byte aligned");
+  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(item_bits) % (W % 2 ? 8 : 16) == 0,
+               "item_bits must be %d-byte aligned", W % 2 ? 8 : 16);
   RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
   if (B == 0) return kOk;
   const int kind = score_f32 ? kScoreF32FromI32 : kScoreI32;

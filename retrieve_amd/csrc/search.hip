@@ -31,9 +31,12 @@ constexpr int kIvfMaxWgsPerRow = 64;
 // Per row: abs_max = max(max |x|, 1e-8); scale = abs_max * fp32(1/127); code =
 // clamp(rint(fp32(fp64(x) / fp64(abs_max)) * 127), -128, 127) (fork_search_cuda.cu:680-699;
 // retrieve/src/retrieve/indexing/quantize.py:9-18). One workgroup per row.
+// scale_div: scales = abs_max / 127 (quantize_int8, indexing/quantize.py:9-18); else
+// abs_max * fp32(1/127) (probe_prep_kernel, fork_search_cuda.cu:689). The codes are the same.
 __global__ void __launch_bounds__(kQuantThreads) quantize_rows_kernel(const float* x,
                                                                       int64_t dim, int8_t* codes,
-                                                                      float* scales) {
+                                                                      float* scales,
+                                                                      int scale_div) {
   __shared__ float red[kQuantThreads / kWave];
   const int64_t row = blockIdx.x;
   const float* xr = x + row * dim;
@@ -46,7 +49,7 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_rows_kernel(const floa
   m = red[0];
   for (int w = 1; w < kQuantThreads / kWave; ++w) m = fmaxf(m, red[w]);
   m = fmaxf(m, 1e-8f);
-  if (threadIdx.x == 0) scales[row] = m * (1.0f / 127.0f);
+  if (threadIdx.x == 0) scales[row] = scale_div ? m / 127.0f : m * (1.0f / 127.0f);
   const double a = static_cast<double>(m);
   int8_t* out = codes + row * dim;
   for (int64_t d = threadIdx.x; d < dim; d += kQuantThreads) {
@@ -54,6 +57,19 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_rows_kernel(const floa
     v = fminf(fmaxf(rintf(v), -128.0f), 127.0f);
     out[d] = static_cast<int8_t>(v);
   }
+}
+
+// Sign bits of float rows, LSB-first: bit b of word w of row r is x[r, 64 w + b] > 0
+// (_pack_signs_to_int64, retrieve/src/retrieve/indexing/quantize.py:63-72). One wave per word:
+// lane b reads element 64 w + b and the ballot is the word (NaN and -0 give 0 bits, as the
+// reference's comparison does).
+__global__ void __launch_bounds__(256) pack_signs_kernel(const float* x, int64_t words_total,
+                                                         uint64_t* words) {
+  const int64_t w = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / kWave;
+  if (w >= words_total) return;  // whole waves
+  const bool pos = x[w * kWave + lane_id()] > 0.0f;
+  const uint64_t word = __ballot(pos);
+  if (lane_id() == 0) words[w] = word;
 }
 
 // ---- range scan ------------------------------------------------------------------------------
@@ -283,12 +299,26 @@ static int64_t ivf_gx(int64_t B, int64_t width) {
 using namespace rt;
 
 extern "C" int rt_quantize_int8_rows(const float* x, int64_t rows, int64_t dim, int8_t* codes,
-                                     float* scales, hipStream_t stream) {
+                                     float* scales, int scale_div, hipStream_t stream) {
   RT_CHECK_ARG(rows >= 0 && dim >= 1, "rows must be >= 0 and dim >= 1");
   RT_CHECK_ARG(rows <= (int64_t{1} << 31) - 1, "too many rows");
   if (rows == 0) return kOk;
-  quantize_rows_kernel<<<static_cast<unsigned>(rows), kQuantThreads, 0, stream>>>(x, dim, codes,
-                                                                                 scales);
+  quantize_rows_kernel<<<static_cast<unsigned>(rows), kQuantThreads, 0, stream>>>(
+      x, dim, codes, scales, scale_div);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+extern "C" int rt_pack_signs(const float* x, int64_t rows, int64_t dim, uint64_t* words,
+                             hipStream_t stream) {
+  RT_CHECK_ARG(rows >= 0 && dim >= 1, "rows must be >= 0 and dim >= 1");
+  RT_CHECK_ARG(dim % 64 == 0, "dim must be a multiple of 64, got %lld",
+               static_cast<long long>(dim));
+  const int64_t total = rows * (dim / 64);
+  if (total == 0) return kOk;
+  const int64_t blocks = cdiv(total * kWave, 256);
+  RT_CHECK_ARG(blocks < (int64_t{1} << 31), "too many rows");
+  pack_signs_kernel<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(x, total, words);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }

@@ -622,3 +622,130 @@ def gemv_scores(query: Tensor, item_embs_t: Tensor) -> Tensor:
 @gemv_scores.register_fake
 def _(query, item_embs_t):
     return query.new_empty((1, item_embs_t.shape[1]), dtype=torch.float32)
+
+
+# --- the reference's per-row quantization and bool masks for the scans ---------------------------
+
+
+@torch.library.custom_op("retrieve::quantize_int8", mutates_args=(), device_types="cuda")
+def quantize_int8(embs: Tensor) -> tuple[Tensor, Tensor]:
+    """Per-row symmetric int8 codes and scales (``retrieve/src/retrieve/indexing/quantize.py:
+    9-18``): ``abs_max = clamp(max |x|, 1e-8)``, ``scale = abs_max / 127``,
+    ``code = clamp(round(fp32(fp64(x) / fp64(abs_max)) * 127), -128, 127)``."""
+    if embs.dim() != 2:
+        raise ValueError(f"embs must be [N, D], got {tuple(embs.shape)}")
+    from retrieve_amd import st
+
+    return st.quantize_rows(embs, scale_div=True)
+
+
+@quantize_int8.register_fake
+def _(embs):
+    return (embs.new_empty(embs.shape, dtype=torch.int8),
+            embs.new_empty(embs.shape[:1], dtype=torch.float32))
+
+
+@torch.library.custom_op("retrieve::pack_mask", mutates_args=(), device_types="cuda")
+def pack_mask(valid: Tensor) -> Tensor:
+    """``[B, N]`` bool → ``[B, ceil(N/64)]`` int64 words, item ``d`` at bit ``63 - d % 64``: the
+    mask form of the fused scans (``int8_scan_topk``, ``dense_scan_topk``,
+    ``hamming_scan_topk``)."""
+    if valid.dim() != 2 or valid.dtype != torch.bool:
+        raise ValueError("valid must be a [B, N] bool tensor")
+    v = valid.contiguous()
+    dev = nat.require_device(v)
+    b, n = v.shape
+    out = torch.empty((b, (n + 63) // 64), dtype=torch.int64, device=dev)
+    if b and n:
+        with torch.cuda.device(dev):
+            st = nat.lib().rt_pack_mask(nat.ptr(v), b, n, nat.ptr(out), nat.stream(dev))
+        nat.check(st)
+    return out
+
+
+@pack_mask.register_fake
+def _(valid):
+    return valid.new_empty((valid.shape[0], (valid.shape[1] + 63) // 64), dtype=torch.int64)
+
+
+@torch.library.custom_op("retrieve::pack_signs", mutates_args=(), device_types="cuda")
+def pack_signs(values: Tensor) -> Tensor:
+    """``[R, D]`` floats → ``[R, D // 64]`` int64, bit ``b`` of word ``w`` set iff ``values[:,
+    64 w + b] > 0`` (``_pack_signs_to_int64``, ``retrieve/src/retrieve/indexing/quantize.py:
+    63-72``). fp16 / bf16 inputs are widened to fp32 first (exact, so the signs are kept)."""
+    if values.dim() != 2:
+        raise ValueError(f"values must be [R, D], got {tuple(values.shape)}")
+    if not values.is_floating_point():
+        raise TypeError(f"values must be floating point, got {values.dtype}")
+    r, d = values.shape
+    if d % 64:
+        raise ValueError(f"D must be a multiple of 64, got {d}")
+    v = values.to(torch.float32).contiguous()
+    dev = nat.require_device(v)
+    out = torch.empty((r, d // 64), dtype=torch.int64, device=dev)
+    if out.numel():
+        with torch.cuda.device(dev):
+            st = nat.lib().rt_pack_signs(nat.ptr(v), r, d, nat.ptr(out), nat.stream(dev))
+        nat.check(st)
+    return out
+
+
+@pack_signs.register_fake
+def _(values):
+    return values.new_empty((values.shape[0], values.shape[1] // 64), dtype=torch.int64)
+
+
+@torch.library.custom_op("retrieve::int8_rerank_topk", mutates_args=(), device_types="cuda")
+def int8_rerank_topk(
+    query_codes: Tensor, query_scales: Tensor, item_codes: Tensor, item_rows: Tensor,
+    global_scale: Tensor, candidate_ids: Tensor, k: int
+) -> tuple[Tensor, Tensor]:
+    """SilverTorch's re-rank of original ids (``modules/silvertorch.py:363-379``): candidate
+    ``c`` (``-1`` = padding, never read or returned) is ``item_codes[item_rows[c]]``, scored as
+    ``(float(dot) * query_scales[b]) * global_scale``; the top ``min(k, P)`` by (score desc, id
+    asc) → ``(ids int64, scores fp32)``, ``-1`` / ``-inf`` past a row's candidates."""
+    if query_codes.dim() != 2 or item_codes.dim() != 2 or candidate_ids.dim() != 2:
+        raise ValueError("query_codes [B, D], item_codes [N, D], candidate_ids [B, P] expected")
+    if query_codes.dtype != torch.int8 or item_codes.dtype != torch.int8:
+        raise TypeError("query_codes and item_codes must be int8")
+    if candidate_ids.dtype != torch.int64 or item_rows.dtype != torch.int64:
+        raise TypeError("candidate_ids and item_rows must be int64")
+    b, d = query_codes.shape
+    n = item_codes.shape[0]
+    if item_codes.shape[1] != d or candidate_ids.shape[0] != b or query_scales.shape != (b,) \
+            or item_rows.shape != (n,) or global_scale.numel() != 1:
+        raise ValueError("shape mismatch among query_codes, query_scales, item_codes, "
+                         "item_rows, global_scale and candidate_ids")
+    _check_items(item_codes=item_codes, item_rows=item_rows)
+    p = candidate_ids.shape[1]
+    kk = min(k, p)
+    if k < 1 or kk > 1024:
+        raise ValueError(f"k must be >= 1 and min(k, P) <= 1024, got k={k}")
+    q = query_codes.contiguous()
+    dev = nat.require_device(q, item_codes, item_rows, candidate_ids)
+    ids = torch.empty((b, kk), dtype=torch.int64, device=dev)
+    scores = torch.empty((b, kk), dtype=torch.float32, device=dev)
+    if b == 0 or kk == 0:
+        return ids, scores
+    cand = candidate_ids.contiguous()
+    qs = query_scales.to(torch.float32).contiguous()
+    gs = global_scale.to(device=dev, dtype=torch.float32).reshape(1).contiguous()
+    counts = torch.full((b,), p, dtype=torch.int64, device=dev)
+    lib = nat.lib()
+    ws = nat.workspace(lib.rt_cand_topk_workspace(b, p, kk), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_int8_rerank_topk(
+            nat.ptr(q), nat.ptr(qs), b, nat.ptr(item_codes), n, d, nat.ptr(item_rows), nat.ptr(gs),
+            nat.ptr(cand), p, nat.ptr(counts), kk, nat.ptr(ids), nat.ptr(scores), nat.ptr(ws),
+            ws.numel(), nat.stream(dev),
+        )
+    nat.check(st)
+    return ids, scores
+
+
+@int8_rerank_topk.register_fake
+def _(query_codes, query_scales, item_codes, item_rows, global_scale, candidate_ids, k):
+    kk = min(k, candidate_ids.shape[1])
+    b = query_codes.shape[0]
+    return (query_codes.new_empty((b, kk), dtype=torch.int64),
+            query_codes.new_empty((b, kk), dtype=torch.float32))

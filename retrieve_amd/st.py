@@ -297,9 +297,10 @@ MAX_SEARCH_K = 1024  # kSelectMaxK
 MAX_PROBE = 1024
 
 
-def quantize_rows(query: Tensor) -> tuple[Tensor, Tensor]:
+def quantize_rows(query: Tensor, scale_div: bool = False) -> tuple[Tensor, Tensor]:
     """float32 ``[B, D]`` → ``(codes int8 [B, D], scales float32 [B])`` on the GPU (the
-    quantization of ``fork_search_cuda.cu:680-699``)."""
+    quantization of ``fork_search_cuda.cu:680-699``; ``scale_div``: the scale as
+    ``quantize_int8``'s ``abs_max / 127``, ``indexing/quantize.py:9-18``)."""
     q = query.to(torch.float32).contiguous()
     dev = nat.require_device(q)
     b, d = q.shape
@@ -308,7 +309,8 @@ def quantize_rows(query: Tensor) -> tuple[Tensor, Tensor]:
     if b and d:
         with torch.cuda.device(dev):
             st = nat.lib().rt_quantize_int8_rows(nat.ptr(q), b, d, nat.ptr(codes),
-                                                 nat.ptr(scales), nat.stream(dev))
+                                                 nat.ptr(scales), int(scale_div),
+                                                 nat.stream(dev))
         nat.check(st)
     return codes, scales
 

@@ -76,6 +76,22 @@ def test_fused_masked_knn_ties_and_duplicates(dev):
     assert ids2.cpu().tolist() == [[3, 7, 7, 9]]
 
 
+def test_duplicated_candidate_at_the_boundary(dev):
+    """A candidate repeated many times ties with itself at the k-th place: the better item
+    listed once must still win (the merge takes every entry above the k-th, then repeats)."""
+    d = 64
+    items = np.zeros((4, d), np.int8)
+    items[1, :] = 2  # best
+    items[2, :] = 1  # repeated
+    q = np.ones((1, d), np.int8)
+    for reps in (7, 300, 5000):
+        cand = np.array([[2] * reps + [1] + [3] * 20], np.int64)
+        ids, sc = torch.ops.retrieve.int8_candidates_topk(
+            _t(dev, q), _t(dev, items), _t(dev, cand), _t(dev, np.array([cand.shape[1]])), 5)
+        assert ids.cpu().tolist() == [[1, 2, 2, 2, 2]], reps
+        assert sc.cpu().tolist() == [[128, 64, 64, 64, 64]]
+
+
 def test_oporp_indirect(dev):
     g = rng(92)
     b, n, w, p = 6, 30000, 8, 2000

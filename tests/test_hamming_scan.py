@@ -49,7 +49,8 @@ def test_popcount_kat(dev, kat):
 @pytest.mark.parametrize(
     "b,n,w,k",
     [(1, 1, 8, 1), (1, 100, 1, 10), (5, 3000, 2, 50), (16, 20000, 8, 100),
-     (65, 10000, 4, 100), (3, 50000, 16, 1000), (70, 4099, 8, 7)],
+     (65, 10000, 4, 100), (3, 50000, 16, 1000), (70, 4099, 8, 7), (9, 7000, 3, 64),
+     (4, 5000, 5, 40), (33, 3000, 12, 100)],
 )
 def test_random_parity(dev, b, n, w, k):
     g = rng(b * 7 + n + w * 13 + k)

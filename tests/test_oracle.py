@@ -149,6 +149,36 @@ def test_quantize_zero_and_tiny_rows():
     assert codes[1, 3] == 0  # 1e-30 / 1e-8 * 127 rounds to 0
 
 
+def _nearest_f32(fr) -> np.float32:
+    """The float32 nearest the rational ``fr`` (ties to even), by exact comparison."""
+    from fractions import Fraction
+
+    lo = np.float32(float(fr))  # within one ulp of fr
+    best = None
+    for c in (np.nextafter(lo, np.float32(-np.inf)), lo, np.nextafter(lo, np.float32(np.inf))):
+        err = abs(Fraction(float(c)) - fr)
+        key = (err, int(np.frombuffer(c.tobytes(), np.uint32)[0]) & 1)
+        if best is None or key < best[0]:
+            best = (key, c)
+    return best[1]
+
+
+def test_quantize_divide_scale_is_the_rounded_quotient():
+    """The ``divide`` scale is the float32 nearest ``abs_max / 127`` (exact rational), which
+    differs from ``abs_max * fp32(1/127)`` for some ``abs_max``; the codes do not depend on it."""
+    from fractions import Fraction
+
+    g = rng(77)
+    x = (g.standard_normal((400, 8)) * np.exp(3 * g.standard_normal((400, 1)))).astype(np.float32)
+    codes_d, s_div = oq.quantize_int8(x, divide=True)
+    codes_m, s_mul = oq.quantize_int8(x)
+    assert np.array_equal(codes_d, codes_m)
+    m = np.abs(x).max(axis=1)
+    for i in range(x.shape[0]):
+        assert s_div[i] == _nearest_f32(Fraction(float(m[i])) / 127)
+    assert (s_div != s_mul).any()
+
+
 def test_pack_signs_lsb_first():
     v = np.full((1, 128), -1.0, np.float32)
     v[0, 0] = 1.0  # word 0 bit 0
