@@ -1,15 +1,24 @@
 // Large-batch dense scans with the exact fused top-k: register-blocked 32x32 MFMA tiles.
 //
-// A workgroup owns 256 queries: each 64-query group's B-operand fragments stay in the registers
-// of its wave(s) for the whole kernel. Item tiles of 64 rows are dealt round-robin to the
-// workgroups of a query group; a tile is read once from HBM with coalesced loads straight into
-// LDS (3-4 stages in flight), and each wave multiplies its rows against its 64 queries in 32x32
-// output tiles (v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_{bf16,f16}: each instruction
-// consumes 32 bytes of K per row). At 512-byte rows two waves share a query group, 32 rows each
-// (8 waves, two per SIMD: one's MFMAs run while the other reads LDS or tests its scores); below,
-// one wave takes all 64 rows (4 waves, two workgroups per CU). Lane l of an output tile holds query
-// (col tile * 32 + l % 32) and, in register i, item (row tile * 32 + (i/4)*8 + (l/32)*4 + i%4).
-// Per MFMA, lane l feeds bytes [32 s + 16 (l / 32), +16) of its row on both sides.
+// A workgroup owns 256 queries, eight 32-query column tiles. Item tiles of 64 rows are dealt
+// round-robin to the workgroups of a query group; a tile is read once from HBM with coalesced
+// loads straight into LDS (3-8 stages in flight). Each wave holds the B-operand fragments of two
+// column tiles in registers for the whole kernel and multiplies staged rows against them in
+// 32x32 output tiles (v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_{bf16,f16}: each instruction
+// consumes 32 bytes of K per row). Two layouts, both with two waves per SIMD:
+// - wide (up to 128 queries): eight waves, one workgroup per CU; wave w takes row half w & 1 of
+//   every 64-row tile against column tiles w / 2 and w / 2 + 4. With fewer than 256 queries the
+//   live column tiles are the low ones, so 64 queries keep one wave per SIMD busy and 128 all
+//   eight.
+// - narrow (larger batches): four waves, two workgroups per CU, each on its own tiles, so one
+//   workgroup's score tests overlap the other's MFMAs (a workgroup's waves move in step through
+//   its per-tile barrier). Wave w takes every row of a tile against column tiles w and w + 4:
+//   64-row tiles (two row tiles per wave) below 512-byte rows, 32-row tiles at 512 bytes, where
+//   the fragments of two column tiles leave registers for one row tile and four stages fit in
+//   half the LDS.
+// Lane l of an output tile holds query (col tile * 32 + l % 32) and, in register i, item
+// (row tile * 32 + (i/4)*8 + (l/32)*4 + i%4). Per MFMA, lane l feeds bytes
+// [32 s + 16 (l / 32), +16) of its row on both sides.
 //
 // Operand reuse: each staged item byte feeds 64 queries per wave and each register-held query
 // byte feeds every item of the grid row, so the matrix cores, not LDS or HBM, bound the
@@ -28,17 +37,33 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
-constexpr int kBlkRows = 64;      // items per staged tile
-constexpr int kBlkQpw = 64;       // queries per wave
-constexpr int kBlkQgWaves = 4;    // 64-query groups per workgroup
-constexpr int kBlkQpg = kBlkQgWaves * kBlkQpw;  // queries per workgroup (query group)
+constexpr int kBlkRows = 64;      // items per staged tile (at most)
+constexpr int kBlkQpw = 64;       // queries per wave (two 32-query column tiles)
+constexpr int kBlkCols = 8;       // 32-query column tiles per workgroup
+constexpr int kBlkQpg = kBlkCols * 32;  // queries per workgroup (query group)
+// Up to this many queries, rows narrower than 512 bytes take the wide layout.
+constexpr int64_t kBlkWideMaxBatch = 128;
 
-// Waves per query group: at 512-byte rows two (each takes 32 rows of a tile: 8 waves, two per
-// SIMD, fit the registers of 64 queries' fragments); below, one wave takes all 64 rows and two
-// 4-wave workgroups share a CU.
-constexpr int blk_row_halves(int64_t rb) { return rb >= 512 ? 2 : 1; }
-constexpr int blk_waves(int64_t rb) { return kBlkQgWaves * blk_row_halves(rb); }
-constexpr int blk_threads(int64_t rb) { return blk_waves(rb) * kWave; }
+template <bool WIDE, int RB>
+struct BlkLayout {
+  static constexpr int waves = WIDE ? 8 : 4;
+  static constexpr int threads = waves * kWave;
+  static constexpr int halves = WIDE ? 2 : 1;  // row tiles split over waves: a query's lists per
+                                               // workgroup
+  // rows per staged tile: 32 for narrow 512-byte rows, so four stages fit in half the LDS
+  static constexpr int rows = !WIDE && RB >= 512 ? 32 : kBlkRows;
+  static constexpr int rtw = rows / 32 / halves;  // 32-row tiles per wave
+  static constexpr int per_cu = WIDE ? 1 : 2;     // resident workgroups per CU
+};
+
+constexpr int blk_rows(int64_t row_bytes, bool wide) {
+  return !wide && row_bytes >= 512 ? 32 : kBlkRows;
+}
+
+static bool blk_wide(int64_t row_bytes, int64_t B) {
+  (void)row_bytes;
+  return B <= kBlkWideMaxBatch;
+}
 // Cache-policy bits of the main pass's direct-to-LDS loads (streamed once: nontemporal).
 constexpr int kNontemporal = 2;
 
@@ -87,21 +112,16 @@ struct F16x32 : BF16x32 {
   }
 };
 
-// Staged tiles: 4 when they fit in LDS beside the lists (more bytes in flight per CU), else 3
-// (512-byte rows with large k).
-constexpr int blk_min_stages(int64_t rb) { return rb >= 512 ? 3 : 4; }
-constexpr int kBlkMaxStages = 4;
+// Staged tiles: as many of 8, 4, 3 as fit in LDS beside the lists (more bytes in flight per CU).
+constexpr int kBlkMinStages = 3;
 
-template <int RB, int STAGES>
+template <int RB, int STAGES, int ROWS>
 constexpr size_t blk_stage_bytes() {
-  return static_cast<size_t>(STAGES) * kBlkRows * RB;
+  return static_cast<size_t>(STAGES) * ROWS * RB;
 }
 
-// Waves per SIMD: two (one 8-wave workgroup per CU at 512-byte rows, two 4-wave ones below).
-template <int RB>
-constexpr int blk_waves_per_simd() {
-  return 2;
-}
+// Waves per SIMD: two (one 8-wave or two 4-wave workgroups per CU).
+constexpr int kBlkWavesPerSimd = 2;
 
 __device__ inline int32_t imax(int32_t a, int32_t b) { return a > b ? a : b; }
 
@@ -136,6 +156,20 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
+// vmcnt <= later * LOADS for a wave-uniform later in [0, MAXL] (the immediate must be constant).
+template <int LOADS, int MAXL>
+__device__ inline void wait_later(int later) {
+  if constexpr (MAXL > 0) {
+    if (later >= MAXL) {
+      wait_vmcnt<MAXL * LOADS>();
+      return;
+    }
+    wait_later<LOADS, MAXL - 1>(later);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
 // Workgroup barrier over the staged tiles: waits for this wave's LDS accesses (lgkmcnt(0)),
 // then s_barrier. __syncthreads() would also wait for every outstanding global load (its
 // workgroup release fence), draining the tiles still in flight; the direct-to-LDS loads of the
@@ -150,49 +184,53 @@ __device__ inline void tile_barrier() {
 
 // SEED: per query, each workgroup's best composite over the strided sample, written to
 // lists[q * gridDim.x + workgroup] (one-entry lists); else candidate lists per (wave, query).
-template <class Op, int RB, bool SEED, int STAGES>
-__global__ void __launch_bounds__(blk_threads(RB))
-    __attribute__((amdgpu_waves_per_eu(blk_waves_per_simd<RB>(), blk_waves_per_simd<RB>())))
+template <class Op, int RB, bool SEED, int STAGES, bool WIDE>
+__global__ void __launch_bounds__((BlkLayout<WIDE, RB>::threads))
+    __attribute__((amdgpu_waves_per_eu(kBlkWavesPerSimd, kBlkWavesPerSimd)))
     scan_blocked_kernel(ScanArgs a) {
   using Score = typename Op::Score;
+  using L = BlkLayout<WIDE, RB>;
+  constexpr int ROWS = L::rows;
   constexpr int KS = RB / 32;  // MFMA steps per row
-  constexpr int kBlkRowHalves = blk_row_halves(RB);
-  constexpr int kBlkWaves = blk_waves(RB);
-  constexpr int kBlkThreads = blk_threads(RB);
-  constexpr int RTW = 2 / kBlkRowHalves;  // 32-row tiles per wave
-  constexpr int TILE_BYTES = kBlkRows * RB;
+  constexpr int RTW = L::rtw;  // 32-row tiles per wave
+  constexpr int kBlkWaves = L::waves;
+  constexpr int kBlkThreads = L::threads;
+  constexpr int kBlkRowHalves = L::halves;
+  constexpr int TILE_BYTES = ROWS * RB;
   constexpr int LOADS = TILE_BYTES / (kBlkThreads * 16);  // 16-byte loads per thread per tile
   constexpr int CH = RB / 16;                              // 16-byte chunks per row
   static_assert(TILE_BYTES % (kBlkThreads * 16) == 0, "tile must split into 16-byte loads");
   static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   int8_t* stage = reinterpret_cast<int8_t*>(smem);
-  uint64_t* scratch = reinterpret_cast<uint64_t*>(stage + blk_stage_bytes<RB, STAGES>());
+  uint64_t* scratch = reinterpret_cast<uint64_t*>(stage + blk_stage_bytes<RB, STAGES, ROWS>());
   const int tid = threadIdx.x;
   const int lane = lane_id();
-  const int wave = tid >> 6;
+  // wave-uniform, so what derives from it (row half, column tiles, list slots) lives in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c32 = lane & 31;
   const int half = lane >> 5;
   int* cnt = reinterpret_cast<int*>(scratch + kBlkWaves * a.capw) + wave * kBlkQpw;
-  const int wq = wave % kBlkQgWaves;  // this wave's 64-query group in the workgroup
-  const int wr = wave / kBlkQgWaves;  // and its 32 rows of each tile
+  const int wr = WIDE ? wave & 1 : 0;      // this wave's first 32-row tile of each tile
+  const int jt = WIDE ? wave >> 1 : wave;  // and its column tiles jt, jt + 4
 
   const int64_t wg = blockIdx.x;
   const int64_t nwg = gridDim.x;
-  const int64_t q0 = static_cast<int64_t>(blockIdx.y) * kBlkQpg + wq * kBlkQpw;
-  // this wave's 32-query column tiles that hold real queries (wave-uniform)
-  const int cols = q0 >= a.B ? 0 : (q0 + 32 >= a.B ? 1 : 2);
+  const int64_t qg0 = static_cast<int64_t>(blockIdx.y) * kBlkQpg;
+  // query of this lane in column tile j (0, 1) of the wave: qg0 + 32 (jt + 4 j) + c32
+  const int64_t q0[2] = {qg0 + 32 * jt, qg0 + 32 * (jt + 4)};
+  // this wave's column tiles that hold real queries (wave-uniform; tile 1 only with tile 0)
+  const int cols = (q0[0] < a.B ? 1 : 0) + (q0[1] < a.B ? 1 : 0);
   const int8_t* Q = static_cast<const int8_t*>(a.queries);
   const int8_t* I = static_cast<const int8_t*>(a.items);
 
-  // this lane's queries: q0 + c32 (col tile 0) and q0 + 32 + c32 (col tile 1)
   v4i qf[2][KS];
   uint64_t tau[2];
   Score ts[2];
   const uint64_t* qmask[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int64_t q = q0 + 32 * j + c32;
+    const int64_t q = q0[j] + c32;
     if (q < a.B) {
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
@@ -211,11 +249,16 @@ __global__ void __launch_bounds__(blk_threads(RB))
   int32_t th[2] = {Op::skey(ts[0]), Op::skey(ts[1])};
   bool raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
   uint64_t best[2] = {0ull, 0ull};  // SEED
-  // list slot of this wave: query group (64 queries) g = blockIdx.y * 4 + wq; a query's lists
-  // are slots g * S + s, s = wg * 2 + wr (S = 2 nwg per query)
-  const int64_t slot =
-      ((static_cast<int64_t>(blockIdx.y) * kBlkQgWaves + wq) * nwg + wg) * kBlkRowHalves + wr;
-  uint64_t* lists = a.lists + slot * kBlkQpw * static_cast<int64_t>(a.capw);
+  // list slots of this wave, one per column tile: a 32-query column tile g = q / 32 has slots
+  // g * S + s, s = wg * 2 + wr (S = 2 nwg), each holding 32 lists of capw entries
+  int64_t slot[2];
+  uint64_t* lists[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t g = static_cast<int64_t>(blockIdx.y) * kBlkCols + jt + 4 * j;
+    slot[j] = (g * nwg + wg) * kBlkRowHalves + wr;
+    lists[j] = a.lists + slot[j] * 32 * static_cast<int64_t>(a.capw);
+  }
   // list lengths of this lane's two queries (the same in both halves of the wave): each list
   // belongs to this wave alone, so appends take positions from ballots, not atomics
   int nq[2] = {0, 0};
@@ -223,7 +266,7 @@ __global__ void __launch_bounds__(blk_threads(RB))
   const int64_t n = a.n_rows;
   // the main pass may scan every tstride-th tile only (the threshold sample pass)
   const int64_t tstride = !SEED && a.tile_stride > 1 ? a.tile_stride : 1;
-  const int64_t ntiles = cdiv(cdiv(n, kBlkRows), tstride);
+  const int64_t ntiles = cdiv(cdiv(n, ROWS), tstride);
   // Staged tile layout (no padding): row r's 16-byte chunk c sits at r * RB + (c ^ (r % CH)) * 16,
   // so the 32 rows of an MFMA read start on different banks. A wave's direct-to-LDS load writes
   // 1 KiB contiguously in lane order, so the swizzle goes into the global address each lane
@@ -241,7 +284,7 @@ __global__ void __launch_bounds__(blk_threads(RB))
   auto issue = [&](int64_t lt, int st) {
     const int64_t tt = lt * tstride;  // the tile in the item table
     int8_t* base = stage + st * TILE_BYTES;
-    if (!SEED && (tt + 1) * kBlkRows <= n) {
+    if (!SEED && (tt + 1) * ROWS <= n) {
       // a full tile of consecutive rows: a uniform tile address plus 32-bit lane offsets
       const int8_t* tile = I + tt * static_cast<int64_t>(TILE_BYTES);
 #pragma unroll
@@ -263,7 +306,7 @@ __global__ void __launch_bounds__(blk_threads(RB))
 #pragma unroll
     for (int l = 0; l < LOADS; ++l) {
       const int r = toff[l] / RB;
-      int64_t row = tt * kBlkRows + r;
+      int64_t row = tt * ROWS + r;
       row = row < n ? row : n - 1;  // rows past the end load a valid row and are never scored
       const int8_t* g = I + row * a.row_stride * RB + toff[l] % RB;
       __builtin_amdgcn_global_load_lds(
@@ -274,25 +317,21 @@ __global__ void __launch_bounds__(blk_threads(RB))
   };
 
   int64_t t = wg;
+  // this workgroup's tiles: wg, wg + nwg, ...
+  const int64_t my_tiles = wg < ntiles ? cdiv(ntiles - wg, nwg) : 0;
 #pragma unroll
   for (int st = 0; st < STAGES - 1; ++st) {
     if (t + st * nwg < ntiles) issue(t + st * nwg, st);
   }
-  static_assert(STAGES >= 3 && STAGES <= 4, "wait ladder covers 1-2 later tiles");
+  static_assert(STAGES >= 3 && STAGES <= 8, "stage count");
   for (int it = 0; t < ntiles; ++it, t += nwg) {
     // Tile t has landed once at most the loads of this workgroup's later tiles issued so far
     // (up to STAGES - 2 of them) are outstanding: vmcnt retires in issue order on this
     // architecture, one counter for loads and stores, so list stores issued in between only
     // make the wait stricter.
-    const int64_t after = (ntiles - 1 - t) / nwg;  // this workgroup's tiles after t
+    const int64_t after = my_tiles - 1 - it;  // this workgroup's tiles after t
     const int later = static_cast<int>(after < STAGES - 2 ? after : STAGES - 2);
-    if (later >= 2) {
-      wait_vmcnt<STAGES >= 4 ? 2 * LOADS : 0>();
-    } else if (later == 1) {
-      wait_vmcnt<LOADS>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    wait_later<LOADS, STAGES - 2>(later);
     // every wave's share of tile t is in LDS, and every wave is done reading tile t - nwg, whose
     // stage the next load goes into
     tile_barrier();
@@ -311,21 +350,36 @@ __global__ void __launch_bounds__(blk_threads(RB))
       for (int i = 0; i < RTW; ++i)
 #pragma unroll
         for (int j = 0; j < NC; ++j) acc[i][j] = Op::zero();
+      // row fragments of step s: lane l reads bytes [32 s + 16 (l / 32), +16) of its row;
+      // PF steps are read ahead so the LDS latency hides behind the MFMAs
+      auto frag = [&](int s, int i) {
+        const int r = 32 * (wr + i) + c32;
+        return *reinterpret_cast<const v4i*>(src + r * RB + (((2 * s + half) ^ (r % CH)) * 16));
+      };
+      constexpr int PF = KS < 4 ? KS : 4;
+      v4i af[PF][RTW];
+#pragma unroll
+      for (int s = 0; s < PF; ++s)
+#pragma unroll
+        for (int i = 0; i < RTW; ++i) af[s][i] = frag(s, i);
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        v4i af[RTW];
+        v4i cur[RTW];
 #pragma unroll
         for (int i = 0; i < RTW; ++i) {
-          const int r = 32 * (wr + i) + c32;
-          af[i] = *reinterpret_cast<const v4i*>(src + r * RB + (((2 * s + half) ^ (r % CH)) * 16));
+          cur[i] = af[s % PF][i];
+          if (s + PF < KS) af[s % PF][i] = frag(s + PF, i);
         }
+        // keep the read of step s + PF ahead of step s's MFMAs (the scheduler would otherwise
+        // sink it next to its use to save registers)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
 #pragma unroll
-          for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(af[i], qf[j][s], acc[i][j]);
+          for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(cur[i], qf[j][s], acc[i][j]);
       }
       // register r of tile (i, j) holds row t * 64 + 32 i + (r / 4) * 8 + 4 half + r % 4
-      const int64_t rt = t * tstride * kBlkRows + 4 * half;
+      const int64_t rt = t * tstride * ROWS + 4 * half;
       if constexpr (SEED) {
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
@@ -392,8 +446,7 @@ __global__ void __launch_bounds__(blk_threads(RB))
                   const int lo = static_cast<int>(static_cast<uint32_t>(kb) >> c32 & 1u);
                   const int hi = static_cast<int>(static_cast<uint32_t>(kb >> 32) >> c32 & 1u);
                   if (keep) {
-                    lists[(32 * j + c32) * static_cast<int64_t>(a.capw) + nq[j] + (half ? lo : 0)] =
-                        c;
+                    lists[j][c32 * static_cast<int64_t>(a.capw) + nq[j] + (half ? lo : 0)] = c;
                   }
                   nq[j] += lo + hi;
                 }
@@ -402,14 +455,14 @@ __global__ void __launch_bounds__(blk_threads(RB))
           // the next one (wave_compact waits for the stores above before reading them back)
 #pragma unroll
           for (int jq = 0; jq < NC; ++jq) {
-            uint64_t need = __ballot(nq[jq] > a.capw - kBlkRows) & 0xffffffffull;
+            uint64_t need = __ballot(nq[jq] > a.capw - ROWS) & 0xffffffffull;
             while (need != 0ull) {
               const int c = __builtin_ctzll(need);
               need &= need - 1;
               const int q = 32 * jq + c;
               if (lane == c) cnt[q] = nq[jq];
-              const uint64_t nt = wave_compact(lists + q * static_cast<int64_t>(a.capw), &cnt[q],
-                                               scratch + wave * a.capw, a.capw, a.k);
+              const uint64_t nt = wave_compact(lists[jq] + c * static_cast<int64_t>(a.capw),
+                                               &cnt[q], scratch + wave * a.capw, a.capw, a.k);
               if (c32 == c) {
                 nq[jq] = cnt[q];
                 if (nt > tau[jq]) {
@@ -437,56 +490,79 @@ __global__ void __launch_bounds__(blk_threads(RB))
     for (int j = 0; j < 2; ++j) {
       const uint64_t o = __shfl_xor(best[j], 32);
       const uint64_t b = o > best[j] ? o : best[j];
-      const int64_t q = q0 + 32 * j + c32;
+      const int64_t q = q0[j] + c32;
       if (half == 0 && q < a.B) a.lists[(q * nwg + wg) * kBlkRowHalves + wr] = b;
     }
   } else if (half == 0) {
-    a.counts[slot * kBlkQpw + c32] = nq[0];
-    a.counts[slot * kBlkQpw + 32 + c32] = nq[1];
+    a.counts[slot[0] * 32 + c32] = nq[0];
+    a.counts[slot[1] * 32 + c32] = nq[1];
   }
 }
 
 constexpr size_t kMaxLds = 160 * 1024;
 
-static size_t blk_lds(int64_t row_bytes, int stages, int capw) {
-  return static_cast<size_t>(stages) * kBlkRows * row_bytes +
-         blk_waves(row_bytes) * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
+static size_t blk_lds(int64_t row_bytes, int stages, int capw, bool wide) {
+  return static_cast<size_t>(stages) * blk_rows(row_bytes, wide) * row_bytes +
+         (wide ? 8 : 4) * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
 }
 
-template <class Op, int RB, bool SEED, int STAGES>
+// The deepest staging that fits a workgroup's share of LDS (all of it wide, half narrow, so two
+// narrow workgroups stay resident), 0 when even three stages do not fit in the whole LDS.
+static int blk_stages(int64_t row_bytes, int capw, bool wide) {
+  const size_t share = wide ? kMaxLds : kMaxLds / 2;
+  const int deepest = wide && row_bytes < 512 ? 8 : 4;
+  for (int s : {8, 4, 3}) {
+    if (s <= deepest && blk_lds(row_bytes, s, capw, wide) <= share) return s;
+  }
+  return blk_lds(row_bytes, kBlkMinStages, capw, wide) <= kMaxLds ? kBlkMinStages : 0;
+}
+
+template <class Op, int RB, bool SEED, int STAGES, bool WIDE>
 static int launch_blk_staged(const ScanArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  const void* fn = reinterpret_cast<const void*>(scan_blocked_kernel<Op, RB, SEED, STAGES>);
+  const void* fn = reinterpret_cast<const void*>(scan_blocked_kernel<Op, RB, SEED, STAGES, WIDE>);
   if (lds > 65536) {
     RT_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds)));
   }
-  scan_blocked_kernel<Op, RB, SEED, STAGES><<<grid, blk_threads(RB), lds, stream>>>(a);
+  scan_blocked_kernel<Op, RB, SEED, STAGES, WIDE>
+      <<<grid, BlkLayout<WIDE, RB>::threads, lds, stream>>>(a);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }
 
+template <class Op, int RB, bool SEED, bool WIDE>
+static int launch_blk_layout(const ScanArgs& a, dim3 grid, int capw, hipStream_t stream) {
+  const int stages = blk_stages(RB, capw, WIDE);
+  const size_t lds = blk_lds(RB, stages, capw, WIDE);
+  if constexpr (WIDE && RB < 512) {
+    if (stages == 8) return launch_blk_staged<Op, RB, SEED, 8, WIDE>(a, grid, lds, stream);
+  }
+  if (stages == 4) return launch_blk_staged<Op, RB, SEED, 4, WIDE>(a, grid, lds, stream);
+  if (stages == 3) return launch_blk_staged<Op, RB, SEED, 3, WIDE>(a, grid, lds, stream);
+  set_error("the blocked scan's lists do not fit in LDS at %d-byte rows", RB);
+  return kInvalidArgument;
+}
+
 template <class Op, int RB>
-static int launch_blk(const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed,
+static int launch_blk(const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed, bool wide,
                       hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.gx), static_cast<unsigned>(nqg));
   const int capw = seed ? 0 : p.capw;
-  const bool deep = blk_lds(RB, kBlkMaxStages, capw) <= kMaxLds;
-  const size_t lds = blk_lds(RB, deep ? kBlkMaxStages : 3, capw);
-  if (seed) {
-    return deep ? launch_blk_staged<Op, RB, true, kBlkMaxStages>(a, grid, lds, stream)
-                : launch_blk_staged<Op, RB, true, 3>(a, grid, lds, stream);
+  if (wide) {
+    return seed ? launch_blk_layout<Op, RB, true, true>(a, grid, capw, stream)
+                : launch_blk_layout<Op, RB, false, true>(a, grid, capw, stream);
   }
-  return deep ? launch_blk_staged<Op, RB, false, kBlkMaxStages>(a, grid, lds, stream)
-              : launch_blk_staged<Op, RB, false, 3>(a, grid, lds, stream);
+  return seed ? launch_blk_layout<Op, RB, true, false>(a, grid, capw, stream)
+              : launch_blk_layout<Op, RB, false, false>(a, grid, capw, stream);
 }
 
 template <class Op>
 static int dispatch_blk(int64_t row_bytes, const ScanArgs& a, const PassPlan& p, int64_t nqg,
-                        bool seed, hipStream_t stream) {
+                        bool seed, bool wide, hipStream_t stream) {
   switch (row_bytes) {
-    case 128: return launch_blk<Op, 128>(a, p, nqg, seed, stream);
-    case 256: return launch_blk<Op, 256>(a, p, nqg, seed, stream);
-    case 512: return launch_blk<Op, 512>(a, p, nqg, seed, stream);
+    case 128: return launch_blk<Op, 128>(a, p, nqg, seed, wide, stream);
+    case 256: return launch_blk<Op, 256>(a, p, nqg, seed, wide, stream);
+    case 512: return launch_blk<Op, 512>(a, p, nqg, seed, wide, stream);
     default:
       set_error("blocked scan supports rows of 128, 256 or 512 bytes, got %lld",
                 static_cast<long long>(row_bytes));
@@ -494,19 +570,22 @@ static int dispatch_blk(int64_t row_bytes, const ScanArgs& a, const PassPlan& p,
   }
 }
 
-static size_t blk_lds_for(int64_t row_bytes, int capw) {
-  return blk_lds(row_bytes, blk_min_stages(row_bytes), capw);
+// List capacity: k plus a tile's appends (64 per query), a power of two (sorted whole).
+static int blk_capw(int64_t k) { return static_cast<int>(next_pow2(k + kBlkRows)); }
+
+static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int64_t target_cus) {
+  const bool wide = blk_wide(row_bytes, B);
+  return plan_scan(B, N, k, kBlkQpg, (wide ? 8 : 4) * kBlkQpw, target_cus * (wide ? 1 : 2),
+                   blk_capw(k), kBlkRows);
 }
 
-// The threshold sample pass (512-byte rows, batches of at least kSampleMinBatch queries: where
+// The threshold sample pass (batches of at least kSampleMinBatch queries: where
 // the list appends behind the seed's bound cost more than the pass): every kSampleTileStride-th
 // tile, when that gives kSampleMinTiles tiles or more.
 constexpr int64_t kSampleMinBatch = 512;
 constexpr int64_t kSampleTileStride = 8;
 constexpr int64_t kSampleMinTiles = 4096;
 
-// List capacity: k plus a tile's appends (64 per query), a power of two (sorted whole).
-static int blk_capw(int64_t k) { return static_cast<int>(next_pow2(k + kBlkRows)); }
 
 
 template <class Op>
@@ -529,11 +608,9 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   if (hipGetDevice(&dev) == hipSuccess) {
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   }
-  // workgroups resident per CU: one 8-wave workgroup at 512-byte rows, two 4-wave ones below
-  const int64_t per_cu = row_bytes >= 512 ? 1 : 2;
-  const ScanPlan plan = plan_scan(B, N, k, kBlkQpg, blk_waves(row_bytes) * kBlkQpw,
-                                  cus * per_cu, blk_capw(k), kBlkRows);
-  RT_CHECK_ARG(blk_lds_for(row_bytes, plan.main.capw) <= kMaxLds,
+  const bool wide = blk_wide(row_bytes, B);
+  const ScanPlan plan = blk_plan(B, N, k, row_bytes, cus);
+  RT_CHECK_ARG(blk_stages(row_bytes, plan.main.capw, wide) != 0,
                "k = %lld is too large for the blocked scan at %lld-byte rows",
                static_cast<long long>(k), static_cast<long long>(row_bytes));
   if (workspace_bytes < plan.total) {
@@ -559,7 +636,7 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   MergeArgs m{};
   m.lists = lists;
   m.counts = counts;
-  m.qpw = kBlkQpw;  // one list per query per slot; a slot is (64-query group, workgroup)
+  m.qpw = 32;  // one list per query per slot; a slot is (32-query column tile, workgroup, half)
   m.B = B;
   m.k = static_cast<int>(k);
 
@@ -568,7 +645,7 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
     a.row_stride = plan.seed.row_stride;
     a.capw = 1;
     a.tau_in = nullptr;
-    int st = dispatch_blk<Op>(row_bytes, a, plan.seed, plan.n_qgroups, true, stream);
+    int st = dispatch_blk<Op>(row_bytes, a, plan.seed, plan.n_qgroups, true, wide, stream);
     if (st != kOk) return st;
     m.capw = 1;
     m.flat = true;
@@ -583,13 +660,13 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   a.row_stride = 1;
   a.capw = plan.main.capw;
   a.tau_in = plan.seeded ? tau : nullptr;
-  if (plan.seeded && row_bytes >= 512 && B >= kSampleMinBatch &&
+  if (plan.seeded && B >= kSampleMinBatch &&
       N >= kSampleMinTiles * kSampleTileStride * kBlkRows) {
     // at large batches the list appends behind a loose bound cost more than the matrix work:
     // the exact k-th over every kSampleTileStride-th tile (the main kernel on those tiles, then
     // a threshold merge) tightens the bound about N / (sample rows) fold for the main pass
     a.tile_stride = kSampleTileStride;
-    int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, stream);
+    int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, wide, stream);
     if (st != kOk) return st;
     m.capw = plan.main.capw;
     m.S = plan.main.S;
@@ -603,7 +680,7 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   }
   hipEvent_t stop;
   profile_begin(stream, &stop);
-  int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, stream);
+  int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, wide, stream);
   profile_end(stream, stop);
   if (st != kOk) return st;
   m.capw = plan.main.capw;
@@ -620,9 +697,8 @@ using namespace rt;
 
 extern "C" size_t rt_blocked_scan_topk_workspace(int64_t B, int64_t N, int64_t row_bytes,
                                                  int64_t k) {
-  return plan_scan(B, N, k, kBlkQpg, blk_waves(row_bytes) * kBlkQpw, kMaxResidentWorkgroups,
-                   blk_capw(k), kBlkRows)
-      .total;
+  // (the most workgroups any device runs: the workspace covers every CU count)
+  return blk_plan(B, N, k, row_bytes, kMaxResidentWorkgroups).total;
 }
 
 // dtype: 0 int8 (int32 scores), 1 bf16, 2 fp16 (float scores); D elements per row.

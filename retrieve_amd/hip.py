@@ -33,8 +33,9 @@ _BLOCKED_ROW_BYTES = (128, 256, 512)
 
 def _use_blocked(b: int, row_bytes: int, k: int) -> bool:
     capw = 1 << (k + 64 - 1).bit_length()
-    waves = 8 if row_bytes >= 512 else 4
-    lds = (3 if row_bytes >= 512 else 4) * 64 * row_bytes + waves * (capw * 8 + 64 * 4)
+    wide = b <= 128  # the kernel's wide / narrow layout
+    rows = 32 if not wide and row_bytes >= 512 else 64
+    lds = 3 * rows * row_bytes + (8 if wide else 4) * (capw * 8 + 64 * 4)
     return b >= BLOCKED_MIN_BATCH and row_bytes in _BLOCKED_ROW_BYTES and lds <= 160 * 1024
 
 
