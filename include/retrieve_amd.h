@@ -60,10 +60,12 @@ int rt_dense_scan_topk(const void* queries, int64_t B, const void* items, int64_
  * 32x32 MFMA tiles, 256 queries per workgroup held in registers, item tiles shared through
  * LDS. dtype 0 = int8 (int32 scores), 1 = bf16, 2 = fp16 (float scores). Rows of 128, 256 or
  * 512 bytes (int8 D in {128, 256, 512}; 16-bit D in {64, 128, 256}). `row_bytes` of the
- * workspace function is D times the element size.
+ * workspace function is D times the element size; `masked` != 0 sizes it for a call with a mask
+ * (the mask is transposed into the workspace, ceil(N/64) x B words rounded up to 256 queries).
  * Replaces: the same reference paths as rt_int8_scan_topk / rt_dense_scan_topk at batches
  *   where they become a GEMM (B >= 128). */
-size_t rt_blocked_scan_topk_workspace(int64_t B, int64_t N, int64_t row_bytes, int64_t k);
+size_t rt_blocked_scan_topk_workspace(int64_t B, int64_t N, int64_t row_bytes, int64_t k,
+                                      int masked);
 int rt_blocked_scan_topk(const void* queries, int64_t B, const void* items, int64_t N, int64_t D,
                          int64_t k, int dtype, const uint64_t* mask, int64_t mask_words,
                          int64_t* out_ids, void* out_scores, void* workspace,
@@ -72,11 +74,13 @@ int rt_blocked_scan_topk(const void* queries, int64_t B, const void* items, int6
 /* Exact 1-bit Hamming top-k over a full code table: query_bits [B, W] x item_bits [N, W]
  * (uint64 words, bit b of word w = dimension 64 w + b), score = 64 W - 2 popcount(q ^ item),
  * top-k by (score desc, index asc) -> ids int64 [B, k], scores [B, k] (int32, or float when
- * score_f32 != 0). 1 <= W <= 16; 1 <= k <= 1024. `mask` as for rt_int8_scan_topk.
+ * score_f32 != 0). 1 <= W <= 16; 1 <= k <= 1024. `mask` as for rt_int8_scan_topk. 512-bit
+ * codes (W = 8) from 8 queries on run on the int8 matrix cores (bits as bytes); `masked` of the
+ * workspace function as for rt_blocked_scan_topk_workspace.
  * Replaces: the Triton full-scan kernel + torch.topk of
  *   retrieve/src/retrieve/ops/triton/oporp_1bit_match_topk.py:47-122, 217-234, 261-273
  *   (torch.ops.retrieve.oporp_1bit_match_topk_full). */
-size_t rt_hamming_scan_topk_workspace(int64_t B, int64_t N, int64_t W, int64_t k);
+size_t rt_hamming_scan_topk_workspace(int64_t B, int64_t N, int64_t W, int64_t k, int masked);
 int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits,
                          int64_t N, int64_t W, int64_t k, const uint64_t* mask,
                          int64_t mask_words, int64_t* out_ids, void* out_scores, int score_f32,

@@ -25,7 +25,7 @@ _c_int = ctypes.c_int
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rt_last_error": (ctypes.c_char_p, []),
     "rt_int8_scan_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
-    "rt_hamming_scan_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "rt_hamming_scan_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
     "rt_hamming_scan_topk": (
         _c_int,
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_int, _c_p,
@@ -37,7 +37,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_p, _c_p,
          _c_sz, _c_p],
     ),
-    "rt_blocked_scan_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "rt_blocked_scan_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
     "rt_blocked_scan_topk": (
         _c_int,
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_p, _c_p,

@@ -1,704 +1,13 @@
-// Large-batch dense scans with the exact fused top-k: register-blocked 32x32 MFMA tiles.
-//
-// A workgroup owns 256 queries, eight 32-query column tiles. Item tiles of 64 rows are dealt
-// round-robin to the workgroups of a query group; a tile is read once from HBM with coalesced
-// loads straight into LDS (3-8 stages in flight). Each wave holds the B-operand fragments of two
-// column tiles in registers for the whole kernel and multiplies staged rows against them in
-// 32x32 output tiles (v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_{bf16,f16}: each instruction
-// consumes 32 bytes of K per row). Two layouts, both with two waves per SIMD:
-// - wide (up to 128 queries): eight waves, one workgroup per CU; wave w takes row half w & 1 of
-//   every 64-row tile against column tiles w / 2 and w / 2 + 4. With fewer than 256 queries the
-//   live column tiles are the low ones, so 64 queries keep one wave per SIMD busy and 128 all
-//   eight.
-// - narrow (larger batches): four waves, two workgroups per CU, each on its own tiles, so one
-//   workgroup's score tests overlap the other's MFMAs (a workgroup's waves move in step through
-//   its per-tile barrier). Wave w takes every row of a tile against column tiles w and w + 4:
-//   64-row tiles (two row tiles per wave) below 512-byte rows, 32-row tiles at 512 bytes, where
-//   the fragments of two column tiles leave registers for one row tile and four stages fit in
-//   half the LDS.
-// Lane l of an output tile holds query (col tile * 32 + l % 32) and, in register i, item
-// (row tile * 32 + (i/4)*8 + (l/32)*4 + i%4). Per MFMA, lane l feeds bytes
-// [32 s + 16 (l / 32), +16) of its row on both sides.
-//
-// Operand reuse: each staged item byte feeds 64 queries per wave and each register-held query
-// byte feeds every item of the grid row, so the matrix cores, not LDS or HBM, bound the
-// kernel at large batches.
-#include <type_traits>
-
-#include "profile.h"
-#include "scan_common.h"
-#include "wave_lists.h"
-
-namespace rt {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-
-constexpr int kBlkRows = 64;      // items per staged tile (at most)
-constexpr int kBlkQpw = 64;       // queries per wave (two 32-query column tiles)
-constexpr int kBlkCols = 8;       // 32-query column tiles per workgroup
-constexpr int kBlkQpg = kBlkCols * 32;  // queries per workgroup (query group)
-// Up to this many queries, rows narrower than 512 bytes take the wide layout.
-constexpr int64_t kBlkWideMaxBatch = 128;
-
-template <bool WIDE, int RB>
-struct BlkLayout {
-  static constexpr int waves = WIDE ? 8 : 4;
-  static constexpr int threads = waves * kWave;
-  static constexpr int halves = WIDE ? 2 : 1;  // row tiles split over waves: a query's lists per
-                                               // workgroup
-  // rows per staged tile: 32 for narrow 512-byte rows, so four stages fit in half the LDS
-  static constexpr int rows = !WIDE && RB >= 512 ? 32 : kBlkRows;
-  static constexpr int rtw = rows / 32 / halves;  // 32-row tiles per wave
-  static constexpr int per_cu = WIDE ? 1 : 2;     // resident workgroups per CU
-};
-
-constexpr int blk_rows(int64_t row_bytes, bool wide) {
-  return !wide && row_bytes >= 512 ? 32 : kBlkRows;
-}
-
-static bool blk_wide(int64_t row_bytes, int64_t B) {
-  (void)row_bytes;
-  return B <= kBlkWideMaxBatch;
-}
-// Cache-policy bits of the main pass's direct-to-LDS loads (streamed once: nontemporal).
-constexpr int kNontemporal = 2;
-
-struct I8x32 {
-  using Score = int32_t;
-  using Acc = v16i;
-  static constexpr int kind = kScoreI32;
-  __device__ static Acc zero() { return Acc{}; }
-  __device__ static Acc mma(v4i a, v4i b, Acc c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-  }
-  __device__ static uint32_t key(Score s) { return key_of_i32(s); }
-  __device__ static Score thresh(uint64_t tau) { return i32_of_key(composite_key(tau)); }
-  // scores are already ordered ints: the hit test takes maxima of the raw values
-  static constexpr bool kIntScores = true;
-  __device__ static int32_t skey(Score s) { return s; }
-};
-
-struct BF16x32 {
-  using Score = float;
-  using Acc = v16f;
-  static constexpr int kind = kScoreF32;
-  __device__ static Acc zero() { return Acc{}; }
-  __device__ static Acc mma(v4i a, v4i b, Acc c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a),
-                                                   __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
-  }
-  __device__ static uint32_t key(Score s) { return key_of_f32(s); }
-  __device__ static Score thresh(uint64_t tau) {
-    const uint32_t k = composite_key(tau);
-    return k <= key_of_f32(-INFINITY) ? -INFINITY : f32_of_key(k);
-  }
-  static constexpr bool kIntScores = false;
-  // Order-preserving map of a float to int32 (signed compare): the bits of a non-negative
-  // float, the magnitude bits flipped for a negative one (-0.0 maps below +0.0, as in key order).
-  __device__ static int32_t skey(Score s) {
-    const int32_t b = __builtin_bit_cast(int32_t, s);
-    return b >= 0 ? b : b ^ 0x7fffffff;
-  }
-};
-
-struct F16x32 : BF16x32 {
-  __device__ static Acc mma(v4i a, v4i b, Acc c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a),
-                                                  __builtin_bit_cast(v8h, b), c, 0, 0, 0);
-  }
-};
-
-// Staged tiles: as many of 8, 4, 3 as fit in LDS beside the lists (more bytes in flight per CU).
-constexpr int kBlkMinStages = 3;
-
-template <int RB, int STAGES, int ROWS>
-constexpr size_t blk_stage_bytes() {
-  return static_cast<size_t>(STAGES) * ROWS * RB;
-}
-
-// Waves per SIMD: two (one 8-wave or two 4-wave workgroups per CU).
-constexpr int kBlkWavesPerSimd = 2;
-
-__device__ inline int32_t imax(int32_t a, int32_t b) { return a > b ? a : b; }
-
-// Max of 4 accumulator values in the signed-int key domain of Op::skey. RAW: take maxima of the
-// raw bits as ints (v_max3_i32, no NaN canonicalisation) -- exact for every value with the sign
-// bit clear and below every such value otherwise, so it decides "max >= threshold" whenever the
-// threshold's key is >= 0. Else the float max (NaN drops out) mapped through skey.
-// (by value: __builtin_bit_cast applied directly to a vector element v[i] reads element 0)
-template <class S>
-__device__ inline int32_t raw_bits(S s) {
-  return __builtin_bit_cast(int32_t, s);
-}
-
-template <class Op, bool RAW, class Acc>
-__device__ inline int32_t group_max(const Acc& v, int g) {
-  if constexpr (RAW) {
-    return imax(imax(imax(raw_bits(v[4 * g]), raw_bits(v[4 * g + 1])), raw_bits(v[4 * g + 2])),
-                raw_bits(v[4 * g + 3]));
-  } else {
-    const float m = __builtin_fmaxf(__builtin_fmaxf(static_cast<float>(v[4 * g]),
-                                                    static_cast<float>(v[4 * g + 1])),
-                                    __builtin_fmaxf(static_cast<float>(v[4 * g + 2]),
-                                                    static_cast<float>(v[4 * g + 3])));
-    return Op::skey(static_cast<typename Op::Score>(m));
-  }
-}
-
-// s_waitcnt immediate: vmcnt <= N (N < 64), expcnt and lgkmcnt unconstrained (gfx9 encoding).
-template <int N>
-__device__ inline void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
-
-// vmcnt <= later * LOADS for a wave-uniform later in [0, MAXL] (the immediate must be constant).
-template <int LOADS, int MAXL>
-__device__ inline void wait_later(int later) {
-  if constexpr (MAXL > 0) {
-    if (later >= MAXL) {
-      wait_vmcnt<MAXL * LOADS>();
-      return;
-    }
-    wait_later<LOADS, MAXL - 1>(later);
-  } else {
-    wait_vmcnt<0>();
-  }
-}
-
-// Workgroup barrier over the staged tiles: waits for this wave's LDS accesses (lgkmcnt(0)),
-// then s_barrier. __syncthreads() would also wait for every outstanding global load (its
-// workgroup release fence), draining the tiles still in flight; the direct-to-LDS loads of the
-// tile about to be read are covered by the wait_vmcnt before this. The empty asm statements
-// keep the compiler from moving memory accesses across the barrier.
-__device__ inline void tile_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt and expcnt unconstrained
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// SEED: per query, each workgroup's best composite over the strided sample, written to
-// lists[q * gridDim.x + workgroup] (one-entry lists); else candidate lists per (wave, query).
-template <class Op, int RB, bool SEED, int STAGES, bool WIDE>
-__global__ void __launch_bounds__((BlkLayout<WIDE, RB>::threads))
-    __attribute__((amdgpu_waves_per_eu(kBlkWavesPerSimd, kBlkWavesPerSimd)))
-    scan_blocked_kernel(ScanArgs a) {
-  using Score = typename Op::Score;
-  using L = BlkLayout<WIDE, RB>;
-  constexpr int ROWS = L::rows;
-  constexpr int KS = RB / 32;  // MFMA steps per row
-  constexpr int RTW = L::rtw;  // 32-row tiles per wave
-  constexpr int kBlkWaves = L::waves;
-  constexpr int kBlkThreads = L::threads;
-  constexpr int kBlkRowHalves = L::halves;
-  constexpr int TILE_BYTES = ROWS * RB;
-  constexpr int LOADS = TILE_BYTES / (kBlkThreads * 16);  // 16-byte loads per thread per tile
-  constexpr int CH = RB / 16;                              // 16-byte chunks per row
-  static_assert(TILE_BYTES % (kBlkThreads * 16) == 0, "tile must split into 16-byte loads");
-  static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
-  extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
-  int8_t* stage = reinterpret_cast<int8_t*>(smem);
-  uint64_t* scratch = reinterpret_cast<uint64_t*>(stage + blk_stage_bytes<RB, STAGES, ROWS>());
-  const int tid = threadIdx.x;
-  const int lane = lane_id();
-  // wave-uniform, so what derives from it (row half, column tiles, list slots) lives in SGPRs
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c32 = lane & 31;
-  const int half = lane >> 5;
-  int* cnt = reinterpret_cast<int*>(scratch + kBlkWaves * a.capw) + wave * kBlkQpw;
-  const int wr = WIDE ? wave & 1 : 0;      // this wave's first 32-row tile of each tile
-  const int jt = WIDE ? wave >> 1 : wave;  // and its column tiles jt, jt + 4
-
-  const int64_t wg = blockIdx.x;
-  const int64_t nwg = gridDim.x;
-  const int64_t qg0 = static_cast<int64_t>(blockIdx.y) * kBlkQpg;
-  // query of this lane in column tile j (0, 1) of the wave: qg0 + 32 (jt + 4 j) + c32
-  const int64_t q0[2] = {qg0 + 32 * jt, qg0 + 32 * (jt + 4)};
-  // this wave's column tiles that hold real queries (wave-uniform; tile 1 only with tile 0)
-  const int cols = (q0[0] < a.B ? 1 : 0) + (q0[1] < a.B ? 1 : 0);
-  const int8_t* Q = static_cast<const int8_t*>(a.queries);
-  const int8_t* I = static_cast<const int8_t*>(a.items);
-
-  v4i qf[2][KS];
-  uint64_t tau[2];
-  Score ts[2];
-  const uint64_t* qmask[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t q = q0[j] + c32;
-    if (q < a.B) {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        qf[j][s] = *reinterpret_cast<const v4i*>(Q + q * RB + 32 * s + 16 * half);
-      }
-      tau[j] = a.tau_in != nullptr ? a.tau_in[q] : 0ull;
-    } else {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) qf[j][s] = v4i{0, 0, 0, 0};
-      tau[j] = ~0ull;
-    }
-    ts[j] = Op::thresh(tau[j]);
-    qmask[j] = a.mask != nullptr && q < a.B ? a.mask + q * a.mask_words : nullptr;
-  }
-  // thresholds in the skey domain, and whether the raw-bits group maxima decide the hit test
-  int32_t th[2] = {Op::skey(ts[0]), Op::skey(ts[1])};
-  bool raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
-  uint64_t best[2] = {0ull, 0ull};  // SEED
-  // list slots of this wave, one per column tile: a 32-query column tile g = q / 32 has slots
-  // g * S + s, s = wg * 2 + wr (S = 2 nwg), each holding 32 lists of capw entries
-  int64_t slot[2];
-  uint64_t* lists[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t g = static_cast<int64_t>(blockIdx.y) * kBlkCols + jt + 4 * j;
-    slot[j] = (g * nwg + wg) * kBlkRowHalves + wr;
-    lists[j] = a.lists + slot[j] * 32 * static_cast<int64_t>(a.capw);
-  }
-  // list lengths of this lane's two queries (the same in both halves of the wave): each list
-  // belongs to this wave alone, so appends take positions from ballots, not atomics
-  int nq[2] = {0, 0};
-
-  const int64_t n = a.n_rows;
-  // the main pass may scan every tstride-th tile only (the threshold sample pass)
-  const int64_t tstride = !SEED && a.tile_stride > 1 ? a.tile_stride : 1;
-  const int64_t ntiles = cdiv(cdiv(n, ROWS), tstride);
-  // Staged tile layout (no padding): row r's 16-byte chunk c sits at r * RB + (c ^ (r % CH)) * 16,
-  // so the 32 rows of an MFMA read start on different banks. A wave's direct-to-LDS load writes
-  // 1 KiB contiguously in lane order, so the swizzle goes into the global address each lane
-  // fetches (a permutation within the row: still one contiguous 1 KiB span per instruction).
-  int toff[LOADS];  // this lane's byte offset in a full tile (row r, swizzled chunk c)
-#pragma unroll
-  for (int l = 0; l < LOADS; ++l) {
-    const int sidx = l * kBlkThreads + wave * kWave + lane;  // 16-byte slot of the tile
-    const int r = sidx / CH;
-    toff[l] = r * RB + ((sidx % CH) ^ (r % CH)) * 16;
-  }
-  // Several query groups (gridDim.y > 1) read the same tiles from this XCD's L2: keep the lines
-  // (temporal loads); with one group each tile is read once and streams past (nontemporal).
-  const bool shared_tiles = gridDim.y > 1;
-  auto issue = [&](int64_t lt, int st) {
-    const int64_t tt = lt * tstride;  // the tile in the item table
-    int8_t* base = stage + st * TILE_BYTES;
-    if (!SEED && (tt + 1) * ROWS <= n) {
-      // a full tile of consecutive rows: a uniform tile address plus 32-bit lane offsets
-      const int8_t* tile = I + tt * static_cast<int64_t>(TILE_BYTES);
-#pragma unroll
-      for (int l = 0; l < LOADS; ++l) {
-        // (the global address goes through a named pointer: passing the sum straight to the
-        // builtin drops the kernel from the host-side compile)
-        const int8_t* g = tile + toff[l];
-        int8_t* dst = base + (l * kBlkThreads + wave * kWave) * 16;
-        if (shared_tiles) {
-          __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(dst), 16,
-                                           0, 0);
-        } else {
-          __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(dst), 16,
-                                           0, kNontemporal);
-        }
-      }
-      return;
-    }
-#pragma unroll
-    for (int l = 0; l < LOADS; ++l) {
-      const int r = toff[l] / RB;
-      int64_t row = tt * ROWS + r;
-      row = row < n ? row : n - 1;  // rows past the end load a valid row and are never scored
-      const int8_t* g = I + row * a.row_stride * RB + toff[l] % RB;
-      __builtin_amdgcn_global_load_lds(
-          g,
-          (__attribute__((address_space(3))) void*)(base + (l * kBlkThreads + wave * kWave) * 16),
-          16, 0, 0);
-    }
-  };
-
-  int64_t t = wg;
-  // this workgroup's tiles: wg, wg + nwg, ...
-  const int64_t my_tiles = wg < ntiles ? cdiv(ntiles - wg, nwg) : 0;
-#pragma unroll
-  for (int st = 0; st < STAGES - 1; ++st) {
-    if (t + st * nwg < ntiles) issue(t + st * nwg, st);
-  }
-  static_assert(STAGES >= 3 && STAGES <= 8, "stage count");
-  for (int it = 0; t < ntiles; ++it, t += nwg) {
-    // Tile t has landed once at most the loads of this workgroup's later tiles issued so far
-    // (up to STAGES - 2 of them) are outstanding: vmcnt retires in issue order on this
-    // architecture, one counter for loads and stores, so list stores issued in between only
-    // make the wait stricter.
-    const int64_t after = my_tiles - 1 - it;  // this workgroup's tiles after t
-    const int later = static_cast<int>(after < STAGES - 2 ? after : STAGES - 2);
-    wait_later<LOADS, STAGES - 2>(later);
-    // every wave's share of tile t is in LDS, and every wave is done reading tile t - nwg, whose
-    // stage the next load goes into
-    tile_barrier();
-    const int64_t tn = t + (STAGES - 1) * nwg;
-    if (tn < ntiles) issue(tn, (it + STAGES - 1) % STAGES);
-
-    // only the 32-query column tiles that hold real queries are multiplied (NC of them; a
-    // wave of padding only helps with the loads)
-    auto tile_body = [&](auto nc) {
-      constexpr int NC = decltype(nc)::value;
-      const int8_t* src = stage + (it % STAGES) * TILE_BYTES;
-      // 2 x 2 output tiles (rows 32 i + ..., this wave's query columns 32 j + ...): four
-      // independent accumulator chains keep the matrix pipeline full
-      typename Op::Acc acc[RTW][NC];
-#pragma unroll
-      for (int i = 0; i < RTW; ++i)
-#pragma unroll
-        for (int j = 0; j < NC; ++j) acc[i][j] = Op::zero();
-      // row fragments of step s: lane l reads bytes [32 s + 16 (l / 32), +16) of its row;
-      // PF steps are read ahead so the LDS latency hides behind the MFMAs
-      auto frag = [&](int s, int i) {
-        const int r = 32 * (wr + i) + c32;
-        return *reinterpret_cast<const v4i*>(src + r * RB + (((2 * s + half) ^ (r % CH)) * 16));
-      };
-      constexpr int PF = KS < 4 ? KS : 4;
-      v4i af[PF][RTW];
-#pragma unroll
-      for (int s = 0; s < PF; ++s)
-#pragma unroll
-        for (int i = 0; i < RTW; ++i) af[s][i] = frag(s, i);
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        v4i cur[RTW];
-#pragma unroll
-        for (int i = 0; i < RTW; ++i) {
-          cur[i] = af[s % PF][i];
-          if (s + PF < KS) af[s % PF][i] = frag(s + PF, i);
-        }
-        // keep the read of step s + PF ahead of step s's MFMAs (the scheduler would otherwise
-        // sink it next to its use to save registers)
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < RTW; ++i)
-#pragma unroll
-          for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(cur[i], qf[j][s], acc[i][j]);
-      }
-      // register r of tile (i, j) holds row t * 64 + 32 i + (r / 4) * 8 + 4 half + r % 4
-      const int64_t rt = t * tstride * ROWS + 4 * half;
-      if constexpr (SEED) {
-#pragma unroll
-        for (int i = 0; i < RTW; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int64_t row = rt + 32 * (wr + i) + (r / 4) * 8 + (r % 4);
-            const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
-#pragma unroll
-            for (int j = 0; j < NC; ++j) {
-              bool ok = row < n;
-              if (ok && qmask[j] != nullptr) {
-                ok = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
-              }
-              const uint64_t c = composite(Op::key(acc[i][j][r]), item);
-              best[j] = ok && c > best[j] ? c : best[j];
-            }
-          }
-      } else {
-        // fast path: the max of each group of 4 registers (rows 8 g + 4 half + 0..3), and one
-        // compare per tile column against the max of its 4 group maxima
-        int32_t gm[RTW][NC][4];
-        bool hit = false;
-        if (raw) {
-#pragma unroll
-          for (int i = 0; i < RTW; ++i)
-#pragma unroll
-            for (int j = 0; j < NC; ++j) {
-#pragma unroll
-              for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, true>(acc[i][j], g);
-              hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= th[j];
-            }
-        } else {
-#pragma unroll
-          for (int i = 0; i < RTW; ++i)
-#pragma unroll
-            for (int j = 0; j < NC; ++j) {
-#pragma unroll
-              for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, false>(acc[i][j], g);
-              hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= th[j];
-            }
-        }
-        if (__any(hit)) {
-          // slow path, narrowed by wave-uniform ballots: groups with a hit, then their registers
-#pragma unroll
-          for (int i = 0; i < RTW; ++i)
-#pragma unroll
-            for (int j = 0; j < NC; ++j)
-#pragma unroll
-              for (int g = 0; g < 4; ++g) {
-                if (__ballot(gm[i][j][g] >= th[j]) == 0ull) continue;
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                  const Score sc = acc[i][j][4 * g + u];
-                  if (__ballot(sc >= ts[j]) == 0ull) continue;
-                  const int64_t row = rt + 32 * (wr + i) + 8 * g + u;
-                  const uint32_t item = static_cast<uint32_t>(row);
-                  const uint64_t c = composite(Op::key(sc), item);
-                  bool keep = row < n && sc >= ts[j] && c >= tau[j];
-                  if (keep && qmask[j] != nullptr) {
-                    keep = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
-                  }
-                  // lanes l and l ^ 32 score the same query: the upper half's entry goes second
-                  const uint64_t kb = __ballot(keep);
-                  const int lo = static_cast<int>(static_cast<uint32_t>(kb) >> c32 & 1u);
-                  const int hi = static_cast<int>(static_cast<uint32_t>(kb >> 32) >> c32 & 1u);
-                  if (keep) {
-                    lists[j][c32 * static_cast<int64_t>(a.capw) + nq[j] + (half ? lo : 0)] = c;
-                  }
-                  nq[j] += lo + hi;
-                }
-              }
-          // a query gains at most 32 entries per tile: compact the lists that could overflow on
-          // the next one (wave_compact waits for the stores above before reading them back)
-#pragma unroll
-          for (int jq = 0; jq < NC; ++jq) {
-            uint64_t need = __ballot(nq[jq] > a.capw - ROWS) & 0xffffffffull;
-            while (need != 0ull) {
-              const int c = __builtin_ctzll(need);
-              need &= need - 1;
-              const int q = 32 * jq + c;
-              if (lane == c) cnt[q] = nq[jq];
-              const uint64_t nt = wave_compact(lists[jq] + c * static_cast<int64_t>(a.capw),
-                                               &cnt[q], scratch + wave * a.capw, a.capw, a.k);
-              if (c32 == c) {
-                nq[jq] = cnt[q];
-                if (nt > tau[jq]) {
-                  tau[jq] = nt;
-                  ts[jq] = Op::thresh(nt);
-                  th[jq] = Op::skey(ts[jq]);
-                }
-              }
-            }
-          }
-          raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
-        }
-      }
-    };
-    if (cols == 2) {
-      tile_body(std::integral_constant<int, 2>{});
-    } else if (cols == 1) {
-      tile_body(std::integral_constant<int, 1>{});
-    }
-  }
-
-  if constexpr (SEED) {
-    // flat one-entry lists: a query's maxima, one per workgroup, at lists[q * nwg + wg]
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint64_t o = __shfl_xor(best[j], 32);
-      const uint64_t b = o > best[j] ? o : best[j];
-      const int64_t q = q0[j] + c32;
-      if (half == 0 && q < a.B) a.lists[(q * nwg + wg) * kBlkRowHalves + wr] = b;
-    }
-  } else if (half == 0) {
-    a.counts[slot[0] * 32 + c32] = nq[0];
-    a.counts[slot[1] * 32 + c32] = nq[1];
-  }
-}
-
-constexpr size_t kMaxLds = 160 * 1024;
-
-static size_t blk_lds(int64_t row_bytes, int stages, int capw, bool wide) {
-  return static_cast<size_t>(stages) * blk_rows(row_bytes, wide) * row_bytes +
-         (wide ? 8 : 4) * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
-}
-
-// The deepest staging that fits a workgroup's share of LDS (all of it wide, half narrow, so two
-// narrow workgroups stay resident), 0 when even three stages do not fit in the whole LDS.
-static int blk_stages(int64_t row_bytes, int capw, bool wide) {
-  const size_t share = wide ? kMaxLds : kMaxLds / 2;
-  const int deepest = wide && row_bytes < 512 ? 8 : 4;
-  for (int s : {8, 4, 3}) {
-    if (s <= deepest && blk_lds(row_bytes, s, capw, wide) <= share) return s;
-  }
-  return blk_lds(row_bytes, kBlkMinStages, capw, wide) <= kMaxLds ? kBlkMinStages : 0;
-}
-
-template <class Op, int RB, bool SEED, int STAGES, bool WIDE>
-static int launch_blk_staged(const ScanArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  const void* fn = reinterpret_cast<const void*>(scan_blocked_kernel<Op, RB, SEED, STAGES, WIDE>);
-  if (lds > 65536) {
-    RT_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     static_cast<int>(lds)));
-  }
-  scan_blocked_kernel<Op, RB, SEED, STAGES, WIDE>
-      <<<grid, BlkLayout<WIDE, RB>::threads, lds, stream>>>(a);
-  RT_CHECK_HIP(hipGetLastError());
-  return kOk;
-}
-
-template <class Op, int RB, bool SEED, bool WIDE>
-static int launch_blk_layout(const ScanArgs& a, dim3 grid, int capw, hipStream_t stream) {
-  const int stages = blk_stages(RB, capw, WIDE);
-  const size_t lds = blk_lds(RB, stages, capw, WIDE);
-  if constexpr (WIDE && RB < 512) {
-    if (stages == 8) return launch_blk_staged<Op, RB, SEED, 8, WIDE>(a, grid, lds, stream);
-  }
-  if (stages == 4) return launch_blk_staged<Op, RB, SEED, 4, WIDE>(a, grid, lds, stream);
-  if (stages == 3) return launch_blk_staged<Op, RB, SEED, 3, WIDE>(a, grid, lds, stream);
-  set_error("the blocked scan's lists do not fit in LDS at %d-byte rows", RB);
-  return kInvalidArgument;
-}
-
-template <class Op, int RB>
-static int launch_blk(const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed, bool wide,
-                      hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(p.gx), static_cast<unsigned>(nqg));
-  const int capw = seed ? 0 : p.capw;
-  if (wide) {
-    return seed ? launch_blk_layout<Op, RB, true, true>(a, grid, capw, stream)
-                : launch_blk_layout<Op, RB, false, true>(a, grid, capw, stream);
-  }
-  return seed ? launch_blk_layout<Op, RB, true, false>(a, grid, capw, stream)
-              : launch_blk_layout<Op, RB, false, false>(a, grid, capw, stream);
-}
-
-template <class Op>
-static int dispatch_blk(int64_t row_bytes, const ScanArgs& a, const PassPlan& p, int64_t nqg,
-                        bool seed, bool wide, hipStream_t stream) {
-  switch (row_bytes) {
-    case 128: return launch_blk<Op, 128>(a, p, nqg, seed, wide, stream);
-    case 256: return launch_blk<Op, 256>(a, p, nqg, seed, wide, stream);
-    case 512: return launch_blk<Op, 512>(a, p, nqg, seed, wide, stream);
-    default:
-      set_error("blocked scan supports rows of 128, 256 or 512 bytes, got %lld",
-                static_cast<long long>(row_bytes));
-      return kInvalidArgument;
-  }
-}
-
-// List capacity: k plus a tile's appends (64 per query), a power of two (sorted whole).
-static int blk_capw(int64_t k) { return static_cast<int>(next_pow2(k + kBlkRows)); }
-
-static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int64_t target_cus) {
-  const bool wide = blk_wide(row_bytes, B);
-  return plan_scan(B, N, k, kBlkQpg, (wide ? 8 : 4) * kBlkQpw, target_cus * (wide ? 1 : 2),
-                   blk_capw(k), kBlkRows);
-}
-
-// The threshold sample pass (batches of at least kSampleMinBatch queries: where
-// the list appends behind the seed's bound cost more than the pass): every kSampleTileStride-th
-// tile, when that gives kSampleMinTiles tiles or more.
-constexpr int64_t kSampleMinBatch = 512;
-constexpr int64_t kSampleTileStride = 8;
-constexpr int64_t kSampleMinTiles = 4096;
-
-
-
-template <class Op>
-static int run_blocked(const void* queries, int64_t B, const void* items, int64_t N,
-                       int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
-                       int64_t* out_ids, void* out_scores, void* workspace,
-                       size_t workspace_bytes, hipStream_t stream) {
-  RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
-  RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
-               static_cast<long long>(kMaxK), static_cast<long long>(k));
-  RT_CHECK_ARG(N < 0xffffffffll, "N must be < 2**32 - 1");
-  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(queries) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(items) % 16 == 0,
-               "queries and items must be 16-byte aligned");
-  RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
-  if (B == 0) return kOk;
-  if (N == 0) return launch_pad(out_ids, out_scores, B, k, Op::kind, stream);
-  int dev = 0;
-  int cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  }
-  const bool wide = blk_wide(row_bytes, B);
-  const ScanPlan plan = blk_plan(B, N, k, row_bytes, cus);
-  RT_CHECK_ARG(blk_stages(row_bytes, plan.main.capw, wide) != 0,
-               "k = %lld is too large for the blocked scan at %lld-byte rows",
-               static_cast<long long>(k), static_cast<long long>(row_bytes));
-  if (workspace_bytes < plan.total) {
-    set_error("workspace too small: %zu < %zu", workspace_bytes, plan.total);
-    return kWorkspaceTooSmall;
-  }
-  char* ws = static_cast<char*>(workspace);
-  uint64_t* lists = reinterpret_cast<uint64_t*>(ws + plan.off_lists);
-  int* counts = reinterpret_cast<int*>(ws + plan.off_counts);
-  uint64_t* tau = reinterpret_cast<uint64_t*>(ws + plan.off_tau);
-
-  ScanArgs a{};
-  a.queries = queries;
-  a.B = B;
-  a.items = items;
-  a.k = static_cast<int>(k);
-  a.qpw = kBlkQpw;
-  a.mask = mask;
-  a.mask_words = mask_words;
-  a.lists = lists;
-  a.counts = counts;
-
-  MergeArgs m{};
-  m.lists = lists;
-  m.counts = counts;
-  m.qpw = 32;  // one list per query per slot; a slot is (32-query column tile, workgroup, half)
-  m.B = B;
-  m.k = static_cast<int>(k);
-
-  if (plan.seeded) {
-    a.n_rows = plan.seed.n_rows;
-    a.row_stride = plan.seed.row_stride;
-    a.capw = 1;
-    a.tau_in = nullptr;
-    int st = dispatch_blk<Op>(row_bytes, a, plan.seed, plan.n_qgroups, true, wide, stream);
-    if (st != kOk) return st;
-    m.capw = 1;
-    m.flat = true;
-    m.S = plan.seed.S;
-    m.tau_out = tau;
-    st = launch_merge(m, stream);
-    if (st != kOk) return st;
-    m.tau_out = nullptr;
-    m.flat = false;
-  }
-  a.n_rows = N;
-  a.row_stride = 1;
-  a.capw = plan.main.capw;
-  a.tau_in = plan.seeded ? tau : nullptr;
-  if (plan.seeded && B >= kSampleMinBatch &&
-      N >= kSampleMinTiles * kSampleTileStride * kBlkRows) {
-    // at large batches the list appends behind a loose bound cost more than the matrix work:
-    // the exact k-th over every kSampleTileStride-th tile (the main kernel on those tiles, then
-    // a threshold merge) tightens the bound about N / (sample rows) fold for the main pass
-    a.tile_stride = kSampleTileStride;
-    int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, wide, stream);
-    if (st != kOk) return st;
-    m.capw = plan.main.capw;
-    m.S = plan.main.S;
-    m.tau_out = tau;
-    m.tau_keep = true;
-    st = launch_merge(m, stream);
-    if (st != kOk) return st;
-    m.tau_out = nullptr;
-    m.tau_keep = false;
-    a.tile_stride = 1;
-  }
-  hipEvent_t stop;
-  profile_begin(stream, &stop);
-  int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, wide, stream);
-  profile_end(stream, stop);
-  if (st != kOk) return st;
-  m.capw = plan.main.capw;
-  m.S = plan.main.S;
-  m.out_ids = out_ids;
-  m.out_scores = out_scores;
-  m.score_kind = Op::kind;
-  return launch_merge(m, stream);
-}
-
-}  // namespace rt
+// The large-batch dense scans' C entry points; the kernels are in scan_blocked.h, instantiated
+// per operand type in scan_blocked_{i8,bf16,f16,bits}.hip.
+#include "scan_blocked.h"
 
 using namespace rt;
 
 extern "C" size_t rt_blocked_scan_topk_workspace(int64_t B, int64_t N, int64_t row_bytes,
-                                                 int64_t k) {
+                                                 int64_t k, int masked) {
   // (the most workgroups any device runs: the workspace covers every CU count)
-  return blk_plan(B, N, k, row_bytes, kMaxResidentWorkgroups).total;
+  return blk_plan(B, N, k, row_bytes, kMaxResidentWorkgroups, false, masked != 0).total;
 }
 
 // dtype: 0 int8 (int32 scores), 1 bf16, 2 fp16 (float scores); D elements per row.
@@ -708,16 +17,17 @@ extern "C" int rt_blocked_scan_topk(const void* queries, int64_t B, const void* 
                                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
   switch (dtype) {
     case 0:
-      return run_blocked<I8x32>(queries, B, items, N, D, k, mask, mask_words, out_ids,
-                                out_scores, workspace, workspace_bytes, stream);
+      return blocked_scan_i8(queries, B, items, N, D, k, mask, mask_words, out_ids, out_scores,
+                             workspace, workspace_bytes, stream);
     case 1:
-      return run_blocked<BF16x32>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
-                                  out_scores, workspace, workspace_bytes, stream);
+      return blocked_scan_bf16(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
+                               out_scores, workspace, workspace_bytes, stream);
     case 2:
-      return run_blocked<F16x32>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
-                                 out_scores, workspace, workspace_bytes, stream);
+      return blocked_scan_f16(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
+                              out_scores, workspace, workspace_bytes, stream);
     default:
       set_error("blocked scan dtype must be 0 (int8), 1 (bf16) or 2 (fp16), got %d", dtype);
       return kInvalidType;
   }
 }
+

@@ -36,6 +36,8 @@ struct ScanArgs {
   const uint64_t* tau_in;  // [B] lower bounds (composites) or null
   const uint64_t* mask;    // [B, mask_words] item bits, item d at bit 63 - d % 64, or null
   int64_t mask_words;
+  const uint64_t* mask_t;  // the mask transposed, [ceil(N/64), mask_t_stride] (blocked scan)
+  int64_t mask_t_stride;
   uint64_t* lists;         // [slots, qpw, capw]
   int* counts;             // [slots, qpw]
 };
@@ -92,6 +94,16 @@ constexpr int64_t kMainWorkgroupsPerCU = 2;
 
 // Main-pass workgroups for the current device: CUs x kMainWorkgroupsPerCU.
 int64_t main_workgroups();
+
+// The 1-bit Hamming top-k on the int8 matrix cores (scan_blocked.hip): codes of W 64-bit words
+// (W == 8), scores 64 W - 2 popcount(q ^ x) written as score_kind (kScoreI32 or
+// kScoreF32FromI32).
+bool blocked_hamming_fits(int64_t B, int64_t W, int64_t k, bool masked);  // lists fit in LDS
+size_t blocked_hamming_workspace(int64_t B, int64_t N, int64_t W, int64_t k, bool masked);
+int blocked_hamming(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, int64_t N,
+                    int64_t W, int64_t k, const uint64_t* mask, int64_t mask_words,
+                    int64_t* out_ids, void* out_scores, int score_kind, void* workspace,
+                    size_t workspace_bytes, hipStream_t stream);
 
 // Sizes the passes for B queries over N rows and top-k. A workgroup row (grid.y) covers qpg
 // queries and each workgroup keeps lists_per_wg candidate lists (of main_capw entries in the

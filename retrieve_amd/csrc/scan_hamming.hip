@@ -234,12 +234,23 @@ static int dispatch_ham(int64_t W, const ScanArgs& a, const PassPlan& p, int64_t
 
 static int ham_qpw(int64_t B) { return static_cast<int>(B < kHamMaxQpw ? B : kHamMaxQpw); }
 
+// From this batch on, 512-bit codes are scored on the int8 matrix cores (the blocked scan with
+// bits expanded to bytes); below, one XOR + popcount pass per query and word.
+constexpr int64_t kHamMfmaMinBatch = 8;
+
+static bool ham_mfma(int64_t B, int64_t W, int64_t k, bool masked) {
+  return W == 8 && B >= kHamMfmaMinBatch && blocked_hamming_fits(B, W, k, masked);
+}
+
 }  // namespace rt
 
 using namespace rt;
 
-extern "C" size_t rt_hamming_scan_topk_workspace(int64_t B, int64_t N, int64_t W, int64_t k) {
-  (void)W;
+extern "C" size_t rt_hamming_scan_topk_workspace(int64_t B, int64_t N, int64_t W, int64_t k,
+                                                 int masked) {
+  if (ham_mfma(B, W, k, masked != 0)) {
+    return blocked_hamming_workspace(B, N, W, k, masked != 0);
+  }
   const int qpw = ham_qpw(B > 0 ? B : 1);
   return plan_scan(B, N, k, qpw, kScanWaves * qpw, kMaxResidentWorkgroups, ham_capw(k),
                    kScanWaves * kHamTile)
@@ -265,6 +276,10 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B,
   if (B == 0) return kOk;
   const int kind = score_f32 ? kScoreF32FromI32 : kScoreI32;
   if (N == 0) return launch_pad(out_ids, out_scores, B, k, kind, stream);
+  if (ham_mfma(B, W, k, mask != nullptr)) {
+    return blocked_hamming(query_bits, B, item_bits, N, W, k, mask, mask_words, out_ids,
+                           out_scores, kind, workspace, workspace_bytes, stream);
+  }
   const int qpw = ham_qpw(B);
   const ScanPlan plan = plan_scan(B, N, k, qpw, kScanWaves * qpw, main_workgroups(), ham_capw(k),
                                   kScanWaves * kHamTile);

@@ -35,7 +35,8 @@ def _use_blocked(b: int, row_bytes: int, k: int) -> bool:
     capw = 1 << (k + 64 - 1).bit_length()
     wide = b <= 128  # the kernel's wide / narrow layout
     rows = 32 if not wide and row_bytes >= 512 else 64
-    lds = 3 * rows * row_bytes + (8 if wide else 4) * (capw * 8 + 64 * 4)
+    stage = rows * row_bytes + 256 * (rows // 32) * 4  # a tile and its mask words
+    lds = 3 * stage + (8 if wide else 4) * (capw * 8 + 64 * 4)
     return b >= BLOCKED_MIN_BATCH and row_bytes in _BLOCKED_ROW_BYTES and lds <= 160 * 1024
 
 
@@ -45,7 +46,8 @@ def _blocked(q: Tensor, items: Tensor, k: int, dtype: int, mask: Tensor | None,
     n = items.shape[0]
     lib = nat.lib()
     dev = q.device
-    ws = nat.workspace(lib.rt_blocked_scan_topk_workspace(b, n, d * q.element_size(), k), dev)
+    ws = nat.workspace(lib.rt_blocked_scan_topk_workspace(b, n, d * q.element_size(), k,
+                                                          int(mask is not None)), dev)
     with torch.cuda.device(dev):
         st = lib.rt_blocked_scan_topk(
             nat.ptr(q), b, nat.ptr(items), n, d, k, dtype, nat.ptr(mask),
@@ -212,7 +214,8 @@ def _hamming_call(query_bits, item_bits, k, mask, score_dtype):
     ids = torch.empty((b, k), dtype=torch.int64, device=dev)
     scores = torch.empty((b, k), dtype=score_dtype, device=dev)
     lib = nat.lib()
-    ws = nat.workspace(lib.rt_hamming_scan_topk_workspace(b, n, w, k), dev)
+    ws = nat.workspace(lib.rt_hamming_scan_topk_workspace(b, n, w, k, int(mask is not None)),
+                       dev)
     with torch.cuda.device(dev):
         st = lib.rt_hamming_scan_topk(
             nat.ptr(q), b, nat.ptr(item_bits), n, w, k, nat.ptr(mask),

@@ -94,6 +94,45 @@ def test_unseeded_large_k(dev):
     _check(dev, q, items, 1000)
 
 
+@pytest.mark.parametrize("b,n,k,masked", [(8, 5000, 100, False), (33, 20000, 1000, True),
+                                          (128, 9000, 100, False), (129, 20000, 100, True),
+                                          (300, 7000, 1000, False), (64, 3000, 1, True)])
+def test_matrix_core_path(dev, b, n, k, masked):
+    """512-bit codes from 8 queries on run on the int8 matrix cores (bits expanded to bytes,
+    the accumulator started at 64 W - 2 popcount(q)): wide and narrow layouts, k up to 1000,
+    masks."""
+    g = rng(b * 3 + n + k)
+    q = _codes(g, b, 8)
+    items = _codes(g, n, 8)
+    items[7] = q[0]  # an exact match: the maximum score 512
+    items[9] = ~q[1]  # the minimum -512
+    mask = None
+    if masked:
+        mask = g.random((b, n)) < 0.2
+        mask[0, 7] = True
+    _check(dev, q, items, k, mask)
+
+
+def test_matrix_core_ties(dev):
+    """Few distinct 512-bit rows: every score ties in large groups, broken by the lower id."""
+    g = rng(36)
+    base = _codes(g, 5, 8)
+    items = base[g.integers(0, 5, 30000)]
+    q = np.concatenate([base[:3], _codes(g, 40, 8)])
+    _check(dev, q, items, 1000)
+    _check(dev, q[:9], items, 37)
+
+
+def test_matrix_core_sample_pass(dev):
+    """B >= 512 over N >= 2.1M rows: the seed, the threshold sample pass and the main pass."""
+    g = rng(37)
+    q = _codes(g, 520, 8)
+    base = _codes(g, 4096, 8)
+    items = base[g.integers(0, 4096, 2_200_000)]  # repeated rows keep the oracle's work small
+    mask = g.random((520, 2_200_000)) < 0.5
+    _check(dev, q, items, 100, mask)
+
+
 def test_oporp_full_schema(dev):
     g = rng(34)
     q = torch.from_numpy(_codes(g, 4, 8)).to(dev)
