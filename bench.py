@@ -39,7 +39,6 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
-VALU_PEAK = 256 * 64 * 2.4e9  # 32-bit lane-ops/s: 256 CUs x 64 lanes x 2.4 GHz
 # HBM bytes per launch of the main scan (FETCH_SIZE + WRITE_SIZE, copy-calibrated), measured with
 # rocprofv3 --pmc for these exact workloads; keyed by (workload, N, D, B, k). See profiles/.
 MEASURED_TRAFFIC: dict = {
@@ -336,10 +335,13 @@ def main() -> int:
             return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
 
         scan_bytes = n * d // 8 + b * d // 8
-        scan_ops = 2 * b * n * (d // 32)  # XOR + popcount per 32-bit word pair
+        # 512-bit codes from 8 queries on are scored on the int8 matrix cores, one multiply-add
+        # per bit (bits as {0, 1} and {-2, +2} bytes): 2 ops per bit, item and query
+        mfma_scan = d == 512 and b >= 8
+        scan_ops = 2 * b * n * d if mfma_scan else 2 * b * n * (d // 32)
         step_bytes = scan_bytes + flt.bytes(n, b) + b * k1 * d
-        bound = "hbm"
-        dtype = "u64 (1-bit codes) / int8 rerank"
+        bound = "mfma" if mfma_scan else "hbm"
+        dtype = "int8" if mfma_scan else "u64"
         data = ("synthetic: N(0,1) rows (seed 556) and queries (seed 557), SimHash over a "
                 "N(0,1) 512x512 projection (seed 555), int8 codes of the same rows; attributes "
                 "Zipf(1.1) (seed 4321), query sets numpy seed 77")
@@ -403,9 +405,9 @@ def main() -> int:
         unit = "TFLOP/s"
     log(f"ms/step {ms_step:.3f}; main scan {kernel_ms:.3f} ms ({achieved:.0f} {unit})")
     if wl == "binary":
-        # the Hamming scan's VALU use: 2 ops (XOR, popcount) per 32-bit word pair and query
-        extra["hamming_valu_lane_ops_per_s"] = scan_ops / (kernel_ms * 1e-3)
-        extra["hamming_valu_frac"] = extra["hamming_valu_lane_ops_per_s"] / VALU_PEAK
+        extra["hamming_path"] = ("int8 matrix cores (bits as bytes)" if bound == "mfma"
+                                 else "XOR + popcount")
+        extra["hamming_hbm_gbs"] = scan_bytes / (kernel_ms * 1e-3) / 1e9
 
     cpu = None
     if not args.no_cpu:
