@@ -14,6 +14,8 @@ Other workloads (the remaining configurations, same JSON line):
   int8     the plain int8 scan top-k (configuration 4; ``--batch`` 1 / 16 / 256 / 1024)
   dense    bf16 top-100 over 10M x 128 clustered, L2-normalised items (configuration 2), with
            recall@100 against exact float32 scoring of the unrounded items
+  filtered-dense  the same items under the Bloom pre-filter + exact clause post-check at 10 %,
+           B = 256 (configuration 3)
   binary   1-bit retrieval: SimHash codes (sign of a Gaussian projection, 512 bits) scanned by
            Hamming score for the top-1000 under the Bloom + exact filter at 10 %, re-ranked by
            the int8 codes of the same vectors to the top-100 (configuration 5, B = 256)
@@ -195,10 +197,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("filtered", "int8", "dense", "binary"),
+    ap.add_argument("--workload", choices=("filtered", "int8", "dense", "filtered-dense", "binary"),
                     default="filtered")
     ap.add_argument("--batch", type=int, default=None,
-                    help="query batch (default: 16 filtered / int8, 64 dense, 256 binary)")
+                    help="query batch (default: 16 filtered / int8, 64 dense, 256 "
+                         "filtered-dense / binary)")
     ap.add_argument("--n", type=int, default=None,
                     help="items (default: 30M, dense 10M)")
     ap.add_argument("--d", type=int, default=None, help="dimensions (default 512, dense 128)")
@@ -226,9 +229,11 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     wl = args.workload
-    b = args.batch or {"filtered": 16, "int8": 16, "dense": 64, "binary": 256}[wl]
-    n = args.n or (10_000_000 if wl == "dense" else 30_000_000)
-    d = args.d or (128 if wl == "dense" else 512)
+    b = args.batch or {"filtered": 16, "int8": 16, "dense": 64, "filtered-dense": 256,
+                       "binary": 256}[wl]
+    dense_wl = wl in ("dense", "filtered-dense")
+    n = args.n or (10_000_000 if dense_wl else 30_000_000)
+    d = args.d or (128 if dense_wl else 512)
     k = args.k
     extra: dict = {}
     cpu_fn = None
@@ -271,6 +276,42 @@ def main() -> int:
             if flt:
                 what = "the exact value-set filter (torch.isin) gating " + what
             return t_s * (n / ns), threads, f"B={b} queries x first {ns} of {n} items ({what})"
+
+    elif wl == "filtered-dense":
+        log(f"generating {n}x{d} clustered items (1024 centres) and {b} queries")
+        gen = torch.Generator(device=dev).manual_seed(2024)
+        centres = torch.randn((1024, d), generator=gen, device=dev)
+        items = dense_table(n, d, centres, 2025, dev).bfloat16()
+        queries = dense_table(b, d, centres, 2026, dev).bfloat16()
+        flt = Filter(n, b, args.selectivity, dev)
+
+        def step():
+            return torch.ops.retrieve.dense_scan_topk(queries, items, k, flt.mask())
+
+        scan_bytes = n * d * 2 + b * d * 2
+        scan_ops = 2 * b * n * d
+        step_bytes = scan_bytes + flt.bytes(n, b)
+        bound = "hbm" if b < 312 else "mfma"  # bf16 ridge: 312.5 FLOP/B
+        dtype = "bf16"
+        data = ("synthetic: 1024 N(0,1) centres (seed 2024), items centre + 0.3 N(0,1) "
+                "L2-normalised (seed 2025), queries likewise (seed 2026), stored bf16; attributes "
+                "Zipf(1.1) (seed 4321), query sets numpy seed 77")
+        workload = (f"filtered dense bf16 top-{k}: N={n} D={d} B={b}; Bloom {BLOOM_BITS} "
+                    f"bits/item, {BLOOM_K} hashes pre-filter + exact AND-of-OR clause post-check "
+                    f"over 8 attributes at {args.selectivity:.0%} target selectivity")
+        extra["measured_selectivity"] = float(flt.selectivity.mean())
+        metric = "queries/sec + achieved HBM GB/s, filtered bf16 top-100 over 10Mx128 items"
+
+        def cpu_fn():
+            from oracle import baseline
+
+            ns = min(args.cpu_sample or 1_000_000, n)
+            t_s, threads = baseline.time_topk(queries.cpu().float(), items[:ns].cpu().float(), k,
+                                              valid_fn=flt.valid_fn(ns))
+            return (t_s * (n / ns), threads,
+                    f"B={b} queries x first {ns} of {n} items (the exact value-set filter "
+                    "(torch.isin) gating float32 torch.mm over 2M-row chunks + topk + lowest-id "
+                    "merge)")
 
     elif wl == "dense":
         log(f"generating {n}x{d} clustered items (1024 centres) and {b} queries")

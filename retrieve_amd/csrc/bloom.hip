@@ -260,7 +260,7 @@ __device__ inline void write_column(const BloomSearchArgs& a, int64_t b, int64_t
 constexpr int kFoldDepth = 4;
 constexpr int kProgMaxPos = 4;
 constexpr int kColMaxWidth = 64;
-constexpr int kProgMaxOps = 512;
+constexpr int kProgMaxOps = 2048;
 constexpr int kPrepThreads = 256;
 constexpr uint32_t kColPosBytes = kBloomWordsPerBundle * sizeof(uint64_t);  // 256
 
@@ -284,6 +284,9 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
                                                                   uint32_t* prog) {
   __shared__ uint8_t ops[kProgMaxOps];
   __shared__ uint8_t place[kProgMaxOps];
+  __shared__ uint8_t flat[kProgMaxOps];        // an AND / OR under a parent of the same operator
+  __shared__ int16_t parent[kProgMaxOps];      // -1 for the root
+  __shared__ int16_t first_child[kProgMaxOps];
   __shared__ uint32_t term_pos[kProgMaxOps][2];  // the positions part of each term's words
   __shared__ int32_t stk[kBloomMaxStack];
   const int64_t b = blockIdx.x;
@@ -306,6 +309,9 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
   for (int64_t i = tid; i < n_ops; i += kPrepThreads) {
     ops[i] = src[i];
     place[i] = kPlacePush;
+    flat[i] = 0;
+    parent[i] = -1;
+    first_child[i] = -1;
   }
   const uint64_t* hashes = reinterpret_cast<const uint64_t*>(a.data) + o[6] / 8;
   // a valid plan uses at most n_ops terms (each is an op)
@@ -346,13 +352,16 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
         bad = true;
         break;
       }
-      for (int q = sp - n + 1; q < sp; ++q) place[stk[q]] = op == kOpAnd ? kPlaceAnd : kPlaceOr;
+      for (int q = sp - n; q < sp; ++q) parent[stk[q]] = static_cast<int16_t>(i);
+      first_child[i] = static_cast<int16_t>(stk[sp - n]);
       sp -= n;
     } else if (op == kOpNot) {
       if (sp < 1) {
         bad = true;
         break;
       }
+      parent[stk[sp - 1]] = static_cast<int16_t>(i);
+      first_child[i] = static_cast<int16_t>(stk[sp - 1]);
       sp -= 1;
     } else if (op != kOpEmpty) {
       bad = true;
@@ -368,6 +377,24 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
     write_header(hdr, b, kPlanNone, 0, 0);
     return;
   }
+  // Places, top-down (post-order: a parent follows its children). An AND / OR under a parent of
+  // the same operator is flattened into it (associativity): its first child takes its place and
+  // it becomes a no-op, so nested fan-out-limited ORs of a long value set fold at one level. A
+  // first child pushes; the others fold with their parent's operator.
+  for (int64_t i = n_ops - 1; i >= 0; --i) {
+    const int p = parent[i];
+    const uint8_t op = ops[i];
+    if (p >= 0 && (op == kOpAnd || op == kOpOr) && ops[p] == op) flat[i] = 1;
+    if (p < 0) {
+      place[i] = kPlacePush;
+    } else if (ops[p] == kOpNot) {
+      place[i] = kPlacePush;
+    } else if (first_child[p] == i) {
+      place[i] = flat[p] ? place[p] : kPlacePush;
+    } else {
+      place[i] = ops[p] == kOpAnd ? kPlaceAnd : kPlaceOr;
+    }
+  }
   // the folded evaluation's depth, and the program
   int depth = 0;
   int deepest = 0;
@@ -377,21 +404,26 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
     const uint8_t op = ops[i];
     uint32_t w0 = 0u;
     uint32_t w1 = 0u;
-    if (op == kOpTerm) {
+    uint32_t where = place[i];
+    if (flat[i]) {
+      // a no-op: all ones AND-ed into the top (its children folded into the parent's level)
+      w0 = kKindEmpty;
+      where = kPlaceAnd;
+    } else if (op == kOpTerm) {
       w0 = kKindTerm | term_pos[term][0];
       w1 = term_pos[term][1];
-      ++term;
     } else if (op == kOpEmpty) {
       w0 = kKindEmpty;
     } else {
       w0 = op == kOpNot ? kKindNot : kKindPass;
       --depth;
     }
-    if (place[i] == kPlacePush) {
+    if (op == kOpTerm) ++term;
+    if (where == kPlacePush) {
       ++depth;
       deepest = depth > deepest ? depth : deepest;
     }
-    out[2 * i] = w0 | (static_cast<uint32_t>(place[i]) << 2);
+    out[2 * i] = w0 | (where << 2);
     out[2 * i + 1] = w1;
   }
   write_header(hdr, b, deepest <= kFoldDepth ? kPlanProgram : kPlanStack,

@@ -193,6 +193,29 @@ def test_search_paths(dev, bits, k, hash_k, n):
         assert np.array_equal(row, want), e
 
 
+def test_long_plans(dev):
+    """Value sets of hundreds of terms (plans of 500 - 2000 ops, the program's capacity) and one
+    past it (the stack evaluation), against the oracle."""
+    g = rng(91)
+    n = 3000
+    attrs = _attrs(g, n, 3, 1, 400, 0.1)
+    words, offs = _build(dev, attrs, 3, bits=64)
+    ow, oo = of.bloom_build(attrs, 3, bits_per_doc=64)
+
+    def ors(c, vals):
+        return "(" + " OR ".join(f"{c}:{v}" for v in vals) + ")"
+
+    exprs = [ors(0, range(300)),
+             ors(0, range(0, 400, 2)) + " AND " + ors(1, range(250)),
+             ors(0, range(200)) + " AND " + ors(1, range(200)) + " AND " + ors(2, range(300)),
+             "NOT " + ors(2, range(350)),
+             ors(0, range(400)) + " AND " + ors(1, range(400)) + " AND " + ors(2, range(400))]
+    got = _unpack(_search(dev, words, offs, exprs, 3, 7), n)
+    for e, row in zip(exprs, got):
+        want = of.bloom_expression_mask(ow, oo, n, e, 3, 7)
+        assert np.array_equal(row, want), e[:60]
+
+
 def test_stack_limit_matches_nothing(dev):
     """A plan that needs more stack than max_stack_size matches nothing; the others evaluate."""
     g = rng(90)
