@@ -394,6 +394,7 @@ __global__ void __launch_bounds__(kClauseThreads) clause_qmask_kernel(ClauseArgs
 // Lane l of a wave takes item (wave base + 63 - l), so a ballot is a mask word as it is stored
 // (item d at bit 63 - d % 64); lane r keeps row r's word and the rows store together.
 constexpr int kTabStride = kSetDomain + 1;
+constexpr int kRowUnroll = 4;  // 64-item words per wave per step of the row kernel
 
 template <class T, int C>
 struct RowShape {
@@ -461,25 +462,47 @@ __device__ inline uint32_t row_slot(const uint32_t (&w)[RowShape<T, C>::kWords],
   }
 }
 
-template <class T, int C>
+// In-wave transpose of a 64 x 64 bit matrix: lane i holds row i (bit j = column j); after six
+// exchange stages lane j holds column j (bit i = row i's bit j). Stage s swaps the off-diagonal
+// s x s blocks between lanes i and i ^ s.
+__device__ inline uint64_t wave_transpose64(uint64_t x, int lane) {
+  constexpr uint64_t kKeep[6] = {0x5555555555555555ull, 0x3333333333333333ull,
+                                 0x0f0f0f0f0f0f0f0full, 0x00ff00ff00ff00ffull,
+                                 0x0000ffff0000ffffull, 0x00000000ffffffffull};
+#pragma unroll
+  for (int t = 5; t >= 0; --t) {
+    const int s = 1 << t;
+    const uint64_t m = kKeep[t];  // the bits j with (j & s) == 0
+    const uint64_t y = __shfl_xor(x, s);
+    x = (lane & s) ? (((y >> s) & m) | (x & ~m)) : ((x & m) | ((y & m) << s));
+  }
+  return x;
+}
+
+// ROWS query rows per workgroup (32, or 64 for the bit masks of larger batches), M their mask
+// word type.
+template <class T, int C, int ROWS>
 __global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a) {
   using S = RowShape<T, C>;
-  extern __shared__ uint32_t tab[];  // [C][kTabStride]
-  __shared__ uint32_t row_active[kQmaskRows];
-  __shared__ uint32_t clause_fold[2][C];  // XOR, then OR, per clause
-  __shared__ uint32_t slow_rows;
+  using M = typename std::conditional<ROWS == 64, uint64_t, uint32_t>::type;
+  extern __shared__ __attribute__((aligned(8))) uint32_t tab_raw[];
+  M* tab = reinterpret_cast<M*>(tab_raw);  // [C][kTabStride]
+  __shared__ uint32_t row_active[ROWS];
+  __shared__ M clause_fold[2][C];  // XOR, then OR, per clause
+  __shared__ M slow_rows;
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid / kWave;
   const uint32_t rev_mask = a.rev_mask[0];
-  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * kQmaskRows;
-  const int nrows = static_cast<int>(b0 + kQmaskRows < a.B ? kQmaskRows : a.B - b0);
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * ROWS;
+  const int nrows = static_cast<int>(b0 + ROWS < a.B ? ROWS : a.B - b0);
+  constexpr M kOne = 1;
 
-  for (int i = tid; i < C * kTabStride; i += kClauseThreads) tab[i] = 0u;
-  if (tid == 0) slow_rows = 0u;
-  if (tid < kQmaskRows) row_active[tid] = tid < nrows ? a.active[b0 + tid] : 0u;
+  for (int i = tid; i < C * kTabStride; i += kClauseThreads) tab[i] = 0;
+  if (tid == 0) slow_rows = 0;
+  if (tid < ROWS) row_active[tid] = tid < nrows ? a.active[b0 + tid] : 0u;
   __syncthreads();
-  if (tid < nrows && a.small[b0 + tid] == 0u) atomicOr(&slow_rows, 1u << tid);
+  if (tid < nrows && a.small[b0 + tid] == 0u) atomicOr(&slow_rows, kOne << tid);
   // every (row, clause) value of the bitmap rows sets its row's bit
   for (int rc = tid; rc < nrows * C; rc += kClauseThreads) {
     const int r = rc / C;
@@ -488,14 +511,14 @@ __global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a
     if (a.small[b] == 0u) continue;
     const int64_t* vals = a.qc + (b * C + c) * a.V;
     const int n = a.nv[b * C + c];
-    for (int v = 0; v < n; ++v) atomicOr(&tab[c * kTabStride + vals[v]], 1u << r);
+    for (int v = 0; v < n; ++v) atomicOr(&tab[c * kTabStride + vals[v]], kOne << r);
   }
   __syncthreads();
-  const uint32_t slow = slow_rows;
+  const M slow = slow_rows;
   if (tid < C) {
-    uint32_t unconstrained = slow;
-    for (int r = 0; r < nrows; ++r) unconstrained |= (row_active[r] >> tid) & 1u ? 0u : 1u << r;
-    clause_fold[0][tid] = (rev_mask >> tid) & 1u ? ~0u : 0u;
+    M unconstrained = slow;
+    for (int r = 0; r < nrows; ++r) unconstrained |= (row_active[r] >> tid) & 1u ? 0 : kOne << r;
+    clause_fold[0][tid] = (rev_mask >> tid) & 1u ? ~M{0} : M{0};
     clause_fold[1][tid] = unconstrained;
   }
   __syncthreads();
@@ -504,54 +527,77 @@ __global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a
     tab[i] = (tab[i] ^ clause_fold[0][c]) | clause_fold[1][c];
   }
   __syncthreads();
-  const uint32_t fast = ~slow;
+  const M fast = ~slow;
 
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kClauseThreads; base < a.N;
-       base += static_cast<int64_t>(gridDim.x) * kClauseThreads) {
-    const int64_t wbase = base + wave * kWave;
-    const int64_t d = wbase + (kWave - 1 - lane);
-    const bool valid = d < a.N;
-    const int64_t wword = wbase >> 6;
-    uint64_t am = ~0ull;
-    if (a.mode == kClauseBits && a.and_mask != nullptr && lane < nrows && wword < a.W) {
-      am = a.and_mask[(b0 + lane) * a.and_words + wword];
+  // Each workgroup takes one contiguous run of 64-item words, each wave kRowUnroll consecutive
+  // words per step with every load of the step issued first: enough bytes in flight per CU to
+  // cover HBM latency, and a workgroup's mask stores fill whole lines of each row.
+  const int64_t words = (a.N + kWave - 1) / kWave;
+  constexpr int kStepWords = kRowUnroll * (kClauseThreads / kWave);
+  const int64_t steps = (words + kStepWords - 1) / kStepWords;
+  const int64_t per_wg = (steps + gridDim.x - 1) / gridDim.x * kStepWords;
+  const int64_t w_lo = static_cast<int64_t>(blockIdx.x) * per_wg;
+  const int64_t w_hi = w_lo + per_wg < words ? w_lo + per_wg : words;
+  const bool bits = a.mode == kClauseBits;
+  for (int64_t w0 = w_lo + wave * kRowUnroll; w0 < w_hi; w0 += kStepWords) {
+    uint32_t w[kRowUnroll][S::kWords];
+    uint64_t am[kRowUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t d = (w0 + u) * kWave + (kWave - 1 - lane);
+      const bool valid = w0 + u < w_hi && d < a.N;
+      load_row<T, C>(static_cast<const char*>(a.attrs) + (valid ? d : 0) * S::kBytes, w[u]);
+      am[u] = ~0ull;
+      if (bits && a.and_mask != nullptr && lane < nrows && w0 + u < w_hi) {
+        am[u] = a.and_mask[(b0 + lane) * a.and_words + w0 + u];
+      }
     }
-    uint32_t w[S::kWords];
-    load_row<T, C>(static_cast<const char*>(a.attrs) + (valid ? d : 0) * S::kBytes, w);
-    uint32_t slot[C];
-    int64_t at[kRegAttrs];
 #pragma unroll
-    for (int c = 0; c < kRegAttrs; ++c) at[c] = -1;
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int64_t wword = w0 + u;
+      const int64_t d = wword * kWave + (kWave - 1 - lane);
+      const bool valid = wword < w_hi && d < a.N;
+      uint32_t slot[C];
+      int64_t at[kRegAttrs];
 #pragma unroll
-    for (int c = 0; c < C; ++c) slot[c] = row_slot<T, C>(w, c, at[c]);
-    uint32_t m = fast;
+      for (int c = 0; c < kRegAttrs; ++c) at[c] = -1;
 #pragma unroll
-    for (int c = 0; c < C; ++c) m &= tab[c * kTabStride + slot[c]];
-    for (uint32_t rest = slow; rest != 0u; rest &= rest - 1u) {
-      const int r = __builtin_ctz(rest);
-      const bool pass = clause_pass<true, T>(a, at, nullptr, b0 + r, rev_mask, nullptr,
-                                             row_active[r]);
-      m |= pass ? 1u << r : 0u;
-    }
-    if (!valid) m = 0u;
+      for (int c = 0; c < C; ++c) slot[c] = row_slot<T, C>(w[u], c, at[c]);
+      M m = fast;
+#pragma unroll
+      for (int c = 0; c < C; ++c) m &= tab[c * kTabStride + slot[c]];
+      for (M rest = slow; rest != 0; rest &= rest - 1) {
+        const int r = ROWS == 64 ? __builtin_ctzll(rest) : __builtin_ctz(rest);
+        const bool pass = clause_pass<true, T>(a, at, nullptr, b0 + r, rev_mask, nullptr,
+                                               row_active[r]);
+        m |= pass ? kOne << r : M{0};
+      }
+      if (!valid) m = 0;
 
-    if (a.mode == kClauseBits) {
-      uint64_t mine = 0ull;
-      for (int r = 0; r < nrows; ++r) {
-        const uint64_t word = __ballot((m >> r) & 1u);
-        mine = lane == r ? word : mine;
-      }
-      if (lane < nrows && wword < a.W) {
-        static_cast<uint64_t*>(a.out)[(b0 + lane) * a.W + wword] = mine & am;
-      }
-    } else if (valid) {
-      for (int r = 0; r < nrows; ++r) {
-        const int64_t b = b0 + r;
-        const bool pass = (m >> r) & 1u;
-        if (a.mode == kClauseBool) {
-          static_cast<uint8_t*>(a.out)[b * a.N + d] = pass ? 1 : 0;
+      if (bits) {
+        uint64_t mine = 0ull;
+        if (nrows > 8) {
+          // lane l holds item (word base + 63 - l)'s row bits: the transpose gives lane r row
+          // r's word with item d at bit 63 - d % 64, as stored
+          mine = wave_transpose64(static_cast<uint64_t>(m), lane);
         } else {
-          static_cast<float*>(a.out)[b * a.N + d] = pass ? a.scores[b * a.N + d] : -INFINITY;
+          for (int r = 0; r < nrows; ++r) {
+            const uint64_t word = __ballot((m >> r) & 1u);
+            mine = lane == r ? word : mine;
+          }
+        }
+        if (lane < nrows && wword < w_hi) {
+          static_cast<uint64_t*>(a.out)[(b0 + lane) * a.W + wword] = mine & am[u];
+        }
+      } else if (valid) {
+        for (int r = 0; r < nrows; ++r) {
+          const int64_t b = b0 + r;
+          const bool pass = (m >> r) & 1u;
+          if (a.mode == kClauseBool) {
+            static_cast<uint8_t*>(a.out)[b * a.N + d] = pass ? 1 : 0;
+          } else {
+            static_cast<float*>(a.out)[b * a.N + d] = pass ? a.scores[b * a.N + d] : -INFINITY;
+          }
         }
       }
     }
@@ -561,8 +607,18 @@ __global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a
 template <class T, int C>
 static bool launch_row_kernel(const ClauseArgs& a, dim3 grid, hipStream_t stream) {
   if (reinterpret_cast<uintptr_t>(a.attrs) % RowShape<T, C>::kLoad != 0) return false;
-  const size_t lds = static_cast<size_t>(C) * kTabStride * sizeof(uint32_t);
-  clause_row_kernel<T, C><<<grid, kClauseThreads, lds, stream>>>(a);
+  if (a.rows_per_wg == 64) {
+    const size_t lds = static_cast<size_t>(C) * kTabStride * sizeof(uint64_t);
+    if (lds > 65536) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&clause_row_kernel<T, C, 64>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds));
+    }
+    clause_row_kernel<T, C, 64><<<grid, kClauseThreads, lds, stream>>>(a);
+  } else {
+    const size_t lds = static_cast<size_t>(C) * kTabStride * sizeof(uint32_t);
+    clause_row_kernel<T, C, 32><<<grid, kClauseThreads, lds, stream>>>(a);
+  }
   return true;
 }
 
@@ -590,6 +646,13 @@ static bool launch_row_typed(const ClauseArgs& a, dim3 grid, hipStream_t stream)
     case 16: return launch_row_kernel<T, 16>(a, grid, stream);
     default: return false;
   }
+}
+
+// Whether the row kernel's widest loads fit the attribute table's alignment (RowShape's kLoad).
+static bool row_loads_aligned(const void* attrs, int attr_bytes, int64_t C) {
+  const int64_t bytes = C * attr_bytes;
+  const int64_t load = bytes % 16 == 0 ? 16 : bytes % 8 == 0 ? 8 : bytes % 4 == 0 ? 4 : 2;
+  return reinterpret_cast<uintptr_t>(attrs) % static_cast<uintptr_t>(load) == 0;
 }
 
 template <int MODE, class T>
@@ -884,8 +947,14 @@ extern "C" int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t 
   // a wave's lanes carry the rows' words (bits mode) and the staged row flags
   a.rows_per_wg = a.rows_per_wg < kWave ? a.rows_per_wg : kWave;
   if (C >= 1 && C <= kQmaskClauses) {
-    // the query-mask form: 32 rows per workgroup, the table built once per workgroup
+    // the query-mask form: 32 rows per workgroup, the table built once per workgroup; 64 rows
+    // (the row kernel's 64-bit tables, masks written through an in-wave transpose) for the bit
+    // masks of larger batches when its loads are aligned
     a.rows_per_wg = kQmaskRows;
+    if (mode == kClauseBits && B > kQmaskRows && A == 1 &&
+        row_loads_aligned(item_attrs, attr_bytes, C)) {
+      a.rows_per_wg = 64;
+    }
     gx = cdiv(N, kClauseThreads);
     gx = gx < 2048 ? gx : 2048;
   }

@@ -245,3 +245,22 @@ def test_row_groups_mixed_rows(dev, c, a):
     assert np.array_equal(bits.cpu().numpy(), _pack(want & pre))
     m = torch.ops.retrieve.clause_mask(_t(dev, attrs), _t(dev, rev), _t(dev, sets[:, :, 0]))
     assert np.array_equal(m.cpu().numpy(), of.clause_match(attrs, rev, sets[:, :, 0]))
+
+
+@pytest.mark.parametrize("dtype", [np.int16, np.int64])
+def test_wide_row_groups(dev, dtype):
+    """Bit masks of more than 32 query rows go 64 rows to a workgroup: several groups (the last
+    partial), list rows on either side of bit 32 of a group and in the last group, an AND mask."""
+    g = rng(61)
+    n, c, b = 20_011, 5, 150
+    attrs = g.integers(-2, 50, (n, c, 1), dtype=np.int64)
+    sets = g.integers(0, 50, (b, c, 3), dtype=np.int64)
+    sets[g.random(sets.shape) < 0.55] = -1
+    sets[[31, 32, 63, 64, 140], 1, 0] = [2000, -1, 4000, -9, 1500]  # -1 just pads
+    sets[[5, 100]] = -1
+    rev = np.array([0, 0, 1, 0, 1], bool)
+    want = of.clause_match_sets(attrs, sets, rev)
+    pre = g.random((b, n)) < 0.8
+    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs.astype(dtype)), _t(dev, rev),
+                                          _t(dev, sets), _t(dev, _pack(pre)))
+    assert np.array_equal(bits.cpu().numpy(), _pack(want & pre))
