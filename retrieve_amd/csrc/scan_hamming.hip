@@ -3,8 +3,8 @@
 // oporp_1bit_match_topk.py:9-17), ties to the lower item index.
 //
 // Each lane scores its own item (its 2W dwords in VGPRs) against one wave-uniform query at a
-// time: v_xor_b32 with the query dword (an SGPR) and v_bcnt_u32_b32 accumulating the
-// popcount, 2 VALU per dword. A query's fast-path test is ham <= its threshold; the rare
+// time: v_xor_b32 with the query dword (an SGPR, read by scalar loads through the constant
+// address space) and v_bcnt_u32_b32 accumulating the popcount, 2 VALU per dword. A query's fast-path test is ham <= its threshold; the rare
 // candidates go to the per-(wave, query) lists of uniform_topk.h and the shared merge.
 #include "profile.h"
 #include "scan_common.h"
@@ -40,8 +40,13 @@ __device__ inline void load_codes(const uint32_t* __restrict__ I, int64_t item, 
   }
 }
 
-template <int W>
-__device__ inline int hamming(const uint32_t* iw, const uint32_t* qw) {
+// Query codes through the constant address space: with a wave-uniform address the loads are
+// scalar (s_load into SGPRs), so the XORs take the query dword as their scalar operand and no
+// LDS bandwidth goes to broadcasting it. The queries are never written by the scan.
+typedef __attribute__((address_space(4))) const uint32_t ku32;
+
+template <int W, class Q>
+__device__ inline int hamming(const uint32_t* iw, Q qw) {
   int h = 0;
 #pragma unroll
   for (int d = 0; d < 2 * W; ++d) h = __builtin_popcount(iw[d] ^ qw[d]) + h;
@@ -73,7 +78,7 @@ __global__ void __launch_bounds__(kScanThreads) seed_hamming_kernel(ScanArgs a) 
   __shared__ uint64_t best[kScanWaves][kHamMaxQpw];
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
-  const uint32_t* Q = static_cast<const uint32_t*>(a.queries);
+  ku32* Q = (ku32*)(a.queries);
   const uint32_t* I = static_cast<const uint32_t*>(a.items);
   const int64_t wi = static_cast<int64_t>(blockIdx.x) * kScanWaves + wave;
   const int64_t S = static_cast<int64_t>(gridDim.x) * kScanWaves;
@@ -104,19 +109,18 @@ __global__ void __launch_bounds__(kScanThreads) seed_hamming_kernel(ScanArgs a) 
   for (int qi = lane; qi < nq; qi += kWave) a.lists[(q0 + qi) * S + wi] = best[wave][qi];
 }
 
-// Main pass over every item: tiles of 64 rows dealt round-robin to the group's waves. The
-// group's query codes are staged in LDS (read back as broadcasts); queries go two at a time.
+// Main pass over every item: tiles of 64 rows dealt round-robin to the group's waves; queries
+// go two at a time, their codes in SGPRs, each query's popcount limit in lane q of a VGPR (read
+// back with v_readlane).
 template <int W>
 __global__ void __launch_bounds__(kScanThreads) scan_hamming_kernel(ScanArgs a, int scratch_n) {
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   const int lane = lane_id();
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int qpw = a.qpw;
-  uint32_t* qcodes = reinterpret_cast<uint32_t*>(smem);  // [qpw][2W]
-  uint64_t* rest = smem + qpw * W;
+  uint64_t* rest = smem;
   uint64_t* scratch = rest + wave * scratch_n;
   uint64_t* tau = rest + kScanWaves * scratch_n + wave * qpw;
-  int* hlim = reinterpret_cast<int*>(rest + kScanWaves * (scratch_n + qpw)) + wave * qpw;
   int* cnt = reinterpret_cast<int*>(rest + kScanWaves * (scratch_n + qpw)) +
              kScanWaves * qpw + wave * qpw;
   const int64_t wave_in_group = static_cast<int64_t>(blockIdx.x) * kScanWaves + wave;
@@ -124,12 +128,12 @@ __global__ void __launch_bounds__(kScanThreads) scan_hamming_kernel(ScanArgs a, 
   const int64_t slot = static_cast<int64_t>(blockIdx.y) * waves + wave_in_group;
   const int64_t q0 = static_cast<int64_t>(blockIdx.y) * qpw;
   const int nq = static_cast<int>(a.B - q0 < qpw ? a.B - q0 : qpw);
-  const uint32_t* Q = static_cast<const uint32_t*>(a.queries);
-  for (int i = threadIdx.x; i < nq * 2 * W; i += kScanThreads) qcodes[i] = Q[q0 * 2 * W + i];
+  ku32* qcodes = (ku32*)(a.queries) + q0 * 2 * W;  // [nq][2W]
+  int hlim = -1;  // lane q: query q's popcount limit (qpw <= kWave)
   for (int i = lane; i < qpw; i += kWave) {
     const uint64_t t = i < nq ? (a.tau_in != nullptr ? a.tau_in[q0 + i] : 0ull) : ~0ull;
     tau[i] = t;
-    hlim[i] = i < nq ? hamming_limit<W>(t) : -1;
+    hlim = i < nq ? hamming_limit<W>(t) : -1;
     cnt[i] = 0;
   }
   WaveTopKUniform top;
@@ -151,10 +155,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_hamming_kernel(ScanArgs a, 
     const uint64_t after =
         top.push(qi, ok, key_of_i32(64 * W - 2 * h), item,
                  a.mask != nullptr ? a.mask + (q0 + qi) * a.mask_words : nullptr);
-    if (after != before) {
-      if (lane == 0) hlim[qi] = hamming_limit<W>(after);
-      wave_sync_memory();
-    }
+    if (after != before) hlim = lane == qi ? hamming_limit<W>(after) : hlim;
   };
   for (int64_t t = wave_in_group; t < ntiles; t += waves) {
     const int64_t row = t * kHamTile + lane;
@@ -166,8 +167,8 @@ __global__ void __launch_bounds__(kScanThreads) scan_hamming_kernel(ScanArgs a, 
     for (; qi + 1 < nq; qi += 2) {
       const int h0 = hamming<W>(iw, qcodes + qi * 2 * W);
       const int h1 = hamming<W>(iw, qcodes + (qi + 1) * 2 * W);
-      const bool ok0 = valid && h0 <= hlim[qi];
-      const bool ok1 = valid && h1 <= hlim[qi + 1];
+      const bool ok0 = valid && h0 <= __builtin_amdgcn_readlane(hlim, qi);
+      const bool ok1 = valid && h1 <= __builtin_amdgcn_readlane(hlim, qi + 1);
       if (__any(ok0 || ok1)) {
         handle(qi, ok0, h0, item);
         handle(qi + 1, ok1, h1, item);
@@ -175,7 +176,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_hamming_kernel(ScanArgs a, 
     }
     if (qi < nq) {
       const int h = hamming<W>(iw, qcodes + qi * 2 * W);
-      handle(qi, valid && h <= hlim[qi], h, item);
+      handle(qi, valid && h <= __builtin_amdgcn_readlane(hlim, qi), h, item);
     }
   }
   wave_sync_memory();
@@ -186,9 +187,8 @@ static int ham_capw(int64_t k) {
   return static_cast<int>(align_up(static_cast<size_t>(k) + kWave, 64));
 }
 
-static size_t ham_lds(int qpw, int scratch_n, int64_t W) {
-  return static_cast<size_t>(qpw) * W * sizeof(uint64_t) +
-         kScanWaves * (scratch_n * sizeof(uint64_t) + qpw * (sizeof(uint64_t) + 2 * sizeof(int)));
+static size_t ham_lds(int qpw, int scratch_n) {
+  return kScanWaves * (scratch_n * sizeof(uint64_t) + qpw * (sizeof(uint64_t) + 2 * sizeof(int)));
 }
 
 template <int W>
@@ -201,7 +201,7 @@ static int launch_ham(const ScanArgs& a, const PassPlan& p, int64_t nqg, bool se
     return kOk;
   }
   const int scratch_n = static_cast<int>(next_pow2(a.capw));
-  const size_t lds = ham_lds(a.qpw, scratch_n, W);
+  const size_t lds = ham_lds(a.qpw, scratch_n);
   if (lds > 65536) {
     RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(scan_hamming_kernel<W>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -235,8 +235,14 @@ static int dispatch_ham(int64_t W, const ScanArgs& a, const PassPlan& p, int64_t
 static int ham_qpw(int64_t B) { return static_cast<int>(B < kHamMaxQpw ? B : kHamMaxQpw); }
 
 // From this batch on, 512-bit codes are scored on the int8 matrix cores (the blocked scan with
-// bits expanded to bytes); below, one XOR + popcount pass per query and word.
-constexpr int64_t kHamMfmaMinBatch = 8;
+// bits expanded to bytes); below, one XOR + popcount pass per query and word. Measured over 30M
+// codes: the popcount pass costs ~0.33 ms + ~52 us per query (VALU-bound: 2 VALU per 32 bits),
+// the matrix path ~2.1-2.2 ms from 8 to 64 queries (the per-row bit expansion, shared by up to
+// 256 queries, dominates at small batches); they cross at about 36 queries.
+#ifndef RT_HAM_MFMA_MIN_BATCH
+#define RT_HAM_MFMA_MIN_BATCH 36
+#endif
+constexpr int64_t kHamMfmaMinBatch = RT_HAM_MFMA_MIN_BATCH;
 
 static bool ham_mfma(int64_t B, int64_t W, int64_t k, bool masked) {
   return W == 8 && B >= kHamMfmaMinBatch && blocked_hamming_fits(B, W, k, masked);
