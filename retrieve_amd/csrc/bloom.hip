@@ -279,6 +279,50 @@ __device__ inline void write_header(int32_t* hdr, int64_t b, int32_t status, int
 enum ProgKind : uint32_t { kKindTerm = 0, kKindEmpty = 1, kKindPass = 2, kKindNot = 3 };
 enum ProgPlace : uint32_t { kPlacePush = 0, kPlaceAnd = 1, kPlaceOr = 2 };
 
+// Block-wide exclusive prefix sum of one value per thread (every thread calls it); total gets
+// the sum over the block. tmp: kPrepThreads / kWave ints of LDS.
+__device__ inline int prep_scan_excl(int v, int* tmp, int& total) {
+  const int lane = lane_id();
+  const int w = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    x += lane >= off ? y : 0;
+  }
+  if (lane == kWave - 1) tmp[w] = x;
+  __syncthreads();
+  int base = 0;
+  total = 0;
+#pragma unroll
+  for (int i = 0; i < kPrepThreads / kWave; ++i) {
+    base += i < w ? tmp[i] : 0;
+    total += tmp[i];
+  }
+  __syncthreads();
+  return base + x - v;
+}
+
+// Block-wide maximum (every thread calls it).
+__device__ inline int prep_max(int v, int* tmp) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const int y = __shfl_xor(v, off);
+    v = y > v ? y : v;
+  }
+  if (lane_id() == 0) tmp[threadIdx.x / kWave] = v;
+  __syncthreads();
+  int m = tmp[0];
+#pragma unroll
+  for (int i = 1; i < kPrepThreads / kWave; ++i) m = tmp[i] > m ? tmp[i] : m;
+  __syncthreads();
+  return m;
+}
+
+// One workgroup per plan. The stack check (the stack evaluation's, recording each node's parent
+// and first child) is a single pass of one thread over LDS copies of the ops and child counts;
+// the flattening, the places, the term numbering and the folded depth are computed by the whole
+// workgroup (a walk up the parent links per op, block prefix sums).
 __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArgs a,
                                                                   int32_t* hdr,
                                                                   uint32_t* prog) {
@@ -287,8 +331,11 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
   __shared__ uint8_t flat[kProgMaxOps];        // an AND / OR under a parent of the same operator
   __shared__ int16_t parent[kProgMaxOps];      // -1 for the root
   __shared__ int16_t first_child[kProgMaxOps];
+  __shared__ int32_t nchild[kProgMaxOps];      // an AND / OR's child count (offs[i+1] - offs[i])
   __shared__ uint32_t term_pos[kProgMaxOps][2];  // the positions part of each term's words
   __shared__ int32_t stk[kBloomMaxStack];
+  __shared__ int32_t red[kPrepThreads / kWave];
+  __shared__ int32_t verdict;
   const int64_t b = blockIdx.x;
   const int64_t* o = a.plan_offsets + 8 * b;
   const int tid = threadIdx.x;
@@ -306,12 +353,13 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
     return;
   }
   const uint8_t* src = reinterpret_cast<const uint8_t*>(a.data + o[0]);
+  const int32_t* offs = reinterpret_cast<const int32_t*>(a.data + o[2]);
+  const int64_t n_offs = (o[3] - o[2]) / 4;
   for (int64_t i = tid; i < n_ops; i += kPrepThreads) {
     ops[i] = src[i];
-    place[i] = kPlacePush;
-    flat[i] = 0;
     parent[i] = -1;
     first_child[i] = -1;
+    nchild[i] = i + 1 < n_offs ? offs[i + 1] - offs[i] : -1;  // -1: no count (a bad AND / OR)
   }
   const uint64_t* hashes = reinterpret_cast<const uint64_t*>(a.data) + o[6] / 8;
   // a valid plan uses at most n_ops terms (each is an op)
@@ -326,96 +374,116 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
     term_pos[t][1] = off[2] | (off[3] << 16);
   }
   __syncthreads();
-  if (tid != 0) return;
 
-  // the stack evaluation's checks, recording each node's place
-  const int32_t* offs = reinterpret_cast<const int32_t*>(a.data + o[2]);
-  const int64_t n_offs = (o[3] - o[2]) / 4;
-  bool bad = false;
-  int sp = 0;
-  int64_t term = 0;
-  for (int64_t i = 0; i < n_ops && !bad; ++i) {
-    const uint8_t op = ops[i];
-    if (op == kOpTerm) {
-      if ((term + 1) * a.hash_k > nh) {
+  if (tid == 0) {
+    // the stack evaluation's checks, recording each node's parent and first child
+    bool bad = false;
+    int sp = 0;
+    int64_t term = 0;
+    for (int64_t i = 0; i < n_ops && !bad; ++i) {
+      const uint8_t op = ops[i];
+      if (op == kOpTerm) {
+        if ((term + 1) * a.hash_k > nh) {
+          bad = true;
+          break;
+        }
+        ++term;
+      } else if (op == kOpAnd || op == kOpOr) {
+        const int n = nchild[i];
+        if (n < 1 || n > sp) {
+          bad = true;
+          break;
+        }
+        for (int q = sp - n; q < sp; ++q) parent[stk[q]] = static_cast<int16_t>(i);
+        first_child[i] = static_cast<int16_t>(stk[sp - n]);
+        sp -= n;
+      } else if (op == kOpNot) {
+        if (sp < 1) {
+          bad = true;
+          break;
+        }
+        parent[stk[sp - 1]] = static_cast<int16_t>(i);
+        first_child[i] = static_cast<int16_t>(stk[sp - 1]);
+        sp -= 1;
+      } else if (op != kOpEmpty) {
         bad = true;
         break;
       }
-      ++term;
-    } else if (op == kOpAnd || op == kOpOr) {
-      if (i + 1 >= n_offs) {
+      if (sp >= a.max_stack) {
         bad = true;
         break;
       }
-      const int n = offs[i + 1] - offs[i];
-      if (n < 1 || n > sp) {
-        bad = true;
-        break;
-      }
-      for (int q = sp - n; q < sp; ++q) parent[stk[q]] = static_cast<int16_t>(i);
-      first_child[i] = static_cast<int16_t>(stk[sp - n]);
-      sp -= n;
-    } else if (op == kOpNot) {
-      if (sp < 1) {
-        bad = true;
-        break;
-      }
-      parent[stk[sp - 1]] = static_cast<int16_t>(i);
-      first_child[i] = static_cast<int16_t>(stk[sp - 1]);
-      sp -= 1;
-    } else if (op != kOpEmpty) {
-      bad = true;
-      break;
+      stk[sp++] = static_cast<int32_t>(i);
     }
-    if (sp >= a.max_stack) {
-      bad = true;
-      break;
-    }
-    stk[sp++] = static_cast<int32_t>(i);
+    verdict = bad || sp != 1 ? 1 : 0;
+    if (verdict) write_header(hdr, b, kPlanNone, 0, 0);
   }
-  if (bad || sp != 1) {
-    write_header(hdr, b, kPlanNone, 0, 0);
-    return;
-  }
-  // Places, top-down (post-order: a parent follows its children). An AND / OR under a parent of
-  // the same operator is flattened into it (associativity): its first child takes its place and
-  // it becomes a no-op, so nested fan-out-limited ORs of a long value set fold at one level. A
-  // first child pushes; the others fold with their parent's operator.
-  for (int64_t i = n_ops - 1; i >= 0; --i) {
+  __syncthreads();
+  if (verdict) return;
+
+  // An AND / OR under a parent of the same operator is flattened into it (associativity): its
+  // first child takes its place and it becomes a no-op, so nested fan-out-limited ORs of a long
+  // value set fold at one level.
+  for (int64_t i = tid; i < n_ops; i += kPrepThreads) {
     const int p = parent[i];
     const uint8_t op = ops[i];
-    if (p >= 0 && (op == kOpAnd || op == kOpOr) && ops[p] == op) flat[i] = 1;
-    if (p < 0) {
-      place[i] = kPlacePush;
-    } else if (ops[p] == kOpNot) {
-      place[i] = kPlacePush;
-    } else if (first_child[p] == i) {
-      place[i] = flat[p] ? place[p] : kPlacePush;
-    } else {
-      place[i] = ops[p] == kOpAnd ? kPlaceAnd : kPlaceOr;
-    }
+    flat[i] = p >= 0 && (op == kOpAnd || op == kOpOr) && ops[p] == op ? 1 : 0;
   }
-  // the folded evaluation's depth, and the program
-  int depth = 0;
-  int deepest = 0;
-  term = 0;
-  uint32_t* out = prog + b * kProgMaxOps * 2;
-  for (int64_t i = 0; i < n_ops; ++i) {
+  __syncthreads();
+  // Places: a first child pushes (or, under a flattened parent, takes the parent's place: walk
+  // up); the others fold with their parent's operator.
+  for (int64_t i = tid; i < n_ops; i += kPrepThreads) {
+    int j = static_cast<int>(i);
+    uint8_t where = kPlacePush;
+    for (;;) {
+      const int p = parent[j];
+      if (p < 0 || ops[p] == kOpNot) break;
+      if (first_child[p] != j) {
+        where = ops[p] == kOpAnd ? kPlaceAnd : kPlaceOr;
+        break;
+      }
+      if (!flat[p]) break;
+      j = p;
+    }
+    place[i] = where;
+  }
+  __syncthreads();
+
+  // the program: each thread a run of consecutive ops, its first term's number and its depth
+  // at entry from block prefix sums; the folded evaluation's depth is the deepest push
+  const int chunk = static_cast<int>((n_ops + kPrepThreads - 1) / kPrepThreads);
+  const int64_t c0 = static_cast<int64_t>(tid) * chunk;
+  const int64_t c1 = c0 + chunk < n_ops ? c0 + chunk : n_ops;
+  int my_terms = 0;
+  int my_delta = 0;
+  for (int64_t i = c0; i < c1; ++i) {
     const uint8_t op = ops[i];
-    uint32_t w0 = 0u;
-    uint32_t w1 = 0u;
+    my_terms += op == kOpTerm ? 1 : 0;
+    const bool pops = !flat[i] && op != kOpTerm && op != kOpEmpty;  // AND, OR, NOT
+    const bool push = !flat[i] && place[i] == kPlacePush;
+    my_delta += (push ? 1 : 0) - (pops ? 1 : 0);
+  }
+  int total = 0;
+  int term = prep_scan_excl(my_terms, red, total);
+  int depth = prep_scan_excl(my_delta, red, total);
+  int deepest = 0;
+  uint32_t* out = prog + b * kProgMaxOps * 2;
+  for (int64_t i = c0; i < c1; ++i) {
+    const uint8_t op = ops[i];
+    uint32_t w0w = 0u;
+    uint32_t w1w = 0u;
     uint32_t where = place[i];
     if (flat[i]) {
       // a no-op: all ones AND-ed into the top (its children folded into the parent's level)
-      w0 = kKindEmpty;
+      w0w = kKindEmpty;
       where = kPlaceAnd;
     } else if (op == kOpTerm) {
-      w0 = kKindTerm | term_pos[term][0];
-      w1 = term_pos[term][1];
+      w0w = kKindTerm | term_pos[term][0];
+      w1w = term_pos[term][1];
     } else if (op == kOpEmpty) {
-      w0 = kKindEmpty;
+      w0w = kKindEmpty;
     } else {
-      w0 = op == kOpNot ? kKindNot : kKindPass;
+      w0w = op == kOpNot ? kKindNot : kKindPass;
       --depth;
     }
     if (op == kOpTerm) ++term;
@@ -423,11 +491,14 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
       ++depth;
       deepest = depth > deepest ? depth : deepest;
     }
-    out[2 * i] = w0 | (where << 2);
-    out[2 * i + 1] = w1;
+    out[2 * i] = w0w | (where << 2);
+    out[2 * i + 1] = w1w;
   }
-  write_header(hdr, b, deepest <= kFoldDepth ? kPlanProgram : kPlanStack,
-               static_cast<int32_t>(n_ops), o[6] / 8);
+  deepest = prep_max(deepest, red);
+  if (tid == 0) {
+    write_header(hdr, b, deepest <= kFoldDepth ? kPlanProgram : kPlanStack,
+                 static_cast<int32_t>(n_ops), o[6] / 8);
+  }
 }
 
 // ---- column kernel: programs over LDS-staged bundles -------------------------------------
