@@ -185,22 +185,23 @@ __device__ inline int32_t group_max(const Acc& v, int g) {
   }
 }
 
-// group_max over the rows of the group that pass the mask: nib bit 3 - u is row u's mask bit;
-// rows that fail count as INT32_MIN (below every threshold).
+// group_max over the rows of the group that pass the mask: bit 31 - 8 g - u of w is row u's
+// mask bit; rows that fail count as INT32_MIN (below every threshold). Per row one signed
+// bit-field extract (0 or -1) and one bit-field insert, then two 3-way maxima.
 template <class Op, bool RAW, class Acc>
-__device__ inline int32_t group_max_masked(const Acc& v, int g, uint32_t nib) {
-  int32_t m = INT32_MIN;
+__device__ inline int32_t group_max_masked(const Acc& v, int g, uint32_t w) {
+  int32_t kv[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    int32_t kv;
     if constexpr (RAW) {
-      kv = raw_bits(v[4 * g + u]);
+      kv[u] = raw_bits(v[4 * g + u]);
     } else {
-      kv = Op::skey(static_cast<typename Op::Score>(v[4 * g + u]));
+      kv[u] = Op::skey(static_cast<typename Op::Score>(v[4 * g + u]));
     }
-    m = ((nib >> (3 - u)) & 1u) ? imax(m, kv) : m;
+    const int32_t m = __builtin_amdgcn_sbfe(static_cast<int32_t>(w), 31 - 8 * g - u, 1);
+    kv[u] = (kv[u] & m) | (INT32_MIN & ~m);
   }
-  return m;
+  return imax(imax(imax(kv[0], kv[1]), kv[2]), kv[3]);
 }
 
 // s_waitcnt immediate: vmcnt <= N (N < 64), expcnt and lgkmcnt unconstrained (gfx9 encoding).
@@ -568,8 +569,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
 #pragma unroll
               for (int g = 0; g < 4; ++g) {
                 if constexpr (masked) {
-                  const uint32_t nib = (mw[i][j] >> (28 - 8 * g - 4 * half)) & 0xfu;
-                  gm[i][j][g] = group_max_masked<Op, RAWV>(acc[i][j], g, nib);
+                  gm[i][j][g] = group_max_masked<Op, RAWV>(acc[i][j], g, mw[i][j] << (4 * half));
                 } else {
                   gm[i][j][g] = group_max<Op, RAWV>(acc[i][j], g);
                 }

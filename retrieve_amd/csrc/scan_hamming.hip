@@ -4,8 +4,9 @@
 //
 // Each lane scores its own item (its 2W dwords in VGPRs) against one wave-uniform query at a
 // time: v_xor_b32 with the query dword (an SGPR, read by scalar loads through the constant
-// address space) and v_bcnt_u32_b32 accumulating the popcount, 2 VALU per dword. A query's fast-path test is ham <= its threshold; the rare
-// candidates go to the per-(wave, query) lists of uniform_topk.h and the shared merge.
+// address space) and v_bcnt_u32_b32 accumulating the popcount, 2 VALU per dword. A query's
+// fast-path test is ham <= its threshold; the rare candidates go to the per-(wave, query) lists
+// of uniform_topk.h and the shared merge.
 #include "profile.h"
 #include "scan_common.h"
 #include "uniform_topk.h"
