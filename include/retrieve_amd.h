@@ -74,9 +74,11 @@ int rt_blocked_scan_topk(const void* queries, int64_t B, const void* items, int6
 /* Exact 1-bit Hamming top-k over a full code table: query_bits [B, W] x item_bits [N, W]
  * (uint64 words, bit b of word w = dimension 64 w + b), score = 64 W - 2 popcount(q ^ item),
  * top-k by (score desc, index asc) -> ids int64 [B, k], scores [B, k] (int32, or float when
- * score_f32 != 0). 1 <= W <= 16; 1 <= k <= 1024. `mask` as for rt_int8_scan_topk. 512-bit
- * codes (W = 8) from 36 queries on run on the int8 matrix cores (bits as bytes); `masked` of the
- * workspace function as for rt_blocked_scan_topk_workspace.
+ * score_f32 != 0). 1 <= W <= 16; 1 <= k <= 8192 (above 1024 the k-th score is found by
+ * counting the 64 W + 1 scores and the ties at it by id bins: LiNR V3's candidate pools).
+ * `mask` as for rt_int8_scan_topk. 512-bit codes (W = 8) from 36 queries on (k <= 1024) run on
+ * the int8 matrix cores (bits as bytes); `masked` of the workspace function as for
+ * rt_blocked_scan_topk_workspace.
  * Replaces: the Triton full-scan kernel + torch.topk of
  *   retrieve/src/retrieve/ops/triton/oporp_1bit_match_topk.py:47-122, 217-234, 261-273
  *   (torch.ops.retrieve.oporp_1bit_match_topk_full). */

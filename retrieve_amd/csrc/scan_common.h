@@ -18,6 +18,9 @@ constexpr int kScanThreads = kScanWaves * kWave;
 constexpr int kTile = 16;           // items per MFMA tile
 constexpr int kMergeThreads = 512;
 constexpr int64_t kMaxK = 1024;
+// The 1-bit full scan's bound: above kMaxK it selects by counting scores (a score takes only
+// 64 W + 1 values).
+constexpr int64_t kMaxKHamming = 8192;
 constexpr int64_t kMaxMergeSlots = 8192;  // lists a query's merge reads
 
 // The scan kernels' arguments (the element type of queries/items is the kernel's).
@@ -100,6 +103,12 @@ int64_t main_workgroups();
 // kScoreF32FromI32).
 bool blocked_hamming_fits(int64_t B, int64_t W, int64_t k, bool masked);  // lists fit in LDS
 size_t blocked_hamming_workspace(int64_t B, int64_t N, int64_t W, int64_t k, bool masked);
+// The 1-bit full scan for kMaxK < k <= kMaxKHamming (scan_hamming_large.hip).
+size_t hamming_large_k_workspace(int64_t B, int64_t N, int64_t W);
+int hamming_large_k(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, int64_t N,
+                    int64_t W, int64_t k, const uint64_t* mask, int64_t mask_words,
+                    int64_t* out_ids, void* out_scores, int score_kind, void* workspace,
+                    size_t workspace_bytes, hipStream_t stream);
 int blocked_hamming(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, int64_t N,
                     int64_t W, int64_t k, const uint64_t* mask, int64_t mask_words,
                     int64_t* out_ids, void* out_scores, int score_kind, void* workspace,

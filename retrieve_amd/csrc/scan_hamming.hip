@@ -255,6 +255,7 @@ using namespace rt;
 
 extern "C" size_t rt_hamming_scan_topk_workspace(int64_t B, int64_t N, int64_t W, int64_t k,
                                                  int masked) {
+  if (k > kMaxK) return hamming_large_k_workspace(B > 0 ? B : 1, N, W);
   if (ham_mfma(B, W, k, masked != 0)) {
     return blocked_hamming_workspace(B, N, W, k, masked != 0);
   }
@@ -271,8 +272,8 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B,
                                     int score_f32, void* workspace, size_t workspace_bytes,
                                     hipStream_t stream) {
   RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
-  RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
-               static_cast<long long>(kMaxK), static_cast<long long>(k));
+  RT_CHECK_ARG(k >= 1 && k <= kMaxKHamming, "k must be in [1, %lld], got %lld",
+               static_cast<long long>(kMaxKHamming), static_cast<long long>(k));
   RT_CHECK_ARG(N < 0xffffffffll, "N must be < 2**32 - 1");
   RT_CHECK_ARG(W >= 1 && W <= kHamMaxWords,
                "W (64-bit words per code) must be in [1, %d], got %lld", kHamMaxWords,
@@ -283,6 +284,10 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B,
   if (B == 0) return kOk;
   const int kind = score_f32 ? kScoreF32FromI32 : kScoreI32;
   if (N == 0) return launch_pad(out_ids, out_scores, B, k, kind, stream);
+  if (k > kMaxK) {
+    return hamming_large_k(query_bits, B, item_bits, N, W, k, mask, mask_words, out_ids,
+                           out_scores, kind, workspace, workspace_bytes, stream);
+  }
   if (ham_mfma(B, W, k, mask != nullptr)) {
     return blocked_hamming(query_bits, B, item_bits, N, W, k, mask, mask_words, out_ids,
                            out_scores, kind, workspace, workspace_bytes, stream);

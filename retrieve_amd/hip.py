@@ -183,6 +183,11 @@ def _(query, item_embs, k, mask=None):
 # --- 1-bit Hamming full scan + top-k --------------------------------------------------------
 
 
+# The full 1-bit scan selects up to this many items (above 1024 by counting its 64 W + 1 scores);
+# the other scans up to 1024.
+HAMMING_MAX_K = 8192
+
+
 def _hamming_prep(query_bits: Tensor, item_bits: Tensor, k: int, mask: Tensor | None):
     """``_oporp_prep``'s checks (``ops/triton/oporp_1bit_match_topk.py:148-165``)."""
     if query_bits.dim() != 2 or item_bits.dim() != 2:
@@ -193,8 +198,8 @@ def _hamming_prep(query_bits: Tensor, item_bits: Tensor, k: int, mask: Tensor | 
         raise ValueError(
             f"W mismatch: query_bits W={query_bits.shape[1]} vs item_bits W={item_bits.shape[1]}"
         )
-    if not 1 <= k <= 1024:
-        raise ValueError(f"k must be in [1, 1024], got {k}")
+    if not 1 <= k <= HAMMING_MAX_K:
+        raise ValueError(f"k must be in [1, {HAMMING_MAX_K}], got {k}")
     _check_items(item_bits=item_bits)
     b, n = query_bits.shape[0], item_bits.shape[0]
     if mask is not None:

@@ -27,7 +27,7 @@ from torch import Tensor, nn
 
 from retrieve_amd import _native as nat
 from retrieve_amd import bloom as _bloom
-from retrieve_amd import hip as _hip  # noqa: F401  (registers torch.ops.retrieve.*)
+from retrieve_amd import hip as _hip  # registers torch.ops.retrieve.*
 from retrieve_amd import st as _st  # registers torch.ops.st.*
 
 ops = torch.ops.retrieve
@@ -476,8 +476,8 @@ class LiNRV3(RetrievalModule):
     items, then exact fp16 rescoring to ``k``. With a filter, the shortlist is the Hamming
     full scan under the filter's packed words: the same items as the reference's compaction
     followed by the indirect Hamming top-k (both keep the best ``candidate_pool`` passing items,
-    ties to the lower id), without the ``[B, N]`` id list. The fused scans select at most 1024
-    items, so ``candidate_pool`` above that (the reference's default is 5000) raises
+    ties to the lower id), without the ``[B, N]`` id list. Pools above 1024 (the reference's
+    default is 5000) are selected by counting the Hamming scores; above 8192 they raise
     ``ValueError``."""
 
     capturable = True
@@ -519,9 +519,9 @@ class LiNRV3(RetrievalModule):
 
 
 def _check_pool(candidate_pool: int) -> None:
-    if candidate_pool > 1024:
-        raise ValueError(f"candidate_pool={candidate_pool} exceeds the fused scans' top-k "
-                         "limit of 1024")
+    if candidate_pool > _hip.HAMMING_MAX_K:
+        raise ValueError(f"candidate_pool={candidate_pool} exceeds the 1-bit scan's top-k "
+                         f"limit of {_hip.HAMMING_MAX_K}")
 
 
 VARIANTS = {"v1": LiNRV1, "v2": LiNRV2, "v3": LiNRV3}

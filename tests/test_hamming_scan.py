@@ -145,3 +145,23 @@ def test_oporp_full_schema(dev):
         torch.ops.retrieve.oporp_1bit_match_topk_full(q.int(), it, 3)
     with pytest.raises(ValueError):
         torch.ops.retrieve.oporp_1bit_match_topk_full(q[:, :4], it, 3)
+
+
+@pytest.mark.parametrize(
+    "b,n,w,k,masked,distinct",
+    [(3, 20000, 8, 5000, False, 0), (9, 30000, 3, 2000, True, 0), (2, 30000, 8, 3000, False, 5),
+     (4, 9000, 16, 8192, True, 0), (1, 1500, 2, 1100, False, 0), (5, 40000, 1, 4000, True, 3)],
+)
+def test_large_k(dev, b, n, w, k, masked, distinct):
+    """k above 1024 (LiNR V3's candidate pools): selection by counting the 64 W + 1 scores, the
+    ties at the cut resolved by id bins of 8192 (heavy ties span several bins), pads when fewer
+    than k items pass."""
+    g = rng(b * 5 + n + w + k)
+    q = _codes(g, b, w)
+    if distinct:
+        base = _codes(g, distinct, w)
+        items = base[g.integers(0, distinct, n)]
+    else:
+        items = _codes(g, n, w)
+    mask = (g.random((b, n)) < 0.3) if masked else None
+    _check(dev, q, items, k, mask)

@@ -321,8 +321,14 @@ def test_linr_variants(dev):
             assert np.allclose(sc[r, :mm], exact[r, ids[r, :mm]], rtol=1e-3, atol=1e-4)
             kth = exact[r, want_ids[r, mm - 1]] if mm else 0.0
             assert (exact[r, ids[r, :mm]] >= kth - 2e-3 * max(abs(kth), 1e-3)).all()
+    # the reference's default pool of 5000 (selected by counting Hamming scores): over these
+    # 5000 items the shortlist holds every passing item, so the result is the exact filtered top-k
+    v3d = LiNRV3(k, seed=2, filter=ExactAttributeFilter())
+    v3d.register_index(_t(dev, items), _t(dev, attrs))
+    ids, sc = v3d(_t(dev, q), v3d.prepare_queries(_t(dev, qa)))
+    _dense_check(_np(ids), _np(sc), q16, i16, k, valid)
     with pytest.raises(ValueError):
-        LiNRV3(k)  # the reference's default pool of 5000 is above the fused top-k limit
+        LiNRV3(k, candidate_pool=9000)
     built = (LiNRBuilder("v2", k=k).set_filter(ExactAttributeFilter(), _t(dev, attrs))
              .set_item_embeddings(_t(dev, items)).build())
     ids2, _ = built(_t(dev, q), built.prepare_queries(_t(dev, qa)))

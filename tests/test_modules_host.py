@@ -99,7 +99,7 @@ def test_module_argument_checks(mods):
     with pytest.raises(ValueError):
         mods.SilverTorch(10, 4, 2, m_bits=64)
     with pytest.raises(ValueError):
-        mods.LiNRV3(100)  # pool 5000 > 1024
+        mods.LiNRV3(100, candidate_pool=9000)  # above the 1-bit scan's 8192
     with pytest.raises(ValueError):
         mods.LiNRV3(100, candidate_pool=50)
     with pytest.raises(ValueError):
