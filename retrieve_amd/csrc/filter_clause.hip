@@ -479,6 +479,34 @@ __device__ inline uint64_t wave_transpose64(uint64_t x, int lane) {
   return x;
 }
 
+// The same for 32 rows: lane l holds 32 row bits; lane r < 32 ends with row r's 64-bit word
+// (bit l = lane l's bit r). A 32 x 32 transpose within each half-wave (five stages, partners
+// reached by ds_swizzle's xor mode, which stays within 32 lanes), then the upper half's word of
+// row r moves to lane r as the high dword.
+template <int T>
+__device__ inline uint32_t transpose32_stage(uint32_t x, int lane) {
+  constexpr int s = 1 << T;
+  // the bits j with (j & s) == 0
+  constexpr uint32_t m = T == 0   ? 0x55555555u
+                         : T == 1 ? 0x33333333u
+                         : T == 2 ? 0x0f0f0f0fu
+                         : T == 3 ? 0x00ff00ffu
+                                  : 0x0000ffffu;
+  const uint32_t y =
+      static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(x), 0x1f | (s << 10)));
+  return (lane & s) ? (((y >> s) & m) | (x & ~m)) : ((x & m) | ((y & m) << s));
+}
+
+__device__ inline uint64_t wave_transpose32(uint32_t x, int lane) {
+  x = transpose32_stage<4>(x, lane);
+  x = transpose32_stage<3>(x, lane);
+  x = transpose32_stage<2>(x, lane);
+  x = transpose32_stage<1>(x, lane);
+  x = transpose32_stage<0>(x, lane);
+  const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(x), (lane + 32) & 63));
+  return (static_cast<uint64_t>(hi) << 32) | x;
+}
+
 // ROWS query rows per workgroup (32, or 64 for the bit masks of larger batches), M their mask
 // word type.
 template <class T, int C, int ROWS>
@@ -576,10 +604,14 @@ __global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a
 
       if (bits) {
         uint64_t mine = 0ull;
-        if (nrows > 8) {
+        if (nrows > 6) {
           // lane l holds item (word base + 63 - l)'s row bits: the transpose gives lane r row
           // r's word with item d at bit 63 - d % 64, as stored
-          mine = wave_transpose64(static_cast<uint64_t>(m), lane);
+          if constexpr (ROWS == 64) {
+            mine = wave_transpose64(m, lane);
+          } else {
+            mine = wave_transpose32(m, lane);
+          }
         } else {
           for (int r = 0; r < nrows; ++r) {
             const uint64_t word = __ballot((m >> r) & 1u);

@@ -258,20 +258,21 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
         pre[s] = run;
       }
     }
-    part[tid] = run;
-    __syncthreads();
-    if (tid == 0) {
-      int acc = 0;
-      for (int t = 0; t < kMergeThreads; ++t) {
-        const int v = part[t];
-        part[t] = acc;
-        acc += v;
-      }
+    // exclusive prefix of the threads' runs: a scan within each wave, then the waves' totals
+    int incl = run;
+    const int lane = tid & (kWave - 1);
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int t = __shfl_up(incl, off);
+      incl += lane >= off ? t : 0;
     }
+    if (lane == kWave - 1) part[tid / kWave] = incl;
     __syncthreads();
+    int base = incl - run;
+    for (int w = 0; w < tid / kWave; ++w) base += part[w];
     for (int i = 0; i < per; ++i) {
       const int s = tid * per + i;
-      if (s < S) pre[s] += part[tid];
+      if (s < S) pre[s] += base;
     }
     __syncthreads();
     total = pre[S - 1];
@@ -343,6 +344,18 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     __syncthreads();
   }
 
+  if (m.tau_out != nullptr) {
+    // only the k-th composite: held <= k entries remain, the best k of everything when held == k
+    uint64_t lo = 0ull;
+    uint64_t hi = 0ull;
+    if (held == k) block_minmax(buf, held, red, &lo, &hi);
+    if (tid == 0) {
+      const uint64_t t = held == k ? lo : 0ull;
+      const uint64_t old = m.tau_keep ? m.tau_out[q] : 0ull;
+      m.tau_out[q] = t > old ? t : old;
+    }
+    return;
+  }
   for (int i = held + tid; i < KP; i += kMergeThreads) buf[i] = 0ull;
   __syncthreads();
   for (int size = 2; size <= KP; size <<= 1) {
@@ -362,14 +375,6 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     }
   }
 
-  if (m.tau_out != nullptr) {
-    if (tid == 0) {
-      const uint64_t t = held >= k ? buf[k - 1] : 0ull;
-      const uint64_t old = m.tau_keep ? m.tau_out[q] : 0ull;
-      m.tau_out[q] = t > old ? t : old;
-    }
-    return;
-  }
   for (int j = tid; j < k; j += kMergeThreads) {
     const uint64_t c = buf[j];
     const bool ok = c != 0ull;
