@@ -376,9 +376,9 @@ def main() -> int:
             return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
 
         scan_bytes = n * d // 8 + b * d // 8
-        # 512-bit codes from 36 queries on are scored on the int8 matrix cores, one multiply-add
+        # 512-bit codes from 33 queries on are scored on the int8 matrix cores, one multiply-add
         # per bit (bits as {0, 1} and {-2, +2} bytes): 2 ops per bit, item and query
-        mfma_scan = d == 512 and b >= 36
+        mfma_scan = d == 512 and b >= 33
         scan_ops = 2 * b * n * d if mfma_scan else 2 * b * n * (d // 32)
         step_bytes = scan_bytes + flt.bytes(n, b) + b * k1 * d
         bound = "mfma" if mfma_scan else "hbm"

@@ -49,23 +49,36 @@ constexpr int kBlkQpg = kBlkCols * 32;  // queries per workgroup (query group)
 // Up to this many queries, rows narrower than 512 bytes take the wide layout.
 constexpr int64_t kBlkWideMaxBatch = 128;
 
-// Rows per staged tile: 32 for narrow 512-byte rows, so four stages fit in half the LDS; 64
-// otherwise, and for 64-byte bit-code rows as many as make a tile one 16-byte load per thread
-// (64 narrow, 128 wide).
+// Rows per staged tile: 32 for narrow 512-byte rows, so four stages fit in half the LDS; 128
+// for the wide layout below 512-byte rows (its row quarters are 32 rows); 64 otherwise; for
+// 64-byte bit-code rows as many as make a tile one 16-byte load per thread (64 narrow, 128
+// wide).
 constexpr int blk_rows(int64_t row_bytes, bool wide, bool bits) {
-  return bits ? (wide ? 128 : 64) : (!wide && row_bytes >= 512 ? 32 : 64);
+  return bits ? (wide ? 128 : 64)
+              : (wide ? (row_bytes < 512 ? 128 : 64) : (row_bytes >= 512 ? 32 : 64));
+}
+
+// Row parts a tile is split into over the waves (a query's lists per workgroup): the wide
+// layout's eight waves take 2 row halves x 4 column-tile pairs at 512-byte rows, and 4 row
+// quarters x 2 column-tile pairs below, so from 33 queries on every wave holds a real column
+// tile; the narrow layout's four waves take whole tiles.
+constexpr int blk_halves(int64_t row_bytes, bool wide) {
+  return wide ? (row_bytes < 512 ? 4 : 2) : 1;
 }
 
 template <bool WIDE, int RB, bool BITS>
 struct BlkLayout {
   static constexpr int waves = WIDE ? 8 : 4;
   static constexpr int threads = waves * kWave;
-  static constexpr int halves = WIDE ? 2 : 1;  // row tiles split over waves: a query's lists per
-                                               // workgroup
+  static constexpr int halves = blk_halves(RB, WIDE);
+  // a wave's two column tiles: jt and jt + cstride (jt < 8 / cstride)
+  static constexpr int cstride = halves == 4 ? 2 : 4;
   static constexpr int rows = blk_rows(RB, WIDE, BITS);
   static constexpr int rtw = rows / 32 / halves;  // 32-row tiles per wave
   static constexpr int per_cu = WIDE ? 1 : 2;     // resident workgroups per CU
 };
+
+static_assert(kBlkWideMaxBatch <= kBlkQpg / 2, "the row-quarter layout covers 4 column tiles");
 
 static bool blk_wide(int64_t row_bytes, int64_t B) {
   (void)row_bytes;
@@ -281,14 +294,15 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   const int c32 = lane & 31;
   const int half = lane >> 5;
   int* cnt = reinterpret_cast<int*>(scratch + kBlkWaves * a.capw) + wave * kBlkQpw;
-  const int wr = WIDE ? wave & 1 : 0;      // this wave's first 32-row tile of each tile
-  const int jt = WIDE ? wave >> 1 : wave;  // and its column tiles jt, jt + 4
+  const int wr = WIDE ? wave % kBlkRowHalves : 0;  // this wave's row part of each tile
+  const int jt = WIDE ? wave / kBlkRowHalves : wave;  // and its column tiles jt, jt + CST
+  constexpr int CST = L::cstride;
 
   const int64_t wg = blockIdx.x;
   const int64_t nwg = gridDim.x;
   const int64_t qg0 = static_cast<int64_t>(blockIdx.y) * kBlkQpg;
-  // query of this lane in column tile j (0, 1) of the wave: qg0 + 32 (jt + 4 j) + c32
-  const int64_t q0[2] = {qg0 + 32 * jt, qg0 + 32 * (jt + 4)};
+  // query of this lane in column tile j (0, 1) of the wave: qg0 + 32 (jt + CST j) + c32
+  const int64_t q0[2] = {qg0 + 32 * jt, qg0 + 32 * (jt + CST)};
   // this wave's column tiles that hold real queries (wave-uniform; tile 1 only with tile 0)
   const int cols = (q0[0] < a.B ? 1 : 0) + (q0[1] < a.B ? 1 : 0);
   const int8_t* Q = static_cast<const int8_t*>(a.queries);
@@ -337,7 +351,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   uint64_t* lists[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int64_t g = static_cast<int64_t>(blockIdx.y) * kBlkCols + jt + 4 * j;
+    const int64_t g = static_cast<int64_t>(blockIdx.y) * kBlkCols + jt + CST * j;
     slot[j] = (g * nwg + wg) * kBlkRowHalves + wr;
     lists[j] = a.lists + slot[j] * 32 * static_cast<int64_t>(a.capw);
   }
@@ -555,7 +569,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
           for (int i = 0; i < RTW; ++i)
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-              mw[i][j] = ms[(32 * (jt + 4 * j) + c32) * MASK_DW + wr * RTW + i];
+              mw[i][j] = ms[(32 * (jt + CST * j) + c32) * MASK_DW + wr * RTW + i];
             }
         }
         // (with a mask, the maxima over the rows that pass it: a low masked bound would
@@ -675,9 +689,8 @@ static size_t blk_lds(int64_t row_bytes, int stages, int capw, bool wide, bool b
 // narrow workgroups stay resident), 0 when even three stages do not fit in the whole LDS.
 static int blk_stages(int64_t row_bytes, int capw, bool wide, bool bits, bool masked) {
   const size_t share = wide ? kMaxLds : kMaxLds / 2;
-  const int deepest = wide && row_bytes < 512 ? 8 : 4;
-  for (int s : {8, 4, 3}) {
-    if (s <= deepest && blk_lds(row_bytes, s, capw, wide, bits, masked) <= share) return s;
+  for (int s : {4, 3}) {
+    if (blk_lds(row_bytes, s, capw, wide, bits, masked) <= share) return s;
   }
   if (bits && blk_lds(row_bytes, 2, capw, wide, bits, masked) <= share) return 2;
   return blk_lds(row_bytes, kBlkMinStages, capw, wide, bits, masked) <= kMaxLds ? kBlkMinStages
@@ -715,17 +728,11 @@ static int launch_blk_layout(const ScanArgs& a, dim3 grid, int capw, hipStream_t
     return launch_blk_staged<Op, RB, true, 4, WIDE>(
         a, grid, blk_lds(RB, 4, 0, WIDE, kBits, false), stream);
   } else {
-    // the stage counts compiled: 8 or 3 (wide layout below 512-byte rows), else 4 or 3; 2 for
-    // bit codes with the lists of a large k
+    // the stage counts compiled: 4 or 3; 2 for bit codes with the lists of a large k
     const bool masked = a.mask != nullptr;
-    int stages = blk_stages(RB, capw, WIDE, kBits, masked);
-    if (WIDE && RB < 512 && stages == 4) stages = 3;
+    const int stages = blk_stages(RB, capw, WIDE, kBits, masked);
     const size_t lds = blk_lds(RB, stages, capw, WIDE, kBits, masked);
-    if constexpr (WIDE && RB < 512) {
-      if (stages == 8) return launch_blk_staged<Op, RB, false, 8, WIDE>(a, grid, lds, stream);
-    } else {
-      if (stages == 4) return launch_blk_staged<Op, RB, false, 4, WIDE>(a, grid, lds, stream);
-    }
+    if (stages == 4) return launch_blk_staged<Op, RB, false, 4, WIDE>(a, grid, lds, stream);
     if (stages == 3) return launch_blk_staged<Op, RB, false, 3, WIDE>(a, grid, lds, stream);
     if constexpr (kBits) {
       if (stages == 2) return launch_blk_staged<Op, RB, false, 2, WIDE>(a, grid, lds, stream);
@@ -798,7 +805,11 @@ static int blk_capw(int64_t k, int rows) { return static_cast<int>(next_pow2(k +
 static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int64_t target_cus,
                          bool bits, bool masked, size_t* off_mask_t = nullptr) {
   const bool wide = blk_wide(row_bytes, B);
-  ScanPlan p = plan_scan(B, N, k, kBlkQpg, (wide ? 8 : 4) * kBlkQpw, target_cus * (wide ? 1 : 2),
+  // the row-quarter layout covers column tiles 0-3 only (B <= kBlkWideMaxBatch = 128): its
+  // lists are sized for those 128 queries
+  const int halves = blk_halves(row_bytes, wide);
+  const int64_t qpg = halves == 4 ? kBlkQpg / 2 : kBlkQpg;
+  ScanPlan p = plan_scan(B, N, k, qpg, halves * qpg, target_cus * (wide ? 1 : 2),
                          blk_capw(k, blk_rows(row_bytes, wide, bits)), kBlkRows);
   if (off_mask_t != nullptr) *off_mask_t = align_up(p.total, 256);
   if (masked) {

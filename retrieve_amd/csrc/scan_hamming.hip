@@ -237,11 +237,12 @@ static int ham_qpw(int64_t B) { return static_cast<int>(B < kHamMaxQpw ? B : kHa
 
 // From this batch on, 512-bit codes are scored on the int8 matrix cores (the blocked scan with
 // bits expanded to bytes); below, one XOR + popcount pass per query and word. Measured over 30M
-// codes: the popcount pass costs ~0.33 ms + ~52 us per query (VALU-bound: 2 VALU per 32 bits),
-// the matrix path ~2.1-2.2 ms from 8 to 64 queries (the per-row bit expansion, shared by up to
-// 256 queries, dominates at small batches); they cross at about 36 queries.
+// codes: the popcount pass costs ~0.33 ms + ~52 us per query (VALU-bound: 2 VALU per 32 bits);
+// the matrix path ~2.1 ms up to 32 queries (one real column tile: half the waves idle, the
+// per-row bit expansion dominates) and 1.6 ms at 64 (every wave holds a column tile), so it
+// takes over from the second column tile on.
 #ifndef RT_HAM_MFMA_MIN_BATCH
-#define RT_HAM_MFMA_MIN_BATCH 36
+#define RT_HAM_MFMA_MIN_BATCH 33
 #endif
 constexpr int64_t kHamMfmaMinBatch = RT_HAM_MFMA_MIN_BATCH;
 

@@ -34,7 +34,10 @@ _BLOCKED_ROW_BYTES = (128, 256, 512)
 def _use_blocked(b: int, row_bytes: int, k: int) -> bool:
     capw = 1 << (k + 64 - 1).bit_length()
     wide = b <= 128  # the kernel's wide / narrow layout
-    rows = 32 if not wide and row_bytes >= 512 else 64
+    if wide:
+        rows = 128 if row_bytes < 512 else 64
+    else:
+        rows = 32 if row_bytes >= 512 else 64
     stage = rows * row_bytes + 256 * (rows // 32) * 4  # a tile and its mask words
     lds = 3 * stage + (8 if wide else 4) * (capw * 8 + 64 * 4)
     return b >= BLOCKED_MIN_BATCH and row_bytes in _BLOCKED_ROW_BYTES and lds <= 160 * 1024
