@@ -617,7 +617,9 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
                   const uint32_t item = static_cast<uint32_t>(row);
                   const uint64_t c = composite(Op::key(sc), item);
                   bool keep = row < n && sc >= ts[j] && c >= tau[j];
-                  if constexpr (masked) keep = keep && ((mw[i][j] >> (31 - 8 * g - 4 * half - u)) & 1u);
+                  if constexpr (masked) {
+                    keep = keep && ((mw[i][j] >> (31 - 8 * g - 4 * half - u)) & 1u);
+                  }
                   // lanes l and l ^ 32 score the same query: the upper half's entry goes second
                   const uint64_t kb = __ballot(keep);
                   const int lo = static_cast<int>(static_cast<uint32_t>(kb) >> c32 & 1u);
@@ -692,7 +694,10 @@ static int blk_stages(int64_t row_bytes, int capw, bool wide, bool bits, bool ma
   for (int s : {4, 3}) {
     if (blk_lds(row_bytes, s, capw, wide, bits, masked) <= share) return s;
   }
-  if (bits && blk_lds(row_bytes, 2, capw, wide, bits, masked) <= share) return 2;
+  // two stages: the small bit-code tiles, and the wide layout's 32 KiB tiles, beside the lists
+  // of a large k
+  const bool two = bits || (wide && row_bytes < 512);
+  if (two && blk_lds(row_bytes, 2, capw, wide, bits, masked) <= share) return 2;
   return blk_lds(row_bytes, kBlkMinStages, capw, wide, bits, masked) <= kMaxLds ? kBlkMinStages
                                                                                  : 0;
 }
@@ -728,13 +733,14 @@ static int launch_blk_layout(const ScanArgs& a, dim3 grid, int capw, hipStream_t
     return launch_blk_staged<Op, RB, true, 4, WIDE>(
         a, grid, blk_lds(RB, 4, 0, WIDE, kBits, false), stream);
   } else {
-    // the stage counts compiled: 4 or 3; 2 for bit codes with the lists of a large k
+    // the stage counts compiled: 4 or 3; 2 for bit codes and the wide layout below 512-byte rows
+    // with the lists of a large k
     const bool masked = a.mask != nullptr;
     const int stages = blk_stages(RB, capw, WIDE, kBits, masked);
     const size_t lds = blk_lds(RB, stages, capw, WIDE, kBits, masked);
     if (stages == 4) return launch_blk_staged<Op, RB, false, 4, WIDE>(a, grid, lds, stream);
     if (stages == 3) return launch_blk_staged<Op, RB, false, 3, WIDE>(a, grid, lds, stream);
-    if constexpr (kBits) {
+    if constexpr (kBits || (WIDE && RB < 512)) {
       if (stages == 2) return launch_blk_staged<Op, RB, false, 2, WIDE>(a, grid, lds, stream);
     }
     set_error("the blocked scan's lists do not fit in LDS at %d-byte rows", RB);

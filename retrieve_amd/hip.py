@@ -32,14 +32,17 @@ _BLOCKED_ROW_BYTES = (128, 256, 512)
 
 
 def _use_blocked(b: int, row_bytes: int, k: int) -> bool:
-    capw = 1 << (k + 64 - 1).bit_length()
+    """Mirrors the kernel's LDS plan (``blk_rows``, ``blk_capw``, ``blk_lds``, ``blk_stages`` in
+    ``csrc/scan_blocked.h``): the blocked scan only where its lists and fewest stages fit."""
     wide = b <= 128  # the kernel's wide / narrow layout
     if wide:
         rows = 128 if row_bytes < 512 else 64
     else:
         rows = 32 if row_bytes >= 512 else 64
+    capw = 1 << (k + rows - 1).bit_length()  # the next power of two >= k + rows
     stage = rows * row_bytes + 256 * (rows // 32) * 4  # a tile and its mask words
-    lds = 3 * stage + (8 if wide else 4) * (capw * 8 + 64 * 4)
+    # the fewest stages the kernel is built with: 2 for the wide layout's 32 KiB tiles, else 3
+    lds = (2 if wide and row_bytes < 512 else 3) * stage + (8 if wide else 4) * (capw * 8 + 64 * 4)
     return b >= BLOCKED_MIN_BATCH and row_bytes in _BLOCKED_ROW_BYTES and lds <= 160 * 1024
 
 

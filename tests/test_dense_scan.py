@@ -71,9 +71,11 @@ def test_random_parity(dev, b, n, d, k):
 
 
 @pytest.mark.parametrize("b,n,d,k", [(128, 20000, 128, 100), (1024, 5000, 64, 10),
-                                     (300, 3000, 256, 1000), (40, 9000, 128, 100)])
+                                     (300, 3000, 256, 1000), (40, 9000, 128, 100),
+                                     (64, 20000, 128, 700), (96, 9000, 64, 1000)])
 def test_large_batch_parity(dev, b, n, d, k):
-    """B >= 32 (rows of 128, 256 or 512 bytes) runs the register-blocked kernel."""
+    """B >= 32 (rows of 128, 256 or 512 bytes) runs the register-blocked kernel; B <= 128 below
+    512-byte rows the row-quarter layout, two stages beside the lists of k = 700 and 1000."""
     g = rng(b + n + d + k + 5)
     q = g.standard_normal((b, d)).astype(np.float32)
     it = g.standard_normal((n, d)).astype(np.float32)

@@ -118,3 +118,14 @@ def test_postfilter_loads_reference_state_dict(mods):
     again = mods.LiNRBuilder("v1", k=5).set_state_dict(
         {"idx." + k: v for k, v in own.state_dict().items()}).build()
     assert torch.equal(again.idx.item_embs, e)
+
+
+def test_blocked_gate_mirrors_the_kernel_plan():
+    """The Python gate's LDS estimate follows the kernel's (tile rows and list capacity per
+    layout): lists of k + 128 entries at the wide layout's 128-row tiles."""
+    from retrieve_amd import hip
+
+    assert hip._use_blocked(64, 256, 384) and not hip._use_blocked(64, 256, 900)
+    assert hip._use_blocked(64, 256, 700)  # two 32 KiB stages beside 1024-entry lists
+    assert not hip._use_blocked(31, 256, 100)  # below the blocked batch
+    assert hip._use_blocked(300, 512, 990)  # narrow 32-row tiles: lists of 1024
