@@ -504,12 +504,13 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
 // ---- column kernel: programs over LDS-staged bundles -------------------------------------
 //
 // A workgroup stages two bundles (64 columns, 2 * 64 * 32 words = 32 KiB at 64 bits per doc)
-// in LDS once; its four waves then run the programs of its plans (wave w: plans w, w + 4, ...),
-// lane <-> column, the top of the folded stack in a register and the levels below it in LDS.
+// in LDS once; its four (or eight) waves then run the programs of its plans (wave w: plans w,
+// w + waves, ...), lane <-> column, the top of the folded stack in a register and the levels
+// below it in LDS.
 // Every index word leaves HBM once per workgroup. Lanes of a bundle whose width differs from
 // bundle 0's resolve their positions from the stored hashes and read HBM.
-constexpr int kColThreads = 256;
-constexpr int kColWaves = kColThreads / kWave;
+// Plans per workgroup from which the column kernel runs eight waves instead of four.
+constexpr int64_t kColWidePlans = 64;
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 // A term from its stored hashes for a bundle of width w (any width the build allows): the AND of
@@ -675,9 +676,12 @@ __device__ inline uint64_t run_program(const BloomSearchArgs& a, gu32* prog, uin
   return f.top;
 }
 
-// KK = min(k, hash_k): the positions every term's program words carry.
-template <int KK>
-__global__ void __launch_bounds__(kColThreads) bloom_column_kernel(BloomSearchArgs a) {
+// KK = min(k, hash_k): the positions every term's program words carry. THREADS: 256, or 512
+// when a workgroup has many plans (its bundles' staging then feeds twice the waves).
+template <int KK, int THREADS>
+__global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a) {
+  constexpr int kColThreads = THREADS;
+  constexpr int kColWaves = THREADS / kWave;
   __shared__ uint64_t idx[2 * kColMaxWidth * kBloomWordsPerBundle];
   __shared__ uint64_t fold[kColWaves][kFoldDepth - 1][kWave];
   const int tid = threadIdx.x;
@@ -995,7 +999,8 @@ extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_of
   const int64_t cx = cdiv(n_bundles, 2);
   RT_CHECK_ARG(cx < (int64_t{1} << 31), "too many bundles");
   int64_t cy = cdiv(2048, cx);
-  const int64_t max_cy = cdiv(plan_count, kColWaves);
+  const int col_waves = cdiv(plan_count, cy) >= kColWidePlans ? 8 : 4;
+  const int64_t max_cy = cdiv(plan_count, col_waves);
   cy = cy > max_cy ? max_cy : cy;
   cy = cy < 1 ? 1 : cy;
   cy = cy > 65535 ? 65535 : cy;
@@ -1004,13 +1009,29 @@ extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_of
   const dim3 cgrid(static_cast<unsigned>(cx), static_cast<unsigned>(cy));
   const int64_t kk = k < hash_k ? k : hash_k;  // > kProgMaxPos: every plan takes the stack path
   if (kk == 1) {
-    bloom_column_kernel<1><<<cgrid, kColThreads, 0, stream>>>(a);
+    if (col_waves == 8) {
+      bloom_column_kernel<1, 512><<<cgrid, 512, 0, stream>>>(a);
+    } else {
+      bloom_column_kernel<1, 256><<<cgrid, 256, 0, stream>>>(a);
+    }
   } else if (kk == 2) {
-    bloom_column_kernel<2><<<cgrid, kColThreads, 0, stream>>>(a);
+    if (col_waves == 8) {
+      bloom_column_kernel<2, 512><<<cgrid, 512, 0, stream>>>(a);
+    } else {
+      bloom_column_kernel<2, 256><<<cgrid, 256, 0, stream>>>(a);
+    }
   } else if (kk == 3) {
-    bloom_column_kernel<3><<<cgrid, kColThreads, 0, stream>>>(a);
+    if (col_waves == 8) {
+      bloom_column_kernel<3, 512><<<cgrid, 512, 0, stream>>>(a);
+    } else {
+      bloom_column_kernel<3, 256><<<cgrid, 256, 0, stream>>>(a);
+    }
   } else if (kk == 4) {
-    bloom_column_kernel<4><<<cgrid, kColThreads, 0, stream>>>(a);
+    if (col_waves == 8) {
+      bloom_column_kernel<4, 512><<<cgrid, 512, 0, stream>>>(a);
+    } else {
+      bloom_column_kernel<4, 256><<<cgrid, 256, 0, stream>>>(a);
+    }
   }
   RT_CHECK_HIP(hipGetLastError());
 
