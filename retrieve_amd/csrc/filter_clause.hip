@@ -510,7 +510,10 @@ __device__ inline uint64_t wave_transpose32(uint32_t x, int lane) {
 // ROWS query rows per workgroup (32, or 64 for the bit masks of larger batches), M their mask
 // word type.
 template <class T, int C, int ROWS>
-__global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a) {
+__global__ void __launch_bounds__((ROWS == 64 ? 2 : 1) * kClauseThreads)
+    clause_row_kernel(ClauseArgs a) {
+  // eight waves for the 64-row groups (their tables fill LDS to two workgroups per CU)
+  constexpr int kThreads = (ROWS == 64 ? 2 : 1) * kClauseThreads;
   using S = RowShape<T, C>;
   using M = typename std::conditional<ROWS == 64, uint64_t, uint32_t>::type;
   extern __shared__ __attribute__((aligned(8))) uint32_t tab_raw[];
@@ -526,13 +529,13 @@ __global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a
   const int nrows = static_cast<int>(b0 + ROWS < a.B ? ROWS : a.B - b0);
   constexpr M kOne = 1;
 
-  for (int i = tid; i < C * kTabStride; i += kClauseThreads) tab[i] = 0;
+  for (int i = tid; i < C * kTabStride; i += kThreads) tab[i] = 0;
   if (tid == 0) slow_rows = 0;
   if (tid < ROWS) row_active[tid] = tid < nrows ? a.active[b0 + tid] : 0u;
   __syncthreads();
   if (tid < nrows && a.small[b0 + tid] == 0u) atomicOr(&slow_rows, kOne << tid);
   // every (row, clause) value of the bitmap rows sets its row's bit
-  for (int rc = tid; rc < nrows * C; rc += kClauseThreads) {
+  for (int rc = tid; rc < nrows * C; rc += kThreads) {
     const int r = rc / C;
     const int c = rc - r * C;
     const int64_t b = b0 + r;
@@ -550,7 +553,7 @@ __global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a
     clause_fold[1][tid] = unconstrained;
   }
   __syncthreads();
-  for (int i = tid; i < C * kTabStride; i += kClauseThreads) {
+  for (int i = tid; i < C * kTabStride; i += kThreads) {
     const int c = i / kTabStride;
     tab[i] = (tab[i] ^ clause_fold[0][c]) | clause_fold[1][c];
   }
@@ -561,7 +564,7 @@ __global__ void __launch_bounds__(kClauseThreads) clause_row_kernel(ClauseArgs a
   // words per step with every load of the step issued first: enough bytes in flight per CU to
   // cover HBM latency, and a workgroup's mask stores fill whole lines of each row.
   const int64_t words = (a.N + kWave - 1) / kWave;
-  constexpr int kStepWords = kRowUnroll * (kClauseThreads / kWave);
+  constexpr int kStepWords = kRowUnroll * (kThreads / kWave);
   const int64_t steps = (words + kStepWords - 1) / kStepWords;
   const int64_t per_wg = (steps + gridDim.x - 1) / gridDim.x * kStepWords;
   const int64_t w_lo = static_cast<int64_t>(blockIdx.x) * per_wg;
@@ -646,7 +649,7 @@ static bool launch_row_kernel(const ClauseArgs& a, dim3 grid, hipStream_t stream
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(lds));
     }
-    clause_row_kernel<T, C, 64><<<grid, kClauseThreads, lds, stream>>>(a);
+    clause_row_kernel<T, C, 64><<<grid, 2 * kClauseThreads, lds, stream>>>(a);
   } else {
     const size_t lds = static_cast<size_t>(C) * kTabStride * sizeof(uint32_t);
     clause_row_kernel<T, C, 32><<<grid, kClauseThreads, lds, stream>>>(a);
