@@ -241,10 +241,7 @@ static int ham_qpw(int64_t B) { return static_cast<int>(B < kHamMaxQpw ? B : kHa
 // the matrix path ~2.1 ms up to 32 queries (one real column tile: half the waves idle, the
 // per-row bit expansion dominates) and 1.6 ms at 64 (every wave holds a column tile), so it
 // takes over from the second column tile on.
-#ifndef RT_HAM_MFMA_MIN_BATCH
-#define RT_HAM_MFMA_MIN_BATCH 33
-#endif
-constexpr int64_t kHamMfmaMinBatch = RT_HAM_MFMA_MIN_BATCH;
+constexpr int64_t kHamMfmaMinBatch = 33;
 
 static bool ham_mfma(int64_t B, int64_t W, int64_t k, bool masked) {
   return W == 8 && B >= kHamMfmaMinBatch && blocked_hamming_fits(B, W, k, masked);
