@@ -782,7 +782,8 @@ static int dispatch_blk(int64_t row_bytes, const ScanArgs& a, const PassPlan& p,
 }
 
 // The mask transposed for the main pass, [ceil(N/64)][stride] with stride = B rounded up to
-// whole query groups: a 64 x 64 block of words per workgroup through LDS. Padding queries are 0.
+// whole query groups: a 64 x 64 block of words per workgroup through LDS, each thread's sixteen
+// loads issued before any LDS store. Padding queries are 0.
 __global__ void __launch_bounds__(256) mask_transpose_kernel(const uint64_t* mask, int64_t B,
                                                              int64_t mask_words, int64_t W,
                                                              uint64_t* out, int64_t stride) {
@@ -791,15 +792,22 @@ __global__ void __launch_bounds__(256) mask_transpose_kernel(const uint64_t* mas
   const int64_t q0 = static_cast<int64_t>(blockIdx.y) * 64;
   const int tx = threadIdx.x & 63;
   const int ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += 4) {  // row q0 + r of the mask, words w0 + tx
-    const int64_t q = q0 + r;
+  uint64_t v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {  // row q0 + ty + 4 i of the mask, words w0 + tx
+    const int64_t q = q0 + ty + 4 * i;
     const int64_t w = w0 + tx;
-    tile[r][tx] = q < B && w < W ? mask[q * mask_words + w] : 0ull;
+    v[i] = q < B && w < W ? __builtin_nontemporal_load(mask + q * mask_words + w) : 0ull;
   }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tile[ty + 4 * i][tx] = v[i];
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) {  // row w0 + r of the output, queries q0 + tx
-    const int64_t w = w0 + r;
-    if (w < W) out[w * stride + q0 + tx] = tile[tx][r];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = tile[tx][ty + 4 * i];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {  // row w0 + ty + 4 i of the output, queries q0 + tx
+    const int64_t w = w0 + ty + 4 * i;
+    if (w < W) out[w * stride + q0 + tx] = v[i];
   }
 }
 
