@@ -41,9 +41,9 @@ struct LkArgs {
   int64_t mask_words;
   int nb;            // 64 W + 1 popcount bins
   int64_t nbin;      // id bins
-  int32_t* hist;     // [B][nb]
+  uint32_t* hist;    // [B][nb] (N < 2^32 items: a count fits)
   int32_t* cnt;      // [B][4]: appends to A, B, C
-  int32_t* idhist;   // [B][nbin]
+  uint32_t* idhist;  // [B][nbin]
   int32_t* cut;      // [B][8]: h*, lt, need, b*, need2
   uint64_t* buf_a;   // [B][kLkCap]: h < h*
   uint64_t* buf_b;   // [B][kLkCap]: h == h*, id bin < b*
@@ -77,7 +77,7 @@ __device__ inline void lk_load(const uint32_t* __restrict__ I, int64_t item, uin
 // bins up to b*.
 template <int W, int MODE>
 __global__ void __launch_bounds__(kLkThreads) lk_pass_kernel(LkArgs a) {
-  extern __shared__ int32_t lh[];  // MODE 0: [kLkQpw][nb]
+  extern __shared__ uint32_t lh[];  // MODE 0: [kLkQpw][nb]
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t q0 = static_cast<int64_t>(blockIdx.y) * kLkQpw;
@@ -105,7 +105,7 @@ __global__ void __launch_bounds__(kLkThreads) lk_pass_kernel(LkArgs a) {
         ok = (a.mask[q * a.mask_words + (row >> 6)] >> (63 - (row & 63))) & 1ull;
       }
       if constexpr (MODE == 0) {
-        if (ok) atomicAdd(&lh[qi * a.nb + h], 1);
+        if (ok) atomicAdd(&lh[qi * a.nb + h], 1u);
       } else {
         const int hs = a.cut[q * 8];
         if (!__any(ok && h <= hs)) continue;
@@ -115,7 +115,7 @@ __global__ void __launch_bounds__(kLkThreads) lk_pass_kernel(LkArgs a) {
             const int pos = atomicAdd(&a.cnt[q * 4], 1);
             if (pos < kLkCap) a.buf_a[q * kLkCap + pos] = c;
           } else if (ok && h == hs) {
-            atomicAdd(&a.idhist[q * a.nbin + (row >> kLkIdShift)], 1);
+            atomicAdd(&a.idhist[q * a.nbin + (row >> kLkIdShift)], 1u);
           }
         } else {
           const int64_t bs = a.cut[q * 8 + 3];
@@ -133,54 +133,54 @@ __global__ void __launch_bounds__(kLkThreads) lk_pass_kernel(LkArgs a) {
   if constexpr (MODE == 0) {
     __syncthreads();
     for (int i = threadIdx.x; i < nq * a.nb; i += kLkThreads) {
-      const int v = lh[i];
-      if (v != 0) atomicAdd(&a.hist[(q0 + i / a.nb) * a.nb + i % a.nb], v);
+      const uint32_t v = lh[i];
+      if (v != 0u) atomicAdd(&a.hist[(q0 + i / a.nb) * a.nb + i % a.nb], v);
     }
   }
 }
 
-// Inclusive prefix sum over the wave.
-__device__ inline int lk_wave_scan(int x) {
+// Inclusive prefix sum over the wave (64-bit: the counts of up to 2^32 items).
+__device__ inline uint64_t lk_wave_scan(uint64_t x) {
   const int lane = lane_id();
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_up(x, off);
-    x += lane >= off ? y : 0;
+    const uint64_t y = __shfl_up(x, off);
+    x += lane >= off ? y : 0ull;
   }
   return x;
 }
 
 // The first index of counts[0, n) at which the running sum reaches `want` (>= 1), and the sum
-// before it; n when the counts never reach it. One wave.
-__device__ inline void lk_find(const int32_t* counts, int64_t n, int want, int64_t* at,
+// before it (< want); n when the counts never reach it. One wave.
+__device__ inline void lk_find(const uint32_t* counts, int64_t n, int want, int64_t* at,
                                int* before) {
   const int lane = lane_id();
-  int run = 0;
+  uint64_t run = 0;
   for (int64_t c0 = 0; c0 < n; c0 += kWave) {
-    const int v = c0 + lane < n ? counts[c0 + lane] : 0;
-    const int incl = lk_wave_scan(v);
-    const uint64_t hit = __ballot(run + incl >= want);
+    const uint64_t v = c0 + lane < n ? counts[c0 + lane] : 0u;
+    const uint64_t incl = lk_wave_scan(v);
+    const uint64_t hit = __ballot(run + incl >= static_cast<uint64_t>(want));
     if (hit != 0ull) {
       const int f = __builtin_ctzll(hit);
       *at = c0 + f;
-      *before = run + __shfl(incl - v, f);
+      *before = static_cast<int>(run + __shfl(incl - v, f));
       return;
     }
     run += __shfl(incl, kWave - 1);
   }
   *at = n;
-  *before = run;
+  *before = static_cast<int>(run < static_cast<uint64_t>(want) ? run : want);
 }
 
 // Step 2: h*, lt, need per query (one wave each).
 __global__ void __launch_bounds__(kWave) lk_cut_kernel(LkArgs a) {
   const int64_t q = blockIdx.x;
-  const int32_t* h = a.hist + q * a.nb;
-  int total = 0;
+  const uint32_t* h = a.hist + q * a.nb;
+  uint64_t total = 0;
   for (int i = lane_id(); i < a.nb; i += kWave) total += h[i];
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) total += __shfl_xor(total, off);
-  const int kk = total < a.k ? total : a.k;
+  const int kk = total < static_cast<uint64_t>(a.k) ? static_cast<int>(total) : a.k;
   int64_t hs = -1;  // no passing item: nothing is emitted
   int lt = 0;
   if (kk > 0) lk_find(h, a.nb, kk, &hs, &lt);
@@ -370,9 +370,9 @@ int hamming_large_k(const uint64_t* query_bits, int64_t B, const uint64_t* item_
   a.mask_words = mask_words;
   a.nb = static_cast<int>(64 * W + 1);
   a.nbin = (N + (int64_t{1} << kLkIdShift) - 1) >> kLkIdShift;
-  a.hist = reinterpret_cast<int32_t*>(ws + l.hist);
+  a.hist = reinterpret_cast<uint32_t*>(ws + l.hist);
   a.cnt = reinterpret_cast<int32_t*>(ws + l.cnt);
-  a.idhist = reinterpret_cast<int32_t*>(ws + l.idhist);
+  a.idhist = reinterpret_cast<uint32_t*>(ws + l.idhist);
   a.cut = reinterpret_cast<int32_t*>(ws + l.cut);
   a.buf_a = reinterpret_cast<uint64_t*>(ws + l.a);
   a.buf_b = reinterpret_cast<uint64_t*>(ws + l.b);
@@ -380,7 +380,8 @@ int hamming_large_k(const uint64_t* query_bits, int64_t B, const uint64_t* item_
 
   const int64_t nzero = static_cast<int64_t>(l.zero_end / 4);
   const int64_t zg = cdiv(nzero, 256) < 4096 ? cdiv(nzero, 256) : 4096;
-  lk_zero_kernel<<<static_cast<unsigned>(zg), 256, 0, stream>>>(a.hist, nzero);
+  lk_zero_kernel<<<static_cast<unsigned>(zg), 256, 0, stream>>>(
+      reinterpret_cast<int32_t*>(ws + l.hist), nzero);
   RT_CHECK_HIP(hipGetLastError());
 
   const int64_t tiles = cdiv(N, kWave);
