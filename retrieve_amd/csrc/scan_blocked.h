@@ -402,9 +402,11 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     if constexpr (!SEED) {
       if constexpr (masked) issue_mask(tt, st);
     }
-    if (!SEED && (tt + 1) * ROWS <= n) {
-      // a full tile of consecutive rows: a uniform tile address plus 32-bit lane offsets
-      const int8_t* tile = I + tt * static_cast<int64_t>(TILE_BYTES);
+    if ((tt + 1) * ROWS <= n) {
+      // a full tile of consecutive rows (the seed's sample blocks hold whole tiles): a uniform
+      // tile address plus 32-bit lane offsets
+      static_assert(kSeedBlock % ROWS == 0, "seed sample blocks hold whole tiles");
+      const int8_t* tile = I + sample_item(tt * ROWS, a.row_stride) * static_cast<int64_t>(RB);
 #pragma unroll
       for (int l = 0; l < TLOADS; ++l) {
         // (the global address goes through a named pointer: passing the sum straight to the
@@ -426,7 +428,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       const int r = toff[l] / RB;
       int64_t row = tt * ROWS + r;
       row = row < n ? row : n - 1;  // rows past the end load a valid row and are never scored
-      const int8_t* g = I + row * a.row_stride * RB + toff[l] % RB;
+      const int8_t* g = I + sample_item(row, a.row_stride) * RB + toff[l] % RB;
       __builtin_amdgcn_global_load_lds(
           g,
           (__attribute__((address_space(3))) void*)(base + (l * kBlkThreads + wave * kWave) * 16),
@@ -543,7 +545,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int64_t row = rt + 32 * (wr * RTW + i) + (r / 4) * 8 + (r % 4);
-            const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
+            const uint32_t item = static_cast<uint32_t>(sample_item(row, a.row_stride));
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
               const uint64_t c = composite(Op::key(acc[i][j][r]), item);

@@ -67,6 +67,17 @@ struct MergeArgs {
   int score_kind;
 };
 
+// The seed pass samples blocks of kSeedBlock consecutive rows spread evenly over the table
+// (row_stride = N / sample rows > 1), so each block is read as one contiguous run; sample row r
+// is item sample_item(r, stride). The sample's k-th best is a lower bound of the table's for any
+// choice of rows. The sample size is a multiple of kSeedBlock, and the last block ends at most at
+// N - 1 - (kSeedBlock - 1) (stride - 1).
+constexpr int64_t kSeedBlock = 256;
+
+__host__ __device__ inline int64_t sample_item(int64_t r, int64_t stride) {
+  return stride == 1 ? r : (r / kSeedBlock) * (kSeedBlock * stride) + (r % kSeedBlock);
+}
+
 // One pass of a scan: its grid and list geometry.
 struct PassPlan {
   int64_t n_rows = 0;

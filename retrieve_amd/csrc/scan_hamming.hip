@@ -91,7 +91,7 @@ __global__ void __launch_bounds__(kScanThreads) seed_hamming_kernel(ScanArgs a) 
   for (int64_t t = wi; t < ntiles; t += S) {
     const int64_t row = t * kHamTile + lane;
     const bool valid = row < a.n_rows;
-    const uint32_t item = static_cast<uint32_t>((valid ? row : 0) * a.row_stride);
+    const uint32_t item = static_cast<uint32_t>(sample_item(valid ? row : 0, a.row_stride));
     uint32_t iw[2 * W];
     load_codes<W>(I, item, iw);
     for (int qi = 0; qi < nq; ++qi) {

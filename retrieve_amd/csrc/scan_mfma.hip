@@ -103,7 +103,7 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
     const int64_t rb = r0 + t * kTile;
     int64_t lr = rb + col;
     lr = lr < r1 ? lr : r1 - 1;
-    const int8_t* ip = I + lr * a.row_stride * D + grp * 16;
+    const int8_t* ip = I + sample_item(lr, a.row_stride) * D + grp * 16;
     v4i af[KSTEPS];
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) af[s] = *reinterpret_cast<const v4i*>(ip + s * 64);
@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t row = rb + 4 * grp + r;
-      const uint32_t item = static_cast<uint32_t>(row * a.row_stride);
+      const uint32_t item = static_cast<uint32_t>(sample_item(row, a.row_stride));
       bool ok = row < r1;
       if (ok && qmask != nullptr) ok = (qmask[item >> 6] >> (63 - (item & 63))) & 1ull;
       const uint64_t c = composite(KeyOps<Score>::key(acc[r]), item);
