@@ -767,19 +767,21 @@ template <class Op>
 static int dispatch_blk(int64_t row_bytes, const ScanArgs& a, const PassPlan& p, int64_t nqg,
                         bool seed, bool wide, hipStream_t stream) {
   if constexpr (Op::kBits) {
+    // (only 64-byte rows are instantiated for bit codes)
     if (row_bytes == 64) return launch_blk<Op, 64>(a, p, nqg, seed, wide, stream);
     set_error("the blocked bit-code scan supports 512-bit codes, got %lld bits",
               static_cast<long long>(8 * row_bytes));
     return kInvalidArgument;
-  }
-  switch (row_bytes) {
-    case 128: return launch_blk<Op, 128>(a, p, nqg, seed, wide, stream);
-    case 256: return launch_blk<Op, 256>(a, p, nqg, seed, wide, stream);
-    case 512: return launch_blk<Op, 512>(a, p, nqg, seed, wide, stream);
-    default:
-      set_error("blocked scan supports rows of 128, 256 or 512 bytes, got %lld",
-                static_cast<long long>(row_bytes));
-      return kInvalidArgument;
+  } else {
+    switch (row_bytes) {
+      case 128: return launch_blk<Op, 128>(a, p, nqg, seed, wide, stream);
+      case 256: return launch_blk<Op, 256>(a, p, nqg, seed, wide, stream);
+      case 512: return launch_blk<Op, 512>(a, p, nqg, seed, wide, stream);
+      default:
+        set_error("blocked scan supports rows of 128, 256 or 512 bytes, got %lld",
+                  static_cast<long long>(row_bytes));
+        return kInvalidArgument;
+    }
   }
 }
 
