@@ -842,8 +842,8 @@ static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int
 // the list appends behind the seed's bound cost more than the pass): every kSampleTileStride-th
 // tile, when that gives kSampleMinTiles tiles or more.
 constexpr int64_t kSampleMinBatch = 512;
-constexpr int64_t kSampleTileStride = 8;
-constexpr int64_t kSampleMinTiles = 4096;
+constexpr int64_t kSampleTileStride = 16;
+constexpr int64_t kSampleMinTiles = 2048;
 
 
 
