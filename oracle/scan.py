@@ -78,6 +78,52 @@ def dense_topk(
     return topk_rows(dense_scores(q, items), k, valid)
 
 
+def dense_topk_chunked(
+    q: np.ndarray, items: np.ndarray, k: int, valid: np.ndarray | None = None,
+    chunk: int = 1 << 15,
+) -> tuple[np.ndarray, np.ndarray]:
+    """``dense_topk`` computed over item chunks, for tables whose ``[B, N]`` float64 score
+    matrix does not fit in memory: per chunk the entries at or above each row's chunk-local
+    k-th largest score (the whole boundary tie group), then one lowest-id selection over the
+    survivors. The chunk-then-merge structure of the reference's CPU oracle
+    (``evaluation/bench/oracle.py:95-158``, ``ITEM_CHUNK``; the merge rule ``:83-92``), in
+    float64 on torch's CPU kernels (the chunk's k-th value only: its tie order is irrelevant,
+    every entry equal to it is kept). Pinned against ``dense_topk`` on small inputs with heavy
+    ties (``tests/test_oracle.py``)."""
+    import torch
+
+    q64 = torch.from_numpy(np.ascontiguousarray(q, np.float64))
+    b = q64.shape[0]
+    n = items.shape[0]
+    keep_s: list[list[np.ndarray]] = [[] for _ in range(b)]
+    keep_i: list[list[np.ndarray]] = [[] for _ in range(b)]
+    for s0 in range(0, n, chunk):
+        part = torch.from_numpy(np.ascontiguousarray(items[s0 : s0 + chunk], np.float64))
+        sc = q64 @ part.T
+        m = sc.shape[1]
+        if valid is not None:
+            v = torch.from_numpy(np.ascontiguousarray(valid[:, s0 : s0 + m], bool))
+            sc = sc.masked_fill(~v, float("-inf"))
+        kk = min(k, m)
+        thr = sc.topk(kk, dim=1).values[:, kk - 1 :]
+        sc = sc.numpy()
+        rows, cols = np.nonzero(((sc >= thr.numpy()) & np.isfinite(sc)))
+        bounds = np.searchsorted(rows, np.arange(b + 1))
+        for r in range(b):
+            c = cols[bounds[r] : bounds[r + 1]]
+            keep_s[r].append(sc[r, c])
+            keep_i[r].append(c.astype(np.int64) + s0)
+    ids = np.full((b, k), -1, np.int64)
+    out = np.full((b, k), -np.inf)
+    for r in range(b):
+        s = np.concatenate(keep_s[r]) if keep_s[r] else np.empty(0)
+        i = np.concatenate(keep_i[r]) if keep_i[r] else np.empty(0, np.int64)
+        order = np.lexsort((i, -s))[:k]
+        ids[r, : order.size] = i[order]
+        out[r, : order.size] = s[order]
+    return ids, out
+
+
 def candidate_int8_topk(
     q_codes: np.ndarray,
     item_codes: np.ndarray,

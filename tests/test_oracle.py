@@ -95,6 +95,30 @@ def test_topk_rows_brute_force_heavy_ties(n, k):
         assert sc[r, :m].tolist() == [s[r, i] for i in want[r]]
 
 
+@pytest.mark.parametrize("n,k,chunk", [(1000, 7, 64), (300, 50, 37), (90, 100, 16),
+                                       (5000, 20, 4096)])
+def test_dense_topk_chunked_equals_brute_force(n, k, chunk):
+    """Small-integer-valued rows give exact float64 scores with heavy ties across chunk
+    boundaries: the chunked selection must equal the Python brute force (score desc, id asc),
+    masks and short rows included."""
+    g = rng(n + k + chunk)
+    q = g.integers(-2, 3, (5, 8)).astype(np.float32)
+    items = g.integers(-2, 3, (n, 8)).astype(np.float32)
+    valid = g.random((5, n)) > 0.3
+    valid[1] = False
+    valid[2] = g.random(n) < 0.01
+    s = q.astype(np.float64) @ items.T.astype(np.float64)
+    want = _brute_topk(s, k, valid)
+    ids, sc = osc.dense_topk_chunked(q, items, k, valid, chunk=chunk)
+    for r in range(5):
+        m = len(want[r])
+        assert ids[r, :m].tolist() == want[r]
+        assert (ids[r, m:] == -1).all() and np.isneginf(sc[r, m:]).all()
+        assert sc[r, :m].tolist() == [s[r, i] for i in want[r]]
+    ids2, _ = osc.dense_topk_chunked(q, items, k, None, chunk=chunk)
+    assert np.array_equal(ids2, osc.dense_topk(q, items, k)[0])
+
+
 def test_merge_topk_equals_topk_of_union():
     g = rng(4)
     s = g.integers(0, 5, (3, 40)).astype(np.float32)
@@ -350,3 +374,27 @@ def test_search_oracle_slot_order_by_hand():
     ids, _ = ost.search(q, np.array([[1, 0]]), [0, 4], [4, 2], items, perm, [1.0], 8, 5)
     # width 5 -> 32 slots after rounding: all 6 items, then -1 pads
     assert ids.tolist() == [[14, 15, 10, 11, 12, 13, -1, -1]]
+
+
+def test_search_oracle_warps_then_remainders_by_hand():
+    """The GPU scorer's write order (``fork_search_cuda.cu:989-991`` full warps, ``:1051-1053``
+    remainders): clusters of 40, 50 and 7 docs at positions 0, 40 and 90, probed [1, 0, 2].
+    Slots 0-31: cluster 1's first warp (40-71); 32-63: cluster 0's (0-31); cluster 2 has no full
+    warp; then the remainders in probe order: 64-81 cluster 1 (72-89), 82-89 cluster 0 (32-39),
+    90-96 cluster 2 (90-96). Every dot is equal, so the top-k is the lowest slots."""
+    from oracle import silvertorch as ost
+
+    offs, sizes = [0, 40, 90], [40, 50, 7]
+    want = (list(range(40, 72)) + list(range(0, 32)) + list(range(72, 90)) + list(range(32, 40))
+            + list(range(90, 97)))
+    assert ost.row_slots([1, 0, 2], offs, sizes, 97, 128).tolist() == want
+    assert ost.row_slots([1, 0, 2], offs, sizes, 97, 70).tolist() == want[:70]
+    items = np.ones((97, 16), np.int8)
+    perm = np.arange(97) + 1000
+    q = np.ones((2, 16), np.float32)
+    ids, _ = ost.search(q, np.array([[1, 0, 2], [2, 1, 0]]), offs, sizes, items, perm, [1.0],
+                        97, 97)
+    assert ids[0].tolist() == [1000 + p for p in want]
+    want1 = (list(range(40, 72)) + list(range(0, 32)) + list(range(90, 97)) + list(range(72, 90))
+             + list(range(32, 40)))
+    assert ids[1].tolist() == [1000 + p for p in want1]
