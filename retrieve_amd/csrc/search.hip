@@ -2,10 +2,14 @@
 // query quantization, the int8 scorer over each query's probed clusters, the selection by
 // (key desc, slot asc) and the epilogue id = sort_perm[position], score = dequantized dot.
 //
-// Slots: query row b's probed clusters c_j = probe_ids[b, j] (items at sorted positions
-// cluster_offsets[c_j] .. + cluster_sizes[c_j]) laid end to end in probe order; slot s of the
-// row is the s-th of those items, and ties go to the lower slot. The row holds at most `width`
-// slots (max_tensor_size_per_row rounded up to 32, as the reference's score buffer).
+// Slots: query row b's probed clusters c_j = probe_ids[b, j] hold the items at sorted positions
+// cluster_offsets[c_j] .. + cluster_sizes[c_j]. The row's slots are the reference scorer's write
+// order: the full 32-item warps of every probed cluster in probe order, then every cluster's
+// remaining (< 32) items in probe order (fork_search_cuda.cu:989-991 and :1051-1053;
+// fused_kmean_ann_cuda.cu:592-598 and :443-453). Ties go to the lower slot. The row holds at most
+// `width` slots (max_tensor_size_per_row rounded up to 32, as the reference's score buffer); the
+// reference requires a row's clusters to fit its width, and slots at or past it are dropped here.
+// A filtered-out item keeps its slot (the scorer skips it), so the filter never renumbers slots.
 //
 // Keys: the int32 dot (divisor -1), or the fp16 score fp16(float(dot) / divisor) of the serving
 // path (index_mm_helpers.cuh:48-65), ordered as fp16 values (ties merge distinct dots).
@@ -95,13 +99,16 @@ struct IvfArgs {
   int* list_counts;
 };
 
-// The row's probed ranges: start[j], and prefix[j] = slots before range j (prefix[n] = total,
-// clamped at width). Ranges of invalid clusters, or reaching outside the table, are empty.
+// The row's 2 n_probe slot ranges in slot order: range j < n_probe is probe j's full warps
+// (its first len_j / 32 * 32 items), range n_probe + j probe j's remaining len_j % 32 items.
+// start[r] is range r's first sorted position and prefix[r] the slots before it (prefix[2n] =
+// total, clamped at width). Invalid clusters, or clusters reaching outside the table, are empty.
 __device__ inline int64_t load_ranges(const IvfArgs& a, int64_t b, int64_t* start,
                                       int64_t* prefix) {
   const int tid = threadIdx.x;
-  for (int64_t j = tid; j < a.n_probe; j += blockDim.x) {
-    const int64_t c = a.probe_ids[b * a.n_probe + j];
+  const int64_t np = a.n_probe;
+  for (int64_t j = tid; j < np; j += blockDim.x) {
+    const int64_t c = a.probe_ids[b * np + j];
     int64_t s = 0;
     int64_t len = 0;
     if (c >= 0 && c < a.n_lists) {
@@ -109,19 +116,27 @@ __device__ inline int64_t load_ranges(const IvfArgs& a, int64_t b, int64_t* star
       len = a.cluster_sizes[c];
       if (s < 0 || len < 0 || s > a.N || len > a.N - s) len = 0;
     }
+    const int64_t full = len / 32 * 32;
     start[j] = s;
-    prefix[j + 1] = len;
+    prefix[j + 1] = full;
+    start[np + j] = s + full;
+    prefix[np + j + 1] = len - full;
   }
   __syncthreads();
   if (tid == 0) {
     prefix[0] = 0;
-    for (int64_t j = 0; j < a.n_probe; ++j) {
-      const int64_t t = prefix[j] + prefix[j + 1];
-      prefix[j + 1] = t < a.width ? t : a.width;
+    for (int64_t r = 0; r < 2 * np; ++r) {
+      const int64_t t = prefix[r] + prefix[r + 1];
+      prefix[r + 1] = t < a.width ? t : a.width;
     }
   }
   __syncthreads();
-  return prefix[a.n_probe];
+  return prefix[2 * np];
+}
+
+// LDS bytes of a row's ranges (start[2 n], prefix[2 n + 1]).
+inline size_t ranges_lds(int64_t n_probe) {
+  return static_cast<size_t>(4 * n_probe + 1) * sizeof(int64_t);
 }
 
 // the range holding slot s: the last j with prefix[j] <= s
@@ -149,9 +164,10 @@ template <int L, int NC>
 __global__ void __launch_bounds__(kIvfThreads) ivf_scan_kernel(IvfArgs a) {
   constexpr int R = kWave / L;
   extern __shared__ uint64_t smem[];
+  const int64_t nr = 2 * a.n_probe;  // slot ranges
   int64_t* start = reinterpret_cast<int64_t*>(smem);
-  int64_t* prefix = start + a.n_probe;
-  uint64_t* scratch = reinterpret_cast<uint64_t*>(prefix + a.n_probe + 1);
+  int64_t* prefix = start + nr;
+  uint64_t* scratch = reinterpret_cast<uint64_t*>(prefix + nr + 1);
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid >> 6;
@@ -184,7 +200,7 @@ __global__ void __launch_bounds__(kIvfThreads) ivf_scan_kernel(IvfArgs a) {
     bool ok = s < total;
     int64_t pos = 0;
     if (ok) {
-      const int64_t j = range_of(prefix, a.n_probe, s);
+      const int64_t j = range_of(prefix, nr, s);
       pos = start[j] + (s - prefix[j]);
       if (mrow != nullptr) ok = (mrow[pos >> 6] >> (63 - (pos & 63))) & 1ull;
     }
@@ -244,8 +260,9 @@ struct EpiArgs {
 __global__ void __launch_bounds__(kIvfThreads) search_epilogue_kernel(EpiArgs e) {
   extern __shared__ uint64_t smem[];
   const int64_t b = blockIdx.x;
+  const int64_t nr = e.ranges ? 2 * e.a.n_probe : 0;  // slot ranges
   int64_t* start = reinterpret_cast<int64_t*>(smem);
-  int64_t* prefix = start + (e.ranges ? e.a.n_probe : 0);
+  int64_t* prefix = start + nr;
   if (e.ranges) load_ranges(e.a, b, start, prefix);
   const float qs = e.q_scales[b];
   const float gs = e.global_scale[0];
@@ -256,7 +273,7 @@ __global__ void __launch_bounds__(kIvfThreads) search_epilogue_kernel(EpiArgs e)
     if (x >= 0) {
       int64_t pos = x;
       if (e.ranges) {
-        const int64_t j = range_of(prefix, e.a.n_probe, x);
+        const int64_t j = range_of(prefix, nr, x);
         pos = start[j] + (x - prefix[j]);
       }
       if (pos >= 0 && pos < e.n_perm) {
@@ -389,7 +406,7 @@ extern "C" int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64
   void* raw = ws;
   const int score_kind = divisor == -1 ? kScoreI32 : kScoreF32;
   if (n_probe > 0) {
-    const size_t lds = static_cast<size_t>(2 * n_probe + 1) * sizeof(int64_t) +
+    const size_t lds = ranges_lds(n_probe) +
                        static_cast<size_t>(kIvfWaves) * capw * sizeof(uint64_t) +
                        kIvfWaves * sizeof(int);
     const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(B));
@@ -441,7 +458,7 @@ extern "C" int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64
   e.q_scales = q_scales;
   e.global_scale = global_scale;
   e.divisor = static_cast<int>(divisor);
-  const size_t lds = static_cast<size_t>(2 * n_probe + 1) * sizeof(int64_t);
+  const size_t lds = ranges_lds(n_probe);
   search_epilogue_kernel<<<static_cast<unsigned>(B), kIvfThreads, lds, stream>>>(e);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;

@@ -108,6 +108,32 @@ def test_ties_go_to_the_lower_slot(dev):
     assert np.array_equal(ids, want_ids)
 
 
+def test_slot_order_warps_then_remainders(dev):
+    """The reference GPU scorer's slot order, written out by hand: clusters of 40, 50 and 7
+    equal rows at positions 0, 40 and 90 probed [1, 0, 2] fill slots with cluster 1's full warp
+    (40-71), cluster 0's (0-31), then the remainders in probe order: 72-89, 32-39, 90-96
+    (``fork_search_cuda.cu:989-991``, ``:1051-1053``). Every dot ties, so the top-k is the
+    lowest slots; under a mask a filtered-out doc keeps its slot."""
+    d = 64
+    items = np.full((97, d), 3, np.int8)
+    perm = np.arange(97, dtype=np.int64) + 1000
+    q = np.ones((2, d), np.float32)
+    offs, sizes = np.array([0, 40, 90], np.int64), np.array([40, 50, 7], np.int64)
+    probes = np.array([[1, 0, 2], [1, 0, 2]], np.int64)
+    order = (list(range(40, 72)) + list(range(0, 32)) + list(range(72, 90)) + list(range(32, 40))
+             + list(range(90, 97)))
+    ids, _ = _run(dev, q, probes, offs, sizes, items, perm, 1.0, 97, 97)
+    assert ids[0].tolist() == [1000 + p for p in order]
+    ids, _ = _run(dev, q, probes, offs, sizes, items, perm, 1.0, 70, 97)
+    assert ids[1].tolist() == [1000 + p for p in order[:70]]
+    valid = np.ones((2, 97), bool)
+    valid[:, 40:72:2] = False  # every other doc of cluster 1's warp
+    ids, _ = _run(dev, q, probes, offs, sizes, items, perm, 1.0, 40, 97,
+                  filtering_bit_mask=_t(dev, _pack(valid)))
+    kept = [p for p in order if valid[0, p]]
+    assert ids[0].tolist() == [1000 + p for p in kept[:40]]
+
+
 def test_filters(dev):
     g = rng(105)
     n, d, b, k, c = 30_000, 64, 6, 50, 3
