@@ -43,6 +43,20 @@ int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t* items, int
                       int64_t* out_ids, int32_t* out_scores, void* workspace,
                       size_t workspace_bytes, rt_stream_t stream);
 
+/* rt_int8_scan_topk without a workspace argument: the call allocates nothing (no hipMalloc,
+ * no hipFree, no allocating library routine), so it suits callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid allocation. No
+ * counterpart in the reference. Its scratch is a fixed 160 MiB device array per GPU, held
+ * until the process ends. On a 256-CU part it holds the plan of up to 8192 queries at
+ * k <= 224 and up to 4096 at k <= 480 (the candidate lists take 64 / 128 MiB whatever the
+ * batch); a call whose plan needs more (k > 480 always) returns 1 (invalid argument) before
+ * any launch, as does a null pointer. Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (concurrent streams or threads) race and must be serialized by the caller. Same results
+ * as rt_int8_scan_topk. */
+int rt_int8_scan_topk_noalloc(const int8_t* queries, int64_t B, const int8_t* items, int64_t N,
+                              int64_t D, int64_t k, const uint64_t* mask, int64_t mask_words,
+                              int64_t* out_ids, int32_t* out_scores, rt_stream_t stream);
+
 /* Dense (bf16 / fp16) full-scan top-k: queries [B, D] x items [N, D] of the same 16-bit type
  * (dtype 0 = bf16, 1 = fp16), fp32 accumulation on the matrix cores, top-k by
  * (score desc, index asc) -> ids int64 [B, k], scores float [B, k]. D in {32, 64, 128, 256,

@@ -861,7 +861,10 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
                "queries and items must be 16-byte aligned");
   RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
   if (B == 0) return kOk;
+  RT_CHECK_ARG(out_ids != nullptr && out_scores != nullptr, "out_ids and out_scores are null");
   if (N == 0) return launch_pad(out_ids, out_scores, B, k, score_kind, stream);
+  RT_CHECK_ARG(queries != nullptr && items != nullptr && workspace != nullptr,
+               "queries, items and workspace must not be null");
   int dev = 0;
   int cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) {

@@ -15,6 +15,8 @@
 // by 16 bytes, and read back in the MFMA layout. Tiles are dealt round-robin over all waves of
 // a query group, so the whole GPU streams one contiguous window of the table at a time.
 // Seed pass: the strided sample, read directly in the MFMA layout (rows are not contiguous).
+#include <mutex>
+
 #include "mfma_topk.h"
 #include "profile.h"
 #include "scan_common.h"
@@ -281,7 +283,10 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
                "queries and items must be 16-byte aligned");
   RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
   if (B == 0) return kOk;
+  RT_CHECK_ARG(out_ids != nullptr && out_scores != nullptr, "out_ids and out_scores are null");
   if (N == 0) return launch_pad(out_ids, out_scores, B, k, Op::kind, stream);
+  RT_CHECK_ARG(queries != nullptr && items != nullptr && workspace != nullptr,
+               "queries, items and workspace must not be null");
   const ScanPlan plan = plan_scan(B, N, k, 16, kScanWaves * 16, main_workgroups(), mfma_capw(k),
                                   kScanWaves * kTile);
   if (workspace_bytes < plan.total) {
@@ -363,6 +368,74 @@ extern "C" int rt_int8_scan_topk(const int8_t* queries, int64_t B, const int8_t*
                                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
   return run_mfma_scan<I8Op>(queries, B, items, N, D, k, mask, mask_words, out_ids, out_scores,
                              workspace, workspace_bytes, stream);
+}
+
+// ---- allocation-free int8 scan ------------------------------------------------------------
+//
+// Scratch of rt_int8_scan_topk_noalloc: the candidate lists, their lengths and the seed bounds
+// (the workspace of rt_int8_scan_topk) in a file-scope device array. Each GPU the library runs
+// on holds its own copy until the process ends. The main pass splits a fixed number of
+// workgroups (two per CU) over the 16-query groups, so the lists hardly grow with the batch:
+// on a 256-CU part they take 64 MiB at k <= 224 and 128 MiB at k <= 480, and 160 MiB holds
+// the plan of up to 8192 queries at k <= 224 and 4096 at k <= 480; nothing in it needs clearing
+// (every list length, list entry read and bound is written by the call before it is read).
+constexpr size_t kNoAllocScratchBytes = size_t{160} << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kNoAllocMaxDevices = 64;
+std::once_flag g_scratch_once[kNoAllocMaxDevices];
+void* g_scratch_ptr[kNoAllocMaxDevices];
+hipError_t g_scratch_status[kNoAllocMaxDevices];
+
+// The device address of the current GPU's copy of `scratch`, looked up once per device (with
+// that device current, on its first call). Host code uses only this address: the array's name is
+// a host-side stand-in.
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  RT_CHECK_HIP(hipGetDevice(&dev));
+  RT_CHECK_ARG(dev >= 0 && dev < kNoAllocMaxDevices, "device %d: the allocation-free entry "
+               "point supports devices 0-%d", dev, kNoAllocMaxDevices - 1);
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = p;
+  });
+  if (g_scratch_status[dev] != hipSuccess || g_scratch_ptr[dev] == nullptr) {
+    set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+              hipGetErrorString(g_scratch_status[dev]));
+    return kLaunchFailed;
+  }
+  *out = g_scratch_ptr[dev];
+  return kOk;
+}
+
+}  // namespace
+
+extern "C" int rt_int8_scan_topk_noalloc(const int8_t* queries, int64_t B, const int8_t* items,
+                                         int64_t N, int64_t D, int64_t k, const uint64_t* mask,
+                                         int64_t mask_words, int64_t* out_ids,
+                                         int32_t* out_scores, hipStream_t stream) {
+  RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
+  RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
+               static_cast<long long>(kMaxK), static_cast<long long>(k));
+  RT_CHECK_ARG(B == 0 || (out_ids != nullptr && out_scores != nullptr &&
+                          (N == 0 || (queries != nullptr && items != nullptr))),
+               "queries, items, out_ids and out_scores must not be null");
+  const size_t need = plan_scan(B, N, k, 16, kScanWaves * 16, main_workgroups(), mfma_capw(k),
+                                kScanWaves * kTile)
+                          .total;
+  RT_CHECK_ARG(need <= kNoAllocScratchBytes,
+               "rt_int8_scan_topk_noalloc: B = %lld, N = %lld, k = %lld need %zu bytes of "
+               "scratch, above its fixed %zu bytes (call rt_int8_scan_topk with a workspace)",
+               static_cast<long long>(B), static_cast<long long>(N), static_cast<long long>(k),
+               need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int st = noalloc_scratch(&ws);
+  if (st != kOk) return st;
+  return run_mfma_scan<I8Op>(queries, B, items, N, D, k, mask, mask_words, out_ids, out_scores,
+                             ws, kNoAllocScratchBytes, stream);
 }
 
 extern "C" size_t rt_dense_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {

@@ -75,3 +75,20 @@ def test_workspace_grows_with_batch():
     small = lib.rt_int8_scan_topk_workspace(1, 30_000_000, 512, 100)
     big = lib.rt_int8_scan_topk_workspace(1024, 30_000_000, 512, 100)
     assert 0 < small <= big
+
+
+def test_no_alloc_rejections_need_no_gpu():
+    """The allocation-free int8 scan rejects null pointers, and a plan above its fixed scratch
+    (k = 1000 over 6000 queries of a 1024-row table: 375 MiB), before any device call. The
+    non-null addresses of the second call are placeholders that are never dereferenced."""
+    import torch  # noqa: F401
+
+    from retrieve_amd import _native
+
+    lib = _native.lib()
+    st = lib.rt_int8_scan_topk_noalloc(None, 2, None, 10, 64, 5, None, 0, None, None, None)
+    assert st == 1 and b"must not be null" in lib.rt_last_error()
+    st = lib.rt_int8_scan_topk_noalloc(256, 6000, 512, 1024, 64, 1000, None, 0, 768, 1024, None)
+    assert st == 1 and b"scratch" in lib.rt_last_error()
+    st = lib.rt_int8_scan_topk(None, 2, None, 10, 64, 5, None, 0, None, None, None, 0, None)
+    assert st == 1 and b"null" in lib.rt_last_error()
