@@ -186,6 +186,25 @@ int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, int6
                     int64_t* out_mask, uint8_t* out_bool, void* workspace, size_t workspace_bytes,
                     rt_stream_t stream);
 
+/* The Bloom plans over the probed clusters' columns only: probed cluster i (row i / per_row of a
+ * [rows, per_row] probe table) starts at doc position cluster_starts[i] and spans
+ * column_counts_cumsum[i] - column_counts_cumsum[i - 1] columns (inclusive int32 cumsum) from
+ * column cluster_starts[i] / 64; output word j of that span is row q's plan
+ * (query_plan_index[q], or q) evaluated on its column, in the mask layout. Words from the device
+ * total column_counts_cumsum[n_clusters - 1] up to max_columns are written 0; a plan index or
+ * column outside the plans or the index gives 0. Plans and limits as rt_bloom_search.
+ * Replaces: st::bloom_index_search_batch_return_partial_response[_prepared]
+ *   (silvertorch/.../bloom_index_search.cpp:219-345, 561-601; bloom_index_search_cuda.cu:
+ *   1739-1940). */
+int rt_bloom_search_columns(const uint64_t* words, const int64_t* bundle_b_offsets,
+                            int64_t n_bundles, const int64_t* plan_offsets,
+                            const int8_t* plan_data, int64_t data_bytes, int64_t plan_count,
+                            int64_t max_stack, int64_t k, int64_t hash_k,
+                            const int64_t* cluster_starts, const int32_t* column_counts_cumsum,
+                            int64_t n_clusters, int64_t clusters_per_row,
+                            const int64_t* query_plan_index, int64_t max_columns,
+                            int64_t* out_words, rt_stream_t stream);
+
 /* ---- candidate lists ----------------------------------------------------------------
  *
  * Exact top-k over each query's own candidates: query row b against items
@@ -276,6 +295,34 @@ int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64_t B, const
                   const int64_t* sort_perm, int64_t n_perm, const float* global_scale, int64_t k,
                   int64_t* out_ids, float* out_scores, void* workspace, size_t workspace_bytes,
                   rt_stream_t stream);
+
+/* SilverTorch's raw scorer: every probed doc's score in its slot of a [B, width] buffer.
+ * Row b's probes j hold cluster_length[b, j] docs from cluster_offsets[cluster_ids[b, j]]
+ * (n_offsets entries; an id outside them, or a cluster reaching outside the table, is empty);
+ * the slots are every probe's full 32-doc warps in probe order, then every probe's remaining
+ * docs in probe order, the first `width` of them. A written slot holds the score and the doc's
+ * position (int32 out_indices); a slot past the row's docs or whose doc fails the filter holds the
+ * score type's lowest value (INT32_MIN, fp16 -65504, bf16 / fp32 -max) and invalid_index.
+ * elem: 0 int8 (queries and embeddings int8 [., D]), 1 bf16, 2 fp16, 3 fp32. Scores: int8 ->
+ * int32 dot; int8 with divisor != -1 -> fp16(float(dot) / divisor); int8 with
+ * per_embedding_scale (fp16 [N], taking precedence) -> fp16(float(fp16(dot)) / scale[doc]);
+ * float rows -> the fp32-accumulated dot rounded to the row type. Filters (one at most): `mask`
+ * [mask_rows, mask_words] in the mask layout over positions, row mask_index[b] (or b); or the
+ * partial masks of rt_bloom_search_columns: entry e = mask_row * n_probe + j covers probe j's
+ * docs from bit partial_first_offsets[e] of words partial_counts_cumsum[e - 1] ... D * element
+ * size a multiple of 16, at most 8192 bytes; n_probe <= 1024; N < 2**31.
+ * Replaces: st::fused_kmean_ann / st::fused_kmean_ann_with_partial_masks
+ *   (silvertorch/.../fused_kmean_ann_cuda.cu:2126-2501; schemas fused_kmean_ann.cpp:420-460). */
+int rt_fused_kmean_ann(const void* queries, const void* embeddings, int elem, int64_t B,
+                       int64_t N, int64_t D, const int64_t* cluster_offsets, int64_t n_offsets,
+                       const int64_t* cluster_ids, const int64_t* cluster_length,
+                       int64_t n_probe, int64_t width, const uint64_t* mask, int64_t mask_rows,
+                       int64_t mask_words, const int64_t* mask_index,
+                       const int32_t* partial_counts_cumsum, const int8_t* partial_first_offsets,
+                       const uint64_t* partial_words, int64_t partial_entries,
+                       int64_t partial_n_words, int64_t divisor,
+                       const uint16_t* per_embedding_scale, int64_t invalid_index,
+                       void* out_scores, int32_t* out_indices, rt_stream_t stream);
 
 /* The search epilogue alone, for a one-list search run as a full scan: ids [B, k] hold item
  * positions (-1 empty) and become sort_perm[position]; raw_dots [B, k] int32 -> out_scores. */

@@ -362,3 +362,32 @@ def sets_to_expression(query_sets_row: np.ndarray) -> str:
         if vs:
             parts.append("(" + " OR ".join(f"{ci}:{v}" for v in vs) + ")")
     return " AND ".join(parts)
+
+
+def bloom_partial_response(plan_columns: np.ndarray, starts: np.ndarray, lengths: np.ndarray,
+                           plan_index=None):
+    """The Bloom search over the probed clusters' columns only
+    (``bloom_index_search_batch_return_partial_response``, ``bloom_index_search.cpp:219-345``):
+    for each (row q, probe c) of ``starts`` / ``lengths [B, P]`` (doc positions), its columns
+    ``start // 64 ..`` + ``ceil((len + start % 64) / 64)`` (0 when ``len == 0``) evaluated with
+    plan ``plan_index[q]`` (or ``q``). ``plan_columns [plans, n_cols]`` are each plan's column
+    words over the whole index (the full search's output). Returns ``(column_counts_cumsum
+    int32 [B * P], first_item_offsets int8 [B * P], words int64 [total])``."""
+    cols = np.asarray(plan_columns).view(np.uint64)
+    st = np.asarray(starts, np.int64)
+    ln = np.asarray(lengths, np.int64)
+    b, p = st.shape
+    counts, firsts, words = [], [], []
+    acc = 0
+    for q in range(b):
+        plan = q if plan_index is None else int(plan_index[q])
+        for c in range(p):
+            s, n = int(st[q, c]), int(ln[q, c])
+            off = s % 64
+            cnt = (n + off + 63) // 64 if n > 0 else 0
+            acc += cnt
+            counts.append(acc)
+            firsts.append(off)
+            words.extend(cols[plan, s // 64 : s // 64 + cnt].tolist())
+    return (np.array(counts, np.int32), np.array(firsts, np.int8),
+            np.array(words, np.uint64).view(np.int64))

@@ -90,6 +90,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rt_search_epilogue": (
         _c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p],
     ),
+    "rt_bloom_search_columns": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p,
+         _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p],
+    ),
+    "rt_fused_kmean_ann": (
+        _c_int,
+        [_c_p, _c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64,
+         _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
+         _c_p, _c_p, _c_p],
+    ),
     "rt_int8_scan_topk_noalloc": (
         _c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p],
     ),

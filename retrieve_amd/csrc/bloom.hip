@@ -820,6 +820,74 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
 //
 // Lane <-> column, the evaluation stack in LDS ([max_stack][256] words), positions resolved
 // from the stored hashes per column.
+
+// Plan b over column col (< nb * 32) with this lane's stack column stk[s * kBloomThreads + tid]:
+// the post-order evaluation of bloom_index_search_cuda.cu:471-534 / bloom_index_search.cpp:
+// 88-166; a malformed plan, or one needing more than max_stack slots, matches nothing.
+__device__ inline uint64_t stack_eval(const BloomSearchArgs& a, int64_t b, int64_t col,
+                                      uint64_t* stk, int tid) {
+  const int64_t beta = col / kBloomWordsPerBundle;
+  const int j = static_cast<int>(col % kBloomWordsPerBundle);
+  const int64_t off = a.bundle_off[beta];
+  const int64_t w = a.bundle_off[beta + 1] - off;
+  const uint64_t* wcol = a.words + off * kBloomWordsPerBundle + j;  // position p at wcol[32 p]
+  const int64_t* o = a.plan_offsets + 8 * b;
+  // a malformed plan evaluates to no match instead of reading out of bounds
+  bool bad = !plan_ok(o, a.data_bytes);
+  const uint8_t* ops = reinterpret_cast<const uint8_t*>(a.data + o[0]);
+  const int64_t n_ops = bad ? 0 : o[1] - o[0];
+  const int32_t* offs = reinterpret_cast<const int32_t*>(a.data + o[2]);
+  const int64_t n_offs = (o[3] - o[2]) / 4;
+  const int64_t h0 = o[6] / 8;
+  const int64_t nh = (o[7] - o[6]) / 8;
+  int sp = 0;
+  int64_t term = 0;
+  for (int64_t i = 0; i < n_ops && !bad; ++i) {
+    const uint8_t op = ops[i];
+    uint64_t r = 0ull;
+    if (op == kOpTerm) {
+      if ((term + 1) * a.hash_k > nh) {
+        bad = true;
+        break;
+      }
+      r = term_from_hashes(a, h0, term, wcol, w);
+      ++term;
+    } else if (op == kOpAnd || op == kOpOr) {
+      if (i + 1 >= n_offs) {
+        bad = true;
+        break;
+      }
+      const int n = offs[i + 1] - offs[i];  // children on the stack
+      if (n < 1 || n > sp) {
+        bad = true;
+        break;
+      }
+      r = op == kOpAnd ? ~0ull : 0ull;
+      for (int q = 0; q < n; ++q) {
+        const uint64_t x = stk[(--sp) * kBloomThreads + tid];
+        r = op == kOpAnd ? (r & x) : (r | x);
+      }
+    } else if (op == kOpNot) {
+      if (sp < 1) {
+        bad = true;
+        break;
+      }
+      r = ~stk[(--sp) * kBloomThreads + tid];
+    } else if (op == kOpEmpty) {
+      r = ~0ull;
+    } else {
+      bad = true;
+      break;
+    }
+    if (sp >= a.max_stack) {
+      bad = true;
+      break;
+    }
+    stk[(sp++) * kBloomThreads + tid] = r;
+  }
+  return (!bad && sp == 1) ? stk[tid] : 0ull;
+}
+
 __global__ void __launch_bounds__(kBloomThreads) bloom_search_kernel(BloomSearchArgs a) {
   extern __shared__ uint64_t stk[];  // [max_stack][kBloomThreads]
   const int tid = threadIdx.x;
@@ -832,70 +900,62 @@ __global__ void __launch_bounds__(kBloomThreads) bloom_search_kernel(BloomSearch
   const int64_t ncol = a.nb * kBloomWordsPerBundle;
   const int64_t col = static_cast<int64_t>(blockIdx.x) * kBloomThreads + tid;
   const bool valid = col < ncol;
-  const int64_t beta = valid ? col / kBloomWordsPerBundle : 0;
-  const int j = static_cast<int>(col % kBloomWordsPerBundle);
-  const int64_t off = a.bundle_off[beta];
-  const int64_t w = a.bundle_off[beta + 1] - off;
-  const uint64_t* wcol = a.words + off * kBloomWordsPerBundle + j;  // position p at wcol[32 p]
-
   for (int64_t b = b0; b < b1; ++b) {
     if (a.hdr[4 * b] != kPlanStack) continue;  // the column kernel writes it
-    const int64_t* o = a.plan_offsets + 8 * b;
-    // a malformed plan evaluates to no match instead of reading out of bounds
-    bool bad = !plan_ok(o, a.data_bytes);
-    const uint8_t* ops = reinterpret_cast<const uint8_t*>(a.data + o[0]);
-    const int64_t n_ops = bad ? 0 : o[1] - o[0];
-    const int32_t* offs = reinterpret_cast<const int32_t*>(a.data + o[2]);
-    const int64_t n_offs = (o[3] - o[2]) / 4;
-    const int64_t h0 = o[6] / 8;
-    const int64_t nh = (o[7] - o[6]) / 8;
-    int sp = 0;
-    int64_t term = 0;
-    for (int64_t i = 0; i < n_ops && !bad; ++i) {
-      const uint8_t op = ops[i];
-      uint64_t r = 0ull;
-      if (op == kOpTerm) {
-        if ((term + 1) * a.hash_k > nh) {
-          bad = true;
-          break;
-        }
-        r = term_from_hashes(a, h0, term, wcol, w);
-        ++term;
-      } else if (op == kOpAnd || op == kOpOr) {
-        if (i + 1 >= n_offs) {
-          bad = true;
-          break;
-        }
-        const int n = offs[i + 1] - offs[i];  // children on the stack
-        if (n < 1 || n > sp) {
-          bad = true;
-          break;
-        }
-        r = op == kOpAnd ? ~0ull : 0ull;
-        for (int q = 0; q < n; ++q) {
-          const uint64_t x = stk[(--sp) * kBloomThreads + tid];
-          r = op == kOpAnd ? (r & x) : (r | x);
-        }
-      } else if (op == kOpNot) {
-        if (sp < 1) {
-          bad = true;
-          break;
-        }
-        r = ~stk[(--sp) * kBloomThreads + tid];
-      } else if (op == kOpEmpty) {
-        r = ~0ull;
-      } else {
-        bad = true;
-        break;
-      }
-      if (sp >= a.max_stack) {
-        bad = true;
-        break;
-      }
-      stk[(sp++) * kBloomThreads + tid] = r;
-    }
-    const uint64_t res = (!bad && sp == 1) ? stk[tid] : 0ull;
+    const uint64_t res = stack_eval(a, b, valid ? col : 0, stk, tid);
     if (valid) write_column(a, b, ncol, col, res);
+  }
+}
+
+// ---- the plans over the probed clusters' columns only ----------------------------------
+//
+// bloom_index_search_batch_return_partial_response (bloom_index_search_cuda.cu:1739-1940,
+// bloom_index_search.cpp:219-345): probed cluster i (row i / per_row of a [rows, per_row]
+// probe table) starting at doc position starts[i] spans columns starts[i] / 64 .. + its column
+// count; output word j (cumsum[i - 1] <= j < cumsum[i], cumsum inclusive) is row q's plan
+// (plan_index[q], or q) evaluated on column starts[i] / 64 + j - cumsum[i - 1]. Words at or past
+// the device total cumsum[n - 1] (up to max_columns) are 0. A plan index or column outside the
+// plans or the index gives 0. Lane <-> output word, each with its own plan and stack column.
+struct BloomColumnsArgs {
+  BloomSearchArgs s;
+  const int64_t* starts;   // [n_clusters] first doc positions
+  const int32_t* cumsum;   // [n_clusters] inclusive column counts
+  int64_t n_clusters;
+  int64_t per_row;
+  const int64_t* plan_index;  // [rows] or null
+  int64_t max_columns;
+  int64_t* out;  // [max_columns]
+};
+
+__global__ void __launch_bounds__(kBloomThreads) bloom_columns_kernel(BloomColumnsArgs a) {
+  extern __shared__ uint64_t stk[];  // [max_stack][kBloomThreads]
+  const int tid = threadIdx.x;
+  const int64_t total = a.n_clusters > 0 ? a.cumsum[a.n_clusters - 1] : 0;
+  const int64_t ncol = a.s.nb * kBloomWordsPerBundle;
+  for (int64_t j = static_cast<int64_t>(blockIdx.x) * kBloomThreads + tid; j < a.max_columns;
+       j += static_cast<int64_t>(gridDim.x) * kBloomThreads) {
+    uint64_t res = 0ull;
+    if (j < total) {
+      int64_t lo = 0;
+      int64_t hi = a.n_clusters - 1;
+      while (lo < hi) {  // the first cluster whose inclusive count passes j
+        const int64_t mid = (lo + hi) >> 1;
+        if (static_cast<int64_t>(a.cumsum[mid]) > j) {
+          hi = mid;
+        } else {
+          lo = mid + 1;
+        }
+      }
+      const int64_t first = lo == 0 ? 0 : static_cast<int64_t>(a.cumsum[lo - 1]);
+      const int64_t start = a.starts[lo];
+      const int64_t col = (start >= 0 ? start / 64 : -1) + (j - first);
+      const int64_t q = lo / a.per_row;
+      const int64_t b = a.plan_index != nullptr ? a.plan_index[q] : q;
+      if (start >= 0 && col < ncol && b >= 0 && b < a.s.plan_count) {
+        res = stack_eval(a.s, b, col, stk, tid);
+      }
+    }
+    a.out[j] = static_cast<int64_t>(res);
   }
 }
 
@@ -1052,6 +1112,68 @@ extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_of
   }
   bloom_search_kernel<<<dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)),
                         kBloomThreads, lds, stream>>>(a);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+extern "C" int rt_bloom_search_columns(const uint64_t* words, const int64_t* bundle_b_offsets,
+                                       int64_t n_bundles, const int64_t* plan_offsets,
+                                       const int8_t* plan_data, int64_t data_bytes,
+                                       int64_t plan_count, int64_t max_stack, int64_t k,
+                                       int64_t hash_k, const int64_t* cluster_starts,
+                                       const int32_t* column_counts_cumsum, int64_t n_clusters,
+                                       int64_t clusters_per_row, const int64_t* query_plan_index,
+                                       int64_t max_columns, int64_t* out_words,
+                                       hipStream_t stream) {
+  RT_CHECK_ARG(n_bundles >= 0 && plan_count >= 0 && data_bytes >= 0 && n_clusters >= 0 &&
+                   max_columns >= 0,
+               "sizes must be >= 0");
+  RT_CHECK_ARG(k >= 1 && k <= kBloomMaxK, "k must be in [1, %d], got %lld", kBloomMaxK,
+               static_cast<long long>(k));
+  RT_CHECK_ARG(hash_k >= 1 && hash_k <= 64, "hash_k must be in [1, 64], got %lld",
+               static_cast<long long>(hash_k));
+  RT_CHECK_ARG(max_stack >= 1 && max_stack <= kBloomMaxStack,
+               "max_stack_size must be in [1, %d], got %lld", kBloomMaxStack,
+               static_cast<long long>(max_stack));
+  RT_CHECK_ARG(clusters_per_row >= 1, "clusters_per_row must be >= 1");
+  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(plan_data) % 8 == 0, "plan data must be 8-aligned");
+  if (max_columns == 0) return kOk;
+  RT_CHECK_ARG(out_words != nullptr, "out_words must not be null");
+  // (no clusters, bundles or plans: the kernel writes the zeros, no memset, so a captured
+  // graph holds kernels only)
+  RT_CHECK_ARG(n_clusters == 0 || (cluster_starts != nullptr && column_counts_cumsum != nullptr),
+               "cluster_starts and column_counts_cumsum must not be null");
+  RT_CHECK_ARG(n_bundles == 0 || plan_count == 0 ||
+                   (words != nullptr && bundle_b_offsets != nullptr && plan_offsets != nullptr &&
+                    plan_data != nullptr),
+               "the index and the plans must not be null");
+  BloomColumnsArgs a{};
+  a.s.words = words;
+  a.s.bundle_off = bundle_b_offsets;
+  a.s.nb = n_bundles;
+  a.s.plan_offsets = plan_offsets;
+  a.s.data = plan_data;
+  a.s.data_bytes = data_bytes;
+  a.s.plan_count = plan_count;
+  a.s.max_stack = static_cast<int>(max_stack);
+  a.s.k = static_cast<int>(k);
+  a.s.hash_k = static_cast<int>(hash_k);
+  a.starts = cluster_starts;
+  a.cumsum = column_counts_cumsum;
+  a.n_clusters = n_clusters;
+  a.per_row = clusters_per_row;
+  a.plan_index = query_plan_index;
+  a.max_columns = max_columns;
+  a.out = out_words;
+  int64_t grid = cdiv(max_columns, kBloomThreads);
+  grid = grid < 4096 ? grid : 4096;
+  const size_t lds = static_cast<size_t>(max_stack) * kBloomThreads * sizeof(uint64_t);
+  if (lds > 64 * 1024) {
+    RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&bloom_columns_kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds)));
+  }
+  bloom_columns_kernel<<<static_cast<unsigned>(grid), kBloomThreads, lds, stream>>>(a);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }

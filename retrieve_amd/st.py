@@ -1,8 +1,14 @@
-"""The ``torch.ops.st.*`` surface (SilverTorch's op namespace) on the HIP library: the Bloom
-index build, the expression parser and the Bloom plan search, with the reference's schemas
-(``silvertorch/.../ops/csrc/bloom_indexer.cpp:117-136``, ``expression_query_parser.cpp:457-465``,
-``bloom_index_search.cpp:551-590``). Importing this module registers them (as loading the
-reference's extension does); ``import retrieve_amd`` registers nothing.
+"""The ``torch.ops.st.*`` surface (SilverTorch's op namespace) on the HIP library, with the
+reference's schemas: the raw scorer ``fused_kmean_ann`` (``+ _with_partial_masks``,
+``silvertorch/.../ops/csrc/fused_kmean_ann.cpp:420-460``), the Bloom index build, the expression
+parser, the Bloom plan search over every column or over the probed clusters' columns only
+(``bloom_indexer.cpp:117-136``, ``expression_query_parser.cpp:457-465``,
+``bloom_index_search.cpp:551-601``), ``search`` and ``probe_prep`` (``fork_search.cpp:13-49``).
+Every op has a fake (``silvertorch/silvertorch/ops/_fake.py:26-219``), so forwards trace whole
+under ``torch.compile``. Importing this module registers them (as loading the reference's
+extension does); ``import retrieve_amd`` registers nothing. The reference's loader
+(``retrieve/src/retrieve/ops/official/__init__.py:46-54, 161-167``) accepts the namespace: it
+holds every one of its ``REQUIRED_OPS``.
 
 The parser's plan bytes are this library's own encoding (``retrieve_amd.bloom``), read only by
 the searches here; the index words follow the reference's bundle layout bit for bit.
@@ -62,6 +68,17 @@ def _parse(expressions, silvertorch_ks, bloom_hash_k, return_query_plan=True, ma
 
 
 _LIB.impl("parse_expression_query_batch", _parse, "CompositeExplicitAutograd")
+
+
+@torch.library.register_fake("st::parse_expression_query_batch")
+def _(expressions, silvertorch_ks, bloom_hash_k, return_query_plan=True, max_sub_queries=5):
+    # the parse depends on the strings and ints only: its shapes are the real parse's
+    from torch._subclasses.fake_tensor import unset_fake_temporarily
+
+    with unset_fake_temporarily():
+        stack, tensors = _parse(expressions, None, bloom_hash_k, return_query_plan,
+                                max_sub_queries)
+    return stack, [silvertorch_ks.new_empty(t.shape, dtype=t.dtype) for t in tensors]
 
 
 # --- build ----------------------------------------------------------------------------------
@@ -138,6 +155,15 @@ def _build_upstream(feature_ids, feature_offsets, feature_values, b_multiplier, 
 
 _LIB.impl("bloom_index_build_fixed", _build_fixed, "CUDA")
 _LIB.impl("bloom_index_build", _build_upstream, "CUDA")
+
+
+@torch.library.register_fake("st::bloom_index_build")
+def _(feature_ids, feature_offsets, feature_values, b_multiplier, k, fast_build=False):
+    # the words depend on the bundles' term counts: a size known only after the build
+    n = (feature_offsets.shape[0] - 1) // feature_ids.shape[0]
+    words = torch.library.get_ctx().new_dynamic_size()
+    return (feature_values.new_empty((words,), dtype=torch.int64),
+            feature_values.new_empty((-(-n // DOCS_PER_BUNDLE) + 1,), dtype=torch.int64))
 
 
 @torch.library.register_fake("st::bloom_index_build_fixed")
@@ -235,6 +261,324 @@ def _search_batch(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data,
 
 _LIB.impl("bloom_index_search_batch_prepared", _search_prepared, "CUDA")
 _LIB.impl("bloom_index_search_batch", _search_batch, "CUDA")
+
+
+@torch.library.register_fake("st::bloom_index_search_batch")
+def _(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data, bloom_query_plans_offsets, k,
+      hash_k, return_bool_mask=True):
+    plans = bloom_query_plans_offsets.shape[0] // 8
+    cols = (bloom_bundle_b_offsets.shape[0] - 1) * WORDS_PER_BUNDLE
+    if return_bool_mask:
+        return bloom_index.new_empty((plans, cols * 64), dtype=torch.bool)
+    return bloom_index.new_empty((plans, cols), dtype=torch.int64)
+
+
+# --- Bloom plans over the probed clusters' columns (bloom_index_search.cpp:219-345, 561-601) ---
+
+_LIB.define(
+    "bloom_index_search_batch_return_partial_response(Tensor bloom_index, "
+    "Tensor bloom_bundle_b_offsets, Tensor bloom_query_plans_data, "
+    "Tensor bloom_query_plans_offsets, Tensor selected_cluster_offsets, "
+    "Tensor selected_cluster_lengths, int k, int hash_k, Tensor? query_plan_index=None) "
+    "-> (Tensor, Tensor, Tensor)"
+)
+_LIB.define(
+    "bloom_index_search_batch_return_partial_response_prepared(Tensor bloom_index, "
+    "Tensor bloom_bundle_b_offsets, Tensor plans, int plan_count, int max_stack_size, "
+    "Tensor selected_cluster_offsets, Tensor selected_cluster_lengths, int k, int hash_k, "
+    "Tensor? query_plan_index, int max_columns) -> (Tensor, Tensor, Tensor)"
+)
+
+
+def _column_info(starts: Tensor, lengths: Tensor, plan_count: int,
+                 query_plan_index: Tensor | None) -> tuple[Tensor, Tensor, Tensor]:
+    """``(column_counts_cumsum int32 [B·P], first_item_offsets int8 [B·P], starts int64)`` of the
+    probed clusters (``generate_column_info_for_clusters``, ``bloom_index_search.cpp:447-490``):
+    cluster (q, c) starting ``start % 64`` docs into its first 64-doc column spans
+    ``ceil((len + start % 64) / 64)`` columns, none when it is empty."""
+    if starts.dim() != 2 or lengths.dim() != 2:
+        raise RuntimeError("selected_cluster_offsets and selected_cluster_lengths must be 2-D")
+    if starts.dtype != torch.int64 or lengths.dtype != torch.int64:
+        raise RuntimeError("selected_cluster_offsets and selected_cluster_lengths must be int64")
+    if starts.shape != lengths.shape:
+        raise RuntimeError("selected_cluster_offsets must have the shape of "
+                           "selected_cluster_lengths")
+    if query_plan_index is not None:
+        if query_plan_index.dim() != 1 or query_plan_index.shape[0] != starts.shape[0]:
+            raise RuntimeError("query_plan_index must be [B]")
+    elif plan_count != starts.shape[0]:
+        raise RuntimeError("without query_plan_index there must be one plan per row")
+    starts = starts.contiguous()
+    off = torch.remainder(starts, 64)
+    counts = torch.where(lengths > 0, torch.div(lengths + off + 63, 64, rounding_mode="floor"),
+                         torch.zeros_like(lengths))
+    return (counts.reshape(-1).cumsum(0).to(torch.int32), off.reshape(-1).to(torch.int8),
+            starts.reshape(-1))
+
+
+def _columns(bloom_index, offsets, plan_offsets, data, data_bytes, plan_count, max_stack, k,
+             hash_k, starts, cumsum, per_row, query_plan_index, max_columns) -> Tensor:
+    dev = nat.require_device(bloom_index, offsets, plan_offsets, data, starts)
+    if bloom_index.dtype != torch.int64 or offsets.dtype != torch.int64:
+        raise TypeError("bloom_index and bloom_bundle_b_offsets must be int64")
+    out = torch.empty((max_columns,), dtype=torch.int64, device=dev)
+    if max_columns == 0:
+        return out
+    qpi = None if query_plan_index is None else query_plan_index.to(torch.int64).contiguous()
+    with torch.cuda.device(dev):
+        st = nat.lib().rt_bloom_search_columns(
+            nat.ptr(bloom_index), nat.ptr(offsets), offsets.numel() - 1, nat.ptr(plan_offsets),
+            nat.ptr(data), data_bytes, plan_count, max(1, min(int(max_stack), MAX_STACK)), k,
+            hash_k, nat.ptr(starts), nat.ptr(cumsum), starts.numel(), max(1, per_row),
+            nat.ptr(qpi), max_columns, nat.ptr(out), nat.stream(dev))
+    nat.check(st)
+    return out
+
+
+def _partial_response(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data,
+                      bloom_query_plans_offsets, selected_cluster_offsets,
+                      selected_cluster_lengths, k, hash_k, query_plan_index=None):
+    """Plans as the parser returns them; the output's length is the probed columns' total, so
+    this form reads it back (as the reference's ``repeat_interleave`` does,
+    ``bloom_index_search_cuda.cu:1755-1760``); the ``_prepared`` form does not."""
+    dev = bloom_index.device
+    offs = bloom_query_plans_offsets.to(torch.int64).contiguous()
+    if offs.numel() % 8:
+        raise ValueError("bloom_query_plans_offsets must hold 8 offsets per plan")
+    data = bloom_query_plans_data.contiguous()
+    max_stack = MAX_STACK
+    if data.device.type == "cpu" and offs.device.type == "cpu":
+        max_stack = _max_stack(data.numpy().view(np.uint8), offs.numpy())
+        if max_stack > MAX_STACK:
+            raise ValueError(f"plans need a stack of {max_stack} (> {MAX_STACK})")
+    plan_count = offs.numel() // 8
+    cumsum, first, starts = _column_info(selected_cluster_offsets.to(dev),
+                                         selected_cluster_lengths.to(dev), plan_count,
+                                         query_plan_index)
+    total = int(cumsum[-1].item()) if cumsum.numel() else 0
+    nbytes = data.numel()
+    dev_data = torch.zeros((nbytes + 7) // 8, dtype=torch.int64, device=dev)
+    if nbytes:
+        dev_data.view(torch.uint8)[:nbytes].copy_(data.view(torch.uint8).to(dev))
+    words = _columns(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), offs.to(dev),
+                     dev_data, nbytes, plan_count, max_stack, int(k), int(hash_k), starts, cumsum,
+                     selected_cluster_lengths.shape[1], query_plan_index, total)
+    return cumsum, first, words
+
+
+def _partial_response_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count,
+                               max_stack_size, selected_cluster_offsets, selected_cluster_lengths,
+                               k, hash_k, query_plan_index, max_columns):
+    """Prepared plans, no host sync: ``column_mask_response`` has the caller's static capacity
+    ``max_columns``; its words past the probed columns' total are 0
+    (``bloom_index_search_cuda.cu:1857-1940``)."""
+    if plans.dtype != torch.int64 or plans.dim() != 1 or plans.numel() < 8 * plan_count:
+        raise ValueError("plans must be int64 [8 * plan_count + data words]")
+    if max_stack_size > MAX_STACK:
+        raise ValueError(f"max_stack_size must be <= {MAX_STACK}")
+    if max_columns < 0:
+        raise ValueError("max_columns must be >= 0")
+    plans = plans.contiguous()
+    data = plans[8 * plan_count :]
+    cumsum, first, starts = _column_info(selected_cluster_offsets, selected_cluster_lengths,
+                                         int(plan_count), query_plan_index)
+    words = _columns(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), plans, data,
+                     data.numel() * 8, int(plan_count), int(max_stack_size), int(k), int(hash_k),
+                     starts, cumsum, selected_cluster_lengths.shape[1], query_plan_index,
+                     int(max_columns))
+    return cumsum, first, words
+
+
+_LIB.impl("bloom_index_search_batch_return_partial_response", _partial_response, "CUDA")
+_LIB.impl("bloom_index_search_batch_return_partial_response_prepared",
+          _partial_response_prepared, "CUDA")
+
+
+@torch.library.register_fake("st::bloom_index_search_batch_return_partial_response")
+def _(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data, bloom_query_plans_offsets,
+      selected_cluster_offsets, selected_cluster_lengths, k, hash_k, query_plan_index=None):
+    clusters = selected_cluster_lengths.numel()
+    columns = torch.library.get_ctx().new_dynamic_size()
+    return (bloom_index.new_empty((clusters,), dtype=torch.int32),
+            bloom_index.new_empty((clusters,), dtype=torch.int8),
+            bloom_index.new_empty((columns,), dtype=torch.int64))
+
+
+@torch.library.register_fake("st::bloom_index_search_batch_return_partial_response_prepared")
+def _(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max_stack_size,
+      selected_cluster_offsets, selected_cluster_lengths, k, hash_k, query_plan_index,
+      max_columns):
+    clusters = selected_cluster_lengths.numel()
+    return (bloom_index.new_empty((clusters,), dtype=torch.int32),
+            bloom_index.new_empty((clusters,), dtype=torch.int8),
+            bloom_index.new_empty((max_columns,), dtype=torch.int64))
+
+
+# --- the raw scorer (fused_kmean_ann.cpp:420-460; fused_kmean_ann_cuda.cu:2126-2501) ---------
+
+_LIB.define(
+    "fused_kmean_ann(Tensor cluster_offsets, Tensor cluster_ids, Tensor cluster_length, "
+    "Tensor embeddings, Tensor queries, int max_tensor_size_per_row, "
+    "Tensor? filtering_bit_mask=None, int invalid_index_value=-1, int divisor_for_int8=-1, "
+    "Tensor? filtering_bit_index=None, Tensor? per_embedding_scale=None) -> (Tensor, Tensor)"
+)
+_LIB.define(
+    "fused_kmean_ann_with_partial_masks(Tensor cluster_offsets, Tensor cluster_ids, "
+    "Tensor cluster_length, Tensor embeddings, Tensor queries, int max_tensor_size_per_row, "
+    "Tensor partial_mask_column_counts_cumsum, Tensor partial_mask_first_item_offset_in_column, "
+    "Tensor partial_mask_column_results, int invalid_index_value=-1, int divisor_for_int8=-1, "
+    "Tensor? filtering_bit_index=None, Tensor? per_embedding_scale=None, "
+    "Tensor? cluster_warp_size=None, Tensor? cluster_warp_rounded_length_cumsum=None, "
+    "Tensor? cluster_remaining_length_cumsum=None, Tensor? cluster_warp_size_cumsum=None, "
+    "int total_cluster_rounded_warps=0, int total_cluster_remaining_warps=0) -> (Tensor, Tensor)"
+)
+
+_ELEM = {torch.int8: 0, torch.bfloat16: 1, torch.float16: 2, torch.float32: 3}
+
+
+def _score_dtype(emb_dtype, divisor_for_int8, has_scale):
+    """int8 rows: int32, or fp16 with a divisor or per-doc scales; else the rows' dtype
+    (``fused_kmean_ann.cpp:30-41``)."""
+    if emb_dtype != torch.int8:
+        return emb_dtype
+    return torch.float16 if (divisor_for_int8 != -1 or has_scale) else torch.int32
+
+
+def _kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+               max_tensor_size_per_row, invalid_index_value, divisor_for_int8,
+               filtering_bit_index, per_embedding_scale, mask=None, partial=None):
+    for name, t, dim in (("cluster_offsets", cluster_offsets, 1), ("cluster_ids", cluster_ids, 2),
+                         ("cluster_length", cluster_length, 2), ("embeddings", embeddings, 2),
+                         ("queries", queries, 2)):
+        if t.dim() != dim:
+            raise RuntimeError(f"{name} must be {dim}-D")
+    if cluster_ids.shape != cluster_length.shape or cluster_ids.shape[0] != queries.shape[0]:
+        raise RuntimeError("cluster_ids and cluster_length must be [B, n_probe] with B query rows")
+    if embeddings.shape[1] != queries.shape[1]:
+        raise RuntimeError("embeddings and queries must have the same D")
+    if embeddings.dtype not in _ELEM or queries.dtype != embeddings.dtype:
+        raise RuntimeError("embeddings and queries must be int8, bfloat16, float16 or float32 "
+                           "of one dtype")
+    if not embeddings.is_contiguous():
+        raise RuntimeError("embeddings must be contiguous")
+    b, p = cluster_ids.shape
+    n, d = embeddings.shape
+    dev = nat.require_device(cluster_offsets, cluster_ids, cluster_length, embeddings, queries)
+    scale = None
+    if per_embedding_scale is not None:
+        if per_embedding_scale.dim() != 1 or per_embedding_scale.shape[0] != n or \
+                per_embedding_scale.dtype != torch.float16:
+            raise RuntimeError("per_embedding_scale must be float16 [N]")
+        scale = per_embedding_scale.contiguous()
+    index = None
+    if filtering_bit_index is not None:
+        if filtering_bit_index.dim() != 1 or filtering_bit_index.shape[0] != b:
+            raise RuntimeError("filtering_bit_index must be [B]")
+        index = filtering_bit_index.to(torch.int64).contiguous()
+    if mask is not None:
+        if mask.dtype != torch.int64 or mask.dim() != 2:
+            raise RuntimeError("filtering_bit_mask must be int64 [rows, ceil(N/64)]")
+        if index is None and mask.shape[0] != b:
+            raise RuntimeError("filtering_bit_mask must have B rows without filtering_bit_index")
+        if mask.shape[1] < (n + 63) // 64:
+            raise RuntimeError("filtering_bit_mask must cover every doc (ceil(N/64) words)")
+        mask = mask.contiguous()
+    width = (int(max_tensor_size_per_row) + 31) // 32 * 32
+    dtype = _score_dtype(embeddings.dtype, divisor_for_int8, scale is not None)
+    scores = torch.empty((b, width), dtype=dtype, device=dev)
+    idx = torch.empty((b, width), dtype=torch.int32, device=dev)
+    cum = first = words = None
+    if partial is not None:
+        cum, first, words = partial
+        if cum.dim() != 1 or first.dim() != 1 or words.dim() != 1 or \
+                cum.shape[0] != first.shape[0]:
+            raise RuntimeError("the partial masks must be 1-D, the counts and offsets of one "
+                               "length")
+        if words.dtype != torch.int64 or cum.dtype != torch.int32 or first.dtype != torch.int8:
+            raise RuntimeError("partial masks: int32 counts, int8 offsets, int64 words")
+        if index is None and first.shape[0] != b * p:
+            raise RuntimeError("partial masks must hold one entry per (row, probe)")
+        cum, first, words = cum.contiguous(), first.contiguous(), words.contiguous()
+    offs = cluster_offsets.to(torch.int64).contiguous()
+    ids = cluster_ids.to(torch.int64).contiguous()
+    lens = cluster_length.to(torch.int64).contiguous()
+    q = queries.contiguous()
+    with torch.cuda.device(dev):
+        st = nat.lib().rt_fused_kmean_ann(
+            nat.ptr(q), nat.ptr(embeddings), _ELEM[embeddings.dtype], b, n, d, nat.ptr(offs),
+            offs.numel(), nat.ptr(ids), nat.ptr(lens), p, width, nat.ptr(mask),
+            0 if mask is None else mask.shape[0], 0 if mask is None else mask.shape[1],
+            nat.ptr(index), nat.ptr(cum), nat.ptr(first), nat.ptr(words),
+            0 if first is None else first.numel(), 0 if words is None else words.numel(),
+            int(divisor_for_int8), nat.ptr(scale), int(invalid_index_value), nat.ptr(scores),
+            nat.ptr(idx), nat.stream(dev))
+    nat.check(st)
+    return scores, idx
+
+
+def _fused_kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+                     max_tensor_size_per_row, filtering_bit_mask=None, invalid_index_value=-1,
+                     divisor_for_int8=-1, filtering_bit_index=None, per_embedding_scale=None):
+    """``(scores [B, W], indices int32 [B, W])``, ``W`` = ``max_tensor_size_per_row`` rounded up
+    to 32: every probed doc scored in its slot (the probes' full 32-doc warps in probe order,
+    then their remainders), filtered-out docs and the tail left as pads
+    (``fused_kmean_ann_cuda.cu:2126-2262``)."""
+    return _kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+                      max_tensor_size_per_row, invalid_index_value, divisor_for_int8,
+                      filtering_bit_index, per_embedding_scale, mask=filtering_bit_mask)
+
+
+def _fused_kmean_ann_partial(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+                             max_tensor_size_per_row, partial_mask_column_counts_cumsum,
+                             partial_mask_first_item_offset_in_column,
+                             partial_mask_column_results, invalid_index_value=-1,
+                             divisor_for_int8=-1, filtering_bit_index=None,
+                             per_embedding_scale=None, cluster_warp_size=None,
+                             cluster_warp_rounded_length_cumsum=None,
+                             cluster_remaining_length_cumsum=None, cluster_warp_size_cumsum=None,
+                             total_cluster_rounded_warps=0, total_cluster_remaining_warps=0):
+    """``fused_kmean_ann`` filtered by the probed-column Bloom words of
+    ``bloom_index_search_batch_return_partial_response`` (``fused_kmean_ann_cuda.cu:2335-2501``).
+    The precomputed warp counts and cumsums are accepted and unused: the kernel derives the slot
+    layout from ``cluster_length`` (the totals are ignored upstream too, ``:2459-2460``)."""
+    return _kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+                      max_tensor_size_per_row, invalid_index_value, divisor_for_int8,
+                      filtering_bit_index, per_embedding_scale,
+                      partial=(partial_mask_column_counts_cumsum,
+                               partial_mask_first_item_offset_in_column,
+                               partial_mask_column_results))
+
+
+_LIB.impl("fused_kmean_ann", _fused_kmean_ann, "CUDA")
+_LIB.impl("fused_kmean_ann_with_partial_masks", _fused_kmean_ann_partial, "CUDA")
+
+
+def _scores_fake(cluster_ids, embeddings, max_tensor_size_per_row, divisor_for_int8, scale):
+    width = (max_tensor_size_per_row + 31) // 32 * 32
+    rows = cluster_ids.shape[0]
+    dtype = _score_dtype(embeddings.dtype, divisor_for_int8, scale is not None)
+    return (embeddings.new_empty((rows, width), dtype=dtype),
+            embeddings.new_empty((rows, width), dtype=torch.int32))
+
+
+@torch.library.register_fake("st::fused_kmean_ann")
+def _(cluster_offsets, cluster_ids, cluster_length, embeddings, queries, max_tensor_size_per_row,
+      filtering_bit_mask=None, invalid_index_value=-1, divisor_for_int8=-1,
+      filtering_bit_index=None, per_embedding_scale=None):
+    return _scores_fake(cluster_ids, embeddings, max_tensor_size_per_row, divisor_for_int8,
+                        per_embedding_scale)
+
+
+@torch.library.register_fake("st::fused_kmean_ann_with_partial_masks")
+def _(cluster_offsets, cluster_ids, cluster_length, embeddings, queries, max_tensor_size_per_row,
+      partial_mask_column_counts_cumsum, partial_mask_first_item_offset_in_column,
+      partial_mask_column_results, invalid_index_value=-1, divisor_for_int8=-1,
+      filtering_bit_index=None, per_embedding_scale=None, cluster_warp_size=None,
+      cluster_warp_rounded_length_cumsum=None, cluster_remaining_length_cumsum=None,
+      cluster_warp_size_cumsum=None, total_cluster_rounded_warps=0,
+      total_cluster_remaining_warps=0):
+    return _scores_fake(cluster_ids, embeddings, max_tensor_size_per_row, divisor_for_int8,
+                        per_embedding_scale)
 
 
 @torch.library.register_fake("st::bloom_index_search_batch_prepared")
@@ -342,8 +686,46 @@ def _probe_prep(query, probe_ids, cluster_offsets, cluster_sizes):
 _LIB.impl("probe_prep", _probe_prep, "CUDA")
 
 
+@torch.library.register_fake("st::probe_prep")
+def _(query, probe_ids, cluster_offsets, cluster_sizes):
+    rows, n_probe = probe_ids.shape
+    i64 = probe_ids.new_empty((rows, n_probe), dtype=torch.int64)
+    return (query.new_empty(query.shape, dtype=torch.int8),
+            query.new_empty((rows,), dtype=torch.float32), i64, torch.empty_like(i64),
+            torch.empty_like(i64), probe_ids.new_empty((rows * n_probe,), dtype=torch.int32),
+            probe_ids.new_empty((rows, n_probe), dtype=torch.int32),
+            probe_ids.new_empty((rows * n_probe,), dtype=torch.int32),
+            probe_ids.new_empty((rows * n_probe,), dtype=torch.int32))
+
+
 def _capturing() -> bool:
     return torch.cuda.is_current_stream_capturing()
+
+
+# Row widths (int8 D) the full-scan kernels take; other widths run the IVF kernel.
+_FULL_SCAN_D = (64, 128, 256, 512, 768, 1024)
+# (id, version) of cluster_offsets and cluster_sizes, and N -> whether the one list is [0, N).
+_ONE_LIST: dict = {}
+
+
+def _one_list_is_the_table(offsets: Tensor, sizes: Tensor, n: int) -> bool:
+    """Whether the single list holds every item in order (offset 0, size N): read back from the
+    device once per index and kept until either tensor is freed or modified in place, so a
+    steady-state search makes no host sync. Under graph capture with nothing kept, False (the
+    IVF kernel takes the call, with the same results)."""
+    import weakref
+
+    key = (id(offsets), offsets._version, id(sizes), sizes._version, n)
+    hit = _ONE_LIST.get(key)
+    if hit is None:
+        if _capturing():
+            return False
+        hit = bool(int(offsets.reshape(-1)[0].item()) == 0 and
+                   int(sizes.reshape(-1)[0].item()) == n)
+        _ONE_LIST[key] = hit
+        for t in (offsets, sizes):
+            weakref.finalize(t, _ONE_LIST.pop, key, None)
+    return hit
 
 
 def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sort_perm,
@@ -414,10 +796,11 @@ def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sor
     probes = probe_ids.to(torch.int64).contiguous()
     lib = nat.lib()
     full = (divisor_for_int8 == -1 and offs.numel() == 1 and probes.shape[1] == 1
-            and width >= n and not _capturing()
-            and int(offs[0].item()) == 0 and int(sizes[0].item()) == n)
+            and width >= n and d in _FULL_SCAN_D
+            and _one_list_is_the_table(cluster_offsets, cluster_sizes, n))
     if full:
-        # one list holding every item in order: slot = position, the full-scan kernels
+        # one list holding every item in order: slot = position, the full-scan kernels; a row
+        # whose probe is not list 0 has no slot and ends as pads
         from retrieve_amd import hip  # noqa: F401  (registers torch.ops.retrieve.*)
         pos, dots = torch.ops.retrieve.int8_scan_topk(codes, item_codes, k, mask)
         ids.copy_(pos)
@@ -426,6 +809,9 @@ def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sor
                                         nat.ptr(perm), perm.numel(), nat.ptr(scales), nat.ptr(gs),
                                         nat.stream(dev))
         nat.check(st)
+        probed = probes[:, :1] == 0
+        ids = torch.where(probed, ids, -1)
+        scores = torch.where(probed, scores, float("-inf"))
         return ids, scores
     ws = nat.workspace(lib.rt_ivf_search_workspace(b, width, k), dev)
     with torch.cuda.device(dev):

@@ -134,6 +134,38 @@ def test_slot_order_warps_then_remainders(dev):
     assert ids[0].tolist() == [1000 + p for p in kept[:40]]
 
 
+@pytest.mark.parametrize("d", [192, 384, 1280])
+def test_one_list_widths_without_a_full_scan_kernel(dev, d):
+    """Row widths the full-scan kernels lack (the reference's DIM switch holds them,
+    ``fused_kmean_ann_cuda.cu:1566-1577``) take the IVF kernel on one list, with the same
+    results; a row probing a list that does not exist ends as pads."""
+    g = rng(106 + d)
+    n, b, k = 5000, 4, 50
+    items = g.integers(-128, 128, (n, d), dtype=np.int8)
+    perm = g.permutation(n).astype(np.int64)
+    q = g.standard_normal((b, d)).astype(np.float32)
+    probes = np.zeros((b, 1), np.int64)
+    probes[3, 0] = 1  # no list 1
+    ids, sc = _run(dev, q, probes, [0], [n], items, perm, 0.5, k, n)
+    want_ids, want_sc = ost.search(q, probes, [0], [n], items, perm, [0.5], k, n)
+    assert np.array_equal(ids, want_ids) and np.array_equal(sc, want_sc)
+    assert (ids[3] == -1).all()
+
+
+def test_one_list_full_scan_invalid_probe(dev):
+    """The full-scan path of one list: a row whose probe is not list 0 has no slot."""
+    g = rng(107)
+    n, d, b, k = 20_000, 128, 3, 30
+    items = g.integers(-128, 128, (n, d), dtype=np.int8)
+    perm = g.permutation(n).astype(np.int64)
+    q = g.standard_normal((b, d)).astype(np.float32)
+    probes = np.array([[0], [5], [0]], np.int64)
+    ids, sc = _run(dev, q, probes, [0], [n], items, perm, 2.0, k, n)
+    want_ids, want_sc = ost.search(q, probes, [0], [n], items, perm, [2.0], k, n)
+    assert np.array_equal(ids, want_ids) and np.array_equal(sc, want_sc)
+    assert (ids[1] == -1).all() and np.isneginf(sc[1]).all()
+
+
 def test_filters(dev):
     g = rng(105)
     n, d, b, k, c = 30_000, 64, 6, 50, 3
