@@ -187,10 +187,14 @@ class Plan:
 
 
 def compile_plan(tree, max_sub_queries: int = 5) -> Plan:
-    """Post-order ops with at most ``max_sub_queries`` children per AND / OR (a longer chain
-    becomes a node over the first ``m`` operands, then nodes over the running result and the
-    next ``m - 1``: the same value, a bounded stack)."""
-    m = max(2, int(max_sub_queries))
+    """Post-order ops of the parsed tree, with the reference builder's fan-out rule
+    (``expression_query_parser.cpp:207-290``): along an AND / OR chain, each time
+    ``max_sub_queries`` operands have gathered they become one node, which then stands as the
+    first operand of the rest of the chain; the chain ends in one node over what remains,
+    emitted whenever a batch was cut (so a chain whose last operand completes a batch ends in a
+    one-child node over it), else only for two operands or more. The plan bytes are then Meta's
+    byte for byte (``tests/golden``'s parser fixtures)."""
+    m = int(max_sub_queries)
     ops: list[int] = []
     params: list[list[int]] = []
     terms: list[tuple[int, int]] = []
@@ -205,6 +209,22 @@ def compile_plan(tree, max_sub_queries: int = 5) -> Plan:
         max_depth = max(max_depth, depth)
         return len(ops) - 1
 
+    def chain(op: int, xs) -> int:
+        sub: list[int] = []
+        gathered = 0
+        batched = False
+        for i, x in enumerate(xs):
+            sub.append(emit(x))
+            gathered += 1
+            # (the first operand is batched only when more follow: a chain here has two or more)
+            if gathered == m:
+                sub = [push(op, sub, len(sub))]
+                gathered = 1
+                batched = True
+        if len(sub) <= 1 and not batched:
+            return sub[0]
+        return push(op, sub, len(sub))
+
     def emit(node) -> int:
         kind = node[0]
         if kind == "EMPTY":
@@ -215,16 +235,7 @@ def compile_plan(tree, max_sub_queries: int = 5) -> Plan:
         if kind == "NOT":
             child = emit(node[1])
             return push(NOT, [child], 1)
-        op = AND if kind == "AND" else OR
-        xs = node[1]
-        first = [emit(x) for x in xs[:m]]
-        acc = push(op, first, len(first))
-        i = m
-        while i < len(xs):
-            nxt = [emit(x) for x in xs[i : i + m - 1]]
-            acc = push(op, [acc] + nxt, 1 + len(nxt))
-            i += m - 1
-        return acc
+        return chain(AND if kind == "AND" else OR, node[1])
 
     emit(tree)
     return Plan(ops, params, terms, max_depth)
