@@ -86,6 +86,26 @@ static bool blk_wide(int64_t row_bytes, int64_t B) {
 }
 // Cache-policy bits of the main pass's direct-to-LDS loads (streamed once: nontemporal).
 constexpr int kNontemporal = 2;
+// Word 3 of a raw buffer descriptor (stride 0, byte offsets; out-of-range loads return zeros).
+constexpr int kBufferWord3 = 0x00020000;
+
+// BYTES per lane from base + voffset (out-of-range past base + range: zeros) straight into LDS at
+// lds + lane * BYTES (lds wave-uniform); NT: nontemporal. (The builtin's size and cache-policy
+// operands must be literals, not template parameters.)
+template <int BYTES, bool NT>
+__device__ inline void buffer_load_lds(const void* base, int range, int voffset, void* lds) {
+  static_assert(BYTES == 4 || BYTES == 16, "load size");
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, range, kBufferWord3);
+  auto* l = (__attribute__((address_space(3))) void*)(lds);
+  if constexpr (BYTES == 4) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, l, 4, voffset, 0, 0, 0);
+  } else if constexpr (NT) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, l, 16, voffset, 0, 0, kNontemporal);
+  } else {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, l, 16, voffset, 0, 0, 0);
+  }
+}
 
 struct I8x32 {
   using Score = int32_t;
@@ -380,20 +400,22 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   auto issue_mask = [&](int64_t tt, int st) {
     // word e of the stage: query qg0 + e / MASK_DW, rows tt * ROWS + 32 (e % MASK_DW) + 0..31 at
     // bits 31..0 (the high half of a 64-bit mask word holds its first 32 rows)
+    const int64_t last = ((n + 63) >> 6) - 1;  // the transposed mask's last word row
+    const int64_t w0 = (tt * ROWS) >> 6;       // the tile's first word row (<= last)
+    const int64_t avail = (last - w0 + 1) * a.mask_t_stride * 8;
+    const uint64_t* mbase = a.mask_t + w0 * a.mask_t_stride;
+    const int mrange = static_cast<int>(avail < INT32_MAX ? avail : INT32_MAX);
 #pragma unroll
     for (int l = 0; l < MLOADS; ++l) {
       const int e = (l * kBlkWaves + wave) * kWave + lane;
       // from the transposed mask: a tile's words for the group's queries are contiguous
       const int64_t r0 = tt * ROWS + 32 * (e % MASK_DW);
-      const int64_t last = ((n + 63) >> 6) - 1;  // the transposed mask's last word row
       int64_t w = r0 >> 6;
       w = w < last ? w : last;  // rows past the end: never scored
-      const char* g =
-          reinterpret_cast<const char*>(a.mask_t + w * a.mask_t_stride + qg0 + e / MASK_DW) +
-          ((r0 & 63) ? 0 : 4);
+      const int off = static_cast<int>(((w - w0) * a.mask_t_stride + qg0 + e / MASK_DW) * 8) +
+                      ((r0 & 63) ? 0 : 4);
       int8_t* dst = mstage + st * MASK_BYTES + (l * kBlkWaves + wave) * kWave * 4;
-      __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(dst), 4, 0,
-                                       0);
+      buffer_load_lds<4, false>(mbase, mrange, off, dst);
     }
   };
   auto issue = [&](int64_t lt, int st) {
@@ -402,37 +424,24 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     if constexpr (!SEED) {
       if constexpr (masked) issue_mask(tt, st);
     }
-    if ((tt + 1) * ROWS <= n) {
-      // a full tile of consecutive rows (the seed's sample blocks hold whole tiles): a uniform
-      // tile address plus 32-bit lane offsets
-      static_assert(kSeedBlock % ROWS == 0, "seed sample blocks hold whole tiles");
-      const int8_t* tile = I + sample_item(tt * ROWS, a.row_stride) * static_cast<int64_t>(RB);
-#pragma unroll
-      for (int l = 0; l < TLOADS; ++l) {
-        // (the global address goes through a named pointer: passing the sum straight to the
-        // builtin drops the kernel from the host-side compile)
-        const int8_t* g = tile + toff[l];
-        int8_t* dst = base + (l * kBlkThreads + wave * kWave) * 16;
-        if (shared_tiles) {
-          __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(dst), 16,
-                                           0, 0);
-        } else {
-          __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(dst), 16,
-                                           0, kNontemporal);
-        }
-      }
-      return;
-    }
+    // One buffer descriptor per tile: base = its first row, range = its rows present. A tile's
+    // rows are consecutive (the seed's sample blocks hold whole tiles, and only the last tile
+    // is partial); rows past the end read as zeros and are never scored. Buffer loads rather
+    // than global ones: the compiler counts a pending global load to LDS as an access to both
+    // memories and then waits for every LDS read at once (lgkmcnt(0)), which would serialize
+    // the fragment reads of the MFMA loop.
+    static_assert(kSeedBlock % ROWS == 0, "seed sample blocks hold whole tiles");
+    const int64_t rows_here = n - tt * ROWS < ROWS ? n - tt * ROWS : ROWS;
+    const int8_t* tile = I + sample_item(tt * ROWS, a.row_stride) * static_cast<int64_t>(RB);
+    const int range = static_cast<int>(rows_here * RB);
 #pragma unroll
     for (int l = 0; l < TLOADS; ++l) {
-      const int r = toff[l] / RB;
-      int64_t row = tt * ROWS + r;
-      row = row < n ? row : n - 1;  // rows past the end load a valid row and are never scored
-      const int8_t* g = I + sample_item(row, a.row_stride) * RB + toff[l] % RB;
-      __builtin_amdgcn_global_load_lds(
-          g,
-          (__attribute__((address_space(3))) void*)(base + (l * kBlkThreads + wave * kWave) * 16),
-          16, 0, 0);
+      int8_t* dst = base + (l * kBlkThreads + wave * kWave) * 16;
+      if (shared_tiles) {
+        buffer_load_lds<16, false>(tile, range, toff[l], dst);
+      } else {
+        buffer_load_lds<16, true>(tile, range, toff[l], dst);
+      }
     }
   };
 
