@@ -41,11 +41,20 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
-# HBM bytes per launch of the main scan (FETCH_SIZE + WRITE_SIZE, copy-calibrated), measured with
-# rocprofv3 --pmc for these exact workloads; keyed by (workload, N, D, B, k). See profiles/.
+# HBM bytes per launch of the main scan (FETCH_SIZE x 2 + WRITE_SIZE, calibrated against a plain
+# 2 GiB device copy), measured with rocprofv3 --pmc for these exact workloads; keyed by
+# (workload, N, D, B, k). The profiles/ summaries named below give the counts and commands.
 MEASURED_TRAFFIC: dict = {
-    # profiles/filtered_int8_30Mx512_b16.md: FETCH_SIZE 7,580,854 KiB x 2 + WRITE_SIZE 5,786 KiB
-    ("filtered", 30_000_000, 512, 16, 100): 15_531_514_360,
+    ("filtered", 30_000_000, 512, 16, 100): 15_531_514_360,  # filtered_int8_30Mx512_b16.md
+    ("int8", 30_000_000, 512, 16, 100): 15_366_246_011,  # int8_scan_30Mx512_b16.md
+    ("int8", 30_000_000, 512, 256, 100): 15_454_702_797,  # int8_scan_30Mx512_b256.md
+    ("int8", 30_000_000, 512, 1024, 100): 51_364_477_133,  # int8_scan_30Mx512_b1024.md
+    ("dense", 10_000_000, 128, 64, 100): 2_566_548_500,  # dense_bf16_10Mx128_b64.md
+    ("dense", 10_000_000, 128, 1024, 100): 6_541_851_034,  # dense_bf16_10Mx128_b1024.md
+    ("dense", 10_000_000, 128, 4096, 100): 9_390_756_864,  # dense_bf16_10Mx128_b4096.md
+    # filtered_dense_bf16_10Mx128_b256.md, binary_30Mx512bit_b256.md
+    ("filtered-dense", 10_000_000, 128, 256, 100): 2_909_858_406,
+    ("binary", 30_000_000, 512, 256, 100): 3_761_035_264,
 }
 CARDINALITIES = (16, 32, 64, 128, 256, 512, 1000, 1000)
 BLOOM_BITS, BLOOM_K, HASH_K = 64, 3, 7
@@ -192,6 +201,33 @@ class Filter:
         return baseline.clause_sets_valid(self.attrs[:ns].cpu().long(), self.sets.cpu())
 
 
+def latency_windows(step, windows: int, calls: int, ms_step: float, b: int) -> dict:
+    """The reference harness's protocol after warm-up: several windows of back-to-back calls,
+    each call bracketed by events on the current stream; reports the median window's mean time
+    per call (and its queries/s) and the p95 over every call. Not part of ``value``."""
+    if calls <= 0:
+        calls = int(min(1000, max(20, 6000.0 / max(ms_step, 1e-3))))
+    means, per_call = [], []
+    for _ in range(windows):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(calls + 1)]
+        ev[0].record()
+        for i in range(calls):
+            step()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        ts = [ev[i].elapsed_time(ev[i + 1]) for i in range(calls)]
+        per_call += ts
+        means.append(sum(ts) / calls)
+    med = sorted(means)[len(means) // 2]
+    return {
+        "count": windows,
+        "calls_per_window": calls,
+        "ms_per_call_median_window": med,
+        "queries_per_s_median_window": b / (med * 1e-3),
+        "ms_per_call_p95": float(np.percentile(per_call, 95)),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -212,6 +248,11 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=None,
                     help="items of the CPU baseline's bounded sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--windows", type=int, default=3,
+                    help="latency windows after the timed steps (0: none)")
+    ap.add_argument("--window-calls", type=int, default=0,
+                    help="calls per latency window (default: 1000, fewer when that would "
+                         "exceed about 6 s per window)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 2 GiB device copy three times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against a known byte count)")
@@ -340,7 +381,15 @@ def main() -> int:
         hits = (got.unsqueeze(2) == best_i.unsqueeze(1)).any(2).sum().item()
         extra["recall_at_k_vs_fp32"] = hits / (b * k)
         log(f"recall@{k} vs exact fp32: {extra['recall_at_k_vs_fp32']:.4f}")
+        # the same with fp16 storage (the reference module's dtype), outside the timed region
+        items_h = items32.half()
         del items32
+        got = torch.ops.retrieve.dense_scan_topk(q32.half(), items_h, k)[0]
+        hits = (got.unsqueeze(2) == best_i.unsqueeze(1)).any(2).sum().item()
+        extra["recall_at_k_vs_fp32_fp16_storage"] = hits / (b * k)
+        log(f"recall@{k} vs exact fp32, fp16 storage: "
+            f"{extra['recall_at_k_vs_fp32_fp16_storage']:.4f}")
+        del items_h
 
         scan_bytes = n * d * 2 + b * d * 2
         scan_ops = 2 * b * n * d
@@ -445,6 +494,19 @@ def main() -> int:
         peak = {"int8": 5000.0, "bf16": 2500.0}[dtype]
         unit = "TFLOP/s"
     log(f"ms/step {ms_step:.3f}; main scan {kernel_ms:.3f} ms ({achieved:.0f} {unit})")
+    if bound == "mfma":
+        # what the matrix cores sustain on random operands at the clock they hold under that
+        # load (register-fed chains, no memory traffic): context for the spec-peak fraction
+        rate, mhz = ctypes.c_double(), ctypes.c_double()
+        _native.check(lib.rt_mfma_ceiling(0 if dtype == "int8" else 1, 200_000,
+                                          ctypes.byref(rate), ctypes.byref(mhz), None))
+        extra["mfma_sustained_random_operands"] = {
+            "value": rate.value / 1e12, "unit": unit, "clock_mhz": mhz.value,
+            "main_scan_frac_of_it": achieved / (rate.value / 1e12),
+        }
+        log(f"matrix cores sustain {rate.value / 1e12:.0f} {unit} at {mhz.value:.0f} MHz")
+    if args.windows > 0:
+        extra["windows"] = latency_windows(step, args.windows, args.window_calls, ms_step, b)
     if wl == "binary":
         extra["hamming_path"] = ("int8 matrix cores (bits as bytes)" if bound == "mfma"
                                  else "XOR + popcount")

@@ -108,6 +108,14 @@ int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B, const uint64_t* 
 int rt_profile_enable(int on);
 int rt_profile_collect(double* total_ms, int64_t* launches);
 
+/* Measurement helper, no counterpart in the reference: the sustained rate of the matrix cores on
+ * random operands (dtype 0: v_mfma_i32_32x32x32_i8, 1: v_mfma_f32_32x32x16_bf16), four
+ * register-fed accumulator chains per wave, two waves per SIMD, `iters` steps per chain, and the
+ * shader clock measured over the run (MHz). Sets *ops_per_s (int8 ops or bf16 flops per second).
+ * Synchronizes the stream; allocates a small sink buffer for the duration of the call. */
+int rt_mfma_ceiling(int dtype, int64_t iters, double* ops_per_s, double* clock_mhz,
+                    rt_stream_t stream);
+
 /* ---- exact clause filter --------------------------------------------------------------
  *
  * Replaces the clause kernels behind torch.ops.retrieve.clause_mask / clause_mask_scores

@@ -45,6 +45,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "rt_profile_enable": (_c_int, [_c_int]),
     "rt_profile_collect": (_c_int, [_c_p, _c_p]),
+    "rt_mfma_ceiling": (_c_int, [_c_int, _c_i64, _c_p, _c_p, _c_p]),
     "rt_clause_filter_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),
     "rt_clause_filter": (
         _c_int,

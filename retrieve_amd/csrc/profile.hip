@@ -35,7 +35,115 @@ void profile_end(hipStream_t stream, hipEvent_t stop) {
   if (stop != nullptr) (void)hipEventRecord(stop, stream);
 }
 
+// Sustained matrix-core rate on random operands: four independent 32x32 accumulator chains per
+// wave, operands held in registers (hashed bits, so the multipliers toggle as on real data), two
+// waves per SIMD. Thread 0 of workgroup 0 samples the shader clock (s_memtime) against the
+// 100 MHz constant clock (s_memrealtime) over its lifetime.
+typedef int ceil_v4i __attribute__((ext_vector_type(4)));
+typedef int ceil_v16i __attribute__((ext_vector_type(16)));
+typedef float ceil_v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 ceil_v8bf __attribute__((ext_vector_type(8)));
+
+__device__ inline uint32_t ceil_hash(uint32_t h) {
+  h *= 2654435761u;
+  h ^= h >> 15;
+  h *= 2246822519u;
+  h ^= h >> 13;
+  return h;
+}
+
+template <bool BF>
+__global__ void __launch_bounds__(256) mfma_ceiling_kernel(int64_t iters, int* sink,
+                                                          uint64_t* clocks) {
+  const uint32_t g = blockIdx.x * 256u + threadIdx.x;
+  ceil_v4i a, b;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    uint32_t x = ceil_hash(8 * g + c), y = ceil_hash(8 * g + 4 + c);
+    if (BF) {  // finite bf16 pairs in +-[1, 2)
+      x = (x & 0x80008000u) | 0x3f803f80u | (x & 0x007f007fu);
+      y = (y & 0x80008000u) | 0x3f803f80u | (y & 0x007f007fu);
+    }
+    a[c] = static_cast<int>(x);
+    b[c] = static_cast<int>(y);
+  }
+  const uint64_t c0 = __builtin_readcyclecounter();
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  ceil_v16i acc[4] = {};
+  ceil_v16f facc[4] = {};
+  for (int64_t i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (BF) {
+        facc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(ceil_v8bf, a),
+                                                          __builtin_bit_cast(ceil_v8bf, b),
+                                                          facc[j], 0, 0, 0);
+      } else {
+        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[j], 0, 0, 0);
+      }
+    }
+  }
+  int r = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) r += BF ? static_cast<int>(facc[j][e]) : acc[j][e];
+  sink[g] = r;
+  if (g == 0) {
+    clocks[0] = __builtin_readcyclecounter() - c0;
+    clocks[1] = __builtin_amdgcn_s_memrealtime() - r0;
+  }
+}
+
 }  // namespace rt
+
+extern "C" int rt_mfma_ceiling(int dtype, int64_t iters, double* ops_per_s, double* clock_mhz,
+                               hipStream_t stream) {
+  RT_CHECK_ARG(dtype == 0 || dtype == 1, "dtype must be 0 (int8) or 1 (bf16), got %d", dtype);
+  RT_CHECK_ARG(iters > 0 && ops_per_s != nullptr && clock_mhz != nullptr,
+               "iters must be > 0 and the outputs non-null");
+  int dev = 0, cus = 0;
+  RT_CHECK_HIP(hipGetDevice(&dev));
+  RT_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const int blocks = 2 * cus;  // two 4-wave workgroups per CU: two waves per SIMD
+  int* sink = nullptr;
+  uint64_t* clocks = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  float ms = 0.f;
+  uint64_t clk[2] = {0, 0};
+  // every resource is released on every path
+  hipError_t err = hipMalloc(&sink, sizeof(int) * blocks * 256);
+  if (err == hipSuccess) err = hipMalloc(&clocks, 2 * sizeof(uint64_t));
+  if (err == hipSuccess) err = hipEventCreate(&e0);
+  if (err == hipSuccess) err = hipEventCreate(&e1);
+  if (err == hipSuccess) {
+    auto launch = [&](int64_t n) {
+      if (dtype == 0) {
+        rt::mfma_ceiling_kernel<false><<<blocks, 256, 0, stream>>>(n, sink, clocks);
+      } else {
+        rt::mfma_ceiling_kernel<true><<<blocks, 256, 0, stream>>>(n, sink, clocks);
+      }
+    };
+    launch(iters / 8 + 1);  // warm-up
+    err = hipEventRecord(e0, stream);
+    if (err == hipSuccess) launch(iters);
+    if (err == hipSuccess) err = hipEventRecord(e1, stream);
+    if (err == hipSuccess) err = hipGetLastError();
+    if (err == hipSuccess) err = hipEventSynchronize(e1);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+    if (err == hipSuccess) err = hipMemcpy(clk, clocks, sizeof(clk), hipMemcpyDeviceToHost);
+  }
+  if (e0 != nullptr) (void)hipEventDestroy(e0);
+  if (e1 != nullptr) (void)hipEventDestroy(e1);
+  if (sink != nullptr) (void)hipFree(sink);
+  if (clocks != nullptr) (void)hipFree(clocks);
+  RT_CHECK_HIP(err);
+  const double per_mfma = dtype == 0 ? 2.0 * 32 * 32 * 32 : 2.0 * 32 * 32 * 16;
+  *ops_per_s = per_mfma * 4.0 * static_cast<double>(iters) * blocks * 4 / (ms * 1e-3);
+  *clock_mhz = clk[1] != 0 ? 100.0 * static_cast<double>(clk[0]) / static_cast<double>(clk[1])
+                           : 0.0;
+  return rt::kOk;
+}
 
 extern "C" int rt_profile_enable(int on) {
   rt::g_enabled = on != 0;
