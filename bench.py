@@ -201,31 +201,86 @@ class Filter:
         return baseline.clause_sets_valid(self.attrs[:ns].cpu().long(), self.sets.cpu())
 
 
-def latency_windows(step, windows: int, calls: int, ms_step: float, b: int) -> dict:
-    """The reference harness's protocol after warm-up: several windows of back-to-back calls,
-    each call bracketed by events on the current stream; reports the median window's mean time
-    per call (and its queries/s) and the p95 over every call. Not part of ``value``."""
-    if calls <= 0:
-        calls = int(min(1000, max(20, 6000.0 / max(ms_step, 1e-3))))
-    means, per_call = [], []
-    for _ in range(windows):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(calls + 1)]
-        ev[0].record()
-        for i in range(calls):
-            step()
-            ev[i + 1].record()
-        torch.cuda.synchronize()
-        ts = [ev[i].elapsed_time(ev[i + 1]) for i in range(calls)]
-        per_call += ts
-        means.append(sum(ts) / calls)
-    med = sorted(means)[len(means) // 2]
+def _time_calls(fn, n: int) -> tuple[list, float]:
+    """Per-call ms from an event pair around each call on the current stream, and the window's
+    wall seconds."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s, e in ev:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in ev], time.perf_counter() - t0
+
+
+def window_stats(ms: list, wall_s: float, bs: int) -> dict:
+    """One window's summary with the reference harness's fields
+    (evaluation/bench/measure.py:248-273): linear-interpolated quantiles, the mean trimmed by
+    n // 10 calls at each end, closed-loop queries/s."""
+    t = np.asarray(ms, dtype=np.float64)
+    n = t.size
+    q1, med, q3, p95, p99 = np.percentile(t, [25, 50, 75, 95, 99])
+    mean, std = float(t.mean()), float(t.std())
+    iqr = q3 - q1
+    cut = n // 10
     return {
-        "count": windows,
-        "calls_per_window": calls,
-        "ms_per_call_median_window": med,
-        "queries_per_s_median_window": b / (med * 1e-3),
-        "ms_per_call_p95": float(np.percentile(per_call, 95)),
+        "n": n,
+        "median_ms": float(med),
+        "mean_ms": mean,
+        "trimmed_mean_ms": float(np.sort(t)[cut : n - cut].mean()),
+        "p95_ms": float(p95),
+        "p99_ms": float(p99),
+        "min_ms": float(t.min()),
+        "iqr_ms": float(iqr),
+        "qps": n * bs / wall_s if wall_s > 0 else None,
+        "host_gap_ms": wall_s * 1e3 / n - mean,
+        "outliers_std": int((np.abs(t - mean) > 3 * std).sum()),
+        "outliers_tukey": int(((t < q1 - 1.5 * iqr) | (t > q3 + 1.5 * iqr)).sum()),
+        "load": "closed_loop",
     }
+
+
+def latency_windows(step, windows: int, calls: int, b: int, mode: str, warmup: int = 50,
+                    target_s: float = 2.0, n_min: int = 1000, n_max: int = 5000) -> dict:
+    """The reference harness's latency protocol (evaluation/bench/measure.py:281-345), after
+    the timed steps: `warmup` calls, a 20-call estimate, then `windows` windows of
+    clamp(target_s / median, n_min, n_max) calls (or `calls`), the window with the median
+    median reported with its spread over windows. Not part of ``value``."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    est, _ = _time_calls(step, 20)
+    med = max(float(np.median(est)), 1e-6)
+    n = calls if calls > 0 else int(min(max(target_s * 1e3 / med, n_min), n_max))
+    runs = [_time_calls(step, n) for _ in range(windows)]
+    medians = [float(np.median(ms)) for ms, _ in runs]
+    pick = sorted(range(windows), key=medians.__getitem__)[windows // 2]
+    d = window_stats(*runs[pick], b)
+    d.update(mode=mode, bs=b, windows=windows,
+             spread=(max(medians) - min(medians)) / medians[pick] if medians[pick] > 0 else 0.0,
+             window_medians_ms=medians)
+    d["unstable"] = d["spread"] > 0.05
+    return d
+
+
+def graph_step(step):
+    """The step captured once in a HIP graph (the ops enqueue on torch's current stream with no
+    host sync and no memset); returns a callable that replays it: the reference's ``graph``
+    mode, one graph launch per call."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    return graph.replay
 
 
 def main() -> int:
@@ -249,10 +304,14 @@ def main() -> int:
                     help="items of the CPU baseline's bounded sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--windows", type=int, default=3,
-                    help="latency windows after the timed steps (0: none)")
+                    help="latency windows after the timed steps, the reference harness's "
+                         "protocol (0: none)")
     ap.add_argument("--window-calls", type=int, default=0,
-                    help="calls per latency window (default: 1000, fewer when that would "
-                         "exceed about 6 s per window)")
+                    help="calls per latency window (default: 2 s worth, clamped to 1000-5000)")
+    ap.add_argument("--mode", choices=("eager", "graph"), default="eager",
+                    help="graph: time replays of the step captured in a HIP graph")
+    ap.add_argument("--jsonl", default=None,
+                    help="append the latency record (reference harness fields) to this file")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 2 GiB device copy three times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against a known byte count)")
@@ -470,20 +529,38 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    eager_step = step
 
     lib = _native.lib()
-    _native.check(lib.rt_profile_enable(1))
-    log(f"timing {args.steps} steps")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     total_ms = ctypes.c_double()
     launches = ctypes.c_int64()
+    if args.mode == "graph":
+        # the timed steps replay one capture; the main scan's HIP-event time comes from as many
+        # eager steps right after (events are not recorded inside the capture)
+        step = graph_step(step)
+        log(f"timing {args.steps} graph replays")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        _native.check(lib.rt_profile_enable(1))
+        for _ in range(args.steps):
+            eager_step()
+        torch.cuda.synchronize()
+    else:
+        _native.check(lib.rt_profile_enable(1))
+        log(f"timing {args.steps} steps")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     _native.check(lib.rt_profile_collect(ctypes.byref(total_ms), ctypes.byref(launches)))
     _native.check(lib.rt_profile_enable(0))
+    extra["mode"] = args.mode
     ms_step = wall * 1e3 / args.steps
     kernel_ms = total_ms.value / max(1, launches.value)
     if bound == "hbm":
@@ -506,7 +583,13 @@ def main() -> int:
         }
         log(f"matrix cores sustain {rate.value / 1e12:.0f} {unit} at {mhz.value:.0f} MHz")
     if args.windows > 0:
-        extra["windows"] = latency_windows(step, args.windows, args.window_calls, ms_step, b)
+        rec = latency_windows(step, args.windows, args.window_calls, b, args.mode)
+        extra["latency"] = {k: rec[k] for k in ("mode", "n", "windows", "median_ms", "p95_ms",
+                                                "p99_ms", "qps", "spread")}
+        if args.jsonl:
+            rec.update(workload=wl, n_items=n, d=d, k=k, dtype=dtype)
+            with open(args.jsonl, "a") as f:
+                f.write(json.dumps(rec) + "\n")
     if wl == "binary":
         extra["hamming_path"] = ("int8 matrix cores (bits as bytes)" if bound == "mfma"
                                  else "XOR + popcount")
