@@ -273,6 +273,14 @@ int rt_quantize_int8_rows(const float* x, int64_t rows, int64_t dim, int8_t* cod
  * Replaces: _pack_signs_to_int64 (retrieve/src/retrieve/indexing/quantize.py:63-72), the packing
  *   step of quantize_simhash_1bit / project_simhash_1bit_query and the Sign-OPORP projections
  *   (:99-173). */
+/* quantize_int8_global (retrieve/src/retrieve/indexing/quantize.py:25-52): one scale for the
+ * [rows, dim] float table, abs_max = max(max |x|, 1e-8) written to abs_max[0] (device), codes
+ * clamp(rint(fp32(x / abs_max) * 127), -128, 127); row i of codes from row perm[i] of x when
+ * perm (device, [rows]) is non-null. scratch4: 4 bytes of device memory. No host sync. */
+int rt_quantize_int8_global(const float* x, int64_t rows, int64_t dim, const int64_t* perm,
+                            int8_t* codes, float* abs_max, uint32_t* scratch4,
+                            rt_stream_t stream);
+
 int rt_pack_signs(const float* x, int64_t rows, int64_t dim, uint64_t* words,
                   rt_stream_t stream);
 
@@ -314,7 +322,9 @@ int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64_t B, const
  * elem: 0 int8 (queries and embeddings int8 [., D]), 1 bf16, 2 fp16, 3 fp32. Scores: int8 ->
  * int32 dot; int8 with divisor != -1 -> fp16(float(dot) / divisor); int8 with
  * per_embedding_scale (fp16 [N], taking precedence) -> fp16(float(fp16(dot)) / scale[doc]);
- * float rows -> the fp32-accumulated dot rounded to the row type. Filters (one at most): `mask`
+ * float rows -> the fp32-accumulated dot rounded to the row type; elem + 16 (bf16, fp16 or fp32
+ * rows; an extension for this library's searches above k 1024) keeps the fp32 accumulator, fp32
+ * scores. Filters (one at most): `mask`
  * [mask_rows, mask_words] in the mask layout over positions, row mask_index[b] (or b); or the
  * partial masks of rt_bloom_search_columns: entry e = mask_row * n_probe + j covers probe j's
  * docs from bit partial_first_offsets[e] of words partial_counts_cumsum[e - 1] ... D * element

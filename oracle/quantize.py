@@ -2,7 +2,10 @@
 
 Pinned by: the reference's edge-value tests restated in ``tests/test_oracle.py`` (±abs_max →
 ±127, an all-zero row, a 1e-30 row, exact ``.5`` quotients that round half to even), and the
-closed form below evaluated in fp64 element by element on small inputs.
+closed form below evaluated in fp64 element by element on small inputs. ``quantize_int8_global``
+is pinned against torch's own CPU eager ops on the same inputs (the reference's function is
+those ops) and by its closed-form properties (the extreme element → ±127, the reconstruction
+error bound, the row permutation).
 """
 
 from __future__ import annotations
@@ -31,6 +34,24 @@ def quantize_int8(x: np.ndarray, divide: bool = False) -> tuple[np.ndarray, np.n
     v = np.rint(q * np.float32(127.0))
     codes = np.clip(v, -128, 127).astype(np.int8)
     return codes, scales
+
+
+def quantize_int8_global(x: np.ndarray, rows: np.ndarray | None = None
+                         ) -> tuple[np.ndarray, np.float32]:
+    """One scale for the table (``retrieve/src/retrieve/indexing/quantize.py:25-52``): ``abs_max
+    = max(max x, -min x)`` floored at fp32(1e-8); ``code = clamp(rint(fp32(fp32(x / abs_max) *
+    127)), -128, 127)`` (fp32 throughout); row ``i`` of the codes from row ``rows[i]``. Returns
+    ``(codes int8 [N, D], abs_max float32)``; the scale is ``fp32(abs_max / 127)``."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.size:
+        abs_max = np.float32(max(np.float32(x.max()), -np.float32(x.min())))
+    else:
+        abs_max = np.float32(0.0)
+    abs_max = np.maximum(abs_max, ABS_MAX_FLOOR).astype(np.float32)
+    src = x if rows is None else x[rows]
+    q = (src / abs_max).astype(np.float32) * np.float32(127.0)
+    codes = np.clip(np.rint(q), -128, 127).astype(np.int8)
+    return codes, np.float32(abs_max)
 
 
 def pack_signs(values: np.ndarray) -> np.ndarray:

@@ -74,6 +74,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rt_quantize_int8_rows": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_int, _c_p]),
     "rt_pack_mask": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "rt_pack_signs": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "rt_quantize_int8_global": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "rt_int8_rerank_topk": (
         _c_int,
         [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p,

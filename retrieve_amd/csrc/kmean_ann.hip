@@ -33,6 +33,7 @@ constexpr int kKmMaxRowBytes = 8192;
 
 enum KmElem : int { kElemI8 = 0, kElemBf16 = 1, kElemF16 = 2, kElemF32 = 3 };
 enum KmOut : int { kOutI32 = 0, kOutF16 = 1, kOutBf16 = 2, kOutF32 = 3 };
+constexpr int kKeepF32 = 16;
 
 struct KmArgs {
   const int8_t* queries;  // [B, RB]
@@ -269,7 +270,11 @@ extern "C" int rt_fused_kmean_ann(
     int32_t* out_indices, hipStream_t stream) {
   RT_CHECK_ARG(B >= 0 && N >= 0 && n_probe >= 0 && n_offsets >= 0 && width >= 0,
                "sizes must be >= 0");
-  RT_CHECK_ARG(elem >= kElemI8 && elem <= kElemF32, "element kind must be 0-3, got %d", elem);
+  // elem + kKeepF32: float rows store their fp32 accumulators (the library's top-k above 1024)
+  const bool keep_f32 = elem >= kKeepF32;
+  if (keep_f32) elem -= kKeepF32;
+  RT_CHECK_ARG(elem >= kElemI8 && elem <= kElemF32 && !(keep_f32 && elem == kElemI8),
+               "element kind must be 0-3, or 17-19 for fp32 scores of float rows");
   const int64_t esz = elem == kElemI8 ? 1 : (elem == kElemF32 ? 4 : 2);
   const int64_t rb = D * esz;
   RT_CHECK_ARG(D >= 1 && rb % 16 == 0 && rb <= kKmMaxRowBytes,
@@ -322,7 +327,8 @@ extern "C" int rt_fused_kmean_ann(
   if (elem == kElemI8) {
     a.out_kind = (divisor == -1 && per_embedding_scale == nullptr) ? kOutI32 : kOutF16;
   } else {
-    a.out_kind = elem == kElemBf16 ? kOutBf16 : (elem == kElemF16 ? kOutF16 : kOutF32);
+    a.out_kind = keep_f32 ? kOutF32
+                          : (elem == kElemBf16 ? kOutBf16 : (elem == kElemF16 ? kOutF16 : kOutF32));
   }
   a.out_scores = out_scores;
   a.out_idx = out_indices;

@@ -63,6 +63,63 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_rows_kernel(const floa
   }
 }
 
+// One scale for the whole table (quantize_int8_global, retrieve/src/retrieve/indexing/quantize.py:
+// 25-52): abs_max = max(max x, -min x) floored at 1e-8 (fabsf's maximum, the same value), code
+// = clamp(rint(fp32(x / abs_max) * 127), -128, 127) in fp32, row i of the codes from row
+// perm[i] of x when a permutation is given. NaN inputs are outside the contract (max ignores
+// them here; the reference's int8 cast of a NaN code is unspecified).
+constexpr int kGlobalThreads = 256;
+
+__global__ void abs_max_init_kernel(uint32_t* bits) { bits[0] = 0u; }
+
+// Grid-stride max |x| over n floats, 16-byte loads when x is 16-byte aligned; one atomic per
+// workgroup on the bits of the (non-negative) float, whose unsigned order is the float order.
+__global__ void __launch_bounds__(kGlobalThreads) abs_max_kernel(const float* x, int64_t n,
+                                                                 uint32_t* bits) {
+  __shared__ float red[kGlobalThreads / kWave];
+  float m = 0.f;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kGlobalThreads;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kGlobalThreads + threadIdx.x;
+  if (reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    const v4f* x4 = reinterpret_cast<const v4f*>(x);
+    const int64_t n4 = n / 4;
+    for (int64_t i = t0; i < n4; i += stride) {
+      const v4f v = __builtin_nontemporal_load(x4 + i);
+      m = fmaxf(fmaxf(m, fmaxf(fabsf(v[0]), fabsf(v[1]))), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    }
+    for (int64_t i = 4 * n4 + t0; i < n; i += stride) m = fmaxf(m, fabsf(x[i]));
+  } else {
+    for (int64_t i = t0; i < n; i += stride) m = fmaxf(m, fabsf(x[i]));
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (lane_id() == 0) red[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kGlobalThreads / kWave; ++w) m = fmaxf(m, red[w]);
+    atomicMax(bits, __float_as_uint(m));
+  }
+}
+
+__global__ void __launch_bounds__(kGlobalThreads) quantize_global_kernel(
+    const float* x, int64_t rows, int64_t dim, const int64_t* perm, const uint32_t* bits,
+    int8_t* codes, float* abs_max_out) {
+  const float m = fmaxf(__uint_as_float(bits[0]), 1e-8f);
+  const int64_t total = rows * dim;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kGlobalThreads;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kGlobalThreads + threadIdx.x;
+  if (t0 == 0) abs_max_out[0] = m;
+  for (int64_t i = t0; i < total; i += stride) {
+    const int64_t r = i / dim;
+    const int64_t c = i - r * dim;
+    const int64_t src = perm != nullptr ? perm[r] : r;
+    float v = (x[src * dim + c] / m) * 127.0f;
+    v = fminf(fmaxf(rintf(v), -128.0f), 127.0f);
+    codes[i] = static_cast<int8_t>(v);
+  }
+}
+
 // Sign bits of float rows, LSB-first: bit b of word w of row r is x[r, 64 w + b] > 0
 // (_pack_signs_to_int64, retrieve/src/retrieve/indexing/quantize.py:63-72). One wave per word:
 // lane b reads element 64 w + b and the ballot is the word (NaN and -0 give 0 bits, as the
@@ -322,6 +379,27 @@ extern "C" int rt_quantize_int8_rows(const float* x, int64_t rows, int64_t dim, 
   if (rows == 0) return kOk;
   quantize_rows_kernel<<<static_cast<unsigned>(rows), kQuantThreads, 0, stream>>>(
       x, dim, codes, scales, scale_div);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+extern "C" int rt_quantize_int8_global(const float* x, int64_t rows, int64_t dim,
+                                       const int64_t* perm, int8_t* codes, float* abs_max,
+                                       uint32_t* scratch4, hipStream_t stream) {
+  RT_CHECK_ARG(rows >= 0 && dim >= 1, "rows must be >= 0 and dim >= 1");
+  RT_CHECK_ARG(abs_max != nullptr && scratch4 != nullptr, "abs_max and scratch4 must be given");
+  RT_CHECK_ARG(rows == 0 || (x != nullptr && codes != nullptr), "x and codes must not be null");
+  const int64_t total = rows * dim;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  }
+  const int64_t want = cdiv(total, kGlobalThreads * 4);
+  const unsigned grid = static_cast<unsigned>(want < 8 * cus ? (want > 0 ? want : 1) : 8 * cus);
+  abs_max_init_kernel<<<1, 1, 0, stream>>>(scratch4);
+  if (total > 0) abs_max_kernel<<<grid, kGlobalThreads, 0, stream>>>(x, total, scratch4);
+  quantize_global_kernel<<<grid, kGlobalThreads, 0, stream>>>(x, rows, dim, perm, scratch4,
+                                                              codes, abs_max);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }

@@ -28,6 +28,9 @@ def _check_items(**tables: Tensor) -> None:
 # From this batch on the dense scans run the register-blocked kernel (256 queries per
 # workgroup, item tiles read once per 256 queries) instead of 16 queries per wave.
 BLOCKED_MIN_BATCH = 32
+# The fused scans' list bound; above it int8_scan_topk and dense_scan_topk select from the raw
+# scorer's buffer (retrieve_amd.large_k).
+MAX_FUSED_K = 1024
 _BLOCKED_ROW_BYTES = (128, 256, 512)
 
 
@@ -75,8 +78,8 @@ def _int8_scan_prep(query_codes: Tensor, item_codes: Tensor, k: int, mask: Tenso
         raise ValueError(
             f"D mismatch: query D={query_codes.shape[1]} vs item D={item_codes.shape[1]}"
         )
-    if not 1 <= k <= 1024:
-        raise ValueError(f"k must be in [1, 1024], got {k}")
+    if k < 1:
+        raise ValueError(f"k must be >= 1, got {k}")
     _check_items(item_codes=item_codes)
     b, n = query_codes.shape[0], item_codes.shape[0]
     if mask is not None:
@@ -100,6 +103,10 @@ def int8_scan_topk(
     (``silvertorch/.../fork_search_cuda.cu:1256-1524``)."""
     q, mask = _int8_scan_prep(query_codes, item_codes, k, mask)
     dev = nat.require_device(q, item_codes)
+    if k > MAX_FUSED_K:
+        from retrieve_amd import large_k
+
+        return large_k.full_scan_topk(q, item_codes, k, mask, -(2**31))
     b, d = q.shape
     n = item_codes.shape[0]
     ids = torch.empty((b, k), dtype=torch.int64, device=dev)
@@ -149,8 +156,8 @@ def dense_scan_topk(
         raise TypeError("query and item_embs must both be bfloat16 or both float16")
     if query.shape[1] != item_embs.shape[1]:
         raise ValueError(f"D mismatch: query D={query.shape[1]} vs item D={item_embs.shape[1]}")
-    if not 1 <= k <= 1024:
-        raise ValueError(f"k must be in [1, 1024], got {k}")
+    if k < 1:
+        raise ValueError(f"k must be >= 1, got {k}")
     _check_items(item_embs=item_embs)
     b, d = query.shape
     n = item_embs.shape[0]
@@ -162,6 +169,10 @@ def dense_scan_topk(
         mask = mask.contiguous()
     q = query.contiguous()
     dev = nat.require_device(q, item_embs)
+    if k > MAX_FUSED_K:
+        from retrieve_amd import large_k
+
+        return large_k.full_scan_topk(q, item_embs, k, mask, float("-inf"))
     ids = torch.empty((b, k), dtype=torch.int64, device=dev)
     scores = torch.empty((b, k), dtype=torch.float32, device=dev)
     if _use_blocked(b, 2 * d, k):
@@ -523,8 +534,8 @@ def fused_masked_knn_topk(
     if positive_indices.dim() == 2 and positive_indices.shape[1] < k:
         raise ValueError(
             f"positive_indices has {positive_indices.shape[1]} columns, fewer than k={k}")
-    if not 1 <= k <= 1024:
-        raise ValueError(f"k must be in [1, 1024], got {k}")
+    if k < 1:
+        raise ValueError(f"k must be >= 1, got {k}")
     _check_items(item_embs=item_embs)
     counts = _cand_check(positive_indices, counts, query.shape[0])
     q = query.to(torch.float32).contiguous()
@@ -708,6 +719,41 @@ def pack_signs(values: Tensor) -> Tensor:
 @pack_signs.register_fake
 def _(values):
     return values.new_empty((values.shape[0], values.shape[1] // 64), dtype=torch.int64)
+
+
+@torch.library.custom_op("retrieve::quantize_int8_global", mutates_args=(), device_types="cuda")
+def quantize_int8_global(embs: Tensor, rows: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """One global int8 scale (``quantize_int8_global``, ``retrieve/src/retrieve/indexing/
+    quantize.py:25-52``): ``abs_max = max(max |x|, 1e-8)``, codes ``clamp(round(x / abs_max *
+    127), -128, 127)`` in fp32, row ``i`` from row ``rows[i]`` when given → ``(codes int8
+    [N, D], abs_max float32 [1])``; the scale is ``abs_max / 127``."""
+    if embs.dim() != 2 or embs.dtype != torch.float32:
+        raise ValueError("embs must be a float32 [N, D] tensor")
+    x = embs.contiguous()
+    dev = nat.require_device(x)
+    n, d = x.shape
+    perm = None
+    if rows is not None:
+        if rows.dtype != torch.int64 or rows.shape != (n,):
+            raise ValueError("rows must be an int64 [N] permutation")
+        perm = rows.to(dev).contiguous()
+        # (a build-time op: one host check keeps every row the kernel reads inside the table)
+        if n and (int(perm.min()) < 0 or int(perm.max()) >= n):
+            raise IndexError(f"rows must lie in [0, {n})")
+    codes = torch.empty((n, d), dtype=torch.int8, device=dev)
+    abs_max = torch.empty((1,), dtype=torch.float32, device=dev)
+    scratch = torch.empty((1,), dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        st = nat.lib().rt_quantize_int8_global(
+            nat.ptr(x), n, max(d, 1), nat.ptr(perm) if perm is not None else None,
+            nat.ptr(codes), nat.ptr(abs_max), nat.ptr(scratch), nat.stream(dev))
+    nat.check(st)
+    return codes, abs_max
+
+
+@quantize_int8_global.register_fake
+def _(embs, rows=None):
+    return embs.new_empty(embs.shape, dtype=torch.int8), embs.new_empty((1,))
 
 
 @torch.library.custom_op("retrieve::int8_rerank_topk", mutates_args=(), device_types="cuda")

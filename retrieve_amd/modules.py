@@ -724,7 +724,14 @@ def probe_width(cluster_sizes: Tensor, n_probe: int) -> int:
 def quantize_int8_global(embs: Tensor, rows: Tensor | None = None) -> tuple[Tensor, float]:
     """One global scale (``retrieve/src/retrieve/indexing/quantize.py:34-52``): ``abs_max =
     max(max x, -min x)`` floored at 1e-8, codes ``clamp(round(x / abs_max * 127))`` in fp32,
-    rows written in ``rows`` order when given; returns ``(codes [N, D] int8, abs_max / 127)``."""
+    rows written in ``rows`` order when given; returns ``(codes [N, D] int8, abs_max / 127)``.
+    GPU tables go through the HIP kernels (``torch.ops.retrieve.quantize_int8_global``); a
+    table held on the host (an index built on the CPU) is quantized there with the same
+    arithmetic."""
+    if embs.is_cuda:
+        codes, abs_max = torch.ops.retrieve.quantize_int8_global(
+            embs.to(torch.float32), None if rows is None else rows.to(embs.device))
+        return codes, float((abs_max / 127.0).item())
     abs_max = torch.maximum(embs.amax(), -embs.amin()).clamp(min=1e-8)
     codes = torch.empty(embs.shape, dtype=torch.int8, device=embs.device)
     for s in range(0, embs.shape[0], _CODE_CHUNK_ROWS):

@@ -446,7 +446,8 @@ def _score_dtype(emb_dtype, divisor_for_int8, has_scale):
 
 def _kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
                max_tensor_size_per_row, invalid_index_value, divisor_for_int8,
-               filtering_bit_index, per_embedding_scale, mask=None, partial=None):
+               filtering_bit_index, per_embedding_scale, mask=None, partial=None,
+               f32_scores=False):
     for name, t, dim in (("cluster_offsets", cluster_offsets, 1), ("cluster_ids", cluster_ids, 2),
                          ("cluster_length", cluster_length, 2), ("embeddings", embeddings, 2),
                          ("queries", queries, 2)):
@@ -485,6 +486,10 @@ def _kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries
         mask = mask.contiguous()
     width = (int(max_tensor_size_per_row) + 31) // 32 * 32
     dtype = _score_dtype(embeddings.dtype, divisor_for_int8, scale is not None)
+    elem = _ELEM[embeddings.dtype]
+    if f32_scores and embeddings.dtype != torch.int8:
+        dtype = torch.float32
+        elem += 16
     scores = torch.empty((b, width), dtype=dtype, device=dev)
     idx = torch.empty((b, width), dtype=torch.int32, device=dev)
     cum = first = words = None
@@ -505,7 +510,7 @@ def _kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries
     q = queries.contiguous()
     with torch.cuda.device(dev):
         st = nat.lib().rt_fused_kmean_ann(
-            nat.ptr(q), nat.ptr(embeddings), _ELEM[embeddings.dtype], b, n, d, nat.ptr(offs),
+            nat.ptr(q), nat.ptr(embeddings), elem, b, n, d, nat.ptr(offs),
             offs.numel(), nat.ptr(ids), nat.ptr(lens), p, width, nat.ptr(mask),
             0 if mask is None else mask.shape[0], 0 if mask is None else mask.shape[1],
             nat.ptr(index), nat.ptr(cum), nat.ptr(first), nat.ptr(words),
@@ -514,6 +519,16 @@ def _kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries
             nat.ptr(idx), nat.stream(dev))
     nat.check(st)
     return scores, idx
+
+
+def raw_scores(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+               max_tensor_size_per_row, mask=None, divisor_for_int8=-1):
+    """The raw scorer for this package's own callers (the searches' top-k above 1024): every
+    probed slot's score (int32 dots, fp16 with a divisor, the fp32 accumulator for float items)
+    and its item index (``-1`` for a pad), as ``fused_kmean_ann`` writes them."""
+    return _kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+                      max_tensor_size_per_row, -1, divisor_for_int8, None, None, mask=mask,
+                      f32_scores=True)
 
 
 def _fused_kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
@@ -749,8 +764,8 @@ def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sor
     if exact and (item_clause_attrs is None or clause_slots is None or clause_is_reverse is None):
         raise RuntimeError("the exact filter needs item_clause_attrs, clause_slots and "
                            "clause_is_reverse")
-    if not 1 <= k <= MAX_SEARCH_K:
-        raise RuntimeError(f"k must be in [1, {MAX_SEARCH_K}], got {k}")
+    if k < 1:
+        raise RuntimeError(f"k must be >= 1, got {k}")
     if probe_ids.dim() != 2 or probe_ids.shape[0] != query.shape[0] or \
             probe_ids.shape[1] > MAX_PROBE:
         raise RuntimeError(f"probe_ids must be [B, n_probe <= {MAX_PROBE}]")
@@ -795,6 +810,9 @@ def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sor
     sizes = cluster_sizes.to(torch.int64).contiguous()
     probes = probe_ids.to(torch.int64).contiguous()
     lib = nat.lib()
+    if k > MAX_SEARCH_K:
+        return _search_large_k(codes, scales, item_codes, probes, offs, sizes, width, mask,
+                               int(divisor_for_int8), perm, gs, k)
     full = (divisor_for_int8 == -1 and offs.numel() == 1 and probes.shape[1] == 1
             and width >= n and d in _FULL_SCAN_D
             and _one_list_is_the_table(cluster_offsets, cluster_sizes, n))
@@ -822,6 +840,42 @@ def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sor
             perm.numel(), nat.ptr(gs), k, nat.ptr(ids), nat.ptr(scores), nat.ptr(ws), ws.numel(),
             nat.stream(dev))
     nat.check(st)
+    return ids, scores
+
+
+def _search_large_k(codes, scales, item_codes, probes, offs, sizes, width, mask, divisor, perm,
+                    gs, k):
+    """``search`` above the radix select's 1024: the raw scorer over every probed slot, the rows'
+    top ``k`` by (key desc, slot asc), then the epilogue (``fork_search_cuda.cu:843-915,
+    1490-1520``: ``at::topk`` on the raw buffer and ``epilogue_kernel``): ``id =
+    sort_perm[position]``; score ``(fp32(dot) * q_scale) * global_scale``, or with a divisor
+    ``score16 * ((q_scale * divisor) * global_scale)``; ``-1`` / ``-inf`` pads."""
+    from retrieve_amd import large_k
+
+    b = codes.shape[0]
+    n_lists = offs.numel()
+    dev = codes.device
+    valid = (probes >= 0) & (probes < n_lists)
+    cluster = torch.where(valid, probes, 0)
+    length = torch.where(valid, sizes[cluster], 0)
+    ids = torch.full((b, k), -1, dtype=torch.int64, device=dev)
+    scores = torch.full((b, k), float("-inf"), dtype=torch.float32, device=dev)
+    step = large_k.chunk_rows(width, dev)
+    for r0 in range(0, b, step):
+        r1 = min(b, r0 + step)
+        raw, idx = raw_scores(offs, cluster[r0:r1].contiguous(), length[r0:r1].contiguous(),
+                              item_codes, codes[r0:r1].contiguous(), width,
+                              mask=None if mask is None else mask[r0:r1], divisor_for_int8=divisor)
+        top_raw, slot = large_k.raw_topk(raw, idx, k)
+        hit = slot >= 0
+        pos = idx.gather(1, slot.clamp(min=0)).to(torch.int64)
+        ids[r0:r1] = torch.where(hit, perm[pos.clamp(min=0)], -1)
+        q = scales[r0:r1, None]
+        if divisor == -1:
+            sc = (top_raw.to(torch.float32) * q) * gs
+        else:
+            sc = top_raw.to(torch.float32) * ((q * float(divisor)) * gs)
+        scores[r0:r1] = torch.where(hit, sc, float("-inf"))
     return ids, scores
 
 

@@ -115,6 +115,16 @@ def test_masked(dev):
     _check(dev, q, it, 100, mask=mask)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_k_above_1024(dev, dtype):
+    g = rng(44)
+    q = g.standard_normal((3, 128)).astype(np.float32)
+    it = g.standard_normal((12000, 128)).astype(np.float32)
+    mask = g.random((3, 12000)) < 0.6
+    mask[2] = g.random(12000) < 0.05  # ~600 survivors < k
+    _check(dev, q, it, 1500, dtype=dtype, mask=mask)
+
+
 def test_errors(dev):
     q = torch.zeros((2, 64), dtype=torch.bfloat16, device=dev)
     it = torch.zeros((10, 64), dtype=torch.bfloat16, device=dev)

@@ -85,6 +85,19 @@ def test_masked_and_short_rows(dev):
     _check(dev, q, items, 100, mask)
 
 
+@pytest.mark.parametrize("k", [1025, 3000])
+def test_k_above_1024(dev, k):
+    """Above the fused lists' 1024: the raw scorer's buffer and one key select per row
+    (retrieve_amd.large_k), the same results, ties to the lower index, pads past the mask."""
+    g = rng(14 + k)
+    q = g.integers(-128, 128, (4, 64), dtype=np.int8)
+    items = g.integers(-4, 5, (20000, 64), dtype=np.int8)  # small values: many tied dots
+    mask = g.random((4, 20000)) < 0.5
+    mask[1] = g.random(20000) < 0.02  # ~400 survivors < k
+    _check(dev, q, items, k, mask)
+    _check(dev, q, items, k)
+
+
 def test_k_above_n_pads(dev):
     g = rng(13)
     q = g.integers(-128, 128, (2, 64), dtype=np.int8)

@@ -74,6 +74,33 @@ def test_quantize_int8_op(dev):
     assert np.array_equal(_np(scales), want_s)
 
 
+@pytest.mark.parametrize("n,d,offset", [(5000, 96, 0), (333, 7, 1), (0, 16, 0)])
+def test_quantize_int8_global_op(dev, n, d, offset):
+    """The HIP global quantizer (16-byte and scalar loads: a table offset by one float) against
+    the oracle, with and without a row permutation."""
+    import retrieve_amd.hip  # noqa: F401
+    from retrieve_amd import modules as mods
+
+    g = rng(5)
+    flat = (g.standard_normal(n * d + offset) * 2).astype(np.float32)
+    if n:
+        flat[offset + (n * d) // 2] = 9.5  # a positive extreme
+        flat[offset + 1 :: 97] = np.round(flat[offset + 1 :: 97] * 4) / 4  # quarter values
+    xt = _t(dev, flat)[offset:].view(n, d)
+    x = flat[offset:].reshape(n, d)
+    perm = g.permutation(n)
+    for rows in (None, perm):
+        codes, abs_max = torch.ops.retrieve.quantize_int8_global(
+            xt, None if rows is None else _t(dev, rows))
+        want_c, want_m = oq.quantize_int8_global(x, rows)
+        assert np.array_equal(_np(codes), want_c)
+        assert _np(abs_max)[0] == want_m
+    if n:
+        codes, scale = mods.quantize_int8_global(xt, rows=_t(dev, perm))
+        assert np.array_equal(_np(codes), oq.quantize_int8_global(x, perm)[0])
+        assert scale == float(np.float32(oq.quantize_int8_global(x)[1] / np.float32(127)))
+
+
 def _rerank_oracle(q_codes, q_scales, codes_sorted, inv_perm, gs, cand, k):
     b, p = cand.shape
     kk = min(k, p)

@@ -187,6 +187,39 @@ def _nearest_f32(fr) -> np.float32:
     return best[1]
 
 
+@pytest.mark.parametrize("shape", [(300, 32), (7, 5), (1, 1)])
+def test_quantize_global_against_torch_eager(shape):
+    """The reference's quantize_int8_global is torch eager fp32 ops (indexing/quantize.py:25-52):
+    run those same ops on the CPU and compare bit for bit; plus the closed-form properties."""
+    import torch
+
+    from oracle import quantize as oq
+
+    g = rng(31)
+    x = (g.standard_normal(shape) * 3).astype(np.float32)
+    x.flat[0] = -np.abs(x).max() * 1.5  # the extreme is negative: -min decides
+    perm = g.permutation(shape[0])
+    codes, abs_max = oq.quantize_int8_global(x, perm)
+    t = torch.from_numpy(x)
+    am = torch.maximum(t.amax(), -t.amin()).clamp(min=1e-8)
+    want = (t[torch.from_numpy(perm)] / am * 127.0).round().clamp(-128, 127).to(torch.int8)
+    assert np.array_equal(codes, want.numpy())
+    assert abs_max == np.float32(am.item())
+    # the extreme element maps to -127 exactly; every code reconstructs within half a step
+    assert codes[np.argsort(perm)[0]].flat[0] == -127
+    scale = np.float32(abs_max / np.float32(127))
+    assert (np.abs(codes.astype(np.float64) * scale - x[perm]) <= scale / 2 * (1 + 1e-5)).all()
+    plain, _ = oq.quantize_int8_global(x)
+    assert np.array_equal(plain[perm], codes)
+
+
+def test_quantize_global_zero_table():
+    from oracle import quantize as oq
+
+    codes, abs_max = oq.quantize_int8_global(np.zeros((3, 4), np.float32))
+    assert abs_max == np.float32(1e-8) and not codes.any()
+
+
 def test_quantize_divide_scale_is_the_rounded_quotient():
     """The ``divide`` scale is the float32 nearest ``abs_max / 127`` (exact rational), which
     differs from ``abs_max * fp32(1/127)`` for some ``abs_max``; the codes do not depend on it."""

@@ -96,6 +96,34 @@ def test_ivf_probes(dev, divisor, n_lists, n_probe, width_frac):
     assert np.array_equal(sc, want_sc)
 
 
+@pytest.mark.parametrize("divisor", [-1, 96])
+def test_k_above_1024(dev, divisor):
+    """Above the radix select's 1024 the search selects from the raw scorer's buffer (the
+    reference's ``at::topk`` path, fork_search_cuda.cu:843-915): IVF probes with a full-N mask,
+    and the one-list table."""
+    g = rng(140)
+    n, d, b, k = 30_000, 128, 4, 1500
+    items, offsets, sizes, perm = _ivf(g, n, d, 40)
+    items = (items // 32).astype(np.int8)  # narrow codes: tied keys across slots
+    q = g.standard_normal((b, d)).astype(np.float32)
+    probes = np.stack([g.permutation(40)[:12] for _ in range(b)]).astype(np.int64)
+    probes[1, 0] = 10**6
+    width = int(max(sizes[probes[r][probes[r] < 40]].sum() for r in range(b)))
+    valid = g.random((b, n)) < 0.7
+    ids, sc = _run(dev, q, probes, offsets, sizes, items, perm, 0.5, k, width, divisor,
+                   filtering_bit_mask=_t(dev, _pack(valid)))
+    want_ids, want_sc = ost.search(q, probes, offsets, sizes, items, perm, [0.5], k, width,
+                                   divisor, valid)
+    assert np.array_equal(ids, want_ids)
+    assert np.array_equal(sc, want_sc)
+    one = np.array([0], np.int64), np.array([n], np.int64)
+    probes1 = np.zeros((b, 1), np.int64)
+    ids, sc = _run(dev, q, probes1, *one, items, perm, 0.5, 2000, n, divisor)
+    want_ids, want_sc = ost.search(q, probes1, *one, items, perm, [0.5], 2000, n, divisor)
+    assert np.array_equal(ids, want_ids)
+    assert np.array_equal(sc, want_sc)
+
+
 def test_ties_go_to_the_lower_slot(dev):
     g = rng(104)
     n, d = 5000, 64
