@@ -72,8 +72,9 @@ int rt_dense_scan_topk(const void* queries, int64_t B, const void* items, int64_
 
 /* Large-batch form of rt_int8_scan_topk / rt_dense_scan_topk (same results): register-blocked
  * 32x32 MFMA tiles, 256 queries per workgroup held in registers, item tiles shared through
- * LDS. dtype 0 = int8 (int32 scores), 1 = bf16, 2 = fp16 (float scores). Rows of 128, 256 or
- * 512 bytes (int8 D in {128, 256, 512}; 16-bit D in {64, 128, 256}). `row_bytes` of the
+ * LDS. dtype 0 = int8 (int32 scores), 1 = bf16, 2 = fp16, 3 = fp32 (float scores). Rows of
+ * 128, 256 or 512 bytes (int8 D in {128, 256, 512}; 16-bit D in {64, 128, 256}; fp32 D in
+ * {32, 64, 128}). `row_bytes` of the
  * workspace function is D times the element size; `masked` != 0 sizes it for a call with a mask
  * (the mask is transposed into the workspace, ceil(N/64) x B words rounded up to 256 queries).
  * Replaces: the same reference paths as rt_int8_scan_topk / rt_dense_scan_topk at batches

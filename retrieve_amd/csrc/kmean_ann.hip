@@ -19,6 +19,7 @@
 //
 // Layout: a group of L lanes (L * 16 bytes of a row per step) scores one slot, 64 / L slots a
 // wave; the query row is staged in LDS; partial sums meet by xor-shuffles.
+#include "profile.h"
 #include "scan_common.h"
 
 namespace rt {
@@ -340,6 +341,8 @@ extern "C" int rt_fused_kmean_ann(
   gx = gx < 1 ? 1 : gx;
   const size_t lds = static_cast<size_t>(4 * n_probe + 1) * sizeof(int64_t) + rb;
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(B));
+  hipEvent_t stop;
+  profile_begin(stream, &stop);
   switch (elem) {
     case kElemI8:
       fused_kmean_ann_kernel<kElemI8><<<grid, kKmThreads, lds, stream>>>(a);
@@ -354,6 +357,7 @@ extern "C" int rt_fused_kmean_ann(
       fused_kmean_ann_kernel<kElemF32><<<grid, kKmThreads, lds, stream>>>(a);
       break;
   }
+  profile_end(stream, stop);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }

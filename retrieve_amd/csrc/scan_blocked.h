@@ -39,6 +39,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
@@ -178,6 +179,21 @@ struct F16x32 : BF16x32 {
   __device__ static Acc mma(v4i a, v4i b, Acc c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a),
                                                   __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+  }
+};
+
+// fp32 rows on the fp32 matrix cores (v_mfma_f32_32x32x2_f32): a K step's 16 bytes per lane are
+// four floats, lane half h holding elements 4 h + i of the step's eight; product i pairs element
+// i of both halves, on both operands alike, so the four products sum the step's dot product (in
+// another order than a sequential sum).
+struct F32x32 : BF16x32 {
+  __device__ static Acc mma(v4i a, v4i b, Acc c) {
+    const v4f fa = __builtin_bit_cast(v4f, a);
+    const v4f fb = __builtin_bit_cast(v4f, b);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.x, fb.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.y, fb.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.z, fb.z, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(fa.w, fb.w, c, 0, 0, 0);
   }
 };
 
@@ -992,6 +1008,10 @@ int blocked_scan_bf16(const void* queries, int64_t B, const void* items, int64_t
                       int64_t* out_ids, void* out_scores, void* workspace,
                       size_t workspace_bytes, hipStream_t stream);
 int blocked_scan_f16(const void* queries, int64_t B, const void* items, int64_t N,
+                     int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
+                     int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream);
+int blocked_scan_f32(const void* queries, int64_t B, const void* items, int64_t N,
                      int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                      int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
                      hipStream_t stream);

@@ -10,7 +10,7 @@ extern "C" size_t rt_blocked_scan_topk_workspace(int64_t B, int64_t N, int64_t r
   return blk_plan(B, N, k, row_bytes, kMaxResidentWorkgroups, false, masked != 0).total;
 }
 
-// dtype: 0 int8 (int32 scores), 1 bf16, 2 fp16 (float scores); D elements per row.
+// dtype: 0 int8 (int32 scores), 1 bf16, 2 fp16, 3 fp32 (float scores); D elements per row.
 extern "C" int rt_blocked_scan_topk(const void* queries, int64_t B, const void* items, int64_t N,
                                     int64_t D, int64_t k, int dtype, const uint64_t* mask,
                                     int64_t mask_words, int64_t* out_ids, void* out_scores,
@@ -25,8 +25,12 @@ extern "C" int rt_blocked_scan_topk(const void* queries, int64_t B, const void* 
     case 2:
       return blocked_scan_f16(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
                               out_scores, workspace, workspace_bytes, stream);
+    case 3:
+      return blocked_scan_f32(queries, B, items, N, 4 * D, k, mask, mask_words, out_ids,
+                              out_scores, workspace, workspace_bytes, stream);
     default:
-      set_error("blocked scan dtype must be 0 (int8), 1 (bf16) or 2 (fp16), got %d", dtype);
+      set_error("blocked scan dtype must be 0 (int8), 1 (bf16), 2 (fp16) or 3 (fp32), got %d",
+                dtype);
       return kInvalidType;
   }
 }

@@ -145,15 +145,16 @@ _DENSE_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 def dense_scan_topk(
     query: Tensor, item_embs: Tensor, k: int, mask: Tensor | None = None
 ) -> tuple[Tensor, Tensor]:
-    """Dense full-scan top-k: ``query [B, D]`` against ``item_embs [N, D]`` (both bf16 or both
-    fp16), fp32 accumulation, top ``k`` by (score desc, index asc) → ``(ids int64 [B, k],
-    scores fp32 [B, k])``, ``-1`` / ``-inf`` where fewer than ``k`` items pass ``mask``. LiNR
-    V1's ``torch.mm`` + ``masked_topk`` (``modules/knn.py:62-76``) without the ``[B, N]``
-    score matrix."""
+    """Dense full-scan top-k: ``query [B, D]`` against ``item_embs [N, D]`` (both bf16, both
+    fp16 or both fp32: the fused scan for the 16-bit types up to k 1024, the raw scorer and a
+    key select otherwise), fp32 accumulation, top ``k`` by (score desc, index asc) →
+    ``(ids int64 [B, k], scores fp32 [B, k])``, ``-1`` / ``-inf`` where fewer than ``k`` items
+    pass ``mask``. LiNR V1's ``torch.mm`` + ``masked_topk`` (``modules/knn.py:62-76``); the
+    fused scan has no ``[B, N]`` score matrix."""
     if query.dim() != 2 or item_embs.dim() != 2:
         raise ValueError("query must be [B, D] and item_embs [N, D]")
-    if query.dtype not in _DENSE_DTYPES or item_embs.dtype != query.dtype:
-        raise TypeError("query and item_embs must both be bfloat16 or both float16")
+    if query.dtype not in (*_DENSE_DTYPES, torch.float32) or item_embs.dtype != query.dtype:
+        raise TypeError("query and item_embs must both be bfloat16, float16 or float32")
     if query.shape[1] != item_embs.shape[1]:
         raise ValueError(f"D mismatch: query D={query.shape[1]} vs item D={item_embs.shape[1]}")
     if k < 1:
@@ -169,12 +170,17 @@ def dense_scan_topk(
         mask = mask.contiguous()
     q = query.contiguous()
     dev = nat.require_device(q, item_embs)
-    if k > MAX_FUSED_K:
+    fp32 = q.dtype == torch.float32
+    if k > MAX_FUSED_K or (fp32 and not _use_blocked(b, 4 * d, k)):
+        # every score kept in fp32, then the select (fp32 rows below the blocked scan's batch)
         from retrieve_amd import large_k
 
         return large_k.full_scan_topk(q, item_embs, k, mask, float("-inf"))
     ids = torch.empty((b, k), dtype=torch.int64, device=dev)
     scores = torch.empty((b, k), dtype=torch.float32, device=dev)
+    if fp32:
+        _blocked(q, item_embs, k, 3, mask, ids, scores)
+        return ids, scores
     if _use_blocked(b, 2 * d, k):
         _blocked(q, item_embs, k, 1 + _DENSE_DTYPES[q.dtype], mask, ids, scores)
         return ids, scores

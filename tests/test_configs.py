@@ -1,6 +1,10 @@
 """Every BASELINE configuration's kernels at the batch shape the configuration runs, against the
 oracle:
 
+- configuration 1 (exact inner-product top-100, 100k x 128 fp32 L2-normalised rows, 1024
+  queries; the reference runs it with torch.mm + torch.topk on the CPU): the same problem on the
+  GPU in fp32 (the raw scorer and the key select), at full size, with duplicated rows whose
+  equal scores must come back in index order;
 - configuration 2 (bf16 10M x 128, B in {1, 64, 1024, 4096}): B = 512 / 1024 over 2.2M clustered
   rows, the narrow 256-byte-row layout with the seed pass, the threshold sample pass over every
   16th tile and the main pass, masked and unmasked, bf16 and fp16, with rows whose only survivors
@@ -35,6 +39,19 @@ pytestmark = pytest.mark.gpu
 
 CARDINALITIES = (16, 32, 64, 128, 256, 512, 1000, 1000)
 BLOOM_BITS, BLOOM_K, HASH_K = 64, 3, 7
+
+
+def test_config1_exact_fp32(dev):
+    g = rng(1001)
+    n, d, b, k = 100_000, 128, 1024, 100
+    x = g.standard_normal((n, d))
+    items = (x / np.linalg.norm(x, axis=1, keepdims=True)).astype(np.float32)
+    qx = g.standard_normal((b, d))
+    q = (qx / np.linalg.norm(qx, axis=1, keepdims=True)).astype(np.float32)
+    # exact ties: copies of a query's own direction at three indices
+    items[[500, 70_000, 99_999]] = q[3]
+    ids = _dense_check(dev, q, items, k, dtype=torch.float32)
+    assert ids[3, :3].tolist() == [500, 70_000, 99_999]
 
 
 # --- packed masks too large to unpack whole ----------------------------------------------------

@@ -125,6 +125,19 @@ def test_k_above_1024(dev, dtype):
     _check(dev, q, it, 1500, dtype=dtype, mask=mask)
 
 
+@pytest.mark.parametrize("b,n,d,masked", [(8, 5000, 128, False), (64, 20000, 128, True),
+                                            (256, 30000, 128, False), (300, 20000, 64, True),
+                                            (128, 9000, 32, False)])
+def test_fp32(dev, b, n, d, masked):
+    """fp32 rows: the blocked scan on the fp32 matrix cores from B = 32 (wide and narrow layouts,
+    D 32 / 64 / 128), the raw scorer and key select below."""
+    g = rng(45 + b + d)
+    q = g.standard_normal((b, d)).astype(np.float32)
+    it = g.standard_normal((n, d)).astype(np.float32)
+    mask = (g.random((b, n)) < 0.3) if masked else None
+    _check(dev, q, it, 100, dtype=torch.float32, mask=mask)
+
+
 def test_errors(dev):
     q = torch.zeros((2, 64), dtype=torch.bfloat16, device=dev)
     it = torch.zeros((10, 64), dtype=torch.bfloat16, device=dev)
