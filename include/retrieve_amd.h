@@ -313,6 +313,28 @@ int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64_t B, const
                   int64_t* out_ids, float* out_scores, void* workspace, size_t workspace_bytes,
                   rt_stream_t stream);
 
+/* rt_ivf_search with the reference's per-payload filters in place of a full-N mask: the probed
+ * payloads' Bloom words in rt_bloom_search_columns' partial layout (entry b * n_probe + j for
+ * probe j of row b: its docs from bit partial_first_offsets[e] of words
+ * partial_counts_cumsum[e - 1] ...; null: no Bloom filter), and / or the exact recheck of the
+ * probed docs in the slot layout (clause_slot_values [R, N] int32, clause c in rows
+ * clause_slots[c] .. clause_slots[c + 1], clause_is_reverse [C] int8, query_clause_values [B, C]
+ * int32 with -1 inactive; null: none; C <= 32). A doc is scored when every given filter passes.
+ * Replaces: the payload filtering of st::search (fork_search_cuda.cu:1305-1342; the exact
+ *   payloads of :918-1130 and fork_filters.cuh:15-41; the bloom partial payloads of
+ *   bloom_index_search_cuda.cu:1945-2063). */
+int rt_ivf_search_payload_filters(
+    const int8_t* q_codes, const float* q_scales, int64_t B, const int8_t* item_codes, int64_t N,
+    int64_t D, const int64_t* probe_ids, int64_t n_probe, const int64_t* cluster_offsets,
+    const int64_t* cluster_sizes, int64_t n_lists, int64_t width,
+    const int32_t* partial_counts_cumsum, const int8_t* partial_first_offsets,
+    const uint64_t* partial_words, int64_t partial_entries, int64_t partial_n_words,
+    const int32_t* clause_slot_values, int64_t R, const int64_t* clause_slots, int64_t C,
+    const int8_t* clause_is_reverse, const int32_t* query_clause_values, int64_t divisor,
+    const int64_t* sort_perm, int64_t n_perm, const float* global_scale, int64_t k,
+    int64_t* out_ids, float* out_scores, void* workspace, size_t workspace_bytes,
+    rt_stream_t stream);
+
 /* SilverTorch's raw scorer: every probed doc's score in its slot of a [B, width] buffer.
  * Row b's probes j hold cluster_length[b, j] docs from cluster_offsets[cluster_ids[b, j]]
  * (n_offsets entries; an id outside them, or a cluster reaching outside the table, is empty);

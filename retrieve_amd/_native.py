@@ -84,6 +84,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
     ),
     "rt_ivf_search_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),
+    "rt_ivf_search_payload_filters": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64,
+         _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64,
+         _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],
+    ),
     "rt_ivf_search": (
         _c_int,
         [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_p,

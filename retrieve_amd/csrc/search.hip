@@ -149,6 +149,21 @@ struct IvfArgs {
   int64_t width;
   const uint64_t* mask;  // [B, mask_words], item position d at bit 63 - d % 64, or null
   int64_t mask_words;
+  // or the probed payloads' Bloom words (rt_bloom_search_columns' layout): entry e = b * n_probe
+  // + j covers probe j's docs from bit pfirst[e] of words pcum[e - 1] ... (null: none)
+  const int32_t* pcum;
+  const int8_t* pfirst;
+  const uint64_t* pwords;
+  int64_t p_entries;
+  int64_t p_words;
+  // and / or the exact clauses in the slot layout (slots [R, N] int32, clause c in rows
+  // cslots[c] .. cslots[c + 1], query values qv [B, C], -1 inactive; null: none)
+  const int32_t* slots;
+  int64_t R;
+  const int64_t* cslots;
+  int C;
+  const int8_t* reverse;  // [C], non-zero: a reverse clause
+  const int32_t* qv;
   int divisor;  // -1: int32 keys
   int k;
   int capw;
@@ -217,6 +232,36 @@ __device__ inline uint32_t search_key(int32_t dot, int divisor) {
   return key_of_f32(static_cast<float>(h));
 }
 
+// Bit `off` of probe j's payload in row b's Bloom words (out of range: no match), as
+// fused_kmean_ann_with_partial_masks reads it (fused_kmean_ann_cuda.cu:2264-2501).
+__device__ inline bool payload_bit(const IvfArgs& a, int64_t b, int64_t j, int64_t off) {
+  const int64_t e = b * a.n_probe + j;
+  if (e >= a.p_entries) return false;
+  const int64_t w0 = e == 0 ? 0 : static_cast<int64_t>(a.pcum[e - 1]);
+  const int64_t bit = static_cast<int64_t>(a.pfirst[e]) + off;
+  const int64_t w = w0 + (bit >> 6);
+  return bit >= 0 && w < a.p_words && ((a.pwords[w] >> (63 - (bit & 63))) & 1ull);
+}
+
+// The exact recheck of one probed doc (fork_filters.cuh:15-41): every active clause matches
+// (one of the doc's values equals the query's), negated for a reverse clause.
+__device__ inline bool exact_pass(const IvfArgs& a, int64_t b, int64_t pos, uint32_t rev_mask) {
+  const int32_t* q = a.qv + b * a.C;
+  uint32_t active = 0;
+  uint32_t match = 0;
+  for (int c = 0; c < a.C; ++c) {
+    const int32_t v = q[c];
+    if (v == -1) continue;
+    active |= 1u << c;
+    bool eq = false;
+    const int64_t r0 = a.cslots[c] > 0 ? a.cslots[c] : 0;
+    const int64_t r1 = a.cslots[c + 1] < a.R ? a.cslots[c + 1] : a.R;  // rows inside the table
+    for (int64_t r = r0; r < r1; ++r) eq |= a.slots[r * a.N + pos] == v;
+    match |= eq ? 1u << c : 0u;
+  }
+  return ((match ^ rev_mask) & active) == active;
+}
+
 template <int L, int NC>
 __global__ void __launch_bounds__(kIvfThreads) ivf_scan_kernel(IvfArgs a) {
   constexpr int R = kWave / L;
@@ -248,6 +293,10 @@ __global__ void __launch_bounds__(kIvfThreads) ivf_scan_kernel(IvfArgs a) {
                         : v4i{0, 0, 0, 0};
   }
   const uint64_t* mrow = a.mask != nullptr ? a.mask + b * a.mask_words : nullptr;
+  uint32_t rev_mask = 0;
+  if (a.qv != nullptr) {
+    for (int c = 0; c < a.C; ++c) rev_mask |= a.reverse[c] != 0 ? 1u << c : 0u;
+  }
 
   uint64_t tau = 0;
   int cnt = 0;
@@ -259,7 +308,13 @@ __global__ void __launch_bounds__(kIvfThreads) ivf_scan_kernel(IvfArgs a) {
     if (ok) {
       const int64_t j = range_of(prefix, nr, s);
       pos = start[j] + (s - prefix[j]);
-      if (mrow != nullptr) ok = (mrow[pos >> 6] >> (63 - (pos & 63))) & 1ull;
+      if (mrow != nullptr) {
+        ok = (mrow[pos >> 6] >> (63 - (pos & 63))) & 1ull;
+      } else if (a.pwords != nullptr) {
+        const int64_t p = j < a.n_probe ? j : j - a.n_probe;  // the probe of range j
+        ok = payload_bit(a, b, p, pos - start[p]);
+      }
+      if (ok && a.qv != nullptr) ok = exact_pass(a, b, pos, rev_mask);
     }
     int32_t dot = 0;
     if (ok) {
@@ -428,15 +483,14 @@ extern "C" size_t rt_ivf_search_workspace(int64_t B, int64_t width, int64_t k) {
 
 // Top-k over each row's probed ranges of int8 codes (slots, ties to the lower slot), then the
 // epilogue: out_ids = sort_perm[position] (-1 pads), out_scores dequantized (-inf pads).
-extern "C" int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64_t B,
-                             const int8_t* item_codes, int64_t N, int64_t D,
-                             const int64_t* probe_ids, int64_t n_probe,
-                             const int64_t* cluster_offsets, const int64_t* cluster_sizes,
-                             int64_t n_lists, int64_t width, const uint64_t* mask,
-                             int64_t mask_words, int64_t divisor, const int64_t* sort_perm,
-                             int64_t n_perm, const float* global_scale, int64_t k,
-                             int64_t* out_ids, float* out_scores, void* workspace,
-                             size_t workspace_bytes, hipStream_t stream) {
+static int ivf_search(const int8_t* q_codes, const float* q_scales, int64_t B,
+                      const int8_t* item_codes, int64_t N, int64_t D, const int64_t* probe_ids,
+                      int64_t n_probe, const int64_t* cluster_offsets,
+                      const int64_t* cluster_sizes, int64_t n_lists, int64_t width,
+                      const uint64_t* mask, int64_t mask_words, const IvfArgs& filters,
+                      int64_t divisor, const int64_t* sort_perm, int64_t n_perm,
+                      const float* global_scale, int64_t k, int64_t* out_ids, float* out_scores,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
   RT_CHECK_ARG(B >= 0 && N >= 0 && n_probe >= 0 && n_lists >= 0 && width >= 0,
                "sizes must be >= 0");
   RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
@@ -473,6 +527,17 @@ extern "C" int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64
   a.width = width;
   a.mask = mask;
   a.mask_words = mask_words;
+  a.pcum = filters.pcum;
+  a.pfirst = filters.pfirst;
+  a.pwords = filters.pwords;
+  a.p_entries = filters.p_entries;
+  a.p_words = filters.p_words;
+  a.slots = filters.slots;
+  a.R = filters.R;
+  a.cslots = filters.cslots;
+  a.C = filters.C;
+  a.reverse = filters.reverse;
+  a.qv = filters.qv;
   a.divisor = static_cast<int>(divisor);
   a.k = static_cast<int>(k);
   a.capw = capw;
@@ -540,6 +605,61 @@ extern "C" int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64
   search_epilogue_kernel<<<static_cast<unsigned>(B), kIvfThreads, lds, stream>>>(e);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
+}
+
+extern "C" int rt_ivf_search(const int8_t* q_codes, const float* q_scales, int64_t B,
+                             const int8_t* item_codes, int64_t N, int64_t D,
+                             const int64_t* probe_ids, int64_t n_probe,
+                             const int64_t* cluster_offsets, const int64_t* cluster_sizes,
+                             int64_t n_lists, int64_t width, const uint64_t* mask,
+                             int64_t mask_words, int64_t divisor, const int64_t* sort_perm,
+                             int64_t n_perm, const float* global_scale, int64_t k,
+                             int64_t* out_ids, float* out_scores, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream) {
+  const IvfArgs none{};
+  return ivf_search(q_codes, q_scales, B, item_codes, N, D, probe_ids, n_probe, cluster_offsets,
+                    cluster_sizes, n_lists, width, mask, mask_words, none, divisor, sort_perm,
+                    n_perm, global_scale, k, out_ids, out_scores, workspace, workspace_bytes,
+                    stream);
+}
+
+// rt_ivf_search with the reference's per-payload filters in place of a full-N mask: the probed
+// payloads' Bloom words (partial response, may be null) and / or the exact clause recheck over
+// the probed docs (slot layout, may be null); a doc is scored when both pass.
+extern "C" int rt_ivf_search_payload_filters(
+    const int8_t* q_codes, const float* q_scales, int64_t B, const int8_t* item_codes, int64_t N,
+    int64_t D, const int64_t* probe_ids, int64_t n_probe, const int64_t* cluster_offsets,
+    const int64_t* cluster_sizes, int64_t n_lists, int64_t width,
+    const int32_t* partial_counts_cumsum, const int8_t* partial_first_offsets,
+    const uint64_t* partial_words, int64_t partial_entries, int64_t partial_n_words,
+    const int32_t* clause_slot_values, int64_t R, const int64_t* clause_slots, int64_t C,
+    const int8_t* clause_is_reverse, const int32_t* query_clause_values, int64_t divisor,
+    const int64_t* sort_perm, int64_t n_perm, const float* global_scale, int64_t k,
+    int64_t* out_ids, float* out_scores, void* workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+  RT_CHECK_ARG(partial_words == nullptr ||
+                   (partial_counts_cumsum != nullptr && partial_first_offsets != nullptr &&
+                    partial_entries >= 0 && partial_n_words >= 0),
+               "the partial masks need their counts and first offsets");
+  RT_CHECK_ARG(query_clause_values == nullptr ||
+                   (clause_slots != nullptr && clause_is_reverse != nullptr && C >= 0 &&
+                    C <= 32 && R >= 0 && (R == 0 || clause_slot_values != nullptr)),
+               "the exact clauses need slots, clause_slots and clause_is_reverse, C <= 32");
+  IvfArgs f{};
+  f.pcum = partial_counts_cumsum;
+  f.pfirst = partial_first_offsets;
+  f.pwords = partial_words;
+  f.p_entries = partial_entries;
+  f.p_words = partial_n_words;
+  f.slots = clause_slot_values;
+  f.R = R;
+  f.cslots = clause_slots;
+  f.C = static_cast<int>(C);
+  f.reverse = clause_is_reverse;
+  f.qv = query_clause_values;
+  return ivf_search(q_codes, q_scales, B, item_codes, N, D, probe_ids, n_probe, cluster_offsets,
+                    cluster_sizes, n_lists, width, nullptr, 0, f, divisor, sort_perm, n_perm,
+                    global_scale, k, out_ids, out_scores, workspace, workspace_bytes, stream);
 }
 
 // The epilogue alone, for a full scan's results: in_ids are item positions (-1 empty), raw the

@@ -717,6 +717,48 @@ def _capturing() -> bool:
     return torch.cuda.is_current_stream_capturing()
 
 
+# (id, version) of cluster_sizes -> its largest cluster (the payload columns' static bound)
+_MAX_CLUSTER: dict = {}
+
+
+def _max_cluster(sizes: Tensor) -> int | None:
+    """The largest cluster of an index, read back once per index (kept until the tensor is freed
+    or modified in place); None under graph capture with nothing kept."""
+    import weakref
+
+    key = (id(sizes), sizes._version)
+    hit = _MAX_CLUSTER.get(key)
+    if hit is None:
+        if _capturing():
+            return None
+        hit = int(sizes.max().item()) if sizes.numel() else 0
+        _MAX_CLUSTER[key] = hit
+        weakref.finalize(sizes, _MAX_CLUSTER.pop, key, None)
+    return hit
+
+
+def _payload_bloom(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max_stack_size,
+                   bloom_k, hash_k, query_plan_index, probes, offs, sizes):
+    """The Bloom words of every row's probed payloads only (``bloom_index_search_cuda.cu:
+    1945-2063``, ``partial_response``'s layout): ``(column_counts_cumsum, first_offsets,
+    words)``, entry ``b * n_probe + j`` for probe ``j`` of row ``b``; None when no column bound
+    is at hand (a capture before the first eager search on this index)."""
+    biggest = _max_cluster(sizes)
+    if biggest is None:
+        return None
+    n_lists = offs.numel()
+    valid = (probes >= 0) & (probes < n_lists)
+    cluster = torch.where(valid, probes, 0)
+    starts = torch.where(valid, offs[cluster], 0).contiguous()
+    lengths = torch.where(valid, sizes[cluster], 0).contiguous()
+    # a payload of at most `biggest` docs spans at most biggest / 64 + 2 columns
+    max_columns = probes.numel() * ((biggest + 63) // 64 + 1)
+    qpi = None if query_plan_index is None else query_plan_index.to(torch.int64)
+    return _partial_response_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count,
+                                      max_stack_size, starts, lengths, bloom_k, hash_k, qpi,
+                                      max_columns)
+
+
 # Row widths (int8 D) the full-scan kernels take; other widths run the IVF kernel.
 _FULL_SCAN_D = (64, 128, 256, 512, 768, 1024)
 # (id, version) of cluster_offsets and cluster_sizes, and N -> whether the one list is [0, N).
@@ -775,30 +817,6 @@ def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sor
     b, d = query.shape
     n = item_codes.shape[0]
     codes, scales = quantize_rows(query)
-    mask = None
-    if filtering_bit_mask is not None:
-        mask = filtering_bit_mask.to(torch.int64).contiguous()
-    if plans is not None:
-        if bloom_index is None or bloom_bundle_b_offsets is None:
-            raise RuntimeError("plans need bloom_index and bloom_bundle_b_offsets")
-        bm = _search_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count,
-                              max_stack_size, bloom_k, hash_k, False)
-        mask = bm[query_plan_index.to(torch.int64)] if query_plan_index is not None else bm[:b]
-        mask = mask.contiguous()
-    if exact:
-        out = torch.empty((b, (n + 63) // 64), dtype=torch.int64, device=dev)
-        slots = item_clause_attrs.to(torch.int32).contiguous()
-        cs = clause_slots.to(torch.int64).contiguous()
-        rev = clause_is_reverse.to(torch.int8).contiguous()
-        qv = query_clause_attrs.to(torch.int64)
-        qv = torch.where((qv >= -1) & (qv <= 2**31 - 1), qv, -(2**31)).to(torch.int32)
-        with torch.cuda.device(dev):
-            st = nat.lib().rt_clause_slots_filter(
-                nat.ptr(slots), slots.shape[0] if slots.dim() == 2 else 0, n, nat.ptr(cs),
-                cs.numel() - 1, nat.ptr(rev), nat.ptr(qv.contiguous()), b, nat.ptr(mask),
-                0 if mask is None else mask.shape[1], nat.ptr(out), nat.stream(dev))
-        nat.check(st)
-        mask = out
     width = (int(max_tensor_size_per_row) + 31) // 32 * 32
     ids = torch.empty((b, k), dtype=torch.int64, device=dev)
     scores = torch.empty((b, k), dtype=torch.float32, device=dev)
@@ -810,12 +828,66 @@ def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sor
     sizes = cluster_sizes.to(torch.int64).contiguous()
     probes = probe_ids.to(torch.int64).contiguous()
     lib = nat.lib()
-    if k > MAX_SEARCH_K:
-        return _search_large_k(codes, scales, item_codes, probes, offs, sizes, width, mask,
-                               int(divisor_for_int8), perm, gs, k)
+    if plans is not None and (bloom_index is None or bloom_bundle_b_offsets is None):
+        raise RuntimeError("plans need bloom_index and bloom_bundle_b_offsets")
+    if exact:
+        slots = item_clause_attrs.to(torch.int32).contiguous()
+        cs = clause_slots.to(torch.int64).contiguous()
+        rev = clause_is_reverse.to(torch.int8).contiguous()
+        qv = query_clause_attrs.to(torch.int64)
+        qv = torch.where((qv >= -1) & (qv <= 2**31 - 1), qv, -(2**31)).to(torch.int32)
+        qv = qv.contiguous()
     full = (divisor_for_int8 == -1 and offs.numel() == 1 and probes.shape[1] == 1
             and width >= n and d in _FULL_SCAN_D
             and _one_list_is_the_table(cluster_offsets, cluster_sizes, n))
+    if not full and k <= MAX_SEARCH_K and filtering_bit_mask is None and (plans is not None
+                                                                          or exact):
+        # the IVF kernel with the reference's per-payload filters: Bloom words of the probed
+        # columns only, the exact recheck of the probed docs only
+        partial = None
+        if plans is not None:
+            partial = _payload_bloom(bloom_index, bloom_bundle_b_offsets, plans, plan_count,
+                                     max_stack_size, bloom_k, hash_k, query_plan_index, probes,
+                                     offs, sizes)
+        if partial is not None or plans is None:
+            cum, first, words = partial if partial is not None else (None, None, None)
+            ws = nat.workspace(lib.rt_ivf_search_workspace(b, width, k), dev)
+            with torch.cuda.device(dev):
+                st = lib.rt_ivf_search_payload_filters(
+                    nat.ptr(codes), nat.ptr(scales), b, nat.ptr(item_codes), n, d,
+                    nat.ptr(probes), probes.shape[1], nat.ptr(offs), nat.ptr(sizes), offs.numel(),
+                    width, nat.ptr(cum), nat.ptr(first), nat.ptr(words),
+                    0 if first is None else first.numel(), 0 if words is None else words.numel(),
+                    nat.ptr(slots) if exact else None,
+                    (slots.shape[0] if slots.dim() == 2 else 0) if exact else 0,
+                    nat.ptr(cs) if exact else None, cs.numel() - 1 if exact else 0,
+                    nat.ptr(rev) if exact else None, nat.ptr(qv) if exact else None,
+                    int(divisor_for_int8), nat.ptr(perm), perm.numel(), nat.ptr(gs), k,
+                    nat.ptr(ids), nat.ptr(scores), nat.ptr(ws), ws.numel(), nat.stream(dev))
+            nat.check(st)
+            return ids, scores
+    # a full-N mask: the one-list full scan, top-k above 1024, a caller's mask, or a capture
+    # with no cached column bound for the per-payload Bloom words
+    mask = None
+    if filtering_bit_mask is not None:
+        mask = filtering_bit_mask.to(torch.int64).contiguous()
+    if plans is not None:
+        bm = _search_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count,
+                              max_stack_size, bloom_k, hash_k, False)
+        mask = bm[query_plan_index.to(torch.int64)] if query_plan_index is not None else bm[:b]
+        mask = mask.contiguous()
+    if exact:
+        out = torch.empty((b, (n + 63) // 64), dtype=torch.int64, device=dev)
+        with torch.cuda.device(dev):
+            st = lib.rt_clause_slots_filter(
+                nat.ptr(slots), slots.shape[0] if slots.dim() == 2 else 0, n, nat.ptr(cs),
+                cs.numel() - 1, nat.ptr(rev), nat.ptr(qv), b, nat.ptr(mask),
+                0 if mask is None else mask.shape[1], nat.ptr(out), nat.stream(dev))
+        nat.check(st)
+        mask = out
+    if k > MAX_SEARCH_K:
+        return _search_large_k(codes, scales, item_codes, probes, offs, sizes, width, mask,
+                               int(divisor_for_int8), perm, gs, k)
     if full:
         # one list holding every item in order: slot = position, the full-scan kernels; a row
         # whose probe is not list 0 has no slot and ends as pads

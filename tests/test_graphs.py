@@ -102,6 +102,30 @@ def test_search_one_list(dev):
     print("graph: st::search IVF fp16 keys, masked", flush=True)
     _replays_match(ivf)
 
+    # Bloom plans over the probed payloads only, with the exact recheck (the column bound comes
+    # from the eager calls before the capture)
+    attrs = _zipf_attrs(g, n)
+    sets = _query_sets(g, attrs, b, 0.1)
+    at = torch.from_numpy(attrs).to(dev)
+    fid, fo, fv = st.attrs_to_features(at)
+    words, boffs = torch.ops.st.bloom_index_build_fixed(fid, fo, fv, 64, 3)
+    blob, count, stack = st.prepare_plans(bl.sets_to_expressions(sets), 7, dev)
+    slots = at[:, :, 0].t().contiguous().to(torch.int32)
+    cs = torch.arange(attrs.shape[1] + 1, dtype=torch.int64, device=dev)
+    rev = torch.zeros(attrs.shape[1], dtype=torch.bool, device=dev)
+    qa = torch.full((b, attrs.shape[1]), -1, dtype=torch.int64, device=dev)
+    qa[:, 0] = at[:b, 0, 0]  # one active clause: the value of a doc each row can match
+
+    def payload():
+        return torch.ops.st.search(query, pr, so, ss, items, perm, gs, 50, int(n),
+                                   bloom_index=words, bloom_bundle_b_offsets=boffs, plans=blob,
+                                   plan_count=count, max_stack_size=stack, bloom_k=3, hash_k=7,
+                                   item_clause_attrs=slots, clause_slots=cs,
+                                   clause_is_reverse=rev, query_clause_attrs=qa)
+
+    print("graph: st::search IVF, payload Bloom + exact recheck", flush=True)
+    _replays_match(payload)
+
 
 def test_dense_and_hamming_masked(dev):
     """Configuration 3's masked register-blocked bf16 scan (B = 256, the mask transposed in the

@@ -230,6 +230,19 @@ def test_filters(dev):
                    bloom_index=words, bloom_bundle_b_offsets=boffs, plans=blob,
                    plan_count=count, max_stack_size=max_stack, bloom_k=3, hash_k=7, **kw)
     assert np.array_equal(ids, want[0]) and np.array_equal(sc, want[1])
+    # Bloom plans alone, evaluated on the probed payloads' columns only: the Bloom mask's result
+    # (false positives included), with the plans in another order than the rows
+    wn, bn = words.cpu().numpy(), boffs.cpu().numpy()
+    bloom = np.stack([of.bloom_expression_mask(wn, bn, n, e, 3, 7) for e in exprs])
+    order = g.permutation(b)
+    blob2, count2, stack2 = st.prepare_plans([exprs[i] for i in order], 7, dev)
+    qpi = np.argsort(order).astype(np.int64)  # row r's plan: where exprs[r] went
+    ids, sc = _run(dev, q, probes, offsets, sizes, items, perm, 1.0, k, width,
+                   bloom_index=words, bloom_bundle_b_offsets=boffs, plans=blob2,
+                   plan_count=count2, max_stack_size=stack2, bloom_k=3, hash_k=7,
+                   query_plan_index=_t(dev, qpi))
+    want = ost.search(q, probes, offsets, sizes, items, perm, [1.0], k, width, valid=bloom)
+    assert np.array_equal(ids, want[0]) and np.array_equal(sc, want[1])
 
 
 def test_errors(dev):
