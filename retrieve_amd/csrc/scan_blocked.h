@@ -52,10 +52,11 @@ constexpr int64_t kBlkWideMaxBatch = 128;
 
 // Rows per staged tile: 32 for narrow 512-byte rows, so four stages fit in half the LDS; 128
 // for the wide layout below 512-byte rows (its row quarters are 32 rows); 64 otherwise; for
-// 64-byte bit-code rows as many as make a tile one 16-byte load per thread (64 narrow, 128
-// wide).
+// 64-byte bit-code rows 128 wide (one 16-byte load per thread) and 32 narrow (one row tile per
+// wave, so its accumulators and the query fragments fit in registers; the first two waves load
+// the 2 KiB tile).
 constexpr int blk_rows(int64_t row_bytes, bool wide, bool bits) {
-  return bits ? (wide ? 128 : 64)
+  return bits ? (wide ? 128 : 32)
               : (wide ? (row_bytes < 512 ? 128 : 64) : (row_bytes >= 512 ? 32 : 64));
 }
 
@@ -205,6 +206,9 @@ constexpr int kBlkMinStages = 3;
 // rows.
 constexpr int blk_mask_bytes(int rows) { return kBlkQpg * (rows / 32) * 4; }
 
+// LDS of the bit codes' byte-expansion table (256 entries of 8 bytes).
+constexpr size_t kBitsLutBytes = 256 * sizeof(uint64_t);
+
 // Waves per SIMD: two (one 8-wave or two 4-wave workgroups per CU).
 constexpr int kBlkWavesPerSimd = 2;
 
@@ -304,7 +308,10 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   constexpr int kBlkThreads = L::threads;
   constexpr int kBlkRowHalves = L::halves;
   constexpr int TILE_BYTES = ROWS * RB;
-  constexpr int TLOADS = TILE_BYTES / (kBlkThreads * 16);  // 16-byte loads per thread per tile
+  // waves that load tile data (a tile smaller than one 16-byte load per thread: the first ones)
+  // and their 16-byte loads per thread per tile
+  constexpr int TWAVES = TILE_BYTES >= kBlkThreads * 16 ? kBlkWaves : TILE_BYTES / (kWave * 16);
+  constexpr int TLOADS = TILE_BYTES / (TWAVES * kWave * 16);
   // The main pass stages the tile's mask words too (always issued, from a dummy address when
   // there is no mask, so every tile is the same number of loads): MASK_DW 32-bit words per
   // query, one per 32 rows, MLOADS 4-byte loads per thread.
@@ -313,7 +320,8 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   constexpr int MLOADS = SEED ? 0 : kBlkQpg * MASK_DW / kBlkThreads;
   constexpr int LOADS = TLOADS + MLOADS;  // loads per thread per tile, with a mask
   constexpr int CH = RB / 16;             // 16-byte chunks per row
-  static_assert(TILE_BYTES % (kBlkThreads * 16) == 0, "tile must split into 16-byte loads");
+  static_assert(TWAVES >= 1 && TILE_BYTES % (TWAVES * kWave * 16) == 0,
+                "tile must split into 16-byte loads");
   static_assert(SEED || (kBlkQpg * MASK_DW) % kBlkThreads == 0, "mask words per thread");
   static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
@@ -330,6 +338,19 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   const int c32 = lane & 31;
   const int half = lane >> 5;
   int* cnt = reinterpret_cast<int*>(scratch + kBlkWaves * a.capw) + wave * kBlkQpw;
+  // bit codes, narrow layout: byte -> its 8 bits as {0, 1} bytes (bit e to byte e), 2 KiB after
+  // the lists' counts; filled here, read after the first tile barrier
+  // (the seed pass keeps no lists: its LDS plan counts no list capacity)
+  uint64_t* lut = reinterpret_cast<uint64_t*>(
+      reinterpret_cast<int*>(scratch + kBlkWaves * (SEED ? 0 : a.capw)) + kBlkWaves * kBlkQpw);
+  if constexpr (Op::kBits && !WIDE) {
+    for (int v = tid; v < 256; v += kBlkThreads) {
+      uint64_t x = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x |= static_cast<uint64_t>((v >> e) & 1) << (8 * e);
+      lut[v] = x;
+    }
+  }
   const int wr = WIDE ? wave % kBlkRowHalves : 0;  // this wave's row part of each tile
   const int jt = WIDE ? wave / kBlkRowHalves : wave;  // and its column tiles jt, jt + CST
   constexpr int CST = L::cstride;
@@ -406,7 +427,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   int toff[TLOADS];  // this lane's byte offset in a full tile (row r, swizzled chunk c)
 #pragma unroll
   for (int l = 0; l < TLOADS; ++l) {
-    const int sidx = l * kBlkThreads + wave * kWave + lane;  // 16-byte slot of the tile
+    const int sidx = (l * TWAVES + wave) * kWave + lane;  // 16-byte slot (loading waves)
     const int r = sidx / CH;
     toff[l] = r * RB + ((sidx % CH) ^ (r % CH)) * 16;
   }
@@ -450,9 +471,10 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     const int64_t rows_here = n - tt * ROWS < ROWS ? n - tt * ROWS : ROWS;
     const int8_t* tile = I + sample_item(tt * ROWS, a.row_stride) * static_cast<int64_t>(RB);
     const int range = static_cast<int>(rows_here * RB);
+    if (wave >= TWAVES) return;  // (wave-uniform)
 #pragma unroll
     for (int l = 0; l < TLOADS; ++l) {
-      int8_t* dst = base + (l * kBlkThreads + wave * kWave) * 16;
+      int8_t* dst = base + (l * TWAVES + wave) * kWave * 16;
       if (shared_tiles) {
         buffer_load_lds<16, false>(tile, range, toff[l], dst);
       } else {
@@ -476,10 +498,15 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     // make the wait stricter.
     const int64_t after = my_tiles - 1 - it;  // this workgroup's tiles after t
     const int later = static_cast<int>(after < STAGES - 2 ? after : STAGES - 2);
+    // (a wave that loads no tile data waits for its mask words only)
     if constexpr (masked) {
-      wait_later<LOADS, STAGES - 2>(later);
+      if (wave < TWAVES) {
+        wait_later<LOADS, STAGES - 2>(later);
+      } else {
+        wait_later<MLOADS, STAGES - 2>(later);
+      }
     } else {
-      wait_later<TLOADS, STAGES - 2>(later);
+      if (wave < TWAVES) wait_later<TLOADS, STAGES - 2>(later);
     }
     // every wave's share of tile t is in LDS, and every wave is done reading tile t - nwg, whose
     // stage the next load goes into
@@ -506,30 +533,88 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
           }
         }
       if constexpr (Op::kBits) {
-        // this lane's half of each of its rows (RB / 2 bytes), read once; step s expands 16 bits
+        // this lane's half of each of its rows (RB / 2 bytes); step s expands 16 bits
         constexpr int HC = CH / 2;  // 16-byte chunks per half row
-        v4i hb[RTW][HC];
-#pragma unroll
-        for (int i = 0; i < RTW; ++i) {
-          const int r = 32 * (wr * RTW + i) + c32;
-#pragma unroll
-          for (int m = 0; m < HC; ++m) {
-            hb[i][m] = *reinterpret_cast<const v4i*>(src + r * RB +
-                                                     (((HC * half + m) ^ (r % CH)) * 16));
-          }
-        }
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          v4i cur[RTW];
+        if constexpr (WIDE) {
+          // (read once into registers)
+          v4i hb[RTW][HC];
 #pragma unroll
           for (int i = 0; i < RTW; ++i) {
-            const uint32_t w = static_cast<uint32_t>(hb[i][s / 8][(s / 2) % 4]);
-            cur[i] = Op::item_frag((s % 2) ? (w >> 16) : (w & 0xffffu));
+            const int r = 32 * (wr * RTW + i) + c32;
+#pragma unroll
+            for (int m = 0; m < HC; ++m) {
+              hb[i][m] = *reinterpret_cast<const v4i*>(src + r * RB +
+                                                       (((HC * half + m) ^ (r % CH)) * 16));
+            }
           }
+          // the wide layout (half the MFMAs per expansion at B <= 64, eight waves on the LDS):
+          // each step's 16 bits spread into bytes arithmetically
 #pragma unroll
-          for (int i = 0; i < RTW; ++i)
+          for (int s = 0; s < KS; ++s) {
+            v4i cur[RTW];
 #pragma unroll
-            for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(cur[i], qf[j][s], acc[i][j]);
+            for (int i = 0; i < RTW; ++i) {
+              const uint32_t w = static_cast<uint32_t>(hb[i][s / 8][(s / 2) % 4]);
+              cur[i] = Op::item_frag((s % 2) ? (w >> 16) : (w & 0xffffu));
+            }
+#pragma unroll
+            for (int i = 0; i < RTW; ++i)
+#pragma unroll
+              for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(cur[i], qf[j][s], acc[i][j]);
+          }
+        } else {
+          // narrow: step s's two bytes through the LDS table (two 8-byte reads instead of a
+          // 3-instruction spread per nibble), read BPF steps ahead
+          // the 32-bit word holding a step's bits: from the half rows read once into registers,
+          // or, masked (whose mask words take those registers), from the staged tile
+          v4i hb[masked ? 1 : RTW][masked ? 1 : HC];
+          if constexpr (!masked) {
+#pragma unroll
+            for (int i = 0; i < RTW; ++i) {
+              const int r = 32 * (wr * RTW + i) + c32;
+#pragma unroll
+              for (int m = 0; m < HC; ++m) {
+                hb[i][m] = *reinterpret_cast<const v4i*>(src + r * RB +
+                                                         (((HC * half + m) ^ (r % CH)) * 16));
+              }
+            }
+          }
+          auto bword = [&](int s, int i) {
+            if constexpr (masked) {
+              const int r = 32 * (wr * RTW + i) + c32;
+              return *reinterpret_cast<const uint32_t*>(
+                  src + r * RB + (((HC * half + s / 8) ^ (r % CH)) * 16) + ((s / 2) % 4) * 4);
+            } else {
+              return static_cast<uint32_t>(hb[i][s / 8][(s / 2) % 4]);
+            }
+          };
+          auto bfrag = [&](int s, int i) {
+            const uint32_t w = bword(s, i) >> (16 * (s % 2));
+            const uint64_t lo = lut[w & 0xffu];
+            const uint64_t hi = lut[(w >> 8) & 0xffu];
+            return v4i{static_cast<int>(lo), static_cast<int>(lo >> 32), static_cast<int>(hi),
+                       static_cast<int>(hi >> 32)};
+          };
+          constexpr int BPF = KS < 2 ? KS : 2;
+          v4i bf[BPF][RTW];
+#pragma unroll
+          for (int s = 0; s < BPF; ++s)
+#pragma unroll
+            for (int i = 0; i < RTW; ++i) bf[s][i] = bfrag(s, i);
+#pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            v4i cur[RTW];
+#pragma unroll
+            for (int i = 0; i < RTW; ++i) {
+              cur[i] = bf[s % BPF][i];
+              if (s + BPF < KS) bf[s % BPF][i] = bfrag(s + BPF, i);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < RTW; ++i)
+#pragma unroll
+              for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(cur[i], qf[j][s], acc[i][j]);
+          }
         }
       } else {
         // row fragments of step s: lane l reads bytes [32 s + 16 (l / 32), +16) of its row;
@@ -711,7 +796,8 @@ static size_t blk_lds(int64_t row_bytes, int stages, int capw, bool wide, bool b
                       bool masked) {
   const int rows = blk_rows(row_bytes, wide, bits);
   return static_cast<size_t>(stages) * (rows * row_bytes + (masked ? blk_mask_bytes(rows) : 0)) +
-         (wide ? 8 : 4) * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
+         (wide ? 8 : 4) * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int)) +
+         (bits && !wide ? kBitsLutBytes : 0);
 }
 
 // The deepest staging that fits a workgroup's share of LDS (all of it wide, half narrow, so two
