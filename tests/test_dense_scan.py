@@ -149,8 +149,9 @@ def test_errors(dev):
         torch.ops.retrieve.dense_scan_topk(q[:, :32], it, 3)
 
 
-def test_large_batch_sample_pass(dev):
-    """bf16 at B = 256 over 2.2M clustered rows: the blocked kernel's seeded path."""
+def test_large_batch_seeded_path(dev):
+    """bf16 at B = 256 over 2.2M clustered rows: the blocked kernel's seeded path (the threshold
+    sample pass runs from B = 512: tests/test_configs.py)."""
     g = rng(18)
     centres = g.standard_normal((64, 128))
     it = _clustered(g, 2_200_000, 128, centres)

@@ -215,7 +215,7 @@ def test_large_batch_seeded_ties_masked(dev):
 
 
 def test_large_batch_sample_pass(dev):
-    """512-byte rows, B >= 512 over N >= 2.1M rows run the threshold sample pass (every 8th
+    """512-byte rows, B >= 512 over N >= 2.1M rows run the threshold sample pass (every 16th
     tile) before the main pass: heavy ties across the sampled and unsampled tiles, and a mask
     with an empty row and a row whose few passing items miss the sample."""
     g = rng(17)
