@@ -7,8 +7,11 @@ configuration (cardinalities 16 .. 1000, Zipf(1.1) values) and a 64-bit, 3-hash 
 over its (attribute, value) tokens; each query is an AND over 1-3 attributes of OR over value
 sets, tuned to 10 % selectivity. A step is the filtered forward over one query batch, inputs
 resident in HBM: the Bloom pre-filter (plans prepared once, outside the timed region, as the
-reference's prepare_queries), the exact clause post-check on the Bloom survivors, and the int8
-scan with the fused exact top-100 (ties to the lower index).
+reference's prepare_queries), then the int8 scan with the fused exact top-100 (ties to the lower
+index) and the exact clause post-check inside it: an item is checked against its query's clauses
+where its score beats the query's running bound and its Bloom bit is set, as st::search's scorer
+checks each Bloom-passing doc (``--unfused-filter``: the clause kernel writes the post-checked
+mask first, and the scan reads it).
 
 Other workloads (the remaining configurations, same JSON line):
   int8     the plain int8 scan top-k (configuration 4; ``--batch`` 1 / 16 / 256 / 1024)
@@ -185,14 +188,21 @@ class Filter:
         log(f"selectivity per row: mean {self.selectivity.mean():.4f}, "
             f"min {self.selectivity.min():.4f}, max {self.selectivity.max():.4f}")
 
+    def bloom(self) -> torch.Tensor:
+        """One batch's Bloom pre-filter: [B, ceil(N/64)] words."""
+        return torch.ops.st.bloom_index_search_batch_prepared(
+            self.words, self.offs, self.blob, self.plan_count, self.max_stack, BLOOM_K, HASH_K)
+
     def mask(self) -> torch.Tensor:
         """One batch's filter: Bloom pre-filter, then the exact post-check of its survivors."""
-        pre = torch.ops.st.bloom_index_search_batch_prepared(
-            self.words, self.offs, self.blob, self.plan_count, self.max_stack, BLOOM_K, HASH_K)
-        return torch.ops.retrieve.clause_bits(self.attrs, self.rev, self.sets, pre)
+        return torch.ops.retrieve.clause_bits(self.attrs, self.rev, self.sets, self.bloom())
 
-    def bytes(self, n: int, b: int) -> int:
-        """Algorithmic bytes of one batch's filter: Bloom words, int16 attributes, the masks."""
+    def bytes(self, n: int, b: int, fused: bool = False) -> int:
+        """Algorithmic bytes of one batch's filter: the Bloom words and the Bloom mask written;
+        unfused, also the int16 attributes, the Bloom mask read and the clause mask written
+        (the scan's mask words, and fused its attribute reads, are sparse: candidates only)."""
+        if fused:
+            return n * BLOOM_BITS // 8 + b * n // 8
         return n * BLOOM_BITS // 8 + n * len(CARDINALITIES) * 2 + 3 * b * n // 8
 
     def valid_fn(self, ns: int):
@@ -301,6 +311,9 @@ def main() -> int:
     ap.add_argument("--filter", choices=("bloom", "none"), default=None,
                     help="kept for older command lines: none = --workload int8")
     ap.add_argument("--selectivity", type=float, default=0.1)
+    ap.add_argument("--unfused-filter", action="store_true",
+                    help="filtered: write the clause-checked mask before the scan instead of "
+                         "checking the clauses inside it")
     ap.add_argument("--cpu-sample", type=int, default=None,
                     help="items of the CPU baseline's bounded sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -346,12 +359,16 @@ def main() -> int:
         flt = Filter(n, b, args.selectivity, dev) if wl == "filtered" else None
 
         def step():
-            return torch.ops.retrieve.int8_scan_topk(queries, items, k,
-                                                    flt.mask() if flt else None)
+            if flt is None:
+                return torch.ops.retrieve.int8_scan_topk(queries, items, k)
+            if args.unfused_filter:
+                return torch.ops.retrieve.int8_scan_topk(queries, items, k, flt.mask())
+            return torch.ops.retrieve.int8_scan_topk_clauses(queries, items, k, flt.attrs,
+                                                            flt.rev, flt.sets, flt.bloom())
 
         scan_bytes = n * d + b * d  # the item table once + the query block
         scan_ops = 2 * b * n * d
-        step_bytes = scan_bytes + (flt.bytes(n, b) if flt else 0)
+        step_bytes = scan_bytes + (flt.bytes(n, b, not args.unfused_filter) if flt else 0)
         bound = "hbm" if 2 * b < 625 else "mfma"  # int8 ridge: 625 OP/B
         dtype = "int8"
         data = ("synthetic: per-row int8 of N(0,1) float32 rows (torch generator seeds 1234 / "
@@ -361,7 +378,9 @@ def main() -> int:
         if flt:
             workload = (f"filtered int8 top-{k}: N={n} D={d} B={b}; Bloom {BLOOM_BITS} bits/item, "
                         f"{BLOOM_K} hashes pre-filter + exact AND-of-OR clause post-check over 8 "
-                        f"attributes at {args.selectivity:.0%} target selectivity")
+                        f"attributes at {args.selectivity:.0%} target selectivity"
+                        + ("; the clause mask written before the scan" if args.unfused_filter
+                           else "; the clauses checked inside the scan"))
             extra["measured_selectivity"] = float(flt.selectivity.mean())
         metric = ("queries/sec + achieved HBM GB/s, filtered top-100 over 30Mx512 int8 items"
                   if flt else "queries/sec + achieved HBM GB/s, int8 top-100 over 30Mx512 items")

@@ -139,6 +139,26 @@ int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t N, int64_t 
                      int64_t and_mask_words, void* out, void* workspace, size_t workspace_bytes,
                      rt_stream_t stream);
 
+/* rt_int8_scan_topk (dtype 0) / rt_dense_scan_topk (dtype 1 bf16, 2 fp16) with the exact
+ * clause filter of rt_clause_filter (same arguments and predicate) tested inside the scan: an
+ * item is tested only where its composite beats its query's running bound, so no [B, N] mask is
+ * written or read. `mask` (nullable, the scans' layout, e.g. a Bloom search's words) is AND-ed
+ * in. Same results as the scan over rt_clause_filter's mode-0 bits AND mask; k <= 1024;
+ * B <= 2^21.
+ * Replaces: the exact clause post-check ANDed into the scan's mask
+ *   (retrieve/src/retrieve/ops/triton/clause_mask.py:286-303 feeding
+ *   retrieve/src/retrieve/functional.py:57-85) and st::search's per-doc exact filter inside its
+ *   scorer (silvertorch/silvertorch/ops/csrc/fork_filters.cuh:15-41, called from
+ *   fork_search_cuda.cu:918-1130). */
+size_t rt_scan_topk_clauses_workspace(int64_t B, int64_t N, int64_t D, int64_t k, int64_t C,
+                                      int64_t V);
+int rt_scan_topk_clauses(const void* queries, int64_t B, const void* items, int64_t N, int64_t D,
+                         int64_t k, int dtype, const uint64_t* mask, int64_t mask_words,
+                         const void* item_attrs, int attr_bytes, int64_t C, int64_t A,
+                         const int8_t* clause_is_reverse, const int64_t* query_values, int64_t V,
+                         int64_t* out_ids, void* out_scores, void* workspace,
+                         size_t workspace_bytes, rt_stream_t stream);
+
 /* Packed mask [B, ceil(N/64)] (layout above) -> each row's set items in ascending order:
  * out_indices[b, 0:counts[b]] (int64, [B, N] buffer; the tail is not written), counts [B].
  * The compaction of torch.ops.retrieve.clause_compact

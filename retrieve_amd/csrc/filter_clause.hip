@@ -15,18 +15,16 @@
 // The compaction turns packed bits into ascending item ids per row in three launches: chunk
 // popcounts, a per-row exclusive scan, and a scatter where each 64-item word is expanded by one
 // wave with coalesced writes.
+#include "clause_check.h"
 #include "rt_common.h"
 
 namespace rt {
 
 constexpr int kClauseThreads = 256;
 constexpr int kRegAttrs = 16;  // one value per clause (A == 1), C up to this: held in registers
-constexpr int kMaxClauses = 32;
 constexpr int kCompactWords = 128;  // 64-bit mask words per compaction chunk (one wave)
-// Rows whose values all lie in [0, kSetDomain) test membership in a per-clause bitmap (staged
-// in LDS) instead of walking the value list.
-constexpr int kSetDomain = 1024;
-constexpr int kSetWords = kSetDomain / 64;
+// (rows whose values all lie in [0, kSetDomain) test membership in a per-clause bitmap staged
+// in LDS, instead of walking the value list)
 constexpr int kMaxBitmapLds = 64 * 1024;
 
 enum ClauseMode : int { kClauseBits = 0, kClauseBool = 1, kClauseScores = 2 };
@@ -883,10 +881,6 @@ __global__ void fill_i64_kernel(int64_t* p, int64_t n, int64_t v) {
   if (i < n) p[i] = v;
 }
 
-}  // namespace rt
-
-using namespace rt;
-
 struct ClauseWs {
   size_t nv, qc, small, bitmaps, rev, total;
 };
@@ -902,9 +896,48 @@ static ClauseWs clause_ws_parts(int64_t B, int64_t C, int64_t V) {
   return w;
 }
 
-extern "C" size_t rt_clause_filter_workspace(int64_t B, int64_t C, int64_t V) {
+size_t clause_prep_workspace(int64_t B, int64_t C, int64_t V) {
   if (B <= 0 || C <= 0 || V <= 0) return 256;
   return clause_ws_parts(B, C, V).total;
+}
+
+int clause_prepare(const int64_t* query_values, int64_t B, int64_t C, int64_t V,
+                   const int8_t* clause_is_reverse, void* workspace, size_t workspace_bytes,
+                   ClauseCheck* out, hipStream_t stream) {
+  if (B <= 0 || C <= 0) return kOk;
+  const ClauseWs p = clause_ws_parts(B, C, V);
+  if (workspace_bytes < p.total) {
+    set_error("workspace too small: %zu < %zu", workspace_bytes, p.total);
+    return kWorkspaceTooSmall;
+  }
+  char* ws = static_cast<char*>(workspace);
+  uint32_t* active = reinterpret_cast<uint32_t*>(ws);
+  int32_t* nv = reinterpret_cast<int32_t*>(ws + p.nv);
+  int64_t* qc = reinterpret_cast<int64_t*>(ws + p.qc);
+  uint32_t* small = reinterpret_cast<uint32_t*>(ws + p.small);
+  uint64_t* bitmaps = reinterpret_cast<uint64_t*>(ws + p.bitmaps);
+  uint32_t* rev = reinterpret_cast<uint32_t*>(ws + p.rev);
+  clause_prep_kernel<<<static_cast<unsigned>(B), kPrepThreads, 0, stream>>>(
+      query_values, B, static_cast<int>(C), static_cast<int>(V), clause_is_reverse, active, nv,
+      qc, small, bitmaps, rev);
+  RT_CHECK_HIP(hipGetLastError());
+  out->C = static_cast<int>(C);
+  out->V = static_cast<int>(V);
+  out->active = active;
+  out->nv = nv;
+  out->qc = qc;
+  out->small = small;
+  out->bitmaps = bitmaps;
+  out->rev_mask = rev;
+  return kOk;
+}
+
+}  // namespace rt
+
+using namespace rt;
+
+extern "C" size_t rt_clause_filter_workspace(int64_t B, int64_t C, int64_t V) {
+  return clause_prep_workspace(B, C, V);
 }
 
 extern "C" int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t N, int64_t C,
@@ -945,24 +978,16 @@ extern "C" int rt_clause_filter(const void* item_attrs, int attr_bytes, int64_t 
   a.W = cdiv(N, 64);
   a.mode = mode;
   if (C > 0) {
-    const ClauseWs p = clause_ws_parts(B, C, V);
-    if (workspace_bytes < p.total) {
-      set_error("workspace too small: %zu < %zu", workspace_bytes, p.total);
-      return kWorkspaceTooSmall;
-    }
-    char* ws = static_cast<char*>(workspace);
-    a.active = reinterpret_cast<uint32_t*>(ws);
-    a.nv = reinterpret_cast<int32_t*>(ws + p.nv);
-    a.qc = reinterpret_cast<int64_t*>(ws + p.qc);
-    a.small = reinterpret_cast<uint32_t*>(ws + p.small);
-    a.bitmaps = reinterpret_cast<uint64_t*>(ws + p.bitmaps);
-    a.rev_mask = reinterpret_cast<uint32_t*>(ws + p.rev);
-    clause_prep_kernel<<<static_cast<unsigned>(B), kPrepThreads, 0, stream>>>(
-        query_values, B, static_cast<int>(C), static_cast<int>(V), clause_is_reverse,
-        const_cast<uint32_t*>(a.active), const_cast<int32_t*>(a.nv), const_cast<int64_t*>(a.qc),
-        const_cast<uint32_t*>(a.small), const_cast<uint64_t*>(a.bitmaps),
-        const_cast<uint32_t*>(a.rev_mask));
-    RT_CHECK_HIP(hipGetLastError());
+    ClauseCheck f;
+    const int st = clause_prepare(query_values, B, C, V, clause_is_reverse, workspace,
+                                  workspace_bytes, &f, stream);
+    if (st != kOk) return st;
+    a.active = f.active;
+    a.nv = f.nv;
+    a.qc = f.qc;
+    a.small = f.small;
+    a.bitmaps = f.bitmaps;
+    a.rev_mask = f.rev_mask;
   }
   // about 4096 workgroups in all, each looping over item chunks (the staging is amortized)
   int64_t gx = cdiv(N, kClauseThreads);

@@ -38,6 +38,9 @@ struct WaveTopK16 {
   uint64_t tau;            // this lane's query: lower bound (composite); ~0 = padding column
   Score ts;                // its score part (the fast-path test is score >= ts)
   const uint64_t* qmask;   // this lane's query's item bits (bit 63 - d % 64), or null
+  ClauseCheck clause;      // exact clauses tested per candidate, where `clauses`
+  ClauseRow crow;          // this lane's query's clause state
+  bool clauses;
 
   __device__ void set_tau(uint64_t t) {
     tau = t;
@@ -45,26 +48,56 @@ struct WaveTopK16 {
   }
 
   // Scores acc[r] of rows row0 + r (r < 4) for this lane's query; rows >= r1 are past the
-  // pass. item = row * row_stride. Appends composites >= tau that pass the filter; compacts
-  // lists that could overflow on the next tile.
+  // pass. item = row * row_stride. Appends composites >= tau that pass the mask and the
+  // clauses (tested only for such composites); compacts lists that could overflow on the next
+  // tile. The filters run once per tile for all four rows: one mask word when the rows are
+  // four consecutive items from a multiple of four (they share a word), and the clause tests
+  // one candidate per lane per pass (a wave rarely has more than one per lane).
   __device__ void push(const Score acc[4], int64_t row0, int64_t r1, int64_t row_stride) {
     const Score m01 = acc[0] > acc[1] ? acc[0] : acc[1];
     const Score m23 = acc[2] > acc[3] ? acc[2] : acc[3];
     const bool hit = (m01 > m23 ? m01 : m23) >= ts;
     if (!__any(hit)) return;
     const int col = lane_id() & 15;
+    uint64_t cs[4];
+    uint32_t cand = 0u;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t row = row0 + r;
-      if (row < r1 && acc[r] >= ts) {
-        const uint32_t item = static_cast<uint32_t>(row * row_stride);
-        const uint64_t c = composite(KeyOps<Score>::key(acc[r]), item);
-        bool keep = c >= tau;
-        if (keep && qmask != nullptr) keep = (qmask[item >> 6] >> (63 - (item & 63))) & 1ull;
-        if (keep) {
-          const int pos = atomicAdd(&cnt[col], 1);
-          lists[col * capw + pos] = c;
+      cs[r] = composite(KeyOps<Score>::key(acc[r]), static_cast<uint32_t>(row * row_stride));
+      cand |= row < r1 && acc[r] >= ts && cs[r] >= tau ? 1u << r : 0u;
+    }
+    if (qmask != nullptr && cand != 0u) {
+      const int64_t item0 = row0 * row_stride;
+      if (row_stride == 1 && (row0 & 3) == 0) {
+        const uint64_t w = qmask[item0 >> 6];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          cand &= (w >> (63 - ((item0 + r) & 63))) & 1ull ? ~0u : ~(1u << r);
         }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t item = (row0 + r) * row_stride;
+          if ((cand >> r) & 1u) {
+            cand &= (qmask[item >> 6] >> (63 - (item & 63))) & 1ull ? ~0u : ~(1u << r);
+          }
+        }
+      }
+    }
+    uint32_t todo = clauses ? cand : 0u;
+    while (__any(todo != 0u)) {
+      if (todo != 0u) {
+        const int r = __builtin_ctz(todo);
+        todo &= todo - 1u;
+        if (!clause_pass(clause, crow, (row0 + r) * row_stride)) cand &= ~(1u << r);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if ((cand >> r) & 1u) {
+        const int pos = atomicAdd(&cnt[col], 1);
+        lists[col * capw + pos] = cs[r];
       }
     }
     wave_sync_memory();

@@ -9,6 +9,7 @@
 //   4. final merge: the exact top-k over the main scan's lists.
 #pragma once
 
+#include "clause_check.h"
 #include "rt_common.h"
 
 namespace rt {
@@ -43,6 +44,9 @@ struct ScanArgs {
   int64_t mask_t_stride;
   uint64_t* lists;         // [slots, qpw, capw]
   int* counts;             // [slots, qpw]
+  ClauseCheck clause;      // exact clauses tested per candidate (active null: none; the
+                           // scans of scan_mfma.hip)
+  int clause_lds;          // main pass: the query group's set bitmaps copied to LDS
 };
 
 enum ScoreKind : int {

@@ -96,6 +96,8 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
   load_query_fragments<KSTEPS>(a, qrow, grp, qf);
   const uint64_t* qmask =
       a.mask != nullptr && qrow < a.B ? a.mask + qrow * a.mask_words : nullptr;
+  const bool clauses = a.clause.active != nullptr && qrow < a.B;
+  const ClauseRow crow = clauses ? clause_row(a.clause, qrow) : ClauseRow{};
 
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * a.strip;
   const int64_t r1 = r0 + a.strip < a.n_rows ? r0 + a.strip : a.n_rows;
@@ -112,14 +114,47 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
     typename Op::Acc acc = Op::zero();
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) acc = Op::mma(af[s], qf[s], acc);
+    // the rows whose composite would raise the maximum, then the filters on them only: one
+    // mask word (four sample rows from a multiple of four are consecutive items of one word),
+    // then the clauses from the best row down until one passes
+    uint64_t cs[4];
+    uint32_t cand = 0u;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t row = rb + 4 * grp + r;
-      const uint32_t item = static_cast<uint32_t>(sample_item(row, a.row_stride));
-      bool ok = row < r1;
-      if (ok && qmask != nullptr) ok = (qmask[item >> 6] >> (63 - (item & 63))) & 1ull;
-      const uint64_t c = composite(KeyOps<Score>::key(acc[r]), item);
-      best = ok && c > best ? c : best;
+      cs[r] = composite(KeyOps<Score>::key(acc[r]),
+                        static_cast<uint32_t>(sample_item(row, a.row_stride)));
+      cand |= row < r1 && cs[r] > best ? 1u << r : 0u;
+    }
+    if (qmask != nullptr && cand != 0u) {
+      const int64_t item0 = sample_item(rb + 4 * grp, a.row_stride);
+      const uint64_t w = qmask[item0 >> 6];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        cand &= (w >> (63 - ((item0 + r) & 63))) & 1ull ? ~0u : ~(1u << r);
+      }
+    }
+    if (!clauses) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) best = (cand >> r) & 1u && cs[r] > best ? cs[r] : best;
+    }
+    while (__any(clauses && cand != 0u)) {
+      if (clauses && cand != 0u) {
+        int rb_ = 0;
+        uint64_t cb = 0ull;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if ((cand >> r) & 1u && cs[r] > cb) {
+            cb = cs[r];
+            rb_ = r;
+          }
+        }
+        cand &= ~(1u << rb_);
+        if (clause_pass(a.clause, crow, sample_item(rb + 4 * grp + rb_, a.row_stride))) {
+          best = cb;
+          cand = 0u;
+        }
+      }
     }
   }
   uint64_t o = __shfl_xor(best, 16);
@@ -177,6 +212,26 @@ __global__ void __launch_bounds__(kScanThreads) scan_mfma_kernel(ScanArgs a) {
   top.capw = a.capw;
   top.k = a.k;
   top.qmask = a.mask != nullptr && qrow < a.B ? a.mask + qrow * a.mask_words : nullptr;
+  top.clause = a.clause;
+  top.clauses = a.clause.active != nullptr && qrow < a.B;  // a padding column tests nothing
+  if (a.clause.active != nullptr) {
+    // the group's set bitmaps in LDS (after the lists' counts) when the host planned room
+    const uint64_t* bm = nullptr;
+    if (a.clause_lds) {
+      uint64_t* lds_bm = reinterpret_cast<uint64_t*>(
+          base + main_static_lds<KSTEPS>() + kScanWaves * a.capw * sizeof(uint64_t) +
+          kScanWaves * 16 * sizeof(int));
+      const int per_row = a.clause.C * kSetWords;
+      const int64_t g0 = static_cast<int64_t>(blockIdx.y) * 16;
+      for (int i = threadIdx.x; i < 16 * per_row; i += kScanThreads) {
+        const int64_t b = g0 + i / per_row;
+        lds_bm[i] = b < a.B ? a.clause.bitmaps[b * per_row + i % per_row] : 0ull;
+      }
+      __syncthreads();
+      bm = lds_bm + col * per_row;
+    }
+    if (top.clauses) top.crow = clause_row(a.clause, qrow, bm);
+  }
   top.set_tau(qrow < a.B ? (a.tau_in != nullptr ? a.tau_in[qrow] : 0ull) : ~0ull);
   wave_sync_memory();
 
@@ -226,6 +281,13 @@ static size_t main_lds_bytes(int capw) {
   return main_static_lds<KSTEPS>() + kScanWaves * (capw * sizeof(uint64_t) + 16 * sizeof(int));
 }
 
+// LDS of the clause bitmaps a main-pass workgroup copies (its 16 queries), and the most the main
+// pass gives them: they are copied only while two workgroups still fit a CU.
+static size_t clause_lds_bytes(int C) {
+  return static_cast<size_t>(16) * C * kSetWords * sizeof(uint64_t);
+}
+constexpr size_t kMainLdsForTwo = 80 * 1024;
+
 template <class Op, int KSTEPS>
 static int launch_mfma(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, bool seed,
                        hipStream_t stream) {
@@ -235,13 +297,17 @@ static int launch_mfma(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, 
     RT_CHECK_HIP(hipGetLastError());
     return kOk;
   }
-  const size_t lds = main_lds_bytes<KSTEPS>(p.capw);
+  ScanArgs m = a;
+  size_t lds = main_lds_bytes<KSTEPS>(p.capw);
+  m.clause_lds =
+      a.clause.active != nullptr && lds + clause_lds_bytes(a.clause.C) <= kMainLdsForTwo;
+  if (m.clause_lds) lds += clause_lds_bytes(a.clause.C);
   if (lds > 65536) {
     RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(scan_mfma_kernel<Op, KSTEPS>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds)));
   }
-  scan_mfma_kernel<Op, KSTEPS><<<grid, kScanThreads, lds, stream>>>(a);
+  scan_mfma_kernel<Op, KSTEPS><<<grid, kScanThreads, lds, stream>>>(m);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }
@@ -273,7 +339,8 @@ template <class Op>
 static int run_mfma_scan(const void* queries, int64_t B, const void* items, int64_t N,
                          int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                          int64_t* out_ids, void* out_scores, void* workspace,
-                         size_t workspace_bytes, hipStream_t stream) {
+                         size_t workspace_bytes, hipStream_t stream,
+                         const ClauseCheck& clause = ClauseCheck{}) {
   RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
   RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
                static_cast<long long>(kMaxK), static_cast<long long>(k));
@@ -308,6 +375,7 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   a.mask_words = mask_words;
   a.lists = lists;
   a.counts = counts;
+  a.clause = clause;
 
   MergeArgs m{};
   m.lists = lists;
@@ -337,6 +405,7 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   a.row_stride = 1;
   a.strip = plan.main.strip;
   a.capw = plan.main.capw;
+  a.clause_lds = 0;  // the main pass's launch decides
   a.tau_in = plan.seeded ? tau : nullptr;
   hipEvent_t stop;
   profile_begin(stream, &stop);
@@ -436,6 +505,71 @@ extern "C" int rt_int8_scan_topk_noalloc(const int8_t* queries, int64_t B, const
   if (st != kOk) return st;
   return run_mfma_scan<I8Op>(queries, B, items, N, D, k, mask, mask_words, out_ids, out_scores,
                              ws, kNoAllocScratchBytes, stream);
+}
+
+// ---- scans with the exact clause filter tested per candidate --------------------------------
+
+static size_t mfma_plan_bytes(int64_t B, int64_t N, int64_t k) {
+  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k),
+                   kScanWaves * kTile)
+      .total;
+}
+
+extern "C" size_t rt_scan_topk_clauses_workspace(int64_t B, int64_t N, int64_t D, int64_t k,
+                                                 int64_t C, int64_t V) {
+  (void)D;
+  if (k < 1 || k > kMaxK || B < 0 || N < 0) return 256;
+  return align_up(mfma_plan_bytes(B, N, k), 256) + clause_prep_workspace(B, C, V);
+}
+
+extern "C" int rt_scan_topk_clauses(const void* queries, int64_t B, const void* items, int64_t N,
+                                    int64_t D, int64_t k, int dtype, const uint64_t* mask,
+                                    int64_t mask_words, const void* item_attrs, int attr_bytes,
+                                    int64_t C, int64_t A, const int8_t* clause_is_reverse,
+                                    const int64_t* query_values, int64_t V, int64_t* out_ids,
+                                    void* out_scores, void* workspace, size_t workspace_bytes,
+                                    hipStream_t stream) {
+  RT_CHECK_ARG(dtype >= 0 && dtype <= 2, "dtype must be 0 (int8), 1 (bf16) or 2 (fp16), got %d",
+               dtype);
+  RT_CHECK_ARG(B >= 0 && N >= 0 && k >= 1 && k <= kMaxK, "B, N >= 0 and k in [1, %lld]",
+               static_cast<long long>(kMaxK));
+  RT_CHECK_ARG(C >= 0 && C <= kMaxClauses, "C must be in [0, %d], got %lld", kMaxClauses,
+               static_cast<long long>(C));
+  RT_CHECK_ARG(A >= 0 && A <= 4096 && V >= 1 && V <= 4096, "A must be in [0, 4096] and V in "
+               "[1, 4096]");
+  RT_CHECK_ARG(attr_bytes == 2 || attr_bytes == 4 || attr_bytes == 8,
+               "attr_bytes must be 2, 4 or 8 (int16, int32, int64 attributes)");
+  RT_CHECK_ARG(B <= (int64_t{1} << 21), "B must be <= 2^21 query rows");
+  if (B == 0) return kOk;
+  RT_CHECK_ARG(C == 0 || (clause_is_reverse != nullptr && query_values != nullptr),
+               "clause_is_reverse and query values must not be null");
+  RT_CHECK_ARG(C * A == 0 || N == 0 || item_attrs != nullptr, "item attrs are null");
+  const size_t scan_bytes = align_up(mfma_plan_bytes(B, N, k), 256);
+  const size_t need = scan_bytes + clause_prep_workspace(B, C, V);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("workspace too small: %zu < %zu", workspace_bytes, need);
+    return kWorkspaceTooSmall;
+  }
+  ClauseCheck f;
+  if (C > 0 && N > 0) {
+    const int st = clause_prepare(query_values, B, C, V, clause_is_reverse,
+                                  static_cast<char*>(workspace) + scan_bytes,
+                                  workspace_bytes - scan_bytes, &f, stream);
+    if (st != kOk) return st;
+    f.attrs = item_attrs;
+    f.attr_bytes = attr_bytes;
+    f.A = static_cast<int>(A);
+  }
+  if (dtype == 0) {
+    return run_mfma_scan<I8Op>(queries, B, items, N, D, k, mask, mask_words, out_ids,
+                               out_scores, workspace, scan_bytes, stream, f);
+  }
+  if (dtype == 1) {
+    return run_mfma_scan<BF16Op>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
+                                 out_scores, workspace, scan_bytes, stream, f);
+  }
+  return run_mfma_scan<F16Op>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
+                              out_scores, workspace, scan_bytes, stream, f);
 }
 
 extern "C" size_t rt_dense_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {

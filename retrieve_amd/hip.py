@@ -431,6 +431,117 @@ def _(item_clause_attrs, clause_is_reverse, query_values, and_mask=None):
     return query_values.new_empty((query_values.shape[0], (n + 63) // 64), dtype=torch.int64)
 
 
+# --- full scans with the exact clause filter tested per candidate ----------------------------
+
+
+def _scan_clauses(q: Tensor, items: Tensor, k: int, dtype: int, item_clause_attrs: Tensor,
+                  clause_is_reverse: Tensor, query_values: Tensor, mask: Tensor | None,
+                  scores: Tensor, ids: Tensor) -> bool:
+    """The fused scan of ``rt_scan_topk_clauses`` (dtype 0 int8, 1 bf16, 2 fp16) into ``ids`` /
+    ``scores``; False where it does not apply (the blocked batches, k above the fused lists'
+    bound, fp32), and the caller then scans over ``clause_bits``."""
+    rev, qs = _clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
+    b, d = q.shape
+    n = items.shape[0]
+    if item_clause_attrs.shape[0] != n:
+        raise ValueError(f"item_clause_attrs has {item_clause_attrs.shape[0]} rows, the items {n}")
+    if qs.shape[0] != b:
+        raise ValueError(f"query_values has {qs.shape[0]} rows, the queries {b}")
+    if dtype == 3 or k > MAX_FUSED_K or _use_blocked(b, d * q.element_size(), k):
+        return False
+    dev = nat.require_device(q, items, item_clause_attrs, qs)
+    _, c, a = item_clause_attrs.shape
+    v = qs.shape[2]
+    lib = nat.lib()
+    ws = nat.workspace(lib.rt_scan_topk_clauses_workspace(b, n, d, k, c, v), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_scan_topk_clauses(
+            nat.ptr(q), b, nat.ptr(items), n, d, k, dtype, nat.ptr(mask),
+            0 if mask is None else mask.shape[1], nat.ptr(item_clause_attrs),
+            item_clause_attrs.element_size(), c, a, nat.ptr(rev), nat.ptr(qs), v, nat.ptr(ids),
+            nat.ptr(scores), nat.ptr(ws), ws.numel(), nat.stream(dev),
+        )
+    nat.check(st)
+    return True
+
+
+@torch.library.custom_op("retrieve::int8_scan_topk_clauses", mutates_args=(),
+                         device_types="cuda")
+def int8_scan_topk_clauses(
+    query_codes: Tensor, item_codes: Tensor, k: int, item_clause_attrs: Tensor,
+    clause_is_reverse: Tensor, query_values: Tensor, mask: Tensor | None = None,
+) -> tuple[Tensor, Tensor]:
+    """``int8_scan_topk`` over the items that pass ``mask`` and the exact clauses
+    (``clause_bits``' arguments and predicate): the same results as
+    ``int8_scan_topk(q, items, k, clause_bits(attrs, rev, values, mask))``. Up to the blocked
+    scan's batch the clauses are tested inside the scan, only for the items whose score beats
+    their query's running bound, so no ``[B, N]`` clause mask is written or read (the exact
+    post-check inside the scorer, as ``silvertorch/.../fork_filters.cuh:15-41`` runs in
+    ``fork_search_cuda.cu:918-1130``)."""
+    q, mask = _int8_scan_prep(query_codes, item_codes, k, mask)
+    b = q.shape[0]
+    ids = torch.empty((b, k), dtype=torch.int64, device=q.device)
+    scores = torch.empty((b, k), dtype=torch.int32, device=q.device)
+    if _scan_clauses(q, item_codes, k, 0, item_clause_attrs, clause_is_reverse, query_values,
+                     mask, scores, ids):
+        return ids, scores
+    bits = clause_bits(item_clause_attrs, clause_is_reverse, query_values, mask)
+    return int8_scan_topk(q, item_codes, k, bits)
+
+
+@int8_scan_topk_clauses.register_fake
+def _(query_codes, item_codes, k, item_clause_attrs, clause_is_reverse, query_values, mask=None):
+    b = query_codes.shape[0]
+    return (query_codes.new_empty((b, k), dtype=torch.int64),
+            query_codes.new_empty((b, k), dtype=torch.int32))
+
+
+@torch.library.custom_op("retrieve::dense_scan_topk_clauses", mutates_args=(),
+                         device_types="cuda")
+def dense_scan_topk_clauses(
+    query: Tensor, item_embs: Tensor, k: int, item_clause_attrs: Tensor,
+    clause_is_reverse: Tensor, query_values: Tensor, mask: Tensor | None = None,
+) -> tuple[Tensor, Tensor]:
+    """``dense_scan_topk`` over the items that pass ``mask`` and the exact clauses: the same
+    results as ``dense_scan_topk(q, items, k, clause_bits(attrs, rev, values, mask))``, the
+    clauses tested inside the bf16 / fp16 scan up to the blocked scan's batch (as
+    ``int8_scan_topk_clauses``). LiNR V1's ``ExactAttributeFilter.mask_scores`` +
+    ``masked_topk`` (``retrieve/src/retrieve/modules/filters.py:48-52``,
+    ``functional.py:57-85``) without the ``[B, N]`` scores."""
+    if query.dim() != 2 or item_embs.dim() != 2 or query.dtype != item_embs.dtype:
+        raise ValueError("query [B, D] and item_embs [N, D] of one dtype")
+    dtype = {torch.bfloat16: 1, torch.float16: 2, torch.float32: 3}.get(query.dtype)
+    if dtype is None:
+        raise TypeError("query and item_embs must both be bfloat16, float16 or float32")
+    if query.shape[1] != item_embs.shape[1]:
+        raise ValueError(f"D mismatch: query D={query.shape[1]} vs item D={item_embs.shape[1]}")
+    if k < 1:
+        raise ValueError(f"k must be >= 1, got {k}")
+    _check_items(item_embs=item_embs)
+    b, n = query.shape[0], item_embs.shape[0]
+    if mask is not None:
+        if mask.dtype != torch.int64:
+            raise TypeError("mask must be int64 words")
+        if mask.dim() != 2 or mask.shape[0] != b or mask.shape[1] < (n + 63) // 64:
+            raise ValueError(f"mask must be [B, ceil(N/64)] = [{b}, {(n + 63) // 64}]")
+        mask = mask.contiguous()
+    q = query.contiguous()
+    ids = torch.empty((b, k), dtype=torch.int64, device=q.device)
+    scores = torch.empty((b, k), dtype=torch.float32, device=q.device)
+    if _scan_clauses(q, item_embs, k, dtype, item_clause_attrs, clause_is_reverse, query_values,
+                     mask, scores, ids):
+        return ids, scores
+    bits = clause_bits(item_clause_attrs, clause_is_reverse, query_values, mask)
+    return dense_scan_topk(q, item_embs, k, bits)
+
+
+@dense_scan_topk_clauses.register_fake
+def _(query, item_embs, k, item_clause_attrs, clause_is_reverse, query_values, mask=None):
+    b = query.shape[0]
+    return (query.new_empty((b, k), dtype=torch.int64),
+            query.new_empty((b, k), dtype=torch.float32))
+
+
 def _mask_compact(mask: Tensor, n: int) -> tuple[Tensor, Tensor]:
     b = mask.shape[0]
     dev = mask.device
