@@ -238,8 +238,7 @@ __global__ void __launch_bounds__(kScanThreads) scan_mfma_kernel(ScanArgs a) {
   const int64_t n = a.n_rows;
   const int64_t ntiles = cdiv(n, kTile);
   // load j of a tile covers its bytes [1024 j + 16 lane, +16): row (1024 j + 16 lane) / D
-  v4i v[LOADS];
-  auto load_tile = [&](int64_t t) {
+  auto load_tile = [&](int64_t t, v4i (&v)[LOADS]) {
     const int64_t base_row = t * kTile;
     const v4i* src = reinterpret_cast<const v4i*>(I + base_row * D) + lane;
 #pragma unroll
@@ -249,10 +248,9 @@ __global__ void __launch_bounds__(kScanThreads) scan_mfma_kernel(ScanArgs a) {
       v[j] = row < n ? __builtin_nontemporal_load(src + 64 * j) : v4i{0, 0, 0, 0};
     }
   };
-
-  int64_t t = wave_in_group;
-  if (t < ntiles) load_tile(t);
-  for (; t < ntiles; t += waves) {
+  // one tile: staged from registers, the registers reloaded with tile `next` (when it exists),
+  // then the MFMAs and the candidates
+  auto tile = [&](int64_t t, v4i (&v)[LOADS], int64_t next) {
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const int off = 1024 * j + 16 * lane;
@@ -264,13 +262,30 @@ __global__ void __launch_bounds__(kScanThreads) scan_mfma_kernel(ScanArgs a) {
     for (int s = 0; s < KSTEPS; ++s) {
       af[s] = *reinterpret_cast<const v4i*>(stage + col * P + grp * 16 + s * 64);
     }
-    if (t + waves < ntiles) load_tile(t + waves);
+    if (next < ntiles) load_tile(next, v);
     typename Op::Acc acc = Op::zero();
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) acc = Op::mma(af[s], qf[s], acc);
     const Score sc[4] = {acc[0], acc[1], acc[2], acc[3]};
     top.push(sc, t * kTile + 4 * grp, n, 1);
     wave_sync_memory();
+  };
+
+  // rows up to 512 bytes keep two tiles in flight per wave (two register sets), wider rows one
+  v4i va[LOADS];
+  int64_t t = wave_in_group;
+  if constexpr (KSTEPS <= 8) {
+    v4i vb[LOADS];
+    if (t < ntiles) load_tile(t, va);
+    if (t + waves < ntiles) load_tile(t + waves, vb);
+    for (; t < ntiles; t += 2 * waves) {
+      tile(t, va, t + 2 * waves);
+      if (t + waves >= ntiles) break;
+      tile(t + waves, vb, t + 3 * waves);
+    }
+  } else {
+    if (t < ntiles) load_tile(t, va);
+    for (; t < ntiles; t += waves) tile(t, va, t + waves);
   }
   wave_sync_memory();
   if (lane < 16) a.counts[slot * 16 + lane] = cnt[lane];
