@@ -311,9 +311,12 @@ def main() -> int:
     ap.add_argument("--filter", choices=("bloom", "none"), default=None,
                     help="kept for older command lines: none = --workload int8")
     ap.add_argument("--selectivity", type=float, default=0.1)
+    ap.add_argument("--fused-bits", action="store_true",
+                    help="binary: test the clauses inside the 1-bit scan (default: the clause "
+                         "mask is written first, faster at B = 256)")
     ap.add_argument("--unfused-filter", action="store_true",
-                    help="filtered: write the clause-checked mask before the scan instead of "
-                         "checking the clauses inside it")
+                    help="filtered workloads: write the clause-checked mask before the scan "
+                         "instead of checking the clauses inside it")
     ap.add_argument("--cpu-sample", type=int, default=None,
                     help="items of the CPU baseline's bounded sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -406,11 +409,14 @@ def main() -> int:
         flt = Filter(n, b, args.selectivity, dev)
 
         def step():
-            return torch.ops.retrieve.dense_scan_topk(queries, items, k, flt.mask())
+            if args.unfused_filter:
+                return torch.ops.retrieve.dense_scan_topk(queries, items, k, flt.mask())
+            return torch.ops.retrieve.dense_scan_topk_clauses(queries, items, k, flt.attrs,
+                                                             flt.rev, flt.sets, flt.bloom())
 
         scan_bytes = n * d * 2 + b * d * 2
         scan_ops = 2 * b * n * d
-        step_bytes = scan_bytes + flt.bytes(n, b)
+        step_bytes = scan_bytes + flt.bytes(n, b, not args.unfused_filter)
         bound = "hbm" if b < 312 else "mfma"  # bf16 ridge: 312.5 FLOP/B
         dtype = "bf16"
         data = ("synthetic: 1024 N(0,1) centres (seed 2024), items centre + 0.3 N(0,1) "
@@ -418,7 +424,9 @@ def main() -> int:
                 "Zipf(1.1) (seed 4321), query sets numpy seed 77")
         workload = (f"filtered dense bf16 top-{k}: N={n} D={d} B={b}; Bloom {BLOOM_BITS} "
                     f"bits/item, {BLOOM_K} hashes pre-filter + exact AND-of-OR clause post-check "
-                    f"over 8 attributes at {args.selectivity:.0%} target selectivity")
+                    f"over 8 attributes at {args.selectivity:.0%} target selectivity"
+                    + ("; the clause mask written before the scan" if args.unfused_filter
+                       else "; the clauses checked inside the scan"))
         extra["measured_selectivity"] = float(flt.selectivity.mean())
         metric = "queries/sec + achieved HBM GB/s, filtered bf16 top-100 over 10Mx128 items"
 
@@ -533,7 +541,11 @@ def main() -> int:
         flt = Filter(n, b, args.selectivity, dev)
 
         def step():
-            ids1, _ = torch.ops.retrieve.hamming_scan_topk(q_bits, item_bits, k1, flt.mask())
+            # (the clause mask is written first: faster here than testing the clauses inside
+            # the bit-code kernel, which has no registers to spare)
+            ids1, _ = torch.ops.retrieve.hamming_scan_topk_clauses(
+                q_bits, item_bits, k1, flt.attrs, flt.rev, flt.sets, flt.bloom(),
+                fused=args.fused_bits)
             counts = (ids1 >= 0).sum(1)
             return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
 
@@ -542,14 +554,16 @@ def main() -> int:
         # per bit (bits as {0, 1} and {-2, +2} bytes): 2 ops per bit, item and query
         mfma_scan = d == 512 and b >= 33
         scan_ops = 2 * b * n * d if mfma_scan else 2 * b * n * (d // 32)
-        step_bytes = scan_bytes + flt.bytes(n, b) + b * k1 * d
+        step_bytes = scan_bytes + flt.bytes(n, b, args.fused_bits) + b * k1 * d
         bound = "mfma" if mfma_scan else "hbm"
         dtype = "int8" if mfma_scan else "u64"
         data = ("synthetic: N(0,1) rows (seed 556) and queries (seed 557), SimHash over a "
                 "N(0,1) 512x512 projection (seed 555), int8 codes of the same rows; attributes "
                 "Zipf(1.1) (seed 4321), query sets numpy seed 77")
         workload = (f"binary top-{k1} + int8 rerank top-{k}: N={n} bits={d} B={b}; Bloom + exact "
-                    f"filter at {args.selectivity:.0%} target selectivity")
+                    f"filter at {args.selectivity:.0%} target selectivity"
+                    + ("; the clauses checked inside the scan" if args.fused_bits
+                       else "; the clause mask written before the scan"))
         extra["measured_selectivity"] = float(flt.selectivity.mean())
         metric = ("queries/sec + achieved HBM GB/s, filtered 1-bit top-1000 + int8 rerank "
                   "top-100 over 30M items")

@@ -159,6 +159,39 @@ int rt_scan_topk_clauses(const void* queries, int64_t B, const void* items, int6
                          int64_t* out_ids, void* out_scores, void* workspace,
                          size_t workspace_bytes, rt_stream_t stream);
 
+/* rt_blocked_scan_topk (same dtype codes and row sizes) with rt_scan_topk_clauses' exact clause
+ * filter, for the items that pass `mask` (required here): the candidates that beat their
+ * query's bound and pass the mask enter the lists, the clauses are tested where a list is
+ * compacted and in the final merge (an entry that fails them is dropped), and the sampled bound
+ * takes each lane's best over the mask, kept only when that item passes the clauses. Same
+ * results as rt_blocked_scan_topk over rt_clause_filter's mode-0 bits AND mask.
+ * Replaces: as rt_scan_topk_clauses, at the batches of rt_blocked_scan_topk. */
+size_t rt_blocked_scan_topk_clauses_workspace(int64_t B, int64_t N, int64_t row_bytes, int64_t k,
+                                              int64_t C, int64_t V);
+int rt_blocked_scan_topk_clauses(const void* queries, int64_t B, const void* items, int64_t N,
+                                 int64_t D, int64_t k, int dtype, const uint64_t* mask,
+                                 int64_t mask_words, const void* item_attrs, int attr_bytes,
+                                 int64_t C, int64_t A, const int8_t* clause_is_reverse,
+                                 const int64_t* query_values, int64_t V, int64_t* out_ids,
+                                 void* out_scores, void* workspace, size_t workspace_bytes,
+                                 rt_stream_t stream);
+
+/* rt_hamming_scan_topk with the same fused clause filter, where the matrix-core scan takes the
+ * batch (rt_hamming_scan_topk_clauses_fused(B, W, k) != 0: 512-bit codes, k <= 1024, the
+ * batches of that kernel) and a mask is given; int32 scores, or float when score_f32.
+ * Replaces: LiNR V3's filtered 1-bit shortlist (retrieve/src/retrieve/modules/linr.py:155-162,
+ *   the clause mask of clause_compact feeding oporp_1bit_match_topk). */
+int rt_hamming_scan_topk_clauses_fused(int64_t B, int64_t W, int64_t k);
+size_t rt_hamming_scan_topk_clauses_workspace(int64_t B, int64_t N, int64_t W, int64_t k,
+                                              int64_t C, int64_t V);
+int rt_hamming_scan_topk_clauses(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits,
+                                 int64_t N, int64_t W, int64_t k, const uint64_t* mask,
+                                 int64_t mask_words, const void* item_attrs, int attr_bytes,
+                                 int64_t C, int64_t A, const int8_t* clause_is_reverse,
+                                 const int64_t* query_values, int64_t V, int64_t* out_ids,
+                                 void* out_scores, int score_f32, void* workspace,
+                                 size_t workspace_bytes, rt_stream_t stream);
+
 /* Packed mask [B, ceil(N/64)] (layout above) -> each row's set items in ascending order:
  * out_indices[b, 0:counts[b]] (int64, [B, N] buffer; the tail is not written), counts [B].
  * The compaction of torch.ops.retrieve.clause_compact

@@ -58,6 +58,19 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_int, _c_i64,
          _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],
     ),
+    "rt_blocked_scan_topk_clauses_workspace": (_c_sz, [_c_i64] * 6),
+    "rt_blocked_scan_topk_clauses": (
+        _c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_int, _c_i64,
+         _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],
+    ),
+    "rt_hamming_scan_topk_clauses_fused": (_c_int, [_c_i64, _c_i64, _c_i64]),
+    "rt_hamming_scan_topk_clauses_workspace": (_c_sz, [_c_i64] * 6),
+    "rt_hamming_scan_topk_clauses": (
+        _c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_int, _c_i64, _c_i64,
+         _c_p, _c_p, _c_i64, _c_p, _c_p, _c_int, _c_p, _c_sz, _c_p],
+    ),
     "rt_bloom_bundle_terms": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "rt_bloom_build": (
         _c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p],

@@ -308,6 +308,13 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
                            (e0 + i - lo)];
           }
         }
+        if (m.clause.active != nullptr) {
+          // an entry that fails the query's clauses is empty (0, below every composite)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (v[u] != 0ull && !clause_check(m.clause, q, composite_item(v[u]))) v[u] = 0ull;
+          }
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int i = i0 + u * kMergeThreads;

@@ -293,8 +293,11 @@ __device__ inline void tile_barrier() {
 // SEED: per query, each workgroup's best composite over the strided sample, written to
 // lists[q * gridDim.x + workgroup] (one-entry lists); else candidate lists per (wave, query).
 // MASKED (main pass only): the tiles' mask words are staged and tested; a separate
-// instantiation keeps the unmasked kernel's registers free of it.
-template <class Op, int RB, bool SEED, int STAGES, bool WIDE, bool MASKED>
+// instantiation keeps the unmasked kernel's registers free of it. CLAUSES (with a mask): the
+// exact clauses of a.clause are tested on each seed lane's best, and the main pass's lists
+// (candidates that pass the mask) drop the entries that fail them when compacted (and in the
+// final merge); also a separate instantiation, for the registers of the kernels without.
+template <class Op, int RB, bool SEED, int STAGES, bool WIDE, bool MASKED, bool CLAUSES>
 __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     __attribute__((amdgpu_waves_per_eu(kBlkWavesPerSimd, kBlkWavesPerSimd)))
     scan_blocked_kernel(ScanArgs a) {
@@ -752,8 +755,20 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
               need &= need - 1;
               const int q = 32 * jq + c;
               if (lane == c) cnt[q] = nq[jq];
-              const uint64_t nt = wave_compact(lists[jq] + c * static_cast<int64_t>(a.capw),
-                                               &cnt[q], scratch + wave * a.capw, a.capw, a.k);
+              // (the lists hold candidates that pass the mask: with exact clauses, those that
+              // fail them leave the list here and in the final merge)
+              uint64_t* lq = lists[jq] + c * static_cast<int64_t>(a.capw);
+              uint64_t nt;
+              if constexpr (CLAUSES && masked) {
+                const int64_t gq = q0[jq] + c;
+                const bool cl = gq < a.B;
+                nt = wave_compact(lq, &cnt[q], scratch + wave * a.capw, a.capw, a.k,
+                                  [&](uint64_t v) {
+                                    return !cl || clause_check(a.clause, gq, composite_item(v));
+                                  });
+              } else {
+                nt = wave_compact(lq, &cnt[q], scratch + wave * a.capw, a.capw, a.k);
+              }
               if (c32 == c) {
                 nq[jq] = cnt[q];
                 if (nt > tau[jq]) {
@@ -776,6 +791,19 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   }
 
   if constexpr (SEED) {
+    if constexpr (CLAUSES) {
+      // the maxima were taken over the mask alone: a lane whose best item fails its query's
+      // clauses offers no bound (0), which keeps the bound a lower one (the merge takes the
+      // k-th of at least 4 k maxima a query)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t q = q0[j] + c32;
+        if (q < a.B && best[j] != 0ull &&
+            !clause_check(a.clause, q, composite_item(best[j]))) {
+          best[j] = 0ull;
+        }
+      }
+    }
     // flat one-entry lists: a query's maxima, one per workgroup, at lists[q * nwg + wg]
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -815,28 +843,36 @@ static int blk_stages(int64_t row_bytes, int capw, bool wide, bool bits, bool ma
                                                                                  : 0;
 }
 
-template <class Op, int RB, bool SEED, int STAGES, bool WIDE, bool MASKED>
+template <class Op, int RB, bool SEED, int STAGES, bool WIDE, bool MASKED, bool CLAUSES>
 static int launch_blk_kernel(const ScanArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  const void* fn =
-      reinterpret_cast<const void*>(scan_blocked_kernel<Op, RB, SEED, STAGES, WIDE, MASKED>);
+  const void* fn = reinterpret_cast<const void*>(
+      scan_blocked_kernel<Op, RB, SEED, STAGES, WIDE, MASKED, CLAUSES>);
   if (lds > 65536) {
     RT_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds)));
   }
-  scan_blocked_kernel<Op, RB, SEED, STAGES, WIDE, MASKED>
+  scan_blocked_kernel<Op, RB, SEED, STAGES, WIDE, MASKED, CLAUSES>
       <<<grid, BlkLayout<WIDE, RB, Op::kBits>::threads, lds, stream>>>(a);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
 }
 
+// (exact clauses come with a mask only: run_blocked checks)
 template <class Op, int RB, bool SEED, int STAGES, bool WIDE>
 static int launch_blk_staged(const ScanArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
+  const bool clauses = a.clause.active != nullptr;
   if constexpr (!SEED) {
     if (a.mask != nullptr) {
-      return launch_blk_kernel<Op, RB, false, STAGES, WIDE, true>(a, grid, lds, stream);
+      return clauses ? launch_blk_kernel<Op, RB, false, STAGES, WIDE, true, true>(a, grid, lds,
+                                                                                  stream)
+                     : launch_blk_kernel<Op, RB, false, STAGES, WIDE, true, false>(a, grid, lds,
+                                                                                   stream);
     }
+  } else {
+    if (clauses) return launch_blk_kernel<Op, RB, true, STAGES, WIDE, false, true>(a, grid, lds,
+                                                                                  stream);
   }
-  return launch_blk_kernel<Op, RB, SEED, STAGES, WIDE, false>(a, grid, lds, stream);
+  return launch_blk_kernel<Op, RB, SEED, STAGES, WIDE, false, false>(a, grid, lds, stream);
 }
 
 template <class Op, int RB, bool SEED, bool WIDE>
@@ -962,7 +998,8 @@ template <class Op>
 static int run_blocked(const void* queries, int64_t B, const void* items, int64_t N,
                        int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                        int64_t* out_ids, void* out_scores, void* workspace,
-                       size_t workspace_bytes, hipStream_t stream, int score_kind = Op::kind) {
+                       size_t workspace_bytes, hipStream_t stream, int score_kind = Op::kind,
+                       const ClauseCheck& clause = ClauseCheck{}) {
   RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
   RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
                static_cast<long long>(kMaxK), static_cast<long long>(k));
@@ -971,6 +1008,10 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
                    reinterpret_cast<uintptr_t>(items) % 16 == 0,
                "queries and items must be 16-byte aligned");
   RT_CHECK_ARG(mask == nullptr || mask_words >= cdiv(N, 64), "mask must have ceil(N/64) words");
+  // (the seed pass takes its maxima over the mask and tests only each lane's best against the
+  // clauses: without a mask that bound would rarely hold)
+  RT_CHECK_ARG(clause.active == nullptr || mask != nullptr,
+               "the blocked scan tests exact clauses only together with a mask");
   if (B == 0) return kOk;
   RT_CHECK_ARG(out_ids != nullptr && out_scores != nullptr, "out_ids and out_scores are null");
   if (N == 0) return launch_pad(out_ids, out_scores, B, k, score_kind, stream);
@@ -1007,6 +1048,7 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   a.mask_words = mask_words;
   a.lists = lists;
   a.counts = counts;
+  a.clause = clause;
   if (mask != nullptr) {
     const int64_t W = cdiv(N, 64);
     const int64_t stride = cdiv(B, kBlkQpg) * kBlkQpg;
@@ -1023,6 +1065,7 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   MergeArgs m{};
   m.lists = lists;
   m.counts = counts;
+  m.clause = clause;  // (the main pass's lists hold candidates that pass the mask)
   m.qpw = 32;  // one list per query per slot; a slot is (32-query column tile, workgroup, half)
   m.B = B;
   m.k = static_cast<int>(k);
@@ -1083,23 +1126,24 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
 
 namespace rt {
 
-// One translation unit per operand type (scan_blocked_{i8,bf16,f16}.hip): row_bytes = D times
-// the element size.
+// One translation unit per operand type (scan_blocked_{i8,bf16,f16,f32}.hip): row_bytes = D
+// times the element size; `clause`: exact clauses tested per candidate (with a mask only).
 int blocked_scan_i8(const void* queries, int64_t B, const void* items, int64_t N,
                     int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                     int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
-                    hipStream_t stream);
+                    hipStream_t stream, const ClauseCheck& clause = ClauseCheck{});
 int blocked_scan_bf16(const void* queries, int64_t B, const void* items, int64_t N,
                       int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                       int64_t* out_ids, void* out_scores, void* workspace,
-                      size_t workspace_bytes, hipStream_t stream);
+                      size_t workspace_bytes, hipStream_t stream,
+                      const ClauseCheck& clause = ClauseCheck{});
 int blocked_scan_f16(const void* queries, int64_t B, const void* items, int64_t N,
                      int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                      int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
-                     hipStream_t stream);
+                     hipStream_t stream, const ClauseCheck& clause = ClauseCheck{});
 int blocked_scan_f32(const void* queries, int64_t B, const void* items, int64_t N,
                      int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                      int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
-                     hipStream_t stream);
+                     hipStream_t stream, const ClauseCheck& clause = ClauseCheck{});
 
 }  // namespace rt

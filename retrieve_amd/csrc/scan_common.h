@@ -69,6 +69,8 @@ struct MergeArgs {
   int64_t* out_ids;    // final mode: [B, k]
   void* out_scores;    // final mode: [B, k]
   int score_kind;
+  ClauseCheck clause;  // lists (not flat) whose entries may fail exact clauses: those entries
+                       // count as empty (active null: none)
 };
 
 // The seed pass samples blocks of kSeedBlock consecutive rows spread evenly over the table
@@ -113,9 +115,9 @@ constexpr int64_t kMainWorkgroupsPerCU = 2;
 // Main-pass workgroups for the current device: CUs x kMainWorkgroupsPerCU.
 int64_t main_workgroups();
 
-// The 1-bit Hamming top-k on the int8 matrix cores (scan_blocked.hip): codes of W 64-bit words
-// (W == 8), scores 64 W - 2 popcount(q ^ x) written as score_kind (kScoreI32 or
-// kScoreF32FromI32).
+// The 1-bit Hamming top-k on the int8 matrix cores (scan_blocked_bits.hip): codes of W 64-bit
+// words (W == 8), scores 64 W - 2 popcount(q ^ x) written as score_kind (kScoreI32 or
+// kScoreF32FromI32); `clause`: exact clauses tested per candidate (with a mask only).
 bool blocked_hamming_fits(int64_t B, int64_t W, int64_t k, bool masked);  // lists fit in LDS
 size_t blocked_hamming_workspace(int64_t B, int64_t N, int64_t W, int64_t k, bool masked);
 // The 1-bit full scan for kMaxK < k <= kMaxKHamming (scan_hamming_large.hip).
@@ -127,7 +129,8 @@ int hamming_large_k(const uint64_t* query_bits, int64_t B, const uint64_t* item_
 int blocked_hamming(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, int64_t N,
                     int64_t W, int64_t k, const uint64_t* mask, int64_t mask_words,
                     int64_t* out_ids, void* out_scores, int score_kind, void* workspace,
-                    size_t workspace_bytes, hipStream_t stream);
+                    size_t workspace_bytes, hipStream_t stream,
+                    const ClauseCheck& clause = ClauseCheck{});
 
 // Sizes the passes for B queries over N rows and top-k. A workgroup row (grid.y) covers qpg
 // queries and each workgroup keeps lists_per_wg candidate lists (of main_capw entries in the

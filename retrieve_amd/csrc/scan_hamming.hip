@@ -352,3 +352,67 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B,
   m.score_kind = kind;
   return launch_merge(m, stream);
 }
+
+// The 1-bit scan on the matrix cores with the exact clause filter tested per candidate that
+// passes the mask (required), where the blocked kernel takes the batch (fused != 0).
+extern "C" int rt_hamming_scan_topk_clauses_fused(int64_t B, int64_t W, int64_t k) {
+  return k <= kMaxK && ham_mfma(B, W, k, true) ? 1 : 0;
+}
+
+extern "C" size_t rt_hamming_scan_topk_clauses_workspace(int64_t B, int64_t N, int64_t W,
+                                                         int64_t k, int64_t C, int64_t V) {
+  if (!(k <= kMaxK && ham_mfma(B, W, k, true))) return 256;
+  return align_up(blocked_hamming_workspace(B, N, W, k, true), 256) +
+         clause_prep_workspace(B, C, V);
+}
+
+extern "C" int rt_hamming_scan_topk_clauses(const uint64_t* query_bits, int64_t B,
+                                            const uint64_t* item_bits, int64_t N, int64_t W,
+                                            int64_t k, const uint64_t* mask, int64_t mask_words,
+                                            const void* item_attrs, int attr_bytes, int64_t C,
+                                            int64_t A, const int8_t* clause_is_reverse,
+                                            const int64_t* query_values, int64_t V,
+                                            int64_t* out_ids, void* out_scores, int score_f32,
+                                            void* workspace, size_t workspace_bytes,
+                                            hipStream_t stream) {
+  RT_CHECK_ARG(B >= 0 && B <= (int64_t{1} << 21) && N >= 0, "B in [0, 2^21] and N >= 0");
+  RT_CHECK_ARG(N < 0xffffffffll, "N must be < 2**32 - 1");
+  RT_CHECK_ARG(mask != nullptr && mask_words >= cdiv(N, 64),
+               "the fused clause filter needs a mask of ceil(N/64) words a row");
+  RT_CHECK_ARG(k >= 1 && k <= kMaxK && ham_mfma(B, W, k, true),
+               "the fused clause filter runs where the matrix-core scan takes the batch "
+               "(rt_hamming_scan_topk_clauses_fused)");
+  RT_CHECK_ARG(reinterpret_cast<uintptr_t>(item_bits) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(query_bits) % 16 == 0,
+               "query_bits and item_bits must be 16-byte aligned");
+  RT_CHECK_ARG(C >= 0 && C <= kMaxClauses, "C must be in [0, %d], got %lld", kMaxClauses,
+               static_cast<long long>(C));
+  RT_CHECK_ARG(A >= 0 && A <= 4096 && V >= 1 && V <= 4096, "A must be in [0, 4096] and V in "
+               "[1, 4096]");
+  RT_CHECK_ARG(attr_bytes == 2 || attr_bytes == 4 || attr_bytes == 8,
+               "attr_bytes must be 2, 4 or 8 (int16, int32, int64 attributes)");
+  if (B == 0) return kOk;
+  const int kind = score_f32 ? kScoreF32FromI32 : kScoreI32;
+  if (N == 0) return launch_pad(out_ids, out_scores, B, k, kind, stream);
+  RT_CHECK_ARG(C == 0 || (clause_is_reverse != nullptr && query_values != nullptr),
+               "clause_is_reverse and query values must not be null");
+  RT_CHECK_ARG(C * A == 0 || item_attrs != nullptr, "item attrs are null");
+  const size_t scan_bytes = align_up(blocked_hamming_workspace(B, N, W, k, true), 256);
+  const size_t need = scan_bytes + clause_prep_workspace(B, C, V);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("workspace too small: %zu < %zu", workspace_bytes, need);
+    return kWorkspaceTooSmall;
+  }
+  ClauseCheck f;
+  if (C > 0) {
+    const int st = clause_prepare(query_values, B, C, V, clause_is_reverse,
+                                  static_cast<char*>(workspace) + scan_bytes,
+                                  workspace_bytes - scan_bytes, &f, stream);
+    if (st != kOk) return st;
+    f.attrs = item_attrs;
+    f.attr_bytes = attr_bytes;
+    f.A = static_cast<int>(A);
+  }
+  return blocked_hamming(query_bits, B, item_bits, N, W, k, mask, mask_words, out_ids,
+                         out_scores, kind, workspace, scan_bytes, stream, f);
+}

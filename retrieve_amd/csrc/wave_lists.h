@@ -9,6 +9,8 @@
 // true top-k is in some list, because a wave's threshold never exceeds its own k-th best.
 #pragma once
 
+#include <type_traits>
+
 #include "rt_common.h"
 
 namespace rt {
@@ -40,16 +42,36 @@ __device__ inline void wave_sort_desc(uint64_t* s, int n) {
   }
 }
 
+// Every composite is kept by wave_compact's default filter.
+struct KeepAll {
+  __device__ bool operator()(uint64_t) const { return true; }
+};
+
 // Sorts list[0, *count) (global) through `scratch` (LDS, sort_n entries: a power of two >=
-// *count), keeps the best min(count, k), and returns the k-th composite (0 while fewer than k
-// are held). Called by the whole wave with a wave-uniform list.
+// *count), keeps the best min(count, k) of the entries `keep_entry` accepts (the others drop
+// out), and returns the k-th composite (0 while fewer than k are held). Called by the whole
+// wave with a wave-uniform list.
+template <class Keep = KeepAll>
 __device__ inline uint64_t wave_compact(uint64_t* list, int* count, uint64_t* scratch, int sort_n,
-                                        int k) {
+                                        int k, Keep keep_entry = Keep{}) {
   const int lane = lane_id();
   wave_sync_memory();
-  const int n = *count;
-  for (int i = lane; i < sort_n; i += kWave) {
-    scratch[i] = i < n ? load_coherent(list + i) : 0ull;
+  int n = *count;
+  if constexpr (std::is_same<Keep, KeepAll>::value) {
+    for (int i = lane; i < sort_n; i += kWave) {
+      scratch[i] = i < n ? load_coherent(list + i) : 0ull;
+    }
+  } else {
+    int held = 0;
+    for (int i = lane; i < sort_n; i += kWave) {
+      const uint64_t v = i < n ? load_coherent(list + i) : 0ull;
+      const bool kept = i < n && keep_entry(v);
+      held += kept ? 1 : 0;
+      scratch[i] = kept ? v : 0ull;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) held += __shfl_xor(held, off);
+    n = held;
   }
   wave_sync_memory();
   wave_sort_desc(scratch, sort_n);

@@ -437,9 +437,10 @@ def _(item_clause_attrs, clause_is_reverse, query_values, and_mask=None):
 def _scan_clauses(q: Tensor, items: Tensor, k: int, dtype: int, item_clause_attrs: Tensor,
                   clause_is_reverse: Tensor, query_values: Tensor, mask: Tensor | None,
                   scores: Tensor, ids: Tensor) -> bool:
-    """The fused scan of ``rt_scan_topk_clauses`` (dtype 0 int8, 1 bf16, 2 fp16) into ``ids`` /
-    ``scores``; False where it does not apply (the blocked batches, k above the fused lists'
-    bound, fp32), and the caller then scans over ``clause_bits``."""
+    """The fused scan into ``ids`` / ``scores`` (dtype 0 int8, 1 bf16, 2 fp16, 3 fp32): below
+    the blocked batch ``rt_scan_topk_clauses`` (not fp32), from it ``rt_blocked_scan_topk_clauses``
+    (with a mask only: its sampled bound is taken over the mask); False where neither applies
+    (k above the fused lists' bound too), and the caller then scans over ``clause_bits``."""
     rev, qs = _clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
     b, d = q.shape
     n = items.shape[0]
@@ -447,15 +448,24 @@ def _scan_clauses(q: Tensor, items: Tensor, k: int, dtype: int, item_clause_attr
         raise ValueError(f"item_clause_attrs has {item_clause_attrs.shape[0]} rows, the items {n}")
     if qs.shape[0] != b:
         raise ValueError(f"query_values has {qs.shape[0]} rows, the queries {b}")
-    if dtype == 3 or k > MAX_FUSED_K or _use_blocked(b, d * q.element_size(), k):
+    if k > MAX_FUSED_K:
+        return False
+    blocked = _use_blocked(b, d * q.element_size(), k)
+    if (blocked and mask is None) or (not blocked and dtype == 3):
         return False
     dev = nat.require_device(q, items, item_clause_attrs, qs)
     _, c, a = item_clause_attrs.shape
     v = qs.shape[2]
     lib = nat.lib()
-    ws = nat.workspace(lib.rt_scan_topk_clauses_workspace(b, n, d, k, c, v), dev)
+    if blocked:
+        ws = nat.workspace(lib.rt_blocked_scan_topk_clauses_workspace(
+            b, n, d * q.element_size(), k, c, v), dev)
+        entry = lib.rt_blocked_scan_topk_clauses
+    else:
+        ws = nat.workspace(lib.rt_scan_topk_clauses_workspace(b, n, d, k, c, v), dev)
+        entry = lib.rt_scan_topk_clauses
     with torch.cuda.device(dev):
-        st = lib.rt_scan_topk_clauses(
+        st = entry(
             nat.ptr(q), b, nat.ptr(items), n, d, k, dtype, nat.ptr(mask),
             0 if mask is None else mask.shape[1], nat.ptr(item_clause_attrs),
             item_clause_attrs.element_size(), c, a, nat.ptr(rev), nat.ptr(qs), v, nat.ptr(ids),
@@ -540,6 +550,56 @@ def _(query, item_embs, k, item_clause_attrs, clause_is_reverse, query_values, m
     b = query.shape[0]
     return (query.new_empty((b, k), dtype=torch.int64),
             query.new_empty((b, k), dtype=torch.float32))
+
+
+@torch.library.custom_op("retrieve::hamming_scan_topk_clauses", mutates_args=(),
+                         device_types="cuda")
+def hamming_scan_topk_clauses(
+    query_bits: Tensor, item_bits: Tensor, k: int, item_clause_attrs: Tensor,
+    clause_is_reverse: Tensor, query_values: Tensor, mask: Tensor | None = None,
+    fused: bool = False,
+) -> tuple[Tensor, Tensor]:
+    """``hamming_scan_topk`` over the items that pass ``mask`` and the exact clauses: the same
+    results as ``hamming_scan_topk(q, items, k, clause_bits(attrs, rev, values, mask))``, which
+    is how it runs by default. ``fused``: where the matrix-core scan takes the batch and a mask
+    is given (e.g. a Bloom search's words), the clauses are tested inside the scan instead, for
+    the candidates that pass the mask (no ``[B, ceil(N/64)]`` clause mask in memory; slower at
+    B = 256: the bit-code kernel has no registers to spare for it). LiNR V3's filtered shortlist
+    (``modules/linr.py:155-162``)."""
+    q, mask = _hamming_prep(query_bits, item_bits, k, mask)
+    rev, qs = _clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
+    b, w = q.shape
+    n = item_bits.shape[0]
+    if item_clause_attrs.shape[0] != n:
+        raise ValueError(f"item_clause_attrs has {item_clause_attrs.shape[0]} rows, the items {n}")
+    if qs.shape[0] != b:
+        raise ValueError(f"query_values has {qs.shape[0]} rows, the queries {b}")
+    lib = nat.lib()
+    if not fused or mask is None or not lib.rt_hamming_scan_topk_clauses_fused(b, w, k):
+        bits = clause_bits(item_clause_attrs, clause_is_reverse, query_values, mask)
+        return hamming_scan_topk(q, item_bits, k, bits)
+    dev = nat.require_device(q, item_bits, item_clause_attrs, qs)
+    _, c, a = item_clause_attrs.shape
+    v = qs.shape[2]
+    ids = torch.empty((b, k), dtype=torch.int64, device=dev)
+    scores = torch.empty((b, k), dtype=torch.int32, device=dev)
+    ws = nat.workspace(lib.rt_hamming_scan_topk_clauses_workspace(b, n, w, k, c, v), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_hamming_scan_topk_clauses(
+            nat.ptr(q), b, nat.ptr(item_bits), n, w, k, nat.ptr(mask), mask.shape[1],
+            nat.ptr(item_clause_attrs), item_clause_attrs.element_size(), c, a, nat.ptr(rev),
+            nat.ptr(qs), v, nat.ptr(ids), nat.ptr(scores), 0, nat.ptr(ws), ws.numel(),
+            nat.stream(dev),
+        )
+    nat.check(st)
+    return ids, scores
+
+
+@hamming_scan_topk_clauses.register_fake
+def _(query_bits, item_bits, k, item_clause_attrs, clause_is_reverse, query_values, mask=None,
+      fused=False):
+    b = query_bits.shape[0]
+    return (query_bits.new_empty((b, k)), query_bits.new_empty((b, k), dtype=torch.int32))
 
 
 def _mask_compact(mask: Tensor, n: int) -> tuple[Tensor, Tensor]:

@@ -5,7 +5,10 @@
 to the same kernel's scan over ``clause_bits``. Covers both set forms of the predicate (bitmaps for
 values in [0, 1024), value lists otherwise), reverse and inactive clauses, rows with no active
 clause, rows with fewer than k survivors, the sampled lower bound (N above 2**21), multi-valued
-attributes, int16 / int32 / int64 tables, and the batches that fall back to the clause mask."""
+attributes, int16 / int32 / int64 tables, and the batches that fall back to the clause mask.
+The blocked (large-batch) and 1-bit forms take the clauses with a mask: their lists hold the
+candidates that pass the mask, filtered where a list is compacted and in the final merge; a
+mask that passes everything makes every candidate a clause test and every compaction a filter."""
 
 from __future__ import annotations
 
@@ -186,9 +189,119 @@ def test_opcheck(dev):
     i8 = _t(dev, g.integers(-128, 128, (4000, 64), dtype=np.int8))
     qb = torch.randn((3, 64), device=dev).bfloat16()
     ib = torch.randn((4000, 64), device=dev).bfloat16()
+    qh = _t(dev, g.integers(-2**63, 2**63 - 1, (3, 8), dtype=np.int64))
+    ih = _t(dev, g.integers(-2**63, 2**63 - 1, (4000, 8), dtype=np.int64))
     for op, args in ((torch.ops.retrieve.int8_scan_topk_clauses.default,
                       (q8, i8, 20, attrs, rev, sets)),
                      (torch.ops.retrieve.dense_scan_topk_clauses.default,
-                      (qb, ib, 20, attrs, rev, sets))):
+                      (qb, ib, 20, attrs, rev, sets)),
+                     (torch.ops.retrieve.hamming_scan_topk_clauses.default,
+                      (qh, ih, 20, attrs, rev, sets))):
         print(f"opcheck {op}", flush=True)
         torch.library.opcheck(op, args)
+
+
+def _unfused(dev, op, q, items, k, attrs, rev, sets, mask):
+    bits = torch.ops.retrieve.clause_bits(attrs, rev, sets, mask)
+    return op(q, items, k, bits)
+
+
+@pytest.mark.parametrize("b,n,d,k,dense_mask", [(40, 100_003, 128, 100, False),
+                                                (256, 60_000, 256, 1000, False),
+                                                (64, 50_000, 128, 5, True)])
+def test_blocked_int8_parity(dev, b, n, d, k, dense_mask):
+    """Large batches with a mask against the oracle; a mask of all ones leaves the clauses
+    every decision (lists fill with failing candidates and are filtered when compacted)."""
+    g = rng(b + n + k)
+    print(f"blocked int8 clause scan B={b} N={n} D={d} k={k} all-ones mask={dense_mask}",
+          flush=True)
+    q = g.integers(-128, 128, (b, d), dtype=np.int8)
+    items = g.integers(-128, 128, (n, d), dtype=np.int8)
+    attrs = g.integers(0, 20, (n, 4, 1)).astype(np.int64)
+    sets = _sets(g, b, 4, 3, 20, 0.6)
+    rev = np.array([0, 0, 1, 0], bool)
+    mask = np.ones((b, n), bool) if dense_mask else g.random((b, n)) < 0.6
+    valid = of.clause_match_sets(attrs, sets, rev) & mask
+    ids, sc = torch.ops.retrieve.int8_scan_topk_clauses(
+        _t(dev, q), _t(dev, items), k, _t(dev, attrs.astype(np.int16)), _t(dev, rev),
+        _t(dev, sets), _t(dev, _pack(mask)))
+    want_ids, want_sc = osc.int8_topk(q, items, k, valid)
+    assert np.array_equal(sc.cpu().numpy(), want_sc)
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+
+
+def test_blocked_adversarial_order(dev):
+    """Scores rising with the item index and a mask of all ones: the sampled bound is far below
+    the answer, so the lists fill and are filtered and compacted over and over."""
+    n, b = 200_000, 48
+    items = np.zeros((n, 128), np.int8)
+    items[:, 0] = (np.arange(n) * 255 // n - 127).astype(np.int8)
+    items[:, 1] = ((np.arange(n) * 7) % 5).astype(np.int8)
+    q = np.zeros((b, 128), np.int8)
+    q[:, 0] = 1
+    q[1::2, 1] = 2
+    g = rng(908)
+    attrs = g.integers(0, 10, (n, 2, 1)).astype(np.int64)
+    sets = _sets(g, b, 2, 2, 10, 0.8)
+    rev = np.zeros(2, bool)
+    mask = np.ones((b, n), bool)
+    valid = of.clause_match_sets(attrs, sets, rev)
+    print(f"blocked int8 clause scan, rising scores B={b} N={n}", flush=True)
+    for k in (100, 1000):
+        ids, sc = torch.ops.retrieve.int8_scan_topk_clauses(
+            _t(dev, q), _t(dev, items), k, _t(dev, attrs.astype(np.int16)), _t(dev, rev),
+            _t(dev, sets), _t(dev, _pack(mask)))
+        want_ids, want_sc = osc.int8_topk(q, items, k, valid)
+        assert np.array_equal(sc.cpu().numpy(), want_sc)
+        assert np.array_equal(ids.cpu().numpy(), want_ids)
+
+
+@pytest.mark.parametrize("dtype,b,n,d", [(torch.bfloat16, 256, 300_000, 128),
+                                         (torch.float16, 64, 2_200_000, 64),
+                                         (torch.bfloat16, 512, 2_200_000, 128),
+                                         (torch.float32, 64, 50_000, 64)])
+def test_blocked_dense_equals_unfused(dev, dtype, b, n, d):
+    """bf16 / fp16 / fp32 large batches with a mask equal the same scan over the clause mask:
+    the seeded path (N above 2**21) and, at B = 512, the threshold sample pass."""
+    g = rng(909 + b)
+    print(f"blocked dense clause scan {dtype} B={b} N={n} D={d}", flush=True)
+    q = torch.from_numpy(g.standard_normal((b, d)).astype(np.float32)).to(dev).to(dtype)
+    items = torch.from_numpy(g.standard_normal((n, d)).astype(np.float32)).to(dev).to(dtype)
+    attrs = _t(dev, g.integers(0, 12, (n, 3, 1)).astype(np.int16))
+    sets = _t(dev, _sets(g, b, 3, 3, 12, 0.7))
+    rev = _t(dev, np.array([0, 1, 0], bool))
+    mask = _t(dev, _pack(g.random((b, n)) < 0.5))
+    ids, sc = torch.ops.retrieve.dense_scan_topk_clauses(q, items, 100, attrs, rev, sets, mask)
+    want_ids, want_sc = _unfused(dev, torch.ops.retrieve.dense_scan_topk, q, items, 100, attrs,
+                                 rev, sets, mask)
+    assert torch.equal(ids, want_ids) and torch.equal(sc, want_sc)
+
+
+@pytest.mark.parametrize("b,n,k,ones", [(256, 200_000, 1000, False), (64, 2_200_000, 100, False),
+                                        (96, 100_000, 50, True), (5, 50_000, 20, False)])
+def test_hamming_parity(dev, b, n, k, ones):
+    """512-bit codes: the matrix-core batches fused (B = 256, k = 1000 is the 1-bit
+    configuration's shape), a small batch through the clause mask; against the oracle, and the
+    seeded case against the unfused scan."""
+    g = rng(910 + b + k)
+    print(f"hamming clause scan B={b} N={n} k={k} all-ones mask={ones}", flush=True)
+    q = g.integers(-2**63, 2**63 - 1, (b, 8), dtype=np.int64)
+    items = g.integers(-2**63, 2**63 - 1, (n, 8), dtype=np.int64)
+    attrs = g.integers(0, 16, (n, 3, 1)).astype(np.int64)
+    sets = _sets(g, b, 3, 4, 16, 0.6)
+    rev = np.array([0, 0, 1], bool)
+    mask = np.ones((b, n), bool) if ones else g.random((b, n)) < 0.5
+    args = (_t(dev, attrs.astype(np.int16)), _t(dev, rev), _t(dev, sets), _t(dev, _pack(mask)))
+    qt, it = _t(dev, q), _t(dev, items)
+    ids, sc = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args, fused=True)
+    ids2, sc2 = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args)
+    assert torch.equal(ids, ids2) and torch.equal(sc, sc2)
+    if n > 1_000_000:
+        want_ids, want_sc = _unfused(dev, torch.ops.retrieve.hamming_scan_topk, qt, it, k,
+                                     *args)
+        assert torch.equal(ids, want_ids) and torch.equal(sc, want_sc)
+        return
+    valid = of.clause_match_sets(attrs, sets, rev) & mask
+    want_ids, want_sc = osc.hamming_topk(q, items, k, valid)
+    assert np.array_equal(sc.cpu().numpy(), want_sc)
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
