@@ -248,7 +248,9 @@ __device__ inline void write_column(const BloomSearchArgs& a, int64_t b, int64_t
 // with at most one slot per tree level. The prep pass checks each plan exactly as the stack
 // evaluation does (a malformed plan matches nothing), marks every node "push" (a first child,
 // or the root) or "fold into the top with the parent's operator", and writes two program words
-// per op. A TERM's positions p (for the width of bundle 0) are stored as the byte offsets
+// per op, leaving out the AND / OR nodes flattened into a parent of the same operator (so the
+// fan-out-limited chains of a long value set are one run of folding TERMs). A TERM's positions
+// p (for the width of bundle 0) are stored as the byte offsets
 // p * 256 of their words in a staged bundle column, 14 bits each, the first repeated past the
 // term's distinct positions (AND is idempotent):
 //   word 0: bits 0-1 kind: TERM, EMPTY, PASS (an AND / OR whose children are folded into the
@@ -456,16 +458,20 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
   const int64_t c1 = c0 + chunk < n_ops ? c0 + chunk : n_ops;
   int my_terms = 0;
   int my_delta = 0;
+  int my_kept = 0;
   for (int64_t i = c0; i < c1; ++i) {
     const uint8_t op = ops[i];
     my_terms += op == kOpTerm ? 1 : 0;
     const bool pops = !flat[i] && op != kOpTerm && op != kOpEmpty;  // AND, OR, NOT
     const bool push = !flat[i] && place[i] == kPlacePush;
     my_delta += (push ? 1 : 0) - (pops ? 1 : 0);
+    my_kept += flat[i] ? 0 : 1;
   }
   int total = 0;
   int term = prep_scan_excl(my_terms, red, total);
   int depth = prep_scan_excl(my_delta, red, total);
+  int kept_total = 0;
+  int at = prep_scan_excl(my_kept, red, kept_total);  // the program leaves flattened nodes out
   int deepest = 0;
   uint32_t* out = prog + b * kProgMaxOps * 2;
   for (int64_t i = c0; i < c1; ++i) {
@@ -474,9 +480,9 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
     uint32_t w1w = 0u;
     uint32_t where = place[i];
     if (flat[i]) {
-      // a no-op: all ones AND-ed into the top (its children folded into the parent's level)
-      w0w = kKindEmpty;
-      where = kPlaceAnd;
+      // a no-op (its children folded into the parent's level): not in the program, so the
+      // sibling TERMs on either side stay one run
+      continue;
     } else if (op == kOpTerm) {
       w0w = kKindTerm | term_pos[term][0];
       w1w = term_pos[term][1];
@@ -491,13 +497,14 @@ __global__ void __launch_bounds__(kPrepThreads) bloom_prep_kernel(BloomSearchArg
       ++depth;
       deepest = depth > deepest ? depth : deepest;
     }
-    out[2 * i] = w0w | (where << 2);
-    out[2 * i + 1] = w1w;
+    out[2 * at] = w0w | (where << 2);
+    out[2 * at + 1] = w1w;
+    ++at;
   }
   deepest = prep_max(deepest, red);
   if (tid == 0) {
     write_header(hdr, b, deepest <= kFoldDepth ? kPlanProgram : kPlanStack,
-                 static_cast<int32_t>(n_ops), o[6] / 8);
+                 static_cast<int32_t>(kept_total), o[6] / 8);
   }
 }
 
