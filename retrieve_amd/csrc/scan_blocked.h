@@ -37,6 +37,7 @@ namespace rt {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -125,28 +126,62 @@ struct I8x32 {
   static constexpr bool kBits = false;
 };
 
-// 1-bit codes of 64 W bits (rows of 8 W bytes) on the int8 matrix cores: an item's bits expand
-// to {0, 1} bytes, a query's to {-2, +2} bytes, and the accumulator starts at 64 W - 2 popcount(q),
-// so it ends at 64 W - 2 popcount(q ^ x), the Hamming score, exactly (the sum over bits of
-// x (2 q - 1) is popcount(x & q) - popcount(x & ~q)). A lane's half of a row is bytes
-// [4 W half, +4 W); K step s takes its 16 bits at byte 2 s of that half.
-struct BitsX32 : I8x32 {
+// 1-bit codes of 64 W bits (rows of 8 W bytes) on the fp4 matrix cores
+// (v_mfma_scale_f32_32x32x64_f8f6f4 with e2m1 operands and unit scales): an item's bits expand
+// to {0, 1.0} nibbles, a query's to {-2.0, +2.0}, and the fp32 accumulator starts at
+// 64 W - 2 popcount(q), so it ends at the Hamming score 64 W - 2 popcount(q ^ x) exactly (the sum
+// over bits of x (4 q - 2) is 4 popcount(x & q) - 2 popcount(x), and every partial sum is an
+// integer of magnitude below 2^24). A lane's half of a row is bytes [4 W half, +4 W); K step s
+// takes its 32 bits, dword s of that half (64 K elements a step over the two lane halves; the K
+// order inside an operand is free, the same on both sides). The scores leave the accumulator as
+// int32, so the rest of the scan is the int8 scan's.
+struct BitsF4 : I8x32 {
   static constexpr bool kBits = true;
-  // bit e of b16 -> byte e of the result, {0, 1}: each nibble spreads over a dword
-  __device__ static v4i item_frag(uint32_t b16) {
-    v4i r;
+  static constexpr int kStepBits = 32;  // bits per lane per K step
+  using MAcc = v16f;
+  __device__ static MAcc mstart(int32_t start) {
+    MAcc c;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      r[n] = static_cast<int>((((b16 >> (4 * n)) & 0xfu) * 0x204081u) & 0x01010101u);
-    }
+    for (int e = 0; e < 16; ++e) c[e] = static_cast<float>(start);
+    return c;
+  }
+  __device__ static MAcc mma(v4i a, v4i b, MAcc c) {
+    // (the fp4 form reads the low four registers of each operand)
+    const v8i a8 = __builtin_shufflevector(a, a, 0, 1, 2, 3, 0, 1, 2, 3);
+    const v8i b8 = __builtin_shufflevector(b, b, 0, 1, 2, 3, 0, 1, 2, 3);
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 4, 4, 0, 0x7f7f7f7f, 0,
+                                                          0x7f7f7f7f);
+  }
+  __device__ static Acc finish(MAcc c) {
+    Acc r;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) r[e] = static_cast<int32_t>(c[e]);
     return r;
   }
-  // {-2, +2}: 0xfe - 0xfc * bit per byte (no borrows)
-  __device__ static v4i query_frag(uint32_t b16) {
-    v4i r = item_frag(b16);
+  // the 8 bits of byte x -> bit e at bit 4 e (nibble e holds bit e)
+  __host__ __device__ static uint32_t spread8(uint32_t x) {
+    x = (x | (x << 12)) & 0x000f000fu;
+    x = (x | (x << 6)) & 0x03030303u;
+    return (x | (x << 3)) & 0x11111111u;
+  }
+  __device__ static v4i spread(uint32_t b) {
+    v4i r;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) r[n] = static_cast<int>(spread8((b >> (8 * n)) & 0xffu));
+    return r;
+  }
+  // 1.0 is e2m1 0b0010; +2.0 0b0100 and -2.0 0b1100
+  __device__ static v4i item_frag(uint32_t b) {
+    v4i r = spread(b);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) r[n] = static_cast<int>(static_cast<uint32_t>(r[n]) << 1);
+    return r;
+  }
+  __device__ static v4i query_frag(uint32_t b) {
+    v4i r = spread(b);
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      r[n] = static_cast<int>(0xfefefefeu - static_cast<uint32_t>(r[n]) * 0xfcu);
+      r[n] = static_cast<int>(0xccccccccu ^ (static_cast<uint32_t>(r[n]) << 3));
     }
     return r;
   }
@@ -206,8 +241,8 @@ constexpr int kBlkMinStages = 3;
 // rows.
 constexpr int blk_mask_bytes(int rows) { return kBlkQpg * (rows / 32) * 4; }
 
-// LDS of the bit codes' byte-expansion table (256 entries of 8 bytes).
-constexpr size_t kBitsLutBytes = 256 * sizeof(uint64_t);
+// LDS of the bit codes' byte-expansion table (256 entries of 4 bytes: a byte's 8 nibbles).
+constexpr size_t kBitsLutBytes = 256 * sizeof(uint32_t);
 
 // Waves per SIMD: two (one 8-wave or two 4-wave workgroups per CU).
 constexpr int kBlkWavesPerSimd = 2;
@@ -304,8 +339,8 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   using Score = typename Op::Score;
   using L = BlkLayout<WIDE, RB, Op::kBits>;
   constexpr int ROWS = L::rows;
-  // MFMA steps per row: 32 bytes of K each, or 32 bits of a bit-code row
-  constexpr int KS = Op::kBits ? RB / 4 : RB / 32;
+  // MFMA steps per row: 32 bytes of K each, or 64 bits of a bit-code row (32 a lane half)
+  constexpr int KS = Op::kBits ? RB / 8 : RB / 32;
   constexpr int RTW = L::rtw;  // 32-row tiles per wave
   constexpr int kBlkWaves = L::waves;
   constexpr int kBlkThreads = L::threads;
@@ -341,18 +376,13 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   const int c32 = lane & 31;
   const int half = lane >> 5;
   int* cnt = reinterpret_cast<int*>(scratch + kBlkWaves * a.capw) + wave * kBlkQpw;
-  // bit codes, narrow layout: byte -> its 8 bits as {0, 1} bytes (bit e to byte e), 2 KiB after
-  // the lists' counts; filled here, read after the first tile barrier
+  // bit codes, narrow layout: byte -> its 8 bits as 1.0 / 0 nibbles (bit e to nibble e), 1 KiB
+  // after the lists' counts; filled here, read after the first tile barrier
   // (the seed pass keeps no lists: its LDS plan counts no list capacity)
-  uint64_t* lut = reinterpret_cast<uint64_t*>(
+  uint32_t* lut = reinterpret_cast<uint32_t*>(
       reinterpret_cast<int*>(scratch + kBlkWaves * (SEED ? 0 : a.capw)) + kBlkWaves * kBlkQpw);
   if constexpr (Op::kBits && !WIDE) {
-    for (int v = tid; v < 256; v += kBlkThreads) {
-      uint64_t x = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x |= static_cast<uint64_t>((v >> e) & 1) << (8 * e);
-      lut[v] = x;
-    }
+    for (int v = tid; v < 256; v += kBlkThreads) lut[v] = Op::spread8(v) << 1;
   }
   const int wr = WIDE ? wave % kBlkRowHalves : 0;  // this wave's row part of each tile
   const int jt = WIDE ? wave / kBlkRowHalves : wave;  // and its column tiles jt, jt + CST
@@ -378,7 +408,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     const int64_t q = q0[j] + c32;
     if (q < a.B) {
       if constexpr (Op::kBits) {
-        const uint16_t* qb = reinterpret_cast<const uint16_t*>(Q + q * RB + (RB / 2) * half);
+        const uint32_t* qb = reinterpret_cast<const uint32_t*>(Q + q * RB + (RB / 2) * half);
 #pragma unroll
         for (int s = 0; s < KS; ++s) qf[j][s] = Op::query_frag(qb[s]);
         const uint32_t* qw = reinterpret_cast<const uint32_t*>(Q + q * RB);
@@ -525,18 +555,14 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       // 2 x 2 output tiles (rows 32 i + ..., this wave's query columns 32 j + ...): four
       // independent accumulator chains keep the matrix pipeline full
       typename Op::Acc acc[RTW][NC];
-#pragma unroll
-      for (int i = 0; i < RTW; ++i)
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          acc[i][j] = Op::zero();
-          if constexpr (Op::kBits) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = acc0[j];
-          }
-        }
       if constexpr (Op::kBits) {
-        // this lane's half of each of its rows (RB / 2 bytes); step s expands 16 bits
+        // fp32 accumulators from 64 W - 2 popcount(q), the scores taken out as int32 after
+        typename Op::MAcc macc[RTW][NC];
+#pragma unroll
+        for (int i = 0; i < RTW; ++i)
+#pragma unroll
+          for (int j = 0; j < NC; ++j) macc[i][j] = Op::mstart(acc0[j]);
+        // this lane's half of each of its rows (RB / 2 bytes); step s expands its dword s
         constexpr int HC = CH / 2;  // 16-byte chunks per half row
         if constexpr (WIDE) {
           // (read once into registers)
@@ -551,25 +577,23 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
             }
           }
           // the wide layout (half the MFMAs per expansion at B <= 64, eight waves on the LDS):
-          // each step's 16 bits spread into bytes arithmetically
+          // each step's 32 bits spread into nibbles arithmetically
 #pragma unroll
           for (int s = 0; s < KS; ++s) {
             v4i cur[RTW];
 #pragma unroll
             for (int i = 0; i < RTW; ++i) {
-              const uint32_t w = static_cast<uint32_t>(hb[i][s / 8][(s / 2) % 4]);
-              cur[i] = Op::item_frag((s % 2) ? (w >> 16) : (w & 0xffffu));
+              cur[i] = Op::item_frag(static_cast<uint32_t>(hb[i][s / 4][s % 4]));
             }
 #pragma unroll
             for (int i = 0; i < RTW; ++i)
 #pragma unroll
-              for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(cur[i], qf[j][s], acc[i][j]);
+              for (int j = 0; j < NC; ++j) macc[i][j] = Op::mma(cur[i], qf[j][s], macc[i][j]);
           }
         } else {
-          // narrow: step s's two bytes through the LDS table (two 8-byte reads instead of a
-          // 3-instruction spread per nibble), read BPF steps ahead
-          // the 32-bit word holding a step's bits: from the half rows read once into registers,
-          // or, masked (whose mask words take those registers), from the staged tile
+          // narrow: step s's four bytes through the LDS table, read BPF steps ahead; the step's
+          // dword from the half rows read once into registers, or, masked (whose mask words
+          // take those registers), from the staged tile
           v4i hb[masked ? 1 : RTW][masked ? 1 : HC];
           if constexpr (!masked) {
 #pragma unroll
@@ -586,17 +610,15 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
             if constexpr (masked) {
               const int r = 32 * (wr * RTW + i) + c32;
               return *reinterpret_cast<const uint32_t*>(
-                  src + r * RB + (((HC * half + s / 8) ^ (r % CH)) * 16) + ((s / 2) % 4) * 4);
+                  src + r * RB + (((HC * half + s / 4) ^ (r % CH)) * 16) + (s % 4) * 4);
             } else {
-              return static_cast<uint32_t>(hb[i][s / 8][(s / 2) % 4]);
+              return static_cast<uint32_t>(hb[i][s / 4][s % 4]);
             }
           };
           auto bfrag = [&](int s, int i) {
-            const uint32_t w = bword(s, i) >> (16 * (s % 2));
-            const uint64_t lo = lut[w & 0xffu];
-            const uint64_t hi = lut[(w >> 8) & 0xffu];
-            return v4i{static_cast<int>(lo), static_cast<int>(lo >> 32), static_cast<int>(hi),
-                       static_cast<int>(hi >> 32)};
+            const uint32_t w = bword(s, i);
+            return v4i{static_cast<int>(lut[w & 0xffu]), static_cast<int>(lut[(w >> 8) & 0xffu]),
+                       static_cast<int>(lut[(w >> 16) & 0xffu]), static_cast<int>(lut[w >> 24])};
           };
           constexpr int BPF = KS < 2 ? KS : 2;
           v4i bf[BPF][RTW];
@@ -616,10 +638,18 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
 #pragma unroll
             for (int i = 0; i < RTW; ++i)
 #pragma unroll
-              for (int j = 0; j < NC; ++j) acc[i][j] = Op::mma(cur[i], qf[j][s], acc[i][j]);
+              for (int j = 0; j < NC; ++j) macc[i][j] = Op::mma(cur[i], qf[j][s], macc[i][j]);
           }
         }
+#pragma unroll
+        for (int i = 0; i < RTW; ++i)
+#pragma unroll
+          for (int j = 0; j < NC; ++j) acc[i][j] = Op::finish(macc[i][j]);
       } else {
+#pragma unroll
+        for (int i = 0; i < RTW; ++i)
+#pragma unroll
+          for (int j = 0; j < NC; ++j) acc[i][j] = Op::zero();
         // row fragments of step s: lane l reads bytes [32 s + 16 (l / 32), +16) of its row;
         // PF steps are read ahead so the LDS latency hides behind the MFMAs
         auto frag = [&](int s, int i) {

@@ -1,4 +1,4 @@
-// The blocked scan over 512-bit codes on the int8 matrix cores (scan_blocked.h).
+// The blocked scan over 512-bit codes on the fp4 matrix cores (scan_blocked.h).
 #include "scan_blocked.h"
 
 namespace rt {
@@ -17,7 +17,7 @@ int blocked_hamming(const uint64_t* query_bits, int64_t B, const uint64_t* item_
                     int64_t W, int64_t k, const uint64_t* mask, int64_t mask_words,
                     int64_t* out_ids, void* out_scores, int score_kind, void* workspace,
                     size_t workspace_bytes, hipStream_t stream, const ClauseCheck& clause) {
-  return run_blocked<BitsX32>(query_bits, B, item_bits, N, 8 * W, k, mask, mask_words, out_ids,
+  return run_blocked<BitsF4>(query_bits, B, item_bits, N, 8 * W, k, mask, mask_words, out_ids,
                               out_scores, workspace, workspace_bytes, stream, score_kind, clause);
 }
 
