@@ -57,7 +57,7 @@ MEASURED_TRAFFIC: dict = {
     ("dense", 10_000_000, 128, 4096, 100): 9_390_756_864,  # dense_bf16_10Mx128_b4096.md
     # filtered_dense_bf16_10Mx128_b256.md, binary_30Mx512bit_b256.md
     ("filtered-dense", 10_000_000, 128, 256, 100): 2_909_858_406,
-    ("binary", 30_000_000, 512, 256, 100): 3_761_035_264,
+    ("binary", 30_000_000, 512, 256, 100): 4_093_474_816,
 }
 CARDINALITIES = (16, 32, 64, 128, 256, 512, 1000, 1000)
 BLOOM_BITS, BLOOM_K, HASH_K = 64, 3, 7
@@ -550,13 +550,13 @@ def main() -> int:
             return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
 
         scan_bytes = n * d // 8 + b * d // 8
-        # 512-bit codes from 33 queries on are scored on the int8 matrix cores, one multiply-add
-        # per bit (bits as {0, 1} and {-2, +2} bytes): 2 ops per bit, item and query
+        # 512-bit codes from 33 queries on are scored on the fp4 matrix cores, one multiply-add
+        # per bit (bits as {0, 1.0} and {-2.0, +2.0} e2m1 values): 2 ops per bit, item and query
         mfma_scan = d == 512 and b >= 33
         scan_ops = 2 * b * n * d if mfma_scan else 2 * b * n * (d // 32)
         step_bytes = scan_bytes + flt.bytes(n, b, args.fused_bits) + b * k1 * d
         bound = "mfma" if mfma_scan else "hbm"
-        dtype = "int8" if mfma_scan else "u64"
+        dtype = "fp4" if mfma_scan else "u64"
         data = ("synthetic: N(0,1) rows (seed 556) and queries (seed 557), SimHash over a "
                 "N(0,1) 512x512 projection (seed 555), int8 codes of the same rows; attributes "
                 "Zipf(1.1) (seed 4321), query sets numpy seed 77")
@@ -641,7 +641,7 @@ def main() -> int:
         bound = "mfma"
     else:
         achieved = scan_ops / (kernel_ms * 1e-3) / 1e12
-        peak = {"int8": 5000.0, "bf16": 2500.0}[dtype]
+        peak = {"int8": 5000.0, "bf16": 2500.0, "fp4": 10100.0}[dtype]  # dense MFMA peaks
         unit = "TFLOP/s"
     log(f"ms/step {ms_step:.3f}; main scan {kernel_ms:.3f} ms ({achieved:.0f} {unit})")
     if bound == "mfma" and dtype in ("int8", "bf16"):
@@ -664,7 +664,7 @@ def main() -> int:
             with open(args.jsonl, "a") as f:
                 f.write(json.dumps(rec) + "\n")
     if wl == "binary":
-        extra["hamming_path"] = ("int8 matrix cores (bits as bytes)" if bound == "mfma"
+        extra["hamming_path"] = ("fp4 matrix cores (bits as e2m1 nibbles)" if bound == "mfma"
                                  else "XOR + popcount")
         extra["hamming_hbm_gbs"] = scan_bytes / (kernel_ms * 1e-3) / 1e9
 
