@@ -370,6 +370,7 @@ def main() -> int:
                                                             flt.rev, flt.sets, flt.bloom())
 
         scan_bytes = n * d + b * d  # the item table once + the query block
+        table = items  # the streamed table (the read ceiling is measured over it)
         scan_ops = 2 * b * n * d
         step_bytes = scan_bytes + (flt.bytes(n, b, not args.unfused_filter) if flt else 0)
         bound = "hbm" if 2 * b < 625 else "mfma"  # int8 ridge: 625 OP/B
@@ -415,6 +416,7 @@ def main() -> int:
                                                              flt.rev, flt.sets, flt.bloom())
 
         scan_bytes = n * d * 2 + b * d * 2
+        table = items  # the streamed table (the read ceiling is measured over it)
         scan_ops = 2 * b * n * d
         step_bytes = scan_bytes + flt.bytes(n, b, not args.unfused_filter)
         bound = "hbm" if b < 312 else "mfma"  # bf16 ridge: 312.5 FLOP/B
@@ -459,6 +461,7 @@ def main() -> int:
         extra["recall_at_k_vs_fp32"] = (
             (got.unsqueeze(2) == ref.unsqueeze(1)).any(2).sum().item() / (b * k))
         scan_bytes = n * d * 4 + b * d * 4
+        table = items  # the streamed table (the read ceiling is measured over it)
         scan_ops = 2 * b * n * d
         step_bytes = scan_bytes
         bound = "fp32"
@@ -513,6 +516,7 @@ def main() -> int:
         del items_h
 
         scan_bytes = n * d * 2 + b * d * 2
+        table = items  # the streamed table (the read ceiling is measured over it)
         scan_ops = 2 * b * n * d
         step_bytes = scan_bytes
         bound = "hbm" if b < 312 else "mfma"  # bf16 ridge: 312.5 FLOP/B
@@ -550,6 +554,7 @@ def main() -> int:
             return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
 
         scan_bytes = n * d // 8 + b * d // 8
+        table = item_bits  # the streamed table (the read ceiling is measured over it)
         # 512-bit codes from 33 queries on are scored on the fp4 matrix cores, one multiply-add
         # per bit (bits as {0, 1.0} and {-2.0, +2.0} e2m1 values): 2 ops per bit, item and query
         mfma_scan = d == 512 and b >= 33
@@ -655,6 +660,15 @@ def main() -> int:
             "main_scan_frac_of_it": achieved / (rate.value / 1e12),
         }
         log(f"matrix cores sustain {rate.value / 1e12:.0f} {unit} at {mhz.value:.0f} MHz")
+    if bound == "hbm":
+        # what one plain streaming kernel reads over the same table: the practical ceiling the
+        # scan's HBM fraction is to be read against
+        rate = ctypes.c_double()
+        _native.check(lib.rt_read_ceiling(table.data_ptr(), table.numel() * table.element_size(),
+                                          5, ctypes.byref(rate), None))
+        extra["hbm_read_ceiling"] = {"value": rate.value / 1e9, "unit": "GB/s",
+                                     "main_scan_frac_of_it": achieved / (rate.value / 1e9)}
+        log(f"a plain streaming read of the table: {rate.value / 1e9:.0f} GB/s")
     if args.windows > 0:
         rec = latency_windows(step, args.windows, args.window_calls, b, args.mode)
         extra["latency"] = {k: rec[k] for k in ("mode", "n", "windows", "median_ms", "p95_ms",

@@ -117,6 +117,13 @@ int rt_profile_collect(double* total_ms, int64_t* launches);
 int rt_mfma_ceiling(int dtype, int64_t iters, double* ops_per_s, double* clock_mhz,
                     rt_stream_t stream);
 
+/* Measurement helper (no counterpart in the reference): the streaming-read rate of one kernel
+ * over `bytes` at `data` (16-byte aligned): each 16-byte word read once per rep with
+ * nontemporal loads, 64 workgroups a CU; a warm-up pass, then `reps` timed passes. Sets
+ * *bytes_per_s. Synchronizes the stream; allocates a 4-byte sink for the call. */
+int rt_read_ceiling(const void* data, int64_t bytes, int reps, double* bytes_per_s,
+                    rt_stream_t stream);
+
 /* ---- exact clause filter --------------------------------------------------------------
  *
  * Replaces the clause kernels behind torch.ops.retrieve.clause_mask / clause_mask_scores

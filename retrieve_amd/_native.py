@@ -71,6 +71,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_int, _c_i64, _c_i64,
          _c_p, _c_p, _c_i64, _c_p, _c_p, _c_int, _c_p, _c_sz, _c_p],
     ),
+    "rt_read_ceiling": (_c_int, [_c_p, _c_i64, _c_int, _c_p, _c_p]),
     "rt_bloom_bundle_terms": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "rt_bloom_build": (
         _c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p],
