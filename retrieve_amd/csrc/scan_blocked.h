@@ -158,30 +158,23 @@ struct BitsF4 : I8x32 {
     for (int e = 0; e < 16; ++e) r[e] = static_cast<int32_t>(c[e]);
     return r;
   }
-  // the 8 bits of byte x -> bit e at bit 4 e (nibble e holds bit e)
-  __host__ __device__ static uint32_t spread8(uint32_t x) {
-    x = (x | (x << 12)) & 0x000f000fu;
-    x = (x | (x << 6)) & 0x03030303u;
-    return (x | (x << 3)) & 0x11111111u;
+  // A step's 32 bits per lane fill the 32 nibbles of the fp4 operand: nibble e of dword n holds
+  // bit 4 e + n (the K order inside an operand is free when items and queries share it), so an
+  // item dword is the word masked in place -- bit n of each nibble, e2m1 0.5, 1.0, 2.0 for
+  // n = 0, 1, 2 -- and dword 3 takes bit 3 one place down (2.0; bit 3 is the sign). The query
+  // nibble of the same slot is +-4.0, +-2.0, +-1.0, +-1.0 (sign bit set for a 0 bit), so every
+  // product of an item 1 with a query bit is +-2 exactly, and an item 0 contributes 0.
+  __device__ static v4i item_frag(uint32_t b) {
+    return v4i{static_cast<int>(b & 0x11111111u), static_cast<int>(b & 0x22222222u),
+               static_cast<int>(b & 0x44444444u), static_cast<int>((b >> 1) & 0x44444444u)};
   }
-  __device__ static v4i spread(uint32_t b) {
+  // +4.0 0b0110, +2.0 0b0100, +1.0 0b0010; the sign (bit 3) set where the query bit is 0
+  __device__ static v4i query_frag(uint32_t b) {
+    constexpr uint32_t kMag[4] = {0x66666666u, 0x44444444u, 0x22222222u, 0x22222222u};
     v4i r;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) r[n] = static_cast<int>(spread8((b >> (8 * n)) & 0xffu));
-    return r;
-  }
-  // 1.0 is e2m1 0b0010; +2.0 0b0100 and -2.0 0b1100
-  __device__ static v4i item_frag(uint32_t b) {
-    v4i r = spread(b);
-#pragma unroll
-    for (int n = 0; n < 4; ++n) r[n] = static_cast<int>(static_cast<uint32_t>(r[n]) << 1);
-    return r;
-  }
-  __device__ static v4i query_frag(uint32_t b) {
-    v4i r = spread(b);
-#pragma unroll
     for (int n = 0; n < 4; ++n) {
-      r[n] = static_cast<int>(0xccccccccu ^ (static_cast<uint32_t>(r[n]) << 3));
+      r[n] = static_cast<int>((kMag[n] | 0x88888888u) ^ (((b >> n) & 0x11111111u) << 3));
     }
     return r;
   }
@@ -240,9 +233,6 @@ constexpr int kBlkMinStages = 3;
 // Mask words staged beside each tile of a masked main pass: a 32-bit word per query and 32
 // rows.
 constexpr int blk_mask_bytes(int rows) { return kBlkQpg * (rows / 32) * 4; }
-
-// LDS of the bit codes' byte-expansion table (256 entries of 4 bytes: a byte's 8 nibbles).
-constexpr size_t kBitsLutBytes = 256 * sizeof(uint32_t);
 
 // Waves per SIMD: two (one 8-wave or two 4-wave workgroups per CU).
 constexpr int kBlkWavesPerSimd = 2;
@@ -376,14 +366,6 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   const int c32 = lane & 31;
   const int half = lane >> 5;
   int* cnt = reinterpret_cast<int*>(scratch + kBlkWaves * a.capw) + wave * kBlkQpw;
-  // bit codes, narrow layout: byte -> its 8 bits as 1.0 / 0 nibbles (bit e to nibble e), 1 KiB
-  // after the lists' counts; filled here, read after the first tile barrier
-  // (the seed pass keeps no lists: its LDS plan counts no list capacity)
-  uint32_t* lut = reinterpret_cast<uint32_t*>(
-      reinterpret_cast<int*>(scratch + kBlkWaves * (SEED ? 0 : a.capw)) + kBlkWaves * kBlkQpw);
-  if constexpr (Op::kBits && !WIDE) {
-    for (int v = tid; v < 256; v += kBlkThreads) lut[v] = Op::spread8(v) << 1;
-  }
   const int wr = WIDE ? wave % kBlkRowHalves : 0;  // this wave's row part of each tile
   const int jt = WIDE ? wave / kBlkRowHalves : wave;  // and its column tiles jt, jt + CST
   constexpr int CST = L::cstride;
@@ -562,84 +544,30 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
         for (int i = 0; i < RTW; ++i)
 #pragma unroll
           for (int j = 0; j < NC; ++j) macc[i][j] = Op::mstart(acc0[j]);
-        // this lane's half of each of its rows (RB / 2 bytes); step s expands its dword s
+        // this lane's half of each of its rows (RB / 2 bytes), read once into registers; step s
+        // masks its dword s into the four operand dwords (five VALU, no table)
         constexpr int HC = CH / 2;  // 16-byte chunks per half row
-        if constexpr (WIDE) {
-          // (read once into registers)
-          v4i hb[RTW][HC];
+        v4i hb[RTW][HC];
+#pragma unroll
+        for (int i = 0; i < RTW; ++i) {
+          const int r = 32 * (wr * RTW + i) + c32;
+#pragma unroll
+          for (int m = 0; m < HC; ++m) {
+            hb[i][m] = *reinterpret_cast<const v4i*>(src + r * RB +
+                                                     (((HC * half + m) ^ (r % CH)) * 16));
+          }
+        }
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          v4i cur[RTW];
 #pragma unroll
           for (int i = 0; i < RTW; ++i) {
-            const int r = 32 * (wr * RTW + i) + c32;
-#pragma unroll
-            for (int m = 0; m < HC; ++m) {
-              hb[i][m] = *reinterpret_cast<const v4i*>(src + r * RB +
-                                                       (((HC * half + m) ^ (r % CH)) * 16));
-            }
+            cur[i] = Op::item_frag(static_cast<uint32_t>(hb[i][s / 4][s % 4]));
           }
-          // the wide layout (half the MFMAs per expansion at B <= 64, eight waves on the LDS):
-          // each step's 32 bits spread into nibbles arithmetically
 #pragma unroll
-          for (int s = 0; s < KS; ++s) {
-            v4i cur[RTW];
+          for (int i = 0; i < RTW; ++i)
 #pragma unroll
-            for (int i = 0; i < RTW; ++i) {
-              cur[i] = Op::item_frag(static_cast<uint32_t>(hb[i][s / 4][s % 4]));
-            }
-#pragma unroll
-            for (int i = 0; i < RTW; ++i)
-#pragma unroll
-              for (int j = 0; j < NC; ++j) macc[i][j] = Op::mma(cur[i], qf[j][s], macc[i][j]);
-          }
-        } else {
-          // narrow: step s's four bytes through the LDS table, read BPF steps ahead; the step's
-          // dword from the half rows read once into registers, or, masked (whose mask words
-          // take those registers), from the staged tile
-          v4i hb[masked ? 1 : RTW][masked ? 1 : HC];
-          if constexpr (!masked) {
-#pragma unroll
-            for (int i = 0; i < RTW; ++i) {
-              const int r = 32 * (wr * RTW + i) + c32;
-#pragma unroll
-              for (int m = 0; m < HC; ++m) {
-                hb[i][m] = *reinterpret_cast<const v4i*>(src + r * RB +
-                                                         (((HC * half + m) ^ (r % CH)) * 16));
-              }
-            }
-          }
-          auto bword = [&](int s, int i) {
-            if constexpr (masked) {
-              const int r = 32 * (wr * RTW + i) + c32;
-              return *reinterpret_cast<const uint32_t*>(
-                  src + r * RB + (((HC * half + s / 4) ^ (r % CH)) * 16) + (s % 4) * 4);
-            } else {
-              return static_cast<uint32_t>(hb[i][s / 4][s % 4]);
-            }
-          };
-          auto bfrag = [&](int s, int i) {
-            const uint32_t w = bword(s, i);
-            return v4i{static_cast<int>(lut[w & 0xffu]), static_cast<int>(lut[(w >> 8) & 0xffu]),
-                       static_cast<int>(lut[(w >> 16) & 0xffu]), static_cast<int>(lut[w >> 24])};
-          };
-          constexpr int BPF = KS < 2 ? KS : 2;
-          v4i bf[BPF][RTW];
-#pragma unroll
-          for (int s = 0; s < BPF; ++s)
-#pragma unroll
-            for (int i = 0; i < RTW; ++i) bf[s][i] = bfrag(s, i);
-#pragma unroll
-          for (int s = 0; s < KS; ++s) {
-            v4i cur[RTW];
-#pragma unroll
-            for (int i = 0; i < RTW; ++i) {
-              cur[i] = bf[s % BPF][i];
-              if (s + BPF < KS) bf[s % BPF][i] = bfrag(s + BPF, i);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < RTW; ++i)
-#pragma unroll
-              for (int j = 0; j < NC; ++j) macc[i][j] = Op::mma(cur[i], qf[j][s], macc[i][j]);
-          }
+            for (int j = 0; j < NC; ++j) macc[i][j] = Op::mma(cur[i], qf[j][s], macc[i][j]);
         }
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
@@ -854,8 +782,7 @@ static size_t blk_lds(int64_t row_bytes, int stages, int capw, bool wide, bool b
                       bool masked) {
   const int rows = blk_rows(row_bytes, wide, bits);
   return static_cast<size_t>(stages) * (rows * row_bytes + (masked ? blk_mask_bytes(rows) : 0)) +
-         (wide ? 8 : 4) * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int)) +
-         (bits && !wide ? kBitsLutBytes : 0);
+         (wide ? 8 : 4) * (capw * sizeof(uint64_t) + kBlkQpw * sizeof(int));
 }
 
 // The deepest staging that fits a workgroup's share of LDS (all of it wide, half narrow, so two
