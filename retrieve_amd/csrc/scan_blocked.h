@@ -152,6 +152,27 @@ struct BitsF4 : I8x32 {
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 4, 4, 0, 0x7f7f7f7f, 0,
                                                           0x7f7f7f7f);
   }
+  // The main pass's mask as one more MFMA per 32 x 32 tile: the item operand is a one-hot -1.0
+  // at row m's slot (lane m of the lower half), the query operand the mask word's failing rows
+  // in the same in-place layout (item_frag of the inverted word: 0.5, 1.0, 2.0, 2.0 per set
+  // bit), scaled by 2^14, so a row that fails its query's mask gains at most -8192.
+  __device__ static MAcc mask_mma(v4i onehot, uint32_t mask_word, MAcc c) {
+    const v4i b = item_frag(~mask_word);
+    const v8i a8 = __builtin_shufflevector(onehot, onehot, 0, 1, 2, 3, 0, 1, 2, 3);
+    const v8i b8 = __builtin_shufflevector(b, b, 0, 1, 2, 3, 0, 1, 2, 3);
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 4, 4, 0, 0x7f7f7f7f, 0,
+                                                          0x8d8d8d8d);
+  }
+  // the one-hot operand of this lane: row c32's bit 31 - c32 of a mask word sits in nibble
+  // (31 - c32) / 4 of dword (31 - c32) % 4; -1.0 is e2m1 0b1010; the upper half is zero
+  __device__ static v4i mask_onehot(int c32, int half) {
+    const int b = 31 - c32;
+    const uint32_t v = half == 0 ? 0xau << (4 * (b >> 2)) : 0u;
+    v4i r;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) r[n] = static_cast<int>((b & 3) == n ? v : 0u);
+    return r;
+  }
   __device__ static Acc finish(MAcc c) {
     Acc r;
 #pragma unroll
@@ -178,6 +199,16 @@ struct BitsF4 : I8x32 {
     }
     return r;
   }
+};
+
+// The accumulator of an op's MFMAs: MAcc where the op has one (bit codes), else Acc.
+template <class Op, class = void>
+struct MAccOf {
+  using type = typename Op::Acc;
+};
+template <class Op>
+struct MAccOf<Op, std::void_t<typename Op::MAcc>> {
+  using type = typename Op::MAcc;
 };
 
 struct BF16x32 {
@@ -366,6 +397,9 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   const int c32 = lane & 31;
   const int half = lane >> 5;
   int* cnt = reinterpret_cast<int*>(scratch + kBlkWaves * a.capw) + wave * kBlkQpw;
+  // bit codes, masked main pass: the mask MFMA's item operand
+  v4i onehot = v4i{0, 0, 0, 0};
+  if constexpr (Op::kBits && !SEED && masked) onehot = Op::mask_onehot(c32, half);
   const int wr = WIDE ? wave % kBlkRowHalves : 0;  // this wave's row part of each tile
   const int jt = WIDE ? wave / kBlkRowHalves : wave;  // and its column tiles jt, jt + CST
   constexpr int CST = L::cstride;
@@ -416,6 +450,11 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   // thresholds in the skey domain, and whether the raw-bits group maxima decide the hit test
   int32_t th[2] = {Op::skey(ts[0]), Op::skey(ts[1])};
   bool raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
+  // bit codes, main pass: the hit test compares the fp32 accumulators, started at zero, with the
+  // threshold less the column's start 64 W - 2 popcount(q) (integers, exact in fp32)
+  float thf[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) thf[j] = static_cast<float>(th[j]) - static_cast<float>(acc0[j]);
   uint64_t best[2] = {0ull, 0ull};  // SEED
   // list slots of this wave, one per column tile: a 32-query column tile g = q / 32 has slots
   // g * S + s, s = wg * 2 + wr (S = 2 nwg), each holding 32 lists of capw entries
@@ -537,13 +576,30 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       // 2 x 2 output tiles (rows 32 i + ..., this wave's query columns 32 j + ...): four
       // independent accumulator chains keep the matrix pipeline full
       typename Op::Acc acc[RTW][NC];
-      if constexpr (Op::kBits) {
-        // fp32 accumulators from 64 W - 2 popcount(q), the scores taken out as int32 after
-        typename Op::MAcc macc[RTW][NC];
+      // the main pass's scores in fp32 from zero (bit codes): the hit test reads them as they are
+      constexpr bool FHIT = Op::kBits && !SEED;
+      typename MAccOf<Op>::type macc[RTW][NC];
+      // the staged mask bits of this lane's query over each 32-row tile (bit 31 - x: row x)
+      uint32_t mw[RTW][NC];
+      if constexpr (!SEED && masked) {
+        const uint32_t* ms =
+            reinterpret_cast<const uint32_t*>(mstage + (it % STAGES) * MASK_BYTES);
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
 #pragma unroll
-          for (int j = 0; j < NC; ++j) macc[i][j] = Op::mstart(acc0[j]);
+          for (int j = 0; j < NC; ++j) {
+            mw[i][j] = ms[(32 * (jt + CST * j) + c32) * MASK_DW + wr * RTW + i];
+          }
+      }
+      if constexpr (Op::kBits) {
+        // fp32 accumulators: the seed pass's from 64 W - 2 popcount(q), the scores taken out as
+        // int32 after; the main pass's from zero
+#pragma unroll
+        for (int i = 0; i < RTW; ++i)
+#pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            macc[i][j] = FHIT ? typename Op::MAcc{} : Op::mstart(acc0[j]);
+          }
         // this lane's half of each of its rows (RB / 2 bytes), read once into registers; step s
         // masks its dword s into the four operand dwords (five VALU, no table)
         constexpr int HC = CH / 2;  // 16-byte chunks per half row
@@ -569,10 +625,18 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
 #pragma unroll
             for (int j = 0; j < NC; ++j) macc[i][j] = Op::mma(cur[i], qf[j][s], macc[i][j]);
         }
+        if constexpr (FHIT && masked) {
 #pragma unroll
-        for (int i = 0; i < RTW; ++i)
+          for (int i = 0; i < RTW; ++i)
 #pragma unroll
-          for (int j = 0; j < NC; ++j) acc[i][j] = Op::finish(macc[i][j]);
+            for (int j = 0; j < NC; ++j) macc[i][j] = Op::mask_mma(onehot, mw[i][j], macc[i][j]);
+        }
+        if constexpr (!FHIT) {
+#pragma unroll
+          for (int i = 0; i < RTW; ++i)
+#pragma unroll
+            for (int j = 0; j < NC; ++j) acc[i][j] = Op::finish(macc[i][j]);
+        }
       } else {
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
@@ -631,20 +695,10 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       } else {
         // fast path: the max of each group of 4 registers (rows 8 g + 4 half + 0..3), and one
         // compare per tile column against the max of its 4 group maxima
-        int32_t gm[RTW][NC][4];
+        using GM = std::conditional_t<FHIT, float, int32_t>;
+        GM gm[RTW][NC][4];
+        GM thv[2];
         bool hit = false;
-        // the staged mask bits of this lane's query over each 32-row tile (bit 31 - x: row x)
-        uint32_t mw[RTW][NC];
-        if constexpr (masked) {
-          const uint32_t* ms =
-              reinterpret_cast<const uint32_t*>(mstage + (it % STAGES) * MASK_BYTES);
-#pragma unroll
-          for (int i = 0; i < RTW; ++i)
-#pragma unroll
-            for (int j = 0; j < NC; ++j) {
-              mw[i][j] = ms[(32 * (jt + CST * j) + c32) * MASK_DW + wr * RTW + i];
-            }
-        }
         // (with a mask, the maxima over the rows that pass it: a low masked bound would
         // otherwise send every group whose best row fails the mask to the slow path)
         auto maxima = [&](auto raw_c) {
@@ -662,16 +716,37 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
                 }
               }
         };
-        if (raw) {
-          maxima(std::true_type{});
+        if constexpr (FHIT) {
+          // (rows that fail the mask are below -7000 already)
+#pragma unroll
+          for (int i = 0; i < RTW; ++i)
+#pragma unroll
+            for (int j = 0; j < NC; ++j)
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                const typename MAccOf<Op>::type& v = macc[i][j];
+                gm[i][j][g] = __builtin_fmaxf(
+                    __builtin_fmaxf(__builtin_fmaxf(v[4 * g], v[4 * g + 1]), v[4 * g + 2]),
+                    v[4 * g + 3]);
+              }
+          thv[0] = thf[0];
+          thv[1] = thf[1];
         } else {
-          maxima(std::false_type{});
+          if (raw) {
+            maxima(std::true_type{});
+          } else {
+            maxima(std::false_type{});
+          }
+          thv[0] = th[0];
+          thv[1] = th[1];
         }
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
 #pragma unroll
           for (int j = 0; j < NC; ++j) {
-            hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= th[j];
+            const GM m01 = gm[i][j][0] > gm[i][j][1] ? gm[i][j][0] : gm[i][j][1];
+            const GM m23 = gm[i][j][2] > gm[i][j][3] ? gm[i][j][2] : gm[i][j][3];
+            hit |= (m01 > m23 ? m01 : m23) >= thv[j];
           }
         if (__any(hit)) {
           // slow path, narrowed by wave-uniform ballots: groups with a hit, then their registers
@@ -681,10 +756,15 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
             for (int j = 0; j < NC; ++j)
 #pragma unroll
               for (int g = 0; g < 4; ++g) {
-                if (__ballot(gm[i][j][g] >= th[j]) == 0ull) continue;
+                if (__ballot(gm[i][j][g] >= thv[j]) == 0ull) continue;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                  const Score sc = acc[i][j][4 * g + u];
+                  Score sc;
+                  if constexpr (FHIT) {
+                    sc = static_cast<int32_t>(macc[i][j][4 * g + u]) + acc0[j];
+                  } else {
+                    sc = acc[i][j][4 * g + u];
+                  }
                   if (__ballot(sc >= ts[j]) == 0ull) continue;
                   const int64_t row = rt + 32 * (wr * RTW + i) + 8 * g + u;
                   const uint32_t item = static_cast<uint32_t>(row);
