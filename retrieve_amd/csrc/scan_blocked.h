@@ -53,11 +53,11 @@ constexpr int64_t kBlkWideMaxBatch = 128;
 
 // Rows per staged tile: 32 for narrow 512-byte rows, so four stages fit in half the LDS; 128
 // for the wide layout below 512-byte rows (its row quarters are 32 rows); 64 otherwise; for
-// 64-byte bit-code rows 128 wide (one 16-byte load per thread) and 32 narrow (one row tile per
-// wave, so its accumulators and the query fragments fit in registers; the first two waves load
-// the 2 KiB tile).
+// 64-byte bit-code rows 128 wide (one 16-byte load per thread) and 64 narrow (two row tiles per
+// wave: half the tile barriers and waits of 32-row tiles per MFMA, and whole 64-bit mask words
+// per query).
 constexpr int blk_rows(int64_t row_bytes, bool wide, bool bits) {
-  return bits ? (wide ? 128 : 32)
+  return bits ? (wide ? 128 : 64)
               : (wide ? (row_bytes < 512 ? 128 : 64) : (row_bytes >= 512 ? 32 : 64));
 }
 
@@ -200,6 +200,9 @@ struct BitsF4 : I8x32 {
     return r;
   }
 };
+
+// Start of the bit-code main pass's fp32 accumulators (above twice the largest row width).
+constexpr float kBitsBias = 2048.0f;
 
 // The accumulator of an op's MFMAs: MAcc where the op has one (bit codes), else Acc.
 template <class Op, class = void>
@@ -383,6 +386,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
                 "tile must split into 16-byte loads");
   static_assert(SEED || (kBlkQpg * MASK_DW) % kBlkThreads == 0, "mask words per thread");
   static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
+  static_assert(!Op::kBits || 2.0f * 8 * RB < kBitsBias, "bit-code sums stay below the bias");
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   int8_t* stage = reinterpret_cast<int8_t*>(smem);
   // with a mask: [STAGES][kBlkQpg][MASK_DW] mask words after the tiles (none otherwise)
@@ -450,11 +454,20 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   // thresholds in the skey domain, and whether the raw-bits group maxima decide the hit test
   int32_t th[2] = {Op::skey(ts[0]), Op::skey(ts[1])};
   bool raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
-  // bit codes, main pass: the hit test compares the fp32 accumulators, started at zero, with the
-  // threshold less the column's start 64 W - 2 popcount(q) (integers, exact in fp32)
-  float thf[2];
+  // bit codes, main pass: the fp32 accumulators start at kBitsBias instead of the column's
+  // 64 W - 2 popcount(q), so a row that passes the mask ends positive (|sum| <= 2 * 64 W <
+  // kBitsBias) and one that fails it negative (the mask MFMA's -8192 or less); the hit test takes
+  // signed int maxima of the raw bits, exact among positive floats and below them for negative
+  // ones, against the threshold moved into the same domain (INT32_MIN: every row hits, when the
+  // threshold is not positive there)
+  int32_t thr[2];
+  int32_t accb[2];  // the score of a register: int32(value) + accb
 #pragma unroll
-  for (int j = 0; j < 2; ++j) thf[j] = static_cast<float>(th[j]) - static_cast<float>(acc0[j]);
+  for (int j = 0; j < 2; ++j) {
+    const float t = static_cast<float>(th[j]) - static_cast<float>(acc0[j]) + kBitsBias;
+    thr[j] = t > 0.0f ? __builtin_bit_cast(int32_t, t) : INT32_MIN;
+    accb[j] = acc0[j] - static_cast<int32_t>(kBitsBias);
+  }
   uint64_t best[2] = {0ull, 0ull};  // SEED
   // list slots of this wave, one per column tile: a 32-query column tile g = q / 32 has slots
   // g * S + s, s = wg * 2 + wr (S = 2 nwg), each holding 32 lists of capw entries
@@ -593,12 +606,12 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       }
       if constexpr (Op::kBits) {
         // fp32 accumulators: the seed pass's from 64 W - 2 popcount(q), the scores taken out as
-        // int32 after; the main pass's from zero
+        // int32 after; the main pass's from kBitsBias
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
 #pragma unroll
           for (int j = 0; j < NC; ++j) {
-            macc[i][j] = FHIT ? typename Op::MAcc{} : Op::mstart(acc0[j]);
+            macc[i][j] = Op::mstart(FHIT ? static_cast<int32_t>(kBitsBias) : acc0[j]);
           }
         // this lane's half of each of its rows (RB / 2 bytes), read once into registers; step s
         // masks its dword s into the four operand dwords (five VALU, no table)
@@ -695,9 +708,8 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       } else {
         // fast path: the max of each group of 4 registers (rows 8 g + 4 half + 0..3), and one
         // compare per tile column against the max of its 4 group maxima
-        using GM = std::conditional_t<FHIT, float, int32_t>;
-        GM gm[RTW][NC][4];
-        GM thv[2];
+        int32_t gm[RTW][NC][4];
+        int32_t thv[2];
         bool hit = false;
         // (with a mask, the maxima over the rows that pass it: a low masked bound would
         // otherwise send every group whose best row fails the mask to the slow path)
@@ -717,20 +729,14 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
               }
         };
         if constexpr (FHIT) {
-          // (rows that fail the mask are below -7000 already)
 #pragma unroll
           for (int i = 0; i < RTW; ++i)
 #pragma unroll
             for (int j = 0; j < NC; ++j)
 #pragma unroll
-              for (int g = 0; g < 4; ++g) {
-                const typename MAccOf<Op>::type& v = macc[i][j];
-                gm[i][j][g] = __builtin_fmaxf(
-                    __builtin_fmaxf(__builtin_fmaxf(v[4 * g], v[4 * g + 1]), v[4 * g + 2]),
-                    v[4 * g + 3]);
-              }
-          thv[0] = thf[0];
-          thv[1] = thf[1];
+              for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, true>(macc[i][j], g);
+          thv[0] = thr[0];
+          thv[1] = thr[1];
         } else {
           if (raw) {
             maxima(std::true_type{});
@@ -744,9 +750,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
         for (int i = 0; i < RTW; ++i)
 #pragma unroll
           for (int j = 0; j < NC; ++j) {
-            const GM m01 = gm[i][j][0] > gm[i][j][1] ? gm[i][j][0] : gm[i][j][1];
-            const GM m23 = gm[i][j][2] > gm[i][j][3] ? gm[i][j][2] : gm[i][j][3];
-            hit |= (m01 > m23 ? m01 : m23) >= thv[j];
+            hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= thv[j];
           }
         if (__any(hit)) {
           // slow path, narrowed by wave-uniform ballots: groups with a hit, then their registers
@@ -761,7 +765,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
                 for (int u = 0; u < 4; ++u) {
                   Score sc;
                   if constexpr (FHIT) {
-                    sc = static_cast<int32_t>(macc[i][j][4 * g + u]) + acc0[j];
+                    sc = static_cast<int32_t>(macc[i][j][4 * g + u]) + accb[j];
                   } else {
                     sc = acc[i][j][4 * g + u];
                   }
