@@ -236,6 +236,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   __shared__ uint64_t red[2 * kMergeWaves];
   __shared__ int sh[4];
   const int tid = threadIdx.x;
+  if (m.run_if != nullptr && *m.run_if == 0u) return;  // (uniform: the fallback is not needed)
   const int64_t q = blockIdx.x;
   const int64_t g = q / m.qpw;
   const int qi = static_cast<int>(q % m.qpw);
@@ -358,8 +359,10 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     if (held == k) block_minmax(buf, held, red, &lo, &hi);
     if (tid == 0) {
       const uint64_t t = held == k ? lo : 0ull;
-      const uint64_t old = m.tau_keep ? m.tau_out[q] : 0ull;
+      const uint64_t old =
+          m.tau_keep ? (m.tau_base != nullptr ? m.tau_base[q] : m.tau_out[q]) : 0ull;
       m.tau_out[q] = t > old ? t : old;
+      if (m.spec_flag != nullptr && q == 0) *m.spec_flag = 0u;
     }
     return;
   }
@@ -382,6 +385,9 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     }
   }
 
+  if (m.spec_flag != nullptr && tid == 0 && buf[k - 1] == 0ull && m.spec_tau[q] > m.safe_tau[q]) {
+    atomicOr(m.spec_flag, 1u);
+  }
   for (int j = tid; j < k; j += kMergeThreads) {
     const uint64_t c = buf[j];
     const bool ok = c != 0ull;

@@ -25,6 +25,7 @@
 // kernel at large batches.
 #pragma once
 
+#include <cmath>
 #include <type_traits>
 
 #include "profile.h"
@@ -360,6 +361,7 @@ template <class Op, int RB, bool SEED, int STAGES, bool WIDE, bool MASKED, bool 
 __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     __attribute__((amdgpu_waves_per_eu(kBlkWavesPerSimd, kBlkWavesPerSimd)))
     scan_blocked_kernel(ScanArgs a) {
+  if (a.run_if != nullptr && *a.run_if == 0u) return;  // (uniform: the fallback is not needed)
   using Score = typename Op::Score;
   using L = BlkLayout<WIDE, RB, Op::kBits>;
   constexpr int ROWS = L::rows;
@@ -1008,8 +1010,11 @@ __global__ void __launch_bounds__(256) mask_transpose_kernel(const uint64_t* mas
 static int blk_capw(int64_t k, int rows) { return static_cast<int>(next_pow2(k + rows)); }
 
 // The plan, and with a mask the transposed mask's place at the end of the workspace.
+// The plan; after its own areas the speculative bounds [B] and the fallback flag, then, with a
+// mask, the transposed mask.
 static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int64_t target_cus,
-                         bool bits, bool masked, size_t* off_mask_t = nullptr) {
+                         bool bits, bool masked, size_t* off_mask_t = nullptr,
+                         size_t* off_spec = nullptr) {
   const bool wide = blk_wide(row_bytes, B);
   // the row-quarter layout covers column tiles 0-3 only (B <= kBlkWideMaxBatch = 128): its
   // lists are sized for those 128 queries
@@ -1017,6 +1022,9 @@ static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int
   const int64_t qpg = halves == 4 ? kBlkQpg / 2 : kBlkQpg;
   ScanPlan p = plan_scan(B, N, k, qpg, halves * qpg, target_cus * (wide ? 1 : 2),
                          blk_capw(k, blk_rows(row_bytes, wide, bits)), kBlkRows);
+  if (off_spec != nullptr) *off_spec = align_up(p.total, 256);
+  p.total = align_up(p.total, 256) + align_up(static_cast<size_t>(B) * sizeof(uint64_t), 256) +
+            256;
   if (off_mask_t != nullptr) *off_mask_t = align_up(p.total, 256);
   if (masked) {
     p.total = align_up(p.total, 256) +
@@ -1026,12 +1034,23 @@ static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int
   return p;
 }
 
-// The threshold sample pass (batches of at least kSampleMinBatch queries: where
-// the list appends behind the seed's bound cost more than the pass): every kSampleTileStride-th
-// tile, when that gives kSampleMinTiles tiles or more.
-constexpr int64_t kSampleMinBatch = 512;
+// The threshold sample pass: the main kernel on every kSampleTileStride-th tile, when that gives
+// kSampleMinTiles tiles or more, behind the seed's bound. Its merge takes a speculative bound,
+// the m-th best of the sample with m = sample_rank(k): an unordered table puts about
+// Poisson(k / stride) of its top k in the sample, so m = k / stride + 5 sqrt(k / stride) + 4 falls
+// below the table's k-th best but for a tail of about 1e-6 a query, and the main pass then
+// keeps about m * stride candidates a query instead of the N k / (seed rows) behind the seed's
+// bound. A query that ends with fewer than k entries although its bound was above the seed's
+// raises a flag, and the fallback (the main pass and the merge again behind the seed's bound,
+// both returning at once on the device while the flag is clear) keeps every result exact.
 constexpr int64_t kSampleTileStride = 16;
 constexpr int64_t kSampleMinTiles = 2048;
+
+static int sample_rank(int64_t k) {
+  const double lam = static_cast<double>(k) / kSampleTileStride;
+  const int64_t m = static_cast<int64_t>(std::ceil(lam + 5.0 * std::sqrt(lam) + 4.0));
+  return static_cast<int>(m < k ? m : k);
+}
 
 
 
@@ -1065,8 +1084,9 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   }
   const bool wide = blk_wide(row_bytes, B);
   size_t off_mask_t = 0;
+  size_t off_spec = 0;
   const ScanPlan plan = blk_plan(B, N, k, row_bytes, cus, Op::kBits, mask != nullptr,
-                                 &off_mask_t);
+                                 &off_mask_t, &off_spec);
   RT_CHECK_ARG(blk_stages(row_bytes, plan.main.capw, wide, Op::kBits, mask != nullptr) != 0,
                "k = %lld is too large for the blocked scan at %lld-byte rows",
                static_cast<long long>(k), static_cast<long long>(row_bytes));
@@ -1078,6 +1098,9 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   uint64_t* lists = reinterpret_cast<uint64_t*>(ws + plan.off_lists);
   int* counts = reinterpret_cast<int*>(ws + plan.off_counts);
   uint64_t* tau = reinterpret_cast<uint64_t*>(ws + plan.off_tau);
+  uint64_t* spec = reinterpret_cast<uint64_t*>(ws + off_spec);
+  uint32_t* spec_flag = reinterpret_cast<uint32_t*>(
+      ws + off_spec + align_up(static_cast<size_t>(B) * sizeof(uint64_t), 256));
 
   ScanArgs a{};
   a.queries = queries;
@@ -1131,23 +1154,28 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   a.row_stride = 1;
   a.capw = plan.main.capw;
   a.tau_in = plan.seeded ? tau : nullptr;
-  if (plan.seeded && B >= kSampleMinBatch &&
-      N >= kSampleMinTiles * kSampleTileStride * kBlkRows) {
-    // at large batches the list appends behind a loose bound cost more than the matrix work:
-    // the exact k-th over every kSampleTileStride-th tile (the main kernel on those tiles, then
-    // a threshold merge) tightens the bound about N / (sample rows) fold for the main pass
+  const bool sampled = plan.seeded && N >= kSampleMinTiles * kSampleTileStride * kBlkRows;
+  const bool speculative = sampled && sample_rank(k) < k;
+  if (sampled) {
     a.tile_stride = kSampleTileStride;
     int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, wide, stream);
     if (st != kOk) return st;
     m.capw = plan.main.capw;
     m.S = plan.main.S;
-    m.tau_out = tau;
+    m.k = sample_rank(k);
+    m.tau_out = spec;
     m.tau_keep = true;
+    m.tau_base = tau;
+    m.spec_flag = spec_flag;  // (cleared)
     st = launch_merge(m, stream);
     if (st != kOk) return st;
+    m.k = static_cast<int>(k);
     m.tau_out = nullptr;
     m.tau_keep = false;
+    m.tau_base = nullptr;
+    m.spec_flag = nullptr;
     a.tile_stride = 1;
+    a.tau_in = spec;
   }
   hipEvent_t stop;
   profile_begin(stream, &stop);
@@ -1159,6 +1187,20 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   m.out_ids = out_ids;
   m.out_scores = out_scores;
   m.score_kind = score_kind;
+  if (speculative) {
+    m.spec_flag = spec_flag;
+    m.spec_tau = spec;
+    m.safe_tau = tau;
+  }
+  st = launch_merge(m, stream);
+  if (st != kOk || !speculative) return st;
+  // the fallback behind the seed's bound (returns at once while the flag is clear)
+  a.tau_in = tau;
+  a.run_if = spec_flag;
+  st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, wide, stream);
+  if (st != kOk) return st;
+  m.spec_flag = nullptr;
+  m.run_if = spec_flag;
   return launch_merge(m, stream);
 }
 

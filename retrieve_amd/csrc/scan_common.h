@@ -47,6 +47,7 @@ struct ScanArgs {
   ClauseCheck clause;      // exact clauses tested per candidate (active null: none; the
                            // scans of scan_mfma.hip)
   int clause_lds;          // main pass: the query group's set bitmaps copied to LDS
+  const uint32_t* run_if;  // not null: the pass runs only if *run_if != 0 (a fallback pass)
 };
 
 enum ScoreKind : int {
@@ -65,7 +66,15 @@ struct MergeArgs {
   int64_t B;
   int k;
   uint64_t* tau_out;   // threshold mode: [B]
-  bool tau_keep;       // threshold mode: write max(tau_out[q], the new bound)
+  bool tau_keep;       // threshold mode: write max(tau_base[q] (or tau_out[q]), the new bound)
+  const uint64_t* tau_base;  // threshold mode with tau_keep: the bound to keep, or null
+  const uint32_t* run_if;    // not null: the merge runs only if *run_if != 0 (a fallback merge)
+  // Speculative bounds: in threshold mode block 0 clears *spec_flag; in final mode a query that
+  // holds fewer than k entries although its bound spec_tau[q] is above the safe safe_tau[q]
+  // sets it (its scan may have dropped items between the two bounds).
+  uint32_t* spec_flag;
+  const uint64_t* spec_tau;
+  const uint64_t* safe_tau;
   int64_t* out_ids;    // final mode: [B, k]
   void* out_scores;    // final mode: [B, k]
   int score_kind;

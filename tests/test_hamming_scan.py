@@ -133,6 +133,40 @@ def test_matrix_core_sample_pass(dev):
     _check(dev, q, items, 100, mask)
 
 
+@pytest.mark.parametrize("masked", [False, True])
+def test_matrix_core_speculative_bound(dev, masked):
+    """N >= 2.1M rows below 512 queries: the threshold sample pass bounds the main pass by the
+    sample's m-th best (m = 23 at k = 100, 106 at k = 1000), and the results stay exact."""
+    g = rng(38 + masked)
+    q = _codes(g, 40, 8)
+    base = _codes(g, 4096, 8)
+    items = base[g.integers(0, 4096, 2_200_000)]  # repeated rows keep the oracle's work small
+    mask = g.random((40, 2_200_000)) < 0.5 if masked else None
+    _check(dev, q, items, 100, mask)
+    _check(dev, q[:33], items, 1000, None if mask is None else mask[:33])
+
+
+def _near(q: np.ndarray, d: int) -> np.ndarray:
+    """``q`` with its lowest ``d`` bits flipped (d < 64): the score 64 W - 2 d against q."""
+    x = q.copy()
+    x[0] ^= np.int64((1 << d) - 1)
+    return x
+
+
+def test_matrix_core_speculative_fallback(dev):
+    """Query 0's 30 best rows sit in the table's first tile, which the threshold sample pass
+    reads: the sample's 23rd best (k = 100) bounds the main pass above all but 23 rows, so that
+    query ends short of k, the fallback pass behind the seed's bound runs, and every result is
+    exact."""
+    g = rng(40)
+    q = _codes(g, 40, 8)
+    base = _codes(g, 4096, 8)
+    items = base[g.integers(0, 4096, 2_200_000)]
+    for r in range(30):
+        items[r] = _near(q[0], r + 1)
+    _check(dev, q, items, 100)
+
+
 def test_oporp_full_schema(dev):
     g = rng(34)
     q = torch.from_numpy(_codes(g, 4, 8)).to(dev)

@@ -305,3 +305,37 @@ def test_hamming_parity(dev, b, n, k, ones):
     want_ids, want_sc = osc.hamming_topk(q, items, k, valid)
     assert np.array_equal(sc.cpu().numpy(), want_sc)
     assert np.array_equal(ids.cpu().numpy(), want_ids)
+
+
+def test_hamming_speculative_fallback(dev):
+    """N >= 2.1M rows, clauses tested in the scan: query 0's 30 best rows that pass its clause
+    sit in the table's first tile (read by the threshold sample pass) behind 30 better rows that
+    pass its mask but fail the clause. The sample's bound counts passing rows only (its 23rd best
+    at k = 100), the main pass ends with 23 passing entries, the fallback behind the seed's bound
+    runs, and the results match the oracle."""
+    g = rng(916)
+    b, n, k = 40, 2_200_000, 100
+    print(f"hamming clause scan, speculative fallback B={b} N={n} k={k}", flush=True)
+    q = g.integers(-2**63, 2**63 - 1, (b, 8), dtype=np.int64)
+    base = g.integers(-2**63, 2**63 - 1, (4096, 8), dtype=np.int64)
+    items = base[g.integers(0, 4096, n)]
+    attrs = g.integers(0, 16, (n, 3, 1)).astype(np.int64)
+    sets = _sets(g, b, 3, 4, 16, 0.6)
+    sets[0] = -1
+    sets[0, 0, 0] = 5  # query 0: attribute 0 equal to 5
+    rev = np.array([0, 0, 1], bool)
+    for r in range(60):
+        x = q[0].copy()
+        x[0] ^= np.int64((1 << (61 - r if r < 30 else r - 29)) - 1)
+        items[r] = x  # rows 0-29: 60 .. 31 bits off; rows 30-59: 1 .. 30 bits off
+        attrs[r, 0, 0] = 5 if r < 30 else 6
+    mask = g.random((b, n)) < 0.5
+    mask[0, :60] = True
+    args = (_t(dev, attrs.astype(np.int16)), _t(dev, rev), _t(dev, sets), _t(dev, _pack(mask)))
+    ids, sc = torch.ops.retrieve.hamming_scan_topk_clauses(_t(dev, q), _t(dev, items), k, *args,
+                                                           fused=True)
+    valid = of.clause_match_sets(attrs, sets, rev) & mask
+    want_ids, want_sc = osc.hamming_topk(q, items, k, valid)
+    assert np.array_equal(sc.cpu().numpy(), want_sc)
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+    assert set(range(30)) <= set(ids[0].tolist())
