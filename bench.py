@@ -311,9 +311,9 @@ def main() -> int:
     ap.add_argument("--filter", choices=("bloom", "none"), default=None,
                     help="kept for older command lines: none = --workload int8")
     ap.add_argument("--selectivity", type=float, default=0.1)
-    ap.add_argument("--fused-bits", action="store_true",
-                    help="binary: test the clauses inside the 1-bit scan (default: the clause "
-                         "mask is written first, faster at B = 256)")
+    ap.add_argument("--unfused-bits", action="store_true",
+                    help="binary: write the clause mask before the 1-bit scan (default: the "
+                         "clauses are tested inside the scan, for the candidates only)")
     ap.add_argument("--unfused-filter", action="store_true",
                     help="filtered workloads: write the clause-checked mask before the scan "
                          "instead of checking the clauses inside it")
@@ -545,11 +545,9 @@ def main() -> int:
         flt = Filter(n, b, args.selectivity, dev)
 
         def step():
-            # (the clause mask is written first: faster here than testing the clauses inside
-            # the bit-code kernel, which has no registers to spare)
             ids1, _ = torch.ops.retrieve.hamming_scan_topk_clauses(
                 q_bits, item_bits, k1, flt.attrs, flt.rev, flt.sets, flt.bloom(),
-                fused=args.fused_bits)
+                fused=not args.unfused_bits)
             counts = (ids1 >= 0).sum(1)
             return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
 
@@ -559,7 +557,7 @@ def main() -> int:
         # per bit (bits as {0, 1.0} and {-2.0, +2.0} e2m1 values): 2 ops per bit, item and query
         mfma_scan = d == 512 and b >= 33
         scan_ops = 2 * b * n * d if mfma_scan else 2 * b * n * (d // 32)
-        step_bytes = scan_bytes + flt.bytes(n, b, args.fused_bits) + b * k1 * d
+        step_bytes = scan_bytes + flt.bytes(n, b, not args.unfused_bits) + b * k1 * d
         bound = "mfma" if mfma_scan else "hbm"
         dtype = "fp4" if mfma_scan else "u64"
         data = ("synthetic: N(0,1) rows (seed 556) and queries (seed 557), SimHash over a "
@@ -567,8 +565,8 @@ def main() -> int:
                 "Zipf(1.1) (seed 4321), query sets numpy seed 77")
         workload = (f"binary top-{k1} + int8 rerank top-{k}: N={n} bits={d} B={b}; Bloom + exact "
                     f"filter at {args.selectivity:.0%} target selectivity"
-                    + ("; the clauses checked inside the scan" if args.fused_bits
-                       else "; the clause mask written before the scan"))
+                    + ("; the clause mask written before the scan" if args.unfused_bits
+                       else "; the clauses checked inside the scan"))
         extra["measured_selectivity"] = float(flt.selectivity.mean())
         metric = ("queries/sec + achieved HBM GB/s, filtered 1-bit top-1000 + int8 rerank "
                   "top-100 over 30M items")

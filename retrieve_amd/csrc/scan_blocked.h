@@ -352,7 +352,7 @@ __device__ inline void tile_barrier() {
 
 // SEED: per query, each workgroup's best composite over the strided sample, written to
 // lists[q * gridDim.x + workgroup] (one-entry lists); else candidate lists per (wave, query).
-// MASKED (main pass only): the tiles' mask words are staged and tested; a separate
+// MASKED: the tiles' mask words are staged and tested (seed and main pass); a separate
 // instantiation keeps the unmasked kernel's registers free of it. CLAUSES (with a mask): the
 // exact clauses of a.clause are tested on each seed lane's best, and the main pass's lists
 // (candidates that pass the mask) drop the entries that fail them when compacted (and in the
@@ -381,18 +381,18 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   // query, one per 32 rows, MLOADS 4-byte loads per thread.
   constexpr int MASK_DW = ROWS / 32;
   constexpr int MASK_BYTES = blk_mask_bytes(ROWS);
-  constexpr int MLOADS = SEED ? 0 : kBlkQpg * MASK_DW / kBlkThreads;
+  constexpr int MLOADS = MASKED ? kBlkQpg * MASK_DW / kBlkThreads : 0;
   constexpr int LOADS = TLOADS + MLOADS;  // loads per thread per tile, with a mask
   constexpr int CH = RB / 16;             // 16-byte chunks per row
   static_assert(TWAVES >= 1 && TILE_BYTES % (TWAVES * kWave * 16) == 0,
                 "tile must split into 16-byte loads");
-  static_assert(SEED || (kBlkQpg * MASK_DW) % kBlkThreads == 0, "mask words per thread");
+  static_assert(!MASKED || (kBlkQpg * MASK_DW) % kBlkThreads == 0, "mask words per thread");
   static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
   static_assert(!Op::kBits || 2.0f * 8 * RB < kBitsBias, "bit-code sums stay below the bias");
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   int8_t* stage = reinterpret_cast<int8_t*>(smem);
   // with a mask: [STAGES][kBlkQpg][MASK_DW] mask words after the tiles (none otherwise)
-  constexpr bool masked = MASKED && !SEED;
+  constexpr bool masked = MASKED;
   int8_t* mstage = stage + STAGES * TILE_BYTES;
   uint64_t* scratch =
       reinterpret_cast<uint64_t*>(mstage + (masked ? STAGES * MASK_BYTES : 0));
@@ -423,7 +423,6 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   v4i qf[2][KS];
   uint64_t tau[2];
   Score ts[2];
-  const uint64_t* qmask[2];
   int32_t acc0[2] = {0, 0};  // accumulator start per column tile (bit codes: 64 W - 2 |q|)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -451,7 +450,6 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       tau[j] = ~0ull;
     }
     ts[j] = Op::thresh(tau[j]);
-    qmask[j] = a.mask != nullptr && q < a.B ? a.mask + q * a.mask_words : nullptr;
   }
   // thresholds in the skey domain, and whether the raw-bits group maxima decide the hit test
   int32_t th[2] = {Op::skey(ts[0]), Op::skey(ts[1])};
@@ -504,10 +502,12 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   // (temporal loads); with one group each tile is read once and streams past (nontemporal).
   const bool shared_tiles = gridDim.y > 1;
   auto issue_mask = [&](int64_t tt, int st) {
-    // word e of the stage: query qg0 + e / MASK_DW, rows tt * ROWS + 32 (e % MASK_DW) + 0..31 at
-    // bits 31..0 (the high half of a 64-bit mask word holds its first 32 rows)
-    const int64_t last = ((n + 63) >> 6) - 1;  // the transposed mask's last word row
-    const int64_t w0 = (tt * ROWS) >> 6;       // the tile's first word row (<= last)
+    // word e of the stage: query qg0 + e / MASK_DW, the tile's items i0 + 32 (e % MASK_DW) +
+    // 0..31 at bits 31..0 (the high half of a 64-bit mask word holds its first 32 items); the
+    // seed's tiles lie whole in its sample blocks, so their items are consecutive too
+    const int64_t i0 = SEED ? sample_item(tt * ROWS, a.row_stride) : tt * ROWS;
+    const int64_t last = a.mask_t_rows - 1;  // the transposed mask's last word row
+    const int64_t w0 = i0 >> 6;              // the tile's first word row (<= last)
     const int64_t avail = (last - w0 + 1) * a.mask_t_stride * 8;
     const uint64_t* mbase = a.mask_t + w0 * a.mask_t_stride;
     const int mrange = static_cast<int>(avail < INT32_MAX ? avail : INT32_MAX);
@@ -515,7 +515,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     for (int l = 0; l < MLOADS; ++l) {
       const int e = (l * kBlkWaves + wave) * kWave + lane;
       // from the transposed mask: a tile's words for the group's queries are contiguous
-      const int64_t r0 = tt * ROWS + 32 * (e % MASK_DW);
+      const int64_t r0 = i0 + 32 * (e % MASK_DW);
       int64_t w = r0 >> 6;
       w = w < last ? w : last;  // rows past the end: never scored
       const int off = static_cast<int>(((w - w0) * a.mask_t_stride + qg0 + e / MASK_DW) * 8) +
@@ -527,9 +527,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   auto issue = [&](int64_t lt, int st) {
     const int64_t tt = lt * tstride;  // the tile in the item table
     int8_t* base = stage + st * TILE_BYTES;
-    if constexpr (!SEED) {
-      if constexpr (masked) issue_mask(tt, st);
-    }
+    if constexpr (masked) issue_mask(tt, st);
     // One buffer descriptor per tile: base = its first row, range = its rows present. A tile's
     // rows are consecutive (the seed's sample blocks hold whole tiles, and only the last tile
     // is partial); rows past the end read as zeros and are never scored. Buffer loads rather
@@ -596,7 +594,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       typename MAccOf<Op>::type macc[RTW][NC];
       // the staged mask bits of this lane's query over each 32-row tile (bit 31 - x: row x)
       uint32_t mw[RTW][NC];
-      if constexpr (!SEED && masked) {
+      if constexpr (masked) {
         const uint32_t* ms =
             reinterpret_cast<const uint32_t*>(mstage + (it % STAGES) * MASK_BYTES);
 #pragma unroll
@@ -690,6 +688,15 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       // register r of tile (i, j) holds row t * 64 + 32 i + (r / 4) * 8 + 4 half + r % 4
       const int64_t rt = t * tstride * ROWS + 4 * half;
       if constexpr (SEED) {
+        // the mask words with this lane's half shifted out of the way (bit 31 - 8 g - u: row
+        // 8 g + 4 half + u)
+        uint32_t mwh[RTW][NC];
+        if constexpr (masked) {
+#pragma unroll
+          for (int i = 0; i < RTW; ++i)
+#pragma unroll
+            for (int j = 0; j < NC; ++j) mwh[i][j] = mw[i][j] << (4 * half);
+        }
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
 #pragma unroll
@@ -698,13 +705,17 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
             const uint32_t item = static_cast<uint32_t>(sample_item(row, a.row_stride));
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-              const uint64_t c = composite(Op::key(acc[i][j][r]), item);
-              // the mask word is read only for a composite that would raise the best
-              bool ok = row < n && c > best[j];
-              if (ok && qmask[j] != nullptr) {
-                ok = (qmask[j][item >> 6] >> (63 - (item & 63))) & 1ull;
+              uint32_t key = Op::key(acc[i][j][r]);
+              if constexpr (masked) {
+                // a row that fails the mask keeps key 0: below every score, so it is a lane's
+                // best only where none of its rows pass, and a bound made of such maxima stays
+                // below every passing item
+                const int32_t m = __builtin_amdgcn_sbfe(static_cast<int32_t>(mwh[i][j]),
+                                                        31 - (r / 4) * 8 - (r % 4), 1);
+                key &= static_cast<uint32_t>(m);
               }
-              best[j] = ok ? c : best[j];
+              const uint64_t c = composite(key, item);
+              best[j] = row < n && c > best[j] ? c : best[j];
             }
           }
       } else {
@@ -912,8 +923,13 @@ static int launch_blk_staged(const ScanArgs& a, dim3 grid, size_t lds, hipStream
                                                                                    stream);
     }
   } else {
-    if (clauses) return launch_blk_kernel<Op, RB, true, STAGES, WIDE, false, true>(a, grid, lds,
+    // (the seed takes its maxima over the staged mask too)
+    if (a.mask != nullptr) {
+      return clauses ? launch_blk_kernel<Op, RB, true, STAGES, WIDE, true, true>(a, grid, lds,
+                                                                                 stream)
+                     : launch_blk_kernel<Op, RB, true, STAGES, WIDE, true, false>(a, grid, lds,
                                                                                   stream);
+    }
   }
   return launch_blk_kernel<Op, RB, SEED, STAGES, WIDE, false, false>(a, grid, lds, stream);
 }
@@ -923,7 +939,7 @@ static int launch_blk_layout(const ScanArgs& a, dim3 grid, int capw, hipStream_t
   constexpr bool kBits = Op::kBits;
   if constexpr (SEED) {  // no lists in LDS: four stages always fit
     return launch_blk_staged<Op, RB, true, 4, WIDE>(
-        a, grid, blk_lds(RB, 4, 0, WIDE, kBits, false), stream);
+        a, grid, blk_lds(RB, 4, 0, WIDE, kBits, a.mask != nullptr), stream);
   } else {
     // the stage counts compiled: 4 or 3; 2 for bit codes and the wide layout below 512-byte rows
     // with the lists of a large k
@@ -1124,6 +1140,7 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
     RT_CHECK_HIP(hipGetLastError());
     a.mask_t = mask_t;
     a.mask_t_stride = stride;
+    a.mask_t_rows = W;
   }
 
   MergeArgs m{};

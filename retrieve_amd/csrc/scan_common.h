@@ -42,6 +42,7 @@ struct ScanArgs {
   int64_t mask_words;
   const uint64_t* mask_t;  // the mask transposed, [ceil(N/64), mask_t_stride] (blocked scan)
   int64_t mask_t_stride;
+  int64_t mask_t_rows;     // its word rows, ceil(N/64)
   uint64_t* lists;         // [slots, qpw, capw]
   int* counts;             // [slots, qpw]
   ClauseCheck clause;      // exact clauses tested per candidate (active null: none; the

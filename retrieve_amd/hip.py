@@ -557,14 +557,14 @@ def _(query, item_embs, k, item_clause_attrs, clause_is_reverse, query_values, m
 def hamming_scan_topk_clauses(
     query_bits: Tensor, item_bits: Tensor, k: int, item_clause_attrs: Tensor,
     clause_is_reverse: Tensor, query_values: Tensor, mask: Tensor | None = None,
-    fused: bool = False,
+    fused: bool = True,
 ) -> tuple[Tensor, Tensor]:
     """``hamming_scan_topk`` over the items that pass ``mask`` and the exact clauses: the same
-    results as ``hamming_scan_topk(q, items, k, clause_bits(attrs, rev, values, mask))``, which
-    is how it runs by default. ``fused``: where the matrix-core scan takes the batch and a mask
-    is given (e.g. a Bloom search's words), the clauses are tested inside the scan instead, for
-    the candidates that pass the mask (no ``[B, ceil(N/64)]`` clause mask in memory; slower at
-    B = 256: the bit-code kernel has no registers to spare for it). LiNR V3's filtered shortlist
+    results as ``hamming_scan_topk(q, items, k, clause_bits(attrs, rev, values, mask))``.
+    ``fused`` (default): where the matrix-core scan takes the batch and a mask is given (e.g. a
+    Bloom search's words), the clauses are tested inside the scan, for the candidates that pass
+    the mask (no ``[B, ceil(N/64)]`` clause mask in memory); elsewhere, or with ``fused=False``,
+    the clause mask is written first, as above. LiNR V3's filtered shortlist
     (``modules/linr.py:155-162``)."""
     q, mask = _hamming_prep(query_bits, item_bits, k, mask)
     rev, qs = _clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
@@ -597,7 +597,7 @@ def hamming_scan_topk_clauses(
 
 @hamming_scan_topk_clauses.register_fake
 def _(query_bits, item_bits, k, item_clause_attrs, clause_is_reverse, query_values, mask=None,
-      fused=False):
+      fused=True):
     b = query_bits.shape[0]
     return (query_bits.new_empty((b, k)), query_bits.new_empty((b, k), dtype=torch.int32))
 

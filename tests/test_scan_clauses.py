@@ -294,7 +294,7 @@ def test_hamming_parity(dev, b, n, k, ones):
     args = (_t(dev, attrs.astype(np.int16)), _t(dev, rev), _t(dev, sets), _t(dev, _pack(mask)))
     qt, it = _t(dev, q), _t(dev, items)
     ids, sc = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args, fused=True)
-    ids2, sc2 = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args)
+    ids2, sc2 = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args, fused=False)
     assert torch.equal(ids, ids2) and torch.equal(sc, sc2)
     if n > 1_000_000:
         want_ids, want_sc = _unfused(dev, torch.ops.retrieve.hamming_scan_topk, qt, it, k,
