@@ -51,10 +51,10 @@ MEASURED_TRAFFIC: dict = {
     ("filtered", 30_000_000, 512, 16, 100): 15_565_827_072,  # filtered_int8_30Mx512_b16.md
     ("int8", 30_000_000, 512, 16, 100): 15_366_246_011,  # int8_scan_30Mx512_b16.md
     ("int8", 30_000_000, 512, 256, 100): 15_365_323_008,  # int8_scan_30Mx512_b256.md
-    ("int8", 30_000_000, 512, 1024, 100): 51_364_477_133,  # int8_scan_30Mx512_b1024.md
+    ("int8", 30_000_000, 512, 1024, 100): 44_373_443_584,  # int8_scan_30Mx512_b1024.md
     ("dense", 10_000_000, 128, 64, 100): 2_566_548_500,  # dense_bf16_10Mx128_b64.md
-    ("dense", 10_000_000, 128, 1024, 100): 6_541_851_034,  # dense_bf16_10Mx128_b1024.md
-    ("dense", 10_000_000, 128, 4096, 100): 9_390_756_864,  # dense_bf16_10Mx128_b4096.md
+    ("dense", 10_000_000, 128, 1024, 100): 7_655_515_443,  # dense_bf16_10Mx128_b1024.md
+    ("dense", 10_000_000, 128, 4096, 100): 14_667_483_648,  # dense_bf16_10Mx128_b4096.md
     # filtered_dense_bf16_10Mx128_b256.md, binary_30Mx512bit_b256.md
     ("filtered-dense", 10_000_000, 128, 256, 100): 2_886_129_572,
     ("binary", 30_000_000, 512, 256, 100): 2_909_370_266,
