@@ -553,9 +553,9 @@ def main() -> int:
 
         scan_bytes = n * d // 8 + b * d // 8
         table = item_bits  # the streamed table (the read ceiling is measured over it)
-        # 512-bit codes from 33 queries on are scored on the fp4 matrix cores, one multiply-add
+        # 512-bit codes from 10 queries on are scored on the fp4 matrix cores, one multiply-add
         # per bit (bits as {0, 1.0} and {-2.0, +2.0} e2m1 values): 2 ops per bit, item and query
-        mfma_scan = d == 512 and b >= 33
+        mfma_scan = d == 512 and b >= 10
         scan_ops = 2 * b * n * d if mfma_scan else 2 * b * n * (d // 32)
         step_bytes = scan_bytes + flt.bytes(n, b, not args.unfused_bits) + b * k1 * d
         bound = "mfma" if mfma_scan else "hbm"
