@@ -193,6 +193,14 @@ class Filter:
         return torch.ops.st.bloom_index_search_batch_prepared(
             self.words, self.offs, self.blob, self.plan_count, self.max_stack, BLOOM_K, HASH_K)
 
+    def bloom_t(self) -> torch.Tensor:
+        """The same words stored transposed (``st.bloom_search_t``): the blocked scans of large
+        batches read them without a transpose per call."""
+        import retrieve_amd.st as st
+
+        return st.bloom_search_t(self.words, self.offs, self.blob, self.plan_count,
+                                 self.max_stack, BLOOM_K, HASH_K)
+
     def mask(self) -> torch.Tensor:
         """One batch's filter: Bloom pre-filter, then the exact post-check of its survivors."""
         return torch.ops.retrieve.clause_bits(self.attrs, self.rev, self.sets, self.bloom())
@@ -408,12 +416,15 @@ def main() -> int:
         items = dense_table(n, d, centres, 2025, dev).bfloat16()
         queries = dense_table(b, d, centres, 2026, dev).bfloat16()
         flt = Filter(n, b, args.selectivity, dev)
+        blocked = retrieve_amd.hip._use_blocked(b, 2 * d, k)
 
         def step():
             if args.unfused_filter:
                 return torch.ops.retrieve.dense_scan_topk(queries, items, k, flt.mask())
+            # (the blocked scan of a large batch reads the transposed words directly)
+            words = flt.bloom_t() if blocked else flt.bloom()
             return torch.ops.retrieve.dense_scan_topk_clauses(queries, items, k, flt.attrs,
-                                                             flt.rev, flt.sets, flt.bloom())
+                                                             flt.rev, flt.sets, words)
 
         scan_bytes = n * d * 2 + b * d * 2
         table = items  # the streamed table (the read ceiling is measured over it)
@@ -546,7 +557,8 @@ def main() -> int:
 
         def step():
             ids1, _ = torch.ops.retrieve.hamming_scan_topk_clauses(
-                q_bits, item_bits, k1, flt.attrs, flt.rev, flt.sets, flt.bloom(),
+                q_bits, item_bits, k1, flt.attrs, flt.rev, flt.sets,
+                flt.bloom_t() if b >= 10 and k1 <= 1024 else flt.bloom(),
                 fused=not args.unfused_bits)
             counts = (ids1 >= 0).sum(1)
             return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)

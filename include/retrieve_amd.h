@@ -171,13 +171,17 @@ int rt_scan_topk_clauses(const void* queries, int64_t B, const void* items, int6
  * query's bound and pass the mask enter the lists, the clauses are tested where a list is
  * compacted and in the final merge (an entry that fails them is dropped), and the sampled bound
  * takes each lane's best over the mask, kept only when that item passes the clauses. Same
- * results as rt_blocked_scan_topk over rt_clause_filter's mode-0 bits AND mask.
+ * results as rt_blocked_scan_topk over rt_clause_filter's mode-0 bits AND mask. mask_t_stride
+ * 0: `mask` is [B, mask_words] as above; > 0: it is already transposed, [mask_words, mask_t_stride]
+ * (rt_bloom_search_t's layout: mask_words >= ceil(N/64) rows, mask_t_stride >= B rounded up to
+ * 256), and the scan reads it as it is.
  * Replaces: as rt_scan_topk_clauses, at the batches of rt_blocked_scan_topk. */
 size_t rt_blocked_scan_topk_clauses_workspace(int64_t B, int64_t N, int64_t row_bytes, int64_t k,
                                               int64_t C, int64_t V);
 int rt_blocked_scan_topk_clauses(const void* queries, int64_t B, const void* items, int64_t N,
                                  int64_t D, int64_t k, int dtype, const uint64_t* mask,
-                                 int64_t mask_words, const void* item_attrs, int attr_bytes,
+                                 int64_t mask_words, int64_t mask_t_stride,
+                                 const void* item_attrs, int attr_bytes,
                                  int64_t C, int64_t A, const int8_t* clause_is_reverse,
                                  const int64_t* query_values, int64_t V, int64_t* out_ids,
                                  void* out_scores, void* workspace, size_t workspace_bytes,
@@ -185,7 +189,8 @@ int rt_blocked_scan_topk_clauses(const void* queries, int64_t B, const void* ite
 
 /* rt_hamming_scan_topk with the same fused clause filter, where the matrix-core scan takes the
  * batch (rt_hamming_scan_topk_clauses_fused(B, W, k) != 0: 512-bit codes, k <= 1024, the
- * batches of that kernel) and a mask is given; int32 scores, or float when score_f32.
+ * batches of that kernel) and a mask is given; int32 scores, or float when score_f32. The mask
+ * as for rt_blocked_scan_topk_clauses (mask_t_stride > 0: transposed).
  * Replaces: LiNR V3's filtered 1-bit shortlist (retrieve/src/retrieve/modules/linr.py:155-162,
  *   the clause mask of clause_compact feeding oporp_1bit_match_topk). */
 int rt_hamming_scan_topk_clauses_fused(int64_t B, int64_t W, int64_t k);
@@ -193,7 +198,8 @@ size_t rt_hamming_scan_topk_clauses_workspace(int64_t B, int64_t N, int64_t W, i
                                               int64_t C, int64_t V);
 int rt_hamming_scan_topk_clauses(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits,
                                  int64_t N, int64_t W, int64_t k, const uint64_t* mask,
-                                 int64_t mask_words, const void* item_attrs, int attr_bytes,
+                                 int64_t mask_words, int64_t mask_t_stride,
+                                 const void* item_attrs, int attr_bytes,
                                  int64_t C, int64_t A, const int8_t* clause_is_reverse,
                                  const int64_t* query_values, int64_t V, int64_t* out_ids,
                                  void* out_scores, int score_f32, void* workspace,
@@ -254,6 +260,19 @@ int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, int6
                     int64_t plan_count, int64_t max_stack, int64_t k, int64_t hash_k,
                     int64_t* out_mask, uint8_t* out_bool, void* workspace, size_t workspace_bytes,
                     rt_stream_t stream);
+
+/* rt_bloom_search with the words written transposed: out_mask_t [nb * 32, out_t_stride], column c
+ * of plan b at out_mask_t[c * out_t_stride + b] (out_t_stride >= plan_count; the entries past
+ * plan_count are left as they were). The blocked scans take this layout as their mask directly
+ * (rt_blocked_scan_topk_clauses, rt_hamming_scan_topk_clauses with mask_t_stride > 0) instead of
+ * transposing [B, ceil(N/64)] words themselves.
+ * Replaces: the same search as rt_bloom_search; the layout has no counterpart in the reference
+ *   (its consumers take the row-major words). */
+int rt_bloom_search_t(const uint64_t* words, const int64_t* bundle_b_offsets, int64_t n_bundles,
+                      const int64_t* plan_offsets, const int8_t* plan_data, int64_t data_bytes,
+                      int64_t plan_count, int64_t max_stack, int64_t k, int64_t hash_k,
+                      uint64_t* out_mask_t, int64_t out_t_stride, void* workspace,
+                      size_t workspace_bytes, rt_stream_t stream);
 
 /* The Bloom plans over the probed clusters' columns only: probed cluster i (row i / per_row of a
  * [rows, per_row] probe table) starts at doc position cluster_starts[i] and spans

@@ -61,15 +61,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rt_blocked_scan_topk_clauses_workspace": (_c_sz, [_c_i64] * 6),
     "rt_blocked_scan_topk_clauses": (
         _c_int,
-        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_int, _c_i64,
-         _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_i64, _c_p, _c_int,
+         _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],
     ),
     "rt_hamming_scan_topk_clauses_fused": (_c_int, [_c_i64, _c_i64, _c_i64]),
     "rt_hamming_scan_topk_clauses_workspace": (_c_sz, [_c_i64] * 6),
     "rt_hamming_scan_topk_clauses": (
         _c_int,
-        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_int, _c_i64, _c_i64,
-         _c_p, _c_p, _c_i64, _c_p, _c_p, _c_int, _c_p, _c_sz, _c_p],
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_int, _c_i64,
+         _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_int, _c_p, _c_sz, _c_p],
     ),
     "rt_read_ceiling": (_c_int, [_c_p, _c_i64, _c_int, _c_p, _c_p]),
     "rt_bloom_bundle_terms": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
@@ -81,6 +81,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
          _c_sz, _c_p],
+    ),
+    "rt_bloom_search_t": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
+         _c_p, _c_sz, _c_p],
     ),
     "rt_mask_compact_workspace": (_c_sz, [_c_i64, _c_i64]),
     "rt_mask_compact": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p]),

@@ -182,6 +182,8 @@ struct BloomSearchArgs {
   const uint32_t* prog;   // [plan_count, kProgMaxOps, 2] program words
   int64_t* out_mask;      // [plan_count, nb * 32] or null
   uint8_t* out_bool;      // [plan_count, nb * 32 * 64] or null
+  uint64_t* out_mask_t;   // [nb * 32, out_t_stride]: the words transposed, or null
+  int64_t out_t_stride;
 };
 
 // The first k distinct hash % w among a term's stored hashes (fewer if they do not hold k).
@@ -218,6 +220,12 @@ __device__ inline void write_column(const BloomSearchArgs& a, int64_t b, int64_t
   if (a.out_mask != nullptr) {
     gi64* om = (gi64*)(a.out_mask);
     om[b * ncol + col] = static_cast<int64_t>(res);
+  }
+  if (a.out_mask_t != nullptr) {
+    // (a workgroup takes a run of consecutive plans over its columns: their words of a column
+    // share lines, which fill in L2 before they are written back)
+    gi64* ot = (gi64*)(a.out_mask_t);
+    ot[col * a.out_t_stride + b] = static_cast<int64_t>(res);
   }
   if (a.out_bool != nullptr) {
     // 64 bytes per column, doc 64 col + q at byte q (bit 63 - q of the word)
@@ -1016,12 +1024,13 @@ extern "C" size_t rt_bloom_search_workspace(int64_t data_bytes, int64_t plan_cou
          align_up(static_cast<size_t>(plans) * kProgMaxOps * 2 * sizeof(uint32_t), 256);
 }
 
-extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets,
-                               int64_t n_bundles, const int64_t* plan_offsets,
-                               const int8_t* plan_data, int64_t data_bytes, int64_t plan_count,
-                               int64_t max_stack, int64_t k, int64_t hash_k, int64_t* out_mask,
-                               uint8_t* out_bool, void* workspace, size_t workspace_bytes,
-                               hipStream_t stream) {
+// The search behind rt_bloom_search and rt_bloom_search_t: any of the three outputs.
+static int bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, int64_t n_bundles,
+                        const int64_t* plan_offsets, const int8_t* plan_data, int64_t data_bytes,
+                        int64_t plan_count, int64_t max_stack, int64_t k, int64_t hash_k,
+                        int64_t* out_mask, uint8_t* out_bool, uint64_t* out_mask_t,
+                        int64_t out_t_stride, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
   RT_CHECK_ARG(n_bundles >= 0 && plan_count >= 0 && data_bytes >= 0, "sizes must be >= 0");
   RT_CHECK_ARG(k >= 1 && k <= kBloomMaxK, "k must be in [1, %d], got %lld", kBloomMaxK,
                static_cast<long long>(k));
@@ -1030,7 +1039,9 @@ extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_of
   RT_CHECK_ARG(max_stack >= 1 && max_stack <= kBloomMaxStack,
                "max_stack_size must be in [1, %d], got %lld", kBloomMaxStack,
                static_cast<long long>(max_stack));
-  RT_CHECK_ARG(out_mask != nullptr || out_bool != nullptr, "no output");
+  RT_CHECK_ARG(out_mask != nullptr || out_bool != nullptr || out_mask_t != nullptr, "no output");
+  RT_CHECK_ARG(out_mask_t == nullptr || out_t_stride >= plan_count,
+               "the transposed output's stride must be >= plan_count");
   RT_CHECK_ARG(reinterpret_cast<uintptr_t>(plan_data) % 8 == 0, "plan data must be 8-aligned");
   RT_CHECK_ARG(plan_count <= (int64_t{1} << 31) - 1, "too many plans");
   if (n_bundles == 0 || plan_count == 0) return kOk;
@@ -1058,6 +1069,8 @@ extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_of
   a.prog = prog;
   a.out_mask = out_mask;
   a.out_bool = out_bool;
+  a.out_mask_t = out_mask_t;
+  a.out_t_stride = out_t_stride;
   bloom_prep_kernel<<<static_cast<unsigned>(plan_count), kPrepThreads, 0, stream>>>(a, hdr,
                                                                                      prog);
   RT_CHECK_HIP(hipGetLastError());
@@ -1121,6 +1134,29 @@ extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_of
                         kBloomThreads, lds, stream>>>(a);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
+}
+
+extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets,
+                               int64_t n_bundles, const int64_t* plan_offsets,
+                               const int8_t* plan_data, int64_t data_bytes, int64_t plan_count,
+                               int64_t max_stack, int64_t k, int64_t hash_k, int64_t* out_mask,
+                               uint8_t* out_bool, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+  return bloom_search(words, bundle_b_offsets, n_bundles, plan_offsets, plan_data, data_bytes,
+                      plan_count, max_stack, k, hash_k, out_mask, out_bool, nullptr, 0, workspace,
+                      workspace_bytes, stream);
+}
+
+extern "C" int rt_bloom_search_t(const uint64_t* words, const int64_t* bundle_b_offsets,
+                                 int64_t n_bundles, const int64_t* plan_offsets,
+                                 const int8_t* plan_data, int64_t data_bytes, int64_t plan_count,
+                                 int64_t max_stack, int64_t k, int64_t hash_k, uint64_t* out_mask_t,
+                                 int64_t out_t_stride, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+  RT_CHECK_ARG(out_mask_t != nullptr, "out_mask_t is null");
+  return bloom_search(words, bundle_b_offsets, n_bundles, plan_offsets, plan_data, data_bytes,
+                      plan_count, max_stack, k, hash_k, nullptr, nullptr, out_mask_t,
+                      out_t_stride, workspace, workspace_bytes, stream);
 }
 
 extern "C" int rt_bloom_search_columns(const uint64_t* words, const int64_t* bundle_b_offsets,

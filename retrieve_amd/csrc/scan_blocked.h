@@ -1075,7 +1075,7 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
                        int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                        int64_t* out_ids, void* out_scores, void* workspace,
                        size_t workspace_bytes, hipStream_t stream, int score_kind = Op::kind,
-                       const ClauseCheck& clause = ClauseCheck{}) {
+                       const ClauseCheck& clause = ClauseCheck{}, int64_t mask_t_stride = 0) {
   RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
   RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
                static_cast<long long>(kMaxK), static_cast<long long>(k));
@@ -1129,7 +1129,17 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   a.lists = lists;
   a.counts = counts;
   a.clause = clause;
-  if (mask != nullptr) {
+  if (mask != nullptr && mask_t_stride > 0) {
+    // the mask given transposed: [mask_words >= ceil(N/64) rows, mask_t_stride >= the padded
+    // batch] (rt_bloom_search_t's layout)
+    RT_CHECK_ARG(mask_t_stride >= cdiv(B, kBlkQpg) * kBlkQpg,
+                 "a transposed mask needs a stride of at least %lld, got %lld",
+                 static_cast<long long>(cdiv(B, kBlkQpg) * kBlkQpg),
+                 static_cast<long long>(mask_t_stride));
+    a.mask_t = mask;
+    a.mask_t_stride = mask_t_stride;
+    a.mask_t_rows = mask_words;
+  } else if (mask != nullptr) {
     const int64_t W = cdiv(N, 64);
     const int64_t stride = cdiv(B, kBlkQpg) * kBlkQpg;
     uint64_t* mask_t = reinterpret_cast<uint64_t*>(ws + off_mask_t);
@@ -1231,19 +1241,23 @@ namespace rt {
 int blocked_scan_i8(const void* queries, int64_t B, const void* items, int64_t N,
                     int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                     int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
-                    hipStream_t stream, const ClauseCheck& clause = ClauseCheck{});
+                    hipStream_t stream, const ClauseCheck& clause = ClauseCheck{},
+                    int64_t mask_t_stride = 0);
 int blocked_scan_bf16(const void* queries, int64_t B, const void* items, int64_t N,
                       int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                       int64_t* out_ids, void* out_scores, void* workspace,
                       size_t workspace_bytes, hipStream_t stream,
-                      const ClauseCheck& clause = ClauseCheck{});
+                      const ClauseCheck& clause = ClauseCheck{},
+                    int64_t mask_t_stride = 0);
 int blocked_scan_f16(const void* queries, int64_t B, const void* items, int64_t N,
                      int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                      int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
-                     hipStream_t stream, const ClauseCheck& clause = ClauseCheck{});
+                     hipStream_t stream, const ClauseCheck& clause = ClauseCheck{},
+                    int64_t mask_t_stride = 0);
 int blocked_scan_f32(const void* queries, int64_t B, const void* items, int64_t N,
                      int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                      int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
-                     hipStream_t stream, const ClauseCheck& clause = ClauseCheck{});
+                     hipStream_t stream, const ClauseCheck& clause = ClauseCheck{},
+                    int64_t mask_t_stride = 0);
 
 }  // namespace rt

@@ -48,7 +48,8 @@ extern "C" size_t rt_blocked_scan_topk_clauses_workspace(int64_t B, int64_t N, i
 extern "C" int rt_blocked_scan_topk_clauses(const void* queries, int64_t B, const void* items,
                                             int64_t N, int64_t D, int64_t k, int dtype,
                                             const uint64_t* mask, int64_t mask_words,
-                                            const void* item_attrs, int attr_bytes, int64_t C,
+                                            int64_t mask_t_stride, const void* item_attrs,
+                                            int attr_bytes, int64_t C,
                                             int64_t A, const int8_t* clause_is_reverse,
                                             const int64_t* query_values, int64_t V,
                                             int64_t* out_ids, void* out_scores, void* workspace,
@@ -87,15 +88,16 @@ extern "C" int rt_blocked_scan_topk_clauses(const void* queries, int64_t B, cons
   switch (dtype) {
     case 0:
       return blocked_scan_i8(queries, B, items, N, D, k, mask, mask_words, out_ids, out_scores,
-                             workspace, scan_bytes, stream, f);
+                             workspace, scan_bytes, stream, f,
+                             mask_t_stride);
     case 1:
       return blocked_scan_bf16(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
-                               out_scores, workspace, scan_bytes, stream, f);
+                               out_scores, workspace, scan_bytes, stream, f, mask_t_stride);
     case 2:
       return blocked_scan_f16(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
-                              out_scores, workspace, scan_bytes, stream, f);
+                              out_scores, workspace, scan_bytes, stream, f, mask_t_stride);
     default:
       return blocked_scan_f32(queries, B, items, N, 4 * D, k, mask, mask_words, out_ids,
-                              out_scores, workspace, scan_bytes, stream, f);
+                              out_scores, workspace, scan_bytes, stream, f, mask_t_stride);
   }
 }

@@ -6,9 +6,10 @@ namespace rt {
 int blocked_scan_f32(const void* queries, int64_t B, const void* items, int64_t N,
                      int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                      int64_t* out_ids, void* out_scores, void* workspace, size_t workspace_bytes,
-                     hipStream_t stream, const ClauseCheck& clause) {
+                     hipStream_t stream, const ClauseCheck& clause, int64_t mask_t_stride) {
   return run_blocked<F32x32>(queries, B, items, N, row_bytes, k, mask, mask_words, out_ids,
-                             out_scores, workspace, workspace_bytes, stream, F32x32::kind, clause);
+                             out_scores, workspace, workspace_bytes, stream, F32x32::kind, clause,
+                             mask_t_stride);
 }
 
 }  // namespace rt

@@ -140,7 +140,8 @@ int blocked_hamming(const uint64_t* query_bits, int64_t B, const uint64_t* item_
                     int64_t W, int64_t k, const uint64_t* mask, int64_t mask_words,
                     int64_t* out_ids, void* out_scores, int score_kind, void* workspace,
                     size_t workspace_bytes, hipStream_t stream,
-                    const ClauseCheck& clause = ClauseCheck{});
+                    const ClauseCheck& clause = ClauseCheck{},
+                    int64_t mask_t_stride = 0);
 
 // Sizes the passes for B queries over N rows and top-k. A workgroup row (grid.y) covers qpg
 // queries and each workgroup keeps lists_per_wg candidate lists (of main_capw entries in the

@@ -368,7 +368,8 @@ extern "C" size_t rt_hamming_scan_topk_clauses_workspace(int64_t B, int64_t N, i
 extern "C" int rt_hamming_scan_topk_clauses(const uint64_t* query_bits, int64_t B,
                                             const uint64_t* item_bits, int64_t N, int64_t W,
                                             int64_t k, const uint64_t* mask, int64_t mask_words,
-                                            const void* item_attrs, int attr_bytes, int64_t C,
+                                            int64_t mask_t_stride, const void* item_attrs,
+                                            int attr_bytes, int64_t C,
                                             int64_t A, const int8_t* clause_is_reverse,
                                             const int64_t* query_values, int64_t V,
                                             int64_t* out_ids, void* out_scores, int score_f32,
@@ -377,7 +378,8 @@ extern "C" int rt_hamming_scan_topk_clauses(const uint64_t* query_bits, int64_t 
   RT_CHECK_ARG(B >= 0 && B <= (int64_t{1} << 21) && N >= 0, "B in [0, 2^21] and N >= 0");
   RT_CHECK_ARG(N < 0xffffffffll, "N must be < 2**32 - 1");
   RT_CHECK_ARG(mask != nullptr && mask_words >= cdiv(N, 64),
-               "the fused clause filter needs a mask of ceil(N/64) words a row");
+               "the fused clause filter needs a mask of ceil(N/64) words a row (rows, when "
+               "transposed)");
   RT_CHECK_ARG(k >= 1 && k <= kMaxK && ham_mfma(B, W, k, true),
                "the fused clause filter runs where the matrix-core scan takes the batch "
                "(rt_hamming_scan_topk_clauses_fused)");
@@ -413,5 +415,5 @@ extern "C" int rt_hamming_scan_topk_clauses(const uint64_t* query_bits, int64_t 
     f.A = static_cast<int>(A);
   }
   return blocked_hamming(query_bits, B, item_bits, N, W, k, mask, mask_words, out_ids,
-                         out_scores, kind, workspace, scan_bytes, stream, f);
+                         out_scores, kind, workspace, scan_bytes, stream, f, mask_t_stride);
 }

@@ -211,8 +211,10 @@ def _(query, item_embs, k, mask=None):
 HAMMING_MAX_K = 8192
 
 
-def _hamming_prep(query_bits: Tensor, item_bits: Tensor, k: int, mask: Tensor | None):
-    """``_oporp_prep``'s checks (``ops/triton/oporp_1bit_match_topk.py:148-165``)."""
+def _hamming_prep(query_bits: Tensor, item_bits: Tensor, k: int, mask: Tensor | None,
+                  keep_transposed: bool = False):
+    """``_oporp_prep``'s checks (``ops/triton/oporp_1bit_match_topk.py:148-165``); with
+    ``keep_transposed`` a mask stored transposed (``_transposed_stride``) stays as it is."""
     if query_bits.dim() != 2 or item_bits.dim() != 2:
         raise ValueError("query_bits must be [B, W] and item_bits [N, W]")
     if query_bits.dtype != torch.int64 or item_bits.dtype != torch.int64:
@@ -230,7 +232,8 @@ def _hamming_prep(query_bits: Tensor, item_bits: Tensor, k: int, mask: Tensor | 
             raise TypeError("mask must be int64 words")
         if mask.dim() != 2 or mask.shape[0] != b or mask.shape[1] < (n + 63) // 64:
             raise ValueError(f"mask must be [B, ceil(N/64)] = [{b}, {(n + 63) // 64}]")
-        mask = mask.contiguous()
+        if not (keep_transposed and _transposed_stride(mask, b)):
+            mask = mask.contiguous()
     return query_bits.contiguous(), mask
 
 
@@ -434,6 +437,17 @@ def _(item_clause_attrs, clause_is_reverse, query_values, and_mask=None):
 # --- full scans with the exact clause filter tested per candidate ----------------------------
 
 
+def _transposed_stride(mask: Tensor | None, b: int) -> int:
+    """The row stride S of a ``[B, W]`` mask whose words are stored transposed, ``[W, S]`` with
+    S >= B rounded up to 256 (``st.bloom_search_t``'s layout, viewed as ``[B, W]``), else 0. The
+    blocked scans read such a mask as it is; every other path takes ``mask.contiguous()``."""
+    if mask is None or mask.dim() != 2 or b == 0:
+        return 0
+    s0, s1 = mask.stride()
+    pad = -(-b // 256) * 256
+    return int(s1) if s0 == 1 and s1 >= pad and s1 % 256 == 0 else 0
+
+
 def _scan_clauses(q: Tensor, items: Tensor, k: int, dtype: int, item_clause_attrs: Tensor,
                   clause_is_reverse: Tensor, query_values: Tensor, mask: Tensor | None,
                   scores: Tensor, ids: Tensor) -> bool:
@@ -457,20 +471,24 @@ def _scan_clauses(q: Tensor, items: Tensor, k: int, dtype: int, item_clause_attr
     _, c, a = item_clause_attrs.shape
     v = qs.shape[2]
     lib = nat.lib()
-    if blocked:
-        ws = nat.workspace(lib.rt_blocked_scan_topk_clauses_workspace(
-            b, n, d * q.element_size(), k, c, v), dev)
-        entry = lib.rt_blocked_scan_topk_clauses
-    else:
-        ws = nat.workspace(lib.rt_scan_topk_clauses_workspace(b, n, d, k, c, v), dev)
-        entry = lib.rt_scan_topk_clauses
+    ts = _transposed_stride(mask, b) if blocked else 0
+    if mask is not None and not ts:
+        mask = mask.contiguous()
+    words = 0 if mask is None else mask.shape[1]
+    tail = (nat.ptr(item_clause_attrs), item_clause_attrs.element_size(), c, a, nat.ptr(rev),
+            nat.ptr(qs), v, nat.ptr(ids), nat.ptr(scores))
     with torch.cuda.device(dev):
-        st = entry(
-            nat.ptr(q), b, nat.ptr(items), n, d, k, dtype, nat.ptr(mask),
-            0 if mask is None else mask.shape[1], nat.ptr(item_clause_attrs),
-            item_clause_attrs.element_size(), c, a, nat.ptr(rev), nat.ptr(qs), v, nat.ptr(ids),
-            nat.ptr(scores), nat.ptr(ws), ws.numel(), nat.stream(dev),
-        )
+        if blocked:
+            ws = nat.workspace(lib.rt_blocked_scan_topk_clauses_workspace(
+                b, n, d * q.element_size(), k, c, v), dev)
+            st = lib.rt_blocked_scan_topk_clauses(
+                nat.ptr(q), b, nat.ptr(items), n, d, k, dtype, nat.ptr(mask), words, ts, *tail,
+                nat.ptr(ws), ws.numel(), nat.stream(dev))
+        else:
+            ws = nat.workspace(lib.rt_scan_topk_clauses_workspace(b, n, d, k, c, v), dev)
+            st = lib.rt_scan_topk_clauses(
+                nat.ptr(q), b, nat.ptr(items), n, d, k, dtype, nat.ptr(mask), words, *tail,
+                nat.ptr(ws), ws.numel(), nat.stream(dev))
     nat.check(st)
     return True
 
@@ -534,14 +552,15 @@ def dense_scan_topk_clauses(
             raise TypeError("mask must be int64 words")
         if mask.dim() != 2 or mask.shape[0] != b or mask.shape[1] < (n + 63) // 64:
             raise ValueError(f"mask must be [B, ceil(N/64)] = [{b}, {(n + 63) // 64}]")
-        mask = mask.contiguous()
     q = query.contiguous()
     ids = torch.empty((b, k), dtype=torch.int64, device=q.device)
     scores = torch.empty((b, k), dtype=torch.float32, device=q.device)
+    # (a mask stored transposed reaches the blocked scan as it is)
     if _scan_clauses(q, item_embs, k, dtype, item_clause_attrs, clause_is_reverse, query_values,
                      mask, scores, ids):
         return ids, scores
-    bits = clause_bits(item_clause_attrs, clause_is_reverse, query_values, mask)
+    bits = clause_bits(item_clause_attrs, clause_is_reverse, query_values,
+                       None if mask is None else mask.contiguous())
     return dense_scan_topk(q, item_embs, k, bits)
 
 
@@ -566,7 +585,7 @@ def hamming_scan_topk_clauses(
     the mask (no ``[B, ceil(N/64)]`` clause mask in memory); elsewhere, or with ``fused=False``,
     the clause mask is written first, as above. LiNR V3's filtered shortlist
     (``modules/linr.py:155-162``)."""
-    q, mask = _hamming_prep(query_bits, item_bits, k, mask)
+    q, mask = _hamming_prep(query_bits, item_bits, k, mask, keep_transposed=True)
     rev, qs = _clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
     b, w = q.shape
     n = item_bits.shape[0]
@@ -576,8 +595,10 @@ def hamming_scan_topk_clauses(
         raise ValueError(f"query_values has {qs.shape[0]} rows, the queries {b}")
     lib = nat.lib()
     if not fused or mask is None or not lib.rt_hamming_scan_topk_clauses_fused(b, w, k):
-        bits = clause_bits(item_clause_attrs, clause_is_reverse, query_values, mask)
+        bits = clause_bits(item_clause_attrs, clause_is_reverse, query_values,
+                           None if mask is None else mask.contiguous())
         return hamming_scan_topk(q, item_bits, k, bits)
+    ts = _transposed_stride(mask, b)  # (the blocked scan reads a transposed mask as it is)
     dev = nat.require_device(q, item_bits, item_clause_attrs, qs)
     _, c, a = item_clause_attrs.shape
     v = qs.shape[2]
@@ -586,7 +607,7 @@ def hamming_scan_topk_clauses(
     ws = nat.workspace(lib.rt_hamming_scan_topk_clauses_workspace(b, n, w, k, c, v), dev)
     with torch.cuda.device(dev):
         st = lib.rt_hamming_scan_topk_clauses(
-            nat.ptr(q), b, nat.ptr(item_bits), n, w, k, nat.ptr(mask), mask.shape[1],
+            nat.ptr(q), b, nat.ptr(item_bits), n, w, k, nat.ptr(mask), mask.shape[1], ts,
             nat.ptr(item_clause_attrs), item_clause_attrs.element_size(), c, a, nat.ptr(rev),
             nat.ptr(qs), v, nat.ptr(ids), nat.ptr(scores), 0, nat.ptr(ws), ws.numel(),
             nat.stream(dev),

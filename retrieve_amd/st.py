@@ -236,6 +236,44 @@ def _search_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max
                          int(hash_k), bool(return_bool_mask))
 
 
+def bloom_search_t(bloom_index: Tensor, bloom_bundle_b_offsets: Tensor, plans: Tensor,
+                   plan_count: int, max_stack_size: int, k: int, hash_k: int) -> Tensor:
+    """``bloom_index_search_batch_prepared``'s words (``return_bool_mask=False``) stored
+    transposed: a ``[plan_count, nb * 32]`` view with strides ``(1, S)`` over ``[nb * 32, S]``
+    words, S = plan_count rounded up to 256 (``rt_bloom_search_t``). The values are the same;
+    the blocked scans (``dense_scan_topk_clauses``, ``hamming_scan_topk_clauses`` at their
+    blocked batches) read this layout directly instead of transposing the mask per call, and
+    any other consumer sees an ordinary strided tensor. No counterpart in the reference."""
+    if plans.dtype != torch.int64 or plans.dim() != 1 or plans.numel() < 8 * plan_count:
+        raise ValueError("plans must be int64 [8 * plan_count + data words]")
+    if max_stack_size > MAX_STACK:
+        raise ValueError(f"max_stack_size must be <= {MAX_STACK}")
+    bloom_index = bloom_index.contiguous()
+    offsets = bloom_bundle_b_offsets.contiguous()
+    plans = plans.contiguous()
+    dev = nat.require_device(bloom_index, offsets, plans)
+    if bloom_index.dtype != torch.int64 or offsets.dtype != torch.int64:
+        raise TypeError("bloom_index and bloom_bundle_b_offsets must be int64")
+    data = plans[8 * plan_count :]
+    nb = offsets.numel() - 1
+    cols = max(nb, 0) * WORDS_PER_BUNDLE
+    stride = max(-(-plan_count // 256) * 256, 256)
+    out = torch.empty((cols, stride), dtype=torch.int64, device=dev)
+    view = out.t()[:plan_count]
+    if plan_count == 0 or nb <= 0:
+        return view
+    lib = nat.lib()
+    ws = nat.workspace(lib.rt_bloom_search_workspace(data.numel() * 8, plan_count), dev)
+    with torch.cuda.device(dev):
+        st = lib.rt_bloom_search_t(
+            nat.ptr(bloom_index), nat.ptr(offsets), nb, nat.ptr(plans), nat.ptr(data),
+            data.numel() * 8, plan_count, max(1, min(int(max_stack_size), MAX_STACK)), k, hash_k,
+            nat.ptr(out), stride, nat.ptr(ws), ws.numel(), nat.stream(dev),
+        )
+    nat.check(st)
+    return view
+
+
 def _search_batch(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data,
                   bloom_query_plans_offsets, k, hash_k, return_bool_mask=True):
     """Plans as the parser returns them (host tensors are copied to the index's device)."""

@@ -193,6 +193,23 @@ def test_search_paths(dev, bits, k, hash_k, n):
         assert np.array_equal(row, want), e
 
 
+@pytest.mark.parametrize("plans", [16, 300])
+def test_search_transposed_words(dev, plans):
+    """``st.bloom_search_t``: the same words as the prepared search (stack-evaluated plans
+    included), stored transposed with the plan count rounded up to 256 as the row stride."""
+    g = rng(93 + plans)
+    n = 5000
+    attrs = _attrs(g, n, 4, 1, 6, 0.2)
+    words, offs = _build(dev, attrs, 3, bits=64)
+    exprs = [_random_expr(g) for _ in range(plans - 3)]
+    exprs += [_nested(9), "NOT (0:1 OR 1:1)", "0:0 OR 0:1 OR 0:2"]
+    blob, count, max_stack = st.prepare_plans(exprs, 7, dev)
+    want = torch.ops.st.bloom_index_search_batch_prepared(words, offs, blob, count, max_stack, 3, 7)
+    got = st.bloom_search_t(words, offs, blob, count, max_stack, 3, 7)
+    assert got.shape == want.shape and got.stride() == (1, -(-plans // 256) * 256)
+    assert torch.equal(got, want)
+
+
 def test_long_plans(dev):
     """Value sets of hundreds of terms (plans of 500 - 2000 ops, the program's capacity) and one
     past it (the stack evaluation), against the oracle."""

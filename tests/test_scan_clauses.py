@@ -201,6 +201,16 @@ def test_opcheck(dev):
         torch.library.opcheck(op, args)
 
 
+def _as_transposed(mask: torch.Tensor) -> torch.Tensor:
+    """``mask`` [B, W] with its words stored transposed ([W, S], S = B rounded up to 256), as
+    ``st.bloom_search_t`` returns them: the blocked scans read this layout directly."""
+    b, w = mask.shape
+    s = -(-b // 256) * 256
+    out = torch.full((w, s), -1, dtype=mask.dtype, device=mask.device)  # (padding: never read)
+    out[:, :b] = mask.t()
+    return out.t()[:b]
+
+
 def _unfused(dev, op, q, items, k, attrs, rev, sets, mask):
     bits = torch.ops.retrieve.clause_bits(attrs, rev, sets, mask)
     return op(q, items, k, bits)
@@ -275,6 +285,10 @@ def test_blocked_dense_equals_unfused(dev, dtype, b, n, d):
     want_ids, want_sc = _unfused(dev, torch.ops.retrieve.dense_scan_topk, q, items, 100, attrs,
                                  rev, sets, mask)
     assert torch.equal(ids, want_ids) and torch.equal(sc, want_sc)
+    # the same mask stored transposed
+    ids_t, sc_t = torch.ops.retrieve.dense_scan_topk_clauses(q, items, 100, attrs, rev, sets,
+                                                             _as_transposed(mask))
+    assert torch.equal(ids_t, ids) and torch.equal(sc_t, sc)
 
 
 @pytest.mark.parametrize("b,n,k,ones", [(256, 200_000, 1000, False), (64, 2_200_000, 100, False),
@@ -296,6 +310,11 @@ def test_hamming_parity(dev, b, n, k, ones):
     ids, sc = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args, fused=True)
     ids2, sc2 = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args, fused=False)
     assert torch.equal(ids, ids2) and torch.equal(sc, sc2)
+    # the mask stored transposed (read directly by the blocked scan; copied elsewhere)
+    args_t = args[:3] + (_as_transposed(args[3]),)
+    for fused in (True, False):
+        ids3, sc3 = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args_t, fused=fused)
+        assert torch.equal(ids, ids3) and torch.equal(sc, sc3)
     if n > 1_000_000:
         want_ids, want_sc = _unfused(dev, torch.ops.retrieve.hamming_scan_topk, qt, it, k,
                                      *args)
