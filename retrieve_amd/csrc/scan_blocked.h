@@ -697,25 +697,37 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
 #pragma unroll
             for (int j = 0; j < NC; ++j) mwh[i][j] = mw[i][j] << (4 * half);
         }
+        // A lane's best over the tile is its largest key at the lowest of its rows holding it
+        // (rows rise with the register index, and later tiles hold later items, which lose
+        // ties), so the keys' maximum decides whether the tile can raise the lane's best and
+        // the composite is built only where it does.
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int64_t row = rt + 32 * (wr * RTW + i) + (r / 4) * 8 + (r % 4);
-            const uint32_t item = static_cast<uint32_t>(sample_item(row, a.row_stride));
+          for (int j = 0; j < NC; ++j) {
+            uint32_t keys[16];
+            uint32_t mx = 0u;
 #pragma unroll
-            for (int j = 0; j < NC; ++j) {
-              uint32_t key = Op::key(acc[i][j][r]);
+            for (int r = 0; r < 16; ++r) {
+              keys[r] = Op::key(acc[i][j][r]);
               if constexpr (masked) {
-                // a row that fails the mask keeps key 0: below every score, so it is a lane's
-                // best only where none of its rows pass, and a bound made of such maxima stays
-                // below every passing item
+                // a row that fails the mask keeps key 0, below every score
                 const int32_t m = __builtin_amdgcn_sbfe(static_cast<int32_t>(mwh[i][j]),
                                                         31 - (r / 4) * 8 - (r % 4), 1);
-                key &= static_cast<uint32_t>(m);
+                keys[r] &= static_cast<uint32_t>(m);
               }
-              const uint64_t c = composite(key, item);
-              best[j] = row < n && c > best[j] ? c : best[j];
+              mx = keys[r] > mx ? keys[r] : mx;
+            }
+            const bool up = mx > static_cast<uint32_t>(best[j] >> 32);
+            if (__any(up)) {
+              int rr = 15;
+#pragma unroll
+              for (int r = 15; r >= 0; --r) rr = keys[r] == mx ? r : rr;
+              const int64_t row = rt + 32 * (wr * RTW + i) + (rr / 4) * 8 + (rr % 4);
+              // (the seed's sample is whole tiles: row < n holds; checked all the same)
+              if (up && row < n) {
+                best[j] = composite(mx, static_cast<uint32_t>(sample_item(row, a.row_stride)));
+              }
             }
           }
       } else {
