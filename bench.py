@@ -558,16 +558,16 @@ def main() -> int:
         def step():
             ids1, _ = torch.ops.retrieve.hamming_scan_topk_clauses(
                 q_bits, item_bits, k1, flt.attrs, flt.rev, flt.sets,
-                flt.bloom_t() if b >= 10 and k1 <= 1024 else flt.bloom(),
+                flt.bloom_t() if b >= 8 and k1 <= 1024 else flt.bloom(),
                 fused=not args.unfused_bits)
             counts = (ids1 >= 0).sum(1)
             return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
 
         scan_bytes = n * d // 8 + b * d // 8
         table = item_bits  # the streamed table (the read ceiling is measured over it)
-        # 512-bit codes from 10 queries on are scored on the fp4 matrix cores, one multiply-add
+        # 512-bit codes from 8 queries on are scored on the fp4 matrix cores, one multiply-add
         # per bit (bits as {0, 1.0} and {-2.0, +2.0} e2m1 values): 2 ops per bit, item and query
-        mfma_scan = d == 512 and b >= 10
+        mfma_scan = d == 512 and b >= 8
         scan_ops = 2 * b * n * d if mfma_scan else 2 * b * n * (d // 32)
         step_bytes = scan_bytes + flt.bytes(n, b, not args.unfused_bits) + b * k1 * d
         bound = "mfma" if mfma_scan else "hbm"

@@ -91,7 +91,7 @@ int rt_blocked_scan_topk(const void* queries, int64_t B, const void* items, int6
  * top-k by (score desc, index asc) -> ids int64 [B, k], scores [B, k] (int32, or float when
  * score_f32 != 0). 1 <= W <= 16; 1 <= k <= 8192 (above 1024 the k-th score is found by
  * counting the 64 W + 1 scores and the ties at it by id bins: LiNR V3's candidate pools).
- * `mask` as for rt_int8_scan_topk. 512-bit codes (W = 8) from 10 queries on (k <= 1024) run on
+ * `mask` as for rt_int8_scan_topk. 512-bit codes (W = 8) from 8 queries on (k <= 1024) run on
  * the fp4 matrix cores (bits as e2m1 nibbles); `masked` of the workspace function as for
  * rt_blocked_scan_topk_workspace.
  * Replaces: the Triton full-scan kernel + torch.topk of

@@ -49,40 +49,44 @@ constexpr int kBlkRows = 64;      // items per staged tile (at most)
 constexpr int kBlkQpw = 64;       // queries per wave (two 32-query column tiles)
 constexpr int kBlkCols = 8;       // 32-query column tiles per workgroup
 constexpr int kBlkQpg = kBlkCols * 32;  // queries per workgroup (query group)
-// Up to this many queries, rows narrower than 512 bytes take the wide layout.
+// Up to this many queries, rows narrower than 512 bytes take the wide layout; bit codes up to
+// kBlkWideMaxBatchBits (their wide layout covers two column tiles).
 constexpr int64_t kBlkWideMaxBatch = 128;
+constexpr int64_t kBlkWideMaxBatchBits = 64;
 
 // Rows per staged tile: 32 for narrow 512-byte rows, so four stages fit in half the LDS; 128
 // for the wide layout below 512-byte rows (its row quarters are 32 rows); 64 otherwise; for
-// 64-byte bit-code rows 128 wide (one 16-byte load per thread) and 64 narrow (two row tiles per
-// wave: half the tile barriers and waits of 32-row tiles per MFMA, and whole 64-bit mask words
-// per query).
+// 64-byte bit-code rows 256 wide (eight 32-row parts) and 64 narrow (two row tiles per wave: half
+// the tile barriers and waits of 32-row tiles per MFMA, and whole 64-bit mask words per query).
 constexpr int blk_rows(int64_t row_bytes, bool wide, bool bits) {
-  return bits ? (wide ? 128 : 64)
+  return bits ? (wide ? 256 : 64)
               : (wide ? (row_bytes < 512 ? 128 : 64) : (row_bytes >= 512 ? 32 : 64));
 }
 
 // Row parts a tile is split into over the waves (a query's lists per workgroup): the wide
 // layout's eight waves take 2 row halves x 4 column-tile pairs at 512-byte rows, and 4 row
 // quarters x 2 column-tile pairs below, so from 33 queries on every wave holds a real column
-// tile; the narrow layout's four waves take whole tiles.
-constexpr int blk_halves(int64_t row_bytes, bool wide) {
-  return wide ? (row_bytes < 512 ? 4 : 2) : 1;
+// tile; for bit codes 8 row parts x column tiles 0 and 1 (up to 64 queries: every wave busy from
+// one query on, and two column tiles share each expansion from 33); the narrow layout's four
+// waves take whole tiles.
+constexpr int blk_halves(int64_t row_bytes, bool wide, bool bits = false) {
+  return wide ? (bits ? 8 : (row_bytes < 512 ? 4 : 2)) : 1;
 }
 
 template <bool WIDE, int RB, bool BITS>
 struct BlkLayout {
   static constexpr int waves = WIDE ? 8 : 4;
   static constexpr int threads = waves * kWave;
-  static constexpr int halves = blk_halves(RB, WIDE);
+  static constexpr int halves = blk_halves(RB, WIDE, BITS);
   // a wave's two column tiles: jt and jt + cstride (jt < 8 / cstride)
-  static constexpr int cstride = halves == 4 ? 2 : 4;
+  static constexpr int cstride = halves == 8 ? 1 : (halves == 4 ? 2 : 4);
   static constexpr int rows = blk_rows(RB, WIDE, BITS);
   static constexpr int rtw = rows / 32 / halves;  // 32-row tiles per wave
   static constexpr int per_cu = WIDE ? 1 : 2;     // resident workgroups per CU
 };
 
 static_assert(kBlkWideMaxBatch <= kBlkQpg / 2, "the row-quarter layout covers 4 column tiles");
+static_assert(kBlkWideMaxBatchBits <= 64, "the bit codes' wide layout covers 2 column tiles");
 
 static bool blk_wide(int64_t row_bytes, int64_t B) {
   (void)row_bytes;
@@ -909,6 +913,20 @@ static int blk_stages(int64_t row_bytes, int capw, bool wide, bool bits, bool ma
                                                                                  : 0;
 }
 
+// List capacity: k plus a tile's appends (one per row and query), a power of two (sorted
+// whole).
+static int blk_capw(int64_t k, int rows) { return static_cast<int>(next_pow2(k + rows)); }
+
+// The layout of a batch: wide up to kBlkWideMaxBatch queries; bit codes up to
+// kBlkWideMaxBatchBits, and only where k's lists fit beside the wide layout's 16 KiB tiles (the
+// narrow layout's take less LDS).
+static bool blk_choose_wide(int64_t row_bytes, int64_t B, int64_t k, bool bits, bool masked) {
+  if (!bits) return blk_wide(row_bytes, B);
+  return B <= kBlkWideMaxBatchBits &&
+         blk_stages(row_bytes, blk_capw(k, blk_rows(row_bytes, true, true)), true, true,
+                    masked) != 0;
+}
+
 template <class Op, int RB, bool SEED, int STAGES, bool WIDE, bool MASKED, bool CLAUSES>
 static int launch_blk_kernel(const ScanArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
   const void* fn = reinterpret_cast<const void*>(
@@ -1033,9 +1051,6 @@ __global__ void __launch_bounds__(256) mask_transpose_kernel(const uint64_t* mas
   }
 }
 
-// List capacity: k plus a tile's appends (one per row and query), a power of two (sorted
-// whole).
-static int blk_capw(int64_t k, int rows) { return static_cast<int>(next_pow2(k + rows)); }
 
 // The plan, and with a mask the transposed mask's place at the end of the workspace.
 // The plan; after its own areas the speculative bounds [B] and the fallback flag, then, with a
@@ -1043,11 +1058,11 @@ static int blk_capw(int64_t k, int rows) { return static_cast<int>(next_pow2(k +
 static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int64_t target_cus,
                          bool bits, bool masked, size_t* off_mask_t = nullptr,
                          size_t* off_spec = nullptr) {
-  const bool wide = blk_wide(row_bytes, B);
-  // the row-quarter layout covers column tiles 0-3 only (B <= kBlkWideMaxBatch = 128): its
-  // lists are sized for those 128 queries
-  const int halves = blk_halves(row_bytes, wide);
-  const int64_t qpg = halves == 4 ? kBlkQpg / 2 : kBlkQpg;
+  const bool wide = blk_choose_wide(row_bytes, B, k, bits, masked);
+  // the row-quarter layout covers column tiles 0-3 only (B <= kBlkWideMaxBatch = 128), the bit
+  // codes' eight row parts tiles 0-1 (B <= 64): their lists are sized for those queries
+  const int halves = blk_halves(row_bytes, wide, bits);
+  const int64_t qpg = halves == 8 ? kBlkQpg / 4 : (halves == 4 ? kBlkQpg / 2 : kBlkQpg);
   ScanPlan p = plan_scan(B, N, k, qpg, halves * qpg, target_cus * (wide ? 1 : 2),
                          blk_capw(k, blk_rows(row_bytes, wide, bits)), kBlkRows);
   if (off_spec != nullptr) *off_spec = align_up(p.total, 256);
@@ -1110,7 +1125,7 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   if (hipGetDevice(&dev) == hipSuccess) {
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   }
-  const bool wide = blk_wide(row_bytes, B);
+  const bool wide = blk_choose_wide(row_bytes, B, k, Op::kBits, mask != nullptr);
   size_t off_mask_t = 0;
   size_t off_spec = 0;
   const ScanPlan plan = blk_plan(B, N, k, row_bytes, cus, Op::kBits, mask != nullptr,

@@ -5,7 +5,7 @@ namespace rt {
 
 bool blocked_hamming_fits(int64_t B, int64_t W, int64_t k, bool masked) {
   if (W != 8 || k < 1 || k > kMaxK) return false;
-  const bool wide = blk_wide(8 * W, B);
+  const bool wide = blk_choose_wide(8 * W, B, k, true, masked);
   return blk_stages(8 * W, blk_capw(k, blk_rows(8 * W, wide, true)), wide, true, masked) != 0;
 }
 

@@ -237,10 +237,10 @@ static int ham_qpw(int64_t B) { return static_cast<int>(B < kHamMaxQpw ? B : kHa
 
 // From this batch on, 512-bit codes are scored on the fp4 matrix cores (the blocked scan, bits as
 // e2m1 nibbles); below, one XOR + popcount pass per query and word. Measured over 30M codes
-// (k = 100, a call): the popcount pass costs ~0.33 ms + ~48 us per query (VALU-bound: 2 VALU per
-// 32 bits; B=8 0.59 ms, B=12 0.76 ms), the matrix path ~0.63 ms flat from B=8 to B=32 (one real
-// column tile) and 0.67 ms at B=4, so it takes over from 10 queries.
-constexpr int64_t kHamMfmaMinBatch = 10;
+// (k = 100, a call): the popcount pass costs ~0.33 ms + ~35-48 us per query (VALU-bound: 2 VALU
+// per 32 bits; B=4 0.46 ms, B=8 0.59 ms, B=12 0.76 ms), the matrix path ~0.46-0.52 ms from B=12
+// to B=32 (the eight-part wide layout, one real column tile), so it takes over from 8 queries.
+constexpr int64_t kHamMfmaMinBatch = 8;
 
 static bool ham_mfma(int64_t B, int64_t W, int64_t k, bool masked) {
   return W == 8 && B >= kHamMfmaMinBatch && blocked_hamming_fits(B, W, k, masked);

@@ -94,13 +94,14 @@ def test_unseeded_large_k(dev):
     _check(dev, q, items, 1000)
 
 
-@pytest.mark.parametrize("b,n,k,masked", [(10, 5000, 50, False), (16, 20000, 100, True),
+@pytest.mark.parametrize("b,n,k,masked", [(8, 5000, 50, False), (16, 20000, 100, True),
+                                          (64, 30000, 1000, True),
                                           (32, 9000, 1000, False), (33, 5000, 100, False),
                                           (37, 20000, 1000, True),
                                           (128, 9000, 100, False), (129, 20000, 100, True),
                                           (300, 7000, 1000, False), (64, 3000, 1, True)])
 def test_matrix_core_path(dev, b, n, k, masked):
-    """512-bit codes from 10 queries on run on the fp4 matrix cores (bits as e2m1 nibbles,
+    """512-bit codes from 8 queries on run on the fp4 matrix cores (bits as e2m1 nibbles,
     the accumulator started at 64 W - 2 popcount(q)): wide and narrow layouts, k up to 1000,
     masks."""
     g = rng(b * 3 + n + k)
