@@ -289,9 +289,11 @@ static int dispatch_cand(const CandArgs& a, dim3 grid, size_t lds, hipStream_t s
 
 static int cand_capw(int64_t k) { return static_cast<int>(next_pow2(k + kWave)); }
 
+// Workgroups per query: ~2048 in all, at most one per 128 candidates (a wave's rows are an id
+// load then the row's loads, one step after another: the grid, not the loop, hides that latency).
 static int64_t cand_gx(int64_t B, int64_t P) {
   int64_t gx = cdiv(2048, B > 0 ? B : 1);
-  const int64_t by_rows = cdiv(P, 1024);
+  const int64_t by_rows = cdiv(P, 128);
   gx = gx < by_rows ? gx : by_rows;
   gx = gx < 1 ? 1 : gx;
   return gx < kCandMaxWgsPerQuery ? gx : kCandMaxWgsPerQuery;
