@@ -143,6 +143,19 @@ __device__ void block_minmax(const uint64_t* keys, int n, uint64_t* red, uint64_
   __syncthreads();
 }
 
+// Appends v at dst[*counter + j] when keep, j counting the keeping lanes of the wave before
+// this one: one LDS atomic a wave. Every lane of the wave calls it.
+__device__ __forceinline__ void wave_append(uint64_t* dst, int* counter, bool keep, uint64_t v) {
+  const uint64_t b = __ballot(keep);
+  if (b == 0ull) return;
+  const int before = static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+      static_cast<uint32_t>(b >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b), 0u)));
+  int base = 0;
+  if ((threadIdx.x & (kWave - 1)) == 0) base = atomicAdd(counter, __popcll(b));
+  base = __shfl(base, 0);
+  if (keep) dst[base + before] = v;
+}
+
 // Block-wide radix select over keys[0, n) in LDS, MSB-first digits of up to 8 bits, starting
 // below the bits every key shares (min and max agree there). Returns a bound T with at
 // most kth keys > T and at least kth keys >= T (exactly kth for distinct keys): the kth
@@ -235,6 +248,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   __shared__ int part[kMergeThreads];
   __shared__ uint64_t red[2 * kMergeWaves];
   __shared__ int sh[4];
+  __shared__ int fill;
   const int tid = threadIdx.x;
   if (m.run_if != nullptr && *m.run_if == 0u) return;  // (uniform: the fallback is not needed)
   const int64_t q = blockIdx.x;
@@ -279,15 +293,16 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     total = pre[S - 1];
   }
 
+  // Entries <= thr cannot enter the top k: once a round has kept the best k, thr is their
+  // bound (k entries >= thr, and an entry equal to it is the same composite again), so
+  // later rounds gather only what beats it and their selects run over a few survivors.
+  // Empty entries (0) are dropped from the start.
+  uint64_t thr = 0ull;
   int held = 0;
   for (int e0 = 0; e0 < total; e0 += kMergeChunk) {
     const int n = total - e0 < kMergeChunk ? total - e0 : kMergeChunk;
-    if (m.flat) {
-      const uint64_t* row = m.lists + q * static_cast<int64_t>(S);
-      for (int i = tid; i < n; i += kMergeThreads) buf[held + i] = row[e0 + i];
-    } else {
-      // owner[] maps each entry of the window to its list (LDS only), then every thread
-      // loads independent entries, four in flight
+    if (!m.flat) {
+      // owner[] maps each entry of the window to its list (LDS only)
       for (int s = tid; s < S; s += kMergeThreads) {
         const int lo = s == 0 ? 0 : pre[s - 1];
         const int hi = pre[s];
@@ -295,38 +310,47 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
         const int b = hi < e0 + n ? hi : e0 + n;
         for (int e = a; e < b; ++e) owner[e - e0] = static_cast<short>(s);
       }
-      __syncthreads();
-      for (int i0 = tid; i0 < n; i0 += 4 * kMergeThreads) {
-        uint64_t v[4];
+    }
+    if (tid == 0) fill = 0;
+    __syncthreads();
+    // every thread loads independent entries, four in flight; the trip count is the same for
+    // the whole block, so every lane of a wave takes part in each append
+    const uint64_t* row = m.lists + q * static_cast<int64_t>(S) + e0;
+    const int rounds = (n + 4 * kMergeThreads - 1) / (4 * kMergeThreads);
+    for (int r = 0; r < rounds; ++r) {
+      const int i0 = r * 4 * kMergeThreads + tid;
+      uint64_t v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i = i0 + u * kMergeThreads;
-          v[u] = 0ull;
-          if (i < n) {
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * kMergeThreads;
+        v[u] = 0ull;
+        if (i < n) {
+          if (m.flat) {
+            v[u] = row[i];
+          } else {
             const int s = owner[i];
             const int lo = s == 0 ? 0 : pre[s - 1];
             v[u] = m.lists[((slot0 + s) * m.qpw + qi) * static_cast<int64_t>(m.capw) +
                            (e0 + i - lo)];
           }
         }
-        if (m.clause.active != nullptr) {
-          // an entry that fails the query's clauses is empty (0, below every composite)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if (v[u] != 0ull && !clause_check(m.clause, q, composite_item(v[u]))) v[u] = 0ull;
-          }
-        }
+      }
+      if (!m.flat && m.clause.active != nullptr) {
+        // an entry that fails the query's clauses is empty (0, below every composite); flat
+        // lists (a seed pass's maxima) were tested where they were written
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const int i = i0 + u * kMergeThreads;
-          if (i < n) buf[held + i] = v[u];
+          if (v[u] > thr && !clause_check(m.clause, q, composite_item(v[u]))) v[u] = 0ull;
         }
       }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) wave_append(buf + held, &fill, v[u] > thr, v[u]);
     }
     __syncthreads();
-    const int cnt = held + n;
+    const int cnt = held + fill;
     if (cnt > k) {
       const uint64_t kth = block_select_desc(buf, cnt, k, hist, sh, red);
+      thr = kth;
       if (tid == 0) sh[2] = 0;
       __syncthreads();
       // at most k entries are above kth; equal entries (repeated empty seed entries, or a
