@@ -1077,20 +1077,30 @@ static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int
   return p;
 }
 
-// The threshold sample pass: the main kernel on every kSampleTileStride-th tile, when that gives
+// The threshold sample pass: the main kernel on every stride-th tile, when that gives
 // kSampleMinTiles tiles or more, behind the seed's bound. Its merge takes a speculative bound,
-// the m-th best of the sample with m = sample_rank(k): an unordered table puts about
-// Poisson(k / stride) of its top k in the sample, so m = k / stride + 5 sqrt(k / stride) + 4 falls
-// below the table's k-th best but for a tail of about 1e-6 a query, and the main pass then
+// the m-th best of the sample with m = sample_rank(k, stride): an unordered table puts about
+// Poisson(k / stride) of its top k in the sample, so m = k / stride + 5 sqrt(k / stride) + 4
+// falls below the table's k-th best but for a tail of about 1e-6 a query, and the main pass then
 // keeps about m * stride candidates a query instead of the N k / (seed rows) behind the seed's
-// bound. A query that ends with fewer than k entries although its bound was above the seed's
-// raises a flag, and the fallback (the main pass and the merge again behind the seed's bound,
-// both returning at once on the device while the flag is clear) keeps every result exact.
+// bound. The stride is 32 where that still gives kSampleMinTiles tiles (half the sample pass and
+// its merge for ~20 % more main-pass candidates), else 16. A query that ends with fewer than k
+// entries although its bound was above the seed's raises a flag, and the fallback (the main pass
+// and the merge again behind the seed's bound, both returning at once on the device while the
+// flag is clear) keeps every result exact.
 constexpr int64_t kSampleTileStride = 16;
+constexpr int64_t kSampleWideStride = 32;
 constexpr int64_t kSampleMinTiles = 2048;
 
-static int sample_rank(int64_t k) {
-  const double lam = static_cast<double>(k) / kSampleTileStride;
+// 0: no sample pass (fewer than kSampleMinTiles tiles at the narrow stride)
+static int64_t sample_stride(int64_t N) {
+  if (N >= kSampleMinTiles * kSampleWideStride * kBlkRows) return kSampleWideStride;
+  if (N >= kSampleMinTiles * kSampleTileStride * kBlkRows) return kSampleTileStride;
+  return 0;
+}
+
+static int sample_rank(int64_t k, int64_t stride) {
+  const double lam = static_cast<double>(k) / static_cast<double>(stride);
   const int64_t m = static_cast<int64_t>(std::ceil(lam + 5.0 * std::sqrt(lam) + 4.0));
   return static_cast<int>(m < k ? m : k);
 }
@@ -1208,15 +1218,16 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   a.row_stride = 1;
   a.capw = plan.main.capw;
   a.tau_in = plan.seeded ? tau : nullptr;
-  const bool sampled = plan.seeded && N >= kSampleMinTiles * kSampleTileStride * kBlkRows;
-  const bool speculative = sampled && sample_rank(k) < k;
+  const int64_t stride = plan.seeded ? sample_stride(N) : 0;
+  const bool sampled = stride > 0;
+  const bool speculative = sampled && sample_rank(k, stride) < k;
   if (sampled) {
-    a.tile_stride = kSampleTileStride;
+    a.tile_stride = stride;
     int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, wide, stream);
     if (st != kOk) return st;
     m.capw = plan.main.capw;
     m.S = plan.main.S;
-    m.k = sample_rank(k);
+    m.k = sample_rank(k, stride);
     m.tau_out = spec;
     m.tau_keep = true;
     m.tau_base = tau;
