@@ -61,15 +61,21 @@ def _popcount64(x: torch.Tensor) -> torch.Tensor:
     return ((x * 0x0101010101010101) >> 56) & 0xFF
 
 
-def test_binary_masked_30m(dev):
-    n, w, b, k = 30_000_000, 8, 64, 1000
-    print(f"binary full size N={n} W={w} B={b} k={k}", flush=True)
-    gen = torch.Generator(device=dev).manual_seed(31)
+def _check_binary(dev, n, w, b, k, masked, n_sample, seed):
+    """The 1-bit scan at full size: every id distinct, valid and passing the mask, its score
+    recomputed, descending order with lower ids first on ties, and no sampled passing item
+    that beats the k-th left out."""
+    print(f"binary full size N={n} W={w} B={b} k={k} masked={masked}", flush=True)
+    gen = torch.Generator(device=dev).manual_seed(seed)
     items = torch.randint(-2**63, 2**63 - 1, (n, w), dtype=torch.int64, device=dev,
                           generator=gen)
     q = torch.randint(-2**63, 2**63 - 1, (b, w), dtype=torch.int64, device=dev, generator=gen)
-    valid = torch.rand((b, n), device=dev, generator=gen) < 0.1
-    words = torch.ops.retrieve.pack_mask(valid)
+    if masked:
+        valid = torch.rand((b, n), device=dev, generator=gen) < 0.1
+        words = torch.ops.retrieve.pack_mask(valid)
+    else:
+        valid = torch.ones((b, n), dtype=torch.bool, device=dev)
+        words = None
     ids, sc = torch.ops.retrieve.hamming_scan_topk(q, items, k, words)
     torch.cuda.synchronize()
     assert (ids >= 0).all() and (ids < n).all()
@@ -82,10 +88,20 @@ def test_binary_masked_30m(dev):
     assert (s64[:, :-1] >= s64[:, 1:]).all()
     tie = s64[:, :-1] == s64[:, 1:]
     assert (ids[:, :-1][tie] < ids[:, 1:][tie]).all()
-    sample = torch.randint(0, n, (1_000_000,), device=dev, generator=gen)
+    sample = torch.randint(0, n, (n_sample,), device=dev, generator=gen)
     hs = _popcount64(items[sample].unsqueeze(0) ^ q.unsqueeze(1)).sum(2)  # [b, S]
     ss = 64 * w - 2 * hs
     kth_s, kth_i = s64[:, -1:], ids[:, -1:]
     beats = ((ss > kth_s) | ((ss == kth_s) & (sample.unsqueeze(0) < kth_i))) & valid[:, sample]
     for r in range(b):
         assert not (beats[r] & ~torch.isin(sample, ids[r])).any()
+
+
+def test_binary_masked_30m(dev):
+    """64 queries over 30M rows: the threshold sample pass reads every 32nd tile."""
+    _check_binary(dev, 30_000_000, 8, 64, 1000, True, 1_000_000, 31)
+
+
+def test_binary_large_batch_9m(dev):
+    """512 queries over 9M rows (every 32nd tile sampled) with no mask."""
+    _check_binary(dev, 9_000_000, 8, 512, 100, False, 200_000, 37)
