@@ -181,8 +181,8 @@ class Filter:
             bl.sets_to_expressions(sets), HASH_K, dev)
         self.rev = torch.zeros(len(CARDINALITIES), dtype=torch.bool, device=dev)
         self.sets = torch.from_numpy(sets).to(dev)
-        exact = torch.ops.retrieve.clause_bits(self.attrs, self.rev, self.sets)
-        counts = torch.ops.retrieve.mask_compact(exact, n)[1]
+        exact = torch.ops.retrieve_amd.clause_bits(self.attrs, self.rev, self.sets)
+        counts = torch.ops.retrieve_amd.mask_compact(exact, n)[1]
         self.selectivity = (counts.double() / n).cpu().numpy()
         torch.cuda.synchronize()
         log(f"selectivity per row: mean {self.selectivity.mean():.4f}, "
@@ -203,7 +203,7 @@ class Filter:
 
     def mask(self) -> torch.Tensor:
         """One batch's filter: Bloom pre-filter, then the exact post-check of its survivors."""
-        return torch.ops.retrieve.clause_bits(self.attrs, self.rev, self.sets, self.bloom())
+        return torch.ops.retrieve_amd.clause_bits(self.attrs, self.rev, self.sets, self.bloom())
 
     def bytes(self, n: int, b: int, fused: bool = False) -> int:
         """Algorithmic bytes of one batch's filter: the Bloom words and the Bloom mask written;
@@ -348,7 +348,7 @@ def main() -> int:
     if args.filter == "none":
         args.workload = "int8"
 
-    import retrieve_amd.hip  # noqa: F401  (registers torch.ops.retrieve.*)
+    import retrieve_amd.hip  # noqa: F401  (registers torch.ops.retrieve.* / retrieve_amd.*)
     import retrieve_amd.st  # noqa: F401  (registers torch.ops.st.*)
     from retrieve_amd import _native
 
@@ -371,10 +371,10 @@ def main() -> int:
 
         def step():
             if flt is None:
-                return torch.ops.retrieve.int8_scan_topk(queries, items, k)
+                return torch.ops.retrieve_amd.int8_scan_topk(queries, items, k)
             if args.unfused_filter:
-                return torch.ops.retrieve.int8_scan_topk(queries, items, k, flt.mask())
-            return torch.ops.retrieve.int8_scan_topk_clauses(queries, items, k, flt.attrs,
+                return torch.ops.retrieve_amd.int8_scan_topk(queries, items, k, flt.mask())
+            return torch.ops.retrieve_amd.int8_scan_topk_clauses(queries, items, k, flt.attrs,
                                                             flt.rev, flt.sets, flt.bloom())
 
         scan_bytes = n * d + b * d  # the item table once + the query block
@@ -420,10 +420,10 @@ def main() -> int:
 
         def step():
             if args.unfused_filter:
-                return torch.ops.retrieve.dense_scan_topk(queries, items, k, flt.mask())
+                return torch.ops.retrieve_amd.dense_scan_topk(queries, items, k, flt.mask())
             # (the blocked scan of a large batch reads the transposed words directly)
             words = flt.bloom_t() if blocked else flt.bloom()
-            return torch.ops.retrieve.dense_scan_topk_clauses(queries, items, k, flt.attrs,
+            return torch.ops.retrieve_amd.dense_scan_topk_clauses(queries, items, k, flt.attrs,
                                                              flt.rev, flt.sets, words)
 
         scan_bytes = n * d * 2 + b * d * 2
@@ -463,7 +463,7 @@ def main() -> int:
         queries = queries / queries.norm(dim=1, keepdim=True)
 
         def step():
-            return torch.ops.retrieve.dense_scan_topk(queries, items, k)
+            return torch.ops.retrieve_amd.dense_scan_topk(queries, items, k)
 
         # recall@k against torch's own fp32 product and top-k on the GPU (ties aside, the same)
         torch.backends.cuda.matmul.allow_tf32 = False
@@ -499,7 +499,7 @@ def main() -> int:
         queries = q32.bfloat16()
 
         def step():
-            return torch.ops.retrieve.dense_scan_topk(queries, items, k)
+            return torch.ops.retrieve_amd.dense_scan_topk(queries, items, k)
 
         # recall@k against exact float32 scoring of the unrounded rows (chunked torch.mm)
         torch.backends.cuda.matmul.allow_tf32 = False
@@ -519,7 +519,7 @@ def main() -> int:
         # the same with fp16 storage (the reference module's dtype), outside the timed region
         items_h = items32.half()
         del items32
-        got = torch.ops.retrieve.dense_scan_topk(q32.half(), items_h, k)[0]
+        got = torch.ops.retrieve_amd.dense_scan_topk(q32.half(), items_h, k)[0]
         hits = (got.unsqueeze(2) == best_i.unsqueeze(1)).any(2).sum().item()
         extra["recall_at_k_vs_fp32_fp16_storage"] = hits / (b * k)
         log(f"recall@{k} vs exact fp32, fp16 storage: "
@@ -556,12 +556,12 @@ def main() -> int:
         flt = Filter(n, b, args.selectivity, dev)
 
         def step():
-            ids1, _ = torch.ops.retrieve.hamming_scan_topk_clauses(
+            ids1, _ = torch.ops.retrieve_amd.hamming_scan_topk_clauses(
                 q_bits, item_bits, k1, flt.attrs, flt.rev, flt.sets,
                 flt.bloom_t() if b >= 8 and k1 <= 1024 else flt.bloom(),
                 fused=not args.unfused_bits)
             counts = (ids1 >= 0).sum(1)
-            return torch.ops.retrieve.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
+            return torch.ops.retrieve_amd.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
 
         scan_bytes = n * d // 8 + b * d // 8
         table = item_bits  # the streamed table (the read ceiling is measured over it)

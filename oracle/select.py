@@ -63,6 +63,58 @@ def _neg(s: np.ndarray) -> np.ndarray:
     return -s.astype(np.float64)
 
 
+class RepeatedRows:
+    """``topk_rows`` for a table whose N rows each copy one of R distinct base rows, so that an
+    item's score is its base row's: ``topk(base_scores[b], row_of_item, k, valid)`` equals
+    ``topk_rows(base_scores[:, row_of_item], k, valid)`` without the ``[B, N]`` matrix. The items
+    are taken score group by score group in descending order (a group = every base row of one
+    score value), each group's items in ascending index, until k pass ``valid``: the same
+    (score desc, index asc) order. Pinned against ``topk_rows`` on small tables with heavy ties
+    across and within base rows (``tests/test_oracle.py``)."""
+
+    def __init__(self, row_of_item: np.ndarray, n_base: int):
+        rows = np.asarray(row_of_item, np.int64)
+        self.n = rows.size
+        self.order = np.argsort(rows, kind="stable")  # items of base row j, ascending index
+        self.starts = np.searchsorted(rows[self.order], np.arange(n_base + 1))
+
+    def items_of(self, base: np.ndarray) -> np.ndarray:
+        parts = [self.order[self.starts[j]:self.starts[j + 1]] for j in np.asarray(base).tolist()]
+        return np.sort(np.concatenate(parts)) if parts else np.empty(0, np.int64)
+
+    def topk(self, base_scores: np.ndarray, k: int, valid: np.ndarray | None = None,
+             pad_score=None) -> tuple[np.ndarray, np.ndarray]:
+        """One query: ``base_scores [R]``, ``valid [N]`` bool → ``(ids [k], scores [k])``."""
+        s = np.asarray(base_scores)
+        if pad_score is None:
+            pad_score = INT32_MIN if np.issubdtype(s.dtype, np.integer) else -np.inf
+        neg = _neg(s)
+        r = neg.size
+        m = min(r, 64)
+        while True:
+            ids = np.full(k, -1, np.int64)
+            out = np.full(k, pad_score, dtype=s.dtype)
+            # the m best base rows; every row scoring above the worst of them is among them
+            cand = np.argpartition(neg, m - 1)[:m] if m < r else np.arange(r)
+            lim = neg[cand].max()
+            got = 0
+            for v in np.unique(neg[cand]).tolist():  # descending score
+                # (the worst value's rows may lie partly outside the m: take all of them)
+                rows = cand[neg[cand] == v] if v < lim else np.flatnonzero(neg == v)
+                items = self.items_of(rows)
+                if valid is not None:
+                    items = items[np.asarray(valid, bool)[items]]
+                take = min(k - got, items.size)
+                ids[got:got + take] = items[:take]
+                out[got:got + take] = s[rows[0]]
+                got += take
+                if got == k:
+                    return ids, out
+            if m == r:
+                return ids, out
+            m = min(r, 4 * m)
+
+
 def merge_topk(
     s_a: np.ndarray, i_a: np.ndarray, s_b: np.ndarray, i_b: np.ndarray, k: int
 ) -> tuple[np.ndarray, np.ndarray]:

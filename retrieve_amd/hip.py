@@ -1,6 +1,14 @@
 """The ``"hip"`` op namespace: the reference's ``retrieve.ops.triton`` surface, re-implemented as
 HIP kernels behind the C ABI and registered as ``torch.ops.retrieve.*``.
 
+``torch.ops.retrieve`` holds exactly the reference's seven ops (``clause_mask``,
+``clause_mask_scores``, ``clause_compact``, ``fused_masked_knn_topk``, ``gemv_scores``,
+``oporp_1bit_match_topk_full``, ``oporp_1bit_match_topk_indirect``) with the reference's
+schemas, as its export gate requires (``retrieve/tests/compile/test_export_kernel_ref.py:115-143``).
+The ops this build adds (the fused full scans with and without clauses, ``clause_bits``,
+``mask_compact``, the re-ranks, the quantize and pack kernels) register under
+``torch.ops.retrieve_amd.*`` instead, so they never enter the reference's namespace.
+
 Importing this module registers the ops (the one side-effecting import, as the reference's
 ``retrieve.ops.triton``; ``import retrieve_amd`` registers nothing). Every op validates its
 inputs here (``ValueError`` on shapes / contiguity, ``TypeError`` on dtypes, as
@@ -91,7 +99,7 @@ def _int8_scan_prep(query_codes: Tensor, item_codes: Tensor, k: int, mask: Tenso
     return query_codes.contiguous(), mask
 
 
-@torch.library.custom_op("retrieve::int8_scan_topk", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::int8_scan_topk", mutates_args=(), device_types="cuda")
 def int8_scan_topk(
     query_codes: Tensor, item_codes: Tensor, k: int, mask: Tensor | None = None
 ) -> tuple[Tensor, Tensor]:
@@ -141,7 +149,7 @@ def _(query_codes, item_codes, k, mask=None):
 _DENSE_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 
-@torch.library.custom_op("retrieve::dense_scan_topk", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::dense_scan_topk", mutates_args=(), device_types="cuda")
 def dense_scan_topk(
     query: Tensor, item_embs: Tensor, k: int, mask: Tensor | None = None
 ) -> tuple[Tensor, Tensor]:
@@ -257,7 +265,7 @@ def _hamming_call(query_bits, item_bits, k, mask, score_dtype):
     return ids, scores
 
 
-@torch.library.custom_op("retrieve::hamming_scan_topk", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::hamming_scan_topk", mutates_args=(), device_types="cuda")
 def hamming_scan_topk(
     query_bits: Tensor, item_bits: Tensor, k: int, mask: Tensor | None = None
 ) -> tuple[Tensor, Tensor]:
@@ -403,7 +411,7 @@ def _(scores, item_clause_attrs, clause_is_reverse, query_clause_attrs):
     return torch.empty_like(scores)
 
 
-@torch.library.custom_op("retrieve::clause_bits", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::clause_bits", mutates_args=(), device_types="cuda")
 def clause_bits(
     item_clause_attrs: Tensor, clause_is_reverse: Tensor, query_values: Tensor,
     and_mask: Tensor | None = None,
@@ -440,12 +448,21 @@ def _(item_clause_attrs, clause_is_reverse, query_values, and_mask=None):
 def _transposed_stride(mask: Tensor | None, b: int) -> int:
     """The row stride S of a ``[B, W]`` mask whose words are stored transposed, ``[W, S]`` with
     S >= B rounded up to 256 (``st.bloom_search_t``'s layout, viewed as ``[B, W]``), else 0. The
-    blocked scans read such a mask as it is; every other path takes ``mask.contiguous()``."""
+    blocked scans read such a mask as it is; every other path takes ``mask.contiguous()``.
+
+    The scans stage all ``roundup(B, 256)`` entries of a word row from the view's first element,
+    so a view qualifies only where the last row's block ends inside its storage: a row-sliced or
+    offset view of the transposed buffer (``m[1:]``) would read past the allocation's end and is
+    copied instead."""
     if mask is None or mask.dim() != 2 or b == 0:
         return 0
     s0, s1 = mask.stride()
     pad = -(-b // 256) * 256
-    return int(s1) if s0 == 1 and s1 >= pad and s1 % 256 == 0 else 0
+    if not (s0 == 1 and s1 >= pad and s1 % 256 == 0):
+        return 0
+    words = mask.shape[1]
+    end = mask.storage_offset() + (words - 1) * s1 + pad
+    return int(s1) if end <= mask.untyped_storage().nbytes() // mask.element_size() else 0
 
 
 def _scan_clauses(q: Tensor, items: Tensor, k: int, dtype: int, item_clause_attrs: Tensor,
@@ -493,7 +510,7 @@ def _scan_clauses(q: Tensor, items: Tensor, k: int, dtype: int, item_clause_attr
     return True
 
 
-@torch.library.custom_op("retrieve::int8_scan_topk_clauses", mutates_args=(),
+@torch.library.custom_op("retrieve_amd::int8_scan_topk_clauses", mutates_args=(),
                          device_types="cuda")
 def int8_scan_topk_clauses(
     query_codes: Tensor, item_codes: Tensor, k: int, item_clause_attrs: Tensor,
@@ -524,7 +541,7 @@ def _(query_codes, item_codes, k, item_clause_attrs, clause_is_reverse, query_va
             query_codes.new_empty((b, k), dtype=torch.int32))
 
 
-@torch.library.custom_op("retrieve::dense_scan_topk_clauses", mutates_args=(),
+@torch.library.custom_op("retrieve_amd::dense_scan_topk_clauses", mutates_args=(),
                          device_types="cuda")
 def dense_scan_topk_clauses(
     query: Tensor, item_embs: Tensor, k: int, item_clause_attrs: Tensor,
@@ -571,7 +588,7 @@ def _(query, item_embs, k, item_clause_attrs, clause_is_reverse, query_values, m
             query.new_empty((b, k), dtype=torch.float32))
 
 
-@torch.library.custom_op("retrieve::hamming_scan_topk_clauses", mutates_args=(),
+@torch.library.custom_op("retrieve_amd::hamming_scan_topk_clauses", mutates_args=(),
                          device_types="cuda")
 def hamming_scan_topk_clauses(
     query_bits: Tensor, item_bits: Tensor, k: int, item_clause_attrs: Tensor,
@@ -640,7 +657,7 @@ def _mask_compact(mask: Tensor, n: int) -> tuple[Tensor, Tensor]:
     return ids, counts
 
 
-@torch.library.custom_op("retrieve::mask_compact", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::mask_compact", mutates_args=(), device_types="cuda")
 def mask_compact(mask: Tensor, n: int) -> tuple[Tensor, Tensor]:
     """Packed mask ``[B, ceil(n/64)]`` int64 → ``(ids [B, n] int64, counts [B] int64)``: row
     ``b``'s set items in ascending order on ``[0, counts[b])``; the tail is not written."""
@@ -785,7 +802,7 @@ def _(query_bits, item_bits, k, positive_indices, counts):
             query_bits.new_empty((b, kk), dtype=torch.float32))
 
 
-@torch.library.custom_op("retrieve::int8_candidates_topk", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::int8_candidates_topk", mutates_args=(), device_types="cuda")
 def int8_candidates_topk(
     query_codes: Tensor, item_codes: Tensor, positive_indices: Tensor, counts: Tensor, k: int
 ) -> tuple[Tensor, Tensor]:
@@ -851,7 +868,7 @@ def _(query, item_embs_t):
 # --- the reference's per-row quantization and bool masks for the scans ---------------------------
 
 
-@torch.library.custom_op("retrieve::quantize_int8", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::quantize_int8", mutates_args=(), device_types="cuda")
 def quantize_int8(embs: Tensor) -> tuple[Tensor, Tensor]:
     """Per-row symmetric int8 codes and scales (``retrieve/src/retrieve/indexing/quantize.py:
     9-18``): ``abs_max = clamp(max |x|, 1e-8)``, ``scale = abs_max / 127``,
@@ -869,7 +886,7 @@ def _(embs):
             embs.new_empty(embs.shape[:1], dtype=torch.float32))
 
 
-@torch.library.custom_op("retrieve::pack_mask", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::pack_mask", mutates_args=(), device_types="cuda")
 def pack_mask(valid: Tensor) -> Tensor:
     """``[B, N]`` bool → ``[B, ceil(N/64)]`` int64 words, item ``d`` at bit ``63 - d % 64``: the
     mask form of the fused scans (``int8_scan_topk``, ``dense_scan_topk``,
@@ -892,7 +909,7 @@ def _(valid):
     return valid.new_empty((valid.shape[0], (valid.shape[1] + 63) // 64), dtype=torch.int64)
 
 
-@torch.library.custom_op("retrieve::pack_signs", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::pack_signs", mutates_args=(), device_types="cuda")
 def pack_signs(values: Tensor) -> Tensor:
     """``[R, D]`` floats → ``[R, D // 64]`` int64, bit ``b`` of word ``w`` set iff ``values[:,
     64 w + b] > 0`` (``_pack_signs_to_int64``, ``retrieve/src/retrieve/indexing/quantize.py:
@@ -919,7 +936,7 @@ def _(values):
     return values.new_empty((values.shape[0], values.shape[1] // 64), dtype=torch.int64)
 
 
-@torch.library.custom_op("retrieve::quantize_int8_global", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::quantize_int8_global", mutates_args=(), device_types="cuda")
 def quantize_int8_global(embs: Tensor, rows: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """One global int8 scale (``quantize_int8_global``, ``retrieve/src/retrieve/indexing/
     quantize.py:25-52``): ``abs_max = max(max |x|, 1e-8)``, codes ``clamp(round(x / abs_max *
@@ -954,7 +971,7 @@ def _(embs, rows=None):
     return embs.new_empty(embs.shape, dtype=torch.int8), embs.new_empty((1,))
 
 
-@torch.library.custom_op("retrieve::int8_rerank_topk", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("retrieve_amd::int8_rerank_topk", mutates_args=(), device_types="cuda")
 def int8_rerank_topk(
     query_codes: Tensor, query_scales: Tensor, item_codes: Tensor, item_rows: Tensor,
     global_scale: Tensor, candidate_ids: Tensor, k: int

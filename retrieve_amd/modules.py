@@ -3,7 +3,7 @@ fused HIP ops: the same classes, constructors, ``register_index`` / ``prepare_qu
 ``forward`` signatures, buffer names and outputs, with each score-then-select pair replaced by
 one fused scan or candidate kernel, so no ``[B, N]`` score matrix is written.
 
-- LiNR: ``ExactAttributeFilter``, ``PostfilterKNN``, ``PrefilterKNN``, ``OneBitKNN``,
+- LiNR: ``ExactAttributeFilter``, ``PostfilterKNN``, ``PrefilterKNN``, ``FullScanKNN``, ``OneBitKNN``,
   ``SimHashKNN``, ``LiNRV1`` / ``LiNRV2`` / ``LiNRV3``, ``LiNRBuilder``.
 - SilverTorch: ``SilverTorch`` (IVF + int8 with a none / bloom / exact filter),
   ``SilverTorchBuilder``, ``OfficialConfig``, ``PreparedFilter``.
@@ -27,14 +27,16 @@ from torch import Tensor, nn
 
 from retrieve_amd import _native as nat
 from retrieve_amd import bloom as _bloom
-from retrieve_amd import hip as _hip  # registers torch.ops.retrieve.*
+from retrieve_amd import hip as _hip  # registers torch.ops.retrieve.* / retrieve_amd.*
 from retrieve_amd import st as _st  # registers torch.ops.st.*
 
-ops = torch.ops.retrieve
+ops = torch.ops.retrieve  # the reference's seven ops
+xops = torch.ops.retrieve_amd  # the fused scans, masks, re-ranks and packing this build adds
 
 __all__ = [
     "ExactAttributeFilter",
     "FilterModule",
+    "FullScanKNN",
     "KMeans",
     "LiNRBuilder",
     "LiNRV1",
@@ -100,11 +102,11 @@ class FilterModule(nn.Module, abc.ABC):
     def evaluate_mask(self, q: Tensor, start: int = 0, end: int | None = None) -> Tensor: ...
 
     def mask_bits(self, q: Tensor) -> Tensor:
-        return ops.pack_mask(self.evaluate_mask(q))
+        return xops.pack_mask(self.evaluate_mask(q))
 
     def evaluate_indices(self, q: Tensor) -> tuple[Tensor, Tensor]:
         bits = self.mask_bits(q)
-        return ops.mask_compact(bits, self._n_items())
+        return xops.mask_compact(bits, self._n_items())
 
     def evaluate_subset(self, q: Tensor, candidate_ids: Tensor) -> Tensor:
         return self.evaluate_mask(q).gather(1, candidate_ids)
@@ -155,7 +157,7 @@ class ExactAttributeFilter(FilterModule):
 
     def mask_bits(self, q: Tensor, and_mask: Tensor | None = None) -> Tensor:
         """The packed ``[B, ceil(N/64)]`` words, optionally AND-ed with ``and_mask``."""
-        return ops.clause_bits(self.item_clause_attrs, self.clause_is_reverse, q, and_mask)
+        return xops.clause_bits(self.item_clause_attrs, self.clause_is_reverse, q, and_mask)
 
     def mask_scores(self, scores: Tensor, q: Tensor) -> Tensor:
         return ops.clause_mask_scores(scores, self.item_clause_attrs, self.clause_is_reverse, q)
@@ -210,10 +212,10 @@ class PostfilterKNN(RetrievalModule):
 
     def forward_bits(self, query: Tensor, bits: Tensor | None) -> tuple[Tensor, Tensor]:
         """Top-k over the items whose bit is set in the packed ``bits`` (all items if None)."""
-        return ops.dense_scan_topk(query.to(torch.float16), self.item_embs, self.k, bits)
+        return xops.dense_scan_topk(query.to(torch.float16), self.item_embs, self.k, bits)
 
     def forward(self, query: Tensor, mask: Tensor | None = None) -> tuple[Tensor, Tensor]:
-        bits = None if mask is None else ops.pack_mask(mask)
+        bits = None if mask is None else xops.pack_mask(mask)
         return self.forward_bits(query, bits)
 
 
@@ -237,13 +239,66 @@ class PrefilterKNN(RetrievalModule):
                 counts: Tensor | None = None) -> tuple[Tensor, Tensor]:
         query = query.to(torch.float16)
         if candidate_ids is None:
-            return ops.dense_scan_topk(query, self.item_embs, self.k)
+            return xops.dense_scan_topk(query, self.item_embs, self.k)
         b, p = candidate_ids.shape
         if counts is None:
             counts = torch.full((b,), p, dtype=torch.int64, device=query.device)
         if p < self.k:  # the op needs >= k columns; lanes past counts are never read
             candidate_ids = torch.nn.functional.pad(candidate_ids, (0, self.k - p), value=-1)
         return ops.fused_masked_knn_topk(query, self.item_embs, candidate_ids, counts, self.k)
+
+
+class FullScanKNN(RetrievalModule):
+    """Exhaustive scan + top-k with POST-filter semantics (``modules/knn.py:125-170``).
+
+    - ``mask [B, N]`` bool: the top k over every item first, then the hits that fail the mask
+      tombstoned to id ``-1`` with their scores kept (``post_filter_topk``,
+      ``functional.py:146-155``): a masked hit is not replaced by the next passing item.
+    - ``candidate_ids [B, P]``: re-rank the given ids only; ``-1`` entries are padding, never
+      scored or returned; ``min(k, P)`` columns, short rows ending in ``-1`` / ``-inf``.
+
+    Items keep their dtype (fp32, fp16 or bf16) and scores come back in it, as the reference's
+    ``query @ item_embs.T`` does; here they are accumulated in fp32 by the fused scan
+    (``dense_scan_topk``) or the candidate kernel (``fused_masked_knn_topk``) and rounded once.
+    Ties go to the lower item id."""
+
+    item_embs: Tensor
+
+    def __init__(self, k: int) -> None:
+        super().__init__()
+        self.k = k
+        nat.lib()
+
+    def register_index(self, item_embs: Tensor) -> None:
+        self.register_buffer("item_embs", item_embs.contiguous())
+
+    def forward(self, query: Tensor, mask: Tensor | None = None,
+                candidate_ids: Tensor | None = None) -> tuple[Tensor, Tensor]:
+        if query.dtype != self.item_embs.dtype:
+            raise RuntimeError(f"expected query and item_embs to have the same dtype, got "
+                               f"{query.dtype} and {self.item_embs.dtype}")
+        if candidate_ids is not None:
+            return self._rerank(query, candidate_ids)
+        n = self.item_embs.shape[0]
+        if self.k > n:  # torch.topk's own check on the [B, N] scores
+            raise RuntimeError(f"selected index k out of range: k={self.k}, N={n}")
+        ids, scores = xops.dense_scan_topk(query, self.item_embs, self.k)
+        if mask is not None:
+            ids = ids.masked_fill(~mask.gather(1, ids), -1)
+        return ids, scores.to(query.dtype)
+
+    def _rerank(self, query: Tensor, candidate_ids: Tensor) -> tuple[Tensor, Tensor]:
+        b, p = candidate_ids.shape
+        valid = candidate_ids >= 0
+        # the real ids first, in their order: the candidate kernel reads a prefix of counts[b]
+        order = torch.argsort((~valid).to(torch.int8), dim=1, stable=True)
+        cand = candidate_ids.gather(1, order)
+        if p < self.k:
+            cand = torch.nn.functional.pad(cand, (0, self.k - p), value=-1)
+        ids, scores = ops.fused_masked_knn_topk(query, self.item_embs, cand, valid.sum(1),
+                                                self.k)
+        kk = min(self.k, p)
+        return ids[:, :kk], scores[:, :kk].to(query.dtype)
 
 
 # --- 1-bit codes ---------------------------------------------------------------------------
@@ -253,7 +308,7 @@ def _pack_rows(x: Tensor, words: int, project) -> Tensor:
     """``project`` ([R, D] → [R, 64 * words] floats) and the sign packing, chunk by chunk."""
     out = torch.empty((x.shape[0], words), dtype=torch.int64, device=x.device)
     for s in range(0, x.shape[0], _CODE_CHUNK_ROWS):
-        out[s:s + _CODE_CHUNK_ROWS] = ops.pack_signs(project(x[s:s + _CODE_CHUNK_ROWS]))
+        out[s:s + _CODE_CHUNK_ROWS] = xops.pack_signs(project(x[s:s + _CODE_CHUNK_ROWS]))
     return out
 
 
@@ -309,7 +364,7 @@ class _PackedBitsKNN(RetrievalModule):
     def forward_bits(self, query: Tensor, bits: Tensor | None) -> tuple[Tensor, Tensor]:
         """Full scan restricted to the items set in packed ``bits``: ``(ids, fp32 scores)``,
         ``-1`` / ``-inf`` past the passing items."""
-        ids, s = ops.hamming_scan_topk(self._project_query(query), self.item_bits, self.k, bits)
+        ids, s = xops.hamming_scan_topk(self._project_query(query), self.item_bits, self.k, bits)
         return ids, torch.where(ids >= 0, s.to(torch.float32), float("-inf"))
 
     def forward(self, query: Tensor, candidate_ids: Tensor | None = None,
@@ -358,7 +413,7 @@ class OneBitKNN(_PackedBitsKNN):
         if query.dim() != 2:
             raise ValueError(f"expected 2-D [B, D] query, got shape {tuple(query.shape)}")
         k_bits = _oporp_k_bits(query.shape[1], self.k_bits)
-        return ops.pack_signs(_oporp_sketch(query, self.oporp_signs, self.oporp_perm, k_bits))
+        return xops.pack_signs(_oporp_sketch(query, self.oporp_signs, self.oporp_perm, k_bits))
 
 
 def _rederive_k_bits(module: OneBitKNN, incompatible_keys) -> None:
@@ -390,7 +445,7 @@ class SimHashKNN(_PackedBitsKNN):
     def _project_query(self, query: Tensor) -> Tensor:
         if query.dim() != 2:
             raise ValueError(f"expected 2-D [B, D] query, got shape {tuple(query.shape)}")
-        return ops.pack_signs(query @ self.simhash_R.t())
+        return xops.pack_signs(query @ self.simhash_R.t())
 
 
 # --- LiNR variants ---------------------------------------------------------------------------
@@ -725,11 +780,11 @@ def quantize_int8_global(embs: Tensor, rows: Tensor | None = None) -> tuple[Tens
     """One global scale (``retrieve/src/retrieve/indexing/quantize.py:34-52``): ``abs_max =
     max(max x, -min x)`` floored at 1e-8, codes ``clamp(round(x / abs_max * 127))`` in fp32,
     rows written in ``rows`` order when given; returns ``(codes [N, D] int8, abs_max / 127)``.
-    GPU tables go through the HIP kernels (``torch.ops.retrieve.quantize_int8_global``); a
+    GPU tables go through the HIP kernels (``torch.ops.retrieve_amd.quantize_int8_global``); a
     table held on the host (an index built on the CPU) is quantized there with the same
     arithmetic."""
     if embs.is_cuda:
-        codes, abs_max = torch.ops.retrieve.quantize_int8_global(
+        codes, abs_max = torch.ops.retrieve_amd.quantize_int8_global(
             embs.to(torch.float32), None if rows is None else rows.to(embs.device))
         return codes, float((abs_max / 127.0).item())
     abs_max = torch.maximum(embs.amax(), -embs.amin()).clamp(min=1e-8)
@@ -960,8 +1015,8 @@ class SilverTorch(RetrievalModule):
     def _forward_candidates(self, query: Tensor, candidate_ids: Tensor):
         """Re-rank original ids (``-1`` = padding): ``min(k, P)`` columns, ``-1`` / ``-inf``
         past a row's candidates (``modules/silvertorch.py:363-379``)."""
-        q_codes, q_scales = ops.quantize_int8(query.to(torch.float32))
-        return ops.int8_rerank_topk(q_codes, q_scales, self.item_codes, self.inv_perm,
+        q_codes, q_scales = xops.quantize_int8(query.to(torch.float32))
+        return xops.int8_rerank_topk(q_codes, q_scales, self.item_codes, self.inv_perm,
                                     self.global_scale, candidate_ids.to(torch.int64), self.k)
 
 

@@ -930,7 +930,7 @@ def _st_search(query, probe_ids, cluster_offsets, cluster_sizes, item_codes, sor
         # one list holding every item in order: slot = position, the full-scan kernels; a row
         # whose probe is not list 0 has no slot and ends as pads
         from retrieve_amd import hip  # noqa: F401  (registers torch.ops.retrieve.*)
-        pos, dots = torch.ops.retrieve.int8_scan_topk(codes, item_codes, k, mask)
+        pos, dots = torch.ops.retrieve_amd.int8_scan_topk(codes, item_codes, k, mask)
         ids.copy_(pos)
         with torch.cuda.device(dev):
             st = lib.rt_search_epilogue(nat.ptr(ids), nat.ptr(dots), nat.ptr(scores), b, k,

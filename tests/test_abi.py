@@ -78,9 +78,9 @@ def test_workspace_grows_with_batch():
 
 
 def test_no_alloc_rejections_need_no_gpu():
-    """The allocation-free int8 scan rejects null pointers, and a plan above its fixed scratch
-    (k = 1000 over 6000 queries of a 1024-row table: 375 MiB), before any device call. The
-    non-null addresses of the second call are placeholders that are never dereferenced."""
+    """The allocation-free int8 scan rejects null pointers before any device call. (Its
+    rejection of a plan above the fixed scratch is tested with real device buffers, on the GPU,
+    in ``tests/test_zz_no_alloc.py``: no call here passes an address that is not a buffer.)"""
     import torch  # noqa: F401
 
     from retrieve_amd import _native
@@ -88,7 +88,5 @@ def test_no_alloc_rejections_need_no_gpu():
     lib = _native.lib()
     st = lib.rt_int8_scan_topk_noalloc(None, 2, None, 10, 64, 5, None, 0, None, None, None)
     assert st == 1 and b"must not be null" in lib.rt_last_error()
-    st = lib.rt_int8_scan_topk_noalloc(256, 6000, 512, 1024, 64, 1000, None, 0, 768, 1024, None)
-    assert st == 1 and b"scratch" in lib.rt_last_error()
     st = lib.rt_int8_scan_topk(None, 2, None, 10, 64, 5, None, 0, None, None, None, 0, None)
     assert st == 1 and b"null" in lib.rt_last_error()

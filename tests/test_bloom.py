@@ -130,11 +130,11 @@ def test_bloom_and_exact_is_exact(dev):
     assert (_unpack(bmask.cpu().numpy(), n) | ~exact).all()  # no false negatives
     rev = torch.zeros(c, dtype=torch.bool, device=dev)
     ta = torch.from_numpy(attrs).to(dev)
-    both = torch.ops.retrieve.clause_bits(ta, rev, torch.from_numpy(sets).to(dev), bmask)
+    both = torch.ops.retrieve_amd.clause_bits(ta, rev, torch.from_numpy(sets).to(dev), bmask)
     assert np.array_equal(both.cpu().numpy(), _pack(exact))
     codes = g.integers(-128, 128, (n, 64), dtype=np.int8)
     qc = g.integers(-128, 128, (7, 64), dtype=np.int8)
-    ids, sc = torch.ops.retrieve.int8_scan_topk(torch.from_numpy(qc).to(dev),
+    ids, sc = torch.ops.retrieve_amd.int8_scan_topk(torch.from_numpy(qc).to(dev),
                                                torch.from_numpy(codes).to(dev), 20, both)
     want_ids, want_sc = osc.int8_topk(qc, codes, 20, exact)
     assert np.array_equal(ids.cpu().numpy(), want_ids)

@@ -86,7 +86,7 @@ def test_duplicated_candidate_at_the_boundary(dev):
     q = np.ones((1, d), np.int8)
     for reps in (7, 300, 5000):
         cand = np.array([[2] * reps + [1] + [3] * 20], np.int64)
-        ids, sc = torch.ops.retrieve.int8_candidates_topk(
+        ids, sc = torch.ops.retrieve_amd.int8_candidates_topk(
             _t(dev, q), _t(dev, items), _t(dev, cand), _t(dev, np.array([cand.shape[1]])), 5)
         assert ids.cpu().tolist() == [[1, 2, 2, 2, 2]], reps
         assert sc.cpu().tolist() == [[128, 64, 64, 64, 64]]
@@ -122,10 +122,10 @@ def test_int8_candidates_rerank(dev):
     q = g.integers(-128, 128, (b, d), dtype=np.int8)
     bits = g.integers(-(2**63), 2**63 - 1, (n, 8), dtype=np.int64)
     qbits = g.integers(-(2**63), 2**63 - 1, (b, 8), dtype=np.int64)
-    hids, _ = torch.ops.retrieve.hamming_scan_topk(_t(dev, qbits), _t(dev, bits), 1000)
+    hids, _ = torch.ops.retrieve_amd.hamming_scan_topk(_t(dev, qbits), _t(dev, bits), 1000)
     hids[:, :100] = torch.arange(1099, 999, -1, device=dev)  # ties, descending ids
     counts = torch.full((b,), 1000, dtype=torch.int64, device=dev)
-    ids, sc = torch.ops.retrieve.int8_candidates_topk(_t(dev, q), _t(dev, codes), hids, counts,
+    ids, sc = torch.ops.retrieve_amd.int8_candidates_topk(_t(dev, q), _t(dev, codes), hids, counts,
                                                       100)
     cand = hids.cpu().numpy()
     want_ids, want_sc = osc.candidate_topk(
@@ -145,7 +145,7 @@ def test_large_p_and_bad_ids(dev):
     counts[0] = max(counts[0], 1000)  # enough valid candidates to fill k
     cand[0, 5] = -3  # outside the table: skipped
     cand[0, 6] = n + 10
-    ids, sc = torch.ops.retrieve.int8_candidates_topk(_t(dev, q), _t(dev, codes), _t(dev, cand),
+    ids, sc = torch.ops.retrieve_amd.int8_candidates_topk(_t(dev, q), _t(dev, codes), _t(dev, cand),
                                                       _t(dev, counts), k)
 
     def score(r, c):

@@ -128,10 +128,10 @@ def test_bits_layout_and_and_mask(dev):
     q = _queries(g, 9, 4, 7, 0.4)
     rev = np.array([1, 0, 0, 1], bool)
     want = of.clause_match(attrs, rev, q)
-    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, q))
+    bits = torch.ops.retrieve_amd.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, q))
     assert np.array_equal(bits.cpu().numpy(), _pack(want))
     pre = g.random((9, n)) < 0.5
-    bits2 = torch.ops.retrieve.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, q),
+    bits2 = torch.ops.retrieve_amd.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, q),
                                            _t(dev, _pack(pre)))
     assert np.array_equal(bits2.cpu().numpy(), _pack(want & pre))
 
@@ -144,7 +144,7 @@ def test_value_sets(dev):
     sets = g.integers(0, 12, (11, c, 4), dtype=np.int64)
     sets[g.random(sets.shape) < 0.4] = -1
     sets[3] = -1  # no active clause
-    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs), _t(dev, np.zeros(c, bool)),
+    bits = torch.ops.retrieve_amd.clause_bits(_t(dev, attrs), _t(dev, np.zeros(c, bool)),
                                           _t(dev, sets))
     assert np.array_equal(bits.cpu().numpy(), _pack(of.clause_match_sets(attrs, sets)))
 
@@ -155,7 +155,7 @@ def test_mask_compact_random_bits(dev):
     valid = g.random((5, n)) < np.array([0.0, 0.01, 0.5, 0.99, 1.0])[:, None]
     words = _pack(valid)
     words[:, -1] |= np.int64(0x7FFF)  # bits past item n - 1 are ignored
-    ids, counts = torch.ops.retrieve.mask_compact(_t(dev, words), n)
+    ids, counts = torch.ops.retrieve_amd.mask_compact(_t(dev, words), n)
     ids, counts = ids.cpu().numpy(), counts.cpu().numpy()
     for r in range(5):
         assert counts[r] == valid[r].sum()
@@ -171,8 +171,8 @@ def test_filtered_int8_scan(dev):
     rev = np.zeros(2, bool)
     codes = g.integers(-128, 128, (n, d), dtype=np.int8)
     qc = g.integers(-128, 128, (b, d), dtype=np.int8)
-    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, q))
-    ids, sc = torch.ops.retrieve.int8_scan_topk(_t(dev, qc), _t(dev, codes), k, bits)
+    bits = torch.ops.retrieve_amd.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, q))
+    ids, sc = torch.ops.retrieve_amd.int8_scan_topk(_t(dev, qc), _t(dev, codes), k, bits)
     want_ids, want_sc = osc.int8_topk(qc, codes, k, of.clause_match(attrs, rev, q))
     assert np.array_equal(sc.cpu().numpy(), want_sc)
     assert np.array_equal(ids.cpu().numpy(), want_ids)
@@ -202,7 +202,7 @@ def test_compact_attr_tables(dev, dtype):
     attrs = _attrs(g, n, c, 1, 1000, 0.1)
     sets = g.integers(0, 1000, (5, c, 3), dtype=np.int64)
     sets[g.random(sets.shape) < 0.6] = -1
-    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs.astype(dtype)),
+    bits = torch.ops.retrieve_amd.clause_bits(_t(dev, attrs.astype(dtype)),
                                           _t(dev, np.zeros(c, bool)), _t(dev, sets))
     assert np.array_equal(bits.cpu().numpy(), _pack(of.clause_match_sets(attrs, sets)))
     with pytest.raises(TypeError):
@@ -222,7 +222,7 @@ def test_large_and_negative_values(dev):
     sets[1, 0, 0] = 2500  # list rows
     sets[5, 2, 1] = -4
     rev = np.array([0, 1, 0, 0], bool)
-    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, sets))
+    bits = torch.ops.retrieve_amd.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, sets))
     assert np.array_equal(bits.cpu().numpy(), _pack(of.clause_match_sets(attrs, sets, rev)))
 
 
@@ -240,7 +240,7 @@ def test_row_groups_mixed_rows(dev, c, a):
     rev = (np.arange(c) % 3 == 1)
     want = of.clause_match_sets(attrs, sets, rev)
     pre = g.random((b, n)) < 0.7
-    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, sets),
+    bits = torch.ops.retrieve_amd.clause_bits(_t(dev, attrs), _t(dev, rev), _t(dev, sets),
                                           _t(dev, _pack(pre)))
     assert np.array_equal(bits.cpu().numpy(), _pack(want & pre))
     m = torch.ops.retrieve.clause_mask(_t(dev, attrs), _t(dev, rev), _t(dev, sets[:, :, 0]))
@@ -261,6 +261,6 @@ def test_wide_row_groups(dev, dtype):
     rev = np.array([0, 0, 1, 0, 1], bool)
     want = of.clause_match_sets(attrs, sets, rev)
     pre = g.random((b, n)) < 0.8
-    bits = torch.ops.retrieve.clause_bits(_t(dev, attrs.astype(dtype)), _t(dev, rev),
+    bits = torch.ops.retrieve_amd.clause_bits(_t(dev, attrs.astype(dtype)), _t(dev, rev),
                                           _t(dev, sets), _t(dev, _pack(pre)))
     assert np.array_equal(bits.cpu().numpy(), _pack(want & pre))

@@ -88,7 +88,7 @@ def _check_dense_large(dev, q32, it32, k, dtype, mask: PackedMask | None = None)
     qt = torch.from_numpy(q32).to(dev).to(dtype)
     it = torch.from_numpy(it32).to(dev).to(dtype)
     mt = None if mask is None else torch.from_numpy(mask.words.view(np.int64)).to(dev)
-    ids, sc = torch.ops.retrieve.dense_scan_topk(qt, it, k, mt)
+    ids, sc = torch.ops.retrieve_amd.dense_scan_topk(qt, it, k, mt)
     torch.cuda.synchronize()
     ids, sc = ids.cpu().numpy(), sc.cpu().numpy()
     qv = qt.float().cpu().numpy().astype(np.float64)
@@ -242,7 +242,7 @@ def _filter_mask(dev, attrs, sets):
     pre = torch.ops.st.bloom_index_search_batch_prepared(words, offs, blob, count, stack,
                                                          BLOOM_K, HASH_K)
     rev = torch.zeros(len(CARDINALITIES), dtype=torch.bool, device=dev)
-    final = torch.ops.retrieve.clause_bits(at.to(torch.int16), rev,
+    final = torch.ops.retrieve_amd.clause_bits(at.to(torch.int16), rev,
                                            torch.from_numpy(sets).to(dev), pre)
     torch.cuda.synchronize()
     return final, pre.cpu().numpy()
@@ -313,11 +313,11 @@ def test_config5_pipeline(dev):
     print(f"config 5 pipeline B={b} N={n}", flush=True)
     qb = torch.from_numpy(q_bits).to(dev)
     ib = torch.from_numpy(item_bits).to(dev)
-    ids1, s1 = torch.ops.retrieve.hamming_scan_topk(qb, ib, 1000, final)
+    ids1, s1 = torch.ops.retrieve_amd.hamming_scan_topk(qb, ib, 1000, final)
     counts = (ids1 >= 0).sum(1)
     qc = torch.from_numpy(q_codes).to(dev)
     ic = torch.from_numpy(item_codes).to(dev)
-    ids, sc = torch.ops.retrieve.int8_candidates_topk(qc, ic, ids1, counts, 100)
+    ids, sc = torch.ops.retrieve_amd.int8_candidates_topk(qc, ic, ids1, counts, 100)
     torch.cuda.synchronize()
     want1, want_s1 = osc.hamming_topk(q_bits, item_bits, 1000, valid)
     assert np.array_equal(ids1.cpu().numpy(), want1)

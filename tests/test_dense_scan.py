@@ -1,7 +1,7 @@
 """bf16 / fp16 dense full scan + top-k on the GPU against the float64 oracle: returned scores
 within 1e-3 relative of the float64 dot of the returned ids; ids equal to the exact top-k
 except inside a tolerance band around the k-th score (near-ties may swap); recall@k against
-exact scoring 1.0 on clustered data (``torch.ops.retrieve.dense_scan_topk``)."""
+exact scoring 1.0 on clustered data (``torch.ops.retrieve_amd.dense_scan_topk``)."""
 
 from __future__ import annotations
 
@@ -30,7 +30,7 @@ def _check(dev, q32, it32, k, dtype=torch.bfloat16, mask=None):
     qt = torch.from_numpy(q32).to(dev).to(dtype)
     it = torch.from_numpy(it32).to(dev).to(dtype)
     mt = None if mask is None else torch.from_numpy(_pack(mask)).to(dev)
-    ids, sc = torch.ops.retrieve.dense_scan_topk(qt, it, k, mt)
+    ids, sc = torch.ops.retrieve_amd.dense_scan_topk(qt, it, k, mt)
     torch.cuda.synchronize()
     ids, sc = ids.cpu().numpy(), sc.cpu().numpy()
     # exact scores of the values the kernel saw (the 16-bit roundings), in float64
@@ -142,11 +142,11 @@ def test_errors(dev):
     q = torch.zeros((2, 64), dtype=torch.bfloat16, device=dev)
     it = torch.zeros((10, 64), dtype=torch.bfloat16, device=dev)
     with pytest.raises(TypeError):
-        torch.ops.retrieve.dense_scan_topk(q.float(), it, 3)
+        torch.ops.retrieve_amd.dense_scan_topk(q.float(), it, 3)
     with pytest.raises(TypeError):
-        torch.ops.retrieve.dense_scan_topk(q, it.half(), 3)
+        torch.ops.retrieve_amd.dense_scan_topk(q, it.half(), 3)
     with pytest.raises(ValueError):
-        torch.ops.retrieve.dense_scan_topk(q[:, :32], it, 3)
+        torch.ops.retrieve_amd.dense_scan_topk(q[:, :32], it, 3)
 
 
 def test_large_batch_seeded_path(dev):

@@ -38,8 +38,8 @@ def test_bloom_no_false_negatives_30m(dev):
                                                          bench.BLOOM_K, bench.HASH_K)
     rev = torch.zeros(len(bench.CARDINALITIES), dtype=torch.bool, device=dev)
     qs = torch.from_numpy(sets).to(dev)
-    exact = torch.ops.retrieve.clause_bits(attrs, rev, qs)
-    both = torch.ops.retrieve.clause_bits(attrs, rev, qs, pre)
+    exact = torch.ops.retrieve_amd.clause_bits(attrs, rev, qs)
+    both = torch.ops.retrieve_amd.clause_bits(attrs, rev, qs, pre)
     nw = (n + 63) // 64
     # the search writes whole 2048-document bundles: words past the last document's are padding
     assert exact.shape == (b, nw) and pre.shape[0] == b and pre.shape[1] >= nw
@@ -47,8 +47,8 @@ def test_bloom_no_false_negatives_30m(dev):
     assert not (exact & ~pre).any()  # no false negatives
     assert torch.equal(both, exact)
     # the pre-filter passes a superset, and rejects most non-matching documents
-    counts = torch.ops.retrieve.mask_compact(exact, n)[1].double()
-    pcounts = torch.ops.retrieve.mask_compact(pre, n)[1].double()
+    counts = torch.ops.retrieve_amd.mask_compact(exact, n)[1].double()
+    pcounts = torch.ops.retrieve_amd.mask_compact(pre, n)[1].double()
     assert (pcounts >= counts).all() and (counts > 0).all()
     assert float((pcounts / n).max()) < 0.9
 
@@ -72,11 +72,11 @@ def _check_binary(dev, n, w, b, k, masked, n_sample, seed):
     q = torch.randint(-2**63, 2**63 - 1, (b, w), dtype=torch.int64, device=dev, generator=gen)
     if masked:
         valid = torch.rand((b, n), device=dev, generator=gen) < 0.1
-        words = torch.ops.retrieve.pack_mask(valid)
+        words = torch.ops.retrieve_amd.pack_mask(valid)
     else:
         valid = torch.ones((b, n), dtype=torch.bool, device=dev)
         words = None
-    ids, sc = torch.ops.retrieve.hamming_scan_topk(q, items, k, words)
+    ids, sc = torch.ops.retrieve_amd.hamming_scan_topk(q, items, k, words)
     torch.cuda.synchronize()
     assert (ids >= 0).all() and (ids < n).all()
     for r in range(b):

@@ -61,8 +61,8 @@ def test_filtered_int8_step(dev):
 
     def step():
         pre = torch.ops.st.bloom_index_search_batch_prepared(words, offs, blob, count, stack, 3, 7)
-        mask = torch.ops.retrieve.clause_bits(a16, rev, qs, pre)
-        return torch.ops.retrieve.int8_scan_topk(q, items, 100, mask)
+        mask = torch.ops.retrieve_amd.clause_bits(a16, rev, qs, pre)
+        return torch.ops.retrieve_amd.int8_scan_topk(q, items, 100, mask)
 
     print("graph: filtered int8 step B=16 N=2.2M", flush=True)
     _replays_match(step)
@@ -136,8 +136,8 @@ def test_dense_and_hamming_masked(dev):
     it = torch.from_numpy(g.standard_normal((n, 128)).astype(np.float32)).to(dev).bfloat16()
     mask = torch.from_numpy(_pack(g.random((256, n)) < 0.1)).to(dev)
     print("graph: masked bf16 B=256", flush=True)
-    _replays_match(lambda: torch.ops.retrieve.dense_scan_topk(q, it, 100, mask))
+    _replays_match(lambda: torch.ops.retrieve_amd.dense_scan_topk(q, it, 100, mask))
     qb = torch.from_numpy(g.integers(-(2**63), 2**63 - 1, (256, 8), dtype=np.int64)).to(dev)
     ib = torch.from_numpy(g.integers(-(2**63), 2**63 - 1, (n, 8), dtype=np.int64)).to(dev)
     print("graph: masked hamming B=256 k=1000", flush=True)
-    _replays_match(lambda: torch.ops.retrieve.hamming_scan_topk(qb, ib, 1000, mask))
+    _replays_match(lambda: torch.ops.retrieve_amd.hamming_scan_topk(qb, ib, 1000, mask))

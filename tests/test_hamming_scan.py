@@ -1,5 +1,5 @@
 """1-bit Hamming full scan + exact top-k on the GPU against the oracle (bit-exact integer
-scores and ids, ties to the lower index): ``torch.ops.retrieve.hamming_scan_topk`` and the
+scores and ids, ties to the lower index): ``torch.ops.retrieve_amd.hamming_scan_topk`` and the
 reference-schema ``torch.ops.retrieve.oporp_1bit_match_topk_full``."""
 
 from __future__ import annotations
@@ -25,7 +25,7 @@ def _check(dev, q, items, k, mask=None):
     qt = torch.from_numpy(q).to(dev)
     it = torch.from_numpy(items).to(dev)
     mt = None if mask is None else torch.from_numpy(_pack(mask)).to(dev)
-    ids, sc = torch.ops.retrieve.hamming_scan_topk(qt, it, k, mt)
+    ids, sc = torch.ops.retrieve_amd.hamming_scan_topk(qt, it, k, mt)
     torch.cuda.synchronize()
     want_ids, want_sc = osc.hamming_topk(q, items, k, mask)
     assert np.array_equal(sc.cpu().numpy(), want_sc)
@@ -38,7 +38,7 @@ def test_popcount_kat(dev, kat):
     a, _ = kat
     items = a["popcount_kat_in"].reshape(-1, 1)
     q = np.zeros((1, 1), np.int64)
-    ids, sc = torch.ops.retrieve.hamming_scan_topk(
+    ids, sc = torch.ops.retrieve_amd.hamming_scan_topk(
         torch.from_numpy(q).to(dev), torch.from_numpy(items).to(dev), items.shape[0]
     )
     got = dict(zip(ids[0].tolist(), sc[0].tolist()))
@@ -176,7 +176,7 @@ def test_oporp_full_schema(dev):
     it = torch.from_numpy(_codes(g, 5000, 8)).to(dev)
     ids, sc = torch.ops.retrieve.oporp_1bit_match_topk_full(q, it, 64)
     assert ids.dtype == torch.int64 and sc.dtype == torch.float32 and sc.shape == (4, 64)
-    ids2, sc2 = torch.ops.retrieve.hamming_scan_topk(q, it, 64)
+    ids2, sc2 = torch.ops.retrieve_amd.hamming_scan_topk(q, it, 64)
     assert torch.equal(ids, ids2) and torch.equal(sc, sc2.float())
     with pytest.raises(TypeError):
         torch.ops.retrieve.oporp_1bit_match_topk_full(q.int(), it, 3)

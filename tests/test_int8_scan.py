@@ -1,5 +1,5 @@
 """int8 full scan + exact top-k on the GPU against the oracle: bit-exact ids and int32 scores,
-ties to the lower index (``torch.ops.retrieve.int8_scan_topk`` through the C ABI)."""
+ties to the lower index (``torch.ops.retrieve_amd.int8_scan_topk`` through the C ABI)."""
 
 from __future__ import annotations
 
@@ -17,7 +17,7 @@ def _run(dev, q, items, k, mask=None):
     qt = torch.from_numpy(q).to(dev)
     it = torch.from_numpy(items).to(dev)
     mt = None if mask is None else torch.from_numpy(_pack(mask)).to(dev)
-    ids, sc = torch.ops.retrieve.int8_scan_topk(qt, it, k, mt)
+    ids, sc = torch.ops.retrieve_amd.int8_scan_topk(qt, it, k, mt)
     torch.cuda.synchronize()
     return ids.cpu().numpy(), sc.cpu().numpy()
 
@@ -139,8 +139,8 @@ def test_deterministic(dev):
     g = rng(15)
     q = torch.from_numpy(g.integers(-128, 128, (8, 512), dtype=np.int8)).to(dev)
     it = torch.from_numpy(g.integers(-128, 128, (100000, 512), dtype=np.int8)).to(dev)
-    a = torch.ops.retrieve.int8_scan_topk(q, it, 100)
-    b = torch.ops.retrieve.int8_scan_topk(q, it, 100)
+    a = torch.ops.retrieve_amd.int8_scan_topk(q, it, 100)
+    b = torch.ops.retrieve_amd.int8_scan_topk(q, it, 100)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
@@ -148,13 +148,13 @@ def test_errors(dev):
     q = torch.zeros((2, 64), dtype=torch.int8, device=dev)
     it = torch.zeros((10, 64), dtype=torch.int8, device=dev)
     with pytest.raises(TypeError):
-        torch.ops.retrieve.int8_scan_topk(q.float(), it, 3)
+        torch.ops.retrieve_amd.int8_scan_topk(q.float(), it, 3)
     with pytest.raises(ValueError):
-        torch.ops.retrieve.int8_scan_topk(q, it.t(), 3)
+        torch.ops.retrieve_amd.int8_scan_topk(q, it.t(), 3)
     with pytest.raises(ValueError):
-        torch.ops.retrieve.int8_scan_topk(q, it, 0)
+        torch.ops.retrieve_amd.int8_scan_topk(q, it, 0)
     with pytest.raises(ValueError):
-        torch.ops.retrieve.int8_scan_topk(q[:, :32], it[:, :32].contiguous(), 3)
+        torch.ops.retrieve_amd.int8_scan_topk(q[:, :32], it[:, :32].contiguous(), 3)
 
 
 def test_full_size_properties(dev):
@@ -164,7 +164,7 @@ def test_full_size_properties(dev):
     gen = torch.Generator(device=dev).manual_seed(21)
     items = torch.randint(-128, 128, (n, d), dtype=torch.int8, device=dev, generator=gen)
     q = torch.randint(-128, 128, (b, d), dtype=torch.int8, device=dev, generator=gen)
-    ids, sc = torch.ops.retrieve.int8_scan_topk(q, items, k)
+    ids, sc = torch.ops.retrieve_amd.int8_scan_topk(q, items, k)
     torch.cuda.synchronize()
     assert (ids >= 0).all() and (ids < n).all()
     for r in range(b):

@@ -112,6 +112,28 @@ def test_fp16_divisor_ties(dev):
     assert ix[0, :4].cpu().tolist() == [0, 1, 2, 3]
 
 
+def test_per_doc_scale_rounds_twice(dev):
+    """The per-doc fp16 scale branch is ``c10::Half(dot) / scale`` (``index_mm_helpers.cuh:
+    51-53``): the dot is rounded to fp16 before the division and the quotient again. Known
+    answers from IEEE half arithmetic: dot 2051 → fp16 2052 (a tie at spacing 2, to even), / 1.5
+    = 1368; dot 2053 → 2052, / 0.75 = 2736. Rounding once (Meta's CPU twin,
+    ``fused_kmean_ann.cpp:200-202``) gives 1367 and 2738 instead; this build follows the CUDA
+    op."""
+    d = 64
+    q = np.ones((1, d), np.int8)
+    emb = np.zeros((2, d), np.int8)
+    emb[:, :16] = 127  # 2032
+    emb[:, 16] = [19, 21]  # dots 2051, 2053
+    scale = np.array([1.5, 0.75], np.float16)
+    offsets = np.array([0, 2], np.int64)
+    sc, ix = torch.ops.st.fused_kmean_ann(_t(dev, offsets), _t(dev, np.zeros((1, 1), np.int64)),
+                                          _t(dev, np.array([[2]], np.int64)), _t(dev, emb),
+                                          _t(dev, q), 2, per_embedding_scale=_t(dev, scale))
+    assert sc.dtype == torch.float16
+    assert sc[0, :2].float().cpu().tolist() == [1368.0, 2736.0]
+    assert ix[0, :2].cpu().tolist() == [0, 1]
+
+
 @pytest.mark.parametrize("dtype,rtol", [(torch.bfloat16, 2.0**-7), (torch.float16, 2.0**-10),
                                         (torch.float32, 1e-5)])
 def test_float_raw_scores(dev, dtype, rtol):

@@ -47,7 +47,7 @@ def test_pack_mask_and_signs(dev):
 
     g = rng(1)
     valid = g.random((5, 1000)) < 0.4
-    words = _np(torch.ops.retrieve.pack_mask(_t(dev, valid)))
+    words = _np(torch.ops.retrieve_amd.pack_mask(_t(dev, valid)))
     bits = ((words.view(np.uint64)[:, :, None] >> np.arange(63, -1, -1, dtype=np.uint64)) & 1)
     assert np.array_equal(bits.reshape(5, -1)[:, :1000].astype(bool), valid)
     assert (bits.reshape(5, -1)[:, 1000:] == 0).all()
@@ -55,10 +55,10 @@ def test_pack_mask_and_signs(dev):
     x = g.standard_normal((37, 256)).astype(np.float32)
     x[0, :4] = [0.0, -0.0, np.nan, 1e-45]
     x[1] = 0.0
-    got = _np(torch.ops.retrieve.pack_signs(_t(dev, x)))
+    got = _np(torch.ops.retrieve_amd.pack_signs(_t(dev, x)))
     assert np.array_equal(got, oq.pack_signs(x))
     h = torch.from_numpy(x).to(dev).to(torch.float16)
-    assert np.array_equal(_np(torch.ops.retrieve.pack_signs(h)),
+    assert np.array_equal(_np(torch.ops.retrieve_amd.pack_signs(h)),
                           oq.pack_signs(h.float().cpu().numpy()))
 
 
@@ -68,7 +68,7 @@ def test_quantize_int8_op(dev):
     g = rng(2)
     x = (g.standard_normal((50, 96)) * np.exp(2 * g.standard_normal((50, 1)))).astype(np.float32)
     x[3] = 0.0
-    codes, scales = torch.ops.retrieve.quantize_int8(_t(dev, x))
+    codes, scales = torch.ops.retrieve_amd.quantize_int8(_t(dev, x))
     want_c, want_s = oq.quantize_int8(x, divide=True)
     assert np.array_equal(_np(codes), want_c)
     assert np.array_equal(_np(scales), want_s)
@@ -90,7 +90,7 @@ def test_quantize_int8_global_op(dev, n, d, offset):
     x = flat[offset:].reshape(n, d)
     perm = g.permutation(n)
     for rows in (None, perm):
-        codes, abs_max = torch.ops.retrieve.quantize_int8_global(
+        codes, abs_max = torch.ops.retrieve_amd.quantize_int8_global(
             xt, None if rows is None else _t(dev, rows))
         want_c, want_m = oq.quantize_int8_global(x, rows)
         assert np.array_equal(_np(codes), want_c)
@@ -133,7 +133,7 @@ def test_int8_rerank_topk(dev):
     cand[1, 100:] = -1
     cand[2, :] = -1
     gs = np.float32(0.0123)
-    ids, sc = torch.ops.retrieve.int8_rerank_topk(
+    ids, sc = torch.ops.retrieve_amd.int8_rerank_topk(
         _t(dev, q_codes), _t(dev, q_scales), _t(dev, codes), _t(dev, inv),
         _t(dev, np.array([gs], np.float32)), _t(dev, cand), k)
     want_ids, want_sc = _rerank_oracle(q_codes, q_scales, codes, inv, gs, cand, k)
@@ -165,7 +165,7 @@ def test_exact_attribute_filter(dev):
     assert np.array_equal(_np(f(qp)), want)
     assert np.array_equal(_np(f.evaluate_mask(qp, 100, 1333)), want[:, 100:1333])
     words = _np(f.mask_bits(qp))
-    assert np.array_equal(words, _np(torch.ops.retrieve.pack_mask(_t(dev, want))))
+    assert np.array_equal(words, _np(torch.ops.retrieve_amd.pack_mask(_t(dev, want))))
     ids, counts = f.evaluate_indices(qp)
     ids, counts = _np(ids), _np(counts)
     for r in range(b):
@@ -249,6 +249,64 @@ def test_prefilter_knn(dev):
     assert (_np(ids)[:, 7:] == -1).all()
     ids, sc = m(_t(dev, q))
     _dense_check(_np(ids), _np(sc), q16, i16, k)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("b", [3, 40])
+def test_full_scan_knn(dev, dtype, b):
+    """``FullScanKNN`` (``modules/knn.py:125-170``): the exact top k in the items' dtype; with a
+    mask the same ids with the failing hits tombstoned to -1 and every score kept (post-filter:
+    a failing hit is not replaced); candidates with -1 padding anywhere re-ranked to min(k, P)
+    columns. Scores are rounded once from fp32, so they sit within that dtype's rounding of the
+    float64 dot."""
+    from retrieve_amd.modules import FullScanKNN
+
+    print(f"FullScanKNN {dtype} B={b}", flush=True)
+    g = rng(13 + b)
+    n, d, k = 5000, 64, 30
+    rtol = {torch.float32: 1e-4, torch.float16: 2e-3, torch.bfloat16: 8e-3}[dtype]
+    m = FullScanKNN(k)
+    m.register_index(torch.from_numpy(g.standard_normal((n, d)).astype(np.float32)).to(dev)
+                     .to(dtype))
+    qt = torch.from_numpy(g.standard_normal((b, d)).astype(np.float32)).to(dev).to(dtype)
+    qv, iv = _np(qt.float()), _np(m.item_embs.float())
+    ids, sc = m(qt)
+    assert ids.shape == (b, k) and sc.dtype == dtype
+    _dense_check(_np(ids), _np(sc.float()), qv, iv, k, rtol=rtol)
+
+    valid = g.random((b, n)) < 0.5
+    ids_pf, sc_pf = m(qt, _t(dev, valid))
+    assert torch.equal(sc_pf, sc)
+    want = np.where(np.take_along_axis(valid, _np(ids), 1), _np(ids), -1)
+    assert np.array_equal(_np(ids_pf), want)
+
+    cand = np.stack([g.choice(n, 60, replace=False) for _ in range(b)]).astype(np.int64)
+    cand[g.random(cand.shape) < 0.3] = -1
+    cand[1] = -1  # a row with no candidates at all
+    exact = osc.dense_scores(qv, iv)
+    for p in (60, 7):
+        ids_c, sc_c = m(qt, candidate_ids=_t(dev, cand[:, :p]))
+        kk = min(k, p)
+        assert ids_c.shape == (b, kk) and sc_c.dtype == dtype
+        ids_c, sc_c = _np(ids_c), _np(sc_c.float())
+        for r in range(b):
+            c = cand[r, :p][cand[r, :p] >= 0]
+            mm = min(kk, c.size)
+            assert (ids_c[r, mm:] == -1).all() and np.isneginf(sc_c[r, mm:]).all()
+            got = ids_c[r, :mm]
+            assert len(set(got.tolist())) == mm and set(got.tolist()) <= set(c.tolist())
+            e = exact[r, got]
+            assert (np.abs(sc_c[r, :mm] - e) <= rtol * np.maximum(np.abs(e), 1e-3)).all()
+            if mm:
+                kth = np.sort(exact[r, c])[::-1][mm - 1]
+                assert (e >= kth - 2 * rtol * max(abs(kth), 1e-3)).all()
+
+    with pytest.raises(RuntimeError, match="same dtype"):
+        m(qt.to(torch.float64))
+    with pytest.raises(RuntimeError, match="out of range"):
+        big = FullScanKNN(n + 1)
+        big.register_index(m.item_embs)
+        big(qt)
 
 
 def _hamming_oracle(qbits, item_bits, k, valid=None):

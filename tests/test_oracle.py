@@ -431,3 +431,53 @@ def test_search_oracle_warps_then_remainders_by_hand():
     want1 = (list(range(40, 72)) + list(range(0, 32)) + list(range(90, 97)) + list(range(72, 90))
              + list(range(32, 40)))
     assert ids[1].tolist() == [1000 + p for p in want1]
+
+
+def test_fused_kmean_ann_per_doc_scale_rounds_twice():
+    """The per-doc fp16 scale branch restates ``c10::Half(dot) / scale``
+    (``index_mm_helpers.cuh:51-53``): fp16(fp32(fp16(dot)) / scale). Hand-computed from IEEE
+    half arithmetic: 2051 lies halfway between the fp16 values 2050 and 2052 (spacing 2 on
+    [2048, 4096)), so it rounds to the even significand, 2052, and 2052 / 1.5 = 1368 exactly;
+    2053 rounds to 2052 too, and 2052 / 0.75 = 2736. One rounding (fp16(2051 / 1.5) = 1367,
+    fp16(2053 / 0.75) = 2738, Meta's CPU twin ``fused_kmean_ann.cpp:200-202``) differs, so the
+    test tells the two apart."""
+    from oracle import silvertorch as ost
+
+    d = 64
+    q = np.ones((1, d), np.int8)
+    emb = np.zeros((2, d), np.int8)
+    emb[:, :16] = 127
+    emb[:, 16] = [19, 21]
+    assert (emb.astype(np.int64) @ q[0].astype(np.int64)).tolist() == [2051, 2053]
+    sc, ix = ost.fused_kmean_ann([0, 2], np.zeros((1, 1), np.int64), np.array([[2]]), emb, q, 2,
+                                 scale=np.array([1.5, 0.75], np.float16))
+    assert sc.dtype == np.float16
+    assert sc[0, :2].astype(np.float64).tolist() == [1368.0, 2736.0]
+    assert ix[0, :2].tolist() == [0, 1]
+    once = [float(np.float16(2051 / 1.5)), float(np.float16(2053 / 0.75))]
+    assert once == [1367.0, 2738.0]
+
+
+@pytest.mark.parametrize("k", [1, 7, 100, 1000, 3500])
+@pytest.mark.parametrize("kind", ["int", "float"])
+@pytest.mark.parametrize("n_base", [60, 700])
+def test_repeated_rows_topk_equals_topk_rows(k, kind, n_base):
+    """``RepeatedRows.topk`` (the GPU tests' oracle over tables of repeated base rows) equals
+    ``topk_rows`` over the expanded ``[B, N]`` scores: few distinct scores (ties across base rows
+    and, by construction, within every base row), masks with empty rows, k above N; 700 base
+    rows take the partial-selection path (more than its first 64 candidates, grown 4x)."""
+    g = rng(1200 + k + n_base)
+    n, b = 3000, 12
+    row_of = g.integers(0, n_base, n)
+    if kind == "int":
+        base = g.integers(-5, 5, (b, n_base)).astype(np.int32)
+    else:
+        base = (g.integers(-5, 5, (b, n_base)) * 0.25).astype(np.float32)
+    valid = g.random((b, n)) < 0.5
+    valid[3] = False
+    rep = osel.RepeatedRows(row_of, n_base)
+    for v in (None, valid):
+        want_i, want_s = osel.topk_rows(base[:, row_of], k, v)
+        for r in range(b):
+            got_i, got_s = rep.topk(base[r], k, None if v is None else v[r])
+            assert np.array_equal(got_i, want_i[r]) and np.array_equal(got_s, want_s[r])

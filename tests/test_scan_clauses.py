@@ -1,5 +1,5 @@
 """Full scans with the exact clause filter tested inside the scan
-(``torch.ops.retrieve.int8_scan_topk_clauses`` / ``dense_scan_topk_clauses`` through
+(``torch.ops.retrieve_amd.int8_scan_topk_clauses`` / ``dense_scan_topk_clauses`` through
 ``rt_scan_topk_clauses``) against the oracle: the int8 top-k over the items that pass
 ``oracle.filters.clause_match_sets`` (and the optional mask), bit for bit; the dense forms equal
 to the same kernel's scan over ``clause_bits``. Covers both set forms of the predicate (bitmaps for
@@ -60,7 +60,7 @@ def _int8_case(dev, g, b, n, d, k, c, a, v, vocab, rev, active_rate=0.5, attr_dt
     at = _t(dev, attrs.astype(attr_dtype))
     qt, it = _t(dev, q), _t(dev, items)
     mt = None if mask is None else _t(dev, _pack(mask))
-    ids, sc = torch.ops.retrieve.int8_scan_topk_clauses(qt, it, k, at, _t(dev, rev),
+    ids, sc = torch.ops.retrieve_amd.int8_scan_topk_clauses(qt, it, k, at, _t(dev, rev),
                                                         _t(dev, sets), mt)
     torch.cuda.synchronize()
     want_ids, want_sc = osc.int8_topk(q, items, k, valid)
@@ -114,9 +114,9 @@ def test_int8_equals_scan_over_clause_bits(dev):
         rev = _t(dev, np.array([0, 1, 0, 0, 0], bool))
         sets = _t(dev, _sets(g, b, 5, 3, 12, 0.6))
         print(f"int8 clause scan vs clause_bits B={b}", flush=True)
-        ids, sc = torch.ops.retrieve.int8_scan_topk_clauses(q, items, 100, attrs, rev, sets)
-        bits = torch.ops.retrieve.clause_bits(attrs, rev, sets)
-        want_ids, want_sc = torch.ops.retrieve.int8_scan_topk(q, items, 100, bits)
+        ids, sc = torch.ops.retrieve_amd.int8_scan_topk_clauses(q, items, 100, attrs, rev, sets)
+        bits = torch.ops.retrieve_amd.clause_bits(attrs, rev, sets)
+        want_ids, want_sc = torch.ops.retrieve_amd.int8_scan_topk(q, items, 100, bits)
         assert torch.equal(ids, want_ids) and torch.equal(sc, want_sc)
 
 
@@ -133,9 +133,9 @@ def test_dense_equals_scan_over_clause_bits(dev, dtype):
         sets_np = _sets(g, b, 3, 2, 10, 0.7)
         rev_np = np.array([0, 0, 1], bool)
         attrs, sets, rev = _t(dev, attrs_np.astype(np.int16)), _t(dev, sets_np), _t(dev, rev_np)
-        ids, sc = torch.ops.retrieve.dense_scan_topk_clauses(q, items, 100, attrs, rev, sets)
-        bits = torch.ops.retrieve.clause_bits(attrs, rev, sets)
-        want_ids, want_sc = torch.ops.retrieve.dense_scan_topk(q, items, 100, bits)
+        ids, sc = torch.ops.retrieve_amd.dense_scan_topk_clauses(q, items, 100, attrs, rev, sets)
+        bits = torch.ops.retrieve_amd.clause_bits(attrs, rev, sets)
+        want_ids, want_sc = torch.ops.retrieve_amd.dense_scan_topk(q, items, 100, bits)
         assert torch.equal(ids, want_ids) and torch.equal(sc, want_sc)
         valid = of.clause_match_sets(attrs_np, sets_np, rev_np)
         got = ids.cpu().numpy()
@@ -152,13 +152,13 @@ def test_empty_and_inactive_rows(dev):
     attrs0 = torch.zeros((0, 2, 1), dtype=torch.int16, device=dev)
     rev = _t(dev, np.zeros(2, bool))
     sets = _t(dev, np.full((2, 2, 1), -1, np.int64))
-    ids, sc = torch.ops.retrieve.int8_scan_topk_clauses(
+    ids, sc = torch.ops.retrieve_amd.int8_scan_topk_clauses(
         q, torch.zeros((0, 64), dtype=torch.int8, device=dev), 5, attrs0, rev, sets)
     assert (ids == -1).all() and (sc == torch.iinfo(torch.int32).min).all()
     items = _t(dev, g.integers(-128, 128, (3000, 64), dtype=np.int8))
     attrs = _t(dev, g.integers(0, 4, (3000, 2, 1)).astype(np.int16))
-    ids, sc = torch.ops.retrieve.int8_scan_topk_clauses(q, items, 50, attrs, rev, sets)
-    want_ids, want_sc = torch.ops.retrieve.int8_scan_topk(q, items, 50)
+    ids, sc = torch.ops.retrieve_amd.int8_scan_topk_clauses(q, items, 50, attrs, rev, sets)
+    want_ids, want_sc = torch.ops.retrieve_amd.int8_scan_topk(q, items, 50)
     assert torch.equal(ids, want_ids) and torch.equal(sc, want_sc)
 
 
@@ -168,14 +168,14 @@ def test_errors(dev):
     rev = torch.zeros(2, dtype=torch.bool, device=dev)
     sets = torch.full((2, 2, 1), -1, dtype=torch.int64, device=dev)
     with pytest.raises(ValueError):
-        torch.ops.retrieve.int8_scan_topk_clauses(
+        torch.ops.retrieve_amd.int8_scan_topk_clauses(
             q, items, 5, torch.zeros((99, 2, 1), dtype=torch.int16, device=dev), rev, sets)
     with pytest.raises(ValueError):
-        torch.ops.retrieve.int8_scan_topk_clauses(
+        torch.ops.retrieve_amd.int8_scan_topk_clauses(
             q, items, 5, torch.zeros((100, 2, 1), dtype=torch.int16, device=dev), rev,
             sets[:1])
     with pytest.raises(TypeError):
-        torch.ops.retrieve.int8_scan_topk_clauses(
+        torch.ops.retrieve_amd.int8_scan_topk_clauses(
             q, items, 5, torch.zeros((100, 2, 1), dtype=torch.float32, device=dev), rev, sets)
 
 
@@ -191,11 +191,11 @@ def test_opcheck(dev):
     ib = torch.randn((4000, 64), device=dev).bfloat16()
     qh = _t(dev, g.integers(-2**63, 2**63 - 1, (3, 8), dtype=np.int64))
     ih = _t(dev, g.integers(-2**63, 2**63 - 1, (4000, 8), dtype=np.int64))
-    for op, args in ((torch.ops.retrieve.int8_scan_topk_clauses.default,
+    for op, args in ((torch.ops.retrieve_amd.int8_scan_topk_clauses.default,
                       (q8, i8, 20, attrs, rev, sets)),
-                     (torch.ops.retrieve.dense_scan_topk_clauses.default,
+                     (torch.ops.retrieve_amd.dense_scan_topk_clauses.default,
                       (qb, ib, 20, attrs, rev, sets)),
-                     (torch.ops.retrieve.hamming_scan_topk_clauses.default,
+                     (torch.ops.retrieve_amd.hamming_scan_topk_clauses.default,
                       (qh, ih, 20, attrs, rev, sets))):
         print(f"opcheck {op}", flush=True)
         torch.library.opcheck(op, args)
@@ -212,7 +212,7 @@ def _as_transposed(mask: torch.Tensor) -> torch.Tensor:
 
 
 def _unfused(dev, op, q, items, k, attrs, rev, sets, mask):
-    bits = torch.ops.retrieve.clause_bits(attrs, rev, sets, mask)
+    bits = torch.ops.retrieve_amd.clause_bits(attrs, rev, sets, mask)
     return op(q, items, k, bits)
 
 
@@ -232,7 +232,7 @@ def test_blocked_int8_parity(dev, b, n, d, k, dense_mask):
     rev = np.array([0, 0, 1, 0], bool)
     mask = np.ones((b, n), bool) if dense_mask else g.random((b, n)) < 0.6
     valid = of.clause_match_sets(attrs, sets, rev) & mask
-    ids, sc = torch.ops.retrieve.int8_scan_topk_clauses(
+    ids, sc = torch.ops.retrieve_amd.int8_scan_topk_clauses(
         _t(dev, q), _t(dev, items), k, _t(dev, attrs.astype(np.int16)), _t(dev, rev),
         _t(dev, sets), _t(dev, _pack(mask)))
     want_ids, want_sc = osc.int8_topk(q, items, k, valid)
@@ -258,7 +258,7 @@ def test_blocked_adversarial_order(dev):
     valid = of.clause_match_sets(attrs, sets, rev)
     print(f"blocked int8 clause scan, rising scores B={b} N={n}", flush=True)
     for k in (100, 1000):
-        ids, sc = torch.ops.retrieve.int8_scan_topk_clauses(
+        ids, sc = torch.ops.retrieve_amd.int8_scan_topk_clauses(
             _t(dev, q), _t(dev, items), k, _t(dev, attrs.astype(np.int16)), _t(dev, rev),
             _t(dev, sets), _t(dev, _pack(mask)))
         want_ids, want_sc = osc.int8_topk(q, items, k, valid)
@@ -281,12 +281,12 @@ def test_blocked_dense_equals_unfused(dev, dtype, b, n, d):
     sets = _t(dev, _sets(g, b, 3, 3, 12, 0.7))
     rev = _t(dev, np.array([0, 1, 0], bool))
     mask = _t(dev, _pack(g.random((b, n)) < 0.5))
-    ids, sc = torch.ops.retrieve.dense_scan_topk_clauses(q, items, 100, attrs, rev, sets, mask)
-    want_ids, want_sc = _unfused(dev, torch.ops.retrieve.dense_scan_topk, q, items, 100, attrs,
+    ids, sc = torch.ops.retrieve_amd.dense_scan_topk_clauses(q, items, 100, attrs, rev, sets, mask)
+    want_ids, want_sc = _unfused(dev, torch.ops.retrieve_amd.dense_scan_topk, q, items, 100, attrs,
                                  rev, sets, mask)
     assert torch.equal(ids, want_ids) and torch.equal(sc, want_sc)
     # the same mask stored transposed
-    ids_t, sc_t = torch.ops.retrieve.dense_scan_topk_clauses(q, items, 100, attrs, rev, sets,
+    ids_t, sc_t = torch.ops.retrieve_amd.dense_scan_topk_clauses(q, items, 100, attrs, rev, sets,
                                                              _as_transposed(mask))
     assert torch.equal(ids_t, ids) and torch.equal(sc_t, sc)
 
@@ -307,16 +307,16 @@ def test_hamming_parity(dev, b, n, k, ones):
     mask = np.ones((b, n), bool) if ones else g.random((b, n)) < 0.5
     args = (_t(dev, attrs.astype(np.int16)), _t(dev, rev), _t(dev, sets), _t(dev, _pack(mask)))
     qt, it = _t(dev, q), _t(dev, items)
-    ids, sc = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args, fused=True)
-    ids2, sc2 = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args, fused=False)
+    ids, sc = torch.ops.retrieve_amd.hamming_scan_topk_clauses(qt, it, k, *args, fused=True)
+    ids2, sc2 = torch.ops.retrieve_amd.hamming_scan_topk_clauses(qt, it, k, *args, fused=False)
     assert torch.equal(ids, ids2) and torch.equal(sc, sc2)
     # the mask stored transposed (read directly by the blocked scan; copied elsewhere)
     args_t = args[:3] + (_as_transposed(args[3]),)
     for fused in (True, False):
-        ids3, sc3 = torch.ops.retrieve.hamming_scan_topk_clauses(qt, it, k, *args_t, fused=fused)
+        ids3, sc3 = torch.ops.retrieve_amd.hamming_scan_topk_clauses(qt, it, k, *args_t, fused=fused)
         assert torch.equal(ids, ids3) and torch.equal(sc, sc3)
     if n > 1_000_000:
-        want_ids, want_sc = _unfused(dev, torch.ops.retrieve.hamming_scan_topk, qt, it, k,
+        want_ids, want_sc = _unfused(dev, torch.ops.retrieve_amd.hamming_scan_topk, qt, it, k,
                                      *args)
         assert torch.equal(ids, want_ids) and torch.equal(sc, want_sc)
         return
@@ -351,7 +351,7 @@ def test_hamming_speculative_fallback(dev):
     mask = g.random((b, n)) < 0.5
     mask[0, :60] = True
     args = (_t(dev, attrs.astype(np.int16)), _t(dev, rev), _t(dev, sets), _t(dev, _pack(mask)))
-    ids, sc = torch.ops.retrieve.hamming_scan_topk_clauses(_t(dev, q), _t(dev, items), k, *args,
+    ids, sc = torch.ops.retrieve_amd.hamming_scan_topk_clauses(_t(dev, q), _t(dev, items), k, *args,
                                                            fused=True)
     valid = of.clause_match_sets(attrs, sets, rev) & mask
     want_ids, want_sc = osc.hamming_topk(q, items, k, valid)
