@@ -284,21 +284,61 @@ def latency_windows(step, windows: int, calls: int, b: int, mode: str, warmup: i
     return d
 
 
-def graph_step(step):
-    """The step captured once in a HIP graph (the ops enqueue on torch's current stream with no
-    host sync and no memset); returns a callable that replays it: the reference's ``graph``
-    mode, one graph launch per call."""
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        step()
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    torch.cuda.synchronize()
-    return graph.replay
+GRAPH_LAUNCH_EVENTS = ("cudaGraphLaunch", "hipGraphLaunch")
+
+
+class NotCapturable(RuntimeError):
+    """The step does not compile to one graph launch per call."""
+
+
+def mark_static(fn) -> None:
+    """Mark the device tensors a step closure reads (directly, or as attributes of an object it
+    holds) as static addresses, so the compiled graph reads them in place instead of copying
+    them into its input buffers before every replay (a module's buffers, as the reference's
+    tables are, are static already)."""
+    seen: set[int] = set()
+
+    def visit(obj, depth):
+        if isinstance(obj, torch.Tensor):
+            if obj.is_cuda and id(obj) not in seen:
+                seen.add(id(obj))
+                torch._dynamo.mark_static_address(obj)
+        elif depth == 0 and hasattr(obj, "__dict__") and not isinstance(obj, torch.nn.Module):
+            for v in vars(obj).values():
+                visit(v, 1)
+
+    for cell in getattr(fn, "__closure__", None) or ():
+        visit(cell.cell_contents, 0)
+
+
+def graph_callable(fn, *example_args, warmup: int = 5):
+    """The reference harness's ``graph`` mode (``evaluation/bench/measure.py:348-373``):
+    ``torch.compile(fn, mode="reduce-overhead", dynamic=False, fullgraph=True)`` warmed on
+    ``example_args`` under ``inference_mode``; raises ``NotCapturable`` unless the warm-up
+    caused no cudagraph skip and one call is exactly one graph launch. Call the result under
+    ``torch.inference_mode()`` too (the mode it was captured in)."""
+    from torch._dynamo.utils import counters
+    from torch.profiler import ProfilerActivity, profile
+
+    mark_static(fn)
+    skips_before = int(counters["inductor"]["cudagraph_skips"])
+    compiled = torch.compile(fn, mode="reduce-overhead", dynamic=False, fullgraph=True)
+    with torch.inference_mode():
+        for _ in range(warmup):
+            compiled(*example_args)
+        torch.cuda.synchronize()
+        skips = int(counters["inductor"]["cudagraph_skips"]) - skips_before
+        if skips:
+            raise NotCapturable(f"cudagraph_skips={skips}")
+        with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+            compiled(*example_args)
+            torch.cuda.synchronize()
+    events = prof.key_averages()
+    launches = sum(e.count for e in events if e.key in GRAPH_LAUNCH_EVENTS)
+    if launches != 1:
+        seen = sorted({e.key for e in events if "raph" in e.key})
+        raise NotCapturable(f"graph launches per call = {launches}, expected 1 ({seen})")
+    return compiled
 
 
 def main() -> int:
@@ -334,7 +374,9 @@ def main() -> int:
     ap.add_argument("--window-calls", type=int, default=0,
                     help="calls per latency window (default: 2 s worth, clamped to 1000-5000)")
     ap.add_argument("--mode", choices=("eager", "graph"), default="eager",
-                    help="graph: time replays of the step captured in a HIP graph")
+                    help="graph: time calls of the step compiled with torch.compile("
+                         "mode='reduce-overhead', fullgraph=True), gated as the reference "
+                         "harness gates it (no cudagraph skip, one graph launch per call)")
     ap.add_argument("--jsonl", default=None,
                     help="append the latency record (reference harness fields) to this file")
     ap.add_argument("--copy-probe", action="store_true",
@@ -618,10 +660,20 @@ def main() -> int:
     total_ms = ctypes.c_double()
     launches = ctypes.c_int64()
     if args.mode == "graph":
-        # the timed steps replay one capture; the main scan's HIP-event time comes from as many
-        # eager steps right after (events are not recorded inside the capture)
-        step = graph_step(step)
-        log(f"timing {args.steps} graph replays")
+        # the timed steps are calls of the compiled step, one graph launch each (the reference
+        # harness's gate); the main scan's HIP-event time comes from as many eager steps right
+        # after (events are not recorded inside the graph)
+        log("compiling the step: torch.compile(mode='reduce-overhead', fullgraph=True)")
+        compiled = graph_callable(step)
+
+        def step():
+            with torch.inference_mode():
+                return compiled()
+
+        for _ in range(max(args.warmup, 3)):  # the compiled calls' own first-call costs
+            step()
+        torch.cuda.synchronize()
+        log(f"timing {args.steps} compiled calls")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):

@@ -236,14 +236,19 @@ def _search_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max
                          int(hash_k), bool(return_bool_mask))
 
 
-def bloom_search_t(bloom_index: Tensor, bloom_bundle_b_offsets: Tensor, plans: Tensor,
-                   plan_count: int, max_stack_size: int, k: int, hash_k: int) -> Tensor:
-    """``bloom_index_search_batch_prepared``'s words (``return_bool_mask=False``) stored
-    transposed: a ``[plan_count, nb * 32]`` view with strides ``(1, S)`` over ``[nb * 32, S]``
-    words, S = plan_count rounded up to 256 (``rt_bloom_search_t``). The values are the same;
-    the blocked scans (``dense_scan_topk_clauses``, ``hamming_scan_topk_clauses`` at their
-    blocked batches) read this layout directly instead of transposing the mask per call, and
-    any other consumer sees an ordinary strided tensor. No counterpart in the reference."""
+def _transposed_shape(offsets: Tensor, plan_count: int) -> tuple[int, int]:
+    """``(nb * 32 columns, S)``: S = plan_count rounded up to 256 (at least 256)."""
+    cols = max(offsets.shape[0] - 1, 0) * WORDS_PER_BUNDLE
+    return cols, max(-(-plan_count // 256) * 256, 256)
+
+
+@torch.library.custom_op("retrieve_amd::bloom_search_cols", mutates_args=(),
+                         device_types="cuda")
+def bloom_search_cols(bloom_index: Tensor, bloom_bundle_b_offsets: Tensor, plans: Tensor,
+                      plan_count: int, max_stack_size: int, k: int, hash_k: int) -> Tensor:
+    """The Bloom search's words column-major: ``[nb * 32, S]`` int64, column ``c`` of plan ``b``
+    at ``[c, b]`` (``rt_bloom_search_t``); entries ``[:, plan_count:]`` are not written. Use
+    ``bloom_search_t`` for the ``[plan_count, nb * 32]`` view."""
     if plans.dtype != torch.int64 or plans.dim() != 1 or plans.numel() < 8 * plan_count:
         raise ValueError("plans must be int64 [8 * plan_count + data words]")
     if max_stack_size > MAX_STACK:
@@ -256,12 +261,10 @@ def bloom_search_t(bloom_index: Tensor, bloom_bundle_b_offsets: Tensor, plans: T
         raise TypeError("bloom_index and bloom_bundle_b_offsets must be int64")
     data = plans[8 * plan_count :]
     nb = offsets.numel() - 1
-    cols = max(nb, 0) * WORDS_PER_BUNDLE
-    stride = max(-(-plan_count // 256) * 256, 256)
+    cols, stride = _transposed_shape(offsets, plan_count)
     out = torch.empty((cols, stride), dtype=torch.int64, device=dev)
-    view = out.t()[:plan_count]
     if plan_count == 0 or nb <= 0:
-        return view
+        return out
     lib = nat.lib()
     ws = nat.workspace(lib.rt_bloom_search_workspace(data.numel() * 8, plan_count), dev)
     with torch.cuda.device(dev):
@@ -271,7 +274,25 @@ def bloom_search_t(bloom_index: Tensor, bloom_bundle_b_offsets: Tensor, plans: T
             nat.ptr(out), stride, nat.ptr(ws), ws.numel(), nat.stream(dev),
         )
     nat.check(st)
-    return view
+    return out
+
+
+@bloom_search_cols.register_fake
+def _(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max_stack_size, k, hash_k):
+    return bloom_index.new_empty(_transposed_shape(bloom_bundle_b_offsets, plan_count))
+
+
+def bloom_search_t(bloom_index: Tensor, bloom_bundle_b_offsets: Tensor, plans: Tensor,
+                   plan_count: int, max_stack_size: int, k: int, hash_k: int) -> Tensor:
+    """``bloom_index_search_batch_prepared``'s words (``return_bool_mask=False``) stored
+    transposed: a ``[plan_count, nb * 32]`` view with strides ``(1, S)`` over ``[nb * 32, S]``
+    words, S = plan_count rounded up to 256 (``bloom_search_cols``). The values are the same;
+    the blocked scans (``dense_scan_topk_clauses``, ``hamming_scan_topk_clauses`` at their
+    blocked batches) read this layout directly instead of transposing the mask per call, and
+    any other consumer sees an ordinary strided tensor. (A view of the op's output, so it
+    traces under ``torch.compile``.) No counterpart in the reference."""
+    return bloom_search_cols(bloom_index, bloom_bundle_b_offsets, plans, plan_count,
+                             max_stack_size, k, hash_k).t()[:plan_count]
 
 
 def _search_batch(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data,

@@ -39,14 +39,15 @@ EXTRAS = (
     "int8_scan_topk", "int8_scan_topk_clauses", "dense_scan_topk", "dense_scan_topk_clauses",
     "hamming_scan_topk", "hamming_scan_topk_clauses", "clause_bits", "mask_compact",
     "int8_candidates_topk", "int8_rerank_topk", "quantize_int8", "quantize_int8_global",
-    "pack_mask", "pack_signs",
+    "pack_mask", "pack_signs", "bloom_search_cols",
 )
 
 
 def _schemas(ns: str) -> dict:
     import torch
 
-    import retrieve_amd.hip  # noqa: F401  (registers both namespaces)
+    import retrieve_amd.hip  # noqa: F401  (registers torch.ops.retrieve / retrieve_amd)
+    import retrieve_amd.st  # noqa: F401  (registers torch.ops.st and the transposed search)
 
     pre = ns + "::"
     return {s.name.removeprefix(pre): s for s in torch._C._jit_get_all_schemas()
