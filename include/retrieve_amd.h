@@ -274,6 +274,37 @@ int rt_bloom_search_t(const uint64_t* words, const int64_t* bundle_b_offsets, in
                       uint64_t* out_mask_t, int64_t out_t_stride, void* workspace,
                       size_t workspace_bytes, rt_stream_t stream);
 
+/* The search in two parts, so a batch's plans are compiled once (as the reference prepares them
+ * once outside the forward, retrieve/src/retrieve/ops/official/adapter.py:184-236) and searched
+ * any number of times. rt_bloom_compile writes every plan's folded program (or its stack-path /
+ * no-match status) into `compiled` (rt_bloom_compiled_bytes(plan_count) bytes; the programs
+ * depend on the plans, k, hash_k, max_stack and the width of bundle 0, nothing else of the
+ * index). rt_bloom_search_compiled then searches, writing out_mask ([plan_count, nb * 32]) or
+ * out_mask_t (rt_bloom_search_t's layout), exactly the words rt_bloom_search writes.
+ * Clause mode (n_clauses in [1, 128]; 0: every plan runs its program): plans that are an AND of
+ * clauses (a clause: an OR of terms, a term, or the NOT of either) over the batch's n_clauses
+ * distinct clauses. Clause c is the OR of its terms, entries clause_ptr[c] .. clause_ptr[c + 1]
+ * of clause_terms (4 words each: the term's program word pair, the index of its hash_k stored
+ * hashes in plan_data as uint64 words, low and high). plan_desc[b]: bit 31 set for such a plan,
+ * bits 12-30 its first entry in plan_refs, bits 0-11 its count; plan_refs: bits 0-14 a clause,
+ * bit 15 its NOT. The column kernel evaluates each distinct clause once per column and such a
+ * plan is the AND of its clauses' words; retrieve_amd/st.py's clause pass writes the tables.
+ * Replaces: st::bloom_index_search_batch_prepared (silvertorch/.../bloom_index_search.cpp:
+ *   576-590) split at its plan preparation; no separate counterpart in the reference. */
+size_t rt_bloom_compiled_bytes(int64_t plan_count);
+int rt_bloom_compile(const int64_t* bundle_b_offsets, int64_t n_bundles,
+                     const int64_t* plan_offsets, const int8_t* plan_data, int64_t data_bytes,
+                     int64_t plan_count, int64_t max_stack, int64_t k, int64_t hash_k,
+                     void* compiled, size_t compiled_bytes, rt_stream_t stream);
+int rt_bloom_search_compiled(const uint64_t* words, const int64_t* bundle_b_offsets,
+                             int64_t n_bundles, const int64_t* plan_offsets,
+                             const int8_t* plan_data, int64_t data_bytes, int64_t plan_count,
+                             int64_t max_stack, int64_t k, int64_t hash_k, const void* compiled,
+                             size_t compiled_bytes, const uint32_t* clause_ptr,
+                             const uint32_t* clause_terms, const uint32_t* plan_desc,
+                             const uint32_t* plan_refs, int64_t n_clauses, int64_t* out_mask,
+                             uint64_t* out_mask_t, int64_t out_t_stride, rt_stream_t stream);
+
 /* The Bloom plans over the probed clusters' columns only: probed cluster i (row i / per_row of a
  * [rows, per_row] probe table) starts at doc position cluster_starts[i] and spans
  * column_counts_cumsum[i] - column_counts_cumsum[i - 1] columns (inclusive int32 cumsum) from

@@ -180,6 +180,13 @@ struct BloomSearchArgs {
   bool words_aligned16;
   const int32_t* hdr;    // [plan_count, 4] from the prep pass: PlanStatus, ops, hash word 0
   const uint32_t* prog;   // [plan_count, kProgMaxOps, 2] program words
+  // clause mode (see "Clauses" below): the batch's distinct clauses and the plans over them
+  const uint32_t* clause_ptr;    // [n_clauses + 1]: clause c's terms are entries [ptr[c], ptr[c+1])
+  const uint32_t* clause_terms;  // [*, 4]: a term's program word pair, its hashes' index lo / hi
+  const uint32_t* plan_desc;     // [plan_count]: bit 31 a clause plan, bits 12-30 its first
+                                 // ref, bits 0-11 its ref count; 0: the plan runs its program
+  const uint32_t* plan_refs;     // bits 0-14 a clause, bit 15 NOT
+  int n_clauses;                 // 0: every plan runs its program
   int64_t* out_mask;      // [plan_count, nb * 32] or null
   uint8_t* out_bool;      // [plan_count, nb * 32 * 64] or null
   uint64_t* out_mask_t;   // [nb * 32, out_t_stride]: the words transposed, or null
@@ -267,10 +274,18 @@ __device__ inline void write_column(const BloomSearchArgs& a, int64_t b, int64_t
 //   word 1: bits 0-13 offset 2; bits 16-29 offset 3
 // Plans the program cannot hold (more than kFoldDepth levels, more than 4 positions a term,
 // bundle 0 wider than 64 bits, more than kProgMaxOps ops) are left to the stack evaluation.
+//
+// Clauses: a batch's plans are mostly ANDs of value-set clauses (an OR of terms, a term, or the
+// NOT of either), and plans repeat clauses (a popular value set). A host pass over the compiled
+// programs (retrieve_amd/st.py) finds the plans of that form and the batch's distinct clauses
+// (the same set of stored hash lists: the same word in every column, whatever the bundle's
+// width). The column kernel's CLAUSES form evaluates each distinct clause once per column into
+// LDS, and such a plan is the AND of a few LDS words; the other plans run their programs.
 constexpr int kFoldDepth = 4;
 constexpr int kProgMaxPos = 4;
 constexpr int kColMaxWidth = 64;
 constexpr int kProgMaxOps = 2048;
+constexpr int kMaxClauses = 128;  // LDS: 128 clauses x 64 columns x 8 bytes beside the staging
 constexpr int kPrepThreads = 256;
 constexpr uint32_t kColPosBytes = kBloomWordsPerBundle * sizeof(uint64_t);  // 256
 
@@ -693,12 +708,13 @@ __device__ inline uint64_t run_program(const BloomSearchArgs& a, gu32* prog, uin
 
 // KK = min(k, hash_k): the positions every term's program words carry. THREADS: 256, or 512
 // when a workgroup has many plans (its bundles' staging then feeds twice the waves).
-template <int KK, int THREADS>
+template <int KK, int THREADS, bool CLAUSES>
 __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a) {
   constexpr int kColThreads = THREADS;
   constexpr int kColWaves = THREADS / kWave;
   __shared__ uint64_t idx[2 * kColMaxWidth * kBloomWordsPerBundle];
   __shared__ uint64_t fold[kColWaves][kFoldDepth - 1][kWave];
+  extern __shared__ uint64_t clause_words[];  // CLAUSES: [a.n_clauses][64 columns]
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -780,6 +796,29 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
   const int64_t my_w = valid ? (half == 0 ? off[1] - off[0] : off[2] - off[1]) : 0;
   const uint64_t* wcol = a.words + my_off * kBloomWordsPerBundle + j;
   uint64_t(&stk)[kFoldDepth - 1][kWave] = fold[wave];
+  const uint64_t* clause_col = clause_words + lane;
+  if constexpr (CLAUSES) {
+    // the batch's distinct clauses, each once per column (an OR of its terms: from the staged
+    // positions, or for a bundle of another width from the terms' stored hashes)
+    const int n_clauses = __builtin_amdgcn_readfirstlane(a.n_clauses);
+    for (int c = wave; c < n_clauses; c += kColWaves) {
+      const int t0 = __builtin_amdgcn_readfirstlane(a.clause_ptr[c]);
+      const int t1 = __builtin_amdgcn_readfirstlane(a.clause_ptr[c + 1]);
+      uint64_t v = 0ull;
+      for (int t = t0; t < t1; ++t) {
+        const uint32_t* e = a.clause_terms + 4 * static_cast<int64_t>(t);
+        const uint32_t p0 = __builtin_amdgcn_readfirstlane(e[0]);
+        const uint32_t p1 = __builtin_amdgcn_readfirstlane(e[1]);
+        const int64_t hidx = static_cast<int64_t>(
+            (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(e[3])) << 32) |
+            __builtin_amdgcn_readfirstlane(e[2]));
+        v |= mine_staged ? staged_term<KK>(lcol, p0, p1)
+                         : term_from_hashes(a, hidx, 0, wcol, my_w);
+      }
+      clause_words[c * kWave + lane] = v;
+    }
+    __syncthreads();
+  }
 
   const int64_t b0 = static_cast<int64_t>(blockIdx.y) * a.plans_per_wg;
   const int64_t b1 = b0 + a.plans_per_wg < a.plan_count ? b0 + a.plans_per_wg : a.plan_count;
@@ -808,6 +847,22 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
       h_next = hdrs[nb];
       lo_next = progs[nb * kProgMaxOps * 2 + 2 * lane];
       hi_next = progs[nb * kProgMaxOps * 2 + 2 * lane + 1];
+    }
+    if constexpr (CLAUSES) {
+      // a plan of clauses: the AND of its clauses' words (NOT: inverted)
+      const uint32_t desc = __builtin_amdgcn_readfirstlane(a.plan_desc[b]);
+      if (desc >> 31) {
+        const uint32_t* refs = a.plan_refs + ((desc >> 12) & 0x7ffffu);
+        const int cnt = static_cast<int>(desc & 0xfffu);
+        uint64_t top = ~0ull;
+        for (int r = 0; r < cnt; ++r) {
+          const uint32_t ref = __builtin_amdgcn_readfirstlane(refs[r]);
+          const uint64_t w = clause_col[(ref & 0x7fffu) * kWave];
+          top &= (ref & 0x8000u) != 0u ? ~w : w;
+        }
+        if (valid) write_column(a, b, ncol, col, top);
+        continue;
+      }
     }
     const int32_t st = __builtin_amdgcn_readfirstlane(h[0]);
     if (st == kPlanStack) continue;  // the stack evaluation writes it
@@ -1024,13 +1079,13 @@ extern "C" size_t rt_bloom_search_workspace(int64_t data_bytes, int64_t plan_cou
          align_up(static_cast<size_t>(plans) * kProgMaxOps * 2 * sizeof(uint32_t), 256);
 }
 
-// The search behind rt_bloom_search and rt_bloom_search_t: any of the three outputs.
-static int bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, int64_t n_bundles,
-                        const int64_t* plan_offsets, const int8_t* plan_data, int64_t data_bytes,
-                        int64_t plan_count, int64_t max_stack, int64_t k, int64_t hash_k,
-                        int64_t* out_mask, uint8_t* out_bool, uint64_t* out_mask_t,
-                        int64_t out_t_stride, void* workspace, size_t workspace_bytes,
-                        hipStream_t stream) {
+extern "C" size_t rt_bloom_compiled_bytes(int64_t plan_count) {
+  return rt_bloom_search_workspace(0, plan_count);
+}
+
+// The checks every search makes of its plans and sizes.
+static int bloom_check(int64_t n_bundles, const int8_t* plan_data, int64_t data_bytes,
+                       int64_t plan_count, int64_t max_stack, int64_t k, int64_t hash_k) {
   RT_CHECK_ARG(n_bundles >= 0 && plan_count >= 0 && data_bytes >= 0, "sizes must be >= 0");
   RT_CHECK_ARG(k >= 1 && k <= kBloomMaxK, "k must be in [1, %d], got %lld", kBloomMaxK,
                static_cast<long long>(k));
@@ -1039,20 +1094,17 @@ static int bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, 
   RT_CHECK_ARG(max_stack >= 1 && max_stack <= kBloomMaxStack,
                "max_stack_size must be in [1, %d], got %lld", kBloomMaxStack,
                static_cast<long long>(max_stack));
-  RT_CHECK_ARG(out_mask != nullptr || out_bool != nullptr || out_mask_t != nullptr, "no output");
-  RT_CHECK_ARG(out_mask_t == nullptr || out_t_stride >= plan_count,
-               "the transposed output's stride must be >= plan_count");
   RT_CHECK_ARG(reinterpret_cast<uintptr_t>(plan_data) % 8 == 0, "plan data must be 8-aligned");
   RT_CHECK_ARG(plan_count <= (int64_t{1} << 31) - 1, "too many plans");
-  if (n_bundles == 0 || plan_count == 0) return kOk;
-  const size_t need = rt_bloom_search_workspace(data_bytes, plan_count);
-  if (workspace_bytes < need) {
-    set_error("workspace too small: %zu < %zu", workspace_bytes, need);
-    return kWorkspaceTooSmall;
-  }
-  int32_t* hdr = static_cast<int32_t*>(workspace);
-  uint32_t* prog = reinterpret_cast<uint32_t*>(
-      static_cast<char*>(workspace) + align_up(static_cast<size_t>(plan_count) * 16, 256));
+  return kOk;
+}
+
+// The plans' shared fields; hdr / prog point into a compiled buffer (header, then programs).
+static BloomSearchArgs bloom_args(const uint64_t* words, const int64_t* bundle_b_offsets,
+                                  int64_t n_bundles, const int64_t* plan_offsets,
+                                  const int8_t* plan_data, int64_t data_bytes,
+                                  int64_t plan_count, int64_t max_stack, int64_t k,
+                                  int64_t hash_k, void* compiled) {
   BloomSearchArgs a{};
   a.words = words;
   a.bundle_off = bundle_b_offsets;
@@ -1065,15 +1117,54 @@ static int bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, 
   a.k = static_cast<int>(k);
   a.hash_k = static_cast<int>(hash_k);
   a.words_aligned16 = reinterpret_cast<uintptr_t>(words) % 16 == 0;
-  a.hdr = hdr;
-  a.prog = prog;
-  a.out_mask = out_mask;
-  a.out_bool = out_bool;
-  a.out_mask_t = out_mask_t;
-  a.out_t_stride = out_t_stride;
-  bloom_prep_kernel<<<static_cast<unsigned>(plan_count), kPrepThreads, 0, stream>>>(a, hdr,
-                                                                                     prog);
+  a.hdr = static_cast<int32_t*>(compiled);
+  a.prog = reinterpret_cast<uint32_t*>(
+      static_cast<char*>(compiled) + align_up(static_cast<size_t>(plan_count) * 16, 256));
+  return a;
+}
+
+// The column kernel for KK positions a term, 4 or 8 waves, with the shared terms' LDS.
+template <int KK, bool CLAUSES>
+static int launch_column(const BloomSearchArgs& a, dim3 grid, int waves, size_t lds,
+                         hipStream_t stream) {
+  const void* fn = waves == 8
+                       ? reinterpret_cast<const void*>(&bloom_column_kernel<KK, 512, CLAUSES>)
+                       : reinterpret_cast<const void*>(&bloom_column_kernel<KK, 256, CLAUSES>);
+  if (lds > 0) {
+    RT_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds)));
+  }
+  if (waves == 8) {
+    bloom_column_kernel<KK, 512, CLAUSES><<<grid, 512, lds, stream>>>(a);
+  } else {
+    bloom_column_kernel<KK, 256, CLAUSES><<<grid, 256, lds, stream>>>(a);
+  }
   RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+// The prep pass: each plan's program (or its stack-path / no-match status) into `a`'s buffers.
+static int bloom_compile_into(const BloomSearchArgs& a, hipStream_t stream) {
+  bloom_prep_kernel<<<static_cast<unsigned>(a.plan_count), kPrepThreads, 0, stream>>>(
+      a, const_cast<int32_t*>(a.hdr), const_cast<uint32_t*>(a.prog));
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+// The searches over compiled plans: the column kernel (programs; with a.n_clauses > 0 the
+// plans of clauses over the batch's distinct clauses)// terms), then the stack evaluation of the rest; any of the three outputs.
+static int bloom_run(BloomSearchArgs a, hipStream_t stream) {
+  const int64_t n_bundles = a.nb;
+  const int64_t plan_count = a.plan_count;
+  const int64_t kk = a.k < a.hash_k ? a.k : a.hash_k;  // > kProgMaxPos: the stack path only
+  const int64_t n_clauses = a.n_clauses;
+  RT_CHECK_ARG(n_clauses >= 0 && n_clauses <= kMaxClauses,
+               "clauses must be in [0, %d], got %lld", kMaxClauses,
+               static_cast<long long>(n_clauses));
+  RT_CHECK_ARG(n_clauses == 0 || (kk <= kProgMaxPos && a.clause_ptr != nullptr &&
+                                  a.clause_terms != nullptr && a.plan_desc != nullptr &&
+                                  a.plan_refs != nullptr),
+               "clauses need at most %d positions a term and their tables", kProgMaxPos);
 
   // column kernel: two bundles per workgroup, plans split over y when that gives too few
   const int64_t cx = cdiv(n_bundles, 2);
@@ -1087,33 +1178,28 @@ static int bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, 
   a.plans_per_wg = cdiv(plan_count, cy);
   cy = cdiv(plan_count, a.plans_per_wg);
   const dim3 cgrid(static_cast<unsigned>(cx), static_cast<unsigned>(cy));
-  const int64_t kk = k < hash_k ? k : hash_k;  // > kProgMaxPos: every plan takes the stack path
-  if (kk == 1) {
-    if (col_waves == 8) {
-      bloom_column_kernel<1, 512><<<cgrid, 512, 0, stream>>>(a);
+  const size_t lds = static_cast<size_t>(n_clauses) * kWave * sizeof(uint64_t);
+  int st = kOk;
+  if (n_clauses > 0) {  // (kk <= kProgMaxPos, checked above)
+    if (kk == 1) {
+      st = launch_column<1, true>(a, cgrid, col_waves, lds, stream);
+    } else if (kk == 2) {
+      st = launch_column<2, true>(a, cgrid, col_waves, lds, stream);
+    } else if (kk == 3) {
+      st = launch_column<3, true>(a, cgrid, col_waves, lds, stream);
     } else {
-      bloom_column_kernel<1, 256><<<cgrid, 256, 0, stream>>>(a);
+      st = launch_column<4, true>(a, cgrid, col_waves, lds, stream);
     }
+  } else if (kk == 1) {
+    st = launch_column<1, false>(a, cgrid, col_waves, 0, stream);
   } else if (kk == 2) {
-    if (col_waves == 8) {
-      bloom_column_kernel<2, 512><<<cgrid, 512, 0, stream>>>(a);
-    } else {
-      bloom_column_kernel<2, 256><<<cgrid, 256, 0, stream>>>(a);
-    }
+    st = launch_column<2, false>(a, cgrid, col_waves, 0, stream);
   } else if (kk == 3) {
-    if (col_waves == 8) {
-      bloom_column_kernel<3, 512><<<cgrid, 512, 0, stream>>>(a);
-    } else {
-      bloom_column_kernel<3, 256><<<cgrid, 256, 0, stream>>>(a);
-    }
+    st = launch_column<3, false>(a, cgrid, col_waves, 0, stream);
   } else if (kk == 4) {
-    if (col_waves == 8) {
-      bloom_column_kernel<4, 512><<<cgrid, 512, 0, stream>>>(a);
-    } else {
-      bloom_column_kernel<4, 256><<<cgrid, 256, 0, stream>>>(a);
-    }
+    st = launch_column<4, false>(a, cgrid, col_waves, 0, stream);
   }
-  RT_CHECK_HIP(hipGetLastError());
+  if (st != kOk) return st;
 
   // stack evaluation of the rest (its workgroups skip the plans the column kernel wrote)
   const int64_t gx = cdiv(n_bundles * kBloomWordsPerBundle, kBloomThreads);
@@ -1124,16 +1210,46 @@ static int bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, 
   gy = gy > 65535 ? 65535 : gy;
   a.plans_per_wg = cdiv(plan_count, gy);
   gy = cdiv(plan_count, a.plans_per_wg);
-  const size_t lds = static_cast<size_t>(max_stack) * kBloomThreads * sizeof(uint64_t);
-  if (lds > 64 * 1024) {
+  const size_t slds = static_cast<size_t>(a.max_stack) * kBloomThreads * sizeof(uint64_t);
+  if (slds > 64 * 1024) {
     RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&bloom_search_kernel),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     static_cast<int>(lds)));
+                                     static_cast<int>(slds)));
   }
   bloom_search_kernel<<<dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)),
-                        kBloomThreads, lds, stream>>>(a);
+                        kBloomThreads, slds, stream>>>(a);
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
+}
+
+// The search behind rt_bloom_search and rt_bloom_search_t: the plans compiled into the
+// workspace, then searched; any of the three outputs.
+static int bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets, int64_t n_bundles,
+                        const int64_t* plan_offsets, const int8_t* plan_data, int64_t data_bytes,
+                        int64_t plan_count, int64_t max_stack, int64_t k, int64_t hash_k,
+                        int64_t* out_mask, uint8_t* out_bool, uint64_t* out_mask_t,
+                        int64_t out_t_stride, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
+  int st = bloom_check(n_bundles, plan_data, data_bytes, plan_count, max_stack, k, hash_k);
+  if (st != kOk) return st;
+  RT_CHECK_ARG(out_mask != nullptr || out_bool != nullptr || out_mask_t != nullptr, "no output");
+  RT_CHECK_ARG(out_mask_t == nullptr || out_t_stride >= plan_count,
+               "the transposed output's stride must be >= plan_count");
+  if (n_bundles == 0 || plan_count == 0) return kOk;
+  const size_t need = rt_bloom_search_workspace(data_bytes, plan_count);
+  if (workspace_bytes < need) {
+    set_error("workspace too small: %zu < %zu", workspace_bytes, need);
+    return kWorkspaceTooSmall;
+  }
+  BloomSearchArgs a = bloom_args(words, bundle_b_offsets, n_bundles, plan_offsets, plan_data,
+                                 data_bytes, plan_count, max_stack, k, hash_k, workspace);
+  a.out_mask = out_mask;
+  a.out_bool = out_bool;
+  a.out_mask_t = out_mask_t;
+  a.out_t_stride = out_t_stride;
+  st = bloom_compile_into(a, stream);
+  if (st != kOk) return st;
+  return bloom_run(a, stream);
 }
 
 extern "C" int rt_bloom_search(const uint64_t* words, const int64_t* bundle_b_offsets,
@@ -1157,6 +1273,57 @@ extern "C" int rt_bloom_search_t(const uint64_t* words, const int64_t* bundle_b_
   return bloom_search(words, bundle_b_offsets, n_bundles, plan_offsets, plan_data, data_bytes,
                       plan_count, max_stack, k, hash_k, nullptr, nullptr, out_mask_t,
                       out_t_stride, workspace, workspace_bytes, stream);
+}
+
+extern "C" int rt_bloom_compile(const int64_t* bundle_b_offsets, int64_t n_bundles,
+                                const int64_t* plan_offsets, const int8_t* plan_data,
+                                int64_t data_bytes, int64_t plan_count, int64_t max_stack,
+                                int64_t k, int64_t hash_k, void* compiled, size_t compiled_bytes,
+                                hipStream_t stream) {
+  int st = bloom_check(n_bundles, plan_data, data_bytes, plan_count, max_stack, k, hash_k);
+  if (st != kOk) return st;
+  if (plan_count == 0) return kOk;
+  RT_CHECK_ARG(n_bundles >= 1, "compiling needs the index's bundle widths (no bundles given)");
+  RT_CHECK_ARG(compiled != nullptr && compiled_bytes >= rt_bloom_compiled_bytes(plan_count),
+               "the compiled buffer needs %zu bytes", rt_bloom_compiled_bytes(plan_count));
+  const BloomSearchArgs a = bloom_args(nullptr, bundle_b_offsets, n_bundles, plan_offsets,
+                                       plan_data, data_bytes, plan_count, max_stack, k, hash_k,
+                                       compiled);
+  return bloom_compile_into(a, stream);
+}
+
+extern "C" int rt_bloom_search_compiled(const uint64_t* words, const int64_t* bundle_b_offsets,
+                                        int64_t n_bundles, const int64_t* plan_offsets,
+                                        const int8_t* plan_data, int64_t data_bytes,
+                                        int64_t plan_count, int64_t max_stack, int64_t k,
+                                        int64_t hash_k, const void* compiled,
+                                        size_t compiled_bytes, const uint32_t* clause_ptr,
+                                        const uint32_t* clause_terms, const uint32_t* plan_desc,
+                                        const uint32_t* plan_refs, int64_t n_clauses,
+                                        int64_t* out_mask, uint64_t* out_mask_t,
+                                        int64_t out_t_stride, hipStream_t stream) {
+  int st = bloom_check(n_bundles, plan_data, data_bytes, plan_count, max_stack, k, hash_k);
+  if (st != kOk) return st;
+  RT_CHECK_ARG((out_mask != nullptr) != (out_mask_t != nullptr), "one output");
+  RT_CHECK_ARG(out_mask_t == nullptr || out_t_stride >= plan_count,
+               "the transposed output's stride must be >= plan_count");
+  if (n_bundles == 0 || plan_count == 0) return kOk;
+  RT_CHECK_ARG(compiled != nullptr && compiled_bytes >= rt_bloom_compiled_bytes(plan_count),
+               "the compiled buffer needs %zu bytes", rt_bloom_compiled_bytes(plan_count));
+  BloomSearchArgs a = bloom_args(words, bundle_b_offsets, n_bundles, plan_offsets, plan_data,
+                                 data_bytes, plan_count, max_stack, k, hash_k,
+                                 const_cast<void*>(compiled));
+  a.out_mask = out_mask;
+  a.out_mask_t = out_mask_t;
+  a.out_t_stride = out_t_stride;
+  a.clause_ptr = clause_ptr;
+  a.clause_terms = clause_terms;
+  a.plan_desc = plan_desc;
+  a.plan_refs = plan_refs;
+  RT_CHECK_ARG(n_clauses >= 0 && n_clauses <= kMaxClauses, "clauses must be in [0, %d]",
+               kMaxClauses);
+  a.n_clauses = static_cast<int>(n_clauses);
+  return bloom_run(a, stream);
 }
 
 extern "C" int rt_bloom_search_columns(const uint64_t* words, const int64_t* bundle_b_offsets,

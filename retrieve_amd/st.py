@@ -221,19 +221,205 @@ def _bloom_search(bloom_index: Tensor, offsets: Tensor, plan_offsets: Tensor, da
     return out
 
 
+# A batch's plans are compiled once into the column kernel's programs (the prep pass), and the
+# plans that are ANDs of clauses are rewritten over the batch's distinct clauses (the clause
+# pass): keyed by the plan blob and the bundle offsets (id and version: an in-place change
+# recompiles) and the search parameters, kept until either tensor is freed. Under graph capture
+# with nothing kept, the search compiles in its workspace instead.
+_COMPILED: dict = {}
+MAX_CLAUSES = 128  # the column kernel's LDS beside its two staged bundles
+_PROG_MAX_OPS = 2048  # program words per plan (kProgMaxOps)
+_AND, _OR, _NOT, _TERM, _EMPTY = bl.AND, bl.OR, bl.NOT, bl.TERM, bl.EMPTY
+
+
+def clause_plans(blob: np.ndarray, plan_count: int, hash_k: int, hdr: np.ndarray,
+                 prog: np.ndarray, cap: int = MAX_CLAUSES, min_share: float = 2.0):
+    """The clause pass over a batch's compiled plans (``blob`` the prepared int64 words: 8
+    offsets a plan, then the data; ``hdr`` int32 ``[P, 4]`` and ``prog`` uint32 ``[P, ops, 2]``
+    from ``rt_bloom_compile``). A program plan whose tree is an AND (nested ANDs flattened) of
+    clauses -- an OR of terms (nested ORs flattened), a term, or the NOT of either; an EMPTY
+    child passes everything -- is rewritten as references to the batch's distinct clauses: the
+    same set of stored hash lists, so the same word in every column of any bundle width.
+    Returns ``(clause_ptr [C + 1], clause_terms [T, 4], plan_desc [P], plan_refs [R])`` as
+    uint32 (the layouts of ``rt_bloom_search_compiled``), or None when no plan has that form,
+    the batch has more than ``cap`` distinct clauses, or its clause plans reference fewer than
+    ``min_share`` times the distinct clauses' terms. A term's entry is its program word pair
+    and the index of its stored hashes in the data (uint64 words): term t of a plan is its t-th
+    TERM op, as the compiled program numbers them."""
+    words = np.asarray(blob).view(np.int64)
+    offs = words[: 8 * plan_count].reshape(plan_count, 8)
+    data = words[8 * plan_count :].view(np.uint8)
+    h64 = words[8 * plan_count :].view(np.uint64)
+    slots: dict = {}
+    clause_terms: list = []
+    desc = np.zeros(plan_count, np.uint32)
+    refs: list[int] = []
+    for b in range(plan_count):
+        if hdr[b, 0] != 0:  # not a program plan (stack path, or no match)
+            continue
+        o = offs[b]
+        ops = data[o[0] : o[1]]
+        ends = data[o[2] : o[3]].view(np.int32)
+        params = data[o[4] : o[5]].view(np.int32)
+        pw = prog[b, : hdr[b, 1]]
+        is_term = (pw[:, 0] & 3) == 0
+        tw0 = pw[is_term, 0] & np.uint32(0xFFFFFFF0)  # kind TERM, place push
+        tw1 = pw[is_term, 1]
+        ordinal = np.cumsum(ops == _TERM) - 1
+        h0 = int(np.uint32(hdr[b, 2])) | (int(hdr[b, 3]) << 32)
+
+        def children(i):
+            return params[ends[i] : ends[i + 1]].tolist()
+
+        def or_terms(i):
+            if ops[i] == _TERM:
+                return [int(ordinal[i])]
+            if ops[i] != _OR:
+                return None
+            out = []
+            for ch in children(i):
+                got = or_terms(ch)
+                if got is None:
+                    return None
+                out += got
+            return out
+
+        def clauses(i):
+            if ops[i] == _AND:
+                out = []
+                for ch in children(i):
+                    got = clauses(ch)
+                    if got is None:
+                        return None
+                    out += got
+                return out
+            if ops[i] == _EMPTY:
+                return []
+            neg = ops[i] == _NOT
+            got = or_terms(children(i)[0] if neg else i)
+            return None if got is None else [(got, neg)]
+
+        found = clauses(ops.size - 1)
+        if found is None or len(found) > 0xFFF or len(refs) + len(found) > (1 << 19):
+            continue
+        first = len(refs)
+        for terms, neg in found:
+            key = frozenset(tuple(h64[h0 + t * hash_k : h0 + (t + 1) * hash_k].tolist())
+                            for t in terms)
+            slot = slots.get(key)
+            if slot is None:
+                slot = slots[key] = len(slots)
+                clause_terms.append([(int(tw0[t]), int(tw1[t]), h0 + t * hash_k)
+                                     for t in terms])
+            refs.append(slot | (0x8000 if neg else 0))
+        desc[b] = np.uint32((1 << 31) | (first << 12) | len(found))
+    if not slots or len(slots) > cap:
+        return None
+    # the clause table costs LDS (occupancy) and a barrier: it pays where the clause plans
+    # reference each distinct clause's terms min_share times over (a batch of plans that share
+    # little runs its programs)
+    refs_terms = sum(len(clause_terms[r & 0x7FFF]) for r in refs)
+    if refs_terms < min_share * sum(len(c) for c in clause_terms):
+        return None
+    ptr = np.zeros(len(slots) + 1, np.uint32)
+    ptr[1:] = np.cumsum([len(c) for c in clause_terms])
+    flat = [t for c in clause_terms for t in c]
+    terms = np.array([(w0, w1, h & 0xFFFFFFFF, h >> 32) for w0, w1, h in flat], np.uint64)
+    return ptr, terms.astype(np.uint32).reshape(-1, 4), desc, np.array(refs, np.uint32)
+
+
+def _compiled_plans(offsets: Tensor, plans: Tensor, data: Tensor, plan_count: int,
+                    max_stack: int, k: int, hash_k: int):
+    """``(programs uint8, the clause tables (one int32 tensor, the tables' offsets) or None,
+    n_clauses)`` for these plans, compiled once (``rt_bloom_compile`` + ``clause_plans``); None
+    under graph capture with nothing kept."""
+    import weakref
+
+    key = (id(plans), plans._version, id(offsets), offsets._version, plan_count, max_stack, k,
+           hash_k)
+    hit = _COMPILED.get(key)
+    if hit is not None or _capturing():
+        return hit
+    dev = nat.require_device(offsets, plans)
+    lib = nat.lib()
+    nbytes = lib.rt_bloom_compiled_bytes(plan_count)
+    programs = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        nat.check(lib.rt_bloom_compile(
+            nat.ptr(offsets), offsets.numel() - 1, nat.ptr(plans), nat.ptr(data),
+            data.numel() * 8, plan_count, max_stack, k, hash_k, nat.ptr(programs), nbytes,
+            nat.stream(dev)))
+    tables, n_clauses = None, 0
+    if min(k, hash_k) <= 4:  # (above, every plan takes the stack path)
+        host = programs.cpu().numpy()
+        start = -(-plan_count * 16 // 256) * 256
+        hdr = host[: plan_count * 16].view(np.int32).reshape(plan_count, 4)
+        prog = host[start : start + plan_count * _PROG_MAX_OPS * 8].view(np.uint32)
+        found = clause_plans(plans.cpu().numpy(), plan_count, hash_k, hdr,
+                             prog.reshape(plan_count, _PROG_MAX_OPS, 2))
+        if found is not None:
+            n_clauses = int(found[0].size - 1)
+            # one int32 tensor: clause_ptr, plan_desc, plan_refs, clause_terms
+            parts = [found[0], found[2], found[3], found[1].reshape(-1)]
+            at = np.cumsum([0] + [p.size for p in parts])
+            tables = (torch.from_numpy(np.concatenate(parts).view(np.int32)).to(dev),
+                      tuple(int(x) for x in at[:4]))
+    hit = (programs, tables, n_clauses)
+    _COMPILED[key] = hit
+    for t in (plans, offsets):
+        weakref.finalize(t, _COMPILED.pop, key, None)
+    return hit
+
+
+def _search_compiled(bloom_index: Tensor, offsets: Tensor, plans: Tensor, data: Tensor,
+                     plan_count: int, max_stack: int, k: int, hash_k: int, compiled,
+                     out: Tensor, transposed: bool) -> None:
+    programs, tables, n_clauses = compiled
+    dev = bloom_index.device
+    lib = nat.lib()
+    ptrs = [None] * 4
+    if tables is not None:
+        base, at = nat.ptr(tables[0]), tables[1]
+        ptrs = [base + 4 * a for a in at]  # clause_ptr, plan_desc, plan_refs, clause_terms
+    with torch.cuda.device(dev):
+        nat.check(lib.rt_bloom_search_compiled(
+            nat.ptr(bloom_index), nat.ptr(offsets), offsets.numel() - 1, nat.ptr(plans),
+            nat.ptr(data), data.numel() * 8, plan_count, max_stack, k, hash_k,
+            nat.ptr(programs), programs.numel(), ptrs[0], ptrs[3], ptrs[1], ptrs[2], n_clauses,
+            None if transposed else nat.ptr(out), nat.ptr(out) if transposed else None,
+            out.shape[1] if transposed else 0, nat.stream(dev)))
+
+
 def _search_prepared(bloom_index, bloom_bundle_b_offsets, plans, plan_count, max_stack_size, k,
                      hash_k, return_bool_mask=False):
     """Plans prepared once on the device: ``plans`` int64 ``[8 * plan_count + data words]``,
-    the offsets then the parser's data (``bloom_index_search_cuda.cu:103-137``)."""
+    the offsets then the parser's data (``bloom_index_search_cuda.cu:103-137``). The words
+    come from the plans' compiled programs (compiled on the first search of a blob)."""
     if plans.dtype != torch.int64 or plans.dim() != 1 or plans.numel() < 8 * plan_count:
         raise ValueError("plans must be int64 [8 * plan_count + data words]")
     if max_stack_size > MAX_STACK:
         raise ValueError(f"max_stack_size must be <= {MAX_STACK}")
     plans = plans.contiguous()
     data = plans[8 * plan_count :]
-    return _bloom_search(bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous(), plans,
-                         data, data.numel() * 8, int(plan_count), int(max_stack_size), int(k),
-                         int(hash_k), bool(return_bool_mask))
+    index, offsets = bloom_index.contiguous(), bloom_bundle_b_offsets.contiguous()
+    plan_count, max_stack_size, k, hash_k = (int(plan_count), int(max_stack_size), int(k),
+                                             int(hash_k))
+    nb = offsets.numel() - 1
+    if not return_bool_mask and plan_count > 0 and nb > 0:
+        nat.require_device(index, offsets, plans)
+        if index.dtype != torch.int64 or offsets.dtype != torch.int64:
+            raise TypeError("bloom_index and bloom_bundle_b_offsets must be int64")
+        compiled = _compiled_plans(offsets, plans, data, plan_count,
+                                   max(1, min(max_stack_size, MAX_STACK)), k, hash_k)
+        if compiled is not None:
+            out = torch.empty((plan_count, nb * WORDS_PER_BUNDLE), dtype=torch.int64,
+                              device=index.device)
+            _search_compiled(index, offsets, plans, data, plan_count,
+                             max(1, min(max_stack_size, MAX_STACK)), k, hash_k, compiled, out,
+                             False)
+            return out
+    return _bloom_search(index, offsets, plans, data, data.numel() * 8, plan_count,
+                         max_stack_size, k, hash_k, bool(return_bool_mask))
 
 
 def _transposed_shape(offsets: Tensor, plan_count: int) -> tuple[int, int]:
@@ -264,6 +450,12 @@ def bloom_search_cols(bloom_index: Tensor, bloom_bundle_b_offsets: Tensor, plans
     cols, stride = _transposed_shape(offsets, plan_count)
     out = torch.empty((cols, stride), dtype=torch.int64, device=dev)
     if plan_count == 0 or nb <= 0:
+        return out
+    depth = max(1, min(int(max_stack_size), MAX_STACK))
+    compiled = _compiled_plans(offsets, plans, data, int(plan_count), depth, int(k), int(hash_k))
+    if compiled is not None:
+        _search_compiled(bloom_index, offsets, plans, data, int(plan_count), depth, int(k),
+                         int(hash_k), compiled, out, True)
         return out
     lib = nat.lib()
     ws = nat.workspace(lib.rt_bloom_search_workspace(data.numel() * 8, plan_count), dev)

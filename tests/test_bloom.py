@@ -233,6 +233,71 @@ def test_long_plans(dev):
         assert np.array_equal(row, want), e[:60]
 
 
+@pytest.mark.parametrize("mode", ["fixed", "upstream"])
+@pytest.mark.parametrize("n_sets", [25, 150])
+def test_compiled_plans_and_clauses(dev, mode, n_sets):
+    """The prepared search compiles a blob's programs once. With 25 value sets behind 60 plans
+    (clauses repeat across plans) the ANDs of clauses read the batch's distinct clauses,
+    evaluated once per column, while the plans of other shapes (nested, NOT of an AND, a
+    random mix) run their programs in the same search; with 150 value sets there are more
+    distinct clauses than the table holds and every plan runs its program. Either way the words
+    equal the search that compiles in its workspace (uniform widths; mixed widths, whose
+    unstaged bundles evaluate the clauses' terms from their hashes) and the oracle; a blob
+    changed in place is compiled again."""
+    g = rng(97 + n_sets + (mode == "upstream"))
+    n = 9000
+    attrs = _attrs(g, n, 3, 1, 200, 0.1)
+    if mode == "fixed":
+        words, offs = _build(dev, attrs, 3, bits=64)
+        ow, oo = of.bloom_build(attrs, 3, bits_per_doc=64)
+    else:
+        attrs[5000:, 1:, :] = -1  # bundles of different widths
+        words, offs = _build(dev, attrs, 3, mult=3.0)
+        ow, oo = of.bloom_build(attrs, 3, b_multiplier=3.0)
+    sets = [(int(g.integers(0, 3)), np.sort(g.choice(200, int(g.integers(1, 40)), replace=False)))
+            for _ in range(n_sets)]
+
+    def exprs_of(shift):
+        out = []
+        for r in range(max(60, n_sets)):
+            c1, v1 = sets[r % n_sets]
+            c2, v2 = sets[(7 * r + 3) % n_sets]
+            e = "(" + " OR ".join(f"{c1}:{(v + shift) % 200}" for v in v1) + ")"
+            if r % 3:
+                e += " AND " + ("NOT " if r % 5 == 0 else "") + \
+                    "(" + " OR ".join(f"{c2}:{(v + shift) % 200}" for v in v2) + ")"
+            out.append(e)
+        return out + [_nested(5), "NOT (0:1 AND 1:2)", "", _random_expr(g), _random_expr(g)]
+
+    exprs = exprs_of(0)
+    blob, count, depth = st.prepare_plans(exprs, 7, dev)
+    print(f"compiled plans {mode}, {n_sets} value sets: {count} plans", flush=True)
+    got = torch.ops.st.bloom_index_search_batch_prepared(words, offs, blob, count, depth, 3, 7)
+    hits = [v for key, v in st._COMPILED.items() if key[0] == id(blob)]
+    assert len(hits) == 1
+    if n_sets == 25:
+        assert 0 < hits[0][2] <= st.MAX_CLAUSES  # the clause plans read the table
+    else:
+        assert hits[0][2] == 0  # more distinct clauses than the table holds
+    data = blob[8 * count:]
+    ref = st._bloom_search(words, offs, blob, data, data.numel() * 8, count, depth, 3, 7, False)
+    assert torch.equal(got, ref)
+    assert torch.equal(st.bloom_search_t(words, offs, blob, count, depth, 3, 7), got)
+    rows = _unpack(got.cpu().numpy(), n)
+    for e, row in list(zip(exprs, rows))[::7] + list(zip(exprs, rows))[-5:]:
+        assert np.array_equal(row, of.bloom_expression_mask(ow, oo, n, e, 3, 7)), e[:40]
+    # the same blob rewritten in place (same sizes, other values): compiled again
+    exprs2 = exprs_of(7)
+    exprs2[-2:] = exprs[-2:]
+    blob2, count2, depth2 = st.prepare_plans(exprs2, 7, dev)
+    assert blob2.shape == blob.shape and (count2, depth2) == (count, depth)
+    blob.copy_(blob2)
+    got2 = torch.ops.st.bloom_index_search_batch_prepared(words, offs, blob, count, depth, 3, 7)
+    rows2 = _unpack(got2.cpu().numpy(), n)
+    for e, row in list(zip(exprs2, rows2))[::7]:
+        assert np.array_equal(row, of.bloom_expression_mask(ow, oo, n, e, 3, 7)), e[:40]
+
+
 def test_stack_limit_matches_nothing(dev):
     """A plan that needs more stack than max_stack_size matches nothing; the others evaluate."""
     g = rng(90)

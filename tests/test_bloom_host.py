@@ -118,3 +118,95 @@ def test_parse_op_schema():
     )
     assert mx == 2 and data.dtype == torch.int8 and offs.dtype == torch.int64
     assert offs.shape == (24,)
+
+
+def _compiled_stand_in(blob: np.ndarray, count: int):
+    """What the compile pass gives the clause pass, built on the host: every plan a program
+    (status 0) whose t-th TERM op carries the marker t + 1000 * plan in its position bits
+    (kind TERM), other ops PASS; the first hash word's index in the header."""
+    offs = blob[: 8 * count].reshape(count, 8)
+    data = blob[8 * count :].view(np.uint8)
+    hdr = np.zeros((count, 4), np.int32)
+    prog = np.zeros((count, 64, 2), np.uint32)
+    for b in range(count):
+        o = offs[b]
+        ops = data[o[0] : o[1]]
+        hdr[b] = [0, ops.size, o[6] // 8, 0]
+        t = 0
+        for i, op in enumerate(ops.tolist()):
+            if op == bl.TERM:
+                prog[b, i] = [(t + 1000 * b) << 4 | (2 << 2), 7]
+                t += 1
+            else:
+                prog[b, i] = [2, 0]
+    return hdr, prog
+
+
+def test_clause_plans_share_clauses():
+    """The clause pass: ANDs of clauses (an OR of terms with nested ORs flattened, a term, NOT of
+    either, EMPTY) over the batch's distinct clauses (the same set of tokens, in any order);
+    other shapes stay programs. Each clause term's entry carries its program words and the
+    index of its stored hashes."""
+    import retrieve_amd.st as st
+
+    exprs = ["(0:1 OR 0:2) AND 1:5", "(0:2 OR 0:1) AND NOT 2:7", "1:5", "",
+             "0:1 OR 0:2", "NOT (0:1 AND 1:5)", "(0:1 AND 1:5) OR 2:3",
+             "0:1 OR 0:2 OR 0:3 OR 0:4 OR 0:5 OR 0:6 OR 0:7", "1:5 AND (1:5) AND 2:7"]
+    blob, count, _ = st.prepare_plans(exprs, 7, torch.device("cpu"))
+    blob = blob.numpy()
+    hdr, prog = _compiled_stand_in(blob, count)
+    ptr, terms, desc, refs = st.clause_plans(blob, count, 7, hdr, prog, min_share=0)
+    h64 = blob[8 * count :].view(np.uint64)
+
+    def clause(slot):
+        toks = set()
+        for w0, _, lo, hi in terms[ptr[slot] : ptr[slot + 1]].tolist():
+            hidx = lo | (hi << 32)
+            toks.add(next((f, v) for f in range(3) for v in range(1, 8)
+                          if h64[hidx] == of.murmur_hash3_2x64(f, v, 0)))
+        return toks
+
+    def plan(b):
+        d = int(desc[b])
+        if not d >> 31:
+            return None
+        first, n = (d >> 12) & 0x7FFFF, d & 0xFFF
+        return [(frozenset(clause(r & 0x7FFF)), bool(r & 0x8000))
+                for r in refs[first : first + n].tolist()]
+
+    a, b5, c7 = frozenset({(0, 1), (0, 2)}), frozenset({(1, 5)}), frozenset({(2, 7)})
+    assert plan(0) == [(a, False), (b5, False)]
+    assert plan(1) == [(a, False), (c7, True)]
+    assert plan(2) == [(b5, False)]
+    assert plan(3) == []  # EMPTY: an AND of nothing
+    assert plan(4) == [(a, False)]
+    assert plan(5) is None and plan(6) is None  # NOT of an AND, OR of an AND
+    assert plan(7) == [(frozenset((0, v) for v in range(1, 8)), False)]
+    assert plan(8) == [(b5, False), (b5, False), (c7, False)]
+    assert ptr.size - 1 == 4  # {0:1, 0:2}, {1:5}, {2:7}, {0:1 .. 0:7}
+    # a term's entry carries its program words (the marker of its TERM op, place cleared)
+    w0 = terms[ptr[0] : ptr[1], 0]
+    assert sorted(((w0 >> 4) % 1000).tolist()) == [0, 1] and (w0 & 0xF == 0).all()
+    assert (terms[:, 1] == 7).all()
+
+
+def test_clause_plans_decline():
+    """No tables when no plan has the clause form, there are more distinct clauses than the
+    table holds, or the plans share too little of them."""
+    import retrieve_amd.st as st
+
+    blob, count, _ = st.prepare_plans(["NOT (0:1 AND 1:2)", "(0:1 AND 1:2) OR 2:3"], 7,
+                                      torch.device("cpu"))
+    hdr, prog = _compiled_stand_in(blob.numpy(), count)
+    assert st.clause_plans(blob.numpy(), count, 7, hdr, prog) is None
+    blob, count, _ = st.prepare_plans([f"0:{v} AND 1:{v}" for v in range(5)], 7,
+                                      torch.device("cpu"))
+    hdr, prog = _compiled_stand_in(blob.numpy(), count)
+    assert st.clause_plans(blob.numpy(), count, 7, hdr, prog, cap=9, min_share=0) is None
+    assert st.clause_plans(blob.numpy(), count, 7, hdr, prog, cap=10, min_share=0) is not None
+    # ten clauses referenced once each: too little sharing for the table
+    assert st.clause_plans(blob.numpy(), count, 7, hdr, prog) is None
+    blob, count, _ = st.prepare_plans(["0:1 AND 1:2", "0:1 AND 1:3", "(0:1) AND 1:2"], 7,
+                                      torch.device("cpu"))
+    hdr, prog = _compiled_stand_in(blob.numpy(), count)
+    assert st.clause_plans(blob.numpy(), count, 7, hdr, prog) is not None  # 6 refs, 3 terms
