@@ -95,7 +95,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rt_bloom_search_compiled": (
         _c_int,
         [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_sz,
-         _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p],
+         _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p],
     ),
     "rt_mask_compact_workspace": (_c_sz, [_c_i64, _c_i64]),
     "rt_mask_compact": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p]),

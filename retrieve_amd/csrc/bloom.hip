@@ -187,6 +187,7 @@ struct BloomSearchArgs {
                                  // ref, bits 0-11 its ref count; 0: the plan runs its program
   const uint32_t* plan_refs;     // bits 0-14 a clause, bit 15 NOT
   int n_clauses;                 // 0: every plan runs its program
+  bool all_clauses;              // every plan is a clause plan (none runs a program)
   int64_t* out_mask;      // [plan_count, nb * 32] or null
   uint8_t* out_bool;      // [plan_count, nb * 32 * 64] or null
   uint64_t* out_mask_t;   // [nb * 32, out_t_stride]: the words transposed, or null
@@ -800,28 +801,85 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
   if constexpr (CLAUSES) {
     // the batch's distinct clauses, each once per column (an OR of its terms: from the staged
     // positions, or for a bundle of another width from the terms' stored hashes)
+    // The clauses' terms in clause order are split evenly over the waves (clauses differ in
+    // length by 10x): a wave ORs each clause segment of its share in registers, four terms at
+    // a time, and merges it into the clause's word with one LDS atomic OR.
     const int n_clauses = __builtin_amdgcn_readfirstlane(a.n_clauses);
-    for (int c = wave; c < n_clauses; c += kColWaves) {
-      const int t0 = __builtin_amdgcn_readfirstlane(a.clause_ptr[c]);
-      const int t1 = __builtin_amdgcn_readfirstlane(a.clause_ptr[c + 1]);
-      uint64_t v = 0ull;
-      for (int t = t0; t < t1; ++t) {
-        const uint32_t* e = a.clause_terms + 4 * static_cast<int64_t>(t);
-        const uint32_t p0 = __builtin_amdgcn_readfirstlane(e[0]);
-        const uint32_t p1 = __builtin_amdgcn_readfirstlane(e[1]);
-        const int64_t hidx = static_cast<int64_t>(
-            (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(e[3])) << 32) |
-            __builtin_amdgcn_readfirstlane(e[2]));
-        v |= mine_staged ? staged_term<KK>(lcol, p0, p1)
+    for (int i = tid; i < n_clauses * kWave; i += kColThreads) clause_words[i] = 0ull;
+    __syncthreads();
+    const int n_terms = __builtin_amdgcn_readfirstlane(a.clause_ptr[n_clauses]);
+    const int share = (n_terms + kColWaves - 1) / kColWaves;
+    const int t_lo = wave * share;
+    const int t_hi = t_lo + share < n_terms ? t_lo + share : n_terms;
+    auto term = [&](int t) -> uint64_t {
+      const uint32_t* e = a.clause_terms + 4 * static_cast<int64_t>(t);
+      const uint32_t p0 = __builtin_amdgcn_readfirstlane(e[0]);
+      const uint32_t p1 = __builtin_amdgcn_readfirstlane(e[1]);
+      const int64_t hidx = static_cast<int64_t>(
+          (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(e[3])) << 32) |
+          __builtin_amdgcn_readfirstlane(e[2]));
+      return mine_staged ? staged_term<KK>(lcol, p0, p1)
                          : term_from_hashes(a, hidx, 0, wcol, my_w);
+    };
+    int c = 0;
+    while (c < n_clauses && __builtin_amdgcn_readfirstlane(a.clause_ptr[c + 1]) <= t_lo) ++c;
+    for (int t = t_lo; t < t_hi; ++c) {
+      const int end_c = __builtin_amdgcn_readfirstlane(a.clause_ptr[c + 1]);
+      const int end = end_c < t_hi ? end_c : t_hi;
+      uint64_t v = 0ull;
+      for (; t + 3 < end; t += 4) {
+        const uint64_t x0 = term(t);
+        const uint64_t x1 = term(t + 1);
+        const uint64_t x2 = term(t + 2);
+        const uint64_t x3 = term(t + 3);
+        v |= (x0 | x1) | (x2 | x3);
       }
-      clause_words[c * kWave + lane] = v;
+      for (; t < end; ++t) v |= term(t);
+      __hip_atomic_fetch_or(&clause_words[c * kWave + lane], v, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     __syncthreads();
   }
 
   const int64_t b0 = static_cast<int64_t>(blockIdx.y) * a.plans_per_wg;
   const int64_t b1 = b0 + a.plans_per_wg < a.plan_count ? b0 + a.plans_per_wg : a.plan_count;
+  if constexpr (CLAUSES) {
+    if (a.all_clauses && a.out_mask_t != nullptr) {
+      // Every plan reads the clause table, so the staged bundles are dead: their LDS holds a
+      // chunk of 64 plans' words for the 64 columns, swizzled (word p ^ r of row r) so that
+      // both the column-wise stores and the row-wise reads are free of bank conflicts. A
+      // column's 64 words then leave as one contiguous 512-byte run of the transposed output,
+      // instead of 64 scattered 8-byte stores a plan.
+      typedef __attribute__((address_space(1))) int64_t gi64;
+      gi64* ot = (gi64*)(a.out_mask_t);
+      const int64_t col0 = beta0 * kBloomWordsPerBundle;
+      for (int64_t c0 = b0; c0 < b1; c0 += kWave) {
+        for (int64_t pb = c0 + wave; pb < b1 && pb < c0 + kWave; pb += kColWaves) {
+          const uint32_t desc = __builtin_amdgcn_readfirstlane(a.plan_desc[pb]);
+          const uint32_t* refs = a.plan_refs + ((desc >> 12) & 0x7ffffu);
+          const int cnt = static_cast<int>(desc & 0xfffu);
+          uint64_t top = ~0ull;
+          for (int r = 0; r < cnt; ++r) {
+            const uint32_t ref = __builtin_amdgcn_readfirstlane(refs[r]);
+            const uint64_t w = clause_col[(ref & 0x7fffu) * kWave];
+            top &= (ref & 0x8000u) != 0u ? ~w : w;
+          }
+          const int p = static_cast<int>(pb - c0);
+          idx[lane * kWave + (p ^ lane)] = top;
+        }
+        __syncthreads();
+        for (int i = tid; i < kWave * kWave; i += kColThreads) {
+          const int r = i / kWave;
+          const int p = i % kWave;
+          if (c0 + p < b1 && col0 + r < ncol) {
+            ot[(col0 + r) * a.out_t_stride + c0 + p] = static_cast<int64_t>(idx[r * kWave + (p ^ r)]);
+          }
+        }
+        __syncthreads();
+      }
+      return;
+    }
+  }
   // each plan's header and first 64 program ops are loaded while the plan before it runs (a
   // plan's slot holds kProgMaxOps >= 64 ops, so the loads stay inside it)
   gu32* progs = (gu32*)(a.prog);
@@ -1300,8 +1358,9 @@ extern "C" int rt_bloom_search_compiled(const uint64_t* words, const int64_t* bu
                                         size_t compiled_bytes, const uint32_t* clause_ptr,
                                         const uint32_t* clause_terms, const uint32_t* plan_desc,
                                         const uint32_t* plan_refs, int64_t n_clauses,
-                                        int64_t* out_mask, uint64_t* out_mask_t,
-                                        int64_t out_t_stride, hipStream_t stream) {
+                                        int64_t all_clause_plans, int64_t* out_mask,
+                                        uint64_t* out_mask_t, int64_t out_t_stride,
+                                        hipStream_t stream) {
   int st = bloom_check(n_bundles, plan_data, data_bytes, plan_count, max_stack, k, hash_k);
   if (st != kOk) return st;
   RT_CHECK_ARG((out_mask != nullptr) != (out_mask_t != nullptr), "one output");
@@ -1323,6 +1382,7 @@ extern "C" int rt_bloom_search_compiled(const uint64_t* words, const int64_t* bu
   RT_CHECK_ARG(n_clauses >= 0 && n_clauses <= kMaxClauses, "clauses must be in [0, %d]",
                kMaxClauses);
   a.n_clauses = static_cast<int>(n_clauses);
+  a.all_clauses = n_clauses > 0 && all_clause_plans != 0;
   return bloom_run(a, stream);
 }
 

@@ -330,8 +330,8 @@ def clause_plans(blob: np.ndarray, plan_count: int, hash_k: int, hdr: np.ndarray
 
 def _compiled_plans(offsets: Tensor, plans: Tensor, data: Tensor, plan_count: int,
                     max_stack: int, k: int, hash_k: int):
-    """``(programs uint8, the clause tables (one int32 tensor, the tables' offsets) or None,
-    n_clauses)`` for these plans, compiled once (``rt_bloom_compile`` + ``clause_plans``); None
+    """``(programs uint8, the clause tables (one int32 tensor, the tables' offsets, whether
+    every plan is a clause plan) or None, n_clauses)`` for these plans, compiled once (``rt_bloom_compile`` + ``clause_plans``); None
     under graph capture with nothing kept."""
     import weakref
 
@@ -363,7 +363,7 @@ def _compiled_plans(offsets: Tensor, plans: Tensor, data: Tensor, plan_count: in
             parts = [found[0], found[2], found[3], found[1].reshape(-1)]
             at = np.cumsum([0] + [p.size for p in parts])
             tables = (torch.from_numpy(np.concatenate(parts).view(np.int32)).to(dev),
-                      tuple(int(x) for x in at[:4]))
+                      tuple(int(x) for x in at[:4]), bool((found[2] >> 31).all()))
     hit = (programs, tables, n_clauses)
     _COMPILED[key] = hit
     for t in (plans, offsets):
@@ -377,16 +377,17 @@ def _search_compiled(bloom_index: Tensor, offsets: Tensor, plans: Tensor, data: 
     programs, tables, n_clauses = compiled
     dev = bloom_index.device
     lib = nat.lib()
-    ptrs = [None] * 4
+    ptrs, every = [None] * 4, 0
     if tables is not None:
         base, at = nat.ptr(tables[0]), tables[1]
         ptrs = [base + 4 * a for a in at]  # clause_ptr, plan_desc, plan_refs, clause_terms
+        every = int(tables[2])
     with torch.cuda.device(dev):
         nat.check(lib.rt_bloom_search_compiled(
             nat.ptr(bloom_index), nat.ptr(offsets), offsets.numel() - 1, nat.ptr(plans),
             nat.ptr(data), data.numel() * 8, plan_count, max_stack, k, hash_k,
             nat.ptr(programs), programs.numel(), ptrs[0], ptrs[3], ptrs[1], ptrs[2], n_clauses,
-            None if transposed else nat.ptr(out), nat.ptr(out) if transposed else None,
+            every, None if transposed else nat.ptr(out), nat.ptr(out) if transposed else None,
             out.shape[1] if transposed else 0, nat.stream(dev)))
 
 

@@ -298,6 +298,45 @@ def test_compiled_plans_and_clauses(dev, mode, n_sets):
         assert np.array_equal(row, of.bloom_expression_mask(ow, oo, n, e, 3, 7)), e[:40]
 
 
+@pytest.mark.parametrize("n,n_plans", [(9000, 100), (8_500_000, 150)])
+def test_clause_plans_transposed_words(dev, n, n_plans):
+    """Every plan a clause plan: the transposed words are gathered 64 plans at a time in the
+    column kernel's LDS and leave in contiguous runs. 8.5M documents (one workgroup takes every
+    plan: two full chunks and a partial one) and 9000 (plans split over workgroups, a partial
+    chunk each); the words equal the prepared search of the same plans without the clause
+    table (row-major, programs), and the oracle on the small table."""
+    import bench
+
+    g = rng(99 + n_plans)
+    print(f"clause plans, transposed words: N={n} plans={n_plans}", flush=True)
+    if n > 100_000:
+        attrs = bench.attr_table(n, 4321, dev).long()
+    else:
+        attrs = torch.from_numpy(_attrs(g, n, 8, 1, 40, 0.0)).to(dev)
+    fid, fo, fv = st.attrs_to_features(attrs)
+    words, offs = torch.ops.st.bloom_index_build_fixed(fid, fo, fv, 64, 3)
+    del fid, fo, fv
+    pool = [(int(g.integers(0, 8)), np.sort(g.choice(16, int(g.integers(1, 6)), replace=False)))
+            for _ in range(12)]
+    exprs = []
+    for r in range(n_plans):
+        parts = [pool[(r * j + 5) % 12] for j in range(1, 2 + r % 3)]
+        exprs.append(" AND ".join("(" + " OR ".join(f"{c}:{v}" for v in vs) + ")"
+                                  for c, vs in parts))
+    blob, count, depth = st.prepare_plans(exprs, 7, dev)
+    got = st.bloom_search_t(words, offs, blob, count, depth, 3, 7)
+    hits = [v for key, v in st._COMPILED.items() if key[0] == id(blob)]
+    assert len(hits) == 1 and hits[0][2] > 0 and hits[0][1][2]  # every plan a clause plan
+    data = blob[8 * count:]
+    ref = st._bloom_search(words, offs, blob, data, data.numel() * 8, count, depth, 3, 7, False)
+    assert torch.equal(got, ref)
+    if n < 100_000:
+        ow, oo = of.bloom_build(attrs.cpu().numpy(), 3, bits_per_doc=64)
+        rows = _unpack(got.contiguous().cpu().numpy(), n)
+        for e, row in list(zip(exprs, rows))[::9]:
+            assert np.array_equal(row, of.bloom_expression_mask(ow, oo, n, e, 3, 7)), e
+
+
 def test_stack_limit_matches_nothing(dev):
     """A plan that needs more stack than max_stack_size matches nothing; the others evaluate."""
     g = rng(90)
