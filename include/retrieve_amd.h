@@ -289,8 +289,10 @@ int rt_bloom_search_t(const uint64_t* words, const int64_t* bundle_b_offsets, in
  * bits 12-30 its first entry in plan_refs, bits 0-11 its count; plan_refs: bits 0-14 a clause,
  * bit 15 its NOT. The column kernel evaluates each distinct clause once per column and such a
  * plan is the AND of its clauses' words; retrieve_amd/st.py's clause pass writes the tables.
- * all_clause_plans != 0 declares that every plan is a clause plan: the transposed words then
- * leave in contiguous runs (the kernel reuses its staging LDS to gather them).
+ * plan_flags: bit 0 declares that every plan is a clause plan (the transposed words then leave
+ * in contiguous runs: the kernel reuses its staging LDS to gather them); bit 1 that no plan takes
+ * the stack evaluation (every status in `compiled` is a program or no-match): its launch is
+ * skipped.
  * Replaces: st::bloom_index_search_batch_prepared (silvertorch/.../bloom_index_search.cpp:
  *   576-590) split at its plan preparation; no separate counterpart in the reference. */
 size_t rt_bloom_compiled_bytes(int64_t plan_count);
@@ -305,7 +307,7 @@ int rt_bloom_search_compiled(const uint64_t* words, const int64_t* bundle_b_offs
                              size_t compiled_bytes, const uint32_t* clause_ptr,
                              const uint32_t* clause_terms, const uint32_t* plan_desc,
                              const uint32_t* plan_refs, int64_t n_clauses,
-                             int64_t all_clause_plans, int64_t* out_mask, uint64_t* out_mask_t,
+                             int64_t plan_flags, int64_t* out_mask, uint64_t* out_mask_t,
                              int64_t out_t_stride, rt_stream_t stream);
 
 /* The Bloom plans over the probed clusters' columns only: probed cluster i (row i / per_row of a

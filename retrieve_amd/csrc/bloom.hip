@@ -286,7 +286,10 @@ constexpr int kFoldDepth = 4;
 constexpr int kProgMaxPos = 4;
 constexpr int kColMaxWidth = 64;
 constexpr int kProgMaxOps = 2048;
-constexpr int kMaxClauses = 128;  // LDS: 128 clauses x 64 columns x 8 bytes beside the staging
+constexpr int kMaxClauses = 128;
+// rt_bloom_search_compiled's plan_flags
+constexpr int64_t kPlansAllClauses = 1;  // every plan is a clause plan
+constexpr int64_t kPlansNoStack = 2;     // no plan takes the stack evaluation  // LDS: 128 clauses x 64 columns x 8 bytes beside the staging
 constexpr int kPrepThreads = 256;
 constexpr uint32_t kColPosBytes = kBloomWordsPerBundle * sizeof(uint64_t);  // 256
 
@@ -1211,7 +1214,7 @@ static int bloom_compile_into(const BloomSearchArgs& a, hipStream_t stream) {
 
 // The searches over compiled plans: the column kernel (programs; with a.n_clauses > 0 the
 // plans of clauses over the batch's distinct clauses)// terms), then the stack evaluation of the rest; any of the three outputs.
-static int bloom_run(BloomSearchArgs a, hipStream_t stream) {
+static int bloom_run(BloomSearchArgs a, hipStream_t stream, bool stack_plans = true) {
   const int64_t n_bundles = a.nb;
   const int64_t plan_count = a.plan_count;
   const int64_t kk = a.k < a.hash_k ? a.k : a.hash_k;  // > kProgMaxPos: the stack path only
@@ -1259,6 +1262,7 @@ static int bloom_run(BloomSearchArgs a, hipStream_t stream) {
   }
   if (st != kOk) return st;
 
+  if (!stack_plans) return kOk;  // (the compile pass gave every plan a program)
   // stack evaluation of the rest (its workgroups skip the plans the column kernel wrote)
   const int64_t gx = cdiv(n_bundles * kBloomWordsPerBundle, kBloomThreads);
   RT_CHECK_ARG(gx < (int64_t{1} << 31), "too many bundles");
@@ -1358,7 +1362,7 @@ extern "C" int rt_bloom_search_compiled(const uint64_t* words, const int64_t* bu
                                         size_t compiled_bytes, const uint32_t* clause_ptr,
                                         const uint32_t* clause_terms, const uint32_t* plan_desc,
                                         const uint32_t* plan_refs, int64_t n_clauses,
-                                        int64_t all_clause_plans, int64_t* out_mask,
+                                        int64_t plan_flags, int64_t* out_mask,
                                         uint64_t* out_mask_t, int64_t out_t_stride,
                                         hipStream_t stream) {
   int st = bloom_check(n_bundles, plan_data, data_bytes, plan_count, max_stack, k, hash_k);
@@ -1382,8 +1386,8 @@ extern "C" int rt_bloom_search_compiled(const uint64_t* words, const int64_t* bu
   RT_CHECK_ARG(n_clauses >= 0 && n_clauses <= kMaxClauses, "clauses must be in [0, %d]",
                kMaxClauses);
   a.n_clauses = static_cast<int>(n_clauses);
-  a.all_clauses = n_clauses > 0 && all_clause_plans != 0;
-  return bloom_run(a, stream);
+  a.all_clauses = n_clauses > 0 && (plan_flags & kPlansAllClauses) != 0;
+  return bloom_run(a, stream, (plan_flags & kPlansNoStack) == 0);
 }
 
 extern "C" int rt_bloom_search_columns(const uint64_t* words, const int64_t* bundle_b_offsets,

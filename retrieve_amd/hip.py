@@ -339,7 +339,9 @@ def _clause_prep(item_clause_attrs: Tensor, clause_is_reverse: Tensor, query_val
     if c > 32:
         raise ValueError(f"at most 32 clauses, got C={c}")
     _check_items(item_clause_attrs=item_clause_attrs)
-    rev = clause_is_reverse.to(torch.int8).contiguous()
+    rev = clause_is_reverse.contiguous()
+    # (a bool flag is its 0 / 1 byte: a view, not a copy kernel a call)
+    rev = rev.view(torch.int8) if rev.dtype == torch.bool else rev.to(torch.int8)
     q = query_values.contiguous()
     if q.dim() == 2:
         q = q.unsqueeze(2)

@@ -331,7 +331,8 @@ def clause_plans(blob: np.ndarray, plan_count: int, hash_k: int, hdr: np.ndarray
 def _compiled_plans(offsets: Tensor, plans: Tensor, data: Tensor, plan_count: int,
                     max_stack: int, k: int, hash_k: int):
     """``(programs uint8, the clause tables (one int32 tensor, the tables' offsets, whether
-    every plan is a clause plan) or None, n_clauses)`` for these plans, compiled once (``rt_bloom_compile`` + ``clause_plans``); None
+    every plan is a clause plan) or None, n_clauses, whether no plan takes the stack path)``
+    for these plans, compiled once (``rt_bloom_compile`` + ``clause_plans``); None
     under graph capture with nothing kept."""
     import weakref
 
@@ -349,7 +350,7 @@ def _compiled_plans(offsets: Tensor, plans: Tensor, data: Tensor, plan_count: in
             nat.ptr(offsets), offsets.numel() - 1, nat.ptr(plans), nat.ptr(data),
             data.numel() * 8, plan_count, max_stack, k, hash_k, nat.ptr(programs), nbytes,
             nat.stream(dev)))
-    tables, n_clauses = None, 0
+    tables, n_clauses, no_stack = None, 0, False
     if min(k, hash_k) <= 4:  # (above, every plan takes the stack path)
         host = programs.cpu().numpy()
         start = -(-plan_count * 16 // 256) * 256
@@ -364,7 +365,8 @@ def _compiled_plans(offsets: Tensor, plans: Tensor, data: Tensor, plan_count: in
             at = np.cumsum([0] + [p.size for p in parts])
             tables = (torch.from_numpy(np.concatenate(parts).view(np.int32)).to(dev),
                       tuple(int(x) for x in at[:4]), bool((found[2] >> 31).all()))
-    hit = (programs, tables, n_clauses)
+        no_stack = bool((hdr[:, 0] != 2).all())  # (status 2: the stack evaluation)
+    hit = (programs, tables, n_clauses, no_stack)
     _COMPILED[key] = hit
     for t in (plans, offsets):
         weakref.finalize(t, _COMPILED.pop, key, None)
@@ -374,20 +376,20 @@ def _compiled_plans(offsets: Tensor, plans: Tensor, data: Tensor, plan_count: in
 def _search_compiled(bloom_index: Tensor, offsets: Tensor, plans: Tensor, data: Tensor,
                      plan_count: int, max_stack: int, k: int, hash_k: int, compiled,
                      out: Tensor, transposed: bool) -> None:
-    programs, tables, n_clauses = compiled
+    programs, tables, n_clauses, no_stack = compiled
     dev = bloom_index.device
     lib = nat.lib()
-    ptrs, every = [None] * 4, 0
+    ptrs, flags = [None] * 4, 2 if no_stack else 0
     if tables is not None:
         base, at = nat.ptr(tables[0]), tables[1]
         ptrs = [base + 4 * a for a in at]  # clause_ptr, plan_desc, plan_refs, clause_terms
-        every = int(tables[2])
+        flags |= 1 if tables[2] else 0
     with torch.cuda.device(dev):
         nat.check(lib.rt_bloom_search_compiled(
             nat.ptr(bloom_index), nat.ptr(offsets), offsets.numel() - 1, nat.ptr(plans),
             nat.ptr(data), data.numel() * 8, plan_count, max_stack, k, hash_k,
             nat.ptr(programs), programs.numel(), ptrs[0], ptrs[3], ptrs[1], ptrs[2], n_clauses,
-            every, None if transposed else nat.ptr(out), nat.ptr(out) if transposed else None,
+            flags, None if transposed else nat.ptr(out), nat.ptr(out) if transposed else None,
             out.shape[1] if transposed else 0, nat.stream(dev)))
 
 
