@@ -177,6 +177,8 @@ class Filter:
         self.words, self.offs = torch.ops.st.bloom_index_build_fixed(fid, fo, fv, BLOOM_BITS,
                                                                      BLOOM_K)
         del fid, fo, fv
+        # the row view the scans' per-candidate probe reads, built once beside the index
+        self.doc_bits = torch.ops.retrieve_amd.bloom_doc_bits(self.words, self.offs, n)
         self.blob, self.plan_count, self.max_stack = st.prepare_plans(
             bl.sets_to_expressions(sets), HASH_K, dev)
         self.rev = torch.zeros(len(CARDINALITIES), dtype=torch.bool, device=dev)
@@ -201,14 +203,24 @@ class Filter:
         return st.bloom_search_t(self.words, self.offs, self.blob, self.plan_count,
                                  self.max_stack, BLOOM_K, HASH_K)
 
+    def scan(self, queries: torch.Tensor, items: torch.Tensor, k: int):
+        """One batch's filtered top-k with the Bloom plans probed per candidate inside the scan,
+        then the exact clauses (``scan_topk_bloom_clauses``): no Bloom mask is written."""
+        return torch.ops.retrieve_amd.scan_topk_bloom_clauses(
+            queries, items, k, self.attrs, self.rev, self.sets, self.doc_bits, self.words,
+            self.offs, self.blob, self.plan_count, self.max_stack, BLOOM_K, HASH_K)
+
     def mask(self) -> torch.Tensor:
         """One batch's filter: Bloom pre-filter, then the exact post-check of its survivors."""
         return torch.ops.retrieve_amd.clause_bits(self.attrs, self.rev, self.sets, self.bloom())
 
-    def bytes(self, n: int, b: int, fused: bool = False) -> int:
+    def bytes(self, n: int, b: int, fused: bool = False, probed: bool = False) -> int:
         """Algorithmic bytes of one batch's filter: the Bloom words and the Bloom mask written;
         unfused, also the int16 attributes, the Bloom mask read and the clause mask written
-        (the scan's mask words, and fused its attribute reads, are sparse: candidates only)."""
+        (the scan's mask words, and fused its attribute reads, are sparse: candidates only);
+        probed, nothing but the candidates' row bits and attributes (sparse)."""
+        if probed:
+            return 0
         if fused:
             return n * BLOOM_BITS // 8 + b * n // 8
         return n * BLOOM_BITS // 8 + n * len(CARDINALITIES) * 2 + 3 * b * n // 8
@@ -365,6 +377,10 @@ def main() -> int:
     ap.add_argument("--unfused-filter", action="store_true",
                     help="filtered workloads: write the clause-checked mask before the scan "
                          "instead of checking the clauses inside it")
+    ap.add_argument("--bloom-search", action="store_true",
+                    help="filtered: search the Bloom index for the batch's mask first, then "
+                         "scan under it (default: the Bloom plans are probed per candidate "
+                         "inside the scan)")
     ap.add_argument("--cpu-sample", type=int, default=None,
                     help="items of the CPU baseline's bounded sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -416,13 +432,16 @@ def main() -> int:
                 return torch.ops.retrieve_amd.int8_scan_topk(queries, items, k)
             if args.unfused_filter:
                 return torch.ops.retrieve_amd.int8_scan_topk(queries, items, k, flt.mask())
-            return torch.ops.retrieve_amd.int8_scan_topk_clauses(queries, items, k, flt.attrs,
-                                                            flt.rev, flt.sets, flt.bloom())
+            if args.bloom_search:
+                return torch.ops.retrieve_amd.int8_scan_topk_clauses(
+                    queries, items, k, flt.attrs, flt.rev, flt.sets, flt.bloom())
+            return flt.scan(queries, items, k)
 
         scan_bytes = n * d + b * d  # the item table once + the query block
         table = items  # the streamed table (the read ceiling is measured over it)
         scan_ops = 2 * b * n * d
-        step_bytes = scan_bytes + (flt.bytes(n, b, not args.unfused_filter) if flt else 0)
+        probed = not (args.unfused_filter or args.bloom_search)
+        step_bytes = scan_bytes + (flt.bytes(n, b, not args.unfused_filter, probed) if flt else 0)
         bound = "hbm" if 2 * b < 625 else "mfma"  # int8 ridge: 625 OP/B
         dtype = "int8"
         data = ("synthetic: per-row int8 of N(0,1) float32 rows (torch generator seeds 1234 / "
@@ -434,7 +453,10 @@ def main() -> int:
                         f"{BLOOM_K} hashes pre-filter + exact AND-of-OR clause post-check over 8 "
                         f"attributes at {args.selectivity:.0%} target selectivity"
                         + ("; the clause mask written before the scan" if args.unfused_filter
-                           else "; the clauses checked inside the scan"))
+                           else "; the Bloom search's mask, the clauses checked inside the scan"
+                           if args.bloom_search else
+                           "; the Bloom plans probed and the clauses checked inside the scan, "
+                           "per candidate"))
             extra["measured_selectivity"] = float(flt.selectivity.mean())
         metric = ("queries/sec + achieved HBM GB/s, filtered top-100 over 30Mx512 int8 items"
                   if flt else "queries/sec + achieved HBM GB/s, int8 top-100 over 30Mx512 items")

@@ -13,9 +13,13 @@ Pinned by:
   ``0:100 AND NOT 1:201``, ``0:102 OR 1:203`` → hits ``[[0,1,3],[1,3],[2,3]]``,
   ``retrieve/tests/parity/test_official.py:229-245, 353-366``) and the expression mapping
   known answer (``test_official.py:510-514``).
-- Bloom words are not pinned bit for bit against the reference's C++ builder, which needs
-  libtorch and is not built here: the per-word layout is pinned by the hand-computed position
-  and the invariants above only ("parity unpinned" for word-level equality with Meta's build).
+- Bloom words: bit for bit against Meta's CPU builder and search, compiled from the reference's
+  sources into ``oracle/_ref`` (fixtures ``tests/golden/ref_cpu.npz``,
+  ``tests/test_ref_fixtures.py``), at the upstream widths; the fixed-width build (CUDA-only in
+  the reference) by the same position rule, the hand-computed position and the invariants.
+- ``bloom_doc_bits`` (the row view of the bundles): against each document's positions computed
+  from its tokens directly (``bit_positions``), independent of the word layout, and the term
+  test on it against ``term_mask`` (``tests/test_oracle.py``).
 """
 
 from __future__ import annotations
@@ -245,6 +249,28 @@ def term_mask(
             ok &= bool((word >> (63 - d % 64)) & 1)
         out[d] = ok
     return out
+
+
+def bloom_doc_bits(words: np.ndarray, offsets: np.ndarray, n_docs: int) -> np.ndarray:
+    """``[n_docs]`` int64: doc ``d``'s bits in one word, position ``p`` at bit ``p`` -- the row
+    view of the bundle layout (``bloom_indexer.cpp:79-110``: position ``p`` of doc ``d`` is word
+    ``(offsets[β] + p) * 32 + (d % 2048) // 64``, bit ``63 - d % 64``). Bundles up to 64 bits
+    wide; no counterpart in the reference (the fused scans' probe reads it)."""
+    w = np.asarray(words).view(np.uint64)
+    out = np.zeros(n_docs, np.uint64)
+    t = np.arange(DOCS_PER_BUNDLE)
+    col, shift = t // 64, (63 - t % 64).astype(np.uint64)
+    for beta in range(-(-n_docs // DOCS_PER_BUNDLE)):
+        o, b = int(offsets[beta]), int(offsets[beta + 1] - offsets[beta])
+        if b > 64:
+            raise ValueError("bundles wider than 64 bits have no one-word row view")
+        m = min(DOCS_PER_BUNDLE, n_docs - beta * DOCS_PER_BUNDLE)
+        f = np.zeros(m, np.uint64)
+        for p in range(b):
+            row = w[(o + p) * WORDS_PER_BUNDLE : (o + p + 1) * WORDS_PER_BUNDLE]
+            f |= ((row[col[:m]] >> shift[:m]) & np.uint64(1)) << np.uint64(p)
+        out[beta * DOCS_PER_BUNDLE : beta * DOCS_PER_BUNDLE + m] = f
+    return out.view(np.int64)
 
 
 # --- expressions (the reference DSL: EXPRESSION_SYNTAX.md grammar) ---------------------------

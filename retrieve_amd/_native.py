@@ -58,6 +58,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_int, _c_i64,
          _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],
     ),
+    "rt_scan_topk_bloom_clauses": (
+        _c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_i64, _c_p, _c_int,
+         _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p],
+    ),
     "rt_blocked_scan_topk_clauses_workspace": (_c_sz, [_c_i64] * 6),
     "rt_blocked_scan_topk_clauses": (
         _c_int,
@@ -97,6 +102,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_sz,
          _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p],
     ),
+    "rt_bloom_doc_bits": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
+    "rt_bloom_probe_search": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
     "rt_mask_compact_workspace": (_c_sz, [_c_i64, _c_i64]),
     "rt_mask_compact": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "rt_cand_topk_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),

@@ -25,6 +25,7 @@
 // its plans (wave-uniform instruction stream), the evaluation stack lives in LDS. When every
 // bundle has the same width a resolve pass first turns each term's stored hashes into its k
 // positions once, so the column pass does no 64-bit division.
+#include "bloom_prog.h"
 #include "rt_common.h"
 
 namespace rt {
@@ -36,6 +37,7 @@ constexpr int kBloomMaxBuildWidth = 256;  // bits per doc the build keeps in reg
 constexpr int kBloomMaxStack = 64;
 constexpr int kBloomThreads = 256;
 constexpr int kBloomMaxSeeds = 4096;  // build: bound on the seeds tried for k distinct positions
+static_assert(kColPosBytes == kBloomWordsPerBundle * sizeof(uint64_t), "a position's column words");
 
 enum BloomOp : uint8_t { kOpAnd = 1, kOpOr = 2, kOpNot = 3, kOpTerm = 4, kOpEmpty = 5 };
 
@@ -258,23 +260,7 @@ __device__ inline void write_column(const BloomSearchArgs& a, int64_t b, int64_t
 
 // ---- plan prep: a program for the column kernel ----------------------------------------
 //
-// Post-order evaluation pushes every child of an n-ary AND / OR before the operator pops them,
-// so an OR of 30 terms needs 30 stack slots. Folding a node's value into its previous sibling
-// as soon as it is complete (AND / OR are associative and commutative) gives the same result
-// with at most one slot per tree level. The prep pass checks each plan exactly as the stack
-// evaluation does (a malformed plan matches nothing), marks every node "push" (a first child,
-// or the root) or "fold into the top with the parent's operator", and writes two program words
-// per op, leaving out the AND / OR nodes flattened into a parent of the same operator (so the
-// fan-out-limited chains of a long value set are one run of folding TERMs). A TERM's positions
-// p (for the width of bundle 0) are stored as the byte offsets
-// p * 256 of their words in a staged bundle column, 14 bits each, the first repeated past the
-// term's distinct positions (AND is idempotent):
-//   word 0: bits 0-1 kind: TERM, EMPTY, PASS (an AND / OR whose children are folded into the
-//           top: pop it), NOT (pop, invert); bits 2-3 place: push, AND into the top, OR into
-//           the top; bits 4-17 offset 0; bits 18-31 offset 1
-//   word 1: bits 0-13 offset 2; bits 16-29 offset 3
-// Plans the program cannot hold (more than kFoldDepth levels, more than 4 positions a term,
-// bundle 0 wider than 64 bits, more than kProgMaxOps ops) are left to the stack evaluation.
+// The program format is bloom_prog.h's.
 //
 // Clauses: a batch's plans are mostly ANDs of value-set clauses (an OR of terms, a term, or the
 // NOT of either), and plans repeat clauses (a popular value set). A host pass over the compiled
@@ -282,18 +268,11 @@ __device__ inline void write_column(const BloomSearchArgs& a, int64_t b, int64_t
 // (the same set of stored hash lists: the same word in every column, whatever the bundle's
 // width). The column kernel's CLAUSES form evaluates each distinct clause once per column into
 // LDS, and such a plan is the AND of a few LDS words; the other plans run their programs.
-constexpr int kFoldDepth = 4;
-constexpr int kProgMaxPos = 4;
-constexpr int kColMaxWidth = 64;
-constexpr int kProgMaxOps = 2048;
-constexpr int kMaxClauses = 128;
+constexpr int kMaxClauses = 128;  // LDS: 128 clauses x 64 columns x 8 bytes beside the staging
 // rt_bloom_search_compiled's plan_flags
 constexpr int64_t kPlansAllClauses = 1;  // every plan is a clause plan
-constexpr int64_t kPlansNoStack = 2;     // no plan takes the stack evaluation  // LDS: 128 clauses x 64 columns x 8 bytes beside the staging
+constexpr int64_t kPlansNoStack = 2;     // no plan takes the stack evaluation
 constexpr int kPrepThreads = 256;
-constexpr uint32_t kColPosBytes = kBloomWordsPerBundle * sizeof(uint64_t);  // 256
-
-enum PlanStatus : int32_t { kPlanProgram = 0, kPlanNone = 1, kPlanStack = 2 };
 
 // A plan's header: its status, op count and first hash word, one 16-byte load for the column
 // kernel (whose program slot sits at a fixed place, so nothing waits on the plan's offsets).
@@ -305,8 +284,6 @@ __device__ inline void write_header(int32_t* hdr, int64_t b, int32_t status, int
   h[2] = static_cast<int32_t>(h0);
   h[3] = static_cast<int32_t>(h0 >> 32);
 }
-enum ProgKind : uint32_t { kKindTerm = 0, kKindEmpty = 1, kKindPass = 2, kKindNot = 3 };
-enum ProgPlace : uint32_t { kPlacePush = 0, kPlaceAnd = 1, kPlaceOr = 2 };
 
 // Block-wide exclusive prefix sum of one value per thread (every thread calls it); total gets
 // the sum over the block. tmp: kPrepThreads / kWave ints of LDS.
@@ -1090,6 +1067,66 @@ __global__ void __launch_bounds__(kBloomThreads) bloom_columns_kernel(BloomColum
   }
 }
 
+// ---- per-document bits and the probe -----------------------------------------------------
+//
+// The row view of the bit-sliced bundles: document d's bits in one word, position p at bit p,
+// for the per-candidate Bloom probe of the fused scans (bloom_prog.h, probe_wave). One
+// workgroup per bundle stages its w * 32 words in LDS; each thread assembles documents t,
+// t + 256, ... of the bundle (a wave's 64 documents share a column: every LDS read is a
+// broadcast). A bundle whose width is not `width` gets all ones, so its documents pass every
+// probe (the programs' positions are bundle 0's).
+__global__ void __launch_bounds__(kBloomThreads) bloom_doc_bits_kernel(const uint64_t* words,
+                                                                       const int64_t* off,
+                                                                       int64_t n_docs,
+                                                                       int64_t width,
+                                                                       uint64_t* out) {
+  __shared__ uint64_t w[kColMaxWidth * kBloomWordsPerBundle];
+  const int64_t beta = blockIdx.x;
+  const int64_t o0 = off[beta];
+  const int64_t wb = off[beta + 1] - o0;
+  const bool ok = wb == width && wb >= 1 && wb <= kColMaxWidth;
+  const int n = ok ? static_cast<int>(wb) * kBloomWordsPerBundle : 0;
+  for (int i = threadIdx.x; i < n; i += kBloomThreads) w[i] = words[o0 * kBloomWordsPerBundle + i];
+  __syncthreads();
+  const int64_t d0 = beta * kBloomDocsPerBundle;
+  for (int t = threadIdx.x; t < kBloomDocsPerBundle && d0 + t < n_docs; t += kBloomThreads) {
+    uint64_t f = ~0ull;
+    if (ok) {
+      f = 0ull;
+      const uint64_t* col = w + (t >> 6);
+      const int sh = 63 - (t & 63);
+      for (int p = 0; p < static_cast<int>(wb); ++p) {
+        f |= ((col[p * kBloomWordsPerBundle] >> sh) & 1ull) << p;
+      }
+    }
+    out[d0 + t] = f;
+  }
+}
+
+// Every plan over every document through the probe: wave <-> 64 documents of one plan (grid
+// y), one word of the scans' mask layout each, the wave evaluating its documents one at a time.
+// Documents at or past n_docs are 0.
+__global__ void __launch_bounds__(kBloomThreads) bloom_probe_search_kernel(BloomProbe p,
+                                                                           int64_t n_docs,
+                                                                           int64_t n_words,
+                                                                           int64_t* out) {
+  const int lane = lane_id();
+  const int64_t word = static_cast<int64_t>(blockIdx.x) * (kBloomThreads / kWave) +
+                       (threadIdx.x >> 6);
+  const int64_t b = blockIdx.y;
+  if (word >= n_words) return;  // (wave-uniform)
+  const int64_t d = word * 64 + lane;
+  const uint64_t mine = d < n_docs ? p.doc_bits[d] : 0ull;
+  const uint64_t* t = p.tables + p.tables[b];
+  bool hit = false;
+  for (int l = 0; l < kWave; ++l) {
+    const bool pass = probe_wave(t, readlane64(mine, l), lane);
+    if (lane == l) hit = pass && d < n_docs;
+  }
+  const uint64_t bits = __ballot(hit);
+  if (lane == 0) out[b * n_words + word] = static_cast<int64_t>(__builtin_bitreverse64(bits));
+}
+
 }  // namespace rt
 
 using namespace rt;
@@ -1179,8 +1216,8 @@ static BloomSearchArgs bloom_args(const uint64_t* words, const int64_t* bundle_b
   a.hash_k = static_cast<int>(hash_k);
   a.words_aligned16 = reinterpret_cast<uintptr_t>(words) % 16 == 0;
   a.hdr = static_cast<int32_t*>(compiled);
-  a.prog = reinterpret_cast<uint32_t*>(
-      static_cast<char*>(compiled) + align_up(static_cast<size_t>(plan_count) * 16, 256));
+  a.prog = reinterpret_cast<uint32_t*>(static_cast<char*>(compiled) +
+                                       compiled_prog_offset(plan_count));
   return a;
 }
 
@@ -1213,7 +1250,8 @@ static int bloom_compile_into(const BloomSearchArgs& a, hipStream_t stream) {
 }
 
 // The searches over compiled plans: the column kernel (programs; with a.n_clauses > 0 the
-// plans of clauses over the batch's distinct clauses)// terms), then the stack evaluation of the rest; any of the three outputs.
+// plans of clauses over the batch's distinct clauses), then the stack evaluation of the rest;
+// any of the three outputs.
 static int bloom_run(BloomSearchArgs a, hipStream_t stream, bool stack_plans = true) {
   const int64_t n_bundles = a.nb;
   const int64_t plan_count = a.plan_count;
@@ -1388,6 +1426,48 @@ extern "C" int rt_bloom_search_compiled(const uint64_t* words, const int64_t* bu
   a.n_clauses = static_cast<int>(n_clauses);
   a.all_clauses = n_clauses > 0 && (plan_flags & kPlansAllClauses) != 0;
   return bloom_run(a, stream, (plan_flags & kPlansNoStack) == 0);
+}
+
+extern "C" int rt_bloom_doc_bits(const uint64_t* words, const int64_t* bundle_b_offsets,
+                                 int64_t n_bundles, int64_t n_docs, int64_t width,
+                                 uint64_t* out_doc_bits, hipStream_t stream) {
+  RT_CHECK_ARG(n_bundles >= 0 && n_docs >= 0, "sizes must be >= 0");
+  RT_CHECK_ARG(n_docs <= n_bundles * kBloomDocsPerBundle,
+               "n_docs %lld is above the index's %lld bundles of %d documents",
+               static_cast<long long>(n_docs), static_cast<long long>(n_bundles),
+               kBloomDocsPerBundle);
+  RT_CHECK_ARG(width >= 1 && width <= kColMaxWidth, "width must be in [1, %d], got %lld",
+               kColMaxWidth, static_cast<long long>(width));
+  if (n_docs == 0) return kOk;
+  RT_CHECK_ARG(words != nullptr && bundle_b_offsets != nullptr && out_doc_bits != nullptr,
+               "words, bundle offsets and the output must not be null");
+  const int64_t grid = cdiv(n_docs, kBloomDocsPerBundle);
+  RT_CHECK_ARG(grid < (int64_t{1} << 31), "too many bundles");
+  bloom_doc_bits_kernel<<<static_cast<unsigned>(grid), kBloomThreads, 0, stream>>>(
+      words, bundle_b_offsets, n_docs, width, out_doc_bits);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
+extern "C" int rt_bloom_probe_search(const uint64_t* doc_bits, int64_t n_docs,
+                                     const uint64_t* probe_tables, int64_t plan_count,
+                                     int64_t* out_mask, hipStream_t stream) {
+  RT_CHECK_ARG(n_docs >= 0 && plan_count >= 0, "sizes must be >= 0");
+  RT_CHECK_ARG(plan_count <= 65535, "plan_count must be <= 65535, got %lld",
+               static_cast<long long>(plan_count));
+  const int64_t n_words = cdiv(n_docs, 64);
+  if (n_words == 0 || plan_count == 0) return kOk;
+  RT_CHECK_ARG(doc_bits != nullptr && probe_tables != nullptr && out_mask != nullptr,
+               "doc_bits, probe_tables and out_mask must not be null");
+  BloomProbe p;
+  p.doc_bits = doc_bits;
+  p.tables = probe_tables;
+  const int64_t gx = cdiv(n_words, kBloomThreads / kWave);
+  RT_CHECK_ARG(gx < (int64_t{1} << 31), "too many documents");
+  bloom_probe_search_kernel<<<dim3(static_cast<unsigned>(gx), static_cast<unsigned>(plan_count)),
+                              kBloomThreads, 0, stream>>>(p, n_docs, n_words, out_mask);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
 }
 
 extern "C" int rt_bloom_search_columns(const uint64_t* words, const int64_t* bundle_b_offsets,

@@ -100,7 +100,8 @@ ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int64_t qpg, int64_t lists_p
   s.off_lists = 0;
   s.off_counts = align_up(lists, 256);
   s.off_tau = s.off_counts + align_up(counts, 256);
-  s.total = s.off_tau + align_up(static_cast<size_t>(B) * sizeof(uint64_t), 256);
+  s.off_flag = s.off_tau + align_up(static_cast<size_t>(B) * sizeof(uint64_t), 256);
+  s.total = s.off_flag + 256;
   return s;
 }
 
@@ -409,7 +410,8 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     }
   }
 
-  if (m.spec_flag != nullptr && tid == 0 && buf[k - 1] == 0ull && m.spec_tau[q] > m.safe_tau[q]) {
+  if (m.spec_flag != nullptr && tid == 0 && buf[k - 1] == 0ull &&
+      m.spec_tau[q] > (m.safe_tau != nullptr ? m.safe_tau[q] : 0ull)) {
     atomicOr(m.spec_flag, 1u);
   }
   for (int j = tid; j < k; j += kMergeThreads) {

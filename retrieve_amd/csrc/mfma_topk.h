@@ -41,6 +41,17 @@ struct WaveTopK16 {
   ClauseCheck clause;      // exact clauses tested per candidate, where `clauses`
   ClauseRow crow;          // this lane's query's clause state
   bool clauses;
+  // the Bloom plan of this lane's query (its clause table, an LDS copy or the tables' global
+  // copy), probed per candidate by the whole wave where `probing` (after the clauses: the
+  // filter is their AND, and the clause test is one attribute-row load; a passing candidate's
+  // row bits are one uniform load); probe_on (wave-uniform) false: no probe
+  const uint64_t* doc_bits = nullptr;
+  const uint64_t* table = nullptr;  // this lane's query's table (global memory)
+  lds_cu64* lds = nullptr;          // the group's tables in LDS, when tables_lds (uniform)
+  int lds_at = 0;                   // this lane's query's table there
+  bool tables_lds = false;
+  bool probe_on = false;
+  bool probing = false;
 
   __device__ void set_tau(uint64_t t) {
     tau = t;
@@ -48,11 +59,11 @@ struct WaveTopK16 {
   }
 
   // Scores acc[r] of rows row0 + r (r < 4) for this lane's query; rows >= r1 are past the
-  // pass. item = row * row_stride. Appends composites >= tau that pass the mask and the
-  // clauses (tested only for such composites); compacts lists that could overflow on the next
-  // tile. The filters run once per tile for all four rows: one mask word when the rows are
-  // four consecutive items from a multiple of four (they share a word), and the clause tests
-  // one candidate per lane per pass (a wave rarely has more than one per lane).
+  // pass. item = row * row_stride. Appends composites >= tau that pass the mask, the clauses
+  // and the Bloom probe (tested only for such composites); compacts lists that could overflow
+  // on the next tile. The filters run once per tile for all four rows: one mask word when the
+  // rows are four consecutive items from a multiple of four (they share a word), and the clause
+  // and probe tests one candidate per lane per pass (a wave rarely has more than one per lane).
   __device__ void push(const Score acc[4], int64_t row0, int64_t r1, int64_t row_stride) {
     const Score m01 = acc[0] > acc[1] ? acc[0] : acc[1];
     const Score m23 = acc[2] > acc[3] ? acc[2] : acc[3];
@@ -85,13 +96,35 @@ struct WaveTopK16 {
         }
       }
     }
-    uint32_t todo = clauses ? cand : 0u;
+    uint32_t todo = clauses || probing ? cand : 0u;
     while (__any(todo != 0u)) {
+      int r = -1;
+      bool ok = false;
       if (todo != 0u) {
-        const int r = __builtin_ctz(todo);
+        r = __builtin_ctz(todo);
         todo &= todo - 1u;
-        if (!clause_pass(clause, crow, (row0 + r) * row_stride)) cand &= ~(1u << r);
+        ok = !clauses || clause_pass(clause, crow, (row0 + r) * row_stride);
       }
+      if (probe_on) {  // each candidate that passed, one at a time, by the whole wave
+        const uint64_t item = static_cast<uint64_t>((row0 + (r < 0 ? 0 : r)) * row_stride);
+        uint64_t need = __ballot(ok && probing);
+        while (need != 0ull) {
+          const int l = static_cast<int>(__builtin_ctzll(need));
+          need &= need - 1ull;
+          // the candidate's row bits: one uniform (scalar) load, waited for on its own
+          const uint64_t f = doc_bits[readlane64(item, l)];
+          bool pass;
+          if (tables_lds) {
+            pass = probe_wave(lds + __builtin_amdgcn_readlane(lds_at, l), f, lane_id());
+          } else {
+            const uint64_t* t = reinterpret_cast<const uint64_t*>(
+                readlane64(reinterpret_cast<uint64_t>(table), l));
+            pass = probe_wave(t, f, lane_id());
+          }
+          if (lane_id() == l) ok = pass;
+        }
+      }
+      if (r >= 0 && !ok) cand &= ~(1u << r);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {

@@ -9,6 +9,7 @@
 //   4. final merge: the exact top-k over the main scan's lists.
 #pragma once
 
+#include "bloom_prog.h"
 #include "clause_check.h"
 #include "rt_common.h"
 
@@ -47,6 +48,9 @@ struct ScanArgs {
   int* counts;             // [slots, qpw]
   ClauseCheck clause;      // exact clauses tested per candidate (active null: none; the
                            // scans of scan_mfma.hip)
+  BloomProbe probe;        // Bloom plans probed per candidate, plan b for query b (doc_bits
+                           // null: none; the scans of scan_mfma.hip)
+  int probe_lds;           // main pass: the query group's Bloom clause tables copied to LDS
   int clause_lds;          // main pass: the query group's set bitmaps copied to LDS
   const uint32_t* run_if;  // not null: the pass runs only if *run_if != 0 (a fallback pass)
 };
@@ -75,7 +79,7 @@ struct MergeArgs {
   // sets it (its scan may have dropped items between the two bounds).
   uint32_t* spec_flag;
   const uint64_t* spec_tau;
-  const uint64_t* safe_tau;
+  const uint64_t* safe_tau;  // null: 0 (no bound)
   int64_t* out_ids;    // final mode: [B, k]
   void* out_scores;    // final mode: [B, k]
   int score_kind;
@@ -113,7 +117,7 @@ struct ScanPlan {
   PassPlan seed;
   PassPlan main;
   // workspace layout (byte offsets)
-  size_t off_lists = 0, off_counts = 0, off_tau = 0, total = 0;
+  size_t off_lists = 0, off_counts = 0, off_tau = 0, off_flag = 0, total = 0;
 };
 
 // Upper bound on a main pass's workgroups (the workspace functions size for it).

@@ -179,12 +179,18 @@ constexpr size_t main_static_lds() {
   return static_cast<size_t>(kScanWaves) * kTile * tile_pitch<KSTEPS>();
 }
 
+// LDS of the clause bitmaps a main-pass workgroup copies (its 16 queries).
+__host__ __device__ inline size_t clause_lds_bytes(int C) {
+  return static_cast<size_t>(16) * C * kSetWords * sizeof(uint64_t);
+}
+
 // Main pass: every item (row_stride 1), candidate lists per wave.
 template <class Op, int KSTEPS>
 __global__ void __launch_bounds__(kScanThreads) scan_mfma_kernel(ScanArgs a) {
   using Score = typename Op::Score;
   constexpr int64_t D = KSTEPS * 64;  // row bytes
   constexpr int P = tile_pitch<KSTEPS>();
+  if (a.run_if != nullptr && *a.run_if == 0u) return;  // (uniform: the fallback is not needed)
   constexpr int LOADS = KSTEPS;  // 16-byte loads per lane per tile: 16 * D / 1024
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   const int lane = lane_id();
@@ -231,6 +237,33 @@ __global__ void __launch_bounds__(kScanThreads) scan_mfma_kernel(ScanArgs a) {
       bm = lds_bm + col * per_row;
     }
     if (top.clauses) top.crow = clause_row(a.clause, qrow, bm);
+  }
+  if (a.probe.doc_bits != nullptr) {
+    // the group's Bloom clause tables copied to LDS (after the set bitmaps) while they fit, in
+    // query order; the others are read where they are
+    uint64_t* tl = reinterpret_cast<uint64_t*>(
+        base + main_static_lds<KSTEPS>() + kScanWaves * a.capw * sizeof(uint64_t) +
+        kScanWaves * 16 * sizeof(int) + (a.clause_lds ? clause_lds_bytes(a.clause.C) : 0));
+    const int cap = a.probe_lds / static_cast<int>(sizeof(uint64_t));
+    const uint64_t* tables = a.probe.tables;
+    const int64_t g0 = static_cast<int64_t>(blockIdx.y) * 16;
+    const int64_t g1 = g0 + 16 < a.B ? g0 + 16 : a.B;
+    const int64_t o0 = static_cast<int64_t>(tables[g0]);
+    const int words = static_cast<int>(static_cast<int64_t>(tables[g1]) - o0);
+    top.tables_lds = words <= cap;  // (uniform: the group's tables are contiguous)
+    if (top.tables_lds) {
+      for (int w = threadIdx.x; w < words; w += kScanThreads) tl[w] = tables[o0 + w];
+      __syncthreads();
+      top.lds = (lds_cu64*)(tl);
+    }
+    if (qrow < a.B) {
+      const int64_t o = static_cast<int64_t>(tables[qrow]);
+      top.table = tables + o;
+      top.lds_at = static_cast<int>(o - o0);
+    }
+    top.doc_bits = a.probe.doc_bits;
+    top.probe_on = true;
+    top.probing = qrow < a.B;
   }
   top.set_tau(qrow < a.B ? (a.tau_in != nullptr ? a.tau_in[qrow] : 0ull) : ~0ull);
   wave_sync_memory();
@@ -296,12 +329,13 @@ static size_t main_lds_bytes(int capw) {
   return main_static_lds<KSTEPS>() + kScanWaves * (capw * sizeof(uint64_t) + 16 * sizeof(int));
 }
 
-// LDS of the clause bitmaps a main-pass workgroup copies (its 16 queries), and the most the main
-// pass gives them: they are copied only while two workgroups still fit a CU.
-static size_t clause_lds_bytes(int C) {
-  return static_cast<size_t>(16) * C * kSetWords * sizeof(uint64_t);
-}
+// The most the main pass gives the LDS copies below: they are made only while two workgroups
+// still fit a CU.
 constexpr size_t kMainLdsForTwo = 80 * 1024;
+// LDS for a main-pass workgroup's copies of its queries' Bloom clause tables: none below the
+// minimum, at most the maximum, within the two-workgroup budget.
+constexpr size_t kProbeLdsMin = 4 * 1024;
+constexpr size_t kProbeLdsMax = 24 * 1024;
 
 template <class Op, int KSTEPS>
 static int launch_mfma(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, bool seed,
@@ -317,6 +351,12 @@ static int launch_mfma(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, 
   m.clause_lds =
       a.clause.active != nullptr && lds + clause_lds_bytes(a.clause.C) <= kMainLdsForTwo;
   if (m.clause_lds) lds += clause_lds_bytes(a.clause.C);
+  m.probe_lds = 0;
+  if (a.probe.doc_bits != nullptr && lds + kProbeLdsMin <= kMainLdsForTwo) {
+    const size_t room = kMainLdsForTwo - lds;
+    m.probe_lds = static_cast<int>((room < kProbeLdsMax ? room : kProbeLdsMax) / 16 * 16);
+    lds += m.probe_lds;
+  }
   if (lds > 65536) {
     RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(scan_mfma_kernel<Op, KSTEPS>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -355,7 +395,8 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
                          int64_t row_bytes, int64_t k, const uint64_t* mask, int64_t mask_words,
                          int64_t* out_ids, void* out_scores, void* workspace,
                          size_t workspace_bytes, hipStream_t stream,
-                         const ClauseCheck& clause = ClauseCheck{}) {
+                         const ClauseCheck& clause = ClauseCheck{},
+                         const BloomProbe& probe = BloomProbe{}) {
   RT_CHECK_ARG(B >= 0 && N >= 0, "B and N must be >= 0");
   RT_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be in [1, %lld], got %lld",
                static_cast<long long>(kMaxK), static_cast<long long>(k));
@@ -379,6 +420,13 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   uint64_t* lists = reinterpret_cast<uint64_t*>(ws + plan.off_lists);
   int* counts = reinterpret_cast<int*>(ws + plan.off_counts);
   uint64_t* tau = reinterpret_cast<uint64_t*>(ws + plan.off_tau);
+  uint32_t* spec_flag = reinterpret_cast<uint32_t*>(ws + plan.off_flag);
+  // With the Bloom probe the seed takes its bound over the exact clauses alone (a sampled item
+  // that passes them is not probed), which bounds the filter's k-th best only where the plans
+  // pass every item the clauses pass. A query that then ends with fewer than k entries behind a
+  // bound above 0 raises a flag, and a fallback main pass and merge without the bound (both
+  // returning at once while the flag is clear) keep the results exact.
+  const bool speculative = plan.seeded && probe.doc_bits != nullptr;
 
   ScanArgs a{};
   a.queries = queries;
@@ -411,11 +459,14 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
     m.flat = true;  // one entry per seed wave, contiguous per query
     m.S = plan.seed.S;
     m.tau_out = tau;
+    m.spec_flag = speculative ? spec_flag : nullptr;  // (cleared)
     st = launch_merge(m, stream);
     if (st != kOk) return st;
     m.tau_out = nullptr;
     m.flat = false;
+    m.spec_flag = nullptr;
   }
+  a.probe = probe;
   a.n_rows = N;
   a.row_stride = 1;
   a.strip = plan.main.strip;
@@ -432,6 +483,19 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   m.out_ids = out_ids;
   m.out_scores = out_scores;
   m.score_kind = Op::kind;
+  if (speculative) {
+    m.spec_flag = spec_flag;
+    m.spec_tau = tau;
+    m.safe_tau = nullptr;
+  }
+  st = launch_merge(m, stream);
+  if (st != kOk || !speculative) return st;
+  a.tau_in = nullptr;
+  a.run_if = spec_flag;
+  st = dispatch_mfma<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, stream);
+  if (st != kOk) return st;
+  m.spec_flag = nullptr;
+  m.run_if = spec_flag;
   return launch_merge(m, stream);
 }
 
@@ -537,13 +601,15 @@ extern "C" size_t rt_scan_topk_clauses_workspace(int64_t B, int64_t N, int64_t D
   return align_up(mfma_plan_bytes(B, N, k), 256) + clause_prep_workspace(B, C, V);
 }
 
-extern "C" int rt_scan_topk_clauses(const void* queries, int64_t B, const void* items, int64_t N,
-                                    int64_t D, int64_t k, int dtype, const uint64_t* mask,
-                                    int64_t mask_words, const void* item_attrs, int attr_bytes,
-                                    int64_t C, int64_t A, const int8_t* clause_is_reverse,
-                                    const int64_t* query_values, int64_t V, int64_t* out_ids,
-                                    void* out_scores, void* workspace, size_t workspace_bytes,
-                                    hipStream_t stream) {
+// The clause scans' shared body: rt_scan_topk_clauses (mask) and rt_scan_topk_bloom_clauses
+// (Bloom probe).
+static int scan_clauses(const void* queries, int64_t B, const void* items, int64_t N, int64_t D,
+                        int64_t k, int dtype, const uint64_t* mask, int64_t mask_words,
+                        const BloomProbe& probe, const void* item_attrs, int attr_bytes,
+                        int64_t C, int64_t A, const int8_t* clause_is_reverse,
+                        const int64_t* query_values, int64_t V, int64_t* out_ids,
+                        void* out_scores, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
   RT_CHECK_ARG(dtype >= 0 && dtype <= 2, "dtype must be 0 (int8), 1 (bf16) or 2 (fp16), got %d",
                dtype);
   RT_CHECK_ARG(B >= 0 && N >= 0 && k >= 1 && k <= kMaxK, "B, N >= 0 and k in [1, %lld]",
@@ -577,14 +643,44 @@ extern "C" int rt_scan_topk_clauses(const void* queries, int64_t B, const void* 
   }
   if (dtype == 0) {
     return run_mfma_scan<I8Op>(queries, B, items, N, D, k, mask, mask_words, out_ids,
-                               out_scores, workspace, scan_bytes, stream, f);
+                               out_scores, workspace, scan_bytes, stream, f, probe);
   }
   if (dtype == 1) {
     return run_mfma_scan<BF16Op>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
-                                 out_scores, workspace, scan_bytes, stream, f);
+                                 out_scores, workspace, scan_bytes, stream, f, probe);
   }
   return run_mfma_scan<F16Op>(queries, B, items, N, 2 * D, k, mask, mask_words, out_ids,
-                              out_scores, workspace, scan_bytes, stream, f);
+                              out_scores, workspace, scan_bytes, stream, f, probe);
+}
+
+extern "C" int rt_scan_topk_clauses(const void* queries, int64_t B, const void* items, int64_t N,
+                                    int64_t D, int64_t k, int dtype, const uint64_t* mask,
+                                    int64_t mask_words, const void* item_attrs, int attr_bytes,
+                                    int64_t C, int64_t A, const int8_t* clause_is_reverse,
+                                    const int64_t* query_values, int64_t V, int64_t* out_ids,
+                                    void* out_scores, void* workspace, size_t workspace_bytes,
+                                    hipStream_t stream) {
+  return scan_clauses(queries, B, items, N, D, k, dtype, mask, mask_words, BloomProbe{},
+                      item_attrs, attr_bytes, C, A, clause_is_reverse, query_values, V, out_ids,
+                      out_scores, workspace, workspace_bytes, stream);
+}
+
+extern "C" int rt_scan_topk_bloom_clauses(
+    const void* queries, int64_t B, const void* items, int64_t N, int64_t D, int64_t k,
+    int dtype, const uint64_t* doc_bits, const uint64_t* probe_tables, int64_t plan_count,
+    const void* item_attrs, int attr_bytes, int64_t C, int64_t A,
+    const int8_t* clause_is_reverse, const int64_t* query_values, int64_t V, int64_t* out_ids,
+    void* out_scores, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  RT_CHECK_ARG(plan_count == B, "one Bloom plan per query: plan_count %lld != B %lld",
+               static_cast<long long>(plan_count), static_cast<long long>(B));
+  RT_CHECK_ARG(N == 0 || B == 0 || (doc_bits != nullptr && probe_tables != nullptr),
+               "doc_bits and probe_tables must not be null");
+  BloomProbe probe;
+  probe.doc_bits = doc_bits;
+  probe.tables = probe_tables;
+  return scan_clauses(queries, B, items, N, D, k, dtype, nullptr, 0, probe, item_attrs,
+                      attr_bytes, C, A, clause_is_reverse, query_values, V, out_ids, out_scores,
+                      workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t rt_dense_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {

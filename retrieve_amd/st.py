@@ -232,6 +232,100 @@ _PROG_MAX_OPS = 2048  # program words per plan (kProgMaxOps)
 _AND, _OR, _NOT, _TERM, _EMPTY = bl.AND, bl.OR, bl.NOT, bl.TERM, bl.EMPTY
 
 
+def _plan_clauses(words: np.ndarray, plan_count: int, b: int, hdr: np.ndarray,
+                  prog: np.ndarray):
+    """Program plan ``b``'s tree as ``[(terms, negated)]`` (AND of clauses; ``terms`` the
+    ordinals of its TERM ops, which number the program's TERM words) or None when it is not of
+    that form, and the TERM program words (kind TERM, place push; positions only)."""
+    offs = words[: 8 * plan_count].reshape(plan_count, 8)
+    data = words[8 * plan_count :].view(np.uint8)
+    o = offs[b]
+    ops = data[o[0] : o[1]]
+    ends = data[o[2] : o[3]].view(np.int32)
+    params = data[o[4] : o[5]].view(np.int32)
+    pw = prog[b, : hdr[b, 1]]
+    is_term = (pw[:, 0] & 3) == 0
+    tw0 = pw[is_term, 0] & np.uint32(0xFFFFFFF0)  # kind TERM, place push
+    tw1 = pw[is_term, 1]
+    ordinal = np.cumsum(ops == _TERM) - 1
+
+    def children(i):
+        return params[ends[i] : ends[i + 1]].tolist()
+
+    def or_terms(i):
+        if ops[i] == _TERM:
+            return [int(ordinal[i])]
+        if ops[i] != _OR:
+            return None
+        out = []
+        for ch in children(i):
+            got = or_terms(ch)
+            if got is None:
+                return None
+            out += got
+        return out
+
+    def clauses(i):
+        if ops[i] == _AND:
+            out = []
+            for ch in children(i):
+                got = clauses(ch)
+                if got is None:
+                    return None
+                out += got
+            return out
+        if ops[i] == _EMPTY:
+            return []
+        neg = ops[i] == _NOT
+        got = or_terms(children(i)[0] if neg else i)
+        return None if got is None else [(got, neg)]
+
+    return clauses(ops.size - 1), tw0, tw1
+
+
+def _term_bits(w0: int, w1: int) -> int:
+    """A TERM's positions (program words: byte offsets p * 256) as a mask over a doc's bits."""
+    offs = ((w0 >> 4) & 0x3FFF, w0 >> 18, w1 & 0x3FFF, (w1 >> 16) & 0x3FFF)
+    return sum({1 << (x // 256) for x in offs})
+
+
+def probe_tables(blob: np.ndarray, plan_count: int, hdr: np.ndarray, prog: np.ndarray):
+    """The clause tables of the scans' per-candidate Bloom probe (``rt_scan_topk_bloom_clauses``;
+    layout in ``csrc/bloom_prog.h``) as one int64 array: each plan's table offset, then per plan
+    a header (matches nothing, chunk count; the clauses in use; the negated ones) and per chunk
+    of 64 terms the terms' position bits and, per clause, the chunk's lanes holding its terms.
+    None when a plan takes the stack evaluation or is not an AND of at most 64 clauses (an OR of
+    terms, a term, or the NOT of either): the probe cannot hold it."""
+    words = np.asarray(blob).view(np.int64)
+    ones = (1 << 64) - 1
+    tables: list = []
+    for b in range(plan_count):
+        if hdr[b, 0] == 1:  # malformed: matches nothing
+            tables.append([1, 0, 0, 0])
+            continue
+        if hdr[b, 0] != 0:
+            return None
+        found, tw0, tw1 = _plan_clauses(words, plan_count, b, hdr, prog)
+        if found is None or len(found) > 64:
+            return None
+        terms = [(_term_bits(int(tw0[t]), int(tw1[t])), j)
+                 for j, (ts, _) in enumerate(found) for t in ts]
+        chunks = -(-len(terms) // 64)
+        neg = sum(1 << j for j, (_, n) in enumerate(found) if n)
+        table = [chunks << 1, (1 << len(found)) - 1, neg, 0]
+        for c in range(chunks):
+            tm, cl = [ones] * 64, [0] * 64
+            for lane, (bits, j) in enumerate(terms[64 * c : 64 * c + 64]):
+                tm[lane] = bits
+                cl[j] |= 1 << lane
+            table += tm + cl
+        tables.append(table)
+    head = plan_count + 1
+    offs = np.cumsum([head] + [len(t) for t in tables])
+    flat = [int(x) for x in offs] + [w for t in tables for w in t]
+    return np.array(flat, np.uint64).view(np.int64)
+
+
 def clause_plans(blob: np.ndarray, plan_count: int, hash_k: int, hdr: np.ndarray,
                  prog: np.ndarray, cap: int = MAX_CLAUSES, min_share: float = 2.0):
     """The clause pass over a batch's compiled plans (``blob`` the prepared int64 words: 8
@@ -247,8 +341,6 @@ def clause_plans(blob: np.ndarray, plan_count: int, hash_k: int, hdr: np.ndarray
     and the index of its stored hashes in the data (uint64 words): term t of a plan is its t-th
     TERM op, as the compiled program numbers them."""
     words = np.asarray(blob).view(np.int64)
-    offs = words[: 8 * plan_count].reshape(plan_count, 8)
-    data = words[8 * plan_count :].view(np.uint8)
     h64 = words[8 * plan_count :].view(np.uint64)
     slots: dict = {}
     clause_terms: list = []
@@ -257,49 +349,8 @@ def clause_plans(blob: np.ndarray, plan_count: int, hash_k: int, hdr: np.ndarray
     for b in range(plan_count):
         if hdr[b, 0] != 0:  # not a program plan (stack path, or no match)
             continue
-        o = offs[b]
-        ops = data[o[0] : o[1]]
-        ends = data[o[2] : o[3]].view(np.int32)
-        params = data[o[4] : o[5]].view(np.int32)
-        pw = prog[b, : hdr[b, 1]]
-        is_term = (pw[:, 0] & 3) == 0
-        tw0 = pw[is_term, 0] & np.uint32(0xFFFFFFF0)  # kind TERM, place push
-        tw1 = pw[is_term, 1]
-        ordinal = np.cumsum(ops == _TERM) - 1
+        found, tw0, tw1 = _plan_clauses(words, plan_count, b, hdr, prog)
         h0 = int(np.uint32(hdr[b, 2])) | (int(hdr[b, 3]) << 32)
-
-        def children(i):
-            return params[ends[i] : ends[i + 1]].tolist()
-
-        def or_terms(i):
-            if ops[i] == _TERM:
-                return [int(ordinal[i])]
-            if ops[i] != _OR:
-                return None
-            out = []
-            for ch in children(i):
-                got = or_terms(ch)
-                if got is None:
-                    return None
-                out += got
-            return out
-
-        def clauses(i):
-            if ops[i] == _AND:
-                out = []
-                for ch in children(i):
-                    got = clauses(ch)
-                    if got is None:
-                        return None
-                    out += got
-                return out
-            if ops[i] == _EMPTY:
-                return []
-            neg = ops[i] == _NOT
-            got = or_terms(children(i)[0] if neg else i)
-            return None if got is None else [(got, neg)]
-
-        found = clauses(ops.size - 1)
         if found is None or len(found) > 0xFFF or len(refs) + len(found) > (1 << 19):
             continue
         first = len(refs)
@@ -371,6 +422,38 @@ def _compiled_plans(offsets: Tensor, plans: Tensor, data: Tensor, plan_count: in
     for t in (plans, offsets):
         weakref.finalize(t, _COMPILED.pop, key, None)
     return hit
+
+
+_PROBES: dict = {}
+
+
+def _probe_tables(offsets: Tensor, plans: Tensor, plan_count: int, max_stack: int, k: int,
+                  hash_k: int):
+    """``probe_tables`` of these plans on the device, built once (False when the probe cannot
+    hold them); None under graph capture with nothing kept."""
+    import weakref
+
+    key = (id(plans), plans._version, id(offsets), offsets._version, plan_count, max_stack, k,
+           hash_k)
+    hit = _PROBES.get(key)
+    if hit is not None or _capturing():
+        return hit
+    compiled = _compiled_plans(offsets, plans, plans[8 * plan_count:], plan_count, max_stack, k,
+                               hash_k)
+    tables = False
+    if min(k, hash_k) <= 4:
+        host = compiled[0].cpu().numpy()
+        start = -(-plan_count * 16 // 256) * 256
+        hdr = host[: plan_count * 16].view(np.int32).reshape(plan_count, 4)
+        prog = host[start : start + plan_count * _PROG_MAX_OPS * 8].view(np.uint32)
+        found = probe_tables(plans.cpu().numpy(), plan_count, hdr,
+                             prog.reshape(plan_count, _PROG_MAX_OPS, 2))
+        if found is not None:
+            tables = torch.from_numpy(found).to(offsets.device)
+    _PROBES[key] = tables
+    for t in (plans, offsets):
+        weakref.finalize(t, _PROBES.pop, key, None)
+    return tables
 
 
 def _search_compiled(bloom_index: Tensor, offsets: Tensor, plans: Tensor, data: Tensor,
@@ -488,6 +571,161 @@ def bloom_search_t(bloom_index: Tensor, bloom_bundle_b_offsets: Tensor, plans: T
     traces under ``torch.compile``.) No counterpart in the reference."""
     return bloom_search_cols(bloom_index, bloom_bundle_b_offsets, plans, plan_count,
                              max_stack_size, k, hash_k).t()[:plan_count]
+
+
+# --- the Bloom pre-filter probed inside the scans -------------------------------------------
+
+_WIDTHS: dict = {}
+
+
+def _uniform_width(offsets: Tensor) -> int | None:
+    """The index's bits per document when every bundle has the same width of 1 to 64, else 0;
+    read back once per offsets tensor (None under graph capture with nothing kept)."""
+    import weakref
+
+    key = (id(offsets), offsets._version)
+    hit = _WIDTHS.get(key)
+    if hit is not None or _capturing():
+        return hit
+    width = 0
+    if offsets.numel() > 1:
+        d = torch.diff(offsets)
+        lo, hi = (int(x) for x in torch.stack([d.min(), d.max()]).cpu())
+        width = lo if lo == hi and 1 <= lo <= 64 else 0
+    _WIDTHS[key] = width
+    weakref.finalize(offsets, _WIDTHS.pop, key, None)
+    return width
+
+
+@torch.library.custom_op("retrieve_amd::bloom_doc_bits", mutates_args=(), device_types="cuda")
+def bloom_doc_bits(bloom_index: Tensor, bloom_bundle_b_offsets: Tensor, n_docs: int) -> Tensor:
+    """Each document's Bloom bits in one int64 word, position ``p`` at bit ``p``
+    (``rt_bloom_doc_bits``): the row view of the bit-sliced index, which the scans' per-candidate
+    Bloom probe reads (``scan_topk_bloom_clauses``). Every bundle must hold the same 1 to 64
+    bits per document (``bloom_index_build_fixed``'s index). Built once per index, beside it; no
+    counterpart in the reference."""
+    if bloom_index.dtype != torch.int64 or bloom_bundle_b_offsets.dtype != torch.int64:
+        raise TypeError("bloom_index and bloom_bundle_b_offsets must be int64")
+    index = bloom_index.contiguous()
+    offsets = bloom_bundle_b_offsets.contiguous()
+    dev = nat.require_device(index, offsets)
+    nb = offsets.numel() - 1
+    if n_docs < 0 or n_docs > max(nb, 0) * DOCS_PER_BUNDLE:
+        raise ValueError(f"n_docs must be in [0, {max(nb, 0) * DOCS_PER_BUNDLE}], got {n_docs}")
+    out = torch.empty(n_docs, dtype=torch.int64, device=dev)
+    if n_docs == 0:
+        return out
+    width = _uniform_width(offsets)
+    if width is None:
+        raise RuntimeError("bloom_doc_bits reads the bundle widths back: build the row bits "
+                           "outside graph capture")
+    if not width:
+        raise ValueError("every bundle must hold the same 1 to 64 bits per document")
+    lib = nat.lib()
+    with torch.cuda.device(dev):
+        nat.check(lib.rt_bloom_doc_bits(nat.ptr(index), nat.ptr(offsets), nb, n_docs, width,
+                                        nat.ptr(out), nat.stream(dev)))
+    return out
+
+
+@bloom_doc_bits.register_fake
+def _(bloom_index, bloom_bundle_b_offsets, n_docs):
+    return bloom_index.new_empty((n_docs,), dtype=torch.int64)
+
+
+@torch.library.custom_op("retrieve_amd::scan_topk_bloom_clauses", mutates_args=(),
+                         device_types="cuda")
+def scan_topk_bloom_clauses(
+    queries: Tensor, items: Tensor, k: int, item_clause_attrs: Tensor, clause_is_reverse: Tensor,
+    query_values: Tensor, bloom_doc_bits: Tensor, bloom_index: Tensor,
+    bloom_bundle_b_offsets: Tensor, plans: Tensor, plan_count: int, max_stack_size: int,
+    bloom_k: int, hash_k: int,
+) -> tuple[Tensor, Tensor]:
+    """The filtered top-k under a Bloom pre-filter and the exact clause post-check, the Bloom
+    plans probed inside the scan: the same results as ``int8_scan_topk_clauses`` (int8 queries
+    and items, int32 scores) or ``dense_scan_topk_clauses`` (bf16 / fp16 / fp32, float scores)
+    with ``mask = bloom_index_search_batch_prepared(bloom_index, offsets, plans, plan_count,
+    max_stack_size, bloom_k, hash_k)``, plan ``b`` for query ``b``.
+
+    Below the blocked scan's batch, a candidate (an item whose score beats its query's running
+    bound) is tested against the clauses, then against its query's plan on the item's row bits
+    (``bloom_doc_bits``; the plan's clause table ``probe_tables``, all 64 lanes of a wave
+    testing its terms at once): no Bloom mask is written or read, and the index words are not
+    read at all (``bloom_index_search_cuda.cu:471-534`` evaluates the same plans column by
+    column). Where that does not apply (the blocked batches, fp32, plans that are not an AND of
+    at most 64 value-set clauses, bundles of mixed widths, a graph capture before the plans were
+    first seen) the op searches the index and scans under its words, as the unfused pair
+    does."""
+    from retrieve_amd import hip as _hip
+
+    if queries.dim() != 2 or items.dim() != 2 or queries.dtype != items.dtype:
+        raise ValueError("queries [B, D] and items [N, D] of one dtype")
+    dtype = {torch.int8: 0, torch.bfloat16: 1, torch.float16: 2, torch.float32: 3}.get(
+        queries.dtype)
+    if dtype is None:
+        raise TypeError("queries and items must be int8, bfloat16, float16 or float32")
+    if queries.shape[1] != items.shape[1]:
+        raise ValueError(f"D mismatch: query D={queries.shape[1]} vs item D={items.shape[1]}")
+    if k < 1:
+        raise ValueError(f"k must be >= 1, got {k}")
+    if plans.dtype != torch.int64 or plans.dim() != 1 or plans.numel() < 8 * plan_count:
+        raise ValueError("plans must be int64 [8 * plan_count + data words]")
+    b, d = queries.shape
+    n = items.shape[0]
+    if plan_count != b:
+        raise ValueError(f"one Bloom plan per query: plan_count {plan_count} != B {b}")
+    if bloom_doc_bits.dtype != torch.int64 or bloom_doc_bits.shape != (n,):
+        raise ValueError(f"bloom_doc_bits must be int64 [N] = [{n}]")
+    _hip._check_items(items=items, bloom_doc_bits=bloom_doc_bits)
+    fused = (dtype != 3 and 0 < b and 0 < n and k <= _hip.MAX_FUSED_K
+             and not _hip._use_blocked(b, d * queries.element_size(), k))
+    tables = None
+    if fused:
+        offsets = bloom_bundle_b_offsets.contiguous()
+        plans = plans.contiguous()
+        depth = max(1, min(int(max_stack_size), MAX_STACK))
+        tables = _probe_tables(offsets, plans, int(plan_count), depth, int(bloom_k), int(hash_k))
+        fused = tables is not None and tables is not False and bool(_uniform_width(offsets))
+    if not fused:
+        if _hip._use_blocked(b, d * queries.element_size(), k):
+            mask = bloom_search_t(bloom_index, bloom_bundle_b_offsets, plans, plan_count,
+                                  max_stack_size, bloom_k, hash_k)
+        else:
+            mask = torch.ops.st.bloom_index_search_batch_prepared(
+                bloom_index, bloom_bundle_b_offsets, plans, plan_count, max_stack_size, bloom_k,
+                hash_k)
+        op = torch.ops.retrieve_amd.int8_scan_topk_clauses if dtype == 0 else \
+            torch.ops.retrieve_amd.dense_scan_topk_clauses
+        return op(queries, items, k, item_clause_attrs, clause_is_reverse, query_values, mask)
+    rev, qs = _hip._clause_prep(item_clause_attrs, clause_is_reverse, query_values, sets=True)
+    if item_clause_attrs.shape[0] != n:
+        raise ValueError(f"item_clause_attrs has {item_clause_attrs.shape[0]} rows, the items {n}")
+    if qs.shape[0] != b:
+        raise ValueError(f"query_values has {qs.shape[0]} rows, the queries {b}")
+    q = queries.contiguous()
+    dev = nat.require_device(q, items, item_clause_attrs, qs, bloom_doc_bits)
+    _, c, a = item_clause_attrs.shape
+    v = qs.shape[2]
+    ids = torch.empty((b, k), dtype=torch.int64, device=dev)
+    scores = torch.empty((b, k), dtype=torch.int32 if dtype == 0 else torch.float32, device=dev)
+    lib = nat.lib()
+    with torch.cuda.device(dev):
+        ws = nat.workspace(lib.rt_scan_topk_clauses_workspace(b, n, d, k, c, v), dev)
+        nat.check(lib.rt_scan_topk_bloom_clauses(
+            nat.ptr(q), b, nat.ptr(items), n, d, k, dtype, nat.ptr(bloom_doc_bits),
+            nat.ptr(tables), plan_count, nat.ptr(item_clause_attrs),
+            item_clause_attrs.element_size(), c, a, nat.ptr(rev), nat.ptr(qs), v, nat.ptr(ids),
+            nat.ptr(scores), nat.ptr(ws), ws.numel(), nat.stream(dev)))
+    return ids, scores
+
+
+@scan_topk_bloom_clauses.register_fake
+def _(queries, items, k, item_clause_attrs, clause_is_reverse, query_values, bloom_doc_bits,
+      bloom_index, bloom_bundle_b_offsets, plans, plan_count, max_stack_size, bloom_k, hash_k):
+    b = queries.shape[0]
+    return (queries.new_empty((b, k), dtype=torch.int64),
+            queries.new_empty((b, k), dtype=torch.int32 if queries.dtype == torch.int8
+                              else torch.float32))
 
 
 def _search_batch(bloom_index, bloom_bundle_b_offsets, bloom_query_plans_data,

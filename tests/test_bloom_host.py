@@ -210,3 +210,84 @@ def test_clause_plans_decline():
                                       torch.device("cpu"))
     hdr, prog = _compiled_stand_in(blob.numpy(), count)
     assert st.clause_plans(blob.numpy(), count, 7, hdr, prog) is not None  # 6 refs, 3 terms
+
+
+def _compiled_positions(blob: np.ndarray, count: int, hash_k: int, k: int, w: int):
+    """The compile pass's output with real positions, built on the host: every plan a program
+    whose TERM words hold the first k distinct stored hash % w as byte offsets p * 256 (the first
+    repeated past them), other ops PASS; op counts and first hash words in the headers."""
+    offs = blob[: 8 * count].reshape(count, 8)
+    data = blob[8 * count :].view(np.uint8)
+    h64 = blob[8 * count :].view(np.uint64)
+    hdr = np.zeros((count, 4), np.int32)
+    prog = np.zeros((count, 1024, 2), np.uint32)
+    for b in range(count):
+        o = offs[b]
+        ops = data[o[0] : o[1]]
+        h0 = int(o[6]) // 8
+        hdr[b] = [0, ops.size, h0, 0]
+        t = 0
+        for i, op in enumerate(ops.tolist()):
+            if op == bl.TERM:
+                pos: list[int] = []
+                for h in h64[h0 + t * hash_k : h0 + (t + 1) * hash_k].tolist():
+                    if h % w not in pos and len(pos) < k:
+                        pos.append(h % w)
+                pos += [pos[0]] * (4 - len(pos))
+                prog[b, i] = [(pos[0] * 256) << 4 | (pos[1] * 256) << 18,
+                              pos[2] * 256 | (pos[3] * 256) << 16]
+                t += 1
+            else:
+                prog[b, i] = [2, 0]
+    return hdr, prog
+
+
+def _probe(tables: np.ndarray, b: int, f: int) -> bool:
+    """One document through plan b's probe table (the wave's ballots, lane by lane)."""
+    w = [int(x) for x in tables.view(np.uint64)]
+    t = w[w[b] : w[b + 1]]
+    chunks, used, neg = t[0] >> 1, t[1], t[2]
+    hit = [False] * 64  # clause j holds a hit
+    for c in range(chunks):
+        tm, cl = t[4 + 128 * c : 68 + 128 * c], t[68 + 128 * c : 132 + 128 * c]
+        hits = sum(1 << l for l in range(64) if f & tm[l] == tm[l])
+        hit = [hit[j] or bool(hits & cl[j]) for j in range(64)]
+    bad = any(hit[j] == bool(neg >> j & 1) for j in range(64) if used >> j & 1)
+    return not bad and not t[0] & 1
+
+
+def test_probe_tables_match_the_search():
+    """The scans' per-candidate Bloom probe, on the host: tables from ANDs of value-set clauses
+    (NOT, EMPTY, one term, 64 terms, 130 terms over three chunks) evaluated on each document's
+    row bits give the oracle's column search verdicts; other plan shapes, 65 clauses, and stack
+    plans have no tables; a malformed plan matches nothing."""
+    import retrieve_amd.st as st
+
+    g = np.random.default_rng(5)
+    n = 700
+    attrs = g.integers(-1, 6, (n, 4, 1))
+    words, offs = of.bloom_build(attrs, 3, bits_per_doc=64)
+    bits = of.bloom_doc_bits(words, offs, n).view(np.uint64)
+    wide = " AND ".join("(" + " OR ".join(f"{a}:{v}" for v in range(16)) + ")" for a in range(4))
+    long = " AND ".join("(" + " OR ".join(f"{a}:{v}" for v in range(-8, 35)) + ")"
+                        for a in (0, 2, 3)) + " AND NOT (1:2 OR 1:4)"
+    exprs = ["", "1:3", "NOT 2:2", "(0:1 OR 0:2) AND NOT (3:4 OR 3:5) AND 1:0", wide,
+             "NOT 0:0 AND NOT 1:1", "(2:1 OR 2:5 OR 2:-1) AND 0:3", long]
+    blob, count, _ = st.prepare_plans(exprs, 7, torch.device("cpu"))
+    blob = blob.numpy()
+    hdr, prog = _compiled_positions(blob, count, 7, 3, 64)
+    tables = st.probe_tables(blob, count, hdr, prog)
+    assert int(tables[count]) - int(tables[count - 1]) == 4 + 3 * 128  # 131 terms: 3 chunks
+    for b, e in enumerate(exprs):
+        want = of.bloom_expression_mask(words, offs, n, e, 3, 7)
+        got = np.array([_probe(tables, b, int(f)) for f in bits])
+        assert np.array_equal(got, want), e[:60]
+    hdr[2, 0] = 1  # malformed: matches nothing
+    assert not any(_probe(st.probe_tables(blob, count, hdr, prog), 2, int(f)) for f in bits)
+    many = " AND ".join(f"({a}:{v} OR {a}:{v + 1})" for a in range(4) for v in range(17))
+    for other in ["NOT (0:1 AND 1:5)", "(0:1 AND 1:5) OR 2:3", many]:
+        blob2, count2, _ = st.prepare_plans(exprs[:2] + [other], 7, torch.device("cpu"))
+        hdr2, prog2 = _compiled_positions(blob2.numpy(), count2, 7, 3, 64)
+        assert st.probe_tables(blob2.numpy(), count2, hdr2, prog2) is None, other
+    hdr[1, 0] = 2  # a plan of the stack evaluation
+    assert st.probe_tables(blob, count, hdr, prog) is None

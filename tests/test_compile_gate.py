@@ -105,16 +105,21 @@ def test_silvertorch_one_list_and_ivf_bloom(dev):
     _gate(ivf, q, ivf.prepare_queries(_t(dev, _query_attrs(g, b, c=3, card=4))))
 
 
-def test_headline_step_as_bench_compiles_it(dev):
+@pytest.mark.parametrize("bloom", ["probe", "search"])
+def test_headline_step_as_bench_compiles_it(dev, bloom):
+    """bench.py's default step (the Bloom plans probed inside the scan) and its --bloom-search
+    form (the search's mask, then the clause scan)."""
     from torch._inductor.utils import run_and_get_code
 
     n, b, d = 2_300_000, 16, 512
-    print(f"compile gate: headline step B={b} N={n} D={d}", flush=True)
+    print(f"compile gate: headline step B={b} N={n} D={d}, Bloom {bloom}", flush=True)
     items = bench.int8_table(n, d, 1234, dev)
     queries = bench.int8_table(b, d, 99, dev)
     flt = bench.Filter(n, b, 0.1, dev)
 
     def step():
+        if bloom == "probe":
+            return flt.scan(queries, items, 100)
         return torch.ops.retrieve_amd.int8_scan_topk_clauses(queries, items, 100, flt.attrs,
                                                              flt.rev, flt.sets, flt.bloom())
 
@@ -124,5 +129,8 @@ def test_headline_step_as_bench_compiles_it(dev):
         _, codes = run_and_get_code(torch.compile(step, mode="reduce-overhead", dynamic=False,
                                                   fullgraph=True))
     src = "\n".join(codes)
-    assert "bloom_index_search_batch_prepared" in src and "int8_scan_topk_clauses" in src
+    if bloom == "probe":
+        assert "scan_topk_bloom_clauses" in src
+    else:
+        assert "bloom_index_search_batch_prepared" in src and "int8_scan_topk_clauses" in src
     assert "async_compile.triton(" not in src, "the compiler generated a kernel of its own"

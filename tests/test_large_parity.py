@@ -1,10 +1,11 @@
 """Oracle parity at the sizes where the sampled paths run, bit for bit for the integer scans:
 
-- the headline step exactly as ``bench.py`` times it: ``int8_scan_topk_clauses`` at B = 16,
-  D = 512 over 2.3M rows (the small-batch scan's seeded path), the bench's Zipf attributes and
-  10 % value sets, the exact clauses fused, and the Bloom words straight from
-  ``st::bloom_index_search_batch_prepared`` with their bundle-padded width (more words than
-  ceil(N / 64));
+- the headline step exactly as ``bench.py`` times it: ``scan_topk_bloom_clauses`` (the Bloom
+  plans probed per candidate, then the exact clauses, inside the scan) at B = 16, D = 512 over
+  2.3M rows (the small-batch scan's seeded path), the bench's Zipf attributes and 10 % value
+  sets; and its ``--bloom-search`` form, ``int8_scan_topk_clauses`` under the words straight
+  from ``st::bloom_index_search_batch_prepared`` with their bundle-padded width (more words
+  than ceil(N / 64));
 - the blocked scans' stride-32 threshold sample (N >= 2048 * 32 * 64 = 4,194,304 rows): int8 at
   B = 1024, bf16 and fp16 at B = 1024 and 4096 (configuration 2's largest batch, clustered
   rows), and configuration 5's main path (512-bit codes, B = 256, k = 1000, the Bloom words
@@ -81,11 +82,23 @@ def test_headline_step_as_benched(dev):
     words = flt.bloom()
     assert words.shape == (b, -(-n // 2048) * 32) and words.shape[1] > -(-n // 64)
     qt = torch.from_numpy(q).to(dev)
+    exact = _filter_oracle(flt.attrs, flt.sets.cpu().numpy(), words.cpu().numpy(), n)
+    base_sc, rep = osc.int8_scores(q, base), osel.RepeatedRows(row_of, n_base)
+    # bench.py's step: the Bloom plans probed per candidate inside the scan (Filter.scan), whose
+    # plans the probe holds (no fallback to the search)
+    import retrieve_amd.st as st
+
+    depth = max(1, min(flt.max_stack, st.MAX_STACK))
+    assert st._probe_tables(flt.offs, flt.blob, flt.plan_count, depth, bench.BLOOM_K,
+                            bench.HASH_K) is not False
+    ids, sc = flt.scan(qt, items, k)
+    torch.cuda.synchronize()
+    _check_exact(ids, sc, base_sc, rep, k, exact)
+    # its --bloom-search form: the search's words, then the clause scan
     ids, sc = torch.ops.retrieve_amd.int8_scan_topk_clauses(qt, items, k, flt.attrs, flt.rev,
                                                             flt.sets, words)
     torch.cuda.synchronize()
-    exact = _filter_oracle(flt.attrs, flt.sets.cpu().numpy(), words.cpu().numpy(), n)
-    _check_exact(ids, sc, osc.int8_scores(q, base), osel.RepeatedRows(row_of, n_base), k, exact)
+    _check_exact(ids, sc, base_sc, rep, k, exact)
 
 
 def test_int8_b1024_stride32_sample(dev):

@@ -335,6 +335,29 @@ def test_bloom_no_false_negatives():
             assert (m | ~exact).all()  # every doc holding the token is found
 
 
+@pytest.mark.parametrize("bits", [64, 40])
+def test_bloom_doc_bits(bits):
+    """The row view: each document's word is the OR of its tokens' build positions (computed
+    from the tokens, not the words), and a term's test on it (all its search positions set) is
+    ``term_mask``'s column-wise answer."""
+    g = rng(bits)
+    n = 4500  # three bundles, the last one partial
+    attrs = g.integers(-1, 12, (n, 3, 2))
+    words, offs = of.bloom_build(attrs, 3, bits_per_doc=bits)
+    got = of.bloom_doc_bits(words, offs, n).view(np.uint64)
+    want = np.zeros(n, np.uint64)
+    for d in range(n):
+        for c in range(3):
+            for v in attrs[d, c]:
+                if v != -1:
+                    for p in of.bit_positions(c, int(v), bits, 3):
+                        want[d] |= np.uint64(1) << np.uint64(p)
+    assert np.array_equal(got, want)
+    for f, v in [(0, 3), (1, 0), (2, 11)]:
+        m = np.uint64(sum(1 << p for p in of.probe_positions(f, v, bits, 3, 7)))
+        assert np.array_equal((got & m) == m, of.term_mask(words, offs, n, f, v, 3, 7))
+
+
 def test_candidate_topk_brute_force():
     """``candidate_topk`` against a brute-force full sort over each row's first ``counts[b]``
     candidates (tie-heavy scores, duplicates, short rows) and against ``candidate_int8_topk``."""

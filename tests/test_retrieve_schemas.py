@@ -39,7 +39,7 @@ EXTRAS = (
     "int8_scan_topk", "int8_scan_topk_clauses", "dense_scan_topk", "dense_scan_topk_clauses",
     "hamming_scan_topk", "hamming_scan_topk_clauses", "clause_bits", "mask_compact",
     "int8_candidates_topk", "int8_rerank_topk", "quantize_int8", "quantize_int8_global",
-    "pack_mask", "pack_signs", "bloom_search_cols",
+    "pack_mask", "pack_signs", "bloom_search_cols", "bloom_doc_bits", "scan_topk_bloom_clauses",
 )
 
 
