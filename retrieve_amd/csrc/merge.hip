@@ -25,9 +25,6 @@ const char* last_error() { return g_error; }
 
 // Workgroups a seed pass aims for, and the main pass's when the device cannot be queried.
 static constexpr int64_t kTargetWorkgroups = 2048;
-// Rows of the seed sample; the main pass then keeps about k * N / kSeedRows composites a
-// query (in expectation, for items in random order).
-static constexpr int64_t kSeedRows = 1 << 18;
 // At least this many sampled rows per wanted item (keeps the main pass's candidates near
 // k * N / seed_rows for large k).
 static constexpr int64_t kSeedRowsPerK = 1024;
@@ -78,14 +75,16 @@ int64_t main_workgroups() {
 }
 
 ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int64_t qpg, int64_t lists_per_wg,
-                   int64_t target_wgs, int main_capw, int64_t seed_rows_per_wg) {
+                   int64_t target_wgs, int main_capw, int64_t seed_rows_per_wg,
+                   int64_t seed_rows_min) {
   ScanPlan s;
   s.qpg = qpg;
   s.n_qgroups = cdiv(B, qpg);
   // a query's lists per workgroup: every wave scores all of the row's queries (lists_per_wg ==
   // waves * qpg), or one wave owns each query (lists_per_wg == qpg)
   const int64_t lpq = lists_per_wg / qpg;
-  const int64_t seed_rows = kSeedRows > kSeedRowsPerK * k ? kSeedRows : kSeedRowsPerK * k;
+  const int64_t seed_rows =
+      seed_rows_min > kSeedRowsPerK * k ? seed_rows_min : kSeedRowsPerK * k;
   s.seeded = N >= 8 * seed_rows;
   if (s.seeded) {
     // one-entry lists (each seed wave's best); at least 4k of them per query
@@ -101,7 +100,11 @@ ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int64_t qpg, int64_t lists_p
   s.off_counts = align_up(lists, 256);
   s.off_tau = s.off_counts + align_up(counts, 256);
   s.off_flag = s.off_tau + align_up(static_cast<size_t>(B) * sizeof(uint64_t), 256);
-  s.total = s.off_flag + 256;
+  s.off_parts = s.off_flag + 256;
+  s.split = B <= kMergeSplitMaxB;
+  s.total = s.off_parts +
+            (s.split ? align_up(static_cast<size_t>(B) * kMergeParts * k * sizeof(uint64_t), 256)
+                     : 0);
   return s;
 }
 
@@ -252,11 +255,16 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   __shared__ int fill;
   const int tid = threadIdx.x;
   if (m.run_if != nullptr && *m.run_if == 0u) return;  // (uniform: the fallback is not needed)
-  const int64_t q = blockIdx.x;
+  // a split merge's first launch: block = (query, part), the part's lists [s_lo, s_lo + S)
+  const int parts = m.part_out != nullptr ? m.parts : 1;
+  const int64_t q = blockIdx.x / parts;
+  const int my_part = static_cast<int>(blockIdx.x % parts);
+  const int span = static_cast<int>((m.S + parts - 1) / parts);
+  const int s_lo = my_part * span;
+  const int S = static_cast<int>(m.S - s_lo < span ? (m.S - s_lo > 0 ? m.S - s_lo : 0) : span);
   const int64_t g = q / m.qpw;
   const int qi = static_cast<int>(q % m.qpw);
-  const int S = static_cast<int>(m.S);
-  const int64_t slot0 = g * m.S;
+  const int64_t slot0 = g * m.S + s_lo;
   const int k = m.k;
 
   // list lengths → inclusive prefix sums over this query's lists (flat: S one-entry lists
@@ -291,7 +299,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
       if (s < S) pre[s] += base;
     }
     __syncthreads();
-    total = pre[S - 1];
+    total = S > 0 ? pre[S - 1] : 0;
   }
 
   // Entries <= thr cannot enter the top k: once a round has kept the best k, thr is their
@@ -316,7 +324,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     __syncthreads();
     // every thread loads independent entries, four in flight; the trip count is the same for
     // the whole block, so every lane of a wave takes part in each append
-    const uint64_t* row = m.lists + q * static_cast<int64_t>(S) + e0;
+    const uint64_t* row = m.lists + q * m.S + s_lo + e0;
     const int rounds = (n + 4 * kMergeThreads - 1) / (4 * kMergeThreads);
     for (int r = 0; r < rounds; ++r) {
       const int i0 = r * 4 * kMergeThreads + tid;
@@ -377,6 +385,12 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     __syncthreads();
   }
 
+  if (m.part_out != nullptr) {
+    // the part's best k (or all it holds), the rest empty
+    uint64_t* out = m.part_out + blockIdx.x * static_cast<int64_t>(k);
+    for (int i = tid; i < k; i += kMergeThreads) out[i] = i < held ? buf[i] : 0ull;
+    return;
+  }
   if (m.tau_out != nullptr) {
     // only the k-th composite: held <= k entries remain, the best k of everything when held == k
     uint64_t lo = 0ull;
@@ -451,12 +465,8 @@ int launch_pad(int64_t* out_ids, void* out_scores, int64_t B, int64_t k, int sco
   return kOk;
 }
 
-int launch_merge(const MergeArgs& m, hipStream_t stream) {
-  RT_CHECK_ARG(m.k >= 1 && m.k <= kMaxK, "k must be in [1, %lld], got %d",
-               static_cast<long long>(kMaxK), m.k);
-  RT_CHECK_ARG(m.S >= 1 && m.S <= kMaxMergeSlots, "too many scan lists per query");
-  if (m.B == 0) return kOk;
-  const dim3 grid(static_cast<unsigned>(m.B));
+static int launch_merge_grid(const MergeArgs& m, int64_t blocks, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(blocks));
   if (m.k <= 128) {
     merge_kernel<128><<<grid, kMergeThreads, 0, stream>>>(m);
   } else if (m.k <= 256) {
@@ -468,6 +478,45 @@ int launch_merge(const MergeArgs& m, hipStream_t stream) {
   }
   RT_CHECK_HIP(hipGetLastError());
   return kOk;
+}
+
+// A small batch's merge is split when the caller gave room: each query's lists go to up to
+// kMergeParts workgroups (a part at least kMergeMinPartSlots lists), each keeping its part's
+// best k in part_buf, then one workgroup per query merges those (flat, kMergeParts * k
+// entries) with the call's own outputs. Same results: the best k of the union is among the
+// parts' best k.
+constexpr int64_t kMergeMinPartSlots = 256;
+
+int launch_merge(const MergeArgs& m, hipStream_t stream) {
+  RT_CHECK_ARG(m.k >= 1 && m.k <= kMaxK, "k must be in [1, %lld], got %d",
+               static_cast<long long>(kMaxK), m.k);
+  RT_CHECK_ARG(m.S >= 1 && m.S <= kMaxMergeSlots, "too many scan lists per query");
+  if (m.B == 0) return kOk;
+  int64_t parts = m.S / kMergeMinPartSlots;
+  parts = parts < kMergeParts ? parts : kMergeParts;
+  if (m.part_buf == nullptr || m.B > kMergeSplitMaxB || parts < 2) {
+    MergeArgs one = m;
+    one.parts = 1;
+    one.part_out = nullptr;
+    return launch_merge_grid(one, m.B, stream);
+  }
+  MergeArgs first = m;
+  first.parts = static_cast<int>(parts);
+  first.part_out = m.part_buf;
+  first.tau_out = nullptr;
+  first.spec_flag = nullptr;
+  int st = launch_merge_grid(first, m.B * parts, stream);
+  if (st != kOk) return st;
+  MergeArgs second = m;
+  second.lists = m.part_buf;
+  second.counts = nullptr;
+  second.flat = true;
+  second.capw = 1;
+  second.S = parts * m.k;
+  second.clause = ClauseCheck{};  // (the first launch tested them)
+  second.parts = 1;
+  second.part_out = nullptr;
+  return launch_merge_grid(second, m.B, stream);
 }
 
 }  // namespace rt

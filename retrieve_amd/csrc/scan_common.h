@@ -85,7 +85,18 @@ struct MergeArgs {
   int score_kind;
   ClauseCheck clause;  // lists (not flat) whose entries may fail exact clauses: those entries
                        // count as empty (active null: none)
+  // Room for a split merge (null: none): [B, kMergeParts, k] composites. launch_merge then
+  // splits a small batch's lists into parts, each a workgroup keeping its part's best k there,
+  // and merges those (flat) in a second launch.
+  uint64_t* part_buf;
+  // (set by launch_merge) parts per query, and the parts' output in the first launch
+  int parts;
+  uint64_t* part_out;
 };
+
+// Parts of a split merge at most, and the largest batch that splits.
+constexpr int kMergeParts = 8;
+constexpr int64_t kMergeSplitMaxB = 32;
 
 // The seed pass samples blocks of kSeedBlock consecutive rows spread evenly over the table
 // (row_stride = N / sample rows > 1), so each block is read as one contiguous run; sample row r
@@ -117,7 +128,8 @@ struct ScanPlan {
   PassPlan seed;
   PassPlan main;
   // workspace layout (byte offsets)
-  size_t off_lists = 0, off_counts = 0, off_tau = 0, off_flag = 0, total = 0;
+  size_t off_lists = 0, off_counts = 0, off_tau = 0, off_flag = 0, off_parts = 0, total = 0;
+  bool split = false;  // room for a split merge at off_parts
 };
 
 // Upper bound on a main pass's workgroups (the workspace functions size for it).
@@ -151,8 +163,12 @@ int blocked_hamming(const uint64_t* query_bits, int64_t B, const uint64_t* item_
 // queries and each workgroup keeps lists_per_wg candidate lists (of main_capw entries in the
 // main pass); the main pass runs target_wgs workgroups in all; a seed workgroup scores at
 // least seed_rows_per_wg sampled rows.
+// Rows of the seed sample (at least, and kSeedRowsPerK * k at least): the main pass then keeps
+// about k * N / seed rows composites a query (in expectation, for items in random order).
+constexpr int64_t kSeedRows = 1 << 18;
 ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int64_t qpg, int64_t lists_per_wg,
-                   int64_t target_wgs, int main_capw, int64_t seed_rows_per_wg);
+                   int64_t target_wgs, int main_capw, int64_t seed_rows_per_wg,
+                   int64_t seed_rows_min = kSeedRows);
 
 // Writes the -1 / sentinel pads of an empty result.
 int launch_pad(int64_t* out_ids, void* out_scores, int64_t B, int64_t k, int score_kind,

@@ -389,6 +389,13 @@ static int dispatch_mfma(int64_t row_bytes, const ScanArgs& a, const PassPlan& p
 // at most 16 per query), a power of two (the compaction sorts it whole).
 static int mfma_capw(int64_t k) { return static_cast<int>(next_pow2(k + 2 * kTile)); }
 
+// Seed rows: twice the default for one query group over 2^24 rows or more, where the main
+// pass's candidate tests cost more than the larger sample (filtered int8 at B = 16 over 30M rows:
+// 2.51 -> 2.47 ms a step; four groups or 10M rows do better with the default).
+static int64_t mfma_seed_rows(int64_t B, int64_t N) {
+  return B <= 16 && N >= (int64_t{1} << 24) ? 2 * kSeedRows : kSeedRows;
+}
+
 // seed scan → seed threshold merge → main scan → final merge, on `stream`, no host sync
 template <class Op>
 static int run_mfma_scan(const void* queries, int64_t B, const void* items, int64_t N,
@@ -411,7 +418,7 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   RT_CHECK_ARG(queries != nullptr && items != nullptr && workspace != nullptr,
                "queries, items and workspace must not be null");
   const ScanPlan plan = plan_scan(B, N, k, 16, kScanWaves * 16, main_workgroups(), mfma_capw(k),
-                                  kScanWaves * kTile);
+                                  kScanWaves * kTile, mfma_seed_rows(B, N));
   if (workspace_bytes < plan.total) {
     set_error("workspace too small: %zu < %zu", workspace_bytes, plan.total);
     return kWorkspaceTooSmall;
@@ -446,6 +453,7 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   m.qpw = 16;
   m.B = B;
   m.k = static_cast<int>(k);
+  m.part_buf = plan.split ? reinterpret_cast<uint64_t*>(ws + plan.off_parts) : nullptr;
 
   if (plan.seeded) {
     a.n_rows = plan.seed.n_rows;
@@ -506,7 +514,7 @@ using namespace rt;
 extern "C" size_t rt_int8_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
   (void)D;
   return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k),
-                   kScanWaves * kTile)
+                   kScanWaves * kTile, mfma_seed_rows(B, N))
       .total;
 }
 
@@ -572,7 +580,7 @@ extern "C" int rt_int8_scan_topk_noalloc(const int8_t* queries, int64_t B, const
                           (N == 0 || (queries != nullptr && items != nullptr))),
                "queries, items, out_ids and out_scores must not be null");
   const size_t need = plan_scan(B, N, k, 16, kScanWaves * 16, main_workgroups(), mfma_capw(k),
-                                kScanWaves * kTile)
+                                kScanWaves * kTile, mfma_seed_rows(B, N))
                           .total;
   RT_CHECK_ARG(need <= kNoAllocScratchBytes,
                "rt_int8_scan_topk_noalloc: B = %lld, N = %lld, k = %lld need %zu bytes of "
@@ -590,7 +598,7 @@ extern "C" int rt_int8_scan_topk_noalloc(const int8_t* queries, int64_t B, const
 
 static size_t mfma_plan_bytes(int64_t B, int64_t N, int64_t k) {
   return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k),
-                   kScanWaves * kTile)
+                   kScanWaves * kTile, mfma_seed_rows(B, N))
       .total;
 }
 
@@ -686,7 +694,7 @@ extern "C" int rt_scan_topk_bloom_clauses(
 extern "C" size_t rt_dense_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
   (void)D;
   return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k),
-                   kScanWaves * kTile)
+                   kScanWaves * kTile, mfma_seed_rows(B, N))
       .total;
 }
 

@@ -387,8 +387,7 @@ def _compiled_plans(offsets: Tensor, plans: Tensor, data: Tensor, plan_count: in
     under graph capture with nothing kept."""
     import weakref
 
-    key = (id(plans), plans._version, id(offsets), offsets._version, plan_count, max_stack, k,
-           hash_k)
+    key = (_tkey(plans), _tkey(offsets), plan_count, max_stack, k, hash_k)
     hit = _COMPILED.get(key)
     if hit is not None or _capturing():
         return hit
@@ -433,8 +432,7 @@ def _probe_tables(offsets: Tensor, plans: Tensor, plan_count: int, max_stack: in
     hold them); None under graph capture with nothing kept."""
     import weakref
 
-    key = (id(plans), plans._version, id(offsets), offsets._version, plan_count, max_stack, k,
-           hash_k)
+    key = (_tkey(plans), _tkey(offsets), plan_count, max_stack, k, hash_k)
     hit = _PROBES.get(key)
     if hit is not None or _capturing():
         return hit
@@ -583,7 +581,7 @@ def _uniform_width(offsets: Tensor) -> int | None:
     read back once per offsets tensor (None under graph capture with nothing kept)."""
     import weakref
 
-    key = (id(offsets), offsets._version)
+    key = _tkey(offsets)
     hit = _WIDTHS.get(key)
     if hit is not None or _capturing():
         return hit
@@ -1209,6 +1207,13 @@ def _capturing() -> bool:
     return torch.cuda.is_current_stream_capturing()
 
 
+def _tkey(t: Tensor) -> tuple:
+    """A cache key for a tensor's contents: its storage address, size and version counter (views
+    of one storage share the counter), so another object over the same memory -- as a compiled
+    graph may pass -- finds the entry. Entries are dropped with the tensor that made them."""
+    return (t.device.index, t.data_ptr(), t.numel(), t.dtype, t._version)
+
+
 # (id, version) of cluster_sizes -> its largest cluster (the payload columns' static bound)
 _MAX_CLUSTER: dict = {}
 
@@ -1218,7 +1223,7 @@ def _max_cluster(sizes: Tensor) -> int | None:
     or modified in place); None under graph capture with nothing kept."""
     import weakref
 
-    key = (id(sizes), sizes._version)
+    key = _tkey(sizes)
     hit = _MAX_CLUSTER.get(key)
     if hit is None:
         if _capturing():
@@ -1264,7 +1269,7 @@ def _one_list_is_the_table(offsets: Tensor, sizes: Tensor, n: int) -> bool:
     IVF kernel takes the call, with the same results)."""
     import weakref
 
-    key = (id(offsets), offsets._version, id(sizes), sizes._version, n)
+    key = (_tkey(offsets), _tkey(sizes), n)
     hit = _ONE_LIST.get(key)
     if hit is None:
         if _capturing():

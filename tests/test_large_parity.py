@@ -2,8 +2,8 @@
 
 - the headline step exactly as ``bench.py`` times it: ``scan_topk_bloom_clauses`` (the Bloom
   plans probed per candidate, then the exact clauses, inside the scan) at B = 16, D = 512 over
-  2.3M rows (the small-batch scan's seeded path), the bench's Zipf attributes and 10 % value
-  sets; and its ``--bloom-search`` form, ``int8_scan_topk_clauses`` under the words straight
+  2.3M rows (the small-batch scan's seeded path) and over the benched 30M rows, the bench's Zipf
+  attributes and 10 % value sets; and its ``--bloom-search`` form, ``int8_scan_topk_clauses`` under the words straight
   from ``st::bloom_index_search_batch_prepared`` with their bundle-padded width (more words
   than ceil(N / 64));
 - the blocked scans' stride-32 threshold sample (N >= 2048 * 32 * 64 = 4,194,304 rows): int8 at
@@ -70,8 +70,12 @@ def _filter_oracle(attrs: torch.Tensor, sets: np.ndarray, words: np.ndarray, n: 
     return exact
 
 
-def test_headline_step_as_benched(dev):
-    n, b, d, k, n_base = N_SEEDED, 16, 512, 100, 8192
+@pytest.mark.timeout(400)
+@pytest.mark.parametrize("n", [N_SEEDED, 30_000_000])
+def test_headline_step_as_benched(dev, n):
+    """At 2.3M rows (the default seed sample) and at the benched 30M rows (the doubled sample of
+    one query group over 2^24 rows or more)."""
+    b, d, k, n_base = 16, 512, 100, 8192
     print(f"headline step: int8 clause scan B={b} N={n} D={d} k={k}, bench filter", flush=True)
     g = rng(1300)
     base = _int8_rows(g, n_base, d)
