@@ -96,14 +96,27 @@ struct WaveTopK16 {
         }
       }
     }
-    uint32_t todo = clauses || probing ? cand : 0u;
+    const bool held = clauses && clause.held;
+    if (held && cand != 0u) {
+      // every candidate's attribute row in one round of loads, then the tests on them
+      AttrRow rows[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if ((cand >> r) & 1u) rows[r] = load_attr_row(clause, (row0 + r) * row_stride);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if ((cand >> r) & 1u && !clause_pass_held(clause, crow, rows[r])) cand &= ~(1u << r);
+      }
+    }
+    uint32_t todo = (clauses && !held) || probing ? cand : 0u;
     while (__any(todo != 0u)) {
       int r = -1;
       bool ok = false;
       if (todo != 0u) {
         r = __builtin_ctz(todo);
         todo &= todo - 1u;
-        ok = !clauses || clause_pass(clause, crow, (row0 + r) * row_stride);
+        ok = held || !clauses || clause_pass(clause, crow, (row0 + r) * row_stride);
       }
       if (probe_on) {  // each candidate that passed, one at a time, by the whole wave
         const uint64_t item = static_cast<uint64_t>((row0 + (r < 0 ? 0 : r)) * row_stride);

@@ -97,7 +97,21 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
   const uint64_t* qmask =
       a.mask != nullptr && qrow < a.B ? a.mask + qrow * a.mask_words : nullptr;
   const bool clauses = a.clause.active != nullptr && qrow < a.B;
-  const ClauseRow crow = clauses ? clause_row(a.clause, qrow) : ClauseRow{};
+  const uint64_t* bm = nullptr;
+  if (a.clause.active != nullptr && a.clause_lds) {
+    // the group's set bitmaps in LDS (the host sized the launch for them)
+    extern __shared__ __attribute__((aligned(16))) uint64_t seed_bm[];
+    const int per_row = a.clause.C * kSetWords;
+    const int64_t g0 = static_cast<int64_t>(blockIdx.y) * 16;
+    for (int i = threadIdx.x; i < 16 * per_row; i += kScanThreads) {
+      const int64_t b = g0 + i / per_row;
+      seed_bm[i] = b < a.B ? a.clause.bitmaps[b * per_row + i % per_row] : 0ull;
+    }
+    __syncthreads();
+    bm = seed_bm + col * per_row;
+  }
+  const ClauseRow crow = clauses ? clause_row(a.clause, qrow, bm) : ClauseRow{};
+  const bool held = clauses && a.clause.held;
 
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * a.strip;
   const int64_t r1 = r0 + a.strip < a.n_rows ? r0 + a.strip : a.n_rows;
@@ -134,12 +148,26 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
         cand &= (w >> (63 - ((item0 + r) & 63))) & 1ull ? ~0u : ~(1u << r);
       }
     }
-    if (!clauses) {
+    if (held && cand != 0u) {
+      // every candidate's attribute row in one round of loads, then the tests on them
+      AttrRow rows[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if ((cand >> r) & 1u) {
+          rows[r] = load_attr_row(a.clause, sample_item(rb + 4 * grp + r, a.row_stride));
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if ((cand >> r) & 1u && !clause_pass_held(a.clause, crow, rows[r])) cand &= ~(1u << r);
+      }
+    }
+    if (!clauses || held) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) best = (cand >> r) & 1u && cs[r] > best ? cs[r] : best;
     }
-    while (__any(clauses && cand != 0u)) {
-      if (clauses && cand != 0u) {
+    while (__any(clauses && !held && cand != 0u)) {
+      if (clauses && !held && cand != 0u) {
         int rb_ = 0;
         uint64_t cb = 0ull;
 #pragma unroll
@@ -332,6 +360,8 @@ static size_t main_lds_bytes(int capw) {
 // The most the main pass gives the LDS copies below: they are made only while two workgroups
 // still fit a CU.
 constexpr size_t kMainLdsForTwo = 80 * 1024;
+// The most LDS the seed pass gives its copies of the set bitmaps.
+constexpr size_t kSeedClauseLds = 32 * 1024;
 // LDS for a main-pass workgroup's copies of its queries' Bloom clause tables: none below the
 // minimum, at most the maximum, within the two-workgroup budget.
 constexpr size_t kProbeLdsMin = 4 * 1024;
@@ -342,7 +372,11 @@ static int launch_mfma(const ScanArgs& a, const PassPlan& p, int64_t n_qgroups, 
                        hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.gx), static_cast<unsigned>(n_qgroups));
   if (seed) {
-    seed_mfma_kernel<Op, KSTEPS><<<grid, kScanThreads, 0, stream>>>(a);
+    // the seed copies its group's set bitmaps to LDS when they are small
+    ScanArgs s = a;
+    const size_t bm = a.clause.active != nullptr ? clause_lds_bytes(a.clause.C) : 0;
+    s.clause_lds = bm > 0 && bm <= kSeedClauseLds;
+    seed_mfma_kernel<Op, KSTEPS><<<grid, kScanThreads, s.clause_lds ? bm : 0, stream>>>(s);
     RT_CHECK_HIP(hipGetLastError());
     return kOk;
   }
@@ -648,6 +682,7 @@ static int scan_clauses(const void* queries, int64_t B, const void* items, int64
     f.attrs = item_attrs;
     f.attr_bytes = attr_bytes;
     f.A = static_cast<int>(A);
+    f.held = attr_rows_held(item_attrs, attr_bytes, C, A);
   }
   if (dtype == 0) {
     return run_mfma_scan<I8Op>(queries, B, items, N, D, k, mask, mask_words, out_ids,
