@@ -1099,11 +1099,6 @@ static int64_t sample_stride(int64_t N) {
   return 0;
 }
 
-static int sample_rank(int64_t k, int64_t stride) {
-  const double lam = static_cast<double>(k) / static_cast<double>(stride);
-  const int64_t m = static_cast<int64_t>(std::ceil(lam + 5.0 * std::sqrt(lam) + 4.0));
-  return static_cast<int>(m < k ? m : k);
-}
 
 
 

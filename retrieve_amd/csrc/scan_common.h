@@ -9,6 +9,8 @@
 //   4. final merge: the exact top-k over the main scan's lists.
 #pragma once
 
+#include <cmath>
+
 #include "bloom_prog.h"
 #include "clause_check.h"
 #include "rt_common.h"
@@ -107,6 +109,17 @@ constexpr int64_t kSeedBlock = 256;
 
 __host__ __device__ inline int64_t sample_item(int64_t r, int64_t stride) {
   return stride == 1 ? r : (r / kSeedBlock) * (kSeedBlock * stride) + (r % kSeedBlock);
+}
+
+// The rank m whose m-th best sampled composite bounds the k-th best of all items with
+// overwhelming probability when one item in `stride` is sampled: the top k hold about
+// lam = k / stride sampled items (Poisson), and m = lam + 5 sqrt(lam) + 4 exceeds that count
+// all but very rarely. A query that nevertheless ends with fewer than k entries behind the bound
+// raises a flag, and a fallback pass without it keeps the results exact.
+inline int sample_rank(int64_t k, int64_t stride) {
+  const double lam = static_cast<double>(k) / static_cast<double>(stride);
+  const int64_t m = static_cast<int64_t>(std::ceil(lam + 5.0 * std::sqrt(lam) + 4.0));
+  return static_cast<int>(m < k ? m : k);
 }
 
 // One pass of a scan: its grid and list geometry.

@@ -125,6 +125,16 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
     v4i af[KSTEPS];
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) af[s] = *reinterpret_cast<const v4i*>(ip + s * 64);
+    // held rows: this lane's four rows' attributes, loaded with the tile (before it is known
+    // which rows are candidates), so the tests below wait on the same round of loads
+    AttrRow rows[4];
+    if (held) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = rb + 4 * grp + r;
+        rows[r] = load_attr_row(a.clause, sample_item(row < r1 ? row : r1 - 1, a.row_stride));
+      }
+    }
     typename Op::Acc acc = Op::zero();
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) acc = Op::mma(af[s], qf[s], acc);
@@ -149,14 +159,6 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
       }
     }
     if (held && cand != 0u) {
-      // every candidate's attribute row in one round of loads, then the tests on them
-      AttrRow rows[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if ((cand >> r) & 1u) {
-          rows[r] = load_attr_row(a.clause, sample_item(rb + 4 * grp + r, a.row_stride));
-        }
-      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if ((cand >> r) & 1u && !clause_pass_held(a.clause, crow, rows[r])) cand &= ~(1u << r);
@@ -462,12 +464,16 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   int* counts = reinterpret_cast<int*>(ws + plan.off_counts);
   uint64_t* tau = reinterpret_cast<uint64_t*>(ws + plan.off_tau);
   uint32_t* spec_flag = reinterpret_cast<uint32_t*>(ws + plan.off_flag);
-  // With the Bloom probe the seed takes its bound over the exact clauses alone (a sampled item
-  // that passes them is not probed), which bounds the filter's k-th best only where the plans
-  // pass every item the clauses pass. A query that then ends with fewer than k entries behind a
-  // bound above 0 raises a flag, and a fallback main pass and merge without the bound (both
-  // returning at once while the flag is clear) keep the results exact.
-  const bool speculative = plan.seeded && probe.doc_bits != nullptr;
+  // The seed's bound is its sample's rank-th best (sample_rank: k -> about 13 at k = 100 and one
+  // row in 57 sampled), not its k-th: the main pass then keeps about rank * stride candidates a
+  // query instead of k * stride. With the Bloom probe the seed also takes its bound over the
+  // exact clauses alone (a sampled item that passes them is not probed), which bounds the
+  // filter's k-th best only where the plans pass every item the clauses pass. A query that
+  // ends with fewer than k entries behind a bound above 0 raises a flag, and a fallback main
+  // pass and merge without the bound (both returning at once while the flag is clear) keep the
+  // results exact.
+  const int rank = plan.seeded ? sample_rank(k, plan.seed.row_stride) : static_cast<int>(k);
+  const bool speculative = plan.seeded && (rank < k || probe.doc_bits != nullptr);
 
   ScanArgs a{};
   a.queries = queries;
@@ -501,9 +507,11 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
     m.flat = true;  // one entry per seed wave, contiguous per query
     m.S = plan.seed.S;
     m.tau_out = tau;
+    m.k = rank;
     m.spec_flag = speculative ? spec_flag : nullptr;  // (cleared)
     st = launch_merge(m, stream);
     if (st != kOk) return st;
+    m.k = static_cast<int>(k);
     m.tau_out = nullptr;
     m.flat = false;
     m.spec_flag = nullptr;

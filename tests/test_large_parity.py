@@ -195,3 +195,39 @@ def test_config5_main_path_stride32_sample(dev):
     exact = _filter_oracle(attrs, sets, mask_t.contiguous().cpu().numpy(), n)
     _check_exact(ids, sc, osc.hamming_scores(q, base), osel.RepeatedRows(row_of, n_base), k,
                  exact)
+
+
+@pytest.mark.parametrize("clauses", [False, True])
+def test_speculative_seed_bound_falls_back(dev, clauses):
+    """The small-batch scan bounds its main pass by the seed sample's rank-th best (about 10 of
+    k = 100 here), a bound that fails only when the sample holds more of the top k than chance
+    allows. Rows stored in descending score order for query 0 make it fail for that query (the
+    first sample block holds the best rows): its main pass ends short, the flag raises and the
+    fallback pass without the bound must give the exact top-k, bit for bit; the other queries
+    are unaffected either way."""
+    n, b, d, k, n_base = N_SEEDED, 4, 128, 100, 4096
+    print(f"speculative seed fallback B={b} N={n} D={d} k={k} clauses={clauses}", flush=True)
+    g = rng(1400 + clauses)
+    base = _int8_rows(g, n_base, d)
+    q = _int8_rows(g, b, d)
+    base_sc = osc.int8_scores(q, base)
+    order = np.argsort(-base_sc[0], kind="stable")
+    row_of = np.repeat(order, -(-n // n_base))[:n]
+    items = torch.from_numpy(base).to(dev)[torch.from_numpy(row_of).to(dev)]
+    qt = torch.from_numpy(q).to(dev)
+    rep = osel.RepeatedRows(row_of, n_base)
+    if clauses:
+        attrs = g.integers(0, 4, (n, 2, 1)).astype(np.int16)
+        sets = np.full((b, 2, 2), -1, np.int64)
+        sets[:, 0, :2] = [0, 2]
+        sets[1:, 1, 0] = 3
+        rev = np.zeros(2, bool)
+        valid = of.clause_match_sets(attrs, sets, rev)
+        ids, sc = torch.ops.retrieve_amd.int8_scan_topk_clauses(
+            qt, items, k, torch.from_numpy(attrs).to(dev), torch.from_numpy(rev).to(dev),
+            torch.from_numpy(sets).to(dev))
+    else:
+        valid = None
+        ids, sc = torch.ops.retrieve_amd.int8_scan_topk(qt, items, k)
+    torch.cuda.synchronize()
+    _check_exact(ids, sc, base_sc, rep, k, valid)
