@@ -425,11 +425,14 @@ static int dispatch_mfma(int64_t row_bytes, const ScanArgs& a, const PassPlan& p
 // at most 16 per query), a power of two (the compaction sorts it whole).
 static int mfma_capw(int64_t k) { return static_cast<int>(next_pow2(k + 2 * kTile)); }
 
-// Seed rows: twice the default for one query group over 2^24 rows or more, where the main
-// pass's candidate tests cost more than the larger sample (filtered int8 at B = 16 over 30M rows:
-// 2.51 -> 2.47 ms a step; four groups or 10M rows do better with the default).
+// Seed rows: half the default sample. Behind the sample's rank-th best (sample_rank) the main
+// pass keeps about k + 5 sqrt(k * stride) + 4 * stride candidates a query, few enough that the
+// smaller sample's cheaper seed pass wins (filtered int8 at B = 16 over 30M rows: 2.362 ms a
+// step with 2^19 rows, 2.347 with 2^18, 2.344 with 2^17; int8 at B = 1 2.266 / 2.247 / 2.242).
 static int64_t mfma_seed_rows(int64_t B, int64_t N) {
-  return B <= 16 && N >= (int64_t{1} << 24) ? 2 * kSeedRows : kSeedRows;
+  (void)B;
+  (void)N;
+  return kSeedRows / 2;
 }
 
 // seed scan → seed threshold merge → main scan → final merge, on `stream`, no host sync
