@@ -48,8 +48,8 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
 # 2 GiB device copy), measured with rocprofv3 --pmc for these exact workloads; keyed by
 # (workload, N, D, B, k). The profiles/ summaries named below give the counts and commands.
 MEASURED_TRAFFIC: dict = {
-    ("filtered", 30_000_000, 512, 16, 100): 15_565_827_072,  # filtered_int8_30Mx512_b16.md
-    ("int8", 30_000_000, 512, 16, 100): 15_366_246_011,  # int8_scan_30Mx512_b16.md
+    ("filtered", 30_000_000, 512, 16, 100): 15_399_664_224,  # filtered_int8_30Mx512_b16.md
+    ("int8", 30_000_000, 512, 16, 100): 15_361_455_360,  # int8_scan_30Mx512_b16.md
     ("int8", 30_000_000, 512, 256, 100): 15_365_323_008,  # int8_scan_30Mx512_b256.md
     ("int8", 30_000_000, 512, 1024, 100): 44_373_443_584,  # int8_scan_30Mx512_b1024.md
     ("dense", 10_000_000, 128, 64, 100): 2_566_548_500,  # dense_bf16_10Mx128_b64.md
