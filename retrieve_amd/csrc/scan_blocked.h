@@ -28,6 +28,7 @@
 #include <cmath>
 #include <type_traits>
 
+#include "bits_fp4.h"
 #include "profile.h"
 #include "scan_common.h"
 #include "wave_lists.h"
@@ -144,10 +145,11 @@ struct BitsF4 : I8x32 {
   static constexpr bool kBits = true;
   static constexpr int kStepBits = 32;  // bits per lane per K step
   using MAcc = v16f;
-  __device__ static MAcc mstart(int32_t start) {
+  __device__ static MAcc mstart(int32_t start) { return mstart_f(static_cast<float>(start)); }
+  __device__ static MAcc mstart_f(float start) {
     MAcc c;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) c[e] = static_cast<float>(start);
+    for (int e = 0; e < 16; ++e) c[e] = start;
     return c;
   }
   __device__ static MAcc mma(v4i a, v4i b, MAcc c) {
@@ -156,6 +158,21 @@ struct BitsF4 : I8x32 {
     const v8i b8 = __builtin_shufflevector(b, b, 0, 1, 2, 3, 0, 1, 2, 3);
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 4, 4, 0, 0x7f7f7f7f, 0,
                                                           0x7f7f7f7f);
+  }
+  // The main pass's MFMAs for output tile p = 2 i + j (row tile i, column tile j), the query
+  // operand scaled and the accumulators started from an inline constant (fp4::hit_bias).
+  __device__ static float hit_bias(int p) { return fp4::hit_bias(p); }
+  __device__ static MAcc mma_hit(v4i a, v4i b, MAcc c, int p) {
+    const v8i a8 = __builtin_shufflevector(a, a, 0, 1, 2, 3, 0, 1, 2, 3);
+    const v8i b8 = __builtin_shufflevector(b, b, 0, 1, 2, 3, 0, 1, 2, 3);
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, fp4::kFmt, fp4::kFmt, 0,
+                                                          fp4::kUnitScale, 0, fp4::hit_scale(p));
+  }
+  __device__ static int32_t hit_score(float v, int32_t acc0, int p) {
+    return fp4::hit_score(v, acc0, p);
+  }
+  __device__ static int32_t hit_thresh(int32_t th, int32_t acc0, int p) {
+    return fp4::hit_thresh(th, acc0, p);
   }
   // The main pass's mask as one more MFMA per 32 x 32 tile: the item operand is a one-hot -1.0
   // at row m's slot (lane m of the lower half), the query operand the mask word's failing rows
@@ -184,30 +201,11 @@ struct BitsF4 : I8x32 {
     for (int e = 0; e < 16; ++e) r[e] = static_cast<int32_t>(c[e]);
     return r;
   }
-  // A step's 32 bits per lane fill the 32 nibbles of the fp4 operand: nibble e of dword n holds
-  // bit 4 e + n (the K order inside an operand is free when items and queries share it), so an
-  // item dword is the word masked in place -- bit n of each nibble, e2m1 0.5, 1.0, 2.0 for
-  // n = 0, 1, 2 -- and dword 3 takes bit 3 one place down (2.0; bit 3 is the sign). The query
-  // nibble of the same slot is +-4.0, +-2.0, +-1.0, +-1.0 (sign bit set for a 0 bit), so every
-  // product of an item 1 with a query bit is +-2 exactly, and an item 0 contributes 0.
-  __device__ static v4i item_frag(uint32_t b) {
-    return v4i{static_cast<int>(b & 0x11111111u), static_cast<int>(b & 0x22222222u),
-               static_cast<int>(b & 0x44444444u), static_cast<int>((b >> 1) & 0x44444444u)};
-  }
-  // +4.0 0b0110, +2.0 0b0100, +1.0 0b0010; the sign (bit 3) set where the query bit is 0
-  __device__ static v4i query_frag(uint32_t b) {
-    constexpr uint32_t kMag[4] = {0x66666666u, 0x44444444u, 0x22222222u, 0x22222222u};
-    v4i r;
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      r[n] = static_cast<int>((kMag[n] | 0x88888888u) ^ (((b >> n) & 0x11111111u) << 3));
-    }
-    return r;
-  }
+  // A step's 32 bits per lane fill the 32 nibbles of the fp4 operand (fp4::item_frag and
+  // fp4::query_frag: an item 1 adds +-2 with the query bit, an item 0 adds 0).
+  __device__ static v4i item_frag(uint32_t b) { return fp4::item_frag(b); }
+  __device__ static v4i query_frag(uint32_t b) { return fp4::query_frag(b); }
 };
-
-// Start of the bit-code main pass's fp32 accumulators (above twice the largest row width).
-constexpr float kBitsBias = 2048.0f;
 
 // The accumulator of an op's MFMAs: MAcc where the op has one (bit codes), else Acc.
 template <class Op, class = void>
@@ -392,7 +390,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
                 "tile must split into 16-byte loads");
   static_assert(!MASKED || (kBlkQpg * MASK_DW) % kBlkThreads == 0, "mask words per thread");
   static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
-  static_assert(!Op::kBits || 2.0f * 8 * RB < kBitsBias, "bit-code sums stay below the bias");
+  static_assert(!Op::kBits || 2 * 8 * RB < 4 * 512, "scaled bit-code sums stay below the bias");
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   int8_t* stage = reinterpret_cast<int8_t*>(smem);
   // with a mask: [STAGES][kBlkQpg][MASK_DW] mask words after the tiles (none otherwise)
@@ -458,19 +456,18 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   // thresholds in the skey domain, and whether the raw-bits group maxima decide the hit test
   int32_t th[2] = {Op::skey(ts[0]), Op::skey(ts[1])};
   bool raw = Op::kIntScores || __all(th[0] >= 0 && th[1] >= 0);
-  // bit codes, main pass: the fp32 accumulators start at kBitsBias instead of the column's
-  // 64 W - 2 popcount(q), so a row that passes the mask ends positive (|sum| <= 2 * 64 W <
-  // kBitsBias) and one that fails it negative (the mask MFMA's -8192 or less); the hit test takes
-  // signed int maxima of the raw bits, exact among positive floats and below them for negative
-  // ones, against the threshold moved into the same domain (INT32_MIN: every row hits, when the
-  // threshold is not positive there)
-  int32_t thr[2];
-  int32_t accb[2];  // the score of a register: int32(value) + accb
+  // bit codes, main pass: the fp32 accumulators start at BitsF4::hit_bias instead of the
+  // column's 64 W - 2 popcount(q), with the sums scaled down (BitsF4::mma_hit), so a row that passes
+  // the mask ends positive and one that fails it negative (the mask MFMA's -8192 or less); the
+  // hit test takes signed int maxima of the raw bits, exact among positive floats and below them
+  // for negative ones, against the threshold moved into the same domain (INT32_MIN: every row
+  // hits, when the threshold is not positive there)
+  int32_t thr[2][2] = {{INT32_MIN, INT32_MIN}, {INT32_MIN, INT32_MIN}};  // [row tile][column]
+  if constexpr (Op::kBits) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const float t = static_cast<float>(th[j]) - static_cast<float>(acc0[j]) + kBitsBias;
-    thr[j] = t > 0.0f ? __builtin_bit_cast(int32_t, t) : INT32_MIN;
-    accb[j] = acc0[j] - static_cast<int32_t>(kBitsBias);
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) thr[i][j] = Op::hit_thresh(th[j], acc0[j], 2 * i + j);
   }
   uint64_t best[2] = {0ull, 0ull};  // SEED
   // list slots of this wave, one per column tile: a 32-query column tile g = q / 32 has slots
@@ -610,13 +607,14 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
       }
       if constexpr (Op::kBits) {
         // fp32 accumulators: the seed pass's from 64 W - 2 popcount(q), the scores taken out as
-        // int32 after; the main pass's from kBitsBias
+        // int32 after; the main pass's from hit_bias(2 i + j), which its first MFMA reads as an
+        // inline constant
+        if constexpr (!FHIT) {
 #pragma unroll
-        for (int i = 0; i < RTW; ++i)
+          for (int i = 0; i < RTW; ++i)
 #pragma unroll
-          for (int j = 0; j < NC; ++j) {
-            macc[i][j] = Op::mstart(FHIT ? static_cast<int32_t>(kBitsBias) : acc0[j]);
-          }
+            for (int j = 0; j < NC; ++j) macc[i][j] = Op::mstart(acc0[j]);
+        }
         // this lane's half of each of its rows (RB / 2 bytes), read once into registers; step s
         // masks its dword s into the four operand dwords (five VALU, no table)
         constexpr int HC = CH / 2;  // 16-byte chunks per half row
@@ -640,7 +638,15 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
 #pragma unroll
           for (int i = 0; i < RTW; ++i)
 #pragma unroll
-            for (int j = 0; j < NC; ++j) macc[i][j] = Op::mma(cur[i], qf[j][s], macc[i][j]);
+            for (int j = 0; j < NC; ++j) {
+              if constexpr (FHIT) {
+                macc[i][j] = Op::mma_hit(
+                    cur[i], qf[j][s], s == 0 ? Op::mstart_f(Op::hit_bias(2 * i + j)) : macc[i][j],
+                    2 * i + j);
+              } else {
+                macc[i][j] = Op::mma(cur[i], qf[j][s], macc[i][j]);
+              }
+            }
         }
         if constexpr (FHIT && masked) {
 #pragma unroll
@@ -738,7 +744,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
         // fast path: the max of each group of 4 registers (rows 8 g + 4 half + 0..3), and one
         // compare per tile column against the max of its 4 group maxima
         int32_t gm[RTW][NC][4];
-        int32_t thv[2];
+        int32_t thv[RTW][2];  // per row tile and column tile
         bool hit = false;
         // (with a mask, the maxima over the rows that pass it: a low masked bound would
         // otherwise send every group whose best row fails the mask to the slow path)
@@ -764,22 +770,29 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
             for (int j = 0; j < NC; ++j)
 #pragma unroll
               for (int g = 0; g < 4; ++g) gm[i][j][g] = group_max<Op, true>(macc[i][j], g);
-          thv[0] = thr[0];
-          thv[1] = thr[1];
+#pragma unroll
+          for (int i = 0; i < RTW; ++i) {
+            thv[i][0] = thr[i][0];
+            thv[i][1] = thr[i][1];
+          }
         } else {
           if (raw) {
             maxima(std::true_type{});
           } else {
             maxima(std::false_type{});
           }
-          thv[0] = th[0];
-          thv[1] = th[1];
+#pragma unroll
+          for (int i = 0; i < RTW; ++i) {
+            thv[i][0] = th[0];
+            thv[i][1] = th[1];
+          }
         }
 #pragma unroll
         for (int i = 0; i < RTW; ++i)
 #pragma unroll
           for (int j = 0; j < NC; ++j) {
-            hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >= thv[j];
+            hit |= imax(imax(gm[i][j][0], gm[i][j][1]), imax(gm[i][j][2], gm[i][j][3])) >=
+                   thv[i][j];
           }
         if (__any(hit)) {
           // slow path, narrowed by wave-uniform ballots: groups with a hit, then their registers
@@ -789,12 +802,12 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
             for (int j = 0; j < NC; ++j)
 #pragma unroll
               for (int g = 0; g < 4; ++g) {
-                if (__ballot(gm[i][j][g] >= thv[j]) == 0ull) continue;
+                if (__ballot(gm[i][j][g] >= thv[i][j]) == 0ull) continue;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                   Score sc;
                   if constexpr (FHIT) {
-                    sc = static_cast<int32_t>(macc[i][j][4 * g + u]) + accb[j];
+                    sc = Op::hit_score(macc[i][j][4 * g + u], acc0[j], 2 * i + j);
                   } else {
                     sc = acc[i][j][4 * g + u];
                   }
@@ -820,7 +833,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
           // the next one (wave_compact waits for the stores above before reading them back)
 #pragma unroll
           for (int jq = 0; jq < NC; ++jq) {
-            uint64_t need = __ballot(nq[jq] > a.capw - ROWS) & 0xffffffffull;
+            uint64_t need = __ballot(nq[jq] > a.capw - 32 * RTW) & 0xffffffffull;
             while (need != 0ull) {
               const int c = __builtin_ctzll(need);
               need &= need - 1;
@@ -846,6 +859,10 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
                   tau[jq] = nt;
                   ts[jq] = Op::thresh(nt);
                   th[jq] = Op::skey(ts[jq]);
+                  if constexpr (FHIT) {
+                    thr[0][jq] = Op::hit_thresh(th[jq], acc0[jq], jq);
+                    thr[1][jq] = Op::hit_thresh(th[jq], acc0[jq], 2 + jq);
+                  }
                 }
               }
             }
@@ -916,6 +933,7 @@ static int blk_stages(int64_t row_bytes, int capw, bool wide, bool bits, bool ma
 // List capacity: k plus a tile's appends (one per row and query), a power of two (sorted
 // whole).
 static int blk_capw(int64_t k, int rows) { return static_cast<int>(next_pow2(k + rows)); }
+
 
 // The layout of a batch: wide up to kBlkWideMaxBatch queries; bit codes up to
 // kBlkWideMaxBatchBits, and only where k's lists fit beside the wide layout's 16 KiB tiles (the

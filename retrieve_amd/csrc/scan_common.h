@@ -159,6 +159,14 @@ int64_t main_workgroups();
 // kScoreF32FromI32); `clause`: exact clauses tested per candidate (with a mask only).
 bool blocked_hamming_fits(int64_t B, int64_t W, int64_t k, bool masked);  // lists fit in LDS
 size_t blocked_hamming_workspace(int64_t B, int64_t N, int64_t W, int64_t k, bool masked);
+// The 1-bit Hamming top-k of small batches (B >= 1) over 512-bit codes on the fp4 matrix cores,
+// one wave per stream of tiles (scan_bits_mfma.hip); k <= kMaxK, an optional mask of
+// mask_words words a query.
+size_t bits_mfma_workspace(int64_t B, int64_t N, int64_t k);
+int bits_mfma(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, int64_t N,
+              int64_t k, const uint64_t* mask, int64_t mask_words, int64_t* out_ids,
+              void* out_scores, int score_kind, void* workspace, size_t workspace_bytes,
+              hipStream_t stream);
 // The 1-bit full scan for kMaxK < k <= kMaxKHamming (scan_hamming_large.hip).
 size_t hamming_large_k_workspace(int64_t B, int64_t N, int64_t W);
 int hamming_large_k(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, int64_t N,

@@ -235,15 +235,29 @@ static int dispatch_ham(int64_t W, const ScanArgs& a, const PassPlan& p, int64_t
 
 static int ham_qpw(int64_t B) { return static_cast<int>(B < kHamMaxQpw ? B : kHamMaxQpw); }
 
-// From this batch on, 512-bit codes are scored on the fp4 matrix cores (the blocked scan, bits as
-// e2m1 nibbles); below, one XOR + popcount pass per query and word. Measured over 30M codes
-// (k = 100, a call): the popcount pass costs ~0.33 ms + ~35-48 us per query (VALU-bound: 2 VALU
-// per 32 bits; B=4 0.46 ms, B=8 0.59 ms, B=12 0.76 ms), the matrix path ~0.46-0.52 ms from B=12
-// to B=32 (the eight-part wide layout, one real column tile), so it takes over from 8 queries.
+// From this batch on, the blocked scan on the fp4 matrix cores (bits as e2m1 nibbles) takes the
+// 512-bit batches the per-wave scan below does not (more than kBitsMfmaMaxBatch queries, and the
+// scans with exact clauses); below, one XOR + popcount pass per query and word. Measured over
+// 30M codes (k = 100, a call): the popcount pass costs ~0.33 ms + ~35-48 us per query
+// (VALU-bound: 2 VALU per 32 bits; B=4 0.46 ms, B=8 0.59 ms, B=12 0.76 ms), the blocked path
+// ~0.46-0.52 ms from B=12 to B=32, so it takes over from 8 queries.
 constexpr int64_t kHamMfmaMinBatch = 8;
 
 static bool ham_mfma(int64_t B, int64_t W, int64_t k, bool masked) {
   return W == 8 && B >= kHamMfmaMinBatch && blocked_hamming_fits(B, W, k, masked);
+}
+
+// Batches of 512-bit codes from kBitsMfmaMinBatch to kBitsMfmaMaxBatch queries run the per-wave
+// fp4 scan (scan_bits_mfma.hip: no workgroup barriers, every 16-row group read straight into
+// MFMA order), ahead of the blocked scan and the popcount pass. Over 30M codes, k = 100, a call:
+// B = 1-16 0.34-0.35 ms (main pass 0.29 ms, 6.7 TB/s), B = 32 0.38 ms, B = 64 0.50 ms (k = 1000
+// 0.51 ms); the blocked scan took 0.47 / 0.44 / 0.60 ms (1.08 ms) and the popcount pass 0.38 ms
+// at B = 1.
+constexpr int64_t kBitsMfmaMinBatch = 1;
+constexpr int64_t kBitsMfmaMaxBatch = 64;
+
+static bool ham_bits_mfma(int64_t B, int64_t W, int64_t k) {
+  return W == 8 && B >= kBitsMfmaMinBatch && B <= kBitsMfmaMaxBatch && k <= kMaxK;
 }
 
 }  // namespace rt
@@ -253,6 +267,7 @@ using namespace rt;
 extern "C" size_t rt_hamming_scan_topk_workspace(int64_t B, int64_t N, int64_t W, int64_t k,
                                                  int masked) {
   if (k > kMaxK) return hamming_large_k_workspace(B > 0 ? B : 1, N, W);
+  if (ham_bits_mfma(B, W, k)) return bits_mfma_workspace(B, N, k);
   if (ham_mfma(B, W, k, masked != 0)) {
     return blocked_hamming_workspace(B, N, W, k, masked != 0);
   }
@@ -284,6 +299,10 @@ extern "C" int rt_hamming_scan_topk(const uint64_t* query_bits, int64_t B,
   if (k > kMaxK) {
     return hamming_large_k(query_bits, B, item_bits, N, W, k, mask, mask_words, out_ids,
                            out_scores, kind, workspace, workspace_bytes, stream);
+  }
+  if (ham_bits_mfma(B, W, k)) {
+    return bits_mfma(query_bits, B, item_bits, N, k, mask, mask_words, out_ids, out_scores, kind,
+                     workspace, workspace_bytes, stream);
   }
   if (ham_mfma(B, W, k, mask != nullptr)) {
     return blocked_hamming(query_bits, B, item_bits, N, W, k, mask, mask_words, out_ids,

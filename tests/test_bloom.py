@@ -273,7 +273,7 @@ def test_compiled_plans_and_clauses(dev, mode, n_sets):
     blob, count, depth = st.prepare_plans(exprs, 7, dev)
     print(f"compiled plans {mode}, {n_sets} value sets: {count} plans", flush=True)
     got = torch.ops.st.bloom_index_search_batch_prepared(words, offs, blob, count, depth, 3, 7)
-    hits = [v for key, v in st._COMPILED.items() if key[0] == id(blob)]
+    hits = [v for key, v in st._COMPILED.items() if key[0] == st._tkey(blob)]
     assert len(hits) == 1
     if n_sets == 25:
         assert 0 < hits[0][2] <= st.MAX_CLAUSES  # the clause plans read the table
@@ -325,7 +325,7 @@ def test_clause_plans_transposed_words(dev, n, n_plans):
                                   for c, vs in parts))
     blob, count, depth = st.prepare_plans(exprs, 7, dev)
     got = st.bloom_search_t(words, offs, blob, count, depth, 3, 7)
-    hits = [v for key, v in st._COMPILED.items() if key[0] == id(blob)]
+    hits = [v for key, v in st._COMPILED.items() if key[0] == st._tkey(blob)]
     assert len(hits) == 1 and hits[0][2] > 0 and hits[0][1][2]  # every plan a clause plan
     data = blob[8 * count:]
     ref = st._bloom_search(words, offs, blob, data, data.numel() * 8, count, depth, 3, 7, False)

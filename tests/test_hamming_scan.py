@@ -116,6 +116,26 @@ def test_matrix_core_path(dev, b, n, k, masked):
     _check(dev, q, items, k, mask)
 
 
+@pytest.mark.parametrize("b,masked", [(12, False), (12, True), (70, True)])
+def test_matrix_core_skewed_queries(dev, b, masked):
+    """Queries of every popcount (all zeros, all ones, a few bits, most bits) over 1M rows, seeded:
+    the main pass's accumulators start at a fixed bias with the query's start 64 W - 2 |q| moved
+    into each threshold, so the thresholds of these queries sit far from the scores' centre."""
+    g = rng(41 + b + masked)
+    q = _codes(g, b, 8)
+    q[0] = 0
+    q[1] = -1
+    q[2] = np.int64(0x0101010101010101)
+    q[3] = ~np.int64(0x0101010101010101)
+    q[4, :4] = 0
+    base = _codes(g, 4096, 8)
+    items = base[g.integers(0, 4096, 1_000_000)]
+    items[5] = q[0]
+    items[11] = q[1]
+    mask = g.random((b, items.shape[0])) < 0.3 if masked else None
+    _check(dev, q, items, 100, mask)
+
+
 def test_matrix_core_ties(dev):
     """Few distinct 512-bit rows: every score ties in large groups, broken by the lower id."""
     g = rng(36)
