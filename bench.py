@@ -22,6 +22,7 @@ Other workloads (the remaining configurations, same JSON line):
   binary   1-bit retrieval: SimHash codes (sign of a Gaussian projection, 512 bits) scanned by
            Hamming score for the top-1000 under the Bloom + exact filter at 10 %, re-ranked by
            the int8 codes of the same vectors to the top-100 (configuration 5, B = 256)
+  hamming  the plain 1-bit Hamming top-k over the same 30M SimHash codes (B = 16 by default)
 
 Prints one JSON line with the whole-job throughput (queries/s), the dominant kernel's roofline
 fraction measured live with HIP events on its launch stream, and the reference's CPU path timed
@@ -58,6 +59,7 @@ MEASURED_TRAFFIC: dict = {
     # filtered_dense_bf16_10Mx128_b256.md, binary_30Mx512bit_b256.md
     ("filtered-dense", 10_000_000, 128, 256, 100): 2_886_129_572,
     ("binary", 30_000_000, 512, 256, 100): 2_909_370_266,
+    ("hamming", 30_000_000, 512, 16, 100): 1_921_363_968,  # hamming_30Mx512bit_b16.md
 }
 CARDINALITIES = (16, 32, 64, 128, 256, 512, 1000, 1000)
 BLOOM_BITS, BLOOM_K, HASH_K = 64, 3, 7
@@ -147,19 +149,20 @@ def dense_table(n: int, d: int, centres: torch.Tensor, seed: int, dev: torch.dev
 
 
 def simhash_tables(n: int, d: int, proj: torch.Tensor, seed: int, dev: torch.device,
-                   chunk: int = 1 << 20) -> tuple[torch.Tensor, torch.Tensor]:
+                   chunk: int = 1 << 20, with_codes: bool = True):
     """N(0,1) rows x: their SimHash codes (bit b of word w = (x @ proj.T)[64 w + b] > 0, the
-    reference's LSB-first packing) and their per-row int8 codes."""
+    reference's LSB-first packing) and their per-row int8 codes (None without with_codes)."""
     gen = torch.Generator(device=dev).manual_seed(seed)
     bits_out = torch.empty((n, proj.shape[0] // 64), dtype=torch.int64, device=dev)
-    codes = torch.empty((n, d), dtype=torch.int8, device=dev)
+    codes = torch.empty((n, d), dtype=torch.int8, device=dev) if with_codes else None
     shifts = torch.arange(64, device=dev, dtype=torch.int64)
     for s in range(0, n, chunk):
         m = min(chunk, n - s)
         x = torch.randn((m, d), generator=gen, device=dev)
         signs = (x @ proj.t() > 0).view(m, -1, 64).long()
         bits_out[s : s + m] = (signs << shifts).sum(-1)
-        codes[s : s + m] = quantize_rows(x)
+        if codes is not None:
+            codes[s : s + m] = quantize_rows(x)
     return bits_out, codes
 
 
@@ -359,10 +362,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload",
-                    choices=("filtered", "int8", "dense", "filtered-dense", "binary", "exact"),
+                    choices=("filtered", "int8", "dense", "filtered-dense", "binary", "hamming",
+                             "exact"),
                     default="filtered")
     ap.add_argument("--batch", type=int, default=None,
-                    help="query batch (default: 16 filtered / int8, 64 dense, 256 "
+                    help="query batch (default: 16 filtered / int8 / hamming, 64 dense, 256 "
                          "filtered-dense / binary)")
     ap.add_argument("--n", type=int, default=None,
                     help="items (default: 30M, dense 10M)")
@@ -413,7 +417,7 @@ def main() -> int:
     dev = torch.device("cuda:0")
     wl = args.workload
     b = args.batch or {"filtered": 16, "int8": 16, "dense": 64, "filtered-dense": 256,
-                       "binary": 256, "exact": 1024}[wl]
+                       "binary": 256, "hamming": 16, "exact": 1024}[wl]
     dense_wl = wl in ("dense", "filtered-dense", "exact")
     n = args.n or {"exact": 100_000}.get(wl, 10_000_000 if dense_wl else 30_000_000)
     d = args.d or (128 if dense_wl else 512)
@@ -609,6 +613,41 @@ def main() -> int:
             return (t_s * (n / ns), threads,
                     f"B={b} queries x first {ns} of {n} items (float32 torch.mm over 2M-row "
                     "chunks + topk + lowest-id merge)")
+
+    elif wl == "hamming":
+        log(f"generating {n} SimHash codes ({d} bits), {b} queries")
+        gen = torch.Generator(device=dev).manual_seed(555)
+        proj = torch.randn((d, d), generator=gen, device=dev)
+        item_bits, _ = simhash_tables(n, d, proj, 556, dev, with_codes=False)
+        q_bits, _ = simhash_tables(b, d, proj, 557, dev, with_codes=False)
+
+        def step():
+            return torch.ops.retrieve_amd.hamming_scan_topk(q_bits, item_bits, k)
+
+        scan_bytes = n * d // 8 + b * d // 8
+        step_bytes = scan_bytes
+        table = item_bits  # the streamed table (the read ceiling is measured over it)
+        # 512-bit codes are scored on the fp4 matrix cores (2 ops per bit, item and query);
+        # other widths by XOR + popcount. The fp4 ridge is 10.1 PFLOP/s / 8 TB/s = 1262 ops a
+        # byte, 2 b d / (d / 8) = 16 b: HBM-bound up to 78 queries.
+        scan_ops = 2 * b * n * d
+        bound = "mfma" if d == 512 and 16 * b >= 1262 else "hbm"
+        dtype = "fp4" if d == 512 else "u64"
+        data = ("synthetic: N(0,1) rows (seed 556) and queries (seed 557), SimHash over a "
+                "N(0,1) 512x512 projection (seed 555)")
+        workload = f"1-bit Hamming top-{k}: N={n} bits={d} B={b}"
+        metric = "queries/sec + achieved HBM GB/s, 1-bit Hamming top-k over 30M 512-bit codes"
+
+        def cpu_fn():
+            from oracle import baseline
+
+            ns = min(args.cpu_sample or 1_000_000, n)
+            t0 = time.perf_counter()
+            baseline.hamming_topk_cpu(q_bits.cpu().numpy(), item_bits[:ns].cpu().numpy(), k)
+            t_s = time.perf_counter() - t0
+            return (t_s * (n / ns), 1,
+                    f"B={b} queries x first {ns} of {n} items (numpy XOR + bitwise_count in "
+                    "32K-item chunks, top-k by (score, id)), one run, scaled")
 
     else:  # binary
         k1 = 1000

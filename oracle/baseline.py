@@ -78,21 +78,22 @@ def time_topk(q, item_sample, k: int, reps: int = 3, valid_fn=None) -> tuple[flo
     return time_int8(q, item_sample, k, reps=reps, valid_fn=valid_fn)
 
 
-def hamming_rerank_cpu(q_bits: np.ndarray, q_codes: np.ndarray, item_bits: np.ndarray,
-                       item_codes: np.ndarray, k1: int, k: int, valid: np.ndarray | None = None,
-                       chunk: int = 1 << 15):
-    """The 1-bit retrieval with int8 re-rank on the host: score ``64 W - 2 popcount(q ^ item)``
+_NO_SCORE = -(1 << 40)  # below every score, and safe to negate in the sort key
+
+
+def hamming_topk_cpu(q_bits: np.ndarray, item_bits: np.ndarray, k: int,
+                     valid: np.ndarray | None = None, chunk: int = 1 << 15):
+    """The 1-bit top-k on the host: score ``64 W - 2 popcount(q ^ item)``
     (``retrieve/src/retrieve/ops/reference/oporp_1bit_match_topk.py:9-41``), failing items
-    excluded, top ``k1`` by (score desc, id asc); then the int8 dots of those candidates
-    (``modules/silvertorch.py:363-379``), top ``k`` by (dot desc, id asc). Returns ids [B, k]."""
+    excluded, top ``k`` by (score desc, id asc). Returns ``(scores, ids)`` [B, k] (ids -1 and
+    scores below every score where fewer items pass)."""
     b = q_bits.shape[0]
     n = item_bits.shape[0]
     qb = q_bits.view(np.uint64)
     ib = item_bits.view(np.uint64)
     w = ib.shape[1]
-    none = -(1 << 40)  # below every score, and safe to negate in the sort key
-    best_s = np.full((b, k1), none, np.int64)
-    best_i = np.full((b, k1), -1, np.int64)
+    best_s = np.full((b, k), _NO_SCORE, np.int64)
+    best_i = np.full((b, k), -1, np.int64)
     for s in range(0, n, chunk):
         part = ib[s : s + chunk]
         pc = np.zeros((b, part.shape[0]), np.int64)
@@ -100,16 +101,27 @@ def hamming_rerank_cpu(q_bits: np.ndarray, q_codes: np.ndarray, item_bits: np.nd
             pc += np.bitwise_count(qb[:, None, j] ^ part[None, :, j]).astype(np.int64)
         sc = 64 * w - 2 * pc
         if valid is not None:
-            sc[~valid[:, s : s + part.shape[0]]] = none
+            sc[~valid[:, s : s + part.shape[0]]] = _NO_SCORE
         ids = np.broadcast_to(np.arange(s, s + part.shape[0]), sc.shape)
         cs = np.concatenate([best_s, sc], 1)
         ci = np.concatenate([best_i, ids], 1)
-        order = np.lexsort((ci, -cs), axis=1)[:, :k1]
+        order = np.lexsort((ci, -cs), axis=1)[:, :k]
         best_s = np.take_along_axis(cs, order, 1)
         best_i = np.take_along_axis(ci, order, 1)
+    return best_s, best_i
+
+
+def hamming_rerank_cpu(q_bits: np.ndarray, q_codes: np.ndarray, item_bits: np.ndarray,
+                       item_codes: np.ndarray, k1: int, k: int, valid: np.ndarray | None = None,
+                       chunk: int = 1 << 15):
+    """The 1-bit retrieval with int8 re-rank on the host: the top ``k1`` of
+    ``hamming_topk_cpu``, then the int8 dots of those candidates
+    (``modules/silvertorch.py:363-379``), top ``k`` by (dot desc, id asc). Returns ids [B, k]."""
+    b = q_bits.shape[0]
+    best_s, best_i = hamming_topk_cpu(q_bits, item_bits, k1, valid, chunk)
     out = np.full((b, k), -1, np.int64)
     for r in range(b):
-        cand = best_i[r][(best_i[r] >= 0) & (best_s[r] > none)]
+        cand = best_i[r][(best_i[r] >= 0) & (best_s[r] > _NO_SCORE)]
         dots = item_codes[cand].astype(np.int64) @ q_codes[r].astype(np.int64)
         order = np.lexsort((cand, -dots))[:k]
         out[r, : order.size] = cand[order]

@@ -120,10 +120,16 @@ struct BitsQueries {
 };
 
 // Seed pass over the strided sample: per query, each wave's best composite over its rows,
-// written to a.lists[q * S + wave index] (S = waves of the grid row).
+// written to a.lists[q * S + wave index] (S = waves of the grid row). The sample is cut into
+// chunks of kTileRows rows from row 0 (a sample block of kSeedBlock consecutive items holds
+// whole chunks); a workgroup's waves take the parts of the chunks within its strip (a multiple
+// of 16 rows from a multiple of 16) in turn, every load of a part issued before its sums. With
+// strips of 512 rows: 1024 lists a query from the default 2^17 sampled rows, few to merge, and
+// far more than the rank whose best the merge takes.
 template <int NQ>
 __global__ void __launch_bounds__(kScanThreads) bits_seed_kernel(ScanArgs a) {
   constexpr int QPW = 16 * NQ;
+  static_assert(kSeedBlock % kTileRows == 0, "sample blocks hold whole chunks");
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int col = lane & 15;
@@ -132,33 +138,46 @@ __global__ void __launch_bounds__(kScanThreads) bits_seed_kernel(ScanArgs a) {
   BitsQueries<NQ> qs;
   qs.load(a, q0, col, grp);
   const int8_t* I = static_cast<const int8_t*>(a.items);
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * a.strip;
-  const int64_t r1 = r0 + a.strip < a.n_rows ? r0 + a.strip : a.n_rows;
-  const int64_t ngroups = r1 > r0 ? cdiv(r1 - r0, kGroupRows) : 0;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * a.strip;
+  const int64_t s1 = s0 + a.strip < a.n_rows ? s0 + a.strip : a.n_rows;
   uint64_t best[NQ];
 #pragma unroll
   for (int j = 0; j < NQ; ++j) best[j] = 0ull;
-  for (int64_t gi = wave; gi < ngroups; gi += kScanWaves) {
-    // a group's rows are consecutive items (a sample block holds whole groups); rows past the
-    // strip read the last one and are never kept
-    const int64_t rb = r0 + gi * kGroupRows;
-    const int64_t lr = rb + col < r1 ? rb + col : r1 - 1;
-    const v4i x = *reinterpret_cast<const v4i*>(I + sample_item(lr, a.row_stride) * kCodeBytes +
-                                                 grp * 16);
-    v4f acc[NQ];
-    group_sums<NQ>(expand(x), qs.qf, acc);
-    const int64_t row0 = rb + 4 * grp;
-    const int64_t item0 = sample_item(row0 < r1 ? row0 : r1 - 1, a.row_stride);
+  const int64_t c1 = s1 > s0 ? (s1 - 1) / kTileRows : -1;  // the strip's last chunk
+  for (int64_t c = s0 / kTileRows + wave; c <= c1; c += kScanWaves) {
+    const int64_t r0 = c * kTileRows > s0 ? c * kTileRows : s0;
+    const int64_t r1 = c * kTileRows + kTileRows < s1 ? c * kTileRows + kTileRows : s1;
+    // the part's rows are consecutive items from sample_item(r0): one descriptor, rows past
+    // r1 read as zeros and are never kept
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(I + sample_item(r0, a.row_stride) * kCodeBytes), 0,
+        static_cast<int>((r1 - r0) * kCodeBytes), kBufferWord3);
+    v4i x[kTileGroups];
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      const uint64_t w = qs.qmask[j] != nullptr ? qs.qmask[j][item0 >> 6] : ~0ull;
+    for (int g = 0; g < kTileGroups; ++g) {
+      x[g] = __builtin_bit_cast(
+          v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                   rs, col * kCodeBytes + grp * 16 + g * kGroupRows * kCodeBytes, 0, 0));
+    }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        // rows 4 (l / 16) + r of a group from a multiple of 4: items item0 + r, one mask word
-        const uint64_t c = composite(key_of_i32(fp4::hit_score(acc[j][r], qs.acc0[j], j)),
-                                     static_cast<uint32_t>(item0 + r));
-        const bool ok = row0 + r < r1 && ((w >> (63 - ((item0 + r) & 63))) & 1ull) != 0ull;
-        best[j] = ok && c > best[j] ? c : best[j];
+    for (int g = 0; g < kTileGroups; ++g) {
+      if (r0 + g * kGroupRows >= r1) break;  // (uniform)
+      v4f acc[NQ];
+      group_sums<NQ>(expand(x[g]), qs.qf, acc);
+      const int64_t row0 = r0 + g * kGroupRows + 4 * grp;  // this lane's rows row0 + r
+      const int64_t item0 = sample_item(r0, a.row_stride) + (row0 - r0);
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        // rows from a multiple of 4: items item0 + r share one mask word
+        const uint64_t w =
+            qs.qmask[j] != nullptr && row0 < r1 ? qs.qmask[j][item0 >> 6] : ~0ull;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint64_t c = composite(key_of_i32(fp4::hit_score(acc[j][r], qs.acc0[j], j)),
+                                       static_cast<uint32_t>(item0 + r));
+          const bool ok = row0 + r < r1 && ((w >> (63 - ((item0 + r) & 63))) & 1ull) != 0ull;
+          best[j] = ok && c > best[j] ? c : best[j];
+        }
       }
     }
   }
@@ -282,10 +301,8 @@ __global__ void __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_
                                                      kNontemporal));
     }
   };
-  // one 16-row group g of tile t: its sums, the hit test, the candidates
-  auto group = [&](int64_t t, int g, const GroupOps& ops) {
-    v4f acc[NQ];
-    group_sums<NQ>(ops, qs.qf, acc);
+  // the hit test of 16-row group g of tile t (the group's sums acc), then its candidates
+  auto test = [&](int64_t t, int g, const v4f (&acc)[NQ]) {
     const int64_t row0 = t * kTileRows + g * kGroupRows + 4 * grp;
     bool hit[NQ];
     bool any = false;
@@ -303,11 +320,11 @@ __global__ void __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_
     }
   };
 
-  // NB tiles in registers (three up to two query groups, two above, which keeps two waves a
-  // SIMD): the one being scored and the others in flight. Each group's registers are reloaded
+  // NB tiles in registers (three for one query group, two above, which keeps two waves a SIMD
+  // without spills): the one being scored and the others in flight. Each group's registers are reloaded
   // with the same group of the tile NB ahead as soon as the group's operands are expanded, so
   // close to NB tiles stay in flight; the scheduling barriers keep each reload where it is.
-  constexpr int NB = NQ <= 2 ? 3 : 2;
+  constexpr int NB = NQ <= 1 ? 3 : 2;
   const int64_t ntiles = cdiv(n, kTileRows);
   v4i v0[kTileGroups], v1[kTileGroups], v2[kTileGroups];
   int64_t t = wave_in_row;
@@ -332,7 +349,9 @@ __global__ void __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_
           v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, loff + g * kGroupRows * kCodeBytes, 0,
                                                      kNontemporal));
       __builtin_amdgcn_sched_barrier(0);
-      group(tt, g, ops);
+      v4f acc[NQ];
+      group_sums<NQ>(ops, qs.qf, acc);
+      test(tt, g, acc);
     }
   };
   for (; t < ntiles; t += NB * waves) {
@@ -361,7 +380,7 @@ int bits_qgroups(int64_t B) {
 ScanPlan bits_plan(int64_t B, int64_t N, int64_t k, int64_t target_wgs) {
   const int64_t qpg = 16 * bits_qgroups(B);
   return plan_scan(B, N, k, qpg, kScanWaves * qpg, target_wgs, bits_capw(k),
-                   kScanWaves * kGroupRows, kSeedRows / 2);
+                   kScanWaves * kTileRows, kSeedRows / 2);
 }
 
 template <int NQ>
@@ -445,7 +464,6 @@ int bits_mfma(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, 
   m.qpw = static_cast<int>(plan.qpg);
   m.B = B;
   m.k = static_cast<int>(k);
-  m.part_buf = plan.split ? reinterpret_cast<uint64_t*>(ws + plan.off_parts) : nullptr;
 
   if (plan.seeded) {
     a.n_rows = plan.seed.n_rows;
@@ -473,6 +491,9 @@ int bits_mfma(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, 
   a.strip = plan.main.strip;
   a.capw = plan.main.capw;
   a.tau_in = plan.seeded ? tau : nullptr;
+  // the final merge over the main pass's lists split into parts (small batches); the seed's
+  // flat merge above is one launch (its 1024 one-entry lists a query merge faster whole)
+  m.part_buf = plan.split ? reinterpret_cast<uint64_t*>(ws + plan.off_parts) : nullptr;
   hipEvent_t stop;
   profile_begin(stream, &stop);
   int st = dispatch_bits(nq, a, plan.main, plan.n_qgroups, false, stream);
@@ -496,6 +517,7 @@ int bits_mfma(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, 
   if (st != kOk) return st;
   m.spec_flag = nullptr;
   m.run_if = spec_flag;
+  m.part_buf = nullptr;  // (one launch: it returns at once while the flag is clear)
   return launch_merge(m, stream);
 }
 

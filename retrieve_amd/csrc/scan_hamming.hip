@@ -237,7 +237,7 @@ static int ham_qpw(int64_t B) { return static_cast<int>(B < kHamMaxQpw ? B : kHa
 
 // From this batch on, the blocked scan on the fp4 matrix cores (bits as e2m1 nibbles) takes the
 // 512-bit batches the per-wave scan below does not (more than kBitsMfmaMaxBatch queries, and the
-// scans with exact clauses); below, one XOR + popcount pass per query and word. Measured over
+// scans with exact clauses or a transposed mask); below, one XOR + popcount pass per query and word. Measured over
 // 30M codes (k = 100, a call): the popcount pass costs ~0.33 ms + ~35-48 us per query
 // (VALU-bound: 2 VALU per 32 bits; B=4 0.46 ms, B=8 0.59 ms, B=12 0.76 ms), the blocked path
 // ~0.46-0.52 ms from B=12 to B=32, so it takes over from 8 queries.
@@ -250,11 +250,12 @@ static bool ham_mfma(int64_t B, int64_t W, int64_t k, bool masked) {
 // Batches of 512-bit codes from kBitsMfmaMinBatch to kBitsMfmaMaxBatch queries run the per-wave
 // fp4 scan (scan_bits_mfma.hip: no workgroup barriers, every 16-row group read straight into
 // MFMA order), ahead of the blocked scan and the popcount pass. Over 30M codes, k = 100, a call:
-// B = 1-16 0.34-0.35 ms (main pass 0.29 ms, 6.7 TB/s), B = 32 0.38 ms, B = 64 0.50 ms (k = 1000
-// 0.51 ms); the blocked scan took 0.47 / 0.44 / 0.60 ms (1.08 ms) and the popcount pass 0.38 ms
-// at B = 1.
+// B = 1-16 0.34-0.35 ms (main pass 0.29 ms, 6.7 TB/s), B = 32 0.37 ms, B = 64 0.49 ms (k = 1000
+// 0.51 ms), B = 128 0.89 ms; the blocked scan took 0.47 / 0.44 / 0.60 (1.08) / 1.09 ms and the
+// popcount pass 0.38 ms at B = 1. From 256 queries the blocked scan is faster (1.54 against
+// 1.69 ms).
 constexpr int64_t kBitsMfmaMinBatch = 1;
-constexpr int64_t kBitsMfmaMaxBatch = 64;
+constexpr int64_t kBitsMfmaMaxBatch = 128;
 
 static bool ham_bits_mfma(int64_t B, int64_t W, int64_t k) {
   return W == 8 && B >= kBitsMfmaMinBatch && B <= kBitsMfmaMaxBatch && k <= kMaxK;

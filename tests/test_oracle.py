@@ -358,6 +358,23 @@ def test_bloom_doc_bits(bits):
         assert np.array_equal((got & m) == m, of.term_mask(words, offs, n, f, v, 3, 7))
 
 
+def test_cpu_baseline_hamming_topk_equals_oracle():
+    """The bench's CPU baseline for the 1-bit scan (XOR + bitwise_count over item chunks, a
+    lexsort merge per chunk) against the oracle's full-scan top-k: few distinct rows, so every
+    boundary is a tie broken by the lower id, with and without a filter."""
+    from oracle import baseline
+
+    g = rng(71)
+    base = g.integers(-(2**63), 2**63 - 1, (37, 8), dtype=np.int64)
+    items = base[g.integers(0, 37, 5000)]
+    q = g.integers(-(2**63), 2**63 - 1, (5, 8), dtype=np.int64)
+    valid = g.random((5, 5000)) < 0.3
+    for v in (None, valid):
+        s, i = baseline.hamming_topk_cpu(q, items, 50, v, chunk=700)
+        want_i, want_s = osc.hamming_topk(q, items, 50, v)
+        assert np.array_equal(i, want_i) and np.array_equal(s, want_s)
+
+
 def test_candidate_topk_brute_force():
     """``candidate_topk`` against a brute-force full sort over each row's first ``counts[b]``
     candidates (tie-heavy scores, duplicates, short rows) and against ``candidate_int8_topk``."""
