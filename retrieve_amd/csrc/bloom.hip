@@ -689,78 +689,108 @@ __device__ inline uint64_t run_program(const BloomSearchArgs& a, gu32* prog, uin
 
 // KK = min(k, hash_k): the positions every term's program words carry. THREADS: 256, or 512
 // when a workgroup has many plans (its bundles' staging then feeds twice the waves).
+typedef __attribute__((address_space(4))) const uint32_t kcu32;
+typedef __attribute__((address_space(4))) const int64_t kci64;
+
+// Workgroup barrier over LDS only: this wave's LDS accesses done (lgkmcnt(0)), then
+// s_barrier. __syncthreads() would also wait for every global load in flight (its workgroup
+// release fence), draining the next bundle pair's prefetch; the column kernel's barriers order
+// LDS accesses only. The empty asm statements keep the compiler from moving memory accesses
+// across it.
+__device__ inline void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt and expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <int KK, int THREADS, bool CLAUSES>
 __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a) {
   constexpr int kColThreads = THREADS;
   constexpr int kColWaves = THREADS / kWave;
-  __shared__ uint64_t idx[2 * kColMaxWidth * kBloomWordsPerBundle];
+  __shared__ __attribute__((aligned(16))) uint64_t idx[2 * kColMaxWidth * kBloomWordsPerBundle];
   __shared__ uint64_t fold[kColWaves][kFoldDepth - 1][kWave];
   extern __shared__ uint64_t clause_words[];  // CLAUSES: [a.n_clauses][64 columns]
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int64_t beta0 = static_cast<int64_t>(blockIdx.x) * 2;
-  const int64_t w0 = uniform64(a.bundle_off[1] - a.bundle_off[0]);
-  // the two bundles: staged when their width is bundle 0's (the programs' positions)
-  int64_t off[3];
+  // The wave-uniform tables (bundle offsets, clause and plan descriptors) are read through the
+  // constant address space: scalar loads, waited for on lgkmcnt, so they do not wait for the
+  // next bundle pair's words in flight as vector loads (in-order vmcnt) would.
+  kci64* bundle_off = (kci64*)(a.bundle_off);
+  kcu32* clause_ptr = (kcu32*)(a.clause_ptr);
+  kcu32* clause_terms = (kcu32*)(a.clause_terms);
+  kcu32* plan_desc = (kcu32*)(a.plan_desc);
+  kcu32* plan_refs = (kcu32*)(a.plan_refs);
+  const int64_t w0 = uniform64(bundle_off[1] - bundle_off[0]);
+  // A workgroup takes bundle pairs blockIdx.x, + gridDim.x, ...: the next pair's words are
+  // loaded into registers while the current one is searched, so the index read's latency hides
+  // behind the work (one or two workgroups fit a CU, the clause words' LDS allowing).
+  const int64_t n_pairs = (a.nb + 1) / 2;
+  const int n_words = static_cast<int>(w0 >= 1 && w0 <= kColMaxWidth ? w0 : 0) *
+                      kBloomWordsPerBundle;  // a staged bundle's words
+  constexpr int kIt = kColMaxWidth * kBloomWordsPerBundle / 2 / kColThreads;  // 16-byte slots
+  // pair p's bundle offsets, and which of its two bundles are staged (their width is bundle
+  // 0's, the programs' positions)
+  auto geometry = [&](int64_t pair, int64_t(&off)[3], bool(&st)[2]) {
 #pragma unroll
-  for (int h = 0; h < 3; ++h) {
-    off[h] = beta0 + h <= a.nb ? uniform64(a.bundle_off[beta0 + h]) : 0;
-  }
-  bool staged[2];
+    for (int h = 0; h < 3; ++h) {
+      off[h] = 2 * pair + h <= a.nb ? uniform64(bundle_off[2 * pair + h]) : 0;
+    }
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    staged[h] = beta0 + h < a.nb && off[h + 1] - off[h] == w0 && w0 >= 1 && w0 <= kColMaxWidth;
-  }
-  {
-    // every load of both bundles in flight before the first LDS store: 16 bytes a load when
-    // the index is 16-byte aligned (a bundle starts at a multiple of 256 bytes from it)
-    const int n = static_cast<int>(w0) * kBloomWordsPerBundle;  // words per bundle
-    if (a.words_aligned16) {
-      constexpr int kIt = kColMaxWidth * kBloomWordsPerBundle / 2 / kColThreads;
-      v4u r[2][kIt];
+    for (int h = 0; h < 2; ++h) {
+      st[h] = 2 * pair + h < a.nb && off[h + 1] - off[h] == w0 && n_words > 0;
+    }
+  };
+  // every load of both bundles issued before any is used: 16 bytes a load when the index is
+  // 16-byte aligned (a bundle starts at a multiple of 256 bytes from it), else two of 8
+  auto fetch = [&](const int64_t(&off)[3], const bool(&st)[2], v4u(&pre)[2][kIt]) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const v4u* g = reinterpret_cast<const v4u*>(a.words + off[h] * kBloomWordsPerBundle);
+    for (int h = 0; h < 2; ++h) {
+      const uint64_t* g = a.words + off[h] * kBloomWordsPerBundle;
 #pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-          const int i = tid + it * kColThreads;
-          r[h][it] = staged[h] && 2 * i < n ? __builtin_nontemporal_load(g + i) : v4u{0, 0, 0, 0};
+      for (int it = 0; it < kIt; ++it) {
+        const int i = tid + it * kColThreads;
+        v4u v{0, 0, 0, 0};
+        if (st[h] && 2 * i < n_words) {
+          if (a.words_aligned16) {
+            v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(g) + i);
+          } else {
+            const uint64_t x = __builtin_nontemporal_load(g + 2 * i);
+            const uint64_t y = __builtin_nontemporal_load(g + 2 * i + 1);
+            v = v4u{static_cast<uint32_t>(x), static_cast<uint32_t>(x >> 32),
+                    static_cast<uint32_t>(y), static_cast<uint32_t>(y >> 32)};
+          }
         }
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        v4u* l = reinterpret_cast<v4u*>(idx + h * kColMaxWidth * kBloomWordsPerBundle);
-#pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-          const int i = tid + it * kColThreads;
-          if (staged[h] && 2 * i < n) l[i] = r[h][it];
-        }
-      }
-    } else {
-      constexpr int kIt = kColMaxWidth * kBloomWordsPerBundle / kColThreads;
-      uint64_t r[2][kIt];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint64_t* g = a.words + off[h] * kBloomWordsPerBundle;
-#pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-          const int i = tid + it * kColThreads;
-          r[h][it] = staged[h] && i < n ? __builtin_nontemporal_load(g + i) : 0ull;
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        uint64_t* l = idx + h * kColMaxWidth * kBloomWordsPerBundle;
-#pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-          const int i = tid + it * kColThreads;
-          if (staged[h] && i < n) l[i] = r[h][it];
-        }
+        pre[h][it] = v;
       }
     }
+  };
+  int64_t pair = blockIdx.x;
+  int64_t noff[3];
+  bool nst[2];
+  v4u pre[2][kIt];
+  geometry(pair, noff, nst);
+  fetch(noff, nst, pre);
+  for (; pair < n_pairs; pair += gridDim.x) {
+  const int64_t beta0 = 2 * pair;
+  int64_t off[3] = {noff[0], noff[1], noff[2]};
+  bool staged[2] = {nst[0], nst[1]};
+  lds_barrier();  // every wave is done with the previous pair's LDS
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    v4u* l = reinterpret_cast<v4u*>(idx + h * kColMaxWidth * kBloomWordsPerBundle);
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int i = tid + it * kColThreads;
+      if (staged[h] && 2 * i < n_words) l[i] = pre[h][it];
+    }
   }
-  __syncthreads();
+  if (pair + gridDim.x < n_pairs) {
+    geometry(pair + gridDim.x, noff, nst);
+    fetch(noff, nst, pre);
+  }
+  lds_barrier();
 
   const int half = lane >> 5;
   const int j = lane & 31;
@@ -786,39 +816,53 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
     // a time, and merges it into the clause's word with one LDS atomic OR.
     const int n_clauses = __builtin_amdgcn_readfirstlane(a.n_clauses);
     for (int i = tid; i < n_clauses * kWave; i += kColThreads) clause_words[i] = 0ull;
-    __syncthreads();
-    const int n_terms = __builtin_amdgcn_readfirstlane(a.clause_ptr[n_clauses]);
+    lds_barrier();
+    const int n_terms = __builtin_amdgcn_readfirstlane(clause_ptr[n_clauses]);
     const int share = (n_terms + kColWaves - 1) / kColWaves;
     const int t_lo = wave * share;
     const int t_hi = t_lo + share < n_terms ? t_lo + share : n_terms;
-    auto term = [&](int t) -> uint64_t {
-      const uint32_t* e = a.clause_terms + 4 * static_cast<int64_t>(t);
-      const uint32_t p0 = __builtin_amdgcn_readfirstlane(e[0]);
-      const uint32_t p1 = __builtin_amdgcn_readfirstlane(e[1]);
-      const int64_t hidx = static_cast<int64_t>(
-          (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(e[3])) << 32) |
-          __builtin_amdgcn_readfirstlane(e[2]));
-      return mine_staged ? staged_term<KK>(lcol, p0, p1)
-                         : term_from_hashes(a, hidx, 0, wcol, my_w);
-    };
-    int c = 0;
-    while (c < n_clauses && __builtin_amdgcn_readfirstlane(a.clause_ptr[c + 1]) <= t_lo) ++c;
-    for (int t = t_lo; t < t_hi; ++c) {
-      const int end_c = __builtin_amdgcn_readfirstlane(a.clause_ptr[c + 1]);
-      const int end = end_c < t_hi ? end_c : t_hi;
-      uint64_t v = 0ull;
-      for (; t + 3 < end; t += 4) {
-        const uint64_t x0 = term(t);
-        const uint64_t x1 = term(t + 1);
-        const uint64_t x2 = term(t + 2);
-        const uint64_t x3 = term(t + 3);
-        v |= (x0 | x1) | (x2 | x3);
+    // STAGED: both bundles staged (wave-uniform), so the loop holds no global load whose wait
+    // would also wait for the next pair's words in flight
+    auto clause_terms_or = [&](auto staged_c) {
+      constexpr bool STAGED = decltype(staged_c)::value;
+      auto term = [&](int t) -> uint64_t {
+        kcu32* e = clause_terms + 4 * static_cast<int64_t>(t);
+        const uint32_t p0 = __builtin_amdgcn_readfirstlane(e[0]);
+        const uint32_t p1 = __builtin_amdgcn_readfirstlane(e[1]);
+        if constexpr (STAGED) {
+          return staged_term<KK>(lcol, p0, p1);
+        } else {
+          const int64_t hidx = static_cast<int64_t>(
+              (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(e[3])) << 32) |
+              __builtin_amdgcn_readfirstlane(e[2]));
+          return mine_staged ? staged_term<KK>(lcol, p0, p1)
+                             : term_from_hashes(a, hidx, 0, wcol, my_w);
+        }
+      };
+      int c = 0;
+      while (c < n_clauses && __builtin_amdgcn_readfirstlane(clause_ptr[c + 1]) <= t_lo) ++c;
+      for (int t = t_lo; t < t_hi; ++c) {
+        const int end_c = __builtin_amdgcn_readfirstlane(clause_ptr[c + 1]);
+        const int end = end_c < t_hi ? end_c : t_hi;
+        uint64_t v = 0ull;
+        for (; t + 3 < end; t += 4) {
+          const uint64_t x0 = term(t);
+          const uint64_t x1 = term(t + 1);
+          const uint64_t x2 = term(t + 2);
+          const uint64_t x3 = term(t + 3);
+          v |= (x0 | x1) | (x2 | x3);
+        }
+        for (; t < end; ++t) v |= term(t);
+        __hip_atomic_fetch_or(&clause_words[c * kWave + lane], v, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_WORKGROUP);
       }
-      for (; t < end; ++t) v |= term(t);
-      __hip_atomic_fetch_or(&clause_words[c * kWave + lane], v, __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
+    if (all_staged) {
+      clause_terms_or(std::true_type{});
+    } else {
+      clause_terms_or(std::false_type{});
     }
-    __syncthreads();
+    lds_barrier();
   }
 
   const int64_t b0 = static_cast<int64_t>(blockIdx.y) * a.plans_per_wg;
@@ -835,8 +879,8 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
       const int64_t col0 = beta0 * kBloomWordsPerBundle;
       for (int64_t c0 = b0; c0 < b1; c0 += kWave) {
         for (int64_t pb = c0 + wave; pb < b1 && pb < c0 + kWave; pb += kColWaves) {
-          const uint32_t desc = __builtin_amdgcn_readfirstlane(a.plan_desc[pb]);
-          const uint32_t* refs = a.plan_refs + ((desc >> 12) & 0x7ffffu);
+          const uint32_t desc = __builtin_amdgcn_readfirstlane(plan_desc[pb]);
+          kcu32* refs = plan_refs + ((desc >> 12) & 0x7ffffu);
           const int cnt = static_cast<int>(desc & 0xfffu);
           uint64_t top = ~0ull;
           for (int r = 0; r < cnt; ++r) {
@@ -847,7 +891,7 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
           const int p = static_cast<int>(pb - c0);
           idx[lane * kWave + (p ^ lane)] = top;
         }
-        __syncthreads();
+        lds_barrier();
         for (int i = tid; i < kWave * kWave; i += kColThreads) {
           const int r = i / kWave;
           const int p = i % kWave;
@@ -855,9 +899,9 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
             ot[(col0 + r) * a.out_t_stride + c0 + p] = static_cast<int64_t>(idx[r * kWave + (p ^ r)]);
           }
         }
-        __syncthreads();
+        lds_barrier();
       }
-      return;
+      continue;
     }
   }
   // each plan's header and first 64 program ops are loaded while the plan before it runs (a
@@ -888,9 +932,9 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
     }
     if constexpr (CLAUSES) {
       // a plan of clauses: the AND of its clauses' words (NOT: inverted)
-      const uint32_t desc = __builtin_amdgcn_readfirstlane(a.plan_desc[b]);
+      const uint32_t desc = __builtin_amdgcn_readfirstlane(plan_desc[b]);
       if (desc >> 31) {
-        const uint32_t* refs = a.plan_refs + ((desc >> 12) & 0x7ffffu);
+        kcu32* refs = plan_refs + ((desc >> 12) & 0x7ffffu);
         const int cnt = static_cast<int>(desc & 0xfffu);
         uint64_t top = ~0ull;
         for (int r = 0; r < cnt; ++r) {
@@ -922,6 +966,7 @@ __global__ void __launch_bounds__(THREADS) bloom_column_kernel(BloomSearchArgs a
     }
     if (valid) write_column(a, b, ncol, col, top);
   }
+  }  // bundle pairs
 }
 
 // ---- stack evaluation: the plans the program cannot hold --------------------------------
@@ -1231,6 +1276,20 @@ static int launch_column(const BloomSearchArgs& a, dim3 grid, int waves, size_t 
   if (lds > 0) {
     RT_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(lds)));
+  }
+  // as many workgroups over the bundle pairs as stay resident together (each then loops over
+  // its pairs, the next one's words in flight)
+  int occ = 0;
+  int dev = 0;
+  int cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, waves * kWave,
+                                                   static_cast<int>(lds)) == hipSuccess &&
+      hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      occ > 0 && cus > 0) {
+    const int64_t resident = static_cast<int64_t>(occ) * cus;
+    const int64_t gx = cdiv(resident, static_cast<int64_t>(grid.y));
+    if (gx < static_cast<int64_t>(grid.x)) grid.x = static_cast<unsigned>(gx < 1 ? 1 : gx);
   }
   if (waves == 8) {
     bloom_column_kernel<KK, 512, CLAUSES><<<grid, 512, lds, stream>>>(a);
