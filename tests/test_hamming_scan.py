@@ -136,6 +136,42 @@ def test_matrix_core_skewed_queries(dev, b, masked):
     _check(dev, q, items, 100, mask)
 
 
+@pytest.mark.parametrize("b,n,k,masked,wide_mask", [
+    (1, 15, 20, False, False),
+    (17, 16, 16, True, False),
+    (48, 127, 100, True, True),
+    (64, 129, 129, False, False),
+    (65, 1000, 37, True, True),
+    (100, 5000, 1, False, False),
+    (128, 4099, 64, True, False),
+])
+def test_per_wave_bits_edges(dev, b, n, k, masked, wide_mask):
+    """512-bit codes on the per-wave fp4 scan (1 to 128 queries): fewer rows than one 16-row
+    group, partial groups and 128-row tiles (rows past the table read as zeros and are never
+    kept), batches across the 16-query groups of a wave and the grid's second row of groups,
+    k above N (padded), a query no item passes, and mask rows wider than ceil(N/64) words (the
+    extra words all ones, past the table)."""
+    g = rng(b * 11 + n + k)
+    q = _codes(g, b, 8)
+    items = _codes(g, n, 8)
+    mask = None
+    mt = None
+    if masked:
+        mask = g.random((b, n)) < 0.4
+        mask[0] = False
+        packed = _pack(mask)
+        if wide_mask:
+            packed = np.concatenate([packed, np.full((b, 3), -1, np.int64)], 1)
+        mt = torch.from_numpy(packed).to(dev)
+    print(f"per-wave bits B={b} N={n} k={k} mask={masked} wide={wide_mask}", flush=True)
+    ids, sc = torch.ops.retrieve_amd.hamming_scan_topk(
+        torch.from_numpy(q).to(dev), torch.from_numpy(items).to(dev), k, mt)
+    torch.cuda.synchronize()
+    want_ids, want_sc = osc.hamming_topk(q, items, k, mask)
+    assert np.array_equal(sc.cpu().numpy(), want_sc)
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+
+
 def test_matrix_core_ties(dev):
     """Few distinct 512-bit rows: every score ties in large groups, broken by the lower id."""
     g = rng(36)
