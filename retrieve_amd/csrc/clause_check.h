@@ -123,6 +123,30 @@ __device__ inline AttrRow load_attr_row(const ClauseCheck& f, int64_t item) {
   return r;
 }
 
+// load_attr_row for rows of HB bytes (4, 8 or 16; a compile-time size: no branch).
+template <int HB>
+__device__ inline AttrRow load_attr_row_n(const ClauseCheck& f, int64_t item) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  static_assert(HB == 4 || HB == 8 || HB == 16, "held rows are 4, 8 or 16 bytes");
+  const char* row = static_cast<const char*>(f.attrs) + item * HB;
+  AttrRow r{{0u, 0u, 0u, 0u}};
+  if constexpr (HB == 16) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(row);
+    r.w[0] = v[0];
+    r.w[1] = v[1];
+    r.w[2] = v[2];
+    r.w[3] = v[3];
+  } else if constexpr (HB == 8) {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(row);
+    r.w[0] = v[0];
+    r.w[1] = v[1];
+  } else {
+    r.w[0] = *reinterpret_cast<const uint32_t*>(row);
+  }
+  return r;
+}
+
 // Word i of a held row (a select chain: no indexed private array).
 __device__ inline uint32_t row_word(const AttrRow& r, int i) {
   return i == 0 ? r.w[0] : i == 1 ? r.w[1] : i == 2 ? r.w[2] : r.w[3];

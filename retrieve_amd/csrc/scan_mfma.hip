@@ -87,7 +87,7 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
   using Score = typename Op::Score;
   constexpr int64_t D = KSTEPS * 64;  // row bytes
   const int lane = lane_id();
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int8_t* I = static_cast<const int8_t*>(a.items);
@@ -117,30 +117,51 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
   const int64_t r1 = r0 + a.strip < a.n_rows ? r0 + a.strip : a.n_rows;
   const int64_t ntiles = r1 > r0 ? cdiv(r1 - r0, kTile) : 0;
   uint64_t best = 0ull;
-  for (int64_t t = wave; t < ntiles; t += kScanWaves) {
-    const int64_t rb = r0 + t * kTile;
-    int64_t lr = rb + col;
-    lr = lr < r1 ? lr : r1 - 1;
-    const int8_t* ip = I + sample_item(lr, a.row_stride) * D + grp * 16;
+  // Tile t's loads: its rows' fragments, this lane's four rows' attributes (held rows: loaded
+  // before it is known which rows are candidates, so the tests wait on the same round of
+  // loads) and their mask word (four sample rows from a multiple of four are consecutive items
+  // of one word). A wave takes tiles wave, + kScanWaves, ... with two tiles' loads in flight:
+  // buffers A and B alternate, each reloaded with the tile two ahead right after it is scored;
+  // past the strip a buffer reloads the last tile (never used), so every load is unconditional
+  // and the waits before a tile cover only the loads issued before its own.
+  struct SeedTile {
     v4i af[KSTEPS];
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) af[s] = *reinterpret_cast<const v4i*>(ip + s * 64);
-    // held rows: this lane's four rows' attributes, loaded with the tile (before it is known
-    // which rows are candidates), so the tests below wait on the same round of loads
     AttrRow rows[4];
-    if (held) {
+    uint64_t mw;
+  };
+  // HB: the held rows' bytes (0: not held), MASKED: a mask; both compile-time, so no branch
+  // sits between a tile's loads and the waits before it is scored
+  auto run = [&](auto hb_c, auto masked_c) {
+  constexpr int HB = decltype(hb_c)::value;
+  constexpr bool MASKED = decltype(masked_c)::value;
+  auto fetch = [&](int64_t t, SeedTile& b) {
+    const int64_t rb = r0 + (t < ntiles ? t : ntiles - 1) * kTile;
+    const int64_t lr = rb + col < r1 ? rb + col : r1 - 1;
+    const int8_t* ip = I + sample_item(lr, a.row_stride) * D + grp * 16;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) b.af[s] = *reinterpret_cast<const v4i*>(ip + s * 64);
+    const int64_t row0 = rb + 4 * grp;
+    if constexpr (HB > 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t row = rb + 4 * grp + r;
-        rows[r] = load_attr_row(a.clause, sample_item(row < r1 ? row : r1 - 1, a.row_stride));
+        const int64_t row = row0 + r;
+        b.rows[r] = load_attr_row_n<HB>(a.clause,
+                                        sample_item(row < r1 ? row : r1 - 1, a.row_stride));
       }
     }
+    if constexpr (MASKED) {
+      b.mw = qmask[sample_item(row0 < r1 ? row0 : r1 - 1, a.row_stride) >> 6];
+    } else {
+      b.mw = ~0ull;
+    }
+  };
+  auto score = [&](int64_t t, const SeedTile& b) {
+    const int64_t rb = r0 + t * kTile;
     typename Op::Acc acc = Op::zero();
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) acc = Op::mma(af[s], qf[s], acc);
-    // the rows whose composite would raise the maximum, then the filters on them only: one
-    // mask word (four sample rows from a multiple of four are consecutive items of one word),
-    // then the clauses from the best row down until one passes
+    for (int s = 0; s < KSTEPS; ++s) acc = Op::mma(b.af[s], qf[s], acc);
+    // the rows whose composite would raise the maximum, then the filters on them only: the
+    // mask word, then the clauses from the best row down until one passes
     uint64_t cs[4];
     uint32_t cand = 0u;
 #pragma unroll
@@ -150,26 +171,27 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
                         static_cast<uint32_t>(sample_item(row, a.row_stride)));
       cand |= row < r1 && cs[r] > best ? 1u << r : 0u;
     }
-    if (qmask != nullptr && cand != 0u) {
+    if (MASKED && cand != 0u) {
       const int64_t item0 = sample_item(rb + 4 * grp, a.row_stride);
-      const uint64_t w = qmask[item0 >> 6];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        cand &= (w >> (63 - ((item0 + r) & 63))) & 1ull ? ~0u : ~(1u << r);
+        cand &= (b.mw >> (63 - ((item0 + r) & 63))) & 1ull ? ~0u : ~(1u << r);
       }
     }
-    if (held && cand != 0u) {
+    if (HB > 0 && cand != 0u) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        if ((cand >> r) & 1u && !clause_pass_held(a.clause, crow, rows[r])) cand &= ~(1u << r);
+        if ((cand >> r) & 1u && !clause_pass_held(a.clause, crow, b.rows[r])) {
+          cand &= ~(1u << r);
+        }
       }
     }
-    if (!clauses || held) {
+    if (!clauses || HB > 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) best = (cand >> r) & 1u && cs[r] > best ? cs[r] : best;
     }
-    while (__any(clauses && !held && cand != 0u)) {
-      if (clauses && !held && cand != 0u) {
+    while (__any(clauses && HB == 0 && cand != 0u)) {
+      if (clauses && HB == 0 && cand != 0u) {
         int rb_ = 0;
         uint64_t cb = 0ull;
 #pragma unroll
@@ -185,6 +207,38 @@ __global__ void __launch_bounds__(kScanThreads) seed_mfma_kernel(ScanArgs a) {
           cand = 0u;
         }
       }
+    }
+  };
+  SeedTile ba;
+  SeedTile bb;
+  fetch(wave, ba);
+  fetch(wave + kScanWaves, bb);
+  for (int64_t t = wave; t < ntiles; t += 2 * kScanWaves) {
+    score(t, ba);
+    fetch(t + 2 * kScanWaves, ba);
+    if (t + kScanWaves >= ntiles) break;
+    score(t + kScanWaves, bb);
+    fetch(t + 3 * kScanWaves, bb);
+  }
+  };
+  // (uniform: the row size and the mask are the launch's)
+  const int hb = held ? a.clause.C * a.clause.A * a.clause.attr_bytes : 0;
+  auto run_hb = [&](auto masked_c) {
+    if (hb == 16) {
+      run(std::integral_constant<int, 16>{}, masked_c);
+    } else if (hb == 8) {
+      run(std::integral_constant<int, 8>{}, masked_c);
+    } else if (hb == 4) {
+      run(std::integral_constant<int, 4>{}, masked_c);
+    } else {
+      run(std::integral_constant<int, 0>{}, masked_c);
+    }
+  };
+  if (ntiles > 0) {
+    if (qmask != nullptr) {
+      run_hb(std::true_type{});
+    } else {
+      run_hb(std::false_type{});
     }
   }
   uint64_t o = __shfl_xor(best, 16);
@@ -435,6 +489,19 @@ static int64_t mfma_seed_rows(int64_t B, int64_t N) {
   return kSeedRows / 2;
 }
 
+// Rows of the seed sample a workgroup takes: kSeedTiles 16-row tiles a wave, two tiles' loads
+// in flight (2048 one-entry lists a query from 2^17 sampled rows). Four tiles keep four waves a
+// SIMD for the clause tests' dependent LDS lookups; one tile a wave (8192 lists) merged slower,
+// eight (one wave a SIMD) left the clause seed latency-bound: the filtered int8 step at B = 16
+// 2.349-2.352 ms with eight, 2.338-2.341 ms with four (the plain int8 scan 2.253 / 2.260 ms).
+constexpr int kSeedTiles = 4;
+
+// The plan of a scan of B queries over N rows, top-k, over target_wgs main-pass workgroups.
+static ScanPlan mfma_plan(int64_t B, int64_t N, int64_t k, int64_t target_wgs) {
+  return plan_scan(B, N, k, 16, kScanWaves * 16, target_wgs, mfma_capw(k),
+                   kScanWaves * kTile * kSeedTiles, mfma_seed_rows(B, N));
+}
+
 // seed scan → seed threshold merge → main scan → final merge, on `stream`, no host sync
 template <class Op>
 static int run_mfma_scan(const void* queries, int64_t B, const void* items, int64_t N,
@@ -456,8 +523,7 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   if (N == 0) return launch_pad(out_ids, out_scores, B, k, Op::kind, stream);
   RT_CHECK_ARG(queries != nullptr && items != nullptr && workspace != nullptr,
                "queries, items and workspace must not be null");
-  const ScanPlan plan = plan_scan(B, N, k, 16, kScanWaves * 16, main_workgroups(), mfma_capw(k),
-                                  kScanWaves * kTile, mfma_seed_rows(B, N));
+  const ScanPlan plan = mfma_plan(B, N, k, main_workgroups());
   if (workspace_bytes < plan.total) {
     set_error("workspace too small: %zu < %zu", workspace_bytes, plan.total);
     return kWorkspaceTooSmall;
@@ -496,7 +562,6 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   m.qpw = 16;
   m.B = B;
   m.k = static_cast<int>(k);
-  m.part_buf = plan.split ? reinterpret_cast<uint64_t*>(ws + plan.off_parts) : nullptr;
 
   if (plan.seeded) {
     a.n_rows = plan.seed.n_rows;
@@ -524,6 +589,9 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   a.row_stride = 1;
   a.strip = plan.main.strip;
   a.capw = plan.main.capw;
+  // the final merge over the main pass's lists split into parts (small batches); the seed's
+  // flat merge above is one launch (its 1024 one-entry lists a query merge faster whole)
+  m.part_buf = plan.split ? reinterpret_cast<uint64_t*>(ws + plan.off_parts) : nullptr;
   a.clause_lds = 0;  // the main pass's launch decides
   a.tau_in = plan.seeded ? tau : nullptr;
   hipEvent_t stop;
@@ -549,6 +617,7 @@ static int run_mfma_scan(const void* queries, int64_t B, const void* items, int6
   if (st != kOk) return st;
   m.spec_flag = nullptr;
   m.run_if = spec_flag;
+  m.part_buf = nullptr;  // (one launch: it returns at once while the flag is clear)
   return launch_merge(m, stream);
 }
 
@@ -558,8 +627,7 @@ using namespace rt;
 
 extern "C" size_t rt_int8_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
   (void)D;
-  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k),
-                   kScanWaves * kTile, mfma_seed_rows(B, N))
+  return mfma_plan(B, N, k, kMaxResidentWorkgroups)
       .total;
 }
 
@@ -624,8 +692,7 @@ extern "C" int rt_int8_scan_topk_noalloc(const int8_t* queries, int64_t B, const
   RT_CHECK_ARG(B == 0 || (out_ids != nullptr && out_scores != nullptr &&
                           (N == 0 || (queries != nullptr && items != nullptr))),
                "queries, items, out_ids and out_scores must not be null");
-  const size_t need = plan_scan(B, N, k, 16, kScanWaves * 16, main_workgroups(), mfma_capw(k),
-                                kScanWaves * kTile, mfma_seed_rows(B, N))
+  const size_t need = mfma_plan(B, N, k, main_workgroups())
                           .total;
   RT_CHECK_ARG(need <= kNoAllocScratchBytes,
                "rt_int8_scan_topk_noalloc: B = %lld, N = %lld, k = %lld need %zu bytes of "
@@ -642,8 +709,7 @@ extern "C" int rt_int8_scan_topk_noalloc(const int8_t* queries, int64_t B, const
 // ---- scans with the exact clause filter tested per candidate --------------------------------
 
 static size_t mfma_plan_bytes(int64_t B, int64_t N, int64_t k) {
-  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k),
-                   kScanWaves * kTile, mfma_seed_rows(B, N))
+  return mfma_plan(B, N, k, kMaxResidentWorkgroups)
       .total;
 }
 
@@ -739,8 +805,7 @@ extern "C" int rt_scan_topk_bloom_clauses(
 
 extern "C" size_t rt_dense_scan_topk_workspace(int64_t B, int64_t N, int64_t D, int64_t k) {
   (void)D;
-  return plan_scan(B, N, k, 16, kScanWaves * 16, kMaxResidentWorkgroups, mfma_capw(k),
-                   kScanWaves * kTile, mfma_seed_rows(B, N))
+  return mfma_plan(B, N, k, kMaxResidentWorkgroups)
       .total;
 }
 
