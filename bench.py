@@ -658,13 +658,17 @@ def main() -> int:
         q_bits, q_codes = simhash_tables(b, d, proj, 557, dev)
         flt = Filter(n, b, args.selectivity, dev)
 
+        # the 1-bit stage pads a row past its candidates with -1, which the candidate scan skips
+        # (ids outside the table are never read): each row's count is the full width
+        full_counts = torch.full((b,), k1, dtype=torch.int64, device=dev)
+
         def step():
             ids1, _ = torch.ops.retrieve_amd.hamming_scan_topk_clauses(
                 q_bits, item_bits, k1, flt.attrs, flt.rev, flt.sets,
                 flt.bloom_t() if b >= 8 and k1 <= 1024 else flt.bloom(),
                 fused=not args.unfused_bits)
-            counts = (ids1 >= 0).sum(1)
-            return torch.ops.retrieve_amd.int8_candidates_topk(q_codes, item_codes, ids1, counts, k)
+            return torch.ops.retrieve_amd.int8_candidates_topk(q_codes, item_codes, ids1,
+                                                               full_counts, k)
 
         scan_bytes = n * d // 8 + b * d // 8
         table = item_bits  # the streamed table (the read ceiling is measured over it)
