@@ -485,9 +485,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
   int nq[2] = {0, 0};
 
   const int64_t n = a.n_rows;
-  // the main pass may scan every tstride-th tile only (the threshold sample pass)
-  const int64_t tstride = !SEED && a.tile_stride > 1 ? a.tile_stride : 1;
-  const int64_t ntiles = cdiv(cdiv(n, ROWS), tstride);
+  const int64_t ntiles = cdiv(n, ROWS);
   // Staged tile layout (no padding): row r's 16-byte chunk c sits at r * RB + (c ^ (r % CH)) * 16,
   // so the 32 rows of an MFMA read start on different banks. A wave's direct-to-LDS load writes
   // 1 KiB contiguously in lane order, so the swizzle goes into the global address each lane
@@ -526,7 +524,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     }
   };
   auto issue = [&](int64_t lt, int st) {
-    const int64_t tt = lt * tstride;  // the tile in the item table
+    const int64_t tt = lt;  // the tile in the item table
     int8_t* base = stage + st * TILE_BYTES;
     if constexpr (masked) issue_mask(tt, st);
     // One buffer descriptor per tile: base = its first row, range = its rows present. A tile's
@@ -696,7 +694,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
         }
       }
       // register r of tile (i, j) holds row t * 64 + 32 i + (r / 4) * 8 + 4 half + r % 4
-      const int64_t rt = t * tstride * ROWS + 4 * half;
+      const int64_t rt = t * ROWS + 4 * half;
       if constexpr (SEED) {
         // the mask words with this lane's half shifted out of the way (bit 31 - 8 g - u: row
         // 8 g + 4 half + u)
@@ -1095,27 +1093,6 @@ static ScanPlan blk_plan(int64_t B, int64_t N, int64_t k, int64_t row_bytes, int
   return p;
 }
 
-// The threshold sample pass: the main kernel on every stride-th tile, when that gives
-// kSampleMinTiles tiles or more, behind the seed's bound. Its merge takes a speculative bound,
-// the m-th best of the sample with m = sample_rank(k, stride): an unordered table puts about
-// Poisson(k / stride) of its top k in the sample, so m = k / stride + 5 sqrt(k / stride) + 4
-// falls below the table's k-th best but for a tail of about 1e-6 a query, and the main pass then
-// keeps about m * stride candidates a query instead of the N k / (seed rows) behind the seed's
-// bound. The stride is 32 where that still gives kSampleMinTiles tiles (half the sample pass and
-// its merge for ~20 % more main-pass candidates), else 16. A query that ends with fewer than k
-// entries although its bound was above the seed's raises a flag, and the fallback (the main pass
-// and the merge again behind the seed's bound, both returning at once on the device while the
-// flag is clear) keeps every result exact.
-constexpr int64_t kSampleTileStride = 16;
-constexpr int64_t kSampleWideStride = 32;
-constexpr int64_t kSampleMinTiles = 2048;
-
-// 0: no sample pass (fewer than kSampleMinTiles tiles at the narrow stride)
-static int64_t sample_stride(int64_t N) {
-  if (N >= kSampleMinTiles * kSampleWideStride * kBlkRows) return kSampleWideStride;
-  if (N >= kSampleMinTiles * kSampleTileStride * kBlkRows) return kSampleTileStride;
-  return 0;
-}
 
 
 
@@ -1231,28 +1208,33 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
   a.row_stride = 1;
   a.capw = plan.main.capw;
   a.tau_in = plan.seeded ? tau : nullptr;
-  const int64_t stride = plan.seeded ? sample_stride(N) : 0;
-  const bool sampled = stride > 0;
-  const bool speculative = sampled && sample_rank(k, stride) < k;
-  if (sampled) {
-    a.tile_stride = stride;
-    int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, wide, stream);
-    if (st != kOk) return st;
-    m.capw = plan.main.capw;
-    m.S = plan.main.S;
-    m.k = sample_rank(k, stride);
+  // The speculative bound: the seed's rank-th best (sample_rank of its row stride) instead of
+  // its k-th, taken from the same one-entry lists by a second threshold merge (at least the
+  // k-th: tau_keep over tau). The lists hold each seed workgroup's best over its strip of the
+  // sample, so the rank-th of them is at most the sample's rank-th best; the main pass then
+  // keeps about rank * stride candidates a query instead of N k / (seed rows). A query that
+  // ends with fewer than k entries although its bound was above the seed's k-th raises a flag,
+  // and the fallback (the main pass and the merge again behind the k-th, both returning at once
+  // on the device while the flag is clear) keeps every result exact.
+  const int seed_rank = plan.seeded ? sample_rank(k, plan.seed.row_stride) : static_cast<int>(k);
+  const bool speculative = plan.seeded && seed_rank < k;
+  if (speculative) {
+    m.capw = 1;
+    m.flat = true;
+    m.S = plan.seed.S;
+    m.k = seed_rank;
     m.tau_out = spec;
     m.tau_keep = true;
     m.tau_base = tau;
     m.spec_flag = spec_flag;  // (cleared)
-    st = launch_merge(m, stream);
+    int st = launch_merge(m, stream);
     if (st != kOk) return st;
     m.k = static_cast<int>(k);
+    m.flat = false;
     m.tau_out = nullptr;
     m.tau_keep = false;
     m.tau_base = nullptr;
     m.spec_flag = nullptr;
-    a.tile_stride = 1;
     a.tau_in = spec;
   }
   hipEvent_t stop;

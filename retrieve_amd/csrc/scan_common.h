@@ -33,9 +33,7 @@ struct ScanArgs {
   int64_t B;
   const void* items;       // [N, D] (or [N, W] words)
   int64_t n_rows;          // rows of this pass's index space
-  int64_t row_stride;      // item index = row * row_stride (the sample pass strides)
-  int64_t tile_stride;     // blocked main kernel: pass tile t reads tile t * tile_stride (0, 1:
-                           // every tile)
+  int64_t row_stride;      // item index = row * row_stride (the seed's sample strides)
   int64_t strip;           // rows per workgroup, a multiple of kTile
   int k;
   int qpw;                 // queries per wave (a query group), for scans that vary it

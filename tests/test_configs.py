@@ -6,9 +6,9 @@ oracle:
   GPU in fp32 (the raw scorer and the key select), at full size, with duplicated rows whose
   equal scores must come back in index order;
 - configuration 2 (bf16 10M x 128, B in {1, 64, 1024, 4096}): B = 512 / 1024 over 2.2M clustered
-  rows, the narrow 256-byte-row layout with the seed pass, the threshold sample pass over every
-  16th tile and the main pass, masked and unmasked, bf16 and fp16, with rows whose only survivors
-  sit in tiles the sample pass skips;
+  rows, the narrow 256-byte-row layout with the seed pass (its k-th and rank-th bounds) and the
+  main pass, masked and unmasked, bf16 and fp16, with rows whose only survivors sit in two
+  64-row tiles, one of them outside every seed sample block;
 - configuration 3 (filtered bf16, B = 256): the masked register-blocked bf16 / fp16 kernel at
   B in {40, 128, 256} with empty rows, rows of fewer than k survivors and rows whose survivors
   all score below zero (the float hit test's non-raw path), and the whole pipeline (Bloom
@@ -117,10 +117,10 @@ def _check_dense_large(dev, q32, it32, k, dtype, mask: PackedMask | None = None)
 
 
 def _large_mask(g, q32, it32, b, n) -> PackedMask:
-    """Random 1/4-density rows plus the rows the sample pass must not lose: no survivors, 37
-    survivors, survivors only in tiles 1 and 17 (rows 64-127 and 1088-1151: the 64-row tiles of
-    the narrow 256-byte-row layout that the every-16th-tile sample skips), and survivors that
-    all score below zero."""
+    """Random 1/4-density rows plus rows the seed's bounds must not lose: no survivors, 37
+    survivors, survivors only in tiles 1 and 17 (rows 64-127, inside the seed's first sample
+    block, and 1088-1151, outside every block: the 64-row tiles of the narrow 256-byte-row
+    layout), and survivors that all score below zero."""
     w = (n + 63) // 64
     words = g.integers(0, 2**64, (b, w), dtype=np.uint64) & g.integers(0, 2**64, (b, w),
                                                                         dtype=np.uint64)
@@ -145,7 +145,7 @@ def _large_mask(g, q32, it32, b, n) -> PackedMask:
 @pytest.fixture(scope="module")
 def config2_table():
     """configs[1]'s generator (Gaussian clusters, sigma 0.3, L2-normalised) at 2.2M rows: above
-    the sample pass's 2048 x 16 x 64 rows."""
+    the blocked scan's seed threshold (8 x 2^18 rows)."""
     g = rng(2)
     centres = g.standard_normal((1024, 128))
     it = _clustered(g, 2_200_000, 128, centres)
@@ -157,14 +157,14 @@ def config2_table():
                                             (1024, torch.bfloat16, True),
                                             (1024, torch.float16, False),
                                             (512, torch.float16, True)])
-def test_config2_large_batch_sample_pass(dev, config2_table, b, dtype, masked):
+def test_config2_large_batch_seeded(dev, config2_table, b, dtype, masked):
     g, q, it = config2_table
     q = q[:b]
     mask = _large_mask(rng(b + int(masked)), q, it, b, it.shape[0]) if masked else None
     ids = _check_dense_large(dev, q, it, 100, dtype, mask)
     if masked:
-        # the rows the sample pass cannot see: every survivor of row 2 sits in a skipped tile,
-        # and there are 128 of them, so the top-100 is entirely from those tiles
+        # every survivor of row 2 sits in tiles 1 and 17, 128 of them, so the top-100 is
+        # entirely from those tiles
         assert ((64 <= ids[2]) & (ids[2] < 128) | (1088 <= ids[2]) & (ids[2] < 1152)).all()
         assert (ids[0] == -1).all() and (ids[1, :37] >= 0).all() and (ids[1, 37:] == -1).all()
 

@@ -150,8 +150,8 @@ def test_errors(dev):
 
 
 def test_large_batch_seeded_path(dev):
-    """bf16 at B = 256 over 2.2M clustered rows: the blocked kernel's seeded path with the
-    threshold sample pass (every 16th tile from 2.1M rows on, every 32nd from 4.2M)."""
+    """bf16 at B = 256 over 2.2M clustered rows: the blocked kernel's seeded path, the main pass
+    behind the seed sample's rank-th best."""
     g = rng(18)
     centres = g.standard_normal((64, 128))
     it = _clustered(g, 2_200_000, 128, centres)

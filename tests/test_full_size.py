@@ -98,10 +98,10 @@ def _check_binary(dev, n, w, b, k, masked, n_sample, seed):
 
 
 def test_binary_masked_30m(dev):
-    """64 queries over 30M rows: the threshold sample pass reads every 32nd tile."""
+    """64 queries over 30M rows at k = 1000 (a seed of 1,024,000 rows and its rank-th bound)."""
     _check_binary(dev, 30_000_000, 8, 64, 1000, True, 1_000_000, 31)
 
 
 def test_binary_large_batch_9m(dev):
-    """512 queries over 9M rows (every 32nd tile sampled) with no mask."""
+    """512 queries over 9M rows (the blocked scan behind its seed's rank-th bound), no mask."""
     _check_binary(dev, 9_000_000, 8, 512, 100, False, 200_000, 37)

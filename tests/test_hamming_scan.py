@@ -182,8 +182,8 @@ def test_matrix_core_ties(dev):
     _check(dev, q[:9], items, 37)
 
 
-def test_matrix_core_sample_pass(dev):
-    """B >= 512 over N >= 2.1M rows: the seed, the threshold sample pass and the main pass."""
+def test_matrix_core_seeded_large_batch(dev):
+    """B >= 512 over N >= 2.1M rows: the seed (its k-th and rank-th bounds) and the main pass."""
     g = rng(37)
     q = _codes(g, 520, 8)
     base = _codes(g, 4096, 8)
@@ -194,8 +194,8 @@ def test_matrix_core_sample_pass(dev):
 
 @pytest.mark.parametrize("masked", [False, True])
 def test_matrix_core_speculative_bound(dev, masked):
-    """N >= 2.1M rows below 512 queries: the threshold sample pass bounds the main pass by the
-    sample's m-th best (m = 23 at k = 100, 106 at k = 1000), and the results stay exact."""
+    """N >= 2.1M rows below 512 queries: the main pass runs behind the seed sample's rank-th best
+    (23 at k = 100 over a 16th of the rows), and the results stay exact."""
     g = rng(38 + masked)
     q = _codes(g, 40, 8)
     base = _codes(g, 4096, 8)
@@ -212,17 +212,26 @@ def _near(q: np.ndarray, d: int) -> np.ndarray:
     return x
 
 
-def test_matrix_core_speculative_fallback(dev):
-    """Query 0's 30 best rows sit in the table's first tile, which the threshold sample pass
-    reads: the sample's 23rd best (k = 100) bounds the main pass above all but 23 rows, so that
-    query ends short of k, the fallback pass behind the seed's bound runs, and every result is
-    exact."""
+# Items at the first row of seed sample blocks far enough apart to fall in different seed lists,
+# for N = 2.2M rows and k = 100: the blocked scan samples 256-row blocks every 8 blocks (stride
+# 8, 2^18 rows, 128 sample rows a seed workgroup), the per-wave 1-bit scan every 16 (stride 16,
+# 2^17 rows, 128 a seed wave), so items 16384 j start blocks 8 j and 4 j of the two samples.
+SEED_SPREAD = [16384 * j for j in range(1, 41)]
+
+
+@pytest.mark.parametrize("b", [40, 130])
+def test_matrix_core_speculative_fallback(dev, b):
+    """Query 0's 40 best rows sit at the start of 40 seed sample blocks, one a seed list: the
+    seed's rank-th best (23rd at B = 40 on the per-wave scan, 35th at B = 130 on the blocked scan)
+    is one of them, so the main pass keeps 23 / 35 rows for that query and ends short of k = 100,
+    the flag rises, and the fallback pass (unbounded on the per-wave scan, behind the seed's k-th
+    on the blocked one) gives every result exactly."""
     g = rng(40)
-    q = _codes(g, 40, 8)
+    q = _codes(g, b, 8)
     base = _codes(g, 4096, 8)
     items = base[g.integers(0, 4096, 2_200_000)]
-    for r in range(30):
-        items[r] = _near(q[0], r + 1)
+    for j, r in enumerate(SEED_SPREAD):
+        items[r] = _near(q[0], j + 1)
     _check(dev, q, items, 100)
 
 

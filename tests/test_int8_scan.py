@@ -214,10 +214,10 @@ def test_large_batch_seeded_ties_masked(dev):
     _check(dev, q[:130], items[:50000], 100, mask)
 
 
-def test_large_batch_sample_pass(dev):
-    """512-byte rows, B >= 512 over N >= 2.1M rows run the threshold sample pass (every 16th
-    tile) before the main pass: heavy ties across the sampled and unsampled tiles, and a mask
-    with an empty row and a row whose few passing items miss the sample."""
+def test_large_batch_seeded_512b_rows(dev):
+    """512-byte rows, B >= 512 over N >= 2.1M rows: the blocked scan's seed (its k-th and
+    rank-th bounds) and main pass, heavy ties across sampled and unsampled rows, and a mask with
+    an empty row and a row whose few passing items miss the sample."""
     g = rng(17)
     base = g.integers(-127, 128, (256, 512), dtype=np.int8)
     n = 2_100_000

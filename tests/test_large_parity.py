@@ -6,10 +6,11 @@
   attributes and 10 % value sets; and its ``--bloom-search`` form, ``int8_scan_topk_clauses`` under the words straight
   from ``st::bloom_index_search_batch_prepared`` with their bundle-padded width (more words
   than ceil(N / 64));
-- the blocked scans' stride-32 threshold sample (N >= 2048 * 32 * 64 = 4,194,304 rows): int8 at
-  B = 1024, bf16 and fp16 at B = 1024 and 4096 (configuration 2's largest batch, clustered
-  rows), and configuration 5's main path (512-bit codes, B = 256, k = 1000, the Bloom words
-  stored transposed, the exact clauses fused).
+- the blocked scans over 4.3M rows, behind the seed sample's rank-th best: int8 at B = 1024,
+  bf16 and fp16 at B = 1024 and 4096 (configuration 2's largest batch, clustered rows), and
+  configuration 5's main path (512-bit codes, B = 256, k = 1000: a seed of 1,024,000 rows, the
+  Bloom words stored transposed, the exact clauses fused);
+- the small-batch scan's fallback when the seed's rank-th bound fails.
 
 The tables repeat a set of distinct base rows, so the oracle scores only those and selects
 through ``oracle.select.RepeatedRows`` (pinned against ``topk_rows`` in ``tests/test_oracle.py``).
@@ -32,7 +33,7 @@ from tests.conftest import rng
 pytestmark = pytest.mark.gpu
 
 N_SEEDED = 2_300_000  # above the small-batch scan's seed threshold (2**21 rows)
-N_STRIDE32 = 4_300_000  # the blocked scans sample every 32nd tile from 4,194,304 rows
+N_LARGE = 4_300_000  # the blocked scans' seed samples a 16th of it (k = 100), a 4th (k = 1000)
 
 
 @pytest.fixture(scope="module")
@@ -105,9 +106,9 @@ def test_headline_step_as_benched(dev, n):
     _check_exact(ids, sc, base_sc, rep, k, exact)
 
 
-def test_int8_b1024_stride32_sample(dev):
-    n, b, d, k, n_base = N_STRIDE32, 1024, 512, 100, 1 << 16
-    print(f"int8 scan B={b} N={n} D={d} k={k} (stride-32 sample)", flush=True)
+def test_int8_b1024_large(dev):
+    n, b, d, k, n_base = N_LARGE, 1024, 512, 100, 1 << 16
+    print(f"int8 scan B={b} N={n} D={d} k={k} (blocked, seeded)", flush=True)
     g = rng(1301)
     base = _int8_rows(g, n_base, d)
     row_of = g.integers(0, n_base, n)
@@ -126,13 +127,13 @@ def _clustered(g, rows: int, d: int, centres: np.ndarray) -> np.ndarray:
 
 @pytest.mark.parametrize("dtype,b", [(torch.bfloat16, 1024), (torch.bfloat16, 4096),
                                      (torch.float16, 4096)])
-def test_dense_large_batch_stride32_sample(dev, dtype, b):
+def test_dense_large_batch_large(dev, dtype, b):
     """Float scores: within 1e-3 relative of the float64 dot of the rounded values; the k-th
     boundary up to near ties; every item of a base row scoring clearly above the oracle's k-th
     returned; and the copies of one base row (equal scores on the GPU too) taken lowest index
     first, as the tie rule requires."""
-    n, d, k, n_base, rtol = N_STRIDE32, 128, 100, 1 << 16, 1e-3
-    print(f"dense scan {dtype} B={b} N={n} D={d} k={k} (stride-32 sample)", flush=True)
+    n, d, k, n_base, rtol = N_LARGE, 128, 100, 1 << 16, 1e-3
+    print(f"dense scan {dtype} B={b} N={n} D={d} k={k} (blocked, seeded)", flush=True)
     g = rng(1302 + b)
     centres = g.standard_normal((1024, d))
     base = torch.from_numpy(_clustered(g, n_base, d, centres)).to(dtype)
@@ -163,7 +164,7 @@ def test_dense_large_batch_stride32_sample(dev, dtype, b):
 
 
 @pytest.mark.timeout(400)
-def test_config5_main_path_stride32_sample(dev):
+def test_config5_main_path_large(dev):
     """512-bit codes, B = 256, k = 1000 over 4.3M rows under the Bloom words of the bench's 10 %
     value sets, stored transposed (read in place by the blocked scan), the exact clauses fused.
     (The oracle's clause predicate over 256 rows x 4.3M items takes about a minute of CPU.)"""
@@ -171,7 +172,7 @@ def test_config5_main_path_stride32_sample(dev):
     import retrieve_amd.st as st
     from retrieve_amd import bloom as bl
 
-    n, b, w, k, n_base = N_STRIDE32, 256, 8, 1000, 1 << 16
+    n, b, w, k, n_base = N_LARGE, 256, 8, 1000, 1 << 16
     print(f"1-bit clause scan B={b} N={n} W={w} k={k}, transposed Bloom words", flush=True)
     g = rng(1303)
     base = g.integers(-2**63, 2**63 - 1, (n_base, w), dtype=np.int64)
@@ -199,25 +200,35 @@ def test_config5_main_path_stride32_sample(dev):
 
 @pytest.mark.parametrize("clauses", [False, True])
 def test_speculative_seed_bound_falls_back(dev, clauses):
-    """The small-batch scan bounds its main pass by the seed sample's rank-th best (about 10 of
-    k = 100 here), a bound that fails only when the sample holds more of the top k than chance
-    allows. Rows stored in descending score order for query 0 make it fail for that query (the
-    first sample block holds the best rows): its main pass ends short, the flag raises and the
-    fallback pass without the bound must give the exact top-k, bit for bit; the other queries
-    are unaffected either way."""
+    """The small-batch scan bounds its main pass by the seed sample's rank-th best (the 23rd of
+    k = 100 here: 2^17 of 2.3M rows, 256-row blocks every 17 blocks, one seed workgroup a block),
+    a bound that fails only when the sample holds more of the top k than chance allows. Query 0's
+    30 best rows (its own code with 0 .. 29 leading dimensions zeroed, above every base row) sit
+    at the start of sample blocks 1 .. 30, one a seed list, so the 23rd best list is one of them:
+    that query's main pass keeps 23 entries and ends short, the flag rises and the fallback pass
+    without the bound must give the exact top-k, bit for bit; the other queries are unaffected
+    either way."""
     n, b, d, k, n_base = N_SEEDED, 4, 128, 100, 4096
     print(f"speculative seed fallback B={b} N={n} D={d} k={k} clauses={clauses}", flush=True)
     g = rng(1400 + clauses)
     base = _int8_rows(g, n_base, d)
     q = _int8_rows(g, b, d)
+    best = np.repeat(q[:1], 30, axis=0)
+    for c in range(30):
+        best[c, :c] = 0
+    base = np.concatenate([base, best])
     base_sc = osc.int8_scores(q, base)
-    order = np.argsort(-base_sc[0], kind="stable")
-    row_of = np.repeat(order, -(-n // n_base))[:n]
+    assert base_sc[0, n_base:].min() > base_sc[0, :n_base].max()
+    row_of = g.integers(0, n_base, n)
+    planted = 4352 * np.arange(1, 31)  # block j starts at item 256 * 17 * j
+    row_of[planted] = n_base + np.arange(30)
+    n_base += 30
     items = torch.from_numpy(base).to(dev)[torch.from_numpy(row_of).to(dev)]
     qt = torch.from_numpy(q).to(dev)
     rep = osel.RepeatedRows(row_of, n_base)
     if clauses:
         attrs = g.integers(0, 4, (n, 2, 1)).astype(np.int16)
+        attrs[planted, 0, 0] = 0  # query 0's planted rows pass its clause (values 0, 2)
         sets = np.full((b, 2, 2), -1, np.int64)
         sets[:, 0, :2] = [0, 2]
         sets[1:, 1, 0] = 3

@@ -272,7 +272,7 @@ def test_blocked_adversarial_order(dev):
                                          (torch.float32, 64, 50_000, 64)])
 def test_blocked_dense_equals_unfused(dev, dtype, b, n, d):
     """bf16 / fp16 / fp32 large batches with a mask equal the same scan over the clause mask:
-    the seeded path (N above 2**21) and, at B = 512, the threshold sample pass."""
+    the seeded path (N above 2**21) with its rank-th bound."""
     g = rng(909 + b)
     print(f"blocked dense clause scan {dtype} B={b} N={n} D={d}", flush=True)
     q = torch.from_numpy(g.standard_normal((b, d)).astype(np.float32)).to(dev).to(dtype)
@@ -327,11 +327,13 @@ def test_hamming_parity(dev, b, n, k, ones):
 
 
 def test_hamming_speculative_fallback(dev):
-    """N >= 2.1M rows, clauses tested in the scan: query 0's 30 best rows that pass its clause
-    sit in the table's first tile (read by the threshold sample pass) behind 30 better rows that
-    pass its mask but fail the clause. The sample's bound counts passing rows only (its 23rd best
-    at k = 100), the main pass ends with 23 passing entries, the fallback behind the seed's bound
-    runs, and the results match the oracle."""
+    """N >= 2.2M rows, clauses tested in the scan (the blocked 1-bit scan): query 0's 40 best
+    rows that pass its clause sit at the start of 40 seed sample blocks, one a seed workgroup
+    (items 16384 j: blocks 8 j of the seed's stride-8 sample), and 30 better rows that pass its
+    mask but fail the clause sit in the first block. The seed's lists offer passing maxima only
+    (the first block's, a failing row, offers none), so its rank-th best (35th at k = 100) is a
+    planted row; the main pass ends with 35 passing entries, the flag rises, the fallback behind
+    the seed's k-th runs, and the results match the oracle."""
     g = rng(916)
     b, n, k = 40, 2_200_000, 100
     print(f"hamming clause scan, speculative fallback B={b} N={n} k={k}", flush=True)
@@ -343,13 +345,23 @@ def test_hamming_speculative_fallback(dev):
     sets[0] = -1
     sets[0, 0, 0] = 5  # query 0: attribute 0 equal to 5
     rev = np.array([0, 0, 1], bool)
-    for r in range(60):
+    def off(d):  # q[0] with d of its bits flipped (up to 60 in word 0, the rest in word 1)
         x = q[0].copy()
-        x[0] ^= np.int64((1 << (61 - r if r < 30 else r - 29)) - 1)
-        items[r] = x  # rows 0-29: 60 .. 31 bits off; rows 30-59: 1 .. 30 bits off
-        attrs[r, 0, 0] = 5 if r < 30 else 6
+        x[0] ^= np.int64((1 << min(d, 60)) - 1)
+        if d > 60:
+            x[1] ^= np.int64((1 << (d - 60)) - 1)
+        return x
+
+    planted = [16384 * j for j in range(1, 41)]
+    for j, r in enumerate(planted):
+        items[r] = off(31 + j)  # 31 .. 70 bits off
+        attrs[r, 0, 0] = 5
+    for r in range(1, 31):
+        items[r] = off(r)  # 1 .. 30 bits off
+        attrs[r, 0, 0] = 6
     mask = g.random((b, n)) < 0.5
-    mask[0, :60] = True
+    mask[0, planted] = True
+    mask[0, 1:31] = True
     args = (_t(dev, attrs.astype(np.int16)), _t(dev, rev), _t(dev, sets), _t(dev, _pack(mask)))
     ids, sc = torch.ops.retrieve_amd.hamming_scan_topk_clauses(_t(dev, q), _t(dev, items), k, *args,
                                                            fused=True)
@@ -357,4 +369,4 @@ def test_hamming_speculative_fallback(dev):
     want_ids, want_sc = osc.hamming_topk(q, items, k, valid)
     assert np.array_equal(sc.cpu().numpy(), want_sc)
     assert np.array_equal(ids.cpu().numpy(), want_ids)
-    assert set(range(30)) <= set(ids[0].tolist())
+    assert set(planted) <= set(ids[0].tolist())
