@@ -396,11 +396,17 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
     uint64_t lo = 0ull;
     uint64_t hi = 0ull;
     if (held == k) block_minmax(buf, held, red, &lo, &hi);
+    // and the k2-th over the same held entries, the best k2 of everything (a radix select:
+    // block-uniform, as held is)
+    const uint64_t t2 = m.tau2_out != nullptr && held >= m.k2
+                            ? block_select_desc(buf, held, m.k2, hist, sh, red)
+                            : 0ull;
     if (tid == 0) {
       const uint64_t t = held == k ? lo : 0ull;
       const uint64_t old =
           m.tau_keep ? (m.tau_base != nullptr ? m.tau_base[q] : m.tau_out[q]) : 0ull;
       m.tau_out[q] = t > old ? t : old;
+      if (m.tau2_out != nullptr) m.tau2_out[q] = t2 > t ? t2 : t;
       if (m.spec_flag != nullptr && q == 0) *m.spec_flag = 0u;
     }
     return;

@@ -1199,44 +1199,34 @@ static int run_blocked(const void* queries, int64_t B, const void* items, int64_
     m.flat = true;
     m.S = plan.seed.S;
     m.tau_out = tau;
+    // the speculative bound from the same lists (below)
+    const int rank = sample_rank(k, plan.seed.row_stride);
+    if (rank < k) {
+      m.tau2_out = spec;
+      m.k2 = rank;
+      m.spec_flag = spec_flag;  // (cleared)
+    }
     st = launch_merge(m, stream);
     if (st != kOk) return st;
     m.tau_out = nullptr;
+    m.tau2_out = nullptr;
+    m.spec_flag = nullptr;
     m.flat = false;
   }
   a.n_rows = N;
   a.row_stride = 1;
   a.capw = plan.main.capw;
   a.tau_in = plan.seeded ? tau : nullptr;
-  // The speculative bound: the seed's rank-th best (sample_rank of its row stride) instead of
-  // its k-th, taken from the same one-entry lists by a second threshold merge (at least the
-  // k-th: tau_keep over tau). The lists hold each seed workgroup's best over its strip of the
-  // sample, so the rank-th of them is at most the sample's rank-th best; the main pass then
-  // keeps about rank * stride candidates a query instead of N k / (seed rows). A query that
-  // ends with fewer than k entries although its bound was above the seed's k-th raises a flag,
-  // and the fallback (the main pass and the merge again behind the k-th, both returning at once
-  // on the device while the flag is clear) keeps every result exact.
-  const int seed_rank = plan.seeded ? sample_rank(k, plan.seed.row_stride) : static_cast<int>(k);
-  const bool speculative = plan.seeded && seed_rank < k;
-  if (speculative) {
-    m.capw = 1;
-    m.flat = true;
-    m.S = plan.seed.S;
-    m.k = seed_rank;
-    m.tau_out = spec;
-    m.tau_keep = true;
-    m.tau_base = tau;
-    m.spec_flag = spec_flag;  // (cleared)
-    int st = launch_merge(m, stream);
-    if (st != kOk) return st;
-    m.k = static_cast<int>(k);
-    m.flat = false;
-    m.tau_out = nullptr;
-    m.tau_keep = false;
-    m.tau_base = nullptr;
-    m.spec_flag = nullptr;
-    a.tau_in = spec;
-  }
+  // The speculative bound: the seed's rank-th best (sample_rank of its row stride) beside its
+  // k-th, both from the seed merge above (the rank-th at least the k-th). The lists hold each
+  // seed workgroup's best over its strip of the sample, so the rank-th of them is at most the
+  // sample's rank-th best; the main pass then keeps about rank * stride candidates a query
+  // instead of N k / (seed rows). A query that ends with fewer than k entries although its
+  // bound was above the seed's k-th raises a flag, and the fallback (the main pass and the
+  // merge again behind the k-th, both returning at once on the device while the flag is clear)
+  // keeps every result exact.
+  const bool speculative = plan.seeded && sample_rank(k, plan.seed.row_stride) < k;
+  if (speculative) a.tau_in = spec;
   hipEvent_t stop;
   profile_begin(stream, &stop);
   int st = dispatch_blk<Op>(row_bytes, a, plan.main, plan.n_qgroups, false, wide, stream);

@@ -73,6 +73,8 @@ struct MergeArgs {
   uint64_t* tau_out;   // threshold mode: [B]
   bool tau_keep;       // threshold mode: write max(tau_base[q] (or tau_out[q]), the new bound)
   const uint64_t* tau_base;  // threshold mode with tau_keep: the bound to keep, or null
+  uint64_t* tau2_out;  // threshold mode, not null: also the k2-th composite (k2 < k), at least
+  int k2;              // the k-th (0 when fewer than k2 entries exist)
   const uint32_t* run_if;    // not null: the merge runs only if *run_if != 0 (a fallback merge)
   // Speculative bounds: in threshold mode block 0 clears *spec_flag; in final mode a query that
   // holds fewer than k entries although its bound spec_tau[q] is above the safe safe_tau[q]
