@@ -111,6 +111,12 @@ ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int64_t qpg, int64_t lists_p
 // ---- merge ------------------------------------------------------------------------------
 
 constexpr int kMergeChunk = 10240;  // list entries gathered into LDS per round
+// The light form for grids of more queries than CUs whose queries read at most
+// kMergeSlotsLight lists: rounds of kMergeChunkLight entries, ~30 KB of LDS for k <= 128
+// against ~140 KB, so four workgroups share a CU instead of one.
+constexpr int kMergeChunkLight = 2048;
+constexpr int kMergeSlotsLight = 1024;
+constexpr int64_t kMergeLightMinBlocks = 256;
 constexpr int kMergeWaves = kMergeThreads / kWave;
 
 // Block-wide min and max of keys[0, n) (LDS). Every thread calls it; all get the results.
@@ -242,12 +248,12 @@ __device__ uint64_t block_select_desc(const uint64_t* keys, int n, int kth, unsi
 // union is found by radix select and only the entries >= it are kept; the survivors are
 // sorted at the end. With tau_out set, only the k-th composite is written (0 when fewer than
 // k entries exist: no bound; with tau_keep, the larger of it and the bound already there).
-template <int KP>
+template <int KP, int CHUNK = kMergeChunk, int SLOTS = kMaxMergeSlots>
 __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
-  __shared__ uint64_t buf[KP + kMergeChunk];
+  __shared__ uint64_t buf[KP + CHUNK];
   __shared__ uint64_t tmp[KP];
-  __shared__ int pre[kMaxMergeSlots];
-  __shared__ short owner[kMergeChunk];
+  __shared__ int pre[SLOTS];
+  __shared__ short owner[CHUNK];
   __shared__ unsigned hist[256];
   __shared__ int part[kMergeThreads];
   __shared__ uint64_t red[2 * kMergeWaves];
@@ -308,8 +314,8 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(MergeArgs m) {
   // Empty entries (0) are dropped from the start.
   uint64_t thr = 0ull;
   int held = 0;
-  for (int e0 = 0; e0 < total; e0 += kMergeChunk) {
-    const int n = total - e0 < kMergeChunk ? total - e0 : kMergeChunk;
+  for (int e0 = 0; e0 < total; e0 += CHUNK) {
+    const int n = total - e0 < CHUNK ? total - e0 : CHUNK;
     if (!m.flat) {
       // owner[] maps each entry of the window to its list (LDS only)
       for (int s = tid; s < S; s += kMergeThreads) {
@@ -473,6 +479,14 @@ int launch_pad(int64_t* out_ids, void* out_scores, int64_t B, int64_t k, int sco
 
 static int launch_merge_grid(const MergeArgs& m, int64_t blocks, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(blocks));
+#ifndef RT_MERGE_LIGHT
+#define RT_MERGE_LIGHT 1
+#endif
+  if (RT_MERGE_LIGHT && m.k <= 128 && m.S <= kMergeSlotsLight && blocks > kMergeLightMinBlocks) {
+    merge_kernel<128, kMergeChunkLight, kMergeSlotsLight><<<grid, kMergeThreads, 0, stream>>>(m);
+    RT_CHECK_HIP(hipGetLastError());
+    return kOk;
+  }
   if (m.k <= 128) {
     merge_kernel<128><<<grid, kMergeThreads, 0, stream>>>(m);
   } else if (m.k <= 256) {
