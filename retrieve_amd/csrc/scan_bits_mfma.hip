@@ -35,6 +35,11 @@ constexpr int kGroupRows = 16;                        // rows of one MFMA
 constexpr int kTileGroups = 8;                        // row groups of a main-pass tile
 constexpr int kTileRows = kGroupRows * kTileGroups;  // 128 rows, 8 KiB
 constexpr int kMaxQGroups = 4;                        // 16-query groups of a wave
+// Two query groups whose lists leave room for three workgroups a CU: 64-row tiles (four
+// groups), so the kernel fits three waves a SIMD; B = 17-32 0.343-0.353 -> 0.335-0.348 ms a call.
+constexpr int kTileGroupsSmall = 4;
+constexpr int kWavesSmall = 3;
+constexpr size_t kLdsPerCU = 160 * 1024;
 // Word 3 of a raw buffer descriptor (stride 0, byte offsets; out-of-range loads return zeros),
 // and the cache-policy bits of a streamed load (nontemporal).
 constexpr int kBufferWord3 = 0x00020000;
@@ -197,11 +202,13 @@ __global__ void __launch_bounds__(kScanThreads) bits_seed_kernel(ScanArgs a) {
 
 // Main pass: every item, candidate lists per (wave, query). List of query 16 j + c of this
 // wave's group row: lists[(slot * QPW + 16 j + c) * capw], its length cnt[16 j + c] (LDS).
-template <int NQ>
-__global__ void __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2)))
+template <int NQ, int TG = kTileGroups>
+__global__ void __launch_bounds__(kScanThreads)
+    __attribute__((amdgpu_waves_per_eu(TG == kTileGroupsSmall ? kWavesSmall : 2)))
     bits_scan_kernel(ScanArgs a) {
   if (a.run_if != nullptr && *a.run_if == 0u) return;  // (uniform: the fallback is not needed)
   constexpr int QPW = 16 * NQ;
+  constexpr int TR = kGroupRows * TG;  // rows of a tile
   extern __shared__ __attribute__((aligned(16))) uint64_t smem[];
   const int lane = lane_id();
   // wave-uniform, so the tile indices and buffer descriptors derived from it live in SGPRs
@@ -287,15 +294,15 @@ __global__ void __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_
   // the end read as zeros and are never kept; a tile past the table has range 0 and reads no
   // memory), so a lane's offsets are 32-bit constants and every load is issued unconditionally:
   // the waits before each group then count exactly the loads issued after it.
-  auto load = [&](int64_t tt, v4i(&v)[kTileGroups]) {
-    const int64_t rt = tt * kTileRows;
+  auto load = [&](int64_t tt, v4i(&v)[TG]) {
+    const int64_t rt = tt * TR;
     const int64_t left = rt < n ? (n - rt) * kCodeBytes : 0;
-    const int range = static_cast<int>(left < kTileRows * kCodeBytes ? left
-                                                                     : kTileRows * kCodeBytes);
+    const int range = static_cast<int>(left < TR * kCodeBytes ? left
+                                                                     : TR * kCodeBytes);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(I + rt * kCodeBytes), 0, range, kBufferWord3);
 #pragma unroll
-    for (int g = 0; g < kTileGroups; ++g) {
+    for (int g = 0; g < TG; ++g) {
       v[g] = __builtin_bit_cast(
           v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, loff + g * kGroupRows * kCodeBytes, 0,
                                                      kNontemporal));
@@ -303,7 +310,7 @@ __global__ void __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_
   };
   // the hit test of 16-row group g of tile t (the group's sums acc), then its candidates
   auto test = [&](int64_t t, int g, const v4f (&acc)[NQ]) {
-    const int64_t row0 = t * kTileRows + g * kGroupRows + 4 * grp;
+    const int64_t row0 = t * TR + g * kGroupRows + 4 * grp;
     bool hit[NQ];
     bool any = false;
 #pragma unroll
@@ -325,22 +332,22 @@ __global__ void __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_
   // with the same group of the tile NB ahead as soon as the group's operands are expanded, so
   // close to NB tiles stay in flight; the scheduling barriers keep each reload where it is.
   constexpr int NB = NQ <= 1 ? 3 : 2;
-  const int64_t ntiles = cdiv(n, kTileRows);
-  v4i v0[kTileGroups], v1[kTileGroups], v2[kTileGroups];
+  const int64_t ntiles = cdiv(n, TR);
+  v4i v0[TG], v1[TG], v2[TG];
   int64_t t = wave_in_row;
   load(t, v0);
   load(t + waves, v1);
   if constexpr (NB == 3) load(t + 2 * waves, v2);
-  auto step = [&](int64_t tt, v4i(&v)[kTileGroups]) {
+  auto step = [&](int64_t tt, v4i(&v)[TG]) {
     // tile tt from v, v refilled with tile tt + NB waves
-    const int64_t rn = (tt + NB * waves) * kTileRows;
+    const int64_t rn = (tt + NB * waves) * TR;
     const int64_t left = rn < n ? (n - rn) * kCodeBytes : 0;
-    const int range = static_cast<int>(left < kTileRows * kCodeBytes ? left
-                                                                     : kTileRows * kCodeBytes);
+    const int range = static_cast<int>(left < TR * kCodeBytes ? left
+                                                                     : TR * kCodeBytes);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(I + rn * kCodeBytes), 0, range, kBufferWord3);
 #pragma unroll
-    for (int g = 0; g < kTileGroups; ++g) {
+    for (int g = 0; g < TG; ++g) {
       // the group's operands first, so its registers are free for the refill (no copies of a
       // load still in flight)
       const GroupOps ops = expand(v[g]);
@@ -383,23 +390,42 @@ ScanPlan bits_plan(int64_t B, int64_t N, int64_t k, int64_t target_wgs) {
                    kScanWaves * kTileRows, kSeedRows / 2);
 }
 
+// LDS of a main-pass workgroup: each wave's compaction scratch and list lengths.
+size_t bits_main_lds(int capw, int nq) {
+  return kScanWaves * (static_cast<size_t>(capw) * sizeof(uint64_t) + 16 * nq * sizeof(int));
+}
+
+// The 64-row-tile form: two query groups whose lists leave room for three workgroups a CU.
+bool bits_small_tiles(int nq, int capw) {
+  return nq == 2 && kWavesSmall * bits_main_lds(capw, nq) <= kLdsPerCU;
+}
+
+template <int NQ, int TG>
+int launch_main(const ScanArgs& a, const dim3 grid, size_t lds, hipStream_t stream) {
+  if (lds > 65536) {
+    RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(bits_scan_kernel<NQ, TG>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds)));
+  }
+  bits_scan_kernel<NQ, TG><<<grid, kScanThreads, lds, stream>>>(a);
+  RT_CHECK_HIP(hipGetLastError());
+  return kOk;
+}
+
 template <int NQ>
 int launch_bits(const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed,
                 hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.gx), static_cast<unsigned>(nqg));
   if (seed) {
     bits_seed_kernel<NQ><<<grid, kScanThreads, 0, stream>>>(a);
-  } else {
-    const size_t lds = kScanWaves * (p.capw * sizeof(uint64_t) + 16 * NQ * sizeof(int));
-    if (lds > 65536) {
-      RT_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(bits_scan_kernel<NQ>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(lds)));
-    }
-    bits_scan_kernel<NQ><<<grid, kScanThreads, lds, stream>>>(a);
+    RT_CHECK_HIP(hipGetLastError());
+    return kOk;
   }
-  RT_CHECK_HIP(hipGetLastError());
-  return kOk;
+  const size_t lds = bits_main_lds(p.capw, NQ);
+  if constexpr (NQ == 2) {
+    if (bits_small_tiles(NQ, p.capw)) return launch_main<NQ, kTileGroupsSmall>(a, grid, lds, stream);
+  }
+  return launch_main<NQ, kTileGroups>(a, grid, lds, stream);
 }
 
 int dispatch_bits(int nq, const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed,
@@ -434,7 +460,10 @@ int bits_mfma(const uint64_t* query_bits, int64_t B, const uint64_t* item_bits, 
                    reinterpret_cast<uintptr_t>(item_bits) % 16 == 0,
                "query_bits must be 4-byte and item_bits 16-byte aligned");
   const int nq = bits_qgroups(B);
-  const ScanPlan plan = bits_plan(B, N, k, main_workgroups());
+  // (the 64-row-tile form: three workgroups a CU, its occupancy)
+  const bool small_tiles = bits_small_tiles(nq, bits_capw(k));
+  const ScanPlan plan =
+      bits_plan(B, N, k, small_tiles ? main_workgroups() * kWavesSmall / 2 : main_workgroups());
   if (workspace_bytes < plan.total) {
     set_error("workspace too small: %zu < %zu", workspace_bytes, plan.total);
     return kWorkspaceTooSmall;
