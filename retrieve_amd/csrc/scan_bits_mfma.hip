@@ -35,8 +35,9 @@ constexpr int kGroupRows = 16;                        // rows of one MFMA
 constexpr int kTileGroups = 8;                        // row groups of a main-pass tile
 constexpr int kTileRows = kGroupRows * kTileGroups;  // 128 rows, 8 KiB
 constexpr int kMaxQGroups = 4;                        // 16-query groups of a wave
-// Two query groups whose lists leave room for three workgroups a CU: 64-row tiles (four
-// groups), so the kernel fits three waves a SIMD; B = 17-32 0.343-0.353 -> 0.335-0.348 ms a call.
+// Two or three query groups whose lists leave room for three workgroups a CU: 64-row tiles (four
+// groups), so the kernel fits three waves a SIMD (168 VGPRs at three groups; four spill);
+// B = 17-32 0.343-0.353 -> 0.335-0.348 ms a call.
 constexpr int kTileGroupsSmall = 4;
 constexpr int kWavesSmall = 3;
 constexpr size_t kLdsPerCU = 160 * 1024;
@@ -395,9 +396,10 @@ size_t bits_main_lds(int capw, int nq) {
   return kScanWaves * (static_cast<size_t>(capw) * sizeof(uint64_t) + 16 * nq * sizeof(int));
 }
 
-// The 64-row-tile form: two query groups whose lists leave room for three workgroups a CU.
+// The 64-row-tile form: two or three query groups whose lists leave room for three
+// workgroups a CU.
 bool bits_small_tiles(int nq, int capw) {
-  return nq == 2 && kWavesSmall * bits_main_lds(capw, nq) <= kLdsPerCU;
+  return (nq == 2 || nq == 3) && kWavesSmall * bits_main_lds(capw, nq) <= kLdsPerCU;
 }
 
 template <int NQ, int TG>
@@ -422,7 +424,7 @@ int launch_bits(const ScanArgs& a, const PassPlan& p, int64_t nqg, bool seed,
     return kOk;
   }
   const size_t lds = bits_main_lds(p.capw, NQ);
-  if constexpr (NQ == 2) {
+  if constexpr (NQ == 2 || NQ == 3) {
     if (bits_small_tiles(NQ, p.capw)) return launch_main<NQ, kTileGroupsSmall>(a, grid, lds, stream);
   }
   return launch_main<NQ, kTileGroups>(a, grid, lds, stream);
