@@ -87,9 +87,11 @@ ScanPlan plan_scan(int64_t B, int64_t N, int64_t k, int64_t qpg, int64_t lists_p
       seed_rows_min > kSeedRowsPerK * k ? seed_rows_min : kSeedRowsPerK * k;
   s.seeded = N >= 8 * seed_rows;
   if (s.seeded) {
-    // one-entry lists (each seed wave's best); at least 4k of them per query
+    // one-entry lists (each seed wave's best); at least 2k of them per query (their k-th is the
+    // safe bound, their rank-th the speculative one; 4k cost configuration 5's step 1.5 % in
+    // seed workgroups, each loading the group's queries)
     s.seed = plan_pass(seed_rows, N / seed_rows, s.n_qgroups, seed_rows_per_wg, 1, lists_per_wg,
-                       lpq, kTargetWorkgroups, cdiv(4 * k, lpq));
+                       lpq, kTargetWorkgroups, cdiv(2 * k, lpq));
   }
   s.main = plan_pass(N, 1, s.n_qgroups, 1024, main_capw, lists_per_wg, lpq, target_wgs);
   const size_t lists = s.main.lists_bytes > s.seed.lists_bytes ? s.main.lists_bytes

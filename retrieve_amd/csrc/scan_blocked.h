@@ -880,7 +880,7 @@ __global__ void __launch_bounds__((BlkLayout<WIDE, RB, Op::kBits>::threads))
     if constexpr (CLAUSES) {
       // the maxima were taken over the mask alone: a lane whose best item fails its query's
       // clauses offers no bound (0), which keeps the bound a lower one (the merge takes the
-      // k-th of at least 4 k maxima a query)
+      // k-th of at least 2 k maxima a query)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int64_t q = q0[j] + c32;
