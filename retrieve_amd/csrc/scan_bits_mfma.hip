@@ -13,8 +13,9 @@
 //
 // Each wave scores up to four 16-query groups (NQ) against every group of rows it reads, so the
 // expansion of a row word (five VALU per 32 bits) feeds NQ MFMAs. A wave streams 128-row tiles
-// (8 KiB, one 16-byte load per lane per group) dealt round-robin over every wave of the grid,
-// with two or three tiles in registers: the one being scored and the others in flight. The hit test is one
+// (8 KiB, one 16-byte load per lane per group; 64-row tiles for two or three query groups where
+// three workgroups fit a CU) dealt round-robin over every wave of the grid, with two or three
+// tiles in registers: the one being scored and the others in flight. The hit test is one
 // signed-int maximum of the four raw accumulator bits per query group against the threshold in
 // the same domain; candidates (composites >= the query's bound, passing the mask) are appended
 // to per-wave lists and compacted as in every scan (wave_lists.h).
@@ -298,8 +299,7 @@ __global__ void __launch_bounds__(kScanThreads)
   auto load = [&](int64_t tt, v4i(&v)[TG]) {
     const int64_t rt = tt * TR;
     const int64_t left = rt < n ? (n - rt) * kCodeBytes : 0;
-    const int range = static_cast<int>(left < TR * kCodeBytes ? left
-                                                                     : TR * kCodeBytes);
+    const int range = static_cast<int>(left < TR * kCodeBytes ? left : TR * kCodeBytes);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(I + rt * kCodeBytes), 0, range, kBufferWord3);
 #pragma unroll
@@ -343,8 +343,7 @@ __global__ void __launch_bounds__(kScanThreads)
     // tile tt from v, v refilled with tile tt + NB waves
     const int64_t rn = (tt + NB * waves) * TR;
     const int64_t left = rn < n ? (n - rn) * kCodeBytes : 0;
-    const int range = static_cast<int>(left < TR * kCodeBytes ? left
-                                                                     : TR * kCodeBytes);
+    const int range = static_cast<int>(left < TR * kCodeBytes ? left : TR * kCodeBytes);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(I + rn * kCodeBytes), 0, range, kBufferWord3);
 #pragma unroll
